@@ -1,0 +1,351 @@
+"""Gradient evaluations per second of STADE-generated derivative code on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--only NAME]
+                    [--no-cpu-baseline]
+
+A step is one evaluation of a generated function (`<k>_b`, `<k>_d` or `<k>_hv`) through the
+C ABI of libstade_hip.so on synthetic inputs already resident in HBM.  The headline line is
+the workload BASELINE.json quotes its metric on (configs[1], the diffusion adjoint on a
+4096 x 4096 fp64 grid); every other implemented config is measured with the same protocol
+and reported under "configs".
+
+Roofline: the dominant kernel of the headline workload is timed with HIP events recorded on
+its own launch stream by the library's profiler (stade_hip_profile_*), over the timed
+region; achieved = algorithmic bytes per launch / mean launch duration.  Algorithmic bytes
+count each array element the generated function's contract reads once, each written once,
+each read-modify-write twice; scalars and length-1 arrays are ignored.
+
+CPU baseline: the same generated text run by the oracle (oracle/jl2c.py transpiled to C,
+gcc -O2, one thread pinned to one core), on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "stade.jl_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+FP64_PEAK_TFLOPS = 78.6
+
+
+def _tensor(a, dev):
+    import numpy as np
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+class Workload:
+    name = ""
+    kernel = ""           # dominant kernel (profiler name)
+    bound = "hbm"
+    dtype = "f64"
+
+    def setup(self, dev):
+        raise NotImplementedError
+
+    def step(self):
+        raise NotImplementedError
+
+    def algo_bytes(self) -> float:          # per evaluation
+        return 0.0
+
+    def kernel_bytes(self) -> float:        # per launch of the dominant kernel
+        return 0.0
+
+    def kernel_flops(self) -> float:
+        return 0.0
+
+    def config(self) -> dict:
+        return {}
+
+    def cpu_sample(self):
+        """(callable running one evaluation of the oracle, description); None if unavailable."""
+        return None
+
+
+class Diffusion(Workload):
+    dtype = "f64"
+
+    def __init__(self, mode="b", n=4096):
+        self.mode, self.n = mode, n
+        self.name = f"diffusion2d_{mode}"
+        self.kernel = f"diffusion2d_{mode}"
+
+    def setup(self, dev):
+        import numpy as np
+        import torch
+        import stade_hip
+        n = self.n
+        c = n * n
+        rng = stade_hip.api.Rng(stade_hip.stable_seed("diffusion2d"))
+        u = stade_hip.rng_normal(rng, c)
+        z = lambda: torch.zeros(c, dtype=torch.float64, device=dev)
+        self.t = dict(loss=torch.zeros(1, dtype=torch.float64, device=dev),
+                      lossb=torch.ones(1, dtype=torch.float64, device=dev),
+                      lossd=torch.zeros(1, dtype=torch.float64, device=dev),
+                      lossbd=torch.zeros(1, dtype=torch.float64, device=dev),
+                      u=_tensor(u, dev), ub=z(), un=z(), unb=z(), und=z(), unbd=z(), ubd=z())
+        if self.mode in ("d", "hv"):
+            rng2 = stade_hip.api.Rng(stade_hip.stable_seed("diffusion2d") + 1)
+            self.t["ud"] = _tensor(stade_hip.rng_normal(rng2, c), dev)
+        self.host_u = u
+
+    def step(self):
+        import stade_hip
+        t, n = self.t, self.n
+        if self.mode == "b":
+            stade_hip.diffusion2d_b(t["loss"], t["lossb"], t["u"], t["ub"], t["un"], t["unb"], n)
+        elif self.mode == "d":
+            stade_hip.diffusion2d_d(t["loss"], t["lossd"], t["u"], t["ud"], t["un"], t["und"], n)
+        else:
+            stade_hip.diffusion2d_hv(t["loss"], t["lossb"], t["u"], t["ub"], t["un"], t["unb"], n,
+                                     t["lossd"], t["lossbd"], t["ud"], t["ubd"], t["und"], t["unbd"])
+
+    def algo_bytes(self):
+        per = {"b": 48, "d": 32, "hv": 96}[self.mode]
+        return per * self.n * self.n
+
+    def kernel_bytes(self):
+        # pass 1 of the adjoint: u R, un W, unb R, ub R+W (unb's reset is pass 2)
+        per = {"b": 40, "d": 32, "hv": 80}[self.mode]
+        return per * self.n * self.n
+
+    def config(self):
+        return {"workload": f"diffusion2d_{self.mode} (STADE {'adjoint' if self.mode == 'b' else 'tangent' if self.mode == 'd' else 'HVP'}), "
+                            f"periodic 5-point step + sum(un^2), {self.n}x{self.n} fp64, u ~ N(0,1) from val_stable_seed",
+                "n": self.n, "cells": self.n * self.n}
+
+    def cpu_sample(self):
+        import numpy as np
+        from oracle import runner
+        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"diffusion2d_{self.mode}.jl", bounds_check=False)
+        n, c = self.n, self.n * self.n
+        u = self.host_u.copy()
+        z = lambda: np.zeros(c)
+        a = dict(ub=z(), un=z(), unb=z(), ud=np.ones(c), und=z(), ubd=z(), unbd=z())
+
+        def run():
+            if self.mode == "b":
+                lib.call("diffusion2d_b", np.zeros(1), np.ones(1), u, a["ub"], a["un"], a["unb"], n)
+            elif self.mode == "d":
+                lib.call("diffusion2d_d", np.zeros(1), np.zeros(1), u, a["ud"], a["un"], a["und"], n)
+            else:
+                lib.call("diffusion2d_hv", np.zeros(1), np.ones(1), u, a["ub"], a["un"], a["unb"], n,
+                         np.zeros(1), np.zeros(1), a["ud"], a["ubd"], a["und"], a["unbd"])
+        return run, f"diffusion2d_{self.mode} at the full {n}x{n} grid"
+
+
+class Affine(Workload):
+    dtype = "f64"
+
+    def __init__(self, mode="b", m=1024, n=1024):
+        self.mode, self.m, self.n = mode, m, n
+        self.name = f"affine_lsq_{mode}"
+        self.kernel = "affine_cols" if mode != "d" else "affine_rows"
+
+    def setup(self, dev):
+        import torch
+        import stade_hip
+        m, n = self.m, self.n
+        rng = stade_hip.api.Rng(stade_hip.stable_seed("affine_lsq"))
+        w = stade_hip.rng_uniform(rng, m * n, -1.0, 1.0)
+        x, b, t = (stade_hip.rng_normal(rng, k) for k in (n, m, m))
+        rng2 = stade_hip.api.Rng(stade_hip.stable_seed("affine_lsq") + 1)
+        wd, xd, bd, td = (stade_hip.rng_normal(rng2, k) for k in (m * n, n, m, m))
+        f = lambda a: _tensor(a, dev)
+        z = lambda k: torch.zeros(k, dtype=torch.float64, device=dev)
+        self.t = dict(loss=z(1), lossb=f([1.0]), lossd=z(1), lossbd=z(1), w=f(w), wb=z(m * n), x=f(x), xb=z(n),
+                      b=f(b), bb=z(m), t=f(t), tb=z(m), r=z(m), rb=z(m), wd=f(wd), wbd=z(m * n), xd=f(xd), xbd=z(n),
+                      bd=f(bd), bbd=z(m), td=f(td), tbd=z(m), rd=z(m), rbd=z(m))
+
+    def step(self):
+        import stade_hip
+        t, m, n = self.t, self.m, self.n
+        base = [t[k] for k in ("loss",)]
+        if self.mode == "b":
+            stade_hip.affine_lsq_b(t["loss"], t["lossb"], t["w"], t["wb"], t["x"], t["xb"], t["b"], t["bb"], t["t"], t["tb"],
+                                   t["r"], t["rb"], m, n)
+        elif self.mode == "d":
+            stade_hip.affine_lsq_d(t["loss"], t["lossd"], t["w"], t["wd"], t["x"], t["xd"], t["b"], t["bd"], t["t"], t["td"],
+                                   t["r"], t["rd"], m, n)
+        else:
+            stade_hip.affine_lsq_hv(t["loss"], t["lossb"], t["w"], t["wb"], t["x"], t["xb"], t["b"], t["bb"], t["t"], t["tb"],
+                                    t["r"], t["rb"], m, n, t["lossd"], t["lossbd"], t["wd"], t["wbd"], t["xd"], t["xbd"],
+                                    t["bd"], t["bbd"], t["td"], t["tbd"], t["rd"], t["rbd"])
+        del base
+
+    def algo_bytes(self):
+        mn, m, n = self.m * self.n, self.m, self.n
+        if self.mode == "b":   # w R, wb RW, x R, xb RW, b R, bb RW, t R, tb RW, r W, rb RW
+            return 8 * (3 * mn + 3 * n + 9 * m)
+        if self.mode == "d":   # w, wd R; x, xd R; b, bd, t, td R; r, rd W
+            return 8 * (2 * mn + 2 * n + 6 * m)
+        return 8 * (6 * mn + 6 * n + 18 * m)
+
+    def kernel_bytes(self):
+        mn = self.m * self.n
+        return 8 * {"b": 3 * mn, "d": 2 * mn, "hv": 6 * mn}[self.mode]
+
+    def config(self):
+        return {"workload": f"affine_lsq_{self.mode}, loss = 0.5*sum((W*x+b-t)^2), W {self.m}x{self.n} fp64 U[-1,1]",
+                "m": self.m, "n": self.n}
+
+
+WORKLOADS = {
+    "diffusion2d_b": lambda: Diffusion("b"),
+    "diffusion2d_d": lambda: Diffusion("d"),
+    "diffusion2d_hv": lambda: Diffusion("hv"),
+    "affine_lsq_b": lambda: Affine("b"),
+    "affine_lsq_d": lambda: Affine("d"),
+    "affine_lsq_hv": lambda: Affine("hv"),
+}
+HEADLINE = "diffusion2d_b"
+
+
+def _lib():
+    import stade_hip
+    L = stade_hip.lib()
+    L.stade_hip_profile_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]
+    return L
+
+
+def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
+    import torch
+    L = _lib()
+    wl.setup(dev)
+    for _ in range(warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    L.stade_hip_profile_start()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        wl.step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    tot, cnt = ctypes.c_double(0), ctypes.c_int64(0)
+    L.stade_hip_profile_read(wl.kernel.encode(), ctypes.byref(tot), ctypes.byref(cnt))
+    L.stade_hip_profile_stop()
+    ms_step = (t1 - t0) * 1e3 / steps
+    out = {"evals_per_s": steps / (t1 - t0), "ms_per_step": ms_step, "steps": steps, "dtype": wl.dtype}
+    if cnt.value:
+        k_ms = tot.value / cnt.value
+        out["kernel"] = wl.kernel
+        out["kernel_ms"] = k_ms
+        if wl.bound == "hbm":
+            ach = wl.kernel_bytes() / (k_ms * 1e-3) / 1e9
+            out["roofline"] = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                               "frac": ach / HBM_PEAK_GBS, "traffic": None}
+        else:
+            peak = FP32_PEAK_TFLOPS if wl.dtype == "f32" else FP64_PEAK_TFLOPS
+            ach = wl.kernel_flops() / (k_ms * 1e-3) / 1e12
+            out["roofline"] = {"bound": "mfma", "achieved": ach, "peak": peak, "unit": "TFLOP/s",
+                               "frac": ach / peak, "traffic": None}
+    if wl.bound == "hbm" and wl.algo_bytes():
+        out["eval_GBps"] = wl.algo_bytes() / (ms_step * 1e-3) / 1e9
+        out["eval_hbm_frac"] = out["eval_GBps"] / HBM_PEAK_GBS
+    out["config"] = wl.config()
+    return out
+
+
+def cpu_baseline(wl: Workload, budget_s: float = 12.0, max_runs: int = 30) -> dict | None:
+    sample = wl.cpu_sample()
+    if sample is None:
+        return None
+    run, desc = sample
+    try:
+        cpus = sorted(os.sched_getaffinity(0))
+        os.sched_setaffinity(0, {cpus[0]})
+    except (AttributeError, OSError):
+        cpus = None
+    try:
+        run()  # warm-up
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < max_runs and (time.perf_counter() - t_start) < budget_s:
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+    finally:
+        if cpus:
+            os.sched_setaffinity(0, set(cpus))
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu_model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": 1.0 / med, "unit": "evals/s", "cores": 1, "kind": "port",
+            "sample": f"{desc}: median of {len(times)} runs of the oracle (generated Julia text transpiled to C, "
+                      f"gcc -O2, 1 thread pinned to one core, {cpu_model})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--only", action="store_true", help="measure the headline workload only")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU; the multi-GPU design is described, not run "
+              "(--gpus N > 1 is not supported)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    head = WORKLOADS[args.workload]()
+    res = measure(head, args.steps, args.warmup, dev)
+    others = {}
+    if not args.only:
+        for nm, mk in WORKLOADS.items():
+            if nm == args.workload:
+                continue
+            wl = mk()
+            others[nm] = measure(wl, max(5, args.steps // 2), max(2, args.warmup), dev)
+            del wl
+            torch.cuda.empty_cache()
+    cpu = None if args.no_cpu_baseline else cpu_baseline(head)
+    line = {
+        "metric": "gradient evals/sec per config",
+        "value": res["evals_per_s"],
+        "unit": "evals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head.dtype,
+        "data": "synthetic (seeded Julia Xoshiro stream, val_stable_seed of the config name)",
+        "config": res["config"],
+        "roofline": res.get("roofline"),
+        "cpu_baseline": cpu,
+        "eval_hbm_frac": res.get("eval_hbm_frac"),
+        "kernel_ms": res.get("kernel_ms"),
+        "configs": {k: {kk: vv for kk, vv in v.items() if kk != "config"} | {"workload": v["config"].get("workload")}
+                    for k, v in others.items()},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,105 @@
+/*
+ * libstade_hip -- MI355X (gfx950) execution of STADE-generated derivative code.
+ *
+ * Each `stade_hip_<k>_<mode>` entry point replaces one generated host function of
+ * `stade_amdgpu_file` (/root/reference/src/STADE.jl:18604-18605): `<k>_b_amdgpu` (adjoint),
+ * `<k>_d_amdgpu` (tangent) or `<k>_hv_amdgpu` (Hessian-vector product), for the kernel text
+ * `stade.jl_amd/corpus/<k>.jl` and its generated `_b/_d/_hv` texts.
+ *
+ * Conventions, shared by every entry point:
+ *   - Arguments follow the generated function's own order (`agen_signature_args`
+ *     /root/reference/src/STADE.jl:3455-3464: each float argument followed by its shadow,
+ *     Int64 arguments once, then the stacks; `tgen_signature_args` 3306-3315; `hvp_emit`
+ *     6750-6756: the adjoint list, then (xd, xbd) per float argument, then the stacks).
+ *   - Arrays are device pointers to the caller's column-major, densely packed Julia arrays
+ *     (the pointer of a ROCArray).  Indices keep Julia's meaning: element (i, j) of an
+ *     (m, n) array is at offset (i-1) + (j-1)*m.
+ *   - Outputs are mutated in place exactly as the generated code does: primal outputs are
+ *     overwritten, shadows are accumulated (not overwritten), statement resets zero the
+ *     shadows the generated code zeroes, stacks are written by the forward sweep.
+ *   - A float scalar argument is passed by value; its shadow is a host pointer that holds
+ *     the seed on entry and the generated function's returned value on exit (the adjoint
+ *     returns scalar shadows, 3672; the HVP returns (xb, xbd) pairs, 6772-6779).  An entry
+ *     point with such outputs synchronises `stream` once before returning; the others only
+ *     enqueue work on `stream` (NULL = the default stream).
+ *   - Return value: 0 on success; a positive hipError_t code or a negative STADE_HIP_E*
+ *     code on failure, with a message in stade_hip_last_error().  Argument errors are
+ *     reported before any work is enqueued.
+ *   - Calls on one device share a library workspace (reduction partials and tickets):
+ *     calls that overlap on one device, on different streams, race.
+ */
+#ifndef STADE_HIP_H
+#define STADE_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STADE_HIP_OK 0
+#define STADE_HIP_EINVAL (-1)
+#define STADE_HIP_ENOMEM (-2)
+#define STADE_HIP_ERANGE (-3)
+
+/* ---- library ------------------------------------------------------------------------ */
+const char* stade_hip_last_error(void);
+const char* stade_hip_version(void);
+int32_t stade_hip_free(void* p);
+int32_t stade_hip_synchronize(hipStream_t stream);
+
+/* ---- kernel timing (no counterpart in the reference; its timings come from an external
+ * bench kit, /root/reference/claude/manual-stade-dev.md:2040).  While enabled, every kernel
+ * launch is bracketed by HIP events on the launch's stream; read() waits for the pending
+ * events and returns the summed elapsed time and launch count of one kernel name. */
+int32_t stade_hip_profile_start(void);
+int32_t stade_hip_profile_stop(void);
+int32_t stade_hip_profile_read(const char* kernel, double* total_ms, int64_t* launches);
+
+/* ---- inputs: STADE's stable seed and Julia's Random.Xoshiro scalar stream -------------
+ * stade_hip_stable_seed  = `val_stable_seed` (FNV-1a64), /root/reference/src/STADE.jl:16619-16625
+ * stade_hip_rng_seed     = `Random.Xoshiro(seed)` state (Julia 1.10 seeding)
+ * stade_hip_rng_normal_f64 = n draws of `val_normal(rng)`, 16628-16637
+ * stade_hip_rng_uniform_f64 = n draws of `lo + (hi - lo) * rand(rng)`
+ * stade_hip_rng_int_range = n draws of lo + floor(rand(rng) * (hi - lo + 1))
+ * Host memory; no device work. */
+uint64_t stade_hip_stable_seed(const char* name);
+int32_t stade_hip_rng_seed(uint64_t seed, uint64_t state[4]);
+int32_t stade_hip_rng_normal_f64(uint64_t state[4], double* out, int64_t n);
+int32_t stade_hip_rng_uniform_f64(uint64_t state[4], double* out, int64_t n, double lo, double hi);
+int32_t stade_hip_rng_int_range(uint64_t state[4], int64_t* out, int64_t n, int64_t lo, int64_t hi);
+
+/* ---- config 1: affine_lsq(loss, w, x, b, t, r, i_m, i_n) -------------------------------
+ * loss += 0.5 * sum((w * x + b - t) .^ 2), w (i_m, i_n) Float64.
+ * replaces affine_lsq_b_amdgpu / _d_amdgpu / _hv_amdgpu (corpus/affine_lsq_{b,d,hv}.jl) */
+int32_t stade_hip_affine_lsq_b(double* loss, const double* lossb, const double* w, double* wb, const double* x, double* xb,
+                               const double* b, double* bb, const double* t, double* tb, double* r, double* rb,
+                               int64_t i_m, int64_t i_n, hipStream_t stream);
+int32_t stade_hip_affine_lsq_d(double* loss, double* lossd, const double* w, const double* wd, const double* x, const double* xd,
+                               const double* b, const double* bd, const double* t, const double* td, double* r, double* rd,
+                               int64_t i_m, int64_t i_n, hipStream_t stream);
+int32_t stade_hip_affine_lsq_hv(double* loss, const double* lossb, const double* w, double* wb, const double* x, double* xb,
+                                const double* b, double* bb, const double* t, double* tb, double* r, double* rb,
+                                int64_t i_m, int64_t i_n, double* lossd, const double* lossbd, const double* wd, double* wbd,
+                                const double* xd, double* xbd, const double* bd, double* bbd, const double* td, double* tbd,
+                                double* rd, double* rbd, hipStream_t stream);
+
+/* ---- config 2: diffusion2d(loss, u, un, n) ---------------------------------------------
+ * one periodic 5-point step un = u + 0.1 * lap(u) on n x n, then loss += sum(un .^ 2).
+ * replaces diffusion2d_b_amdgpu / _d_amdgpu / _hv_amdgpu (corpus/diffusion2d_{b,d,hv}.jl);
+ * the adjoint scatter is the owner-computes gather of `cgen_gather_periodic_inverse`
+ * (/root/reference/src/STADE.jl:7343-7529).  n <= 46340. */
+int32_t stade_hip_diffusion2d_b(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                                int64_t n, hipStream_t stream);
+int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, const double* ud, double* un, double* und,
+                                int64_t n, hipStream_t stream);
+int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                                 int64_t n, double* lossd, const double* lossbd, const double* ud, double* ubd, double* und,
+                                 double* unbd, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STADE_HIP_H */

@@ -621,6 +621,10 @@ class FuncTypes:
             if e[0] == "ref":
                 for ix in e[2]:
                     mark_int_expr(ix)
+            if e[0] == "call" and e[1] in ("div", "mod", "fld"):
+                # a literal div/mod call is one of shape_infer's Int64 signals (skill-stade rule 11)
+                for a in e[2]:
+                    mark_int_expr(a)
             if e[0] == "range":
                 for part in (e[1], e[2], e[3]):
                     if part is not None:

@@ -1,0 +1,246 @@
+// affine_lsq: tangent, adjoint and HVP of loss += 0.5 * sum((w * x + b - t) .^ 2) with a
+// column-major w of shape (m, n).
+//
+// Generated code this replaces: stade.jl_amd/corpus/affine_lsq_{b,d,hv}.jl (STADE's
+// `agen_emit` /root/reference/src/STADE.jl:3390-3419, `tgen_emit` 3271-3278, `hvp_emit`
+// 6729-6782).  Under `stade_amdgpu_file` the row loop runs one thread per row with the column
+// sum sequential inside it, and the adjoint's `xb[j] += w[i,j] * sb` becomes a per-element
+// atomic (`cgen_device_assign` 11941-11969): m atomics on each of the n entries of xb.
+//
+// Here: 64 x 64 tiles of w, one wave per 16 columns and one lane per row, so every wave
+// load is a 512-byte contiguous column segment.
+//   1. rows:    partial row sums  s_i = sum_j w[i,j] x[j]  per 64-column chunk (LDS tree)
+//   2. finish:  r = (b - t) + sum of chunk partials, loss (grid sum), rb reset, bb, tb, sb
+//   3. columns: wb[i,j] += x[j] sb_i (read-modify-write, the dominant traffic) and the
+//               per-tile column sums of w[i,j] sb_i (DPP wave sums), no atomics
+//   4. xb:      xb[j] += sum over row tiles of the column partials, in tile order
+// Every reduction has a fixed order: results do not depend on scheduling.
+#include "internal.hpp"
+#include "../../include/stade_hip.h"
+
+namespace stade {
+namespace {
+
+constexpr int RT = 64, CT = 64, CW = 16, NT = 256;  // rows per tile, columns per tile, columns per wave
+
+enum Mode { ADJ = 0, TAN = 1, HVP = 2 };
+
+template <int M>
+__global__ __launch_bounds__(NT) void rows_kernel(const double* __restrict__ w, const double* __restrict__ wd,
+                                                  const double* __restrict__ x, const double* __restrict__ xd,
+                                                  double* __restrict__ P, double* __restrict__ Pd, int m, int n) {
+    __shared__ double part[2][4][RT];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int chunk = blockIdx.x, i = blockIdx.y * RT + lane;
+    const int j0 = chunk * CT + wv * CW;
+    double s = 0.0, sd = 0.0;
+    if (i < m) {
+#pragma unroll 4
+        for (int jj = 0; jj < CW; ++jj) {
+            int j = j0 + jj;
+            if (j >= n) break;
+            size_t g = (size_t)j * m + i;
+            double wij = w[g], xj = x[j];
+            if (M != ADJ) sd = sd + (xj * wd[g] + wij * xd[j]);
+            s = s + wij * xj;
+        }
+    }
+    part[0][wv][lane] = s;
+    part[1][wv][lane] = sd;
+    __syncthreads();
+    if (wv == 0 && i < m) {
+        P[(size_t)chunk * m + i] = ((part[0][0][lane] + part[0][1][lane]) + part[0][2][lane]) + part[0][3][lane];
+        if (M != ADJ) Pd[(size_t)chunk * m + i] = ((part[1][0][lane] + part[1][1][lane]) + part[1][2][lane]) + part[1][3][lane];
+    }
+}
+
+struct FinishArgs {
+    const double *b, *t, *bd, *td, *P, *Pd, *lossb, *lossbd;
+    double *r, *rd, *rb, *rbd, *bb, *bbd, *tb, *tbd, *S, *Sd, *loss, *lossd;
+    int m, nchunks;
+};
+
+template <int M>
+__global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partials, unsigned* ticket) {
+    __shared__ double red[32];
+    const int i = blockIdx.x * NT + threadIdx.x;
+    double acc[2] = {0.0, 0.0};
+    if (i < a.m) {
+        double s = a.b[i] - a.t[i];
+        double sd = 0.0;
+        if (M != ADJ) sd = a.bd[i] - a.td[i];
+        for (int c = 0; c < a.nchunks; ++c) {
+            s = s + a.P[(size_t)c * a.m + i];
+            if (M != ADJ) sd = sd + a.Pd[(size_t)c * a.m + i];
+        }
+        if (M != ADJ) {
+            a.rd[i] = sd;
+            acc[1] = 0.5 * ((2.0 * s) * sd);
+        }
+        a.r[i] = s;
+        acc[0] = 0.5 * (s * s);
+        if (M == ADJ) {
+            double rbt = a.rb[i] + 0.5 * (2.0 * s) * a.lossb[0];
+            a.rb[i] = 0.0;
+            a.S[i] = rbt;
+            a.bb[i] = a.bb[i] + rbt;
+            a.tb[i] = a.tb[i] + -rbt;
+        } else if (M == HVP) {
+            double h3 = a.lossb[0], h4 = 0.5 * (2.0 * s);
+            double rbdt = a.rbd[i] + (h3 * (0.5 * (2.0 * sd)) + h4 * a.lossbd[0]);
+            double rbt = a.rb[i] + h4 * h3;
+            a.rbd[i] = 0.0;
+            a.rb[i] = 0.0;
+            a.S[i] = rbt;
+            a.Sd[i] = rbdt;
+            a.bbd[i] = a.bbd[i] + rbdt;
+            a.bb[i] = a.bb[i] + rbt;
+            a.tbd[i] = a.tbd[i] + -rbdt;
+            a.tb[i] = a.tb[i] + -rbt;
+        }
+    }
+    if (M == ADJ) {
+        double v[1] = {acc[0]};
+        grid_sum_into<1>(v, red, partials, ticket, SumOuts{{a.loss}});
+    } else {
+        grid_sum_into<2>(acc, red, partials, ticket, SumOuts{{a.loss, a.lossd}});
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, const double* __restrict__ wd,
+                                                  double* __restrict__ wb, double* __restrict__ wbd,
+                                                  const double* __restrict__ x, const double* __restrict__ xd,
+                                                  const double* __restrict__ S, const double* __restrict__ Sd,
+                                                  double* __restrict__ XP, double* __restrict__ XPd, int m, int n) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int rtile = blockIdx.y, i = rtile * RT + lane;
+    const int j0 = blockIdx.x * CT + wv * CW;
+    const bool live = i < m;
+    const double si = live ? S[i] : 0.0;
+    const double sid = (M == HVP && live) ? Sd[i] : 0.0;
+    for (int jj = 0; jj < CW; ++jj) {
+        int j = j0 + jj;
+        if (j >= n) break;
+        double cx = 0.0, cxd = 0.0;
+        if (live) {
+            size_t g = (size_t)j * m + i;
+            double xj = x[j], wij = w[g];
+            if (M == HVP) {
+                wbd[g] = wbd[g] + (si * xd[j] + xj * sid);
+                cxd = si * wd[g] + wij * sid;
+            }
+            wb[g] = wb[g] + xj * si;
+            cx = wij * si;
+        }
+        cx = wave_sum(cx);
+        if (M == HVP) cxd = wave_sum(cxd);
+        if (lane == 0) {
+            XP[(size_t)rtile * n + j] = cx;
+            if (M == HVP) XPd[(size_t)rtile * n + j] = cxd;
+        }
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(NT) void xfinish_kernel(double* __restrict__ xb, double* __restrict__ xbd,
+                                                     const double* __restrict__ XP, const double* __restrict__ XPd,
+                                                     int n, int mtiles) {
+    const int j = blockIdx.x * NT + threadIdx.x;
+    if (j >= n) return;
+    double s = 0.0, sd = 0.0;
+    for (int r = 0; r < mtiles; ++r) {
+        s += XP[(size_t)r * n + j];
+        if (M == HVP) sd += XPd[(size_t)r * n + j];
+    }
+    if (M == HVP) xbd[j] = xbd[j] + sd;
+    xb[j] = xb[j] + s;
+}
+
+int32_t check_sizes(int64_t m, int64_t n, const char* fn) {
+    if (m < 0 || n < 0) return set_error(STADE_HIP_EINVAL, "%s: negative size (i_m = %lld, i_n = %lld)", fn, (long long)m, (long long)n);
+    if (m > (1 << 26) || n > (1 << 26) || m * n > (int64_t)1 << 34)
+        return set_error(STADE_HIP_ERANGE, "%s: size out of range (i_m = %lld, i_n = %lld)", fn, (long long)m, (long long)n);
+    if ((m + NT - 1) / NT * 2 > kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: i_m too large for the workspace", fn);
+    return STADE_HIP_OK;
+}
+
+template <int M>
+int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double* wbd, const double* x, const double* xd,
+            double* xb, double* xbd, int64_t m, int64_t n, hipStream_t stream) {
+    if (m == 0) return STADE_HIP_OK;
+    Workspace* ws = workspace();
+    if (!ws) return STADE_HIP_ENOMEM;
+    const int nchunks = (int)((n + CT - 1) / CT), mtiles = (int)((m + RT - 1) / RT);
+    const int two = (M == ADJ) ? 1 : 2;
+    size_t nP = (size_t)nchunks * m, nS = (size_t)m, nX = (size_t)mtiles * n;
+    double* base = (double*)scratch(sizeof(double) * two * (nP + nS + nX) + 256);
+    if (!base) return STADE_HIP_ENOMEM;
+    double *P = base, *Pd = P + nP, *S = P + two * nP, *Sd = S + nS, *XP = S + two * nS, *XPd = XP + nX;
+    if (nchunks > 0) {
+        STADE_TIMED("affine_rows", stream, rows_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, x, xd, P, Pd, (int)m, (int)n));
+        STADE_LAUNCHED("affine rows_kernel");
+    }
+    fa.P = P;
+    fa.Pd = Pd;
+    fa.S = S;
+    fa.Sd = Sd;
+    fa.m = (int)m;
+    fa.nchunks = nchunks;
+    STADE_TIMED("affine_finish", stream, finish_kernel<M><<<(unsigned)((m + NT - 1) / NT), NT, 0, stream>>>(fa, ws->partials, ws->tickets + 1));
+    STADE_LAUNCHED("affine finish_kernel");
+    if (M == TAN || n == 0) return STADE_HIP_OK;
+    STADE_TIMED("affine_cols", stream,
+                cols_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, S, Sd, XP, XPd, (int)m, (int)n));
+    STADE_LAUNCHED("affine cols_kernel");
+    STADE_TIMED("affine_xfinish", stream, xfinish_kernel<M><<<(unsigned)((n + NT - 1) / NT), NT, 0, stream>>>(xb, xbd, XP, XPd, (int)n, mtiles));
+    STADE_LAUNCHED("affine xfinish_kernel");
+    return STADE_HIP_OK;
+}
+
+}  // namespace
+}  // namespace stade
+
+using namespace stade;
+
+extern "C" {
+
+int32_t stade_hip_affine_lsq_b(double* loss, const double* lossb, const double* w, double* wb, const double* x, double* xb,
+                               const double* b, double* bb, const double* t, double* tb, double* r, double* rb,
+                               int64_t i_m, int64_t i_n, hipStream_t stream) {
+    if (int32_t rc = check_sizes(i_m, i_n, "stade_hip_affine_lsq_b")) return rc;
+    if (i_m > 0 && (!loss || !lossb || !w || !wb || !x || !xb || !b || !bb || !t || !tb || !r || !rb))
+        return set_error(STADE_HIP_EINVAL, "stade_hip_affine_lsq_b: null pointer");
+    FinishArgs fa{};
+    fa.b = b; fa.t = t; fa.lossb = lossb; fa.r = r; fa.rb = rb; fa.bb = bb; fa.tb = tb; fa.loss = loss;
+    return run<ADJ>(fa, w, nullptr, wb, nullptr, x, nullptr, xb, nullptr, i_m, i_n, stream);
+}
+
+int32_t stade_hip_affine_lsq_d(double* loss, double* lossd, const double* w, const double* wd, const double* x, const double* xd,
+                               const double* b, const double* bd, const double* t, const double* td, double* r, double* rd,
+                               int64_t i_m, int64_t i_n, hipStream_t stream) {
+    if (int32_t rc = check_sizes(i_m, i_n, "stade_hip_affine_lsq_d")) return rc;
+    if (i_m > 0 && (!loss || !lossd || !w || !wd || !x || !xd || !b || !bd || !t || !td || !r || !rd))
+        return set_error(STADE_HIP_EINVAL, "stade_hip_affine_lsq_d: null pointer");
+    FinishArgs fa{};
+    fa.b = b; fa.t = t; fa.bd = bd; fa.td = td; fa.r = r; fa.rd = rd; fa.loss = loss; fa.lossd = lossd;
+    return run<TAN>(fa, w, wd, nullptr, nullptr, x, xd, nullptr, nullptr, i_m, i_n, stream);
+}
+
+int32_t stade_hip_affine_lsq_hv(double* loss, const double* lossb, const double* w, double* wb, const double* x, double* xb,
+                                const double* b, double* bb, const double* t, double* tb, double* r, double* rb,
+                                int64_t i_m, int64_t i_n, double* lossd, const double* lossbd, const double* wd, double* wbd,
+                                const double* xd, double* xbd, const double* bd, double* bbd, const double* td, double* tbd,
+                                double* rd, double* rbd, hipStream_t stream) {
+    if (int32_t rc = check_sizes(i_m, i_n, "stade_hip_affine_lsq_hv")) return rc;
+    if (i_m > 0 && (!loss || !lossb || !w || !wb || !x || !xb || !b || !bb || !t || !tb || !r || !rb || !lossd || !lossbd ||
+                    !wd || !wbd || !xd || !xbd || !bd || !bbd || !td || !tbd || !rd || !rbd))
+        return set_error(STADE_HIP_EINVAL, "stade_hip_affine_lsq_hv: null pointer");
+    FinishArgs fa{};
+    fa.b = b; fa.t = t; fa.bd = bd; fa.td = td; fa.lossb = lossb; fa.lossbd = lossbd;
+    fa.r = r; fa.rd = rd; fa.rb = rb; fa.rbd = rbd; fa.bb = bb; fa.bbd = bbd; fa.tb = tb; fa.tbd = tbd;
+    fa.loss = loss; fa.lossd = lossd;
+    return run<HVP>(fa, w, wd, wb, wbd, x, xd, xb, xbd, i_m, i_n, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,189 @@
+// Shared internals of libstade_hip: error state, per-device workspace, wave64/block reductions.
+//
+// Everything here is CDNA (gfx950) code: 64-lane wavefronts, DPP row operations inside a
+// 16-lane row, LDS trees across waves, and a sync-free last-block second pass for grid-wide
+// sums (the design the reference keeps CUDA-only: `cgen_reduce_block_kernel`
+// /root/reference/src/STADE.jl:10333-10354, `sync_free_reduce` 10303-10316).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#define STADE_HIP_OK 0
+#define STADE_HIP_EINVAL (-1)
+#define STADE_HIP_ENOMEM (-2)
+#define STADE_HIP_ERANGE (-3)
+
+namespace stade {
+
+// ------------------------------------------------------------------------------------------
+// error state (host)
+// ------------------------------------------------------------------------------------------
+int32_t set_error(int32_t code, const char* fmt, ...);
+int32_t check_hip(hipError_t e, const char* what);
+#define STADE_TRY_HIP(expr)                                              \
+    do {                                                                 \
+        hipError_t _e = (expr);                                          \
+        if (_e != hipSuccess) return ::stade::check_hip(_e, #expr);     \
+    } while (0)
+#define STADE_LAUNCHED(what)                                             \
+    do {                                                                 \
+        hipError_t _e = hipGetLastError();                               \
+        if (_e != hipSuccess) return ::stade::check_hip(_e, what);       \
+    } while (0)
+
+// ------------------------------------------------------------------------------------------
+// per-device workspace: grid-reduction partials, tickets and scratch buffers owned by the
+// library.  Calls that share a device must be stream-ordered with respect to each other.
+// ------------------------------------------------------------------------------------------
+struct Workspace {
+    double* partials;       // per-block partial sums, kPartialSlots doubles
+    unsigned int* tickets;  // zero-initialised tickets of the last-block reductions
+    double* dscalars;       // small device scalars handed back to the host
+    void* scratch;          // grows on demand
+    size_t scratch_bytes;
+};
+constexpr int kPartialSlots = 1 << 20;
+constexpr int kTickets = 64;
+constexpr int kDeviceScalars = 64;
+
+// Workspace of the current device; nullptr (with the error set) on failure.
+Workspace* workspace();
+// Scratch of at least `bytes`; nullptr (with the error set) on failure.
+void* scratch(size_t bytes);
+
+// ------------------------------------------------------------------------------------------
+// kernel timing: when enabled (stade_hip_profile_start), every launch made through
+// STADE_TIMED is bracketed by HIP events recorded on the launch's own stream; the elapsed
+// times are summed per kernel name when read (stade_hip_profile_read).
+// ------------------------------------------------------------------------------------------
+bool prof_enabled();
+void prof_begin(const char* kernel, hipStream_t s);
+void prof_end(hipStream_t s);
+#define STADE_TIMED(name, stream, ...)                                   \
+    do {                                                                 \
+        const bool _p = ::stade::prof_enabled();                        \
+        if (_p) ::stade::prof_begin(name, stream);                      \
+        __VA_ARGS__;                                                     \
+        if (_p) ::stade::prof_end(stream);                              \
+    } while (0)
+
+// ------------------------------------------------------------------------------------------
+// device: wave64 and block reductions
+// ------------------------------------------------------------------------------------------
+
+// DPP move of a 64-bit value: both 32-bit halves go through the same lane permutation.
+template <int Ctrl>
+__device__ __forceinline__ double dpp_f64(double v) {
+    int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), Ctrl, 0xF, 0xF, false);
+    int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), Ctrl, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+// DPP controls (gfx9): quad_perm and row rotate
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm:[1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm:[2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;    // row_ror:4
+constexpr int kDppRowRor8 = 0x128;    // row_ror:8
+
+// Sum over the 64 lanes; every lane gets the total.  Inside a 16-lane row: two quad
+// permutations and two row rotations (DPP, no LDS traffic); across rows: two xor shuffles.
+__device__ __forceinline__ double wave_sum(double v) {
+    v += dpp_f64<kDppQuadSwap1>(v);
+    v += dpp_f64<kDppQuadSwap2>(v);
+    v += dpp_f64<kDppRowRor4>(v);
+    v += dpp_f64<kDppRowRor8>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<kDppQuadSwap1>(v);
+    v += dpp_f32<kDppQuadSwap2>(v);
+    v += dpp_f32<kDppRowRor4>(v);
+    v += dpp_f32<kDppRowRor8>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Block sum of NV values per thread (blockDim.x a multiple of 64, at most 1024).  The
+// result is valid in thread 0.  `lds` holds 16 * NV slots.
+template <int NV, typename T>
+__device__ __forceinline__ void block_sum(T (&v)[NV], T* lds) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] = wave_sum(v[k]);
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) lds[wave * NV + k] = v[k];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            T s = lds[k];
+            for (int w = 1; w < nw; ++w) s += lds[w * NV + k];
+            v[k] = s;
+        }
+    }
+    __syncthreads();
+}
+
+// Destinations of a grid-wide sum: out.p[k][0] += total of value k.
+struct SumOuts {
+    double* p[4];
+};
+
+// Grid-wide sum with a sync-free second pass: every block writes its partials, takes a
+// ticket, and the block that takes the last ticket adds the partials in block order (a
+// fixed order, so the result does not depend on scheduling) to `*out.p[k]` and re-arms
+// the ticket.  `partials` holds gridDim * NV values.  Call from every thread of every block.
+template <int NV>
+__device__ __forceinline__ void grid_sum_into(double (&v)[NV], double* lds, double* partials,
+                                              unsigned int* ticket, SumOuts out) {
+    __shared__ bool is_last;
+    block_sum<NV>(v, lds);
+    const unsigned nb = gridDim.x * gridDim.y * gridDim.z;
+    const unsigned bid = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) partials[(size_t)bid * NV + k] = v[k];
+        __threadfence();
+        unsigned t = atomicAdd(ticket, 1u);
+        is_last = (t == nb - 1);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    double acc[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) acc[k] = 0.0;
+    // a strided, in-order walk per thread, then a fixed-shape tree: deterministic
+    for (unsigned b = threadIdx.x; b < nb; b += blockDim.x) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            acc[k] += __hip_atomic_load(&partials[(size_t)b * NV + k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    block_sum<NV>(acc, lds);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) out.p[k][0] = out.p[k][0] + acc[k];
+        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Periodic wrap of a coordinate that is at most one period outside [0, n).
+__device__ __forceinline__ int wrap1(int x, int n) { return x < 0 ? x + n : (x >= n ? x - n : x); }
+// Periodic wrap of any coordinate (floored modulus).
+__device__ __forceinline__ int wrapn(int x, int n) {
+    int r = x % n;
+    return r < 0 ? r + n : r;
+}
+
+}  // namespace stade

@@ -1,0 +1,228 @@
+"""ctypes bindings of libstade_hip.so and the generated-function mirrors built on them."""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent.parent
+_DEFAULT_LIB = _PKG / "lib" / "libstade_hip.so"
+
+
+class StadeHipError(RuntimeError):
+    """A nonzero return code of a libstade_hip entry point, with the library's message."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed with code {code}: {msg}")
+        self.code = code
+
+
+def lib_path() -> Path:
+    return Path(os.environ.get("STADE_HIP_LIB", str(_DEFAULT_LIB)))
+
+
+_lib = None
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+F64 = ctypes.c_double
+F64P = ctypes.POINTER(ctypes.c_double)
+U64P = ctypes.POINTER(ctypes.c_uint64)
+
+# C signatures: argument kinds in generated-function order.
+#   'a' device array pointer, 'i' Int64 by value, 'f' Float64 by value, 'r' host in/out
+#   Float64 (a scalar shadow), 's' stream (appended by the caller)
+ENTRY_POINTS: dict[str, str] = {
+    "stade_hip_affine_lsq_b": "aaaaaaaaaaaaii",
+    "stade_hip_affine_lsq_d": "aaaaaaaaaaaaii",
+    "stade_hip_affine_lsq_hv": "aaaaaaaaaaaaii" + "aaaaaaaaaaaa",
+    "stade_hip_diffusion2d_b": "aaaaaai",
+    "stade_hip_diffusion2d_d": "aaaaaai",
+    "stade_hip_diffusion2d_hv": "aaaaaai" + "aaaaaa",
+}
+
+_CT = {"a": P, "i": I64, "f": F64, "r": F64P}
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        path = lib_path()
+        if not path.exists():
+            raise RuntimeError(f"libstade_hip.so not found at {path}: build it with "
+                               f"`python stade.jl_amd/build.py` (or __graft_entry__.build())")
+        L = ctypes.CDLL(str(path))
+        L.stade_hip_last_error.restype = ctypes.c_char_p
+        L.stade_hip_version.restype = ctypes.c_char_p
+        L.stade_hip_stable_seed.restype = ctypes.c_uint64
+        L.stade_hip_stable_seed.argtypes = [ctypes.c_char_p]
+        L.stade_hip_rng_seed.argtypes = [ctypes.c_uint64, U64P]
+        L.stade_hip_rng_normal_f64.argtypes = [U64P, P, I64]
+        L.stade_hip_rng_uniform_f64.argtypes = [U64P, P, I64, F64, F64]
+        L.stade_hip_rng_int_range.argtypes = [U64P, P, I64, I64, I64]
+        for nm in ("stade_hip_rng_seed", "stade_hip_rng_normal_f64", "stade_hip_rng_uniform_f64",
+                   "stade_hip_rng_int_range", "stade_hip_free", "stade_hip_synchronize"):
+            getattr(L, nm).restype = ctypes.c_int32
+        L.stade_hip_free.argtypes = [P]
+        L.stade_hip_synchronize.argtypes = [P]
+        for nm, kinds in ENTRY_POINTS.items():
+            f = getattr(L, nm)
+            f.restype = ctypes.c_int32
+            f.argtypes = [_CT[k] for k in kinds] + [P]
+        _lib = L
+    return _lib
+
+
+def _check(fn: str, rc: int):
+    if rc != 0:
+        msg = lib().stade_hip_last_error().decode(errors="replace")
+        raise StadeHipError(fn, rc, msg)
+
+
+# ------------------------------------------------------------------------------------------
+# inputs: Julia's Xoshiro stream (host)
+# ------------------------------------------------------------------------------------------
+
+def stable_seed(name: str) -> int:
+    """`val_stable_seed(name)`: FNV-1a64 of the UTF-8 bytes."""
+    return int(lib().stade_hip_stable_seed(name.encode()))
+
+
+class Rng:
+    """`Random.Xoshiro(seed)` scalar draws (host, C++)."""
+
+    def __init__(self, seed: int):
+        self.state = (ctypes.c_uint64 * 4)()
+        _check("stade_hip_rng_seed", lib().stade_hip_rng_seed(ctypes.c_uint64(seed), self.state))
+
+
+def rng_normal(rng: Rng, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float64)
+    _check("stade_hip_rng_normal_f64", lib().stade_hip_rng_normal_f64(rng.state, out.ctypes.data, n))
+    return out
+
+
+def rng_uniform(rng: Rng, n: int, lo: float = 0.0, hi: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float64)
+    _check("stade_hip_rng_uniform_f64", lib().stade_hip_rng_uniform_f64(rng.state, out.ctypes.data, n, lo, hi))
+    return out
+
+
+def rng_int_range(rng: Rng, n: int, lo: int, hi: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int64)
+    _check("stade_hip_rng_int_range", lib().stade_hip_rng_int_range(rng.state, out.ctypes.data, n, lo, hi))
+    return out
+
+
+# ------------------------------------------------------------------------------------------
+# argument marshalling
+# ------------------------------------------------------------------------------------------
+
+def _stream_of(t):
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _arr(name: str, t, dtype, numel: int | None):
+    """Device pointer of a flat contiguous GPU tensor of the given dtype and length."""
+    import torch
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch tensor on a GPU, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: tensor is on {t.device}, not on a GPU (there is no CPU path)")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous (Julia column-major data, flat)")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{name}: length {t.numel()}, expected {numel}")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _int(name: str, v) -> int:
+    if isinstance(v, bool) or not isinstance(v, (int, np.integer)):
+        raise TypeError(f"{name}: expected an Int64, got {type(v).__name__}")
+    return int(v)
+
+
+def _call(fn: str, args: list, stream):
+    _check(fn, getattr(lib(), fn)(*args, stream))
+
+
+# ------------------------------------------------------------------------------------------
+# config 1: affine_lsq(loss, w, x, b, t, r, i_m, i_n)
+# ------------------------------------------------------------------------------------------
+
+def _f64():
+    import torch
+    return torch.float64
+
+
+def affine_lsq_b(loss, lossb, w, wb, x, xb, b, bb, t, tb, r, rb, i_m, i_n):
+    """Adjoint of affine_lsq (corpus/affine_lsq_b.jl); returns nothing."""
+    m, n = _int("i_m", i_m), _int("i_n", i_n)
+    d = _f64()
+    a = [_arr("loss", loss, d, 1), _arr("lossb", lossb, d, 1), _arr("w", w, d, m * n), _arr("wb", wb, d, m * n),
+         _arr("x", x, d, n), _arr("xb", xb, d, n), _arr("b", b, d, m), _arr("bb", bb, d, m),
+         _arr("t", t, d, m), _arr("tb", tb, d, m), _arr("r", r, d, m), _arr("rb", rb, d, m), m, n]
+    _call("stade_hip_affine_lsq_b", a, _stream_of(w))
+
+
+def affine_lsq_d(loss, lossd, w, wd, x, xd, b, bd, t, td, r, rd, i_m, i_n):
+    """Tangent of affine_lsq (corpus/affine_lsq_d.jl); returns nothing."""
+    m, n = _int("i_m", i_m), _int("i_n", i_n)
+    d = _f64()
+    a = [_arr("loss", loss, d, 1), _arr("lossd", lossd, d, 1), _arr("w", w, d, m * n), _arr("wd", wd, d, m * n),
+         _arr("x", x, d, n), _arr("xd", xd, d, n), _arr("b", b, d, m), _arr("bd", bd, d, m),
+         _arr("t", t, d, m), _arr("td", td, d, m), _arr("r", r, d, m), _arr("rd", rd, d, m), m, n]
+    _call("stade_hip_affine_lsq_d", a, _stream_of(w))
+
+
+def affine_lsq_hv(loss, lossb, w, wb, x, xb, b, bb, t, tb, r, rb, i_m, i_n,
+                  lossd, lossbd, wd, wbd, xd, xbd, bd, bbd, td, tbd, rd, rbd):
+    """HVP of affine_lsq (corpus/affine_lsq_hv.jl); returns nothing."""
+    m, n = _int("i_m", i_m), _int("i_n", i_n)
+    d = _f64()
+    a = [_arr("loss", loss, d, 1), _arr("lossb", lossb, d, 1), _arr("w", w, d, m * n), _arr("wb", wb, d, m * n),
+         _arr("x", x, d, n), _arr("xb", xb, d, n), _arr("b", b, d, m), _arr("bb", bb, d, m),
+         _arr("t", t, d, m), _arr("tb", tb, d, m), _arr("r", r, d, m), _arr("rb", rb, d, m), m, n,
+         _arr("lossd", lossd, d, 1), _arr("lossbd", lossbd, d, 1), _arr("wd", wd, d, m * n), _arr("wbd", wbd, d, m * n),
+         _arr("xd", xd, d, n), _arr("xbd", xbd, d, n), _arr("bd", bd, d, m), _arr("bbd", bbd, d, m),
+         _arr("td", td, d, m), _arr("tbd", tbd, d, m), _arr("rd", rd, d, m), _arr("rbd", rbd, d, m)]
+    _call("stade_hip_affine_lsq_hv", a, _stream_of(w))
+
+
+# ------------------------------------------------------------------------------------------
+# config 2: diffusion2d(loss, u, un, n)
+# ------------------------------------------------------------------------------------------
+
+def diffusion2d_b(loss, lossb, u, ub, un, unb, n):
+    """Adjoint of diffusion2d (corpus/diffusion2d_b.jl); returns nothing."""
+    n = _int("n", n)
+    d, c = _f64(), n * n
+    a = [_arr("loss", loss, d, 1), _arr("lossb", lossb, d, 1), _arr("u", u, d, c), _arr("ub", ub, d, c),
+         _arr("un", un, d, c), _arr("unb", unb, d, c), n]
+    _call("stade_hip_diffusion2d_b", a, _stream_of(u))
+
+
+def diffusion2d_d(loss, lossd, u, ud, un, und, n):
+    """Tangent of diffusion2d (corpus/diffusion2d_d.jl); returns nothing."""
+    n = _int("n", n)
+    d, c = _f64(), n * n
+    a = [_arr("loss", loss, d, 1), _arr("lossd", lossd, d, 1), _arr("u", u, d, c), _arr("ud", ud, d, c),
+         _arr("un", un, d, c), _arr("und", und, d, c), n]
+    _call("stade_hip_diffusion2d_d", a, _stream_of(u))
+
+
+def diffusion2d_hv(loss, lossb, u, ub, un, unb, n, lossd, lossbd, ud, ubd, und, unbd):
+    """HVP of diffusion2d (corpus/diffusion2d_hv.jl); returns nothing."""
+    n = _int("n", n)
+    d, c = _f64(), n * n
+    a = [_arr("loss", loss, d, 1), _arr("lossb", lossb, d, 1), _arr("u", u, d, c), _arr("ub", ub, d, c),
+         _arr("un", un, d, c), _arr("unb", unb, d, c), n,
+         _arr("lossd", lossd, d, 1), _arr("lossbd", lossbd, d, 1), _arr("ud", ud, d, c), _arr("ubd", ubd, d, c),
+         _arr("und", und, d, c), _arr("unbd", unbd, d, c)]
+    _call("stade_hip_diffusion2d_hv", a, _stream_of(u))

@@ -1,0 +1,227 @@
+"""`stade_hip_file(in_path, out_path; ...)`: Julia host code that runs generated STADE
+derivative code on libstade_hip.so.
+
+It keeps the shape of the reference's `stade_amdgpu_file(in_path, out_path; precision,
+reduction_threshold, inbounds, dead_scalars)` (/root/reference/src/STADE.jl:18604-18605,
+via `stade_gpu_file` 18571-18599): it reads one `.jl` written by `stade_adjoint_file`,
+`stade_tangent_file` or `stade_hvp_file` (`io_read_kernel_bundle` 17751) and writes one
+`.jl` (`io_write_gpu_file` 17844).  For every generated function of the input it writes a
+host function `<name>_hip` with the same arguments, the same in-place effects and the
+same return convention as the generated function (`agen_emit` 3672, `hvp_emit`
+6772-6779), whose body is one `ccall` into libstade_hip.so:
+
+* `initstacks_<k>_b_hip(sizes...)` allocates the pre-sized stacks as `ROCArray`s
+  (`cgen_stack_device_expr` 9798-9802) with the size formulas of the generated
+  `initstacks_<k>_b`;
+* `<k>_b_hip`, `<k>_d_hip`, `<k>_hv_hip` pass device pointers, Int64 sizes and scalar
+  values, return the scalar shadows, and raise `ErrorException` with the library's
+  message on a nonzero return code.
+
+The kernel is identified by its primal, which STADE copies verbatim into every generated
+file (the trailing `function <k>(...)` of each `_b/_d/_hv` file), compared after removing
+comments and blank lines with the primal of `stade.jl_amd/corpus/<k>.jl`.  A file whose
+primal matches no kernel the library implements is refused with the reason, as STADE
+refuses what it cannot port (e.g. 18532-18534).
+"""
+from __future__ import annotations
+
+import re
+from dataclasses import dataclass
+from pathlib import Path
+
+CORPUS = Path(__file__).resolve().parent.parent / "corpus"
+
+
+@dataclass(frozen=True)
+class Mode:
+    entry: str           # C entry point
+    args: tuple          # (julia name, kind) in generated-function order; kinds:
+                         #   'A' Float array, 'I' Int64, 'F' Float scalar by value,
+                         #   'R' Float scalar shadow (returned), 'S' Int64 stack, 'T' Float stack
+    returns: tuple = ()  # names returned, in order
+
+
+@dataclass(frozen=True)
+class KernelSpec:
+    name: str
+    eltype: str                    # Julia element type of the float arrays
+    modes: dict                    # 'b' | 'd' | 'hv' -> Mode
+    stacks: tuple = ()             # (name, eltype, julia size expression) of initstacks_<k>_b
+    stack_args: tuple = ()         # initstacks_<k>_b arguments
+
+
+def _a(*names):
+    return tuple((n, "A") for n in names)
+
+
+KERNELS: dict[str, KernelSpec] = {
+    "affine_lsq": KernelSpec(
+        "affine_lsq", "Float64",
+        {
+            "b": Mode("stade_hip_affine_lsq_b",
+                      _a("loss", "lossb", "w", "wb", "x", "xb", "b", "bb", "t", "tb", "r", "rb") + (("i_m", "I"), ("i_n", "I"))),
+            "d": Mode("stade_hip_affine_lsq_d",
+                      _a("loss", "lossd", "w", "wd", "x", "xd", "b", "bd", "t", "td", "r", "rd") + (("i_m", "I"), ("i_n", "I"))),
+            "hv": Mode("stade_hip_affine_lsq_hv",
+                       _a("loss", "lossb", "w", "wb", "x", "xb", "b", "bb", "t", "tb", "r", "rb") + (("i_m", "I"), ("i_n", "I"))
+                       + _a("lossd", "lossbd", "wd", "wbd", "xd", "xbd", "bd", "bbd", "td", "tbd", "rd", "rbd")),
+        }),
+    "diffusion2d": KernelSpec(
+        "diffusion2d", "Float64",
+        {
+            "b": Mode("stade_hip_diffusion2d_b", _a("loss", "lossb", "u", "ub", "un", "unb") + (("n", "I"),)),
+            "d": Mode("stade_hip_diffusion2d_d", _a("loss", "lossd", "u", "ud", "un", "und") + (("n", "I"),)),
+            "hv": Mode("stade_hip_diffusion2d_hv", _a("loss", "lossb", "u", "ub", "un", "unb") + (("n", "I"),)
+                       + _a("lossd", "lossbd", "ud", "ubd", "und", "unbd")),
+        }),
+}
+
+
+_FUNC_RE = re.compile(r"^function\s+([A-Za-z_][A-Za-z_0-9!]*)\s*\(([^)]*)\)", re.M)
+
+
+def _split_functions(text: str) -> dict[str, tuple[list[str], str]]:
+    """name -> (argument names, full text) of every top-level `function ... end`."""
+    out = {}
+    starts = [m for m in _FUNC_RE.finditer(text)]
+    for k, m in enumerate(starts):
+        end = starts[k + 1].start() if k + 1 < len(starts) else len(text)
+        body = text[m.start():end]
+        args = [a.split("::")[0].strip() for a in m.group(2).split(",") if a.strip()]
+        out.setdefault(m.group(1), (args, body))
+    return out
+
+
+def _normalise(fn_text: str) -> str:
+    lines = []
+    for ln in fn_text.splitlines():
+        ln = ln.split("#", 1)[0].strip()
+        if ln:
+            lines.append(re.sub(r"\s+", " ", ln))
+    # the generated copy of the primal may drop the final `return nothing`
+    while lines and lines[-1] in ("end",):
+        lines.pop()
+    if lines and lines[-1] == "return nothing":
+        lines.pop()
+    return "\n".join(lines)
+
+
+def _primal_fingerprint(name: str) -> str:
+    text = (CORPUS / f"{name}.jl").read_text()
+    funcs = _split_functions(text)
+    return _normalise(funcs[name][1])
+
+
+class StadeHipRefusal(ValueError):
+    """The input cannot be executed by libstade_hip: the message names the cause."""
+
+
+def identify(text: str) -> tuple[KernelSpec, dict]:
+    funcs = _split_functions(text)
+    for name, spec in KERNELS.items():
+        if name in funcs and _normalise(funcs[name][1]) == _primal_fingerprint(name):
+            return spec, funcs
+    names = ", ".join(sorted(funcs)) or "none"
+    raise StadeHipRefusal(f"no kernel implemented by libstade_hip matches the primal in this file "
+                          f"(functions found: {names}; implemented: {', '.join(sorted(KERNELS))})")
+
+
+def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, str]]) -> str:
+    T = spec.eltype
+    sig, types, vals = [], [], []
+    rets = []
+    for nm, kind in mode.args:
+        sig.append(nm)
+        if kind == "A":
+            types.append(f"Ptr{{{T}}}")
+            vals.append(f"pointer({nm})")
+        elif kind == "I":
+            types.append("Int64")
+            vals.append(f"Int64({nm})")
+        elif kind == "F":
+            types.append("Float64")
+            vals.append(f"Float64({nm})")
+        elif kind == "R":
+            types.append("Ref{Float64}")
+            vals.append(f"__r_{nm}")
+            rets.append(nm)
+    for nm, et in stacks:
+        sig.append(nm)
+        types.append(f"Ptr{{{et}}}")
+        vals.append(f"pointer({nm})")
+    types.append("Ptr{Cvoid}")
+    vals.append("AMDGPU.stream().stream")
+    arrays = [nm for nm, kind in mode.args if kind == "A"] + [nm for nm, _ in stacks]
+    lines = [f"function {fname}_hip({', '.join(sig)})"]
+    for nm in rets:
+        lines.append(f"    __r_{nm} = Ref{{Float64}}({nm})")
+    lines.append(f"    GC.@preserve {' '.join(arrays)} begin")
+    lines.append(f"        __rc = ccall((:{mode.entry}, libstade_hip), Int32,")
+    lines.append(f"                     ({', '.join(types)},),")
+    lines.append(f"                     {', '.join(vals)})")
+    lines.append("    end")
+    lines.append(f"    __rc == 0 || error(\"{mode.entry}: \", unsafe_string(ccall((:stade_hip_last_error, libstade_hip), Cstring, ())))")
+    if not rets:
+        lines.append("    return nothing")
+    elif len(rets) == 1:
+        lines.append(f"    return __r_{rets[0]}[]")
+    else:
+        lines.append("    return (" + ", ".join(f"__r_{r}[]" for r in rets) + ")")
+    lines.append("end")
+    return "\n".join(lines)
+
+
+def stade_hip_file(in_path, out_path, *, precision=None, lib_path: str | None = None) -> str:
+    """Write Julia host code for the generated functions of `in_path` into `out_path`.
+
+    `precision` mirrors `stade_amdgpu_file`'s keyword: `None` keeps the kernel's element
+    type; a precision the library does not implement for that kernel is refused.
+    Returns the written text.
+    """
+    text = Path(in_path).read_text()
+    spec, funcs = identify(text)
+    if precision not in (None, spec.eltype, "Float64" if spec.eltype == "Float64" else spec.eltype):
+        raise StadeHipRefusal(f"{spec.name}: libstade_hip implements {spec.eltype} only, precision={precision} requested")
+    libp = lib_path or "libstade_hip"
+    out = [
+        f"# Generated by stade_hip_file from {Path(in_path).name}: host functions for {spec.name}",
+        "# that run on libstade_hip.so (MI355X, gfx950) through ccall.  Arguments, in-place effects",
+        "# and return values are those of the generated functions they stand for.",
+        "using AMDGPU",
+        f"const libstade_hip = \"{libp}\"",
+        "",
+    ]
+    emitted = 0
+    for fname, (args, _) in funcs.items():
+        if fname.startswith("initstacks_"):
+            if spec.stacks:
+                sa = ", ".join(spec.stack_args)
+                out.append(f"function {fname}_hip({sa})")
+                names = []
+                for nm, et, size in spec.stacks:
+                    out.append(f"    {nm} = ROCArray{{{et}}}(undef, {size})")
+                    names.append(nm)
+                out.append("    return " + (names[0] if len(names) == 1 else "(" + ", ".join(names) + ")"))
+                out.append("end")
+            else:
+                out.append(f"function {fname}_hip({', '.join(args)})")
+                out.append("    return nothing")
+                out.append("end")
+            out.append("")
+            emitted += 1
+            continue
+        for mode_key in ("hv", "b", "d"):
+            if fname == f"{spec.name}_{mode_key}":
+                mode = spec.modes[mode_key]
+                want = [nm for nm, _ in mode.args] + [nm for nm, _, _ in spec.stacks if mode_key != "d"]
+                if args != want:
+                    raise StadeHipRefusal(f"{fname}: argument list {args} differs from the one libstade_hip implements {want}")
+                stacks = [(nm, et) for nm, et, _ in spec.stacks] if mode_key != "d" else []
+                out.append(_jl_call(spec, fname, mode, stacks))
+                out.append("")
+                emitted += 1
+    if emitted == 0:
+        raise StadeHipRefusal(f"{in_path}: no generated _b/_d/_hv function of {spec.name} found")
+    result = "\n".join(out)
+    Path(out_path).write_text(result)
+    return result

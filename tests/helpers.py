@@ -1,0 +1,158 @@
+"""Shared test helpers: oracle loading, seeded inputs, and the parity comparisons."""
+from __future__ import annotations
+
+import os
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+CORPUS = ROOT / "stade.jl_amd" / "corpus"
+REFERENCE = Path("/root/reference")
+REF_CORPUS = REFERENCE / "test" / "val-corpus"
+
+# parity bars of the north star: fp64 1e-12, fp32 1e-5 (relative, normwise)
+RTOL = {np.float64: 1e-12, np.float32: 1e-5}
+
+
+def oracle_lib(name: str, mode: str, precision: str = "f64"):
+    from oracle import runner
+    return runner.load(CORPUS / f"{name}_{mode}.jl", precision=precision)
+
+
+def rel_err(got, want) -> float:
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    if got.shape != want.shape:
+        raise AssertionError(f"shape {got.shape} != {want.shape}")
+    if want.size == 0:
+        return 0.0
+    scale = float(np.max(np.abs(want)))
+    diff = float(np.max(np.abs(got - want)))
+    if scale == 0.0:
+        return diff
+    return diff / scale
+
+
+def assert_close(name, got, want, rtol):
+    got = np.asarray(got)
+    want = np.asarray(want)
+    if np.all(want == 0):
+        assert np.all(got == 0), f"{name}: expected exact zeros, max |got| = {np.max(np.abs(got))}"
+        return
+    e = rel_err(got, want)
+    assert e <= rtol, f"{name}: relative error {e:.3e} > {rtol:.1e}"
+
+
+def normal(seed_name: str, n: int, salt: int = 0) -> np.ndarray:
+    from oracle import rng as jrng
+    g = jrng.Xoshiro(jrng.val_stable_seed(seed_name) + salt)
+    return jrng.val_randn(g, n)
+
+
+def gpu_available() -> bool:
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+def to_dev(a: np.ndarray):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a).ravel(order="F").copy()).to("cuda")
+
+
+def to_host(t) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def make_args(lib, fname: str, shapes: dict, ints: dict, scalars: dict, seed: str, fdt=np.float64,
+              int_arrays: dict | None = None):
+    """Seeded inputs for every argument of a generated function, in its own order.
+
+    Float arrays: N(0,1) from Julia's Xoshiro stream (one stream per argument position);
+    Float scalars: `scalars[name]` or N(0,1); Int64: `ints`; Int64 arrays: `int_arrays`.
+    Stacks (arguments sized by initstacks) are left out: the caller appends them.
+    """
+    from oracle import rng as jrng
+    info = lib.infos[fname]
+    out = []
+    base = jrng.val_stable_seed(seed)
+    for pos, (a, kind) in enumerate(info.args):
+        if a in (shapes.get("__stacks__") or ()):
+            continue
+        if kind == "i":
+            out.append((a, kind, int(ints[a])))
+        elif kind == "f":
+            if a in scalars:
+                out.append((a, kind, float(scalars[a])))
+            else:
+                out.append((a, kind, float(jrng.val_normal(jrng.Xoshiro(base + pos)))))
+        elif kind == "Ai":
+            out.append((a, kind, np.asarray(int_arrays[a], dtype=np.int64).copy()))
+        else:
+            shp = shapes[a]
+            shp = shp if isinstance(shp, tuple) else (shp,)
+            v = jrng.val_randn(jrng.Xoshiro(base + pos), int(np.prod(shp))).astype(fdt)
+            out.append((a, kind, np.asfortranarray(v.reshape(shp, order="F")) if len(shp) > 1 else v))
+    return out
+
+
+def run_parity(name: str, mode: str, shapes: dict, ints: dict, scalars: dict | None = None,
+               seed: str | None = None, precision: str = "f64", rtol: float | None = None,
+               stacks: tuple = (), int_arrays: dict | None = None, oracle=None):
+    """Run one generated function on the oracle and on libstade_hip with the same inputs;
+    compare every argument's final value and the returned scalars.  Returns the worst error."""
+    import stade_hip
+    import torch
+    scalars = scalars or {}
+    fdt = np.float32 if precision == "f32" else np.float64
+    rtol = rtol if rtol is not None else RTOL[fdt]
+    lib = oracle or oracle_lib(name, mode, precision)
+    fname = f"{name}_{mode}"
+    shp = dict(shapes)
+    shp["__stacks__"] = tuple(s for s, _ in stacks)
+    args = make_args(lib, fname, shp, ints, scalars, seed or f"{fname}-{ints}", fdt, int_arrays)
+    host = [v.copy(order="K") if isinstance(v, np.ndarray) else v for _, _, v in args]
+    dev = [torch.from_numpy(np.ascontiguousarray(v.ravel(order="F"))).to("cuda") if isinstance(v, np.ndarray) else v
+           for _, _, v in args]
+    stack_h, stack_d = [], []
+    for sname, (length, kind) in stacks:
+        if kind == "Ai":
+            stack_h.append(np.full(length, -7, dtype=np.int64))
+            stack_d.append(torch.full((length,), -7, dtype=torch.int64, device="cuda"))
+        else:
+            stack_h.append(np.full(length, np.nan, dtype=fdt))
+            stack_d.append(torch.full((length,), float("nan"), dtype=torch.float64 if fdt == np.float64 else torch.float32, device="cuda"))
+    ret_h = lib.call(fname, *host, *stack_h)
+    ret_d = getattr(stade_hip, fname)(*dev, *stack_d)
+    torch.cuda.synchronize()
+    if ret_d is None:
+        ret_d = ()
+    elif not isinstance(ret_d, tuple):
+        ret_d = (ret_d,)
+    worst = 0.0
+    for (a, kind, _), h, d in zip(args, host, dev):
+        if not isinstance(h, np.ndarray):
+            continue
+        got = to_host(d)
+        want = np.ravel(h, order="F")
+        if kind == "Ai":
+            assert np.array_equal(got, want), f"{fname}: Int64 array {a} differs"
+            continue
+        assert_close(f"{fname}:{a}", got, want, rtol)
+        worst = max(worst, rel_err(got, want))
+    for (sname, (length, kind)), h, d in zip(stacks, stack_h, stack_d):
+        got = to_host(d)
+        if kind == "Ai":
+            assert np.array_equal(got, h), f"{fname}: stack {sname} differs"
+        else:
+            wn, gn = np.isnan(h), np.isnan(got)
+            assert np.array_equal(wn, gn), f"{fname}: stack {sname} written at different slots"
+            assert_close(f"{fname}:{sname}", got[~gn], h[~wn], rtol)
+    assert len(ret_h) == len(ret_d), f"{fname}: {len(ret_d)} returned values, expected {len(ret_h)}"
+    for k, (h, d) in enumerate(zip(ret_h, ret_d)):
+        e = abs(d - h) / max(abs(h), 1e-300) if h != 0 else abs(d)
+        assert e <= max(rtol, 1e-300) or abs(d - h) <= rtol * 1e-3, f"{fname}: returned value {k}: {d} vs {h}"
+    return worst

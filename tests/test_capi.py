@@ -1,0 +1,62 @@
+"""The C ABI: the library loads without a GPU, exports every symbol the header declares, and
+rejects bad arguments with an error code and a message before any device work."""
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from helpers import ROOT
+
+HEADER = ROOT / "include" / "stade_hip.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(stade_hip_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    import stade_hip
+    path = stade_hip.lib_path()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (stade_hip_\w+)", out))
+    missing = [s for s in declared() if s not in exported]
+    assert not missing, missing
+    assert len(declared()) >= 15
+
+
+def test_python_entry_table_matches_header():
+    import stade_hip
+    for nm in stade_hip.ENTRY_POINTS:
+        assert nm in declared(), nm
+
+
+def _lib():
+    import stade_hip
+    return stade_hip.lib()
+
+
+def test_argument_errors_before_device_work():
+    L = _lib()
+    null = ctypes.c_void_p(0)
+    rc = L.stade_hip_diffusion2d_b(null, null, null, null, null, null, -1, null)
+    assert rc == -1 and b"negative" in L.stade_hip_last_error()
+    rc = L.stade_hip_diffusion2d_d(null, null, null, null, null, null, 50000, null)
+    assert rc == -3 and b"46340" in L.stade_hip_last_error()
+    rc = L.stade_hip_affine_lsq_b(*([null] * 12), -2, 3, null)
+    assert rc == -1 and b"negative" in L.stade_hip_last_error()
+    # zero-trip: n = 0 runs no loop and needs no device
+    assert L.stade_hip_diffusion2d_b(null, null, null, null, null, null, 0, null) == 0
+    assert L.stade_hip_affine_lsq_d(*([null] * 12), 0, 5, null) == 0
+
+
+def test_product_path_refuses_cpu_tensors():
+    import numpy as np
+    import torch
+    import stade_hip
+    t = torch.zeros(4, dtype=torch.float64)
+    with pytest.raises(ValueError, match="not on a GPU"):
+        stade_hip.diffusion2d_b(t[:1], t[:1], t, t, t, t, 2)
+    with pytest.raises(TypeError, match="Int64"):
+        stade_hip.diffusion2d_b(t[:1], t[:1], t, t, t, t, 2.0)

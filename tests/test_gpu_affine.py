@@ -1,0 +1,25 @@
+"""affine_lsq on the GPU against the oracle (the transpiled generated code), fp64 to 1e-12."""
+import pytest
+
+from helpers import run_parity
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [(1, 1), (3, 5), (64, 64), (65, 130), (200, 77), (1, 300), (300, 1), (1024, 1024)]
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("mn", SIZES)
+def test_affine_lsq_parity(mode, mn):
+    m, n = mn
+    shapes = {}
+    for k in ("w", "wb", "wd", "wbd"):
+        shapes[k] = (m, n)
+    for k in ("x", "xb", "xd", "xbd"):
+        shapes[k] = n
+    for k in ("b", "bb", "bd", "bbd", "t", "tb", "td", "tbd", "r", "rb", "rd", "rbd"):
+        shapes[k] = m
+    for k in ("loss", "lossb", "lossd", "lossbd"):
+        shapes[k] = 1
+    print(f"affine_lsq_{mode} m={m} n={n}", flush=True)
+    run_parity("affine_lsq", mode, shapes, dict(i_m=m, i_n=n))

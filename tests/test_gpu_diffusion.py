@@ -1,0 +1,22 @@
+"""diffusion2d on the GPU against the oracle (the transpiled generated code), fp64 to 1e-12.
+
+Sizes cover the degenerate periodic grids (n = 1, 2: coincident neighbours), grids smaller
+than a tile, ragged tiles, and the benchmark grid n = 4096."""
+import numpy as np
+import pytest
+
+from helpers import run_parity
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [1, 2, 3, 5, 35, 36, 64, 65, 100, 129, 257, 4096]
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("n", SIZES)
+def test_diffusion2d_parity(mode, n):
+    c = n * n
+    shapes = {k: c for k in ("u", "ub", "un", "unb", "ud", "und", "ubd", "unbd")}
+    shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
+    print(f"diffusion2d_{mode} n={n}", flush=True)
+    run_parity("diffusion2d", mode, shapes, dict(n=n))

@@ -1,0 +1,57 @@
+"""The input generator, pinned against the reference's known answers.
+
+/root/reference/test/validate_seed_stable.jl:37-56 holds fixed values of STADE's stable seed
+(FNV-1a) and of `val_randn` over Julia's `Random.Xoshiro(5)`.  Both the oracle's Python
+restatement and the library's C++ generator must reproduce them.
+"""
+import hashlib
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import rng as jrng
+
+
+def stat(a):
+    return [a[0], a[-1], float(np.sum(a)), float(np.sum(a * a))]
+
+
+KNOWN_RANDN = {
+    3: [2.416547687122585, -0.7958130054071307, 1.4808802847422582, 6.492580316065381],
+    1000: [2.416547687122585, 1.0908640603062327, -9.847881789408522, 1027.8518947088467],
+    100000: [2.416547687122585, 0.38438758377031407, 126.25860343825198, 100189.9995648914],
+}
+
+
+def test_stable_seed_known_answers():
+    assert jrng.val_stable_seed("abc") == 0xE71FA2190541574B
+    assert jrng.val_stable_seed("unet") == 0x64C1DFE4857EB8BB
+
+
+def test_xoshiro_rand3_fingerprint():
+    g = jrng.Xoshiro(5)
+    a = [g.rand() for _ in range(3)]
+    assert hashlib.sha256(struct.pack("<3d", *a)).hexdigest()[:12] == "28a825642733"
+
+
+@pytest.mark.parametrize("n", [3, 1000, 100000])
+def test_val_randn_known_answers(n):
+    a = jrng.val_randn(jrng.Xoshiro(5), n)
+    np.testing.assert_allclose(stat(a), KNOWN_RANDN[n], rtol=1e-9)
+
+
+def test_library_rng_matches_oracle_and_known_answers():
+    import stade_hip
+    assert stade_hip.stable_seed("abc") == 0xE71FA2190541574B
+    assert stade_hip.stable_seed("unet") == 0x64C1DFE4857EB8BB
+    a = stade_hip.rng_normal(stade_hip.api.Rng(5), 100000)
+    np.testing.assert_allclose(stat(a), KNOWN_RANDN[100000], rtol=1e-9)
+    b = jrng.val_randn(jrng.Xoshiro(5), 1000)
+    assert np.array_equal(a[:1000], b)
+    u = stade_hip.rng_uniform(stade_hip.api.Rng(5), 3)
+    assert hashlib.sha256(struct.pack("<3d", *u)).hexdigest()[:12] == "28a825642733"
+    big = (1 << 64) - 12345
+    x = stade_hip.rng_uniform(stade_hip.api.Rng(big), 50, -1.0, 1.0)
+    g = jrng.Xoshiro(big)
+    assert np.array_equal(x, jrng.rand_uniform(g, 50, -1.0, 1.0))
