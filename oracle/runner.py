@@ -30,7 +30,13 @@ from . import jl2c
 GEN_DIR = Path(__file__).resolve().parent / "_gen"
 CFLAGS = ["-O2", "-fno-fast-math", "-ffp-contract=off", "-fPIC", "-shared", "-std=gnu11",
           "-Wno-unused-variable", "-Wno-unused-label", "-Wno-unused-but-set-variable"]
-_lock = threading.Lock()
+_locks: dict[str, threading.Lock] = {}
+_locks_mu = threading.Lock()
+
+
+def _lock_for(path: Path) -> threading.Lock:
+    with _locks_mu:
+        return _locks.setdefault(str(path), threading.Lock())
 
 
 class JlArr(ctypes.Structure):
@@ -136,9 +142,12 @@ def load(src: str | os.PathLike, precision: str = "f64", bounds_check: bool = Tr
     ck = (key,)
     if ck in _cache:
         return _cache[ck]
-    GEN_DIR.mkdir(exist_ok=True)
-    so = GEN_DIR / f"{stem}_{precision}{'_bc' if bounds_check else ''}_{key}.so"
-    with _lock:
+    # builds of the reference's own corpus and of inline test texts are CPU-test only: kept
+    # apart from the config builds that the GPU box uses
+    gen = GEN_DIR if (p is not None and "/root/reference" not in str(p.resolve())) else GEN_DIR / "cpu_only"
+    gen.mkdir(parents=True, exist_ok=True)
+    so = gen / f"{stem}_{precision}{'_bc' if bounds_check else ''}_{key}.so"
+    with _lock_for(so):
         if not so.exists():
             c_path = so.with_suffix(".c")
             c_path.write_text(c_src)

@@ -226,8 +226,17 @@ __global__ __launch_bounds__(NT) void diffusion_hv_kernel(const double* __restri
 // pass 2 of the adjoint: the statement reset unb[idx] = 0.0 for every cell
 __global__ __launch_bounds__(NT) void zero2_kernel(double* __restrict__ a, double* __restrict__ b, size_t count) {
     size_t stride = (size_t)gridDim.x * NT * 2;
+    // 16-byte stores need 16-byte aligned bases (a view into a larger allocation may not be)
+    const bool vec = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
     for (size_t k = ((size_t)blockIdx.x * NT + threadIdx.x) * 2; k < count; k += stride) {
-        if (k + 1 < count) {
+        if (!vec) {
+            a[k] = 0.0;
+            if (b) b[k] = 0.0;
+            if (k + 1 < count) {
+                a[k + 1] = 0.0;
+                if (b) b[k + 1] = 0.0;
+            }
+        } else if (k + 1 < count) {
             *reinterpret_cast<double2*>(a + k) = make_double2(0.0, 0.0);
             if (b) *reinterpret_cast<double2*>(b + k) = make_double2(0.0, 0.0);
         } else {

@@ -42,12 +42,16 @@ def test_every_fixture_transpiles():
     from oracle import runner
     files = sorted(glob.glob(str(REF_CORPUS / "*_b.jl")) + glob.glob(str(REF_CORPUS / "*_d.jl")) + glob.glob(str(REF_CORPUS / "*_hv.jl")))
     assert len(files) >= 400
-    bad = []
-    for p in files:
+    import concurrent.futures as cf
+
+    def one(p):
         try:
             runner.load(p)
+            return None
         except Exception as e:  # noqa: BLE001
-            bad.append((os.path.basename(p), str(e)[:120]))
+            return (os.path.basename(p), str(e)[:120])
+    with cf.ThreadPoolExecutor(min(8, os.cpu_count() or 1)) as ex:
+        bad = [r for r in ex.map(one, files) if r is not None]
     assert not bad, bad
 
 
