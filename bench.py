@@ -201,6 +201,109 @@ class Affine(Workload):
                 "m": self.m, "n": self.n}
 
 
+class Burgers(Workload):
+    """Config 5: 2^20 periodic cells, 500 guarded steps, nu = 1e-3, dx = 1/n, dt such that
+    nu dt / dx^2 = 0.2; u0 = sin(2 pi x) + 0.1 N(0,1), x_i = (i - 1) / n; tend = 1 (every
+    step runs)."""
+    dtype = "f64"
+
+    def __init__(self, mode="b", n=1 << 20, nsteps=500):
+        self.mode, self.n, self.T = mode, n, nsteps
+        self.name = f"burgers1d_{mode}"
+        self.kernel = {"b": "burgers1d_bwd", "d": "burgers1d_fwd_hv", "hv": "burgers1d_bwd_hv"}[mode]
+        self.nu = 1e-3
+        self.dx = 1.0 / n
+        self.dt = 0.2 * self.dx * self.dx / self.nu
+        self.tend = 1.0
+
+    def _u0(self):
+        import numpy as np
+        import stade_hip
+        n = self.n
+        x = np.arange(n, dtype=np.float64) / n
+        rng = stade_hip.api.Rng(stade_hip.stable_seed("burgers1d"))
+        return np.sin(2.0 * np.pi * x) + 0.1 * stade_hip.rng_normal(rng, n)
+
+    def setup(self, dev):
+        import torch
+        import stade_hip
+        n = self.n
+        self.host_u = self._u0()
+        rng2 = stade_hip.api.Rng(stade_hip.stable_seed("burgers1d") + 1)
+        ud = stade_hip.rng_normal(rng2, n)
+        z = lambda: torch.zeros(n, dtype=torch.float64, device=dev)
+        self.t = dict(loss=torch.zeros(1, dtype=torch.float64, device=dev), lossb=torch.ones(1, dtype=torch.float64, device=dev),
+                      lossd=torch.zeros(1, dtype=torch.float64, device=dev), lossbd=torch.zeros(1, dtype=torch.float64, device=dev),
+                      u=_tensor(self.host_u, dev), ub=z(), un=z(), unb=z(), ud=_tensor(ud, dev), ubd=z(), und=z(), unbd=z())
+        if self.mode != "d":
+            self.stacks = stade_hip.initstacks_burgers1d_b(n, self.T, dev)
+
+    def step(self):
+        import stade_hip
+        t, n, T = self.t, self.n, self.T
+        if self.mode == "b":
+            stade_hip.burgers1d_b(t["loss"], t["lossb"], t["u"], t["ub"], t["un"], t["unb"], self.nu, 0.0, self.dt, 0.0,
+                                  self.dx, 0.0, self.tend, 0.0, n, T, *self.stacks)
+        elif self.mode == "d":
+            stade_hip.burgers1d_d(t["loss"], t["lossd"], t["u"], t["ud"], t["un"], t["und"], self.nu, 0.01, self.dt, 0.0,
+                                  self.dx, 0.0, self.tend, 0.0, n, T)
+        else:
+            stade_hip.burgers1d_hv(t["loss"], t["lossb"], t["u"], t["ub"], t["un"], t["unb"], self.nu, 0.0, self.dt, 0.0,
+                                   self.dx, 0.0, self.tend, 0.0, n, T, t["lossd"], t["lossbd"], t["ud"], t["ubd"], t["und"],
+                                   t["unbd"], 0.01, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, *self.stacks)
+
+    def _launches(self):
+        return -(-self.T // 32)
+
+    def algo_bytes(self):
+        n, T = self.n, self.T
+        if self.mode == "b":   # tape W + R, u R, un W, ub RW, unb RW
+            return 8 * (2 * T * n + 6 * n)
+        if self.mode == "d":   # u, ud R+W (advanced in place), un, und W
+            return 8 * (6 * n)
+        return 8 * (4 * T * n + 12 * n)
+
+    def kernel_bytes(self):
+        # per launch of the dominant kernel, averaged over the chunks: the tape rows it moves
+        # plus one read and one write of its state vectors
+        n, T, L = self.n, self.T, self._launches()
+        if self.mode == "b":
+            return 8 * (T * n + 2 * n * L) / L
+        if self.mode == "d":
+            return 8 * (4 * n * L) / L
+        return 8 * (2 * T * n + 4 * n * L) / L
+
+    def config(self):
+        return {"workload": f"burgers1d_{self.mode}: 1-D viscous Burgers, {self.n} periodic cells fp64, {self.T} steps in a "
+                            f"counted loop with a guard, nu=1e-3, u0=sin(2 pi x)+0.1 N(0,1), loss=sum(u_T^2)",
+                "n": self.n, "nsteps": self.T, "tape_bytes": 8 * self.T * self.n}
+
+    def cpu_sample(self):
+        import numpy as np
+        from oracle import runner
+        Ts = 20
+        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"burgers1d_{self.mode}.jl", bounds_check=False)
+        n = self.n
+        scale = Ts / self.T
+
+        def run():
+            u = self.host_u.copy()
+            z = lambda: np.zeros(n)
+            if self.mode == "d":
+                lib.call("burgers1d_d", np.zeros(1), np.zeros(1), u, np.ones(n), z(), z(), self.nu, 0.01, self.dt, 0.0,
+                         self.dx, 0.0, self.tend, 0.0, n, Ts)
+            else:
+                st = lib.stacks("initstacks_burgers1d_b", n, Ts, fill_nan=False)
+                if self.mode == "b":
+                    lib.call("burgers1d_b", np.zeros(1), np.ones(1), u, z(), z(), z(), self.nu, 0.0, self.dt, 0.0, self.dx, 0.0,
+                             self.tend, 0.0, n, Ts, *st)
+                else:
+                    lib.call("burgers1d_hv", np.zeros(1), np.ones(1), u, z(), z(), z(), self.nu, 0.0, self.dt, 0.0, self.dx, 0.0,
+                             self.tend, 0.0, n, Ts, np.zeros(1), np.zeros(1), np.ones(n), z(), z(), z(), 0.01, 0.0, 0.0, 0.0,
+                             0.0, 0.0, 0.0, 0.0, *st)
+        return run, f"burgers1d_{self.mode} on {n} cells for {Ts} of the {self.T} steps (time x {1/scale:.0f})", scale
+
+
 WORKLOADS = {
     "diffusion2d_b": lambda: Diffusion("b"),
     "diffusion2d_d": lambda: Diffusion("d"),
@@ -208,6 +311,9 @@ WORKLOADS = {
     "affine_lsq_b": lambda: Affine("b"),
     "affine_lsq_d": lambda: Affine("d"),
     "affine_lsq_hv": lambda: Affine("hv"),
+    "burgers1d_b": lambda: Burgers("b"),
+    "burgers1d_d": lambda: Burgers("d"),
+    "burgers1d_hv": lambda: Burgers("hv"),
 }
 HEADLINE = "diffusion2d_b"
 
@@ -261,7 +367,8 @@ def cpu_baseline(wl: Workload, budget_s: float = 12.0, max_runs: int = 30) -> di
     sample = wl.cpu_sample()
     if sample is None:
         return None
-    run, desc = sample
+    run, desc = sample[0], sample[1]
+    scale = sample[2] if len(sample) > 2 else 1.0   # the sample's share of one evaluation
     try:
         cpus = sorted(os.sched_getaffinity(0))
         os.sched_setaffinity(0, {cpus[0]})
@@ -288,7 +395,7 @@ def cpu_baseline(wl: Workload, budget_s: float = 12.0, max_runs: int = 30) -> di
                 break
     except OSError:
         pass
-    return {"value": 1.0 / med, "unit": "evals/s", "cores": 1, "kind": "port",
+    return {"value": scale / med, "unit": "evals/s", "cores": 1, "kind": "port",
             "sample": f"{desc}: median of {len(times)} runs of the oracle (generated Julia text transpiled to C, "
                       f"gcc -O2, 1 thread pinned to one core, {cpu_model})"}
 
@@ -319,7 +426,10 @@ def main():
             if nm == args.workload:
                 continue
             wl = mk()
-            others[nm] = measure(wl, max(5, args.steps // 2), max(2, args.warmup), dev)
+            heavy = nm.startswith("burgers1d")
+            others[nm] = measure(wl, 5 if heavy else max(5, args.steps // 2), 1 if heavy else max(2, args.warmup), dev)
+            if not args.no_cpu_baseline:
+                others[nm]["cpu_baseline"] = cpu_baseline(wl, budget_s=4.0, max_runs=5)
             del wl
             torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline(head)

@@ -98,6 +98,29 @@ int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double
                                  int64_t n, double* lossd, const double* lossbd, const double* ud, double* ubd, double* und,
                                  double* unbd, hipStream_t stream);
 
+/* ---- config 5: burgers1d(loss, u, un, nu, dt, dx, tend, n, nsteps) ------------------------
+ * explicit viscous Burgers on n periodic cells, at most nsteps steps, each taken while the
+ * elapsed time is below tend (a counted loop with a guard), then loss += sum(u .^ 2).
+ * replaces initstacks_burgers1d_b / burgers1d_b_amdgpu / _d_amdgpu / _hv_amdgpu
+ * (corpus/burgers1d_{b,d,hv}.jl).  Stacks: branch_stack Int64[nsteps] (1 = step taken),
+ * u_stack Float64[nsteps * n] with u_stack[(x-1) + (t-1)*n + 1] = state at the start of step t
+ * (`agen_local_position` /root/reference/src/STADE.jl:4867-4881).  The HVP's shadow tape
+ * (`u_stack_d`, allocated inside the generated _hv, 6864-6866) is library scratch. */
+int32_t stade_hip_burgers1d_stack_lengths(int64_t n, int64_t nsteps, int64_t lengths[2]);
+int32_t stade_hip_initstacks_burgers1d_b(int64_t n, int64_t nsteps, int64_t** branch_stack, double** u_stack);
+int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                              double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
+                              int64_t n, int64_t nsteps, int64_t* branch_stack, double* u_stack, hipStream_t stream);
+int32_t stade_hip_burgers1d_d(double* loss, double* lossd, double* u, double* ud, double* un, double* und, double nu, double nud,
+                              double dt, double dtd, double dx, double dxd, double tend, double tendd, int64_t n, int64_t nsteps,
+                              hipStream_t stream);
+int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                               double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
+                               int64_t n, int64_t nsteps, double* lossd, const double* lossbd, const double* ud, double* ubd,
+                               double* und, double* unbd, double nud, double* nubd, double dtd, double* dtbd, double dxd,
+                               double* dxbd, double tendd, double* tendbd, int64_t* branch_stack, double* u_stack,
+                               hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,7 +61,7 @@ struct FinishArgs {
 };
 
 template <int M>
-__global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partials, unsigned* ticket) {
+__global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partials) {
     __shared__ double red[32];
     const int i = blockIdx.x * NT + threadIdx.x;
     double acc[2] = {0.0, 0.0};
@@ -101,9 +101,9 @@ __global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partia
     }
     if (M == ADJ) {
         double v[1] = {acc[0]};
-        grid_sum_into<1>(v, red, partials, ticket, SumOuts{{a.loss}});
+        block_partials<1>(v, red, partials);
     } else {
-        grid_sum_into<2>(acc, red, partials, ticket, SumOuts{{a.loss, a.lossd}});
+        block_partials<2>(acc, red, partials);
     }
 }
 
@@ -112,7 +112,16 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
                                                   double* __restrict__ wb, double* __restrict__ wbd,
                                                   const double* __restrict__ x, const double* __restrict__ xd,
                                                   const double* __restrict__ S, const double* __restrict__ Sd,
-                                                  double* __restrict__ XP, double* __restrict__ XPd, int m, int n) {
+                                                  double* __restrict__ XP, double* __restrict__ XPd, int m, int n,
+                                                  const double* partials, int nparts, SumOuts outs) {
+    __shared__ double red[32];
+    // second stage of the loss sums of finish_kernel, in the first block
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        if (M == ADJ)
+            finalize_partials<1>(partials, nparts, red, outs);
+        else
+            finalize_partials<2>(partials, nparts, red, outs);
+    }
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int rtile = blockIdx.y, i = rtile * RT + lane;
     const int j0 = blockIdx.x * CT + wv * CW;
@@ -187,11 +196,21 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
     fa.Sd = Sd;
     fa.m = (int)m;
     fa.nchunks = nchunks;
-    STADE_TIMED("affine_finish", stream, finish_kernel<M><<<(unsigned)((m + NT - 1) / NT), NT, 0, stream>>>(fa, ws->partials, ws->tickets + 1));
+    const int nfin = (int)((m + NT - 1) / NT);
+    STADE_TIMED("affine_finish", stream, finish_kernel<M><<<(unsigned)nfin, NT, 0, stream>>>(fa, ws->partials));
     STADE_LAUNCHED("affine finish_kernel");
-    if (M == TAN || n == 0) return STADE_HIP_OK;
+    SumOuts outs{{fa.loss, fa.lossd}};
+    if (M == TAN || n == 0) {
+        if (M == ADJ)
+            finalize_kernel<1><<<1, NT, 0, stream>>>(ws->partials, nfin, outs);
+        else
+            finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, nfin, outs);
+        STADE_LAUNCHED("affine finalize_kernel");
+        return STADE_HIP_OK;
+    }
     STADE_TIMED("affine_cols", stream,
-                cols_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, S, Sd, XP, XPd, (int)m, (int)n));
+                cols_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, S, Sd, XP, XPd, (int)m, (int)n,
+                                                                          ws->partials, nfin, outs));
     STADE_LAUNCHED("affine cols_kernel");
     STADE_TIMED("affine_xfinish", stream, xfinish_kernel<M><<<(unsigned)((n + NT - 1) / NT), NT, 0, stream>>>(xb, xbd, XP, XPd, (int)n, mtiles));
     STADE_LAUNCHED("affine xfinish_kernel");

@@ -1,0 +1,617 @@
+// burgers1d: tangent, adjoint and HVP of explicit 1-D viscous Burgers time stepping with a
+// counted, guarded time loop, then loss += sum(u_T .^ 2).
+//
+// Generated code this replaces: stade.jl_amd/corpus/burgers1d_{b,d,hv}.jl.  Under
+// `stade_amdgpu_file` the time loop stays on the host (a loop containing stack operations is
+// not split, /root/reference/src/STADE.jl:8212-8225, 10613-10615) and issues one launch per
+// inner loop per step: about 2 x 2 x nsteps launches per adjoint, each moving one 8 MiB row.
+//
+// Tape: u_stack[((x - 1) + (t - 1) * n) + 1] (the cell loop is the fastest digit,
+// `agen_local_position` 4867-4881) holds the state at the start of step t; branch_stack[t]
+// holds the guard's outcome (Int64, bit-exact).  The guard `tc < tend` with tc += dt only on
+// taken steps is evaluated on the host with the same IEEE double operations, so the taken
+// steps are a prefix 1..nrun of the loop.
+//
+// Kernels (one block owns S consecutive cells and carries a K-cell halo on each side):
+//   * forward chunk: K time steps in LDS (the valid region shrinks by one cell per step), the
+//     owned part of every state written to the tape; HBM traffic is the tape rows (written
+//     once) plus one state read and write per chunk.
+//   * backward init: w = unb + (ub + (2 u_T) lossb), loss += sum u_T^2, unb = 0 (pointwise).
+//   * backward chunk: K steps of the transposed stencil in gathered (owner-computes) form,
+//     reading tape rows; the scalar shadows of the two coefficients are per-thread sums over
+//     owned cells and steps, then a deterministic grid sum.
+#include "internal.hpp"
+#include "../../include/stade_hip.h"
+
+#include <math.h>
+
+namespace stade {
+namespace {
+
+constexpr int NT = 256, KMAX = 32;
+
+struct Coef {
+    double cadv, cdif, cadvd, cdifd;
+};
+
+__device__ __forceinline__ double step_u(double um, double uc, double up, const Coef& c) {
+    // uc - cadv * uc * (u[ip] - u[im]) + cdif * (u[ip] - 2.0 * uc + u[im])
+    return (uc - (c.cadv * uc) * (up - um)) + c.cdif * ((up - 2.0 * uc) + um);
+}
+
+__device__ __forceinline__ double step_ud(double um, double uc, double up, double dm, double dc, double dp, const Coef& c) {
+    double h1 = up - um;
+    double h2 = (up - 2.0 * uc) + um;
+    double t = ((uc * h1) * c.cadvd + (c.cadv * h1) * dc) + (c.cadv * uc) * (dp + -dm);
+    return (dc + -t) + (h2 * c.cdifd + c.cdif * ((dp + -(2.0 * dc)) + dm));
+}
+
+// ---------------------------------------------------------------------------------------
+// forward: `nk` steps starting at 0-based step t0, from src (+ srcd) to dst (+ dstd)
+// ---------------------------------------------------------------------------------------
+template <bool TAN, int S>
+__global__ __launch_bounds__(NT) void fwd_kernel(const double* __restrict__ src, const double* __restrict__ srcd,
+                                                 double* __restrict__ dst, double* __restrict__ dstd,
+                                                 double* __restrict__ tape, double* __restrict__ taped, int n, int64_t t0,
+                                                 int nk, Coef c) {
+    constexpr int L = S + 2 * KMAX;
+    __shared__ double A[2][L];
+    __shared__ double D[TAN ? 2 : 1][TAN ? L : 1];
+    const int x0 = blockIdx.x * S;
+    const int len = nk == 0 ? S : S + 2 * nk;  // extended region [x0 - nk, x0 + S + nk)
+    const int own = min(S, n - x0);
+    for (int e = threadIdx.x; e < len; e += NT) {
+        int x = wrapn(x0 - nk + e, n);
+        A[0][e] = src[x];
+        if (TAN) D[0][e] = srcd[x];
+    }
+    __syncthreads();
+    int cur = 0;
+    for (int k = 0; k < nk; ++k) {
+        const size_t row = (size_t)(t0 + k) * (size_t)n;
+        if (tape) {
+            for (int e = threadIdx.x; e < own; e += NT) {
+                tape[row + x0 + e] = A[cur][nk + e];
+                if (TAN && taped) taped[row + x0 + e] = D[cur][nk + e];
+            }
+        }
+        for (int e = k + 1 + threadIdx.x; e < len - k - 1; e += NT) {
+            double um = A[cur][e - 1], uc = A[cur][e], up = A[cur][e + 1];
+            if (TAN) D[cur ^ 1][e] = step_ud(um, uc, up, D[cur][e - 1], D[cur][e], D[cur][e + 1], c);
+            A[cur ^ 1][e] = step_u(um, uc, up, c);
+        }
+        __syncthreads();
+        cur ^= 1;
+    }
+    for (int e = threadIdx.x; e < own; e += NT) {
+        dst[x0 + e] = A[cur][nk + e];
+        if (TAN) dstd[x0 + e] = D[cur][nk + e];
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// backward init: loss (+ lossd), the first adjoint state w (+ wd), unb (+ unbd) reset.
+// When no step ran (nrun = 0) this is the whole reverse sweep: ub += (2 u) lossb.
+// ---------------------------------------------------------------------------------------
+template <bool HV>
+__global__ __launch_bounds__(NT) void bwd_init_kernel(const double* __restrict__ uT, const double* __restrict__ udT,
+                                                      double* __restrict__ ub, double* __restrict__ ubd,
+                                                      double* __restrict__ unb, double* __restrict__ unbd,
+                                                      double* __restrict__ w, double* __restrict__ wd,
+                                                      const double* __restrict__ lossb, const double* __restrict__ lossbd,
+                                                      int n, int ran, double* dscal, double* partials) {
+    __shared__ double red[32];
+    if (blockIdx.x == 0 && threadIdx.x < 4) dscal[threadIdx.x] = 0.0;
+    const double lb = lossb[0];
+    const double lbd = HV ? lossbd[0] : 0.0;
+    double acc[2] = {0.0, 0.0};
+    for (int x = blockIdx.x * NT + threadIdx.x; x < n; x += gridDim.x * NT) {
+        double u = uT[x];
+        acc[0] += u * u;
+        double g = ub[x] + (2.0 * u) * lb;
+        double gd = 0.0;
+        if (HV) {
+            double ud = udT[x];
+            acc[1] += (2.0 * u) * ud;
+            gd = ubd[x] + (lb * (2.0 * ud) + (2.0 * u) * lbd);
+        }
+        if (ran) {
+            w[x] = unb[x] + g;
+            unb[x] = 0.0;
+            if (HV) {
+                wd[x] = unbd[x] + gd;
+                unbd[x] = 0.0;
+            }
+        } else {
+            ub[x] = g;
+            if (HV) ubd[x] = gd;
+        }
+    }
+    if (HV) {
+        block_partials<2>(acc, red, partials);
+    } else {
+        double v[1] = {acc[0]};
+        block_partials<1>(v, red, partials);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// backward chunk: nk steps, descending from 0-based step t_hi.  Per cell y of the new state:
+//   ub[y] = B(y+1) + C(y+1) + own(y) + A(y-1) + C(y-1)   (the generated statement order of
+// the interior, with A/B/C the contributions a cell sends to its east/west neighbours)
+// ---------------------------------------------------------------------------------------
+template <bool HV, int S>
+__global__ __launch_bounds__(NT) void bwd_kernel(const double* __restrict__ win, const double* __restrict__ wind,
+                                                 double* __restrict__ vout, double* __restrict__ voutd,
+                                                 const double* __restrict__ tape, const double* __restrict__ taped, int n,
+                                                 int64_t t_hi, int nk, Coef c, double* partials) {
+    constexpr int L = S + 2 * KMAX;
+    __shared__ double W[2][L];
+    __shared__ double U[L];
+    __shared__ double WD[HV ? 2 : 1][HV ? L : 1];
+    __shared__ double UD[HV ? L : 1];
+    __shared__ double red[32];
+    const int x0 = blockIdx.x * S;
+    const int len = S + 2 * nk;
+    const int own = min(S, n - x0);
+    for (int e = threadIdx.x; e < len; e += NT) {
+        int x = wrapn(x0 - nk + e, n);
+        W[0][e] = win[x];
+        if (HV) WD[0][e] = wind[x];
+    }
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};  // cadvb, cdifb, cadvbd, cdifbd
+    int cur = 0;
+    for (int k = 0; k < nk; ++k) {
+        const size_t row = (size_t)(t_hi - k) * (size_t)n;
+        for (int e = k + threadIdx.x; e < len - k; e += NT) {
+            int x = wrapn(x0 - nk + e, n);
+            U[e] = tape[row + x];
+            if (HV) UD[e] = taped[row + x];
+        }
+        __syncthreads();
+        for (int e = k + 1 + threadIdx.x; e < len - k - 1; e += NT) {
+            const double* Wc = W[cur];
+            // contributions of the three cells e-1, e, e+1
+            double um1 = U[e - 1], uc = U[e], up1 = U[e + 1];
+            double wm = Wc[e - 1], wc = Wc[e], wp = Wc[e + 1];
+            // cell e+1 -> west neighbour e:  B = -(c5 * c4), C = cdif * w
+            double c4p = -wp, c5p = c.cadv * up1;
+            double Bp = -(c5p * c4p), Cp = c.cdif * wp;
+            // cell e-1 -> east neighbour e: A = c5 * c4
+            double c4m = -wm, c5m = c.cadv * um1;
+            double Am = c5m * c4m, Cm = c.cdif * wm;
+            // own: ucb = ((w + (cadv * c3) * c4) + 2.0 * -(cdif * w))
+            double c3 = up1 - um1, c4 = -wc;
+            double h7 = c.cadv * c3;
+            double c6 = c.cdif * wc;
+            double own_ = ((0.0 + wc) + h7 * c4) + 2.0 * -c6;
+            double s = ((((0.0 + Bp) + Cp) + own_) + Am) + Cm;
+            double sd = 0.0;
+            const bool owned = e >= nk && e < nk + own;
+            if (owned) {
+                acc[0] += (uc * c3) * c4;
+                acc[1] += ((up1 - 2.0 * uc) + um1) * wc;
+            }
+            if (HV) {
+                const double* WDc = WD[cur];
+                double dm1 = UD[e - 1], dc = UD[e], dp1 = UD[e + 1];
+                double wdm = WDc[e - 1], wdc = WDc[e], wdp = WDc[e + 1];
+                // east neighbour e+1's contributions to e
+                double c4pd = -wdp, c5pd = up1 * c.cadvd + c.cadv * dp1;
+                double h8p = c4p * c5pd + c5p * c4pd;
+                double Bpd = -h8p, Cpd = wp * c.cdifd + c.cdif * wdp;
+                // west neighbour e-1's contributions to e
+                double c4md = -wdm, c5md = um1 * c.cadvd + c.cadv * dm1;
+                double Amd = c4m * c5md + c5m * c4md, Cmd = wm * c.cdifd + c.cdif * wdm;
+                // own
+                double c3d = dp1 + -dm1, c4d = -wdc;
+                double c6d = wc * c.cdifd + c.cdif * wdc;
+                double ownd = ((0.0 + wdc) + (c4 * (c3 * c.cadvd + c.cadv * c3d) + h7 * c4d)) + 2.0 * -c6d;
+                sd = ((((0.0 + Bpd) + Cpd) + ownd) + Amd) + Cmd;
+                WD[cur ^ 1][e] = sd;
+                if (owned) {
+                    double h6 = uc * c3;
+                    acc[2] += c4 * (c3 * dc + uc * c3d) + h6 * c4d;
+                    double h9 = (up1 - 2.0 * uc) + um1;
+                    double h9d = (dp1 + -(2.0 * dc)) + dm1;
+                    acc[3] += wc * h9d + h9 * wdc;
+                }
+            }
+            W[cur ^ 1][e] = s;
+        }
+        __syncthreads();
+        cur ^= 1;
+    }
+    for (int e = threadIdx.x; e < own; e += NT) {
+        vout[x0 + e] = W[cur][nk + e];
+        if (HV) voutd[x0 + e] = WD[cur][nk + e];
+    }
+    if (HV) {
+        block_partials<4>(acc, red, partials);
+    } else {
+        double v[2] = {acc[0], acc[1]};
+        block_partials<2>(v, red, partials);
+    }
+}
+
+// second stage of the reverse sweep's sums: block 0 the loss (init kernel's partials),
+// block 1 the coefficient shadows (all backward chunks' partials, in chunk order)
+template <bool HV>
+__global__ __launch_bounds__(NT) void bwd_finalize_kernel(const double* pinit, int ninit, SumOuts loss_out,
+                                                          const double* pbwd, int nbwd, SumOuts scal_out) {
+    __shared__ double red[64];
+    if (blockIdx.x == 0) {
+        if (HV)
+            finalize_partials<2>(pinit, ninit, red, loss_out);
+        else
+            finalize_partials<1>(pinit, ninit, red, loss_out);
+    } else {
+        if (HV)
+            finalize_partials<4>(pbwd, nbwd, red, scal_out);
+        else
+            finalize_partials<2>(pbwd, nbwd, red, scal_out);
+    }
+}
+
+// tangent: loss += sum u^2, lossd += sum (2 u) ud over the final state
+__global__ __launch_bounds__(NT) void loss2_kernel(const double* __restrict__ u, const double* __restrict__ ud, int n,
+                                                   double* partials) {
+    __shared__ double red[32];
+    double acc[2] = {0.0, 0.0};
+    for (int x = blockIdx.x * NT + threadIdx.x; x < n; x += gridDim.x * NT) {
+        double v = u[x];
+        acc[1] += (2.0 * v) * ud[x];
+        acc[0] += v * v;
+    }
+    block_partials<2>(acc, red, partials);
+}
+
+__global__ __launch_bounds__(NT) void branch_kernel(int64_t* __restrict__ b, int64_t nsteps, int64_t nrun) {
+    for (int64_t t = (int64_t)blockIdx.x * NT + threadIdx.x; t < nsteps; t += (int64_t)gridDim.x * NT) b[t] = t < nrun ? 1 : 0;
+}
+
+__global__ __launch_bounds__(NT) void copy2_kernel(const double* __restrict__ a, double* __restrict__ ao,
+                                                   const double* __restrict__ b, double* __restrict__ bo, int n) {
+    for (int x = blockIdx.x * NT + threadIdx.x; x < n; x += gridDim.x * NT) {
+        ao[x] = a[x];
+        if (b) bo[x] = b[x];
+    }
+}
+
+// the guard: how many leading steps run (tc < tend, tc += dt on taken steps), as the text does
+int64_t taken_steps(double dt, double tend, int64_t nsteps) {
+    double tc = 0.0;
+    int64_t k = 0;
+    for (int64_t t = 0; t < nsteps; ++t) {
+        if (tc < tend) {
+            tc = tc + dt;
+            ++k;
+        }
+    }
+    return k;
+}
+
+double* g_host_scal = nullptr;
+
+int32_t host_scalars(double** out) {
+    if (!g_host_scal) {
+        hipError_t e = hipHostMalloc((void**)&g_host_scal, 8 * sizeof(double), hipHostMallocDefault);
+        if (e != hipSuccess) return check_hip(e, "hipHostMalloc");
+    }
+    *out = g_host_scal;
+    return STADE_HIP_OK;
+}
+
+unsigned grid_for(int n, int per_block) { return (unsigned)((n + per_block - 1) / per_block); }
+
+int32_t check(int64_t n, int64_t nsteps, const char* fn) {
+    if (n < 0 || nsteps < 0) return set_error(STADE_HIP_EINVAL, "%s: negative size (n = %lld, nsteps = %lld)", fn, (long long)n, (long long)nsteps);
+    if (n > (1LL << 30)) return set_error(STADE_HIP_ERANGE, "%s: n = %lld exceeds 2^30 cells", fn, (long long)n);
+    if (grid_for((int)n, 2048) * 4 > (unsigned)kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: n too large for the workspace", fn);
+    return STADE_HIP_OK;
+}
+
+// forward sweep over steps [0, nrun): src (+d) -> final state in fin (+d); tape rows written
+template <bool TAN>
+int32_t forward(const double* src, const double* srcd, double* fin, double* find, double* tape, double* taped, int n,
+                int64_t nrun, const Coef& c, double* P, double* Q, double* Pd, double* Qd, hipStream_t stream) {
+    constexpr int S = 4096;
+    const unsigned nb = grid_for(n, S);
+    const double *cs = src, *csd = srcd;
+    int64_t t0 = 0;
+    int flip = 0;
+    while (t0 < nrun) {
+        int nk = (int)((nrun - t0) < KMAX ? (nrun - t0) : KMAX);
+        bool last = t0 + nk >= nrun;
+        double* d = last ? fin : (flip ? Q : P);
+        double* dd = last ? find : (flip ? Qd : Pd);
+        STADE_TIMED(TAN ? "burgers1d_fwd_hv" : "burgers1d_fwd", stream,
+                    fwd_kernel<TAN, S><<<nb, NT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c));
+        STADE_LAUNCHED("burgers1d fwd_kernel");
+        cs = d;
+        csd = dd;
+        flip ^= 1;
+        t0 += nk;
+    }
+    return STADE_HIP_OK;
+}
+
+// reduction partials: the init kernel's at offset 0, the backward chunks' after it
+constexpr int kInitBlockCells = NT * 8;
+int init_blocks(int64_t n) { return (int)grid_for((int)n, kInitBlockCells); }
+size_t bwd_offset(int64_t n) { return ((size_t)init_blocks(n) * 2 + 1023) / 1024 * 1024; }
+template <bool HV>
+int bwd_blocks(int64_t n) { return (int)grid_for((int)n, HV ? 2048 : 4096); }
+template <bool HV>
+int32_t check_partials(int64_t n, int64_t nrun, const char* fn) {
+    const int64_t chunks = (nrun + KMAX - 1) / KMAX;
+    const int64_t need = (int64_t)bwd_offset(n) + chunks * bwd_blocks<HV>(n) * (HV ? 4 : 2);
+    if (need > kPartialSlots)
+        return set_error(STADE_HIP_ERANGE, "%s: n * nsteps too large for the reduction workspace (%lld slots needed)", fn, (long long)need);
+    return STADE_HIP_OK;
+}
+
+// reverse sweep over steps nrun..1 from w (+d); the final state goes to ub (+d); returns the
+// number of partial blocks written at pbwd
+template <bool HV>
+int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, double* ubd, const double* tape, const double* taped,
+                 int n, int64_t nrun, const Coef& c, double* pbwd, int* nparts, hipStream_t stream) {
+    constexpr int S = HV ? 2048 : 4096;
+    constexpr int NV = HV ? 4 : 2;
+    const unsigned nb = grid_for(n, S);
+    double *cw = w, *cwd = wd, *ow = W2, *owd = W2d;
+    int64_t t = nrun - 1;
+    int chunk = 0;
+    while (t >= 0) {
+        int nk = (int)((t + 1) < KMAX ? (t + 1) : KMAX);
+        bool last = t - nk < 0;
+        double* d = last ? ub : ow;
+        double* dd = last ? ubd : owd;
+        STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
+                    bwd_kernel<HV, S><<<nb, NT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, nk, c,
+                                                             pbwd + (size_t)chunk * nb * NV));
+        STADE_LAUNCHED("burgers1d bwd_kernel");
+        ++chunk;
+        *nparts = chunk * (int)nb;
+        double* tmp = cw;
+        cw = ow;
+        ow = tmp;
+        tmp = cwd;
+        cwd = owd;
+        owd = tmp;
+        t -= nk;
+    }
+    return STADE_HIP_OK;
+}
+
+}  // namespace
+}  // namespace stade
+
+using namespace stade;
+
+extern "C" {
+
+int32_t stade_hip_burgers1d_stack_lengths(int64_t n, int64_t nsteps, int64_t lengths[2]) {
+    // initstacks_burgers1d_b: branch_stack max(0, div(nsteps - 1, 1) + 1),
+    // u_stack max(0, div(nsteps - 1, 1) + 1) * max(0, div(n - 1, 1) + 1)   (Julia div truncates)
+    if (!lengths) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_stack_lengths: null lengths");
+    int64_t a = (nsteps - 1) / 1 + 1, b = (n - 1) / 1 + 1;
+    a = a > 0 ? a : 0;
+    b = b > 0 ? b : 0;
+    lengths[0] = a;
+    lengths[1] = a * b;
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_initstacks_burgers1d_b(int64_t n, int64_t nsteps, int64_t** branch_stack, double** u_stack) {
+    int64_t len[2];
+    if (int32_t rc = stade_hip_burgers1d_stack_lengths(n, nsteps, len)) return rc;
+    if (!branch_stack || !u_stack) return set_error(STADE_HIP_EINVAL, "stade_hip_initstacks_burgers1d_b: null output");
+    *branch_stack = nullptr;
+    *u_stack = nullptr;
+    STADE_TRY_HIP(hipMalloc((void**)branch_stack, (size_t)(len[0] > 0 ? len[0] : 1) * sizeof(int64_t)));
+    hipError_t e = hipMalloc((void**)u_stack, (size_t)(len[1] > 0 ? len[1] : 1) * sizeof(double));
+    if (e != hipSuccess) {
+        hipFree(*branch_stack);
+        *branch_stack = nullptr;
+        return check_hip(e, "hipMalloc(u_stack)");
+    }
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                              double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
+                              int64_t n, int64_t nsteps, int64_t* branch_stack, double* u_stack, hipStream_t stream) {
+    if (int32_t rc = check(n, nsteps, "stade_hip_burgers1d_b")) return rc;
+    if (!nub || !dtb || !dxb || !tendb) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_b: null scalar shadow");
+    if ((n > 0 && (!loss || !lossb || !u || !ub || !un || !unb)) || (nsteps > 0 && (!branch_stack || (n > 0 && !u_stack))))
+        return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_b: null pointer");
+    const double cadv = 0.5 * dt / dx;
+    const double cdif = nu * dt / (dx * dx);
+    const int64_t nrun = taken_steps(dt, tend, nsteps);
+    if (int32_t rc = check_partials<false>(n, nrun, "stade_hip_burgers1d_b")) return rc;
+    Coef c{cadv, cdif, 0.0, 0.0};
+    Workspace* ws = workspace();
+    if (!ws) return STADE_HIP_ENOMEM;
+    if (nsteps > 0) {
+        STADE_TIMED("burgers1d_branch", stream, branch_kernel<<<grid_for((int)(nsteps < (1 << 20) ? nsteps : (1 << 20)), NT), NT, 0, stream>>>(branch_stack, nsteps, nrun));
+        STADE_LAUNCHED("burgers1d branch_kernel");
+    }
+    double cadvb = 0.0, cdifb = 0.0;
+    if (n > 0) {
+        double* P = (double*)scratch(sizeof(double) * 2 * (size_t)n);
+        if (!P) return STADE_HIP_ENOMEM;
+        double* Q = P + n;
+        if (int32_t rc = forward<false>(u, nullptr, un, nullptr, u_stack, nullptr, (int)n, nrun, c, P, Q, nullptr, nullptr, stream)) return rc;
+        const double* uT = nrun > 0 ? un : u;
+        const int gi = init_blocks(n);
+        STADE_TIMED("burgers1d_init", stream,
+                    bwd_init_kernel<false><<<gi, NT, 0, stream>>>(uT, nullptr, ub, nullptr, unb, nullptr, P, nullptr, lossb, nullptr,
+                                                                  (int)n, nrun > 0, ws->dscalars, ws->partials));
+        STADE_LAUNCHED("burgers1d bwd_init_kernel");
+        int nparts = 0;
+        double* pbwd = ws->partials + bwd_offset(n);
+        if (nrun > 0) {
+            if (int32_t rc = backward<false>(P, nullptr, Q, nullptr, ub, nullptr, u_stack, nullptr, (int)n, nrun, c, pbwd, &nparts, stream)) return rc;
+        }
+        STADE_TIMED("finalize", stream,
+                    bwd_finalize_kernel<false><<<2, NT, 0, stream>>>(ws->partials, gi, SumOuts{{loss}}, pbwd, nparts,
+                                                                     SumOuts{{ws->dscalars + 0, ws->dscalars + 1}}));
+        STADE_LAUNCHED("burgers1d bwd_finalize_kernel");
+        double* hs;
+        if (int32_t rc = host_scalars(&hs)) return rc;
+        STADE_TRY_HIP(hipMemcpyAsync(hs, ws->dscalars, 2 * sizeof(double), hipMemcpyDeviceToHost, stream));
+        STADE_TRY_HIP(hipStreamSynchronize(stream));
+        cadvb = hs[0];
+        cdifb = hs[1];
+    } else {
+        STADE_TRY_HIP(hipStreamSynchronize(stream));
+    }
+    // the statements after the time loop, on the host in the generated order
+    double nub_ = *nub, dtb_ = *dtb, dxb_ = *dxb;
+    if (nrun > 0) dtb_ = dtb_ + 0.0;  // dtb = dtb + tcb on each taken step; tcb is never seeded
+    const double o8 = cdifb;
+    const double c9 = dx * dx;
+    nub_ = nub_ + (dt / c9) * o8;
+    dtb_ = dtb_ + (nu / c9) * o8;
+    const double c10 = -((nu * dt) / (c9 * c9)) * o8;
+    dxb_ = dxb_ + dx * c10;
+    dxb_ = dxb_ + dx * c10;
+    const double o11 = cadvb;
+    dtb_ = dtb_ + (0.5 / dx) * o11;
+    dxb_ = dxb_ + -((0.5 * dt) / (dx * dx)) * o11;
+    *nub = nub_;
+    *dtb = dtb_;
+    *dxb = dxb_;
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_burgers1d_d(double* loss, double* lossd, double* u, double* ud, double* un, double* und, double nu, double nud,
+                              double dt, double dtd, double dx, double dxd, double tend, double tendd, int64_t n, int64_t nsteps,
+                              hipStream_t stream) {
+    (void)tendd;
+    if (int32_t rc = check(n, nsteps, "stade_hip_burgers1d_d")) return rc;
+    if (n == 0) return STADE_HIP_OK;
+    if (!loss || !lossd || !u || !ud || !un || !und) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_d: null pointer");
+    const double c0 = dx * dx;
+    Coef c{0.5 * dt / dx, nu * dt / c0, (0.5 * dtd) / dx + -((0.5 * dt) / (dx * dx)) * dxd,
+           (dt * nud + nu * dtd) / c0 + -((nu * dt) / (c0 * c0)) * (dx * dxd + dx * dxd)};
+    const int64_t nrun = taken_steps(dt, tend, nsteps);
+    Workspace* ws = workspace();
+    if (!ws) return STADE_HIP_ENOMEM;
+    double* P = (double*)scratch(sizeof(double) * 4 * (size_t)n);
+    if (!P) return STADE_HIP_ENOMEM;
+    double *Q = P + n, *Pd = Q + n, *Qd = Pd + n;
+    if (nrun > 0) {
+        if (int32_t rc = forward<true>(u, ud, un, und, nullptr, nullptr, (int)n, nrun, c, P, Q, Pd, Qd, stream)) return rc;
+        STADE_TIMED("burgers1d_copy", stream, copy2_kernel<<<grid_for((int)n, NT * 8), NT, 0, stream>>>(un, u, und, ud, (int)n));
+        STADE_LAUNCHED("burgers1d copy2_kernel");
+    }
+    // loss and lossd from the final state, now in u and ud
+    const int gl = init_blocks(n);
+    STADE_TIMED("burgers1d_loss", stream, loss2_kernel<<<gl, NT, 0, stream>>>(u, ud, (int)n, ws->partials));
+    STADE_LAUNCHED("burgers1d loss2_kernel");
+    STADE_TIMED("finalize", stream, finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, gl, SumOuts{{loss, lossd}}));
+    STADE_LAUNCHED("burgers1d finalize_kernel");
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                               double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
+                               int64_t n, int64_t nsteps, double* lossd, const double* lossbd, const double* ud, double* ubd,
+                               double* und, double* unbd, double nud, double* nubd, double dtd, double* dtbd, double dxd,
+                               double* dxbd, double tendd, double* tendbd, int64_t* branch_stack, double* u_stack,
+                               hipStream_t stream) {
+    (void)tendd;
+    if (int32_t rc = check(n, nsteps, "stade_hip_burgers1d_hv")) return rc;
+    if (!nub || !dtb || !dxb || !tendb || !nubd || !dtbd || !dxbd || !tendbd)
+        return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_hv: null scalar shadow");
+    if ((n > 0 && (!loss || !lossb || !u || !ub || !un || !unb || !lossd || !lossbd || !ud || !ubd || !und || !unbd)) ||
+        (nsteps > 0 && (!branch_stack || (n > 0 && !u_stack))))
+        return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_hv: null pointer");
+    const double c0 = dx * dx;
+    Coef c{0.5 * dt / dx, nu * dt / c0, (0.5 * dtd) / dx + -((0.5 * dt) / (dx * dx)) * dxd,
+           (dt * nud + nu * dtd) / c0 + -((nu * dt) / (c0 * c0)) * (dx * dxd + dx * dxd)};
+    const int64_t nrun = taken_steps(dt, tend, nsteps);
+    if (int32_t rc = check_partials<true>(n, nrun, "stade_hip_burgers1d_hv")) return rc;
+    Workspace* ws = workspace();
+    if (!ws) return STADE_HIP_ENOMEM;
+    if (nsteps > 0) {
+        STADE_TIMED("burgers1d_branch", stream, branch_kernel<<<grid_for((int)(nsteps < (1 << 20) ? nsteps : (1 << 20)), NT), NT, 0, stream>>>(branch_stack, nsteps, nrun));
+        STADE_LAUNCHED("burgers1d branch_kernel");
+    }
+    double sc[4] = {0.0, 0.0, 0.0, 0.0};  // cadvb, cdifb, cadvbd, cdifbd
+    if (n > 0) {
+        // u_stack_d: allocated inside the generated _hv (Vector{Float64}(undef, length(u_stack)));
+        // here a library scratch region, reused across calls
+        size_t tape_len = (size_t)nrun * (size_t)n;
+        double* P = (double*)scratch(sizeof(double) * (4 * (size_t)n + tape_len));
+        if (!P) return STADE_HIP_ENOMEM;
+        double *Q = P + n, *Pd = Q + n, *Qd = Pd + n, *taped = Qd + n;
+        if (int32_t rc = forward<true>(u, ud, un, und, u_stack, taped, (int)n, nrun, c, P, Q, Pd, Qd, stream)) return rc;
+        const double* uT = nrun > 0 ? un : u;
+        const double* udT = nrun > 0 ? und : ud;
+        const int gi = init_blocks(n);
+        STADE_TIMED("burgers1d_init", stream,
+                    bwd_init_kernel<true><<<gi, NT, 0, stream>>>(uT, udT, ub, ubd, unb, unbd, P, Pd, lossb, lossbd, (int)n,
+                                                                 nrun > 0, ws->dscalars, ws->partials));
+        STADE_LAUNCHED("burgers1d bwd_init_kernel");
+        int nparts = 0;
+        double* pbwd = ws->partials + bwd_offset(n);
+        if (nrun > 0) {
+            if (int32_t rc = backward<true>(P, Pd, Q, Qd, ub, ubd, u_stack, taped, (int)n, nrun, c, pbwd, &nparts, stream)) return rc;
+        }
+        STADE_TIMED("finalize", stream,
+                    bwd_finalize_kernel<true><<<2, NT, 0, stream>>>(ws->partials, gi, SumOuts{{loss, lossd}}, pbwd, nparts,
+                                                                    SumOuts{{ws->dscalars + 0, ws->dscalars + 1,
+                                                                             ws->dscalars + 2, ws->dscalars + 3}}));
+        STADE_LAUNCHED("burgers1d bwd_finalize_kernel");
+        double* hs;
+        if (int32_t rc = host_scalars(&hs)) return rc;
+        STADE_TRY_HIP(hipMemcpyAsync(hs, ws->dscalars, 4 * sizeof(double), hipMemcpyDeviceToHost, stream));
+        STADE_TRY_HIP(hipStreamSynchronize(stream));
+        for (int k = 0; k < 4; ++k) sc[k] = hs[k];
+    } else {
+        STADE_TRY_HIP(hipStreamSynchronize(stream));
+    }
+    // the statements after the time loop of the generated _hv, on the host in their order
+    double nb_ = *nub, nbd_ = *nubd, db_ = *dtb, dbd_ = *dtbd, xb_ = *dxb, xbd_ = *dxbd;
+    if (nrun > 0) {
+        dbd_ = dbd_ + 0.0;
+        db_ = db_ + 0.0;
+    }
+    const double o8d = sc[3], o8 = sc[1];
+    const double c9d = dx * dxd + dx * dxd, c9 = dx * dx;
+    const double h10d = dtd / c9 + -(dt / (c9 * c9)) * c9d, h10 = dt / c9;
+    nbd_ = nbd_ + (o8 * h10d + h10 * o8d);
+    nb_ = nb_ + h10 * o8;
+    const double h11d = nud / c9 + -(nu / (c9 * c9)) * c9d, h11 = nu / c9;
+    dbd_ = dbd_ + (o8 * h11d + h11 * o8d);
+    db_ = db_ + h11 * o8;
+    const double h12d = dt * nud + nu * dtd, h12 = nu * dt;
+    const double h13d = (2 * c9) * c9d, h13 = c9 * c9;
+    const double c10d = -(h12 / h13) * o8d + -(h12d / h13 + -(h12 / (h13 * h13)) * h13d) * o8;
+    const double c10 = -(h12 / h13) * o8;
+    xbd_ = xbd_ + (c10 * dxd + dx * c10d);
+    xb_ = xb_ + dx * c10;
+    xbd_ = xbd_ + (c10 * dxd + dx * c10d);
+    xb_ = xb_ + dx * c10;
+    const double o11d = sc[2], o11 = sc[0];
+    const double h14d = -(0.5 / (dx * dx)) * dxd, h14 = 0.5 / dx;
+    dbd_ = dbd_ + (o11 * h14d + h14 * o11d);
+    db_ = db_ + h14 * o11;
+    const double dx2 = dx * dx;
+    const double h15d = -((0.5 * dtd) / dx2 + -((0.5 * dt) / (dx2 * dx2)) * ((2 * dx) * dxd));
+    const double h15 = -((0.5 * dt) / dx2);
+    xbd_ = xbd_ + (o11 * h15d + h15 * o11d);
+    xb_ = xb_ + h15 * o11;
+    *nub = nb_;
+    *nubd = nbd_;
+    *dtb = db_;
+    *dtbd = dbd_;
+    *dxb = xb_;
+    *dxbd = xbd_;
+    return STADE_HIP_OK;
+}
+
+}  // extern "C"

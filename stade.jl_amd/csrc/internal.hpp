@@ -34,18 +34,16 @@ int32_t check_hip(hipError_t e, const char* what);
     } while (0)
 
 // ------------------------------------------------------------------------------------------
-// per-device workspace: grid-reduction partials, tickets and scratch buffers owned by the
+// per-device workspace: grid-reduction partials, device scalars and scratch owned by the
 // library.  Calls that share a device must be stream-ordered with respect to each other.
 // ------------------------------------------------------------------------------------------
 struct Workspace {
     double* partials;       // per-block partial sums, kPartialSlots doubles
-    unsigned int* tickets;  // zero-initialised tickets of the last-block reductions
     double* dscalars;       // small device scalars handed back to the host
     void* scratch;          // grows on demand
     size_t scratch_bytes;
 };
-constexpr int kPartialSlots = 1 << 20;
-constexpr int kTickets = 64;
+constexpr int kPartialSlots = 1 << 22;
 constexpr int kDeviceScalars = 64;
 
 // Workspace of the current device; nullptr (with the error set) on failure.
@@ -140,42 +138,50 @@ struct SumOuts {
     double* p[4];
 };
 
-// Grid-wide sum with a sync-free second pass: every block writes its partials, takes a
-// ticket, and the block that takes the last ticket adds the partials in block order (a
-// fixed order, so the result does not depend on scheduling) to `*out.p[k]` and re-arms
-// the ticket.  `partials` holds gridDim * NV values.  Call from every thread of every block.
+// Grid-wide sums in two stages, with no fence and no host synchronisation.
+//
+// Stage 1 (every block of the producing kernel): the block's sums go to
+// partials[bid * NV + k] with plain stores.
+// Stage 2 (one block of a kernel launched after it on the same stream, so the producer's
+// stores are visible at the kernel boundary): the partials are added in a fixed order --
+// a strided in-order walk per thread, then a fixed-shape tree -- so the result does not
+// depend on scheduling, and `out.p[k][0] += total`.
+//
+// The single-kernel alternative (each block fences, takes a ticket, the last block sums)
+// needs a device-scope release fence per block; on MI355X that writes back the XCD's L2
+// and measured 2.8-4.1x slower for the diffusion kernels, so it is not used.
 template <int NV>
-__device__ __forceinline__ void grid_sum_into(double (&v)[NV], double* lds, double* partials,
-                                              unsigned int* ticket, SumOuts out) {
-    __shared__ bool is_last;
+__device__ __forceinline__ void block_partials(double (&v)[NV], double* lds, double* partials) {
     block_sum<NV>(v, lds);
-    const unsigned nb = gridDim.x * gridDim.y * gridDim.z;
     const unsigned bid = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
     if (threadIdx.x == 0) {
 #pragma unroll
         for (int k = 0; k < NV; ++k) partials[(size_t)bid * NV + k] = v[k];
-        __threadfence();
-        unsigned t = atomicAdd(ticket, 1u);
-        is_last = (t == nb - 1);
     }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
+}
+
+// Stage 2, run by all threads of one block.
+template <int NV>
+__device__ __forceinline__ void finalize_partials(const double* partials, int nparts, double* lds, SumOuts out) {
     double acc[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) acc[k] = 0.0;
-    // a strided, in-order walk per thread, then a fixed-shape tree: deterministic
-    for (unsigned b = threadIdx.x; b < nb; b += blockDim.x) {
+    for (int b = threadIdx.x; b < nparts; b += blockDim.x) {
 #pragma unroll
-        for (int k = 0; k < NV; ++k)
-            acc[k] += __hip_atomic_load(&partials[(size_t)b * NV + k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 0; k < NV; ++k) acc[k] += partials[(size_t)b * NV + k];
     }
     block_sum<NV>(acc, lds);
     if (threadIdx.x == 0) {
 #pragma unroll
         for (int k = 0; k < NV; ++k) out.p[k][0] = out.p[k][0] + acc[k];
-        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// Stage 2 as its own launch (one block), for a producer with no follow-on kernel.
+template <int NV>
+__global__ __launch_bounds__(256) void finalize_kernel(const double* partials, int nparts, SumOuts out) {
+    __shared__ double lds[16 * NV];
+    finalize_partials<NV>(partials, nparts, lds, out);
 }
 
 // Periodic wrap of a coordinate that is at most one period outside [0, n).

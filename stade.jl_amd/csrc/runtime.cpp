@@ -47,9 +47,7 @@ Workspace* workspace() {
     if (!g_ws_ready[dev]) {
         Workspace w{};
         if ((e = hipMalloc(&w.partials, sizeof(double) * kPartialSlots)) != hipSuccess ||
-            (e = hipMalloc(&w.tickets, sizeof(unsigned) * kTickets)) != hipSuccess ||
             (e = hipMalloc(&w.dscalars, sizeof(double) * kDeviceScalars)) != hipSuccess ||
-            (e = hipMemset(w.tickets, 0, sizeof(unsigned) * kTickets)) != hipSuccess ||
             (e = hipDeviceSynchronize()) != hipSuccess) {
             check_hip(e, "workspace allocation");
             return nullptr;

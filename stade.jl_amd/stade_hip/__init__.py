@@ -26,6 +26,7 @@ from .api import (  # noqa: F401
     StadeHipError, lib, lib_path, ENTRY_POINTS,
     affine_lsq_b, affine_lsq_d, affine_lsq_hv,
     diffusion2d_b, diffusion2d_d, diffusion2d_hv,
+    burgers1d_b, burgers1d_d, burgers1d_hv, initstacks_burgers1d_b, burgers1d_stack_lengths,
     rng_normal, rng_uniform, rng_int_range, stable_seed,
 )
 from .emit import stade_hip_file  # noqa: F401

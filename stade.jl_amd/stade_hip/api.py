@@ -41,6 +41,9 @@ ENTRY_POINTS: dict[str, str] = {
     "stade_hip_diffusion2d_b": "aaaaaai",
     "stade_hip_diffusion2d_d": "aaaaaai",
     "stade_hip_diffusion2d_hv": "aaaaaai" + "aaaaaa",
+    "stade_hip_burgers1d_b": "aaaaaa" + "frfrfrfr" + "ii" + "aa",
+    "stade_hip_burgers1d_d": "aaaaaa" + "ffffffff" + "ii",
+    "stade_hip_burgers1d_hv": "aaaaaa" + "frfrfrfr" + "ii" + "aaaaaa" + "frfrfrfr" + "aa",
 }
 
 _CT = {"a": P, "i": I64, "f": F64, "r": F64P}
@@ -226,3 +229,80 @@ def diffusion2d_hv(loss, lossb, u, ub, un, unb, n, lossd, lossbd, ud, ubd, und, 
          _arr("lossd", lossd, d, 1), _arr("lossbd", lossbd, d, 1), _arr("ud", ud, d, c), _arr("ubd", ubd, d, c),
          _arr("und", und, d, c), _arr("unbd", unbd, d, c)]
     _call("stade_hip_diffusion2d_hv", a, _stream_of(u))
+
+
+# ------------------------------------------------------------------------------------------
+# config 5: burgers1d(loss, u, un, nu, dt, dx, tend, n, nsteps)
+# ------------------------------------------------------------------------------------------
+
+def burgers1d_stack_lengths(n: int, nsteps: int) -> tuple[int, int]:
+    """Lengths of initstacks_burgers1d_b's (branch_stack, u_stack)."""
+    out = (ctypes.c_int64 * 2)()
+    L = lib()
+    L.stade_hip_burgers1d_stack_lengths.argtypes = [I64, I64, ctypes.POINTER(ctypes.c_int64)]
+    _check("stade_hip_burgers1d_stack_lengths", L.stade_hip_burgers1d_stack_lengths(_int("n", n), _int("nsteps", nsteps), out))
+    return int(out[0]), int(out[1])
+
+
+def initstacks_burgers1d_b(n, nsteps, device=None):
+    """initstacks_burgers1d_b (corpus/burgers1d_b.jl): (branch_stack Int64, u_stack Float64),
+    allocated uninitialised on the GPU as the generated code allocates them with `undef`."""
+    import torch
+    lb, lu = burgers1d_stack_lengths(n, nsteps)
+    dev = device or torch.device("cuda", torch.cuda.current_device())
+    return (torch.empty(lb, dtype=torch.int64, device=dev), torch.empty(lu, dtype=torch.float64, device=dev))
+
+
+def _r(v) -> ctypes.c_double:
+    if isinstance(v, bool) or not isinstance(v, (int, float, np.floating, np.integer)):
+        raise TypeError(f"expected a Float64, got {type(v).__name__}")
+    return ctypes.c_double(float(v))
+
+
+def burgers1d_b(loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, tendb, n, nsteps, branch_stack, u_stack):
+    """Adjoint of burgers1d (corpus/burgers1d_b.jl); returns (nub, dtb, dxb, tendb)."""
+    import torch
+    n, T = _int("n", n), _int("nsteps", nsteps)
+    lb, lu = burgers1d_stack_lengths(n, T)
+    d = _f64()
+    rs = [_r(v) for v in (nub, dtb, dxb, tendb)]
+    a = [_arr("loss", loss, d, 1), _arr("lossb", lossb, d, 1), _arr("u", u, d, n), _arr("ub", ub, d, n),
+         _arr("un", un, d, n), _arr("unb", unb, d, n),
+         float(nu), ctypes.byref(rs[0]), float(dt), ctypes.byref(rs[1]), float(dx), ctypes.byref(rs[2]),
+         float(tend), ctypes.byref(rs[3]), n, T,
+         _arr("branch_stack", branch_stack, torch.int64, lb), _arr("u_stack", u_stack, d, lu)]
+    _call("stade_hip_burgers1d_b", a, _stream_of(u))
+    return tuple(r.value for r in rs)
+
+
+def burgers1d_d(loss, lossd, u, ud, un, und, nu, nud, dt, dtd, dx, dxd, tend, tendd, n, nsteps):
+    """Tangent of burgers1d (corpus/burgers1d_d.jl); returns nothing."""
+    n, T = _int("n", n), _int("nsteps", nsteps)
+    d = _f64()
+    a = [_arr("loss", loss, d, 1), _arr("lossd", lossd, d, 1), _arr("u", u, d, n), _arr("ud", ud, d, n),
+         _arr("un", un, d, n), _arr("und", und, d, n),
+         float(nu), float(nud), float(dt), float(dtd), float(dx), float(dxd), float(tend), float(tendd), n, T]
+    _call("stade_hip_burgers1d_d", a, _stream_of(u))
+
+
+def burgers1d_hv(loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, tendb, n, nsteps,
+                 lossd, lossbd, ud, ubd, und, unbd, nud, nubd, dtd, dtbd, dxd, dxbd, tendd, tendbd,
+                 branch_stack, u_stack):
+    """HVP of burgers1d (corpus/burgers1d_hv.jl); returns (nub, nubd, dtb, dtbd, dxb, dxbd, tendb, tendbd)."""
+    import torch
+    n, T = _int("n", n), _int("nsteps", nsteps)
+    lb, lu = burgers1d_stack_lengths(n, T)
+    d = _f64()
+    rs = [_r(v) for v in (nub, dtb, dxb, tendb)]
+    rd = [_r(v) for v in (nubd, dtbd, dxbd, tendbd)]
+    a = [_arr("loss", loss, d, 1), _arr("lossb", lossb, d, 1), _arr("u", u, d, n), _arr("ub", ub, d, n),
+         _arr("un", un, d, n), _arr("unb", unb, d, n),
+         float(nu), ctypes.byref(rs[0]), float(dt), ctypes.byref(rs[1]), float(dx), ctypes.byref(rs[2]),
+         float(tend), ctypes.byref(rs[3]), n, T,
+         _arr("lossd", lossd, d, 1), _arr("lossbd", lossbd, d, 1), _arr("ud", ud, d, n), _arr("ubd", ubd, d, n),
+         _arr("und", und, d, n), _arr("unbd", unbd, d, n),
+         float(nud), ctypes.byref(rd[0]), float(dtd), ctypes.byref(rd[1]), float(dxd), ctypes.byref(rd[2]),
+         float(tendd), ctypes.byref(rd[3]),
+         _arr("branch_stack", branch_stack, torch.int64, lb), _arr("u_stack", u_stack, d, lu)]
+    _call("stade_hip_burgers1d_hv", a, _stream_of(u))
+    return (rs[0].value, rd[0].value, rs[1].value, rd[1].value, rs[2].value, rd[2].value, rs[3].value, rd[3].value)

@@ -74,6 +74,28 @@ KERNELS: dict[str, KernelSpec] = {
             "hv": Mode("stade_hip_diffusion2d_hv", _a("loss", "lossb", "u", "ub", "un", "unb") + (("n", "I"),)
                        + _a("lossd", "lossbd", "ud", "ubd", "und", "unbd")),
         }),
+    "burgers1d": KernelSpec(
+        "burgers1d", "Float64",
+        {
+            "b": Mode("stade_hip_burgers1d_b",
+                      _a("loss", "lossb", "u", "ub", "un", "unb")
+                      + (("nu", "F"), ("nub", "R"), ("dt", "F"), ("dtb", "R"), ("dx", "F"), ("dxb", "R"),
+                         ("tend", "F"), ("tendb", "R"), ("n", "I"), ("nsteps", "I"))),
+            "d": Mode("stade_hip_burgers1d_d",
+                      _a("loss", "lossd", "u", "ud", "un", "und")
+                      + (("nu", "F"), ("nud", "F"), ("dt", "F"), ("dtd", "F"), ("dx", "F"), ("dxd", "F"),
+                         ("tend", "F"), ("tendd", "F"), ("n", "I"), ("nsteps", "I"))),
+            "hv": Mode("stade_hip_burgers1d_hv",
+                       _a("loss", "lossb", "u", "ub", "un", "unb")
+                       + (("nu", "F"), ("nub", "R"), ("dt", "F"), ("dtb", "R"), ("dx", "F"), ("dxb", "R"),
+                          ("tend", "F"), ("tendb", "R"), ("n", "I"), ("nsteps", "I"))
+                       + _a("lossd", "lossbd", "ud", "ubd", "und", "unbd")
+                       + (("nud", "F"), ("nubd", "R"), ("dtd", "F"), ("dtbd", "R"), ("dxd", "F"), ("dxbd", "R"),
+                          ("tendd", "F"), ("tendbd", "R"))),
+        },
+        stacks=(("branch_stack", "Int64", "max(0, div(nsteps - 1, 1) + 1)"),
+                ("u_stack", "Float64", "max(0, div(nsteps - 1, 1) + 1) * max(0, div(n - 1, 1) + 1)")),
+        stack_args=("n", "nsteps")),
 }
 
 
@@ -145,6 +167,10 @@ def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, s
             types.append("Ref{Float64}")
             vals.append(f"__r_{nm}")
             rets.append(nm)
+    # an HVP returns (xb, xbd) pairs (`hvp_emit` /root/reference/src/STADE.jl:6772-6779)
+    paired = [r for r in rets if not r.endswith("bd")]
+    if len(paired) * 2 == len(rets) and all(p + "d" in rets for p in paired):
+        rets = [x for p in paired for x in (p, p + "d")]
     for nm, et in stacks:
         sig.append(nm)
         types.append(f"Ptr{{{et}}}")
