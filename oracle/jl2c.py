@@ -784,6 +784,20 @@ static inline float jl_fminf(float x, float y) {
     int pick_y = (y < x) || (signbit(y) > signbit(x));
     return pick_y ? (isnan(x) ? x : y) : (isnan(y) ? y : x);
 }
+static inline long double jl_fmaxl(long double x, long double y) {
+    int pick_y = (y > x) || (signbit(y) < signbit(x));
+    return pick_y ? (isnan(x) ? x : y) : (isnan(y) ? y : x);
+}
+static inline long double jl_fminl(long double x, long double y) {
+    int pick_y = (y < x) || (signbit(y) > signbit(x));
+    return pick_y ? (isnan(x) ? x : y) : (isnan(y) ? y : x);
+}
+static inline long double jl_fsignl(long double x) { return x > 0.0L ? 1.0L : (x < 0.0L ? -1.0L : x); }
+static inline long double jl_fmod_flooredl(long double a, long double b) {
+    long double r = fmodl(a, b);
+    if (r != 0.0L && ((r < 0.0L) != (b < 0.0L))) r += b;
+    return r;
+}
 static inline int64_t jl_imax(int64_t a, int64_t b) { return a > b ? a : b; }
 static inline int64_t jl_imin(int64_t a, int64_t b) { return a < b ? a : b; }
 static inline int64_t jl_iabs(int64_t a) { return a < 0 ? -a : a; }
@@ -824,8 +838,11 @@ class CGen:
     def __init__(self, f: Func, types: FuncTypes, precision: str, bounds_check: bool):
         self.f = f
         self.ty = types
-        self.fp = "float" if precision == "f32" else "double"
+        # f80 ("long double", 64-bit significand) runs the same text as a higher-precision truth
+        self.fp = {"f32": "float", "f64": "double", "f80": "long double"}[precision]
         self.f32 = precision == "f32"
+        self.lsfx = {"f32": "f", "f64": "", "f80": "L"}[precision]  # float literal suffix
+        self.msfx = {"f32": "f", "f64": "", "f80": "l"}[precision]  # libm / helper suffix
         self.bc = bounds_check
         self.lines: list[str] = []
         self.ind = 1
@@ -850,7 +867,7 @@ class CGen:
                 txt = "0" + txt
             if txt.endswith("."):
                 txt += "0"
-            return ((f"{txt}f" if self.f32 else txt), "f")
+            return (f"{txt}{self.lsfx}", "f")
         if k == "var":
             t = ty.etype(e)
             if e[1] in ty.arrays:
@@ -890,7 +907,7 @@ class CGen:
         b, tb = self.ex(e[3])
         if op == "/":
             if ta == "i" and tb == "i":
-                return (f"((double){a} / (double){b})", "f")
+                return (f"(({self.fp if self.fp != 'float' else 'double'}){a} / ({self.fp if self.fp != 'float' else 'double'}){b})", "f")
             return (f"({self.tofp(a, ta)} / {self.tofp(b, tb)})", "f")
         if op == "%":
             if ta == "i" and tb == "i":
@@ -916,7 +933,7 @@ class CGen:
             return (f"pow((double){base}, {p})", "f")
         if lit is not None:
             self.tmp += 1
-            one = "1.0f" if self.f32 else "1.0"
+            one = f"1.0{self.lsfx}"
             if lit == 2:
                 return (f"({{{self.fp} __p = {base}; __p * __p;}})", "f")
             if lit == 3:
@@ -930,7 +947,7 @@ class CGen:
             if lit == -2:
                 return (f"({{{self.fp} __p = {one} / ({base}); __p * __p;}})", "f")
         p, tp = self.ex(pe)
-        fn = "powf" if self.f32 else "pow"
+        fn = "pow" + self.msfx
         return (f"{fn}({base}, {self.tofp(p, tp)})", "f")
 
     def call(self, e):
@@ -944,7 +961,7 @@ class CGen:
         ts = [t for _, t in cs]
         txt = [c for c, _ in cs]
         allint = all(t == "i" for t in ts)
-        sfx = "f" if self.f32 else ""
+        sfx = self.msfx
         if fn in ("div", "mod", "fld"):
             if allint:
                 return (f"jl_{fn}({txt[0]}, {txt[1]})", "i")
@@ -1013,7 +1030,7 @@ class CGen:
                 nm = lhs[1]
                 n, _ = self.ex(rhs[2])
                 isint = "Int" in rhs[1]
-                ct = "int64_t" if isint else ("float" if (self.f32 or "Float32" in rhs[1]) else "double")
+                ct = "int64_t" if isint else ("float" if (self.f32 or "Float32" in rhs[1]) else self.fp)
                 self.emit(f"if ({nm}.data) free({nm}.data);")
                 self.emit(f"{nm}.ndim = 1; {nm}.dims[0] = {n} > 0 ? {n} : 0; {nm}.data = jl_alloc({nm}.dims[0], sizeof({ct}), {1 if isint else 0});")
                 return
@@ -1089,11 +1106,11 @@ class CGen:
             if it[0] == "var" and it[1] in self.ty.arrays:
                 # an array returned by initstacks: its length and element type go back, the buffer is freed
                 kinds.append("A" + self.ty.arrays[it[1]])
-                self.emit(f"((double *)__ret)[{j}] = (double)jl_len(&{it[1]});")
+                self.emit(f"((long double *)__ret)[{j}] = (long double)jl_len(&{it[1]});")
             else:
                 c, t = self.ex(it)
                 kinds.append(t)
-                self.emit(f"((double *)__ret)[{j}] = (double){c};")
+                self.emit(f"((long double *)__ret)[{j}] = (long double){c};")
         if self.ret_kinds is None:
             self.ret_kinds = kinds
             self.ret_names = [it[1] if it[0] == "var" else None for it in items]

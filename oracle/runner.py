@@ -52,7 +52,7 @@ class OracleLib:
         self.lib = ctypes.CDLL(str(so_path))
         self.infos = infos
         self.precision = precision
-        self.fdt = np.float32 if precision == "f32" else np.float64
+        self.fdt = {"f32": np.float32, "f64": np.float64, "f80": np.longdouble}[precision]
         self.lib.jl_get_bounds_error.restype = ctypes.c_int
         self._fns = {}
 
@@ -96,11 +96,13 @@ class OracleLib:
                     c = ctypes.c_int64(int(v))
                 elif self.precision == "f32":
                     c = ctypes.c_float(float(v))
+                elif self.precision == "f80":
+                    c = ctypes.c_longdouble(v)
                 else:
                     c = ctypes.c_double(float(v))
                 keep.append(c)
                 argv[j] = ctypes.cast(ctypes.pointer(c), ctypes.c_void_p)
-        ret = (ctypes.c_double * 64)()
+        ret = (ctypes.c_longdouble * 64)()
         n = self._fn(name)(argv, ret)
         if self.lib.jl_get_bounds_error():
             raise IndexError(f"{name}: out-of-bounds array access (see stderr)")
@@ -112,7 +114,7 @@ class OracleLib:
             elif kind.startswith("A"):
                 out.append((int(ret[k]), kind))
             else:
-                out.append(float(self.fdt(ret[k])))
+                out.append(self.fdt(ret[k]) if self.precision == "f80" else float(self.fdt(ret[k])))
         return tuple(out)
 
     def stacks(self, name: str, *args, fill_nan: bool = True):

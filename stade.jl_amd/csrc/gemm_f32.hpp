@@ -1,0 +1,209 @@
+// fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32), with a fused per-element epilogue.
+//
+//   C(m, n) = sum over segments s of  sum_k A_s(m, k) * B_s(k, n),   epi(m, n, C(m, n))
+//
+// A_s is M x K_s and B_s is K_s x N, column-major (Julia) with either storage order:
+//   AK = false: A(m, k) at A[m + k * lda] (m contiguous);  AK = true: at A[k + m * lda]
+//   BK = true:  B(k, n) at B[k + n * ldb] (k contiguous);  BK = false: at B[n + k * ldb]
+// Up to two segments accumulate into one tile, so a tangent product such as
+// W1d * X + W1 * Xd is one launch.
+//
+// Tiling: a 256-thread block (4 waves) computes a 128 x 128 tile of C; each wave a 64 x 64
+// quarter as 2 x 2 MFMA 32 x 32 tiles (64 accumulator registers per lane).  K advances 16 at
+// a time through two LDS buffers (one barrier per step: the next tile's global loads are
+// issued before the MFMAs of the current one and stored to the other buffer after them).
+// LDS rows are padded by 4 floats.  The MFMA operands are swapped (B tile as the matrix-core
+// A operand) so that the accumulator's lane index runs along m: each epilogue store of a
+// wave covers 32 consecutive rows of a column-major C, a 128-byte segment.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace stade {
+namespace gemm {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128, BN = 128, BK = 16, NT = 256, PAD = 4;
+constexpr int LDA_S = BM + PAD, LDB_S = BN + PAD;
+
+struct Seg {
+    const float* A;
+    const float* B;
+    long lda, ldb;
+    int K;
+};
+
+struct Args {
+    Seg seg[2];
+    int nseg;
+    int M, N;
+};
+
+// Registers holding one 128 x 16 operand tile between its global load and its LDS store.
+struct Stage {
+    float4 v[2];
+};
+
+// A tile (m 0..127, k 0..15) of segment s at (m0, k0) into registers; zero outside M x K.
+template <bool KMAJ>
+__device__ __forceinline__ void load_tile(Stage& st, const float* __restrict__ P, long ld, int rows, int K, int r0, int k0,
+                                          bool vec) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int f = threadIdx.x + NT * q;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!KMAJ) {
+            // rows contiguous: f -> (k = f / 32, r4 = (f % 32) * 4)
+            const int kk = f >> 5, r4 = (f & 31) * 4;
+            const int k = k0 + kk, r = r0 + r4;
+            if (k < K) {
+                const float* p = P + (long)r + (long)k * ld;
+                if (vec && r + 3 < rows) {
+                    x = *reinterpret_cast<const float4*>(p);
+                } else {
+                    if (r + 0 < rows) x.x = p[0];
+                    if (r + 1 < rows) x.y = p[1];
+                    if (r + 2 < rows) x.z = p[2];
+                    if (r + 3 < rows) x.w = p[3];
+                }
+            }
+        } else {
+            // k contiguous: f -> (r = f / 4, k4 = (f % 4) * 4)
+            const int rr = f >> 2, k4 = (f & 3) * 4;
+            const int r = r0 + rr, k = k0 + k4;
+            if (r < rows) {
+                const float* p = P + (long)k + (long)r * ld;
+                if (vec && k + 3 < K) {
+                    x = *reinterpret_cast<const float4*>(p);
+                } else {
+                    if (k + 0 < K) x.x = p[0];
+                    if (k + 1 < K) x.y = p[1];
+                    if (k + 2 < K) x.z = p[2];
+                    if (k + 3 < K) x.w = p[3];
+                }
+            }
+        }
+        st.v[q] = x;
+    }
+}
+
+// Registers -> LDS tile S[k][r] (row stride LD)
+template <bool KMAJ, int LD>
+__device__ __forceinline__ void store_tile(const Stage& st, float* __restrict__ S) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int f = threadIdx.x + NT * q;
+        const float4 x = st.v[q];
+        if (!KMAJ) {
+            const int kk = f >> 5, r4 = (f & 31) * 4;
+            *reinterpret_cast<float4*>(S + kk * LD + r4) = x;
+        } else {
+            const int rr = f >> 2, k4 = (f & 3) * 4;
+            S[(k4 + 0) * LD + rr] = x.x;
+            S[(k4 + 1) * LD + rr] = x.y;
+            S[(k4 + 2) * LD + rr] = x.z;
+            S[(k4 + 3) * LD + rr] = x.w;
+        }
+    }
+}
+
+template <bool AK, bool BK, class Epi>
+__global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
+    __shared__ float As[2][BK * LDA_S];
+    __shared__ float Bs[2][BK * LDB_S];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+
+    // the K steps of all segments, in order
+    int steps[2], total = 0;
+    for (int s = 0; s < g.nseg; ++s) {
+        steps[s] = (g.seg[s].K + BK - 1) / BK;
+        total += steps[s];
+    }
+    auto locate = [&](int t, int& s, int& k0) {
+        s = (t < steps[0]) ? 0 : 1;
+        k0 = (s == 0 ? t : t - steps[0]) * BK;
+    };
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    Stage sa, sb;
+    if (total > 0) {
+        int s, k0;
+        locate(0, s, k0);
+        load_tile<AK>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
+        load_tile<!BK ? false : true>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
+        store_tile<AK, LDA_S>(sa, As[0]);
+        store_tile<BK, LDB_S>(sb, Bs[0]);
+    }
+    __syncthreads();
+    for (int t = 0; t < total; ++t) {
+        const int cur = t & 1;
+        const bool more = t + 1 < total;
+        if (more) {
+            int s, k0;
+            locate(t + 1, s, k0);
+            load_tile<AK>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
+            load_tile<BK>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
+        }
+        const float* A_ = As[cur];
+        const float* B_ = Bs[cur];
+#pragma unroll
+        for (int ks = 0; ks < BK / 2; ++ks) {
+            const int kk = ks * 2 + (lane >> 5);
+            float a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) a[i] = A_[kk * LDA_S + wm + i * 32 + (lane & 31)];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b[j] = B_[kk * LDB_S + wn + j * 32 + (lane & 31)];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j], a[i], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            store_tile<AK, LDA_S>(sa, As[cur ^ 1]);
+            store_tile<BK, LDB_S>(sb, Bs[cur ^ 1]);
+        }
+        __syncthreads();
+    }
+    // accumulator (i, j, r): m = m0 + wm + 32 i + lane % 32,  n = n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int m = m0 + wm + i * 32 + (lane & 31);
+        if (m >= g.M) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (n < g.N) epi(m, n, acc[i][j][r]);
+            }
+    }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Launch; returns the hipError of the launch.
+template <bool AK, bool BK, class Epi>
+hipError_t launch(const Args& g, Epi epi, hipStream_t stream) {
+    if (g.M <= 0 || g.N <= 0) return hipSuccess;
+    bool vec = true;
+    for (int s = 0; s < g.nseg; ++s) {
+        vec = vec && aligned16(g.seg[s].A) && aligned16(g.seg[s].B) && g.seg[s].lda % 4 == 0 && g.seg[s].ldb % 4 == 0;
+    }
+    dim3 grid((g.M + BM - 1) / BM, (g.N + BN - 1) / BN);
+    gemm_kernel<AK, BK, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);
+    return hipGetLastError();
+}
+
+}  // namespace gemm
+}  // namespace stade
