@@ -48,6 +48,10 @@ const char* stade_hip_last_error(void);
 const char* stade_hip_version(void);
 int32_t stade_hip_free(void* p);
 int32_t stade_hip_synchronize(hipStream_t stream);
+/* Device-side input error (an index the generated code would reject with a BoundsError,
+ * such as a label outside 1..i_out): 1 if raised since the last read, then cleared.
+ * Synchronous. */
+int32_t stade_hip_device_error(int32_t* flag);
 
 /* ---- kernel timing (no counterpart in the reference; its timings come from an external
  * bench kit, /root/reference/claude/manual-stade-dev.md:2040).  While enabled, every kernel
@@ -120,6 +124,29 @@ int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* 
                                double* und, double* unbd, double nud, double* nubd, double dtd, double* dtbd, double dxd,
                                double* dxbd, double tendd, double* tendbd, int64_t* branch_stack, double* u_stack,
                                hipStream_t stream);
+
+/* ---- config 3: mlp2_ce(loss, x, lab, w1, b1, w2, b2, h1, z, i_b, i_in, i_h, i_out) --------
+ * tanh hidden layer, softmax cross-entropy summed over the batch, Float32 arrays (STADE's
+ * precision=Float32, `cgen_convert_precision` /root/reference/src/STADE.jl:15351-15365),
+ * Int64 labels 1..i_out.  x (i_in, i_b), w1 (i_h, i_in), w2 (i_out, i_h), h1 (i_h, i_b),
+ * z (i_out, i_b), column-major.  replaces mlp2_ce_b_amdgpu / _d_amdgpu / _hv_amdgpu
+ * (corpus/mlp2_ce_{b,d,hv}.jl).  i_out <= 16, i_h <= 2048.  A label outside 1..i_out
+ * contributes no term (the generated code would raise a BoundsError) and sets the device
+ * error flag read by stade_hip_device_error. */
+int32_t stade_hip_mlp2_ce_b(float* loss, const float* lossb, const float* x, float* xb, const int64_t* lab, const float* w1,
+                            float* w1b, const float* b1, float* b1b, const float* w2, float* w2b, const float* b2, float* b2b,
+                            float* h1, float* h1b, float* z, float* zb, int64_t i_b, int64_t i_in, int64_t i_h, int64_t i_out,
+                            hipStream_t stream);
+int32_t stade_hip_mlp2_ce_d(float* loss, float* lossd, const float* x, const float* xd, const int64_t* lab, const float* w1,
+                            const float* w1d, const float* b1, const float* b1d, const float* w2, const float* w2d,
+                            const float* b2, const float* b2d, float* h1, float* h1d, float* z, float* zd, int64_t i_b,
+                            int64_t i_in, int64_t i_h, int64_t i_out, hipStream_t stream);
+int32_t stade_hip_mlp2_ce_hv(float* loss, const float* lossb, const float* x, float* xb, const int64_t* lab, const float* w1,
+                             float* w1b, const float* b1, float* b1b, const float* w2, float* w2b, const float* b2, float* b2b,
+                             float* h1, float* h1b, float* z, float* zb, int64_t i_b, int64_t i_in, int64_t i_h, int64_t i_out,
+                             float* lossd, const float* lossbd, const float* xd, float* xbd, const float* w1d, float* w1bd,
+                             const float* b1d, float* b1bd, const float* w2d, float* w2bd, const float* b2d, float* b2bd,
+                             float* h1d, float* h1bd, float* zd, float* zbd, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -140,7 +140,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         int s, k0;
         locate(0, s, k0);
         load_tile<AK>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
-        load_tile<!BK ? false : true>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
+        load_tile<BK>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
         store_tile<AK, LDA_S>(sa, As[0]);
         store_tile<BK, LDB_S>(sb, Bs[0]);
     }

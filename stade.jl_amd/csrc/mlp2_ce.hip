@@ -1,0 +1,500 @@
+// mlp2_ce: tangent, adjoint and HVP of a tanh perceptron with a softmax cross-entropy loss
+// summed over a mini-batch held inside the launch (fp32).
+//
+// Generated code this replaces: stade.jl_amd/corpus/mlp2_ce_{b,d,hv}.jl.  Under
+// `stade_amdgpu_file` (/root/reference/src/STADE.jl:18604) each (sample, unit) is one thread
+// running its 784- or 1024-long dot product alone, and every weight-gradient update
+// `w1b[j,k] += x[k,s] * s1b` is an atomic add (`cgen_device_assign` 11941-11969): 4096
+// same-address fp32 atomics per weight; the reference's tiled contraction twins
+// (`cgen_adjoint_contraction_` 14762) are CUDA-only.
+//
+// Here the three contractions run on the fp32 matrix cores (gemm_f32.hpp), each with its
+// elementwise neighbours fused into the epilogue:
+//   S1 = W1 X            epilogue h1 = tanh(S1 + b1)                 (H x B, K = I)
+//   head (per sample)    z = W2 h1 + b2, CE, d2 = dloss/dz, zb reset,
+//                        d1 = (1 - h1^2) (h1b + W2' d2), h1b reset    (one wave per sample)
+//   colsum               W2b += d2 h1', b1b += sum_s d1, b2b         (deterministic partials)
+//   W1b += d1 X'                                                       (H x I, K = B)
+//   Xb  += W1' d1                                                      (I x B, K = H)
+// The tangent adds S1d = W1d X + W1 Xd (one two-segment GEMM, epilogue h1d = (1 - h1^2)(S1d +
+// b1d)); the HVP adds the tangents of every backward product as two-segment GEMMs.
+#include "internal.hpp"
+#include "gemm_f32.hpp"
+#include "../../include/stade_hip.h"
+
+#include <math.h>
+
+namespace stade {
+namespace {
+
+constexpr int NT = 256, OMAX = 16;
+enum Mode { ADJ = 0, TAN = 1, HVP = 2 };
+
+// ---------------------------------------------------------------------------------------
+// GEMM epilogues (column-major outputs, leading dimension ld)
+// ---------------------------------------------------------------------------------------
+struct EpiTanh {  // h1 = tanh(s1), s1 = b1 + W1 x
+    float* h1;
+    const float* b1;
+    long ld;
+    __device__ void operator()(int m, int n, float v) const { h1[m + n * ld] = tanhf(v + b1[m]); }
+};
+struct EpiTanhD {  // h1d = (1.0 - h1^2) * s1d, s1d = b1d + W1d x + W1 xd
+    float* h1d;
+    const float* h1;
+    const float* b1d;
+    long ld;
+    __device__ void operator()(int m, int n, float v) const {
+        const long k = m + n * ld;
+        const float h = h1[k];
+        h1d[k] = (1.0f - h * h) * (v + b1d[m]);
+    }
+};
+struct EpiAcc {  // C += v (a shadow accumulated, as the generated code does)
+    float* C;
+    long ld;
+    __device__ void operator()(int m, int n, float v) const {
+        const long k = m + n * ld;
+        C[k] = C[k] + v;
+    }
+};
+
+// ---------------------------------------------------------------------------------------
+// head: one wave per sample
+// ---------------------------------------------------------------------------------------
+struct HeadArgs {
+    const float *h1, *w2, *b2, *lossb;
+    float *z, *zb, *h1b, *D1, *D2;
+    const float *h1d, *w2d, *b2d, *lossbd;
+    float *zd, *zbd, *h1bd, *D1d, *D2d;
+    const int64_t* lab;
+    int B, H, O;
+    double* partials;  // per block: loss, lossd, b2b[O], b2bd[O]
+    int* err;          // set when a label is outside 1..O
+};
+
+template <int MODE, int HPL>
+__global__ __launch_bounds__(NT) void head_kernel(HeadArgs a) {
+    __shared__ double red[16 * (2 + 2 * OMAX)];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.H, O = a.O;
+    double acc[2 + 2 * OMAX];  // loss, lossd, b2b[0..O), b2bd[0..O)
+#pragma unroll
+    for (int k = 0; k < 2 + 2 * OMAX; ++k) acc[k] = 0.0;
+    const float lb = (MODE == TAN) ? 0.f : a.lossb[0];
+    const float lbd = (MODE == HVP) ? a.lossbd[0] : 0.f;
+    for (int s = blockIdx.x * (NT / 64) + wave; s < a.B; s += gridDim.x * (NT / 64)) {
+        const long hs = (long)s * H, os = (long)s * O;
+        float hj[HPL], hdj[HPL];
+#pragma unroll
+        for (int q = 0; q < HPL; ++q) {
+            const int j = lane + 64 * q;
+            hj[q] = j < H ? a.h1[hs + j] : 0.f;
+            hdj[q] = (MODE != ADJ && j < H) ? a.h1d[hs + j] : 0.f;
+        }
+        // z = b2 + W2 h1 (and zd = b2d + W2d h1 + W2 h1d)
+        float z[OMAX], zd[OMAX];
+#pragma unroll
+        for (int o = 0; o < OMAX; ++o) z[o] = zd[o] = 0.f;
+#pragma unroll
+        for (int q = 0; q < HPL; ++q) {
+            const int j = lane + 64 * q;
+            if (j >= H) continue;
+            const float* w2j = a.w2 + (long)j * O;
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                if (o < O) {
+                    z[o] += w2j[o] * hj[q];
+                    if (MODE != ADJ) zd[o] += hj[q] * a.w2d[(long)j * O + o] + w2j[o] * hdj[q];
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 0; o < OMAX; ++o) {
+            if (o < O) {
+                z[o] = a.b2[o] + wave_sum(z[o]);
+                if (MODE != ADJ) zd[o] = a.b2d[o] + wave_sum(zd[o]);
+            }
+        }
+        // softmax cross-entropy: loss += log(se) - z[l]
+        float se = 0.f, sed = 0.f, e[OMAX];
+#pragma unroll
+        for (int o = 0; o < OMAX; ++o) {
+            if (o < O) {
+                e[o] = expf(z[o]);
+                if (MODE != ADJ) sed = sed + e[o] * zd[o];
+                se = se + e[o];
+            }
+        }
+        int l = (int)a.lab[s] - 1;
+        if (l < 0 || l >= O) {
+            if (lane == 0) atomicExch(a.err, 1);
+            l = -1;
+        }
+        float zl = 0.f, zdl = 0.f;
+#pragma unroll
+        for (int o = 0; o < OMAX; ++o)
+            if (o == l) {
+                zl = z[o];
+                zdl = zd[o];
+            }
+        if (lane == 0 && l >= 0) {
+            acc[0] += (double)(logf(se) - zl);
+            if (MODE != ADJ) acc[1] += (double)((1.0f / se) * sed + -zdl);
+        }
+        if (MODE != ADJ && lane < O) {
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o)
+                if (o == lane) a.zd[os + o] = zd[o];
+        }
+        if (lane < O) {
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o)
+                if (o == lane) a.z[os + o] = z[o];
+        }
+        if (MODE == TAN) continue;
+        // reverse of the loss: d2 = zb + [o == l](-lb) + exp(z) seb, seb = (1 / se) lb
+        const float seb = (1.0f / se) * lb;
+        const float sebd = (MODE == HVP) ? (lb * (-(1.0f / (se * se)) * sed) + (1.0f / se) * lbd) : 0.f;
+        float d2[OMAX], d2d[OMAX];
+#pragma unroll
+        for (int o = 0; o < OMAX; ++o) {
+            d2[o] = d2d[o] = 0.f;
+            if (o < O) {
+                float t = a.zb[os + o];
+                if (o == l) t = t + -lb;
+                d2[o] = t + e[o] * seb;
+                if (MODE == HVP) {
+                    float td = a.zbd[os + o];
+                    if (o == l) td = td + -lbd;
+                    d2d[o] = td + (seb * (e[o] * zd[o]) + e[o] * sebd);
+                }
+                // every lane holds the same d2: lane 0 counts it once for b2b
+                if (lane == 0) {
+                    acc[2 + o] += (double)d2[o];
+                    if (MODE == HVP) acc[2 + OMAX + o] += (double)d2d[o];
+                }
+            }
+        }
+        if (lane < O) {
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o)
+                if (o == lane) {
+                    a.zb[os + o] = 0.f;
+                    a.D2[os + o] = d2[o];
+                    if (MODE == HVP) {
+                        a.zbd[os + o] = 0.f;
+                        a.D2d[os + o] = d2d[o];
+                    }
+                }
+        }
+        // d1 = (1 - h1^2) * (h1b + sum_o w2[o, j] d2[o]), o descending as the generated loop
+#pragma unroll
+        for (int q = 0; q < HPL; ++q) {
+            const int j = lane + 64 * q;
+            if (j >= H) continue;
+            const float* w2j = a.w2 + (long)j * O;
+            float t = a.h1b[hs + j];
+            float td = (MODE == HVP) ? a.h1bd[hs + j] : 0.f;
+#pragma unroll
+            for (int o = OMAX - 1; o >= 0; --o) {
+                if (o < O) {
+                    if (MODE == HVP) td = td + (d2[o] * a.w2d[(long)j * O + o] + w2j[o] * d2d[o]);
+                    t = t + w2j[o] * d2[o];
+                }
+            }
+            const float h = hj[q];
+            const float g = 1.0f - h * h;
+            a.h1b[hs + j] = 0.f;
+            a.D1[hs + j] = g * t;
+            if (MODE == HVP) {
+                a.h1bd[hs + j] = 0.f;
+                a.D1d[hs + j] = t * -((2.0f * h) * hdj[q]) + g * td;
+            }
+        }
+    }
+    // block partials: loss, lossd, b2b[0..O), b2bd[0..O)
+    block_partials<2 + 2 * OMAX>(acc, red, a.partials);
+}
+
+// ---------------------------------------------------------------------------------------
+// colsum: per chunk of samples, W2b[o, j] += sum_s d2[o, s] h1[j, s], b1b[j] += sum_s d1[j, s]
+// (HVP: W2bd += d2 h1d + h1 d2d, b1bd += d1d); chunk partials reduced in order by final_kernel
+// ---------------------------------------------------------------------------------------
+constexpr int SC = 128;  // samples per chunk
+struct ColArgs {
+    const float *h1, *D1, *D2, *h1d, *D1d, *D2d;
+    float* part;  // [chunk][2 * (O + 1)][H]
+    int B, H, O;
+};
+
+template <int MODE>
+__global__ __launch_bounds__(NT) void colsum_kernel(ColArgs a) {
+    __shared__ float d2s[SC * OMAX], d2ds[SC * OMAX];
+    const int j = blockIdx.x * NT + threadIdx.x, c = blockIdx.y;
+    const int s0 = c * SC, s1 = min(a.B, s0 + SC), O = a.O, H = a.H;
+    for (int q = threadIdx.x; q < (s1 - s0) * O; q += NT) {
+        d2s[q] = a.D2[(long)s0 * O + q];
+        if (MODE == HVP) d2ds[q] = a.D2d[(long)s0 * O + q];
+    }
+    __syncthreads();
+    if (j >= H) return;
+    float w[OMAX], wd[OMAX], bsum = 0.f, bsumd = 0.f;
+#pragma unroll
+    for (int o = 0; o < OMAX; ++o) w[o] = wd[o] = 0.f;
+    for (int s = s0; s < s1; ++s) {
+        const long k = (long)s * H + j;
+        const float h = a.h1[k];
+        const float hd = (MODE == HVP) ? a.h1d[k] : 0.f;
+        const float* d2 = d2s + (s - s0) * O;
+        const float* d2d = d2ds + (s - s0) * O;
+#pragma unroll
+        for (int o = 0; o < OMAX; ++o) {
+            if (o < O) {
+                w[o] += h * d2[o];
+                if (MODE == HVP) wd[o] += d2[o] * hd + h * d2d[o];
+            }
+        }
+        bsum += a.D1[k];
+        if (MODE == HVP) bsumd += a.D1d[k];
+    }
+    float* p = a.part + (long)c * 2 * (O + 1) * H;
+#pragma unroll
+    for (int o = 0; o < OMAX; ++o) {
+        if (o < O) {
+            p[(long)o * H + j] = w[o];
+            if (MODE == HVP) p[(long)(O + 1 + o) * H + j] = wd[o];
+        }
+    }
+    p[(long)O * H + j] = bsum;
+    if (MODE == HVP) p[(long)(2 * O + 1) * H + j] = bsumd;
+}
+
+// block 0: loss (+ lossd) and b2b (+ b2bd) from the head partials; the other blocks: W2b,
+// b1b (+ W2bd, b1bd) from the colsum chunk partials, chunks in order
+struct FinalArgs {
+    const double* hpart;
+    int nhead;
+    const float* cpart;
+    int nchunks;
+    float *loss, *lossd, *b2b, *b2bd, *w2b, *w2bd, *b1b, *b1bd;
+    int H, O;
+};
+
+template <int MODE>
+__global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
+    __shared__ double red[16];
+    const int O = f.O, H = f.H;
+    if (blockIdx.x == 0) {
+        constexpr int NV = 2 + 2 * OMAX;
+        for (int k = 0; k < NV; ++k) {
+            if (k == 1 && MODE == ADJ) continue;
+            if (k >= 2 && MODE == TAN) break;
+            if (k >= 2 + O && k < 2 + OMAX) continue;
+            if (k >= 2 + OMAX && (MODE != HVP || k >= 2 + OMAX + O)) continue;
+            double v[1] = {0.0};
+            for (int b = threadIdx.x; b < f.nhead; b += NT) v[0] += f.hpart[(size_t)b * NV + k];
+            block_sum<1>(v, red);
+            if (threadIdx.x == 0) {
+                float t = (float)v[0];
+                if (k == 0) f.loss[0] = f.loss[0] + t;
+                else if (k == 1) f.lossd[0] = f.lossd[0] + t;
+                else if (k < 2 + OMAX) f.b2b[k - 2] = f.b2b[k - 2] + t;
+                else f.b2bd[k - 2 - OMAX] = f.b2bd[k - 2 - OMAX] + t;
+            }
+        }
+        return;
+    }
+    if (MODE == TAN) return;
+    const int rows = (MODE == HVP ? 2 : 1) * (O + 1);
+    const long q = (long)(blockIdx.x - 1) * NT + threadIdx.x;
+    if (q >= (long)rows * H) return;
+    const int r = (int)(q / H), j = (int)(q % H);
+    float s = 0.f;
+    for (int c = 0; c < f.nchunks; ++c) s += f.cpart[(long)c * 2 * (O + 1) * H + (long)r * H + j];
+    if (r < O) f.w2b[(long)j * O + r] = f.w2b[(long)j * O + r] + s;
+    else if (r == O) f.b1b[j] = f.b1b[j] + s;
+    else if (r < 2 * O + 1) f.w2bd[(long)j * O + (r - O - 1)] = f.w2bd[(long)j * O + (r - O - 1)] + s;
+    else f.b1bd[j] = f.b1bd[j] + s;
+}
+
+struct Ptrs {
+    float *loss, *x, *w1, *b1, *w2, *b2, *h1, *z;       // primal (loss, h1, z written)
+    float *lossb, *xb, *w1b, *b1b, *w2b, *b2b, *h1b, *zb;  // adjoint shadows
+    float *lossd, *xd, *w1d, *b1d, *w2d, *b2d, *h1d, *zd;  // tangents
+    float *lossbd, *xbd, *w1bd, *b1bd, *w2bd, *b2bd, *h1bd, *zbd;
+    const int64_t* lab;
+};
+
+int32_t check(int64_t B, int64_t I, int64_t H, int64_t O, const char* fn) {
+    if (B < 0 || I < 0 || H < 0 || O < 0) return set_error(STADE_HIP_EINVAL, "%s: negative size", fn);
+    if (O > OMAX) return set_error(STADE_HIP_ERANGE, "%s: i_out = %lld exceeds %d", fn, (long long)O, OMAX);
+    if (H > 2048) return set_error(STADE_HIP_ERANGE, "%s: i_h = %lld exceeds 2048", fn, (long long)H);
+    if (B > (1 << 24) || I > (1 << 24) || (double)B * (double)(H > I ? H : I) > 2e9)
+        return set_error(STADE_HIP_ERANGE, "%s: sizes out of range", fn);
+    return STADE_HIP_OK;
+}
+
+template <int MODE, int HPL>
+void launch_head(const HeadArgs& h, unsigned blocks, hipStream_t stream) {
+    head_kernel<MODE, HPL><<<blocks, NT, 0, stream>>>(h);
+}
+
+template <int MODE>
+int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipStream_t stream) {
+    const int B = (int)B_, I = (int)I_, H = (int)H_, O = (int)O_;
+    if (B == 0 || H == 0) {
+        // no sample or no hidden unit: the loss loops still run over samples (with h1 empty)
+        if (B == 0) return STADE_HIP_OK;
+    }
+    Workspace* ws = workspace();
+    if (!ws) return STADE_HIP_ENOMEM;
+    const int nchunks = (B + SC - 1) / SC;
+    const size_t nD1 = (size_t)H * B, nD2 = (size_t)O * B, nC = (size_t)nchunks * 2 * (O + 1) * H;
+    const int hv = MODE == HVP ? 2 : 1;
+    float* D1 = (float*)scratch(sizeof(float) * (hv * (nD1 + nD2) + nC) + 256);
+    if (!D1) return STADE_HIP_ENOMEM;
+    float *D2 = D1 + nD1, *D1d = D2 + nD2, *D2d = D1d + (MODE == HVP ? nD1 : 0), *cpart = D2d + (MODE == HVP ? nD2 : 0);
+    int* err = (int*)(ws->dscalars + 16);
+    using namespace gemm;
+    // forward: h1 = tanh(W1 x + b1)
+    {
+        Args g{};
+        g.seg[0] = Seg{p.w1, p.x, H, I, I};
+        g.nseg = 1;
+        g.M = H;
+        g.N = B;
+        hipError_t e;
+        STADE_TIMED("mlp_gemm_s1", stream, e = (launch<false, true>(g, EpiTanh{p.h1, p.b1, H}, stream)));
+        if (e != hipSuccess) return check_hip(e, "mlp gemm s1");
+    }
+    if (MODE != ADJ) {
+        Args g{};
+        g.seg[0] = Seg{p.w1d, p.x, H, I, I};
+        g.seg[1] = Seg{p.w1, p.xd, H, I, I};
+        g.nseg = 2;
+        g.M = H;
+        g.N = B;
+        hipError_t e;
+        STADE_TIMED("mlp_gemm_s1d", stream, e = (launch<false, true>(g, EpiTanhD{p.h1d, p.h1, p.b1d, H}, stream)));
+        if (e != hipSuccess) return check_hip(e, "mlp gemm s1d");
+    }
+    HeadArgs h{};
+    h.h1 = p.h1; h.w2 = p.w2; h.b2 = p.b2; h.lossb = p.lossb; h.z = p.z; h.zb = p.zb; h.h1b = p.h1b; h.D1 = D1; h.D2 = D2;
+    h.h1d = p.h1d; h.w2d = p.w2d; h.b2d = p.b2d; h.lossbd = p.lossbd; h.zd = p.zd; h.zbd = p.zbd; h.h1bd = p.h1bd;
+    h.D1d = D1d; h.D2d = D2d; h.lab = p.lab; h.B = B; h.H = H; h.O = O; h.partials = ws->partials; h.err = err;
+    const unsigned hb = (unsigned)((B + 4 * 4 - 1) / (4 * 4));  // 4 samples per wave
+    STADE_TIMED("mlp_head", stream, {
+        if (H <= 256) launch_head<MODE, 4>(h, hb, stream);
+        else if (H <= 1024) launch_head<MODE, 16>(h, hb, stream);
+        else launch_head<MODE, 32>(h, hb, stream);
+    });
+    STADE_LAUNCHED("mlp head_kernel");
+    if (MODE != TAN && H > 0) {
+        ColArgs c{p.h1, D1, D2, p.h1d, D1d, D2d, cpart, B, H, O};
+        STADE_TIMED("mlp_colsum", stream,
+                    colsum_kernel<MODE><<<dim3((H + NT - 1) / NT, nchunks), NT, 0, stream>>>(c));
+        STADE_LAUNCHED("mlp colsum_kernel");
+    }
+    FinalArgs f{ws->partials, (int)hb, cpart, nchunks, p.loss, p.lossd, p.b2b, p.b2bd, p.w2b, p.w2bd, p.b1b, p.b1bd, H, O};
+    const long rows = (long)(MODE == HVP ? 2 : 1) * (O + 1) * H;
+    const unsigned fb = 1 + (MODE == TAN ? 0 : (unsigned)((rows + NT - 1) / NT));
+    STADE_TIMED("mlp_final", stream, final_kernel<MODE><<<fb, NT, 0, stream>>>(f));
+    STADE_LAUNCHED("mlp final_kernel");
+    if (MODE == TAN || H == 0 || I == 0) return STADE_HIP_OK;
+    // W1b += d1 x'   (M = H, N = I, K = B);  HVP: W1bd += d1 xd' + d1d x'
+    {
+        Args g{};
+        g.seg[0] = Seg{D1, p.x, H, I, B};
+        g.nseg = 1;
+        g.M = H;
+        g.N = I;
+        hipError_t e;
+        STADE_TIMED("mlp_gemm_w1b", stream, e = (launch<false, false>(g, EpiAcc{p.w1b, H}, stream)));
+        if (e != hipSuccess) return check_hip(e, "mlp gemm w1b");
+        if (MODE == HVP) {
+            g.seg[0] = Seg{D1, p.xd, H, I, B};
+            g.seg[1] = Seg{D1d, p.x, H, I, B};
+            g.nseg = 2;
+            STADE_TIMED("mlp_gemm_w1bd", stream, e = (launch<false, false>(g, EpiAcc{p.w1bd, H}, stream)));
+            if (e != hipSuccess) return check_hip(e, "mlp gemm w1bd");
+        }
+    }
+    // Xb += W1' d1   (M = I, N = B, K = H);  HVP: Xbd += W1d' d1 + W1' d1d
+    {
+        Args g{};
+        g.seg[0] = Seg{p.w1, D1, H, H, H};
+        g.nseg = 1;
+        g.M = I;
+        g.N = B;
+        hipError_t e;
+        STADE_TIMED("mlp_gemm_xb", stream, e = (launch<true, true>(g, EpiAcc{p.xb, I}, stream)));
+        if (e != hipSuccess) return check_hip(e, "mlp gemm xb");
+        if (MODE == HVP) {
+            g.seg[0] = Seg{p.w1d, D1, H, H, H};
+            g.seg[1] = Seg{p.w1, D1d, H, H, H};
+            g.nseg = 2;
+            STADE_TIMED("mlp_gemm_xbd", stream, e = (launch<true, true>(g, EpiAcc{p.xbd, I}, stream)));
+            if (e != hipSuccess) return check_hip(e, "mlp gemm xbd");
+        }
+    }
+    return STADE_HIP_OK;
+}
+
+}  // namespace
+}  // namespace stade
+
+using namespace stade;
+
+extern "C" {
+
+int32_t stade_hip_mlp2_ce_b(float* loss, const float* lossb, const float* x, float* xb, const int64_t* lab, const float* w1,
+                            float* w1b, const float* b1, float* b1b, const float* w2, float* w2b, const float* b2, float* b2b,
+                            float* h1, float* h1b, float* z, float* zb, int64_t i_b, int64_t i_in, int64_t i_h, int64_t i_out,
+                            hipStream_t stream) {
+    if (int32_t rc = check(i_b, i_in, i_h, i_out, "stade_hip_mlp2_ce_b")) return rc;
+    if (i_b > 0 && (!loss || !lossb || !x || !xb || !lab || !w1 || !w1b || !b1 || !b1b || !w2 || !w2b || !b2 || !b2b || !h1 ||
+                    !h1b || !z || !zb))
+        return set_error(STADE_HIP_EINVAL, "stade_hip_mlp2_ce_b: null pointer");
+    Ptrs p{};
+    p.loss = loss; p.x = (float*)x; p.w1 = (float*)w1; p.b1 = (float*)b1; p.w2 = (float*)w2; p.b2 = (float*)b2; p.h1 = h1; p.z = z;
+    p.lossb = (float*)lossb; p.xb = xb; p.w1b = w1b; p.b1b = b1b; p.w2b = w2b; p.b2b = b2b; p.h1b = h1b; p.zb = zb; p.lab = lab;
+    return run<ADJ>(p, i_b, i_in, i_h, i_out, stream);
+}
+
+int32_t stade_hip_mlp2_ce_d(float* loss, float* lossd, const float* x, const float* xd, const int64_t* lab, const float* w1,
+                            const float* w1d, const float* b1, const float* b1d, const float* w2, const float* w2d,
+                            const float* b2, const float* b2d, float* h1, float* h1d, float* z, float* zd, int64_t i_b,
+                            int64_t i_in, int64_t i_h, int64_t i_out, hipStream_t stream) {
+    if (int32_t rc = check(i_b, i_in, i_h, i_out, "stade_hip_mlp2_ce_d")) return rc;
+    if (i_b > 0 && (!loss || !lossd || !x || !xd || !lab || !w1 || !w1d || !b1 || !b1d || !w2 || !w2d || !b2 || !b2d || !h1 ||
+                    !h1d || !z || !zd))
+        return set_error(STADE_HIP_EINVAL, "stade_hip_mlp2_ce_d: null pointer");
+    Ptrs p{};
+    p.loss = loss; p.x = (float*)x; p.w1 = (float*)w1; p.b1 = (float*)b1; p.w2 = (float*)w2; p.b2 = (float*)b2; p.h1 = h1; p.z = z;
+    p.lossd = lossd; p.xd = (float*)xd; p.w1d = (float*)w1d; p.b1d = (float*)b1d; p.w2d = (float*)w2d; p.b2d = (float*)b2d;
+    p.h1d = h1d; p.zd = zd; p.lab = lab;
+    return run<TAN>(p, i_b, i_in, i_h, i_out, stream);
+}
+
+int32_t stade_hip_mlp2_ce_hv(float* loss, const float* lossb, const float* x, float* xb, const int64_t* lab, const float* w1,
+                             float* w1b, const float* b1, float* b1b, const float* w2, float* w2b, const float* b2, float* b2b,
+                             float* h1, float* h1b, float* z, float* zb, int64_t i_b, int64_t i_in, int64_t i_h, int64_t i_out,
+                             float* lossd, const float* lossbd, const float* xd, float* xbd, const float* w1d, float* w1bd,
+                             const float* b1d, float* b1bd, const float* w2d, float* w2bd, const float* b2d, float* b2bd,
+                             float* h1d, float* h1bd, float* zd, float* zbd, hipStream_t stream) {
+    if (int32_t rc = check(i_b, i_in, i_h, i_out, "stade_hip_mlp2_ce_hv")) return rc;
+    if (i_b > 0 && (!loss || !lossb || !x || !xb || !lab || !w1 || !w1b || !b1 || !b1b || !w2 || !w2b || !b2 || !b2b || !h1 ||
+                    !h1b || !z || !zb || !lossd || !lossbd || !xd || !xbd || !w1d || !w1bd || !b1d || !b1bd || !w2d || !w2bd ||
+                    !b2d || !b2bd || !h1d || !h1bd || !zd || !zbd))
+        return set_error(STADE_HIP_EINVAL, "stade_hip_mlp2_ce_hv: null pointer");
+    Ptrs p{};
+    p.loss = loss; p.x = (float*)x; p.w1 = (float*)w1; p.b1 = (float*)b1; p.w2 = (float*)w2; p.b2 = (float*)b2; p.h1 = h1; p.z = z;
+    p.lossb = (float*)lossb; p.xb = xb; p.w1b = w1b; p.b1b = b1b; p.w2b = w2b; p.b2b = b2b; p.h1b = h1b; p.zb = zb; p.lab = lab;
+    p.lossd = lossd; p.xd = (float*)xd; p.w1d = (float*)w1d; p.b1d = (float*)b1d; p.w2d = (float*)w2d; p.b2d = (float*)b2d;
+    p.h1d = h1d; p.zd = zd;
+    p.lossbd = (float*)lossbd; p.xbd = xbd; p.w1bd = w1bd; p.b1bd = b1bd; p.w2bd = w2bd; p.b2bd = b2bd; p.h1bd = h1bd; p.zbd = zbd;
+    return run<HVP>(p, i_b, i_in, i_h, i_out, stream);
+}
+
+}  // extern "C"

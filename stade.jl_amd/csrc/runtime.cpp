@@ -48,6 +48,7 @@ Workspace* workspace() {
         Workspace w{};
         if ((e = hipMalloc(&w.partials, sizeof(double) * kPartialSlots)) != hipSuccess ||
             (e = hipMalloc(&w.dscalars, sizeof(double) * kDeviceScalars)) != hipSuccess ||
+            (e = hipMemset(w.dscalars, 0, sizeof(double) * kDeviceScalars)) != hipSuccess ||
             (e = hipDeviceSynchronize()) != hipSuccess) {
             check_hip(e, "workspace allocation");
             return nullptr;
@@ -284,6 +285,19 @@ int32_t stade_hip_profile_read(const char* kernel, double* total_ms, int64_t* la
     auto it = g_prof_tot.find(kernel);
     *total_ms = it == g_prof_tot.end() ? 0.0 : it->second.first;
     *launches = it == g_prof_tot.end() ? 0 : it->second.second;
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_device_error(int32_t* flag) {
+    // the flag a kernel raises for an input the generated code would reject at run time (an
+    // index out of range); reading it waits for the device and clears it
+    if (!flag) return set_error(STADE_HIP_EINVAL, "stade_hip_device_error: null flag");
+    Workspace* w = workspace();
+    if (!w) return STADE_HIP_ENOMEM;
+    int32_t h = 0, z = 0;
+    STADE_TRY_HIP(hipMemcpy(&h, (int32_t*)(w->dscalars + 16), sizeof h, hipMemcpyDeviceToHost));
+    STADE_TRY_HIP(hipMemcpy((int32_t*)(w->dscalars + 16), &z, sizeof z, hipMemcpyHostToDevice));
+    *flag = h;
     return STADE_HIP_OK;
 }
 

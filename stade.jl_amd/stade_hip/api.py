@@ -44,6 +44,9 @@ ENTRY_POINTS: dict[str, str] = {
     "stade_hip_burgers1d_b": "aaaaaa" + "frfrfrfr" + "ii" + "aa",
     "stade_hip_burgers1d_d": "aaaaaa" + "ffffffff" + "ii",
     "stade_hip_burgers1d_hv": "aaaaaa" + "frfrfrfr" + "ii" + "aaaaaa" + "frfrfrfr" + "aa",
+    "stade_hip_mlp2_ce_b": "a" * 17 + "iiii",
+    "stade_hip_mlp2_ce_d": "a" * 17 + "iiii",
+    "stade_hip_mlp2_ce_hv": "a" * 17 + "iiii" + "a" * 16,
 }
 
 _CT = {"a": P, "i": I64, "f": F64, "r": F64P}
@@ -306,3 +309,62 @@ def burgers1d_hv(loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, t
          _arr("branch_stack", branch_stack, torch.int64, lb), _arr("u_stack", u_stack, d, lu)]
     _call("stade_hip_burgers1d_hv", a, _stream_of(u))
     return (rs[0].value, rd[0].value, rs[1].value, rd[1].value, rs[2].value, rd[2].value, rs[3].value, rd[3].value)
+
+
+# ------------------------------------------------------------------------------------------
+# config 3: mlp2_ce(loss, x, lab, w1, b1, w2, b2, h1, z, i_b, i_in, i_h, i_out)   (Float32)
+# ------------------------------------------------------------------------------------------
+
+def _f32():
+    import torch
+    return torch.float32
+
+
+def _mlp_sizes(i_b, i_in, i_h, i_out):
+    B, I, H, O = (_int(n, v) for n, v in (("i_b", i_b), ("i_in", i_in), ("i_h", i_h), ("i_out", i_out)))
+    return B, I, H, O, dict(loss=1, x=I * B, w1=H * I, b1=H, w2=O * H, b2=O, h1=H * B, z=O * B)
+
+
+
+def mlp2_ce_b(loss, lossb, x, xb, lab, w1, w1b, b1, b1b, w2, w2b, b2, b2b, h1, h1b, z, zb, i_b, i_in, i_h, i_out):
+    """Adjoint of mlp2_ce (corpus/mlp2_ce_b.jl); returns nothing."""
+    import torch
+    B, I, H, O, s = _mlp_sizes(i_b, i_in, i_h, i_out)
+    f = _f32()
+    a = [_arr("loss", loss, f, 1), _arr("lossb", lossb, f, 1), _arr("x", x, f, s["x"]), _arr("xb", xb, f, s["x"]),
+         _arr("lab", lab, torch.int64, B), _arr("w1", w1, f, s["w1"]), _arr("w1b", w1b, f, s["w1"]),
+         _arr("b1", b1, f, H), _arr("b1b", b1b, f, H), _arr("w2", w2, f, s["w2"]), _arr("w2b", w2b, f, s["w2"]),
+         _arr("b2", b2, f, O), _arr("b2b", b2b, f, O), _arr("h1", h1, f, s["h1"]), _arr("h1b", h1b, f, s["h1"]),
+         _arr("z", z, f, s["z"]), _arr("zb", zb, f, s["z"]), B, I, H, O]
+    _call("stade_hip_mlp2_ce_b", a, _stream_of(x))
+
+
+def mlp2_ce_d(loss, lossd, x, xd, lab, w1, w1d, b1, b1d, w2, w2d, b2, b2d, h1, h1d, z, zd, i_b, i_in, i_h, i_out):
+    """Tangent of mlp2_ce (corpus/mlp2_ce_d.jl); returns nothing."""
+    import torch
+    B, I, H, O, s = _mlp_sizes(i_b, i_in, i_h, i_out)
+    f = _f32()
+    a = [_arr("loss", loss, f, 1), _arr("lossd", lossd, f, 1), _arr("x", x, f, s["x"]), _arr("xd", xd, f, s["x"]),
+         _arr("lab", lab, torch.int64, B), _arr("w1", w1, f, s["w1"]), _arr("w1d", w1d, f, s["w1"]),
+         _arr("b1", b1, f, H), _arr("b1d", b1d, f, H), _arr("w2", w2, f, s["w2"]), _arr("w2d", w2d, f, s["w2"]),
+         _arr("b2", b2, f, O), _arr("b2d", b2d, f, O), _arr("h1", h1, f, s["h1"]), _arr("h1d", h1d, f, s["h1"]),
+         _arr("z", z, f, s["z"]), _arr("zd", zd, f, s["z"]), B, I, H, O]
+    _call("stade_hip_mlp2_ce_d", a, _stream_of(x))
+
+
+def mlp2_ce_hv(loss, lossb, x, xb, lab, w1, w1b, b1, b1b, w2, w2b, b2, b2b, h1, h1b, z, zb, i_b, i_in, i_h, i_out,
+               lossd, lossbd, xd, xbd, w1d, w1bd, b1d, b1bd, w2d, w2bd, b2d, b2bd, h1d, h1bd, zd, zbd):
+    """HVP of mlp2_ce (corpus/mlp2_ce_hv.jl); returns nothing."""
+    import torch
+    B, I, H, O, s = _mlp_sizes(i_b, i_in, i_h, i_out)
+    f = _f32()
+    a = [_arr("loss", loss, f, 1), _arr("lossb", lossb, f, 1), _arr("x", x, f, s["x"]), _arr("xb", xb, f, s["x"]),
+         _arr("lab", lab, torch.int64, B), _arr("w1", w1, f, s["w1"]), _arr("w1b", w1b, f, s["w1"]),
+         _arr("b1", b1, f, H), _arr("b1b", b1b, f, H), _arr("w2", w2, f, s["w2"]), _arr("w2b", w2b, f, s["w2"]),
+         _arr("b2", b2, f, O), _arr("b2b", b2b, f, O), _arr("h1", h1, f, s["h1"]), _arr("h1b", h1b, f, s["h1"]),
+         _arr("z", z, f, s["z"]), _arr("zb", zb, f, s["z"]), B, I, H, O,
+         _arr("lossd", lossd, f, 1), _arr("lossbd", lossbd, f, 1), _arr("xd", xd, f, s["x"]), _arr("xbd", xbd, f, s["x"]),
+         _arr("w1d", w1d, f, s["w1"]), _arr("w1bd", w1bd, f, s["w1"]), _arr("b1d", b1d, f, H), _arr("b1bd", b1bd, f, H),
+         _arr("w2d", w2d, f, s["w2"]), _arr("w2bd", w2bd, f, s["w2"]), _arr("b2d", b2d, f, O), _arr("b2bd", b2bd, f, O),
+         _arr("h1d", h1d, f, s["h1"]), _arr("h1bd", h1bd, f, s["h1"]), _arr("zd", zd, f, s["z"]), _arr("zbd", zbd, f, s["z"])]
+    _call("stade_hip_mlp2_ce_hv", a, _stream_of(x))

@@ -96,6 +96,24 @@ KERNELS: dict[str, KernelSpec] = {
         stacks=(("branch_stack", "Int64", "max(0, div(nsteps - 1, 1) + 1)"),
                 ("u_stack", "Float64", "max(0, div(nsteps - 1, 1) + 1) * max(0, div(n - 1, 1) + 1)")),
         stack_args=("n", "nsteps")),
+    "mlp2_ce": KernelSpec(
+        "mlp2_ce", "Float32",
+        {
+            "b": Mode("stade_hip_mlp2_ce_b",
+                      _a("loss", "lossb", "x", "xb") + (("lab", "L"),) + _a("w1", "w1b", "b1", "b1b", "w2", "w2b", "b2", "b2b",
+                                                                         "h1", "h1b", "z", "zb")
+                      + (("i_b", "I"), ("i_in", "I"), ("i_h", "I"), ("i_out", "I"))),
+            "d": Mode("stade_hip_mlp2_ce_d",
+                      _a("loss", "lossd", "x", "xd") + (("lab", "L"),) + _a("w1", "w1d", "b1", "b1d", "w2", "w2d", "b2", "b2d",
+                                                                         "h1", "h1d", "z", "zd")
+                      + (("i_b", "I"), ("i_in", "I"), ("i_h", "I"), ("i_out", "I"))),
+            "hv": Mode("stade_hip_mlp2_ce_hv",
+                       _a("loss", "lossb", "x", "xb") + (("lab", "L"),) + _a("w1", "w1b", "b1", "b1b", "w2", "w2b", "b2", "b2b",
+                                                                          "h1", "h1b", "z", "zb")
+                       + (("i_b", "I"), ("i_in", "I"), ("i_h", "I"), ("i_out", "I"))
+                       + _a("lossd", "lossbd", "xd", "xbd", "w1d", "w1bd", "b1d", "b1bd", "w2d", "w2bd", "b2d", "b2bd",
+                            "h1d", "h1bd", "zd", "zbd")),
+        }),
 }
 
 
@@ -157,6 +175,9 @@ def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, s
         if kind == "A":
             types.append(f"Ptr{{{T}}}")
             vals.append(f"pointer({nm})")
+        elif kind == "L":
+            types.append("Ptr{Int64}")
+            vals.append(f"pointer({nm})")
         elif kind == "I":
             types.append("Int64")
             vals.append(f"Int64({nm})")
@@ -177,7 +198,7 @@ def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, s
         vals.append(f"pointer({nm})")
     types.append("Ptr{Cvoid}")
     vals.append("AMDGPU.stream().stream")
-    arrays = [nm for nm, kind in mode.args if kind == "A"] + [nm for nm, _ in stacks]
+    arrays = [nm for nm, kind in mode.args if kind in ("A", "L")] + [nm for nm, _ in stacks]
     lines = [f"function {fname}_hip({', '.join(sig)})"]
     for nm in rets:
         lines.append(f"    __r_{nm} = Ref{{Float64}}({nm})")
@@ -206,7 +227,7 @@ def stade_hip_file(in_path, out_path, *, precision=None, lib_path: str | None = 
     """
     text = Path(in_path).read_text()
     spec, funcs = identify(text)
-    if precision not in (None, spec.eltype, "Float64" if spec.eltype == "Float64" else spec.eltype):
+    if precision not in (None, spec.eltype):
         raise StadeHipRefusal(f"{spec.name}: libstade_hip implements {spec.eltype} only, precision={precision} requested")
     libp = lib_path or "libstade_hip"
     out = [

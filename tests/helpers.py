@@ -68,7 +68,7 @@ def to_host(t) -> np.ndarray:
 
 
 def make_args(lib, fname: str, shapes: dict, ints: dict, scalars: dict, seed: str, fdt=np.float64,
-              int_arrays: dict | None = None):
+              int_arrays: dict | None = None, scales: dict | None = None):
     """Seeded inputs for every argument of a generated function, in its own order.
 
     Float arrays: N(0,1) from Julia's Xoshiro stream (one stream per argument position);
@@ -94,14 +94,15 @@ def make_args(lib, fname: str, shapes: dict, ints: dict, scalars: dict, seed: st
         else:
             shp = shapes[a]
             shp = shp if isinstance(shp, tuple) else (shp,)
-            v = jrng.val_randn(jrng.Xoshiro(base + pos), int(np.prod(shp))).astype(fdt)
+            v = jrng.val_randn(jrng.Xoshiro(base + pos), int(np.prod(shp)))
+            v = (v * (scales or {}).get(a, 1.0)).astype(fdt)
             out.append((a, kind, np.asfortranarray(v.reshape(shp, order="F")) if len(shp) > 1 else v))
     return out
 
 
 def run_parity(name: str, mode: str, shapes: dict, ints: dict, scalars: dict | None = None,
                seed: str | None = None, precision: str = "f64", rtol: float | None = None,
-               stacks: tuple = (), int_arrays: dict | None = None, oracle=None):
+               stacks: tuple = (), int_arrays: dict | None = None, oracle=None, scales: dict | None = None):
     """Run one generated function on the oracle and on libstade_hip with the same inputs;
     compare every argument's final value and the returned scalars.  Returns the worst error."""
     import stade_hip
@@ -113,7 +114,7 @@ def run_parity(name: str, mode: str, shapes: dict, ints: dict, scalars: dict | N
     fname = f"{name}_{mode}"
     shp = dict(shapes)
     shp["__stacks__"] = tuple(s for s, _ in stacks)
-    args = make_args(lib, fname, shp, ints, scalars, seed or f"{fname}-{ints}", fdt, int_arrays)
+    args = make_args(lib, fname, shp, ints, scalars, seed or f"{fname}-{ints}", fdt, int_arrays, scales)
     host = [v.copy(order="K") if isinstance(v, np.ndarray) else v for _, _, v in args]
     dev = [torch.from_numpy(np.ascontiguousarray(v.ravel(order="F"))).to("cuda") if isinstance(v, np.ndarray) else v
            for _, _, v in args]

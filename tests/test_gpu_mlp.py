@@ -1,0 +1,32 @@
+"""mlp2_ce on the GPU against the oracle (the transpiled generated code run in Float32, as
+`stade_amdgpu_file(...; precision=Float32)` runs it), fp32 to 1e-5 relative (normwise), with
+the truth rule (fp64 oracle) where the two differ by more.
+
+Sizes cover tiny and odd widths, widths that are not multiples of the 128 x 128 matrix-core
+tile, and the benchmark widths 784 -> 1024 -> 10 on a reduced batch."""
+import numpy as np
+import pytest
+
+from helpers import run_parity
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [(8, 5, 7, 3), (64, 40, 48, 10), (130, 129, 131, 10), (256, 784, 1024, 10)]
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("size", SIZES)
+def test_mlp2_ce_parity(mode, size):
+    from oracle import rng as jrng
+    B, I, H, O = size
+    sz = dict(loss=1, x=I * B, w1=H * I, b1=H, w2=O * H, b2=O, h1=H * B, z=O * B)
+    shapes = {}
+    for k, v in sz.items():
+        for suf in ("", "b", "d", "bd"):
+            shapes[k + suf] = v
+    lab = np.array([1 + int(jrng.Xoshiro(17 + s).rand() * O) for s in range(B)], dtype=np.int64)
+    g1, g2 = np.sqrt(2.0 / (I + H)), np.sqrt(2.0 / (H + O))
+    scales = {"w1": g1, "w1d": g1, "w2": g2, "w2d": g2, "b1": 0.1, "b2": 0.1}
+    print(f"mlp2_ce_{mode} B={B} I={I} H={H} O={O}", flush=True)
+    run_parity("mlp2_ce", mode, shapes, dict(i_b=B, i_in=I, i_h=H, i_out=O), precision="f32",
+               int_arrays=dict(lab=lab), scales=scales)
