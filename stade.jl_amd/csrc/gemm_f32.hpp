@@ -3,8 +3,8 @@
 //   C(m, n) = sum over segments s of  sum_k A_s(m, k) * B_s(k, n),   epi(m, n, C(m, n))
 //
 // A_s is M x K_s and B_s is K_s x N, column-major (Julia) with either storage order:
-//   AK = false: A(m, k) at A[m + k * lda] (m contiguous);  AK = true: at A[k + m * lda]
-//   BK = true:  B(k, n) at B[k + n * ldb] (k contiguous);  BK = false: at B[n + k * ldb]
+//   A_KM = false: A(m, k) at A[m + k * lda] (m contiguous);  A_KM = true: at A[k + m * lda]
+//   B_KM = true:  B(k, n) at B[k + n * ldb] (k contiguous);  B_KM = false: at B[n + k * ldb]
 // Up to two segments accumulate into one tile, so a tangent product such as
 // W1d * X + W1 * Xd is one launch.
 //
@@ -24,7 +24,7 @@ namespace gemm {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 16, NT = 256, PAD = 4;
+constexpr int BM = 128, BN = 128, KT = 16, NT = 256, PAD = 4;
 constexpr int LDA_S = BM + PAD, LDB_S = BN + PAD;
 
 struct Seg {
@@ -108,10 +108,10 @@ __device__ __forceinline__ void store_tile(const Stage& st, float* __restrict__ 
     }
 }
 
-template <bool AK, bool BK, class Epi>
+template <bool A_KM, bool B_KM, class Epi>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
-    __shared__ float As[2][BK * LDA_S];
-    __shared__ float Bs[2][BK * LDB_S];
+    __shared__ float As[2][KT * LDA_S];
+    __shared__ float Bs[2][KT * LDB_S];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
@@ -119,12 +119,12 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     // the K steps of all segments, in order
     int steps[2], total = 0;
     for (int s = 0; s < g.nseg; ++s) {
-        steps[s] = (g.seg[s].K + BK - 1) / BK;
+        steps[s] = (g.seg[s].K + KT - 1) / KT;
         total += steps[s];
     }
     auto locate = [&](int t, int& s, int& k0) {
         s = (t < steps[0]) ? 0 : 1;
-        k0 = (s == 0 ? t : t - steps[0]) * BK;
+        k0 = (s == 0 ? t : t - steps[0]) * KT;
     };
 
     floatx16 acc[2][2];
@@ -139,10 +139,10 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     if (total > 0) {
         int s, k0;
         locate(0, s, k0);
-        load_tile<AK>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
-        load_tile<BK>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
-        store_tile<AK, LDA_S>(sa, As[0]);
-        store_tile<BK, LDB_S>(sb, Bs[0]);
+        load_tile<A_KM>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
+        load_tile<B_KM>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
+        store_tile<A_KM, LDA_S>(sa, As[0]);
+        store_tile<B_KM, LDB_S>(sb, Bs[0]);
     }
     __syncthreads();
     for (int t = 0; t < total; ++t) {
@@ -151,13 +151,13 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         if (more) {
             int s, k0;
             locate(t + 1, s, k0);
-            load_tile<AK>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
-            load_tile<BK>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
+            load_tile<A_KM>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
+            load_tile<B_KM>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
         }
         const float* A_ = As[cur];
         const float* B_ = Bs[cur];
 #pragma unroll
-        for (int ks = 0; ks < BK / 2; ++ks) {
+        for (int ks = 0; ks < KT / 2; ++ks) {
             const int kk = ks * 2 + (lane >> 5);
             float a[2], b[2];
 #pragma unroll
@@ -170,8 +170,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
                 for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j], a[i], acc[i][j], 0, 0, 0);
         }
         if (more) {
-            store_tile<AK, LDA_S>(sa, As[cur ^ 1]);
-            store_tile<BK, LDB_S>(sb, Bs[cur ^ 1]);
+            store_tile<A_KM, LDA_S>(sa, As[cur ^ 1]);
+            store_tile<B_KM, LDB_S>(sb, Bs[cur ^ 1]);
         }
         __syncthreads();
     }
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Launch; returns the hipError of the launch.
-template <bool AK, bool BK, class Epi>
+template <bool A_KM, bool B_KM, class Epi>
 hipError_t launch(const Args& g, Epi epi, hipStream_t stream) {
     if (g.M <= 0 || g.N <= 0) return hipSuccess;
     bool vec = true;
@@ -201,7 +201,7 @@ hipError_t launch(const Args& g, Epi epi, hipStream_t stream) {
         vec = vec && aligned16(g.seg[s].A) && aligned16(g.seg[s].B) && g.seg[s].lda % 4 == 0 && g.seg[s].ldb % 4 == 0;
     }
     dim3 grid((g.M + BM - 1) / BM, (g.N + BN - 1) / BN);
-    gemm_kernel<AK, BK, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);
+    gemm_kernel<A_KM, B_KM, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);
     return hipGetLastError();
 }
 
