@@ -304,6 +304,189 @@ class Burgers(Workload):
         return run, f"burgers1d_{self.mode} on {n} cells for {Ts} of the {self.T} steps (time x {1/scale:.0f})", scale
 
 
+class Mlp(Workload):
+    """Config 3: x (784, 4096) ~ N(0,1), tanh hidden layer of 1024, 10-way softmax
+    cross-entropy, Float32; W1, W2 Glorot-scaled N(0,1), b ~ 0.1 N(0,1), labels uniform in
+    1..10 -- all from the seeded Xoshiro stream."""
+    dtype = "f32"
+    bound = "mfma"
+
+    def __init__(self, mode="b", B=4096, I=784, H=1024, O=10):
+        self.mode, self.B, self.I, self.H, self.O = mode, B, I, H, O
+        self.name = f"mlp2_ce_{mode}"
+        g = 2.0 * H * I * B
+        # flops per launch of each matrix-core kernel (a two-segment launch does two products)
+        self.kernels = {"b": {"mlp_gemm_s1": g, "mlp_gemm_w1b": g, "mlp_gemm_xb": g},
+                        "d": {"mlp_gemm_s1": g, "mlp_gemm_s1d": 2 * g},
+                        "hv": {"mlp_gemm_s1": g, "mlp_gemm_s1d": 2 * g, "mlp_gemm_w1b": g, "mlp_gemm_w1bd": 2 * g,
+                               "mlp_gemm_xb": g, "mlp_gemm_xbd": 2 * g}}[mode]
+        self.kernel = next(iter(self.kernels))
+
+    def _host(self, B):
+        import numpy as np
+        import stade_hip
+        I, H, O = self.I, self.H, self.O
+        rng = stade_hip.api.Rng(stade_hip.stable_seed("mlp2_ce"))
+        x = stade_hip.rng_normal(rng, I * B).astype(np.float32)
+        w1 = (stade_hip.rng_normal(rng, H * I) * np.sqrt(2.0 / (I + H))).astype(np.float32)
+        b1 = (0.1 * stade_hip.rng_normal(rng, H)).astype(np.float32)
+        w2 = (stade_hip.rng_normal(rng, O * H) * np.sqrt(2.0 / (H + O))).astype(np.float32)
+        b2 = (0.1 * stade_hip.rng_normal(rng, O)).astype(np.float32)
+        lab = stade_hip.rng_int_range(rng, B, 1, O)
+        rng2 = stade_hip.api.Rng(stade_hip.stable_seed("mlp2_ce") + 1)
+        d = {k: (stade_hip.rng_normal(rng2, n) * sc).astype(np.float32)
+             for k, n, sc in (("xd", I * B, 1.0), ("w1d", H * I, np.sqrt(2.0 / (I + H))), ("b1d", H, 0.1),
+                              ("w2d", O * H, np.sqrt(2.0 / (H + O))), ("b2d", O, 0.1))}
+        return dict(x=x, w1=w1, b1=b1, w2=w2, b2=b2, lab=lab, **d)
+
+    def setup(self, dev):
+        import torch
+        B, I, H, O = self.B, self.I, self.H, self.O
+        h = self._host(B)
+        f = lambda a: _tensor(a, dev)
+        z = lambda k: torch.zeros(k, dtype=torch.float32, device=dev)
+        t = {k: f(v) for k, v in h.items()}
+        t.update(loss=z(1), lossb=f([1.0]).float(), lossd=z(1), lossbd=z(1))
+        for k, n in (("x", I * B), ("w1", H * I), ("b1", H), ("w2", O * H), ("b2", O), ("h1", H * B), ("z", O * B)):
+            for suf in ("b", "bd") if k not in ("h1", "z") else ("", "b", "d", "bd"):
+                t.setdefault(k + suf, z(n))
+        self.t = t
+
+    def step(self):
+        import stade_hip
+        t = self.t
+        sz = (self.B, self.I, self.H, self.O)
+        if self.mode == "b":
+            stade_hip.mlp2_ce_b(*(t[k] for k in ("loss", "lossb", "x", "xb", "lab", "w1", "w1b", "b1", "b1b", "w2", "w2b",
+                                                "b2", "b2b", "h1", "h1b", "z", "zb")), *sz)
+        elif self.mode == "d":
+            stade_hip.mlp2_ce_d(*(t[k] for k in ("loss", "lossd", "x", "xd", "lab", "w1", "w1d", "b1", "b1d", "w2", "w2d",
+                                                "b2", "b2d", "h1", "h1d", "z", "zd")), *sz)
+        else:
+            stade_hip.mlp2_ce_hv(*(t[k] for k in ("loss", "lossb", "x", "xb", "lab", "w1", "w1b", "b1", "b1b", "w2", "w2b",
+                                                 "b2", "b2b", "h1", "h1b", "z", "zb")), *sz,
+                                 *(t[k] for k in ("lossd", "lossbd", "xd", "xbd", "w1d", "w1bd", "b1d", "b1bd", "w2d", "w2bd",
+                                                  "b2d", "b2bd", "h1d", "h1bd", "zd", "zbd")))
+
+    def eval_flops(self):
+        B, I, H, O = self.B, self.I, self.H, self.O
+        return sum(self.kernels.values()) * 1.0 + {"b": 2, "d": 2, "hv": 4}[self.mode] * 2.0 * O * H * B
+
+    def config(self):
+        return {"workload": f"mlp2_ce_{self.mode}: x {self.I}x{self.B} fp32 -> tanh({self.H}) -> {self.O}-way softmax "
+                            f"cross-entropy summed over the batch",
+                "batch": self.B, "widths": [self.I, self.H, self.O]}
+
+    def cpu_sample(self):
+        import numpy as np
+        from oracle import runner
+        Bs = 128
+        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"mlp2_ce_{self.mode}.jl", precision="f32", bounds_check=False)
+        h = self._host(Bs)
+        I, H, O = self.I, self.H, self.O
+        z = lambda k: np.zeros(k, dtype=np.float32)
+        one = np.ones(1, dtype=np.float32)
+
+        def run():
+            if self.mode == "b":
+                lib.call("mlp2_ce_b", z(1), one, h["x"], z(I * Bs), h["lab"], h["w1"], z(H * I), h["b1"], z(H), h["w2"],
+                         z(O * H), h["b2"], z(O), z(H * Bs), z(H * Bs), z(O * Bs), z(O * Bs), Bs, I, H, O)
+            elif self.mode == "d":
+                lib.call("mlp2_ce_d", z(1), z(1), h["x"], h["xd"], h["lab"], h["w1"], h["w1d"], h["b1"], h["b1d"], h["w2"],
+                         h["w2d"], h["b2"], h["b2d"], z(H * Bs), z(H * Bs), z(O * Bs), z(O * Bs), Bs, I, H, O)
+            else:
+                lib.call("mlp2_ce_hv", z(1), one, h["x"], z(I * Bs), h["lab"], h["w1"], z(H * I), h["b1"], z(H), h["w2"],
+                         z(O * H), h["b2"], z(O), z(H * Bs), z(H * Bs), z(O * Bs), z(O * Bs), Bs, I, H, O,
+                         z(1), z(1), h["xd"], z(I * Bs), h["w1d"], z(H * I), h["b1d"], z(H), h["w2d"], z(O * H), h["b2d"], z(O),
+                         z(H * Bs), z(H * Bs), z(O * Bs), z(O * Bs))
+        return run, f"mlp2_ce_{self.mode} on {Bs} of the {self.B} samples (time x {self.B // Bs})", Bs / self.B
+
+
+class Conv(Workload):
+    """Config 4: 8 images of 256 x 256, 64 -> 64 channels, 3 x 3, zero border held in xp,
+    Float32; xp interior ~ N(0,1), w ~ N(0,1)/sqrt(9 C), from the seeded Xoshiro stream."""
+    dtype = "f32"
+    bound = "mfma"
+
+    def __init__(self, mode="b", N=8, C=64, K=64, H=256, W=256):
+        self.mode, self.N, self.C, self.K, self.H, self.W = mode, N, C, K, H, W
+        self.name = f"conv3x3_{mode}"
+        g = 2.0 * N * K * H * W * 9 * C
+        self.kernels = {"b": {"conv_fwd": g, "conv_wgrad": g, "conv_dgrad": g},
+                        "d": {"conv_fwd_d": 3 * g},
+                        "hv": {"conv_fwd_hv": 3 * g, "conv_wgrad": g, "conv_wgrad2": 2 * g, "conv_dgrad_hv": 3 * g}}[mode]
+        self.kernel = next(iter(self.kernels))
+
+    def _host(self, N, H):
+        import numpy as np
+        import stade_hip
+        C, K, W = self.C, self.K, self.W
+        rng = stade_hip.api.Rng(stade_hip.stable_seed("conv3x3"))
+        xp = np.zeros((N, C, H + 2, W + 2), dtype=np.float32)
+        xp[:, :, 1:-1, 1:-1] = stade_hip.rng_normal(rng, N * C * H * W).reshape(N, C, H, W)
+        w = (stade_hip.rng_normal(rng, 9 * C * K) / np.sqrt(9.0 * C)).astype(np.float32)
+        rng2 = stade_hip.api.Rng(stade_hip.stable_seed("conv3x3") + 1)
+        xpd = np.zeros_like(xp)
+        xpd[:, :, 1:-1, 1:-1] = stade_hip.rng_normal(rng2, N * C * H * W).reshape(N, C, H, W)
+        wd = (stade_hip.rng_normal(rng2, 9 * C * K) / np.sqrt(9.0 * C)).astype(np.float32)
+        return dict(xp=xp.ravel(), w=w, xpd=xpd.ravel(), wd=wd)
+
+    def setup(self, dev):
+        import torch
+        N, C, K, H, W = self.N, self.C, self.K, self.H, self.W
+        h = self._host(N, H)
+        f = lambda a: _tensor(a, dev)
+        z = lambda k: torch.zeros(k, dtype=torch.float32, device=dev)
+        nx, nw, no = N * C * (H + 2) * (W + 2), 9 * C * K, N * K * H * W
+        self.t = {k: f(v) for k, v in h.items()}
+        self.t.update(loss=z(1), lossb=f([1.0]).float(), lossd=z(1), lossbd=z(1), xpb=z(nx), xpbd=z(nx), wb=z(nw), wbd=z(nw),
+                      out=z(no), outb=z(no), outd=z(no), outbd=z(no))
+
+    def step(self):
+        import stade_hip
+        t = self.t
+        sz = (self.N, self.C, self.K, self.H, self.W)
+        if self.mode == "b":
+            stade_hip.conv3x3_b(*(t[k] for k in ("loss", "lossb", "xp", "xpb", "w", "wb", "out", "outb")), *sz)
+        elif self.mode == "d":
+            stade_hip.conv3x3_d(*(t[k] for k in ("loss", "lossd", "xp", "xpd", "w", "wd", "out", "outd")), *sz)
+        else:
+            stade_hip.conv3x3_hv(*(t[k] for k in ("loss", "lossb", "xp", "xpb", "w", "wb", "out", "outb")), *sz,
+                                 *(t[k] for k in ("lossd", "lossbd", "xpd", "xpbd", "wd", "wbd", "outd", "outbd")))
+
+    def eval_flops(self):
+        return sum(self.kernels.values()) * 1.0
+
+    def config(self):
+        return {"workload": f"conv3x3_{self.mode}: {self.N} x {self.C} x {self.H} x {self.W} fp32 input (zero border "
+                            f"held in xp), 3x3 {self.C}->{self.K}, loss = 0.5 sum(out^2)",
+                "batch": self.N, "channels": [self.C, self.K], "image": [self.H, self.W]}
+
+    def cpu_sample(self):
+        import numpy as np
+        from oracle import runner
+        Ns, Hs = 1, 32
+        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"conv3x3_{self.mode}.jl", precision="f32", bounds_check=False)
+        h = self._host(Ns, Hs)
+        C, K, W = self.C, self.K, self.W
+        nx, nw, no = Ns * C * (Hs + 2) * (W + 2), 9 * C * K, Ns * K * Hs * W
+        z = lambda k: np.zeros(k, dtype=np.float32)
+        one = np.ones(1, dtype=np.float32)
+        sz = (Ns, C, K, Hs, W)
+
+        def run():
+            if self.mode == "b":
+                lib.call("conv3x3_b", z(1), one, h["xp"], z(nx), h["w"], z(nw), z(no), z(no), *sz)
+            elif self.mode == "d":
+                lib.call("conv3x3_d", z(1), z(1), h["xp"], h["xpd"], h["w"], h["wd"], z(no), z(no), *sz)
+            else:
+                lib.call("conv3x3_hv", z(1), one, h["xp"], z(nx), h["w"], z(nw), z(no), z(no), *sz,
+                         z(1), z(1), h["xpd"], z(nx), h["wd"], z(nw), z(no), z(no))
+        share = (Ns * Hs) / (self.N * self.H)
+        return run, (f"conv3x3_{self.mode} on {Ns} of the {self.N} images, {Hs} of the {self.H} rows "
+                     f"(time x {1 / share:.0f})"), share
+
+
 WORKLOADS = {
     "diffusion2d_b": lambda: Diffusion("b"),
     "diffusion2d_d": lambda: Diffusion("d"),
@@ -314,6 +497,12 @@ WORKLOADS = {
     "burgers1d_b": lambda: Burgers("b"),
     "burgers1d_d": lambda: Burgers("d"),
     "burgers1d_hv": lambda: Burgers("hv"),
+    "mlp2_ce_b": lambda: Mlp("b"),
+    "mlp2_ce_d": lambda: Mlp("d"),
+    "mlp2_ce_hv": lambda: Mlp("hv"),
+    "conv3x3_b": lambda: Conv("b"),
+    "conv3x3_d": lambda: Conv("d"),
+    "conv3x3_hv": lambda: Conv("hv"),
 }
 HEADLINE = "diffusion2d_b"
 
@@ -339,7 +528,23 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     tot, cnt = ctypes.c_double(0), ctypes.c_int64(0)
-    L.stade_hip_profile_read(wl.kernel.encode(), ctypes.byref(tot), ctypes.byref(cnt))
+    per_kernel = {}
+    if getattr(wl, "kernels", None):
+        # the dominant kernel: the matrix-core launch with the largest total time
+        best = None
+        for k in wl.kernels:
+            t_, c_ = ctypes.c_double(0), ctypes.c_int64(0)
+            L.stade_hip_profile_read(k.encode(), ctypes.byref(t_), ctypes.byref(c_))
+            if c_.value:
+                per_kernel[k] = {"ms": t_.value / c_.value, "launches": c_.value,
+                                 "tflops": wl.kernels[k] / (t_.value / c_.value * 1e-3) / 1e12}
+                if best is None or t_.value > best[1]:
+                    best = (k, t_.value, c_.value)
+        if best:
+            wl.kernel = best[0]
+            tot.value, cnt.value = best[1], best[2]
+    else:
+        L.stade_hip_profile_read(wl.kernel.encode(), ctypes.byref(tot), ctypes.byref(cnt))
     L.stade_hip_profile_stop()
     ms_step = (t1 - t0) * 1e3 / steps
     out = {"evals_per_s": steps / (t1 - t0), "ms_per_step": ms_step, "steps": steps, "dtype": wl.dtype}
@@ -353,9 +558,14 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
                                "frac": ach / HBM_PEAK_GBS, "traffic": None}
         else:
             peak = FP32_PEAK_TFLOPS if wl.dtype == "f32" else FP64_PEAK_TFLOPS
-            ach = wl.kernel_flops() / (k_ms * 1e-3) / 1e12
+            ach = wl.kernels[wl.kernel] / (k_ms * 1e-3) / 1e12
             out["roofline"] = {"bound": "mfma", "achieved": ach, "peak": peak, "unit": "TFLOP/s",
                                "frac": ach / peak, "traffic": None}
+    if per_kernel:
+        out["kernels"] = per_kernel
+    if wl.bound == "mfma":
+        out["eval_TFLOPs"] = wl.eval_flops() / (ms_step * 1e-3) / 1e12
+        out["eval_mfma_frac"] = out["eval_TFLOPs"] / FP32_PEAK_TFLOPS
     if wl.bound == "hbm" and wl.algo_bytes():
         out["eval_GBps"] = wl.algo_bytes() / (ms_step * 1e-3) / 1e9
         out["eval_hbm_frac"] = out["eval_GBps"] / HBM_PEAK_GBS
@@ -408,6 +618,8 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--only", action="store_true", help="measure the headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--configs", default="", help="comma-separated workloads to measure besides the headline "
+                                                  "(default: all)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU; the multi-GPU design is described, not run "
@@ -423,10 +635,10 @@ def main():
     others = {}
     if not args.only:
         for nm, mk in WORKLOADS.items():
-            if nm == args.workload:
+            if nm == args.workload or (args.configs and nm not in args.configs.split(",")):
                 continue
             wl = mk()
-            heavy = nm.startswith("burgers1d")
+            heavy = nm.startswith(("burgers1d", "conv3x3", "mlp2_ce"))
             others[nm] = measure(wl, 5 if heavy else max(5, args.steps // 2), 1 if heavy else max(2, args.warmup), dev)
             if not args.no_cpu_baseline:
                 others[nm]["cpu_baseline"] = cpu_baseline(wl, budget_s=4.0, max_runs=5)

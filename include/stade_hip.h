@@ -148,6 +148,23 @@ int32_t stade_hip_mlp2_ce_hv(float* loss, const float* lossb, const float* x, fl
                              const float* b1d, float* b1bd, const float* w2d, float* w2bd, const float* b2d, float* b2bd,
                              float* h1d, float* h1bd, float* zd, float* zbd, hipStream_t stream);
 
+/* ---- config 4: conv3x3(loss, xp, w, out, i_nb, i_c, i_k, i_h, i_w) ----------------------
+ * 3 x 3 cross-correlation, stride 1, zero padding held in the input, then
+ * loss += 0.5 * sum(out .^ 2); Float32.  xp (i_w+2, i_h+2, i_c, i_nb), w (3, 3, i_c, i_k),
+ * out (i_w, i_h, i_k, i_nb), column-major.  replaces conv3x3_b_amdgpu / _d_amdgpu /
+ * _hv_amdgpu (corpus/conv3x3_{b,d,hv}.jl).  xpb covers the padded frame too: taps that read
+ * the padding accumulate their adjoint there, as the generated scatter does. */
+int32_t stade_hip_conv3x3_b(float* loss, const float* lossb, const float* xp, float* xpb, const float* w, float* wb,
+                            float* out, float* outb, int64_t i_nb, int64_t i_c, int64_t i_k, int64_t i_h, int64_t i_w,
+                            hipStream_t stream);
+int32_t stade_hip_conv3x3_d(float* loss, float* lossd, const float* xp, const float* xpd, const float* w, const float* wd,
+                            float* out, float* outd, int64_t i_nb, int64_t i_c, int64_t i_k, int64_t i_h, int64_t i_w,
+                            hipStream_t stream);
+int32_t stade_hip_conv3x3_hv(float* loss, const float* lossb, const float* xp, float* xpb, const float* w, float* wb,
+                             float* out, float* outb, int64_t i_nb, int64_t i_c, int64_t i_k, int64_t i_h, int64_t i_w,
+                             float* lossd, const float* lossbd, const float* xpd, float* xpbd, const float* wd, float* wbd,
+                             float* outd, float* outbd, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

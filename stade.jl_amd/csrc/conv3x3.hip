@@ -1,0 +1,686 @@
+// Config 4: conv3x3 -- 3 x 3 convolution (stride 1, zero padding held in the input) and
+// half the squared norm of the output, Float32.  Executes the generated adjoint, tangent and
+// HVP of corpus/conv3x3.jl (corpus/conv3x3_{b,d,hv}.jl), the functions `stade_amdgpu_file`
+// would port (/root/reference/src/STADE.jl:18604-18605).
+//
+// Layouts (Julia column-major, 0-based below):
+//   xp  (i_w+2, i_h+2, i_c, i_nb): xp[n][c][yp][xq] at ((n*C + c)*Hp + yp)*Wp + xq
+//   w   (3, 3, i_c, i_k):          w[co][c][ky][kx] at ((co*C + c)*3 + ky)*3 + kx
+//   out (i_w, i_h, i_k, i_nb):     out[n][co][y][x] at ((n*K + co)*H + y)*W + x
+//
+// The generated loops are three products over one index space (pixel, tap, c, co):
+//   forward  out[n][co][y][x]   = sum_{c,ky,kx} w[co][c][ky][kx] xp[n][c][y+ky][x+kx]
+//   adjoint  g = outb + (0.5 (2 out)) lossb  (the accumulated outb, then reset to 0)
+//            wb[co][c][ky][kx] += sum_{n,y,x} g[n][co][y][x] xp[n][c][y+ky][x+kx]
+//            xpb[n][c][yp][xq] += sum_{co,ky,kx} w[co][c][ky][kx] g[n][co][yp-ky][xq-kx]
+// All three run on the fp32 matrix cores (v_mfma_f32_32x32x2_f32) as implicit GEMMs: no
+// im2col buffer; each block stages an input patch and a weight slice in LDS and the MFMA
+// operands are read from the patch at tap-shifted offsets.
+//   tap_kernel    forward (and the tangent's two products) and the interior of xpb, which
+//                 is the same shifted product on g with flipped, transposed weights
+//   border_kernel the one-cell frame of xpb (taps that land on the zero padding)
+//   wgrad_kernel  split over pixel tiles, partial 9 x 64 x 64 weight gradients per block
+//   wreduce_kernel sums the partials in a fixed order into wb
+#include "internal.hpp"
+
+#include <algorithm>
+
+namespace stade {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+constexpr int NT = 256;
+
+enum { FWD_B, FWD_D, FWD_HV, DG_B, DG_HV };
+
+__device__ __forceinline__ floatx16 mfma(float a, float b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------------------------------
+// weight layouts for the tap kernel: wt[cin][t][r] (rows padded to a multiple of 64 with
+// zeros).  Forward: cin = c, r = co, t = 3 ky + kx.  Interior of xpb: cin = co, r = c, and
+// the tap flipped (t' = 8 - t), so both products read their source at (y + ky' - 1 + ...).
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(NT) void prep_kernel(const float* __restrict__ w, int C, int K, float* __restrict__ wf,
+                                                  int Kpad, float* __restrict__ wg, int Cpad) {
+    const long nf = (long)C * 9 * Kpad, ng = wg ? (long)K * 9 * Cpad : 0;
+    const long q = (long)blockIdx.x * NT + threadIdx.x;
+    if (q < nf) {
+        const int r = (int)(q % Kpad);
+        const long ct = q / Kpad;
+        const int t = (int)(ct % 9), c = (int)(ct / 9);
+        wf[q] = r < K ? w[((long)r * C + c) * 9 + t] : 0.f;
+    } else if (q < nf + ng) {
+        const long p = q - nf;
+        const int r = (int)(p % Cpad);
+        const long ct = p / Cpad;
+        const int t = (int)(ct % 9), co = (int)(ct / 9);
+        wg[p] = r < C ? w[((long)co * C + r) * 9 + (8 - t)] : 0.f;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// tap kernel: o[r][y][x] = sum_{cin, ty, tx} wt[cin][3 ty + tx][r] * src[cin][y + ty + ofs][x + tx + ofs]
+//
+// Block: 256 threads, a 64-row (r) x (64 x 4 pixel) output tile.  Wave w owns pixel row
+// y0 + w: 2 x 2 MFMA 32 x 32 tiles (r halves x pixel halves).  Input channels advance CC at a
+// time (CC = 16 with one source, 8 with two); each step stages the (4+2) x (64+2) patch of
+// every channel and the 9 x 64 weight rows in LDS.  The next step's global loads are issued
+// into registers before the MFMAs of the current one.  The MFMA k pair (lane / 32) is a pair
+// of channels at the same tap, so every LDS read has a lane base plus an immediate offset.
+// ------------------------------------------------------------------------------------------
+constexpr int TX = 64, TY = 4, RT = 64;
+constexpr int PXW = TX + 2, PYH = TY + 2, PPL = PXW * PYH;  // patch row, rows, plane (floats)
+constexpr int KW = 9 * RT;                                    // weight floats per channel
+
+struct TapArgs {
+    const float* src[2];  // sources (n, cin, SH, SW)
+    const float* wt[2];   // weights [cin][9][Rpad]
+    int Cin, R, Rpad, N;
+    int SH, SW, ofs;      // source plane and patch origin offset
+    int H, W;             // output domain
+    float* o0;            // out / xpb
+    float* o1;            // outd / xpbd
+    int OH, OW, oofs;     // o[((n*R + r)*OH + y + oofs)*OW + x + oofs]
+    float* g0;            // forward adjoint: g = accumulated outb, and its tangent
+    float* g1;
+    float* ob;            // outb, outbd (read, then reset to zero)
+    float* obd;
+    const float* lossb;
+    const float* lossbd;
+    double* partials;     // loss sums per block
+};
+
+template <int MODE>
+__global__ __launch_bounds__(NT) void tap_kernel(TapArgs a) {
+    constexpr int NP = (MODE == FWD_B || MODE == DG_B) ? 1 : 2;  // sources = weight sets = outputs
+    constexpr int CC = 16 / NP;
+    constexpr int PSZ = CC * PPL, WSZ = CC * KW;
+    constexpr int PLD = (NP * PSZ + NT - 1) / NT;
+    constexpr int WLD = NP * WSZ / 4 / NT;
+    static_assert(NP * WSZ % (4 * NT) == 0, "weight stage");
+    constexpr bool FWD = MODE == FWD_B || MODE == FWD_D || MODE == FWD_HV;
+    constexpr int NV = MODE == FWD_B ? 1 : 2;
+
+    __shared__ float lds[NP * (PSZ + WSZ)];
+    __shared__ double red[16 * NV];
+    float* Ps = lds;
+    float* Ws = lds + NP * PSZ;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int x0 = blockIdx.x * TX, y0 = blockIdx.y * TY;
+    const int rtiles = a.Rpad / RT;
+    const int n = blockIdx.z / rtiles, rt = blockIdx.z - n * rtiles;
+
+    float pr[PLD];
+    float4 wr[WLD];
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int q = 0; q < PLD; ++q) {
+            const int f = threadIdx.x + q * NT;
+            float v = 0.f;
+            if (f < NP * PSZ) {
+                const int p = NP == 1 ? 0 : f / PSZ;
+                const int rem = f - p * PSZ;
+                const int cc = rem / PPL, e = rem - cc * PPL;
+                const int ty = e / PXW, tx = e - ty * PXW;
+                const int c = c0 + cc, sy = y0 + ty + a.ofs, sx = x0 + tx + a.ofs;
+                if (c < a.Cin && (unsigned)sy < (unsigned)a.SH && (unsigned)sx < (unsigned)a.SW)
+                    v = a.src[p][((long)(n * a.Cin + c) * a.SH + sy) * a.SW + sx];
+            }
+            pr[q] = v;
+        }
+#pragma unroll
+        for (int q = 0; q < WLD; ++q) {
+            const int f = threadIdx.x + q * NT;  // float4 slot of [w][cc][t][r]
+            const int wi = NP == 1 ? 0 : f / (WSZ / 4);
+            const int rem = f - wi * (WSZ / 4);
+            const int row = rem / (RT / 4), r4 = (rem - row * (RT / 4)) * 4;
+            const int cc = row / 9, t = row - cc * 9;
+            const int c = c0 + cc;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (c < a.Cin) v = *reinterpret_cast<const float4*>(a.wt[wi] + ((long)c * 9 + t) * a.Rpad + rt * RT + r4);
+            wr[q] = v;
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int q = 0; q < PLD; ++q) {
+            const int f = threadIdx.x + q * NT;
+            if (f < NP * PSZ) Ps[f] = pr[q];
+        }
+#pragma unroll
+        for (int q = 0; q < WLD; ++q) {
+            const int f = threadIdx.x + q * NT;
+            *reinterpret_cast<float4*>(Ws + 4 * f) = wr[q];
+        }
+    };
+
+    floatx16 acc[NP][2][2];
+#pragma unroll
+    for (int o = 0; o < NP; ++o)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[o][i][j][q] = 0.f;
+
+    // lane bases: patch channel (2 qq + h), row (wave + ky), column (32 j + l32 + kx);
+    // weight row (2 qq + h, t), column 32 i + l32
+    const int pbase = h * PPL + wave * PXW + l32;
+    const int wbase = h * KW + l32;
+    const int nchunks = (a.Cin + CC - 1) / CC;
+    if (nchunks > 0) load(0);
+    for (int ch = 0; ch < nchunks; ++ch) {
+        __syncthreads();
+        store();
+        __syncthreads();
+        if (ch + 1 < nchunks) load((ch + 1) * CC);
+#pragma unroll
+        for (int qq = 0; qq < CC / 2; ++qq) {
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const int ky = t / 3, kx = t % 3;
+                float pf[NP][2], wf[NP][2];
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) pf[p][j] = Ps[p * PSZ + pbase + 2 * qq * PPL + ky * PXW + kx + 32 * j];
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) wf[p][i] = Ws[p * WSZ + wbase + (2 * qq * 9 + t) * RT + 32 * i];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        acc[0][i][j] = mfma(wf[0][i], pf[0][j], acc[0][i][j]);
+                        if constexpr (NP == 2) {
+                            acc[1][i][j] = mfma(wf[1][i], pf[0][j], acc[1][i][j]);
+                            acc[1][i][j] = mfma(wf[0][i], pf[1][j], acc[1][i][j]);
+                        }
+                    }
+            }
+        }
+    }
+
+    // epilogue: accumulator (i, j, q) is row r = rt*64 + 32 i + 8 (q / 4) + 4 h + q % 4,
+    // pixel x = x0 + 32 j + l32 of row y = y0 + wave
+    double ls[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) ls[k] = 0.0;
+    float lb = 0.f, lbd = 0.f;
+    if constexpr (MODE == FWD_B || MODE == FWD_HV) lb = a.lossb[0];
+    if constexpr (MODE == FWD_HV) lbd = a.lossbd[0];
+    const int y = y0 + wave;
+    if (y < a.H) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int x = x0 + 32 * j + l32;
+                if (x >= a.W) continue;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int r = rt * RT + 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
+                    if (r >= a.R) continue;
+                    const long oi = ((long)(n * a.R + r) * a.OH + y + a.oofs) * a.OW + x + a.oofs;
+                    const float v = acc[0][i][j][q];
+                    if constexpr (FWD) {
+                        a.o0[oi] = v;
+                        ls[0] += 0.5 * (double)v * (double)v;
+                        if constexpr (MODE == FWD_B) {
+                            a.g0[oi] = a.ob[oi] + (0.5f * (2.0f * v)) * lb;
+                            a.ob[oi] = 0.f;
+                        } else {
+                            const float vd = acc[1][i][j][q];
+                            a.o1[oi] = vd;
+                            ls[1] += 0.5 * ((double)(2.0f * v) * (double)vd);
+                            if constexpr (MODE == FWD_HV) {
+                                const float c8 = 0.5f * (2.0f * v);
+                                a.g1[oi] = a.obd[oi] + (lb * (0.5f * (2.0f * vd)) + c8 * lbd);
+                                a.g0[oi] = a.ob[oi] + c8 * lb;
+                                a.ob[oi] = 0.f;
+                                a.obd[oi] = 0.f;
+                            }
+                        }
+                    } else {
+                        a.o0[oi] = a.o0[oi] + v;
+                        if constexpr (MODE == DG_HV) a.o1[oi] = a.o1[oi] + acc[1][i][j][q];
+                    }
+                }
+            }
+    }
+    if constexpr (FWD) block_partials<NV>(ls, red, a.partials);
+}
+
+// loss (and lossd) += the sum of the tap kernel's block partials, rounded once to Float32
+template <int NV>
+__global__ __launch_bounds__(NT) void loss_kernel(const double* __restrict__ partials, int nparts, float* l0, float* l1) {
+    __shared__ double red[16 * NV];
+    double acc[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) acc[k] = 0.0;
+    for (int b = threadIdx.x; b < nparts; b += NT)
+#pragma unroll
+        for (int k = 0; k < NV; ++k) acc[k] += partials[(long)b * NV + k];
+    block_sum<NV>(acc, red);
+    if (threadIdx.x == 0) {
+        l0[0] = (float)((double)l0[0] + acc[0]);
+        if (NV == 2) l1[0] = (float)((double)l1[0] + acc[NV - 1]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// border of xpb: padded cells with yp in {0, Hp-1} or xq in {0, Wp-1}; only taps that land
+// inside the output image contribute.  One thread per (n, c, cell).
+// ------------------------------------------------------------------------------------------
+struct BorderArgs {
+    const float* w;
+    const float* wd;
+    const float* g;
+    const float* gd;
+    float* xpb;
+    float* xpbd;
+    int N, C, K, H, W;
+};
+
+template <bool HV>
+__global__ __launch_bounds__(NT) void border_kernel(BorderArgs a) {
+    const int Wp = a.W + 2, Hp = a.H + 2;
+    const int nb = 2 * Wp + 2 * a.H;
+    const long q = (long)blockIdx.x * NT + threadIdx.x;
+    if (q >= (long)a.N * a.C * nb) return;
+    const int cell = (int)(q % nb);
+    const long plane = q / nb;
+    const int n = (int)(plane / a.C), c = (int)(plane % a.C);
+    int yp, xq;
+    if (cell < Wp) {
+        yp = 0;
+        xq = cell;
+    } else if (cell < 2 * Wp) {
+        yp = Hp - 1;
+        xq = cell - Wp;
+    } else if (cell < 2 * Wp + a.H) {
+        yp = cell - 2 * Wp + 1;
+        xq = 0;
+    } else {
+        yp = cell - 2 * Wp - a.H + 1;
+        xq = Wp - 1;
+    }
+    double s = 0.0, sd = 0.0;
+    for (int co = 0; co < a.K; ++co) {
+        const long wo = ((long)co * a.C + c) * 9;
+        const long go = (long)(n * a.K + co) * a.H;
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky) {
+            const int yy = yp - ky;
+            if (yy < 0 || yy >= a.H) continue;
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                const int xx = xq - kx;
+                if (xx < 0 || xx >= a.W) continue;
+                const long gi = (go + yy) * a.W + xx;
+                const float wv = a.w[wo + 3 * ky + kx], gv = a.g[gi];
+                s += (double)wv * (double)gv;
+                if (HV) sd += (double)a.wd[wo + 3 * ky + kx] * (double)gv + (double)wv * (double)a.gd[gi];
+            }
+        }
+    }
+    const long oi = (plane * Hp + yp) * Wp + xq;
+    a.xpb[oi] = (float)((double)a.xpb[oi] + s);
+    if (HV) a.xpbd[oi] = (float)((double)a.xpbd[oi] + sd);
+}
+
+// ------------------------------------------------------------------------------------------
+// weight gradient: part[split][ct][kt][t][ci][co] = sum over the split's pixel tiles of
+//   sum_p sum_{pixel} x_p[n][c][y+ky][x+kx] * g_p[n][co][y][x]
+// Block: 256 threads, a 64 (c) x 64 (co) slab of all 9 taps; wave (wa, wb) owns the
+// 32 x 32 quarter (c half wa, co half wb) of every tap: 9 accumulator tiles.  Pixel tiles of
+// 32 x 2 pixels: the (2+2) x (32+2) patch of 64 channels and the 64 x 64 g tile are staged in
+// LDS (next tile prefetched into registers); the MFMA k pair is a pair of adjacent pixels.
+// ------------------------------------------------------------------------------------------
+constexpr int WTX = 32, WTY = 2;
+constexpr int XPX = WTX + 2;                   // 34
+constexpr int XPL = XPX * (WTY + 2);           // 136 floats of one channel's patch
+constexpr int XPP = XPL + 1;                   // LDS plane stride (odd)
+constexpr int GPX = WTX * WTY, GPP = GPX + 1;  // 64 pixels, LDS row stride 65
+constexpr int XSZ = 64 * XPP, GSZ = 64 * GPP;
+
+struct WgArgs {
+    const float* x[2];  // xp-shaped
+    const float* g[2];  // out-shaped
+    int N, C, K, H, W;
+    int ntx, nty, ntiles;
+    float* part;
+};
+
+template <int NPR>
+__global__ __launch_bounds__(NT) void wgrad_kernel(WgArgs a) {
+    constexpr int XLD = 64 * XPL / NT;  // 34
+    constexpr int GLD = 64 * GPX / NT;  // 16
+    static_assert(64 * XPL % NT == 0 && 64 * GPX % NT == 0, "wgrad stage");
+    __shared__ float lds[NPR * (XSZ + GSZ)];
+    float* Xs = lds;
+    float* Gs = lds + NPR * XSZ;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int ktn = (a.K + 63) / 64;
+    const int ct = blockIdx.x / ktn, kt = blockIdx.x - ct * ktn;
+    const int c0 = ct * 64, k0 = kt * 64;
+    const int wa = wave & 1, wb = wave >> 1;
+    const int Hp = a.H + 2, Wp = a.W + 2;
+
+    float xr[NPR][XLD], gr[NPR][GLD];
+    auto load = [&](int tile) {
+        const int xt = tile % a.ntx;
+        const int rest = tile / a.ntx;
+        const int yt = rest % a.nty, n = rest / a.nty;
+        const int x0 = xt * WTX, y0 = yt * WTY;
+#pragma unroll
+        for (int p = 0; p < NPR; ++p) {
+#pragma unroll
+            for (int q = 0; q < XLD; ++q) {
+                const int f = threadIdx.x + q * NT;
+                const int ci = f / XPL, e = f - ci * XPL;
+                const int ty = e / XPX, tx = e - ty * XPX;
+                const int c = c0 + ci, yy = y0 + ty, xx = x0 + tx;
+                xr[p][q] = (c < a.C && yy < Hp && xx < Wp) ? a.x[p][((long)(n * a.C + c) * Hp + yy) * Wp + xx] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < GLD; ++q) {
+                const int f = threadIdx.x + q * NT;
+                const int co = f / GPX, px = f - co * GPX;
+                const int k = k0 + co, yy = y0 + px / WTX, xx = x0 + px % WTX;
+                gr[p][q] = (k < a.K && yy < a.H && xx < a.W) ? a.g[p][((long)(n * a.K + k) * a.H + yy) * a.W + xx] : 0.f;
+            }
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int p = 0; p < NPR; ++p) {
+#pragma unroll
+            for (int q = 0; q < XLD; ++q) {
+                const int f = threadIdx.x + q * NT;
+                const int ci = f / XPL;
+                Xs[p * XSZ + ci * XPP + (f - ci * XPL)] = xr[p][q];
+            }
+#pragma unroll
+            for (int q = 0; q < GLD; ++q) {
+                const int f = threadIdx.x + q * NT;
+                const int co = f / GPX;
+                Gs[p * GSZ + co * GPP + (f - co * GPX)] = gr[p][q];
+            }
+        }
+    };
+
+    floatx16 acc[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[t][q] = 0.f;
+
+    // lane bases: patch channel 32 wa + l32, pixel + h;  g row 32 wb + l32, pixel + h
+    const int xb = (32 * wa + l32) * XPP + h;
+    const int gb = (32 * wb + l32) * GPP + h;
+    int tile = blockIdx.y;
+    if (tile < a.ntiles) load(tile);
+    for (; tile < a.ntiles; tile += gridDim.y) {
+        __syncthreads();
+        store();
+        __syncthreads();
+        if (tile + (int)gridDim.y < a.ntiles) load(tile + gridDim.y);
+#pragma unroll
+        for (int s = 0; s < GPX / 2; ++s) {
+            const int py = (2 * s) / WTX, px = (2 * s) % WTX;
+            float gf[NPR];
+#pragma unroll
+            for (int p = 0; p < NPR; ++p) gf[p] = Gs[p * GSZ + gb + 2 * s];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const int ky = t / 3, kx = t % 3;
+#pragma unroll
+                for (int p = 0; p < NPR; ++p) {
+                    const float xf = Xs[p * XSZ + xb + (py + ky) * XPX + px + kx];
+                    acc[t] = mfma(xf, gf[p], acc[t]);
+                }
+            }
+        }
+    }
+    // accumulator (t, q): c = 32 wa + 8 (q / 4) + 4 h + q % 4, co = 32 wb + l32 (slab-local)
+    float* dst = a.part + (long)(blockIdx.y * gridDim.x + blockIdx.x) * 9 * 4096;
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int ci = 32 * wa + 8 * (q >> 2) + 4 * h + (q & 3), co = 32 * wb + l32;
+            dst[t * 4096 + ci * 64 + co] = acc[t][q];
+        }
+}
+
+// wb[co][c][t] += sum over splits (in split order) of the partials
+__global__ __launch_bounds__(NT) void wreduce_kernel(const float* __restrict__ part, int nsplit, int nslab, int ktn, int C,
+                                                     int K, float* __restrict__ wb) {
+    const long q = (long)blockIdx.x * NT + threadIdx.x;
+    if (q >= (long)nslab * 9 * 4096) return;
+    const int co_l = (int)(q & 63), ci_l = (int)((q >> 6) & 63);
+    const long rest = q >> 12;
+    const int t = (int)(rest % 9), slab = (int)(rest / 9);
+    const int ct = slab / ktn, kt = slab - ct * ktn;
+    const int c = ct * 64 + ci_l, k = kt * 64 + co_l;
+    if (c >= C || k >= K) return;
+    double s = 0.0;
+    for (int sp = 0; sp < nsplit; ++sp) s += part[((long)sp * nslab + slab) * 9 * 4096 + (long)t * 4096 + ci_l * 64 + co_l];
+    const long wi = ((long)k * C + c) * 9 + t;
+    wb[wi] = (float)((double)wb[wi] + s);
+}
+
+// ------------------------------------------------------------------------------------------
+// host
+// ------------------------------------------------------------------------------------------
+enum { ADJ, TAN, HVP };
+
+struct Ptrs {
+    float *loss, *lossb, *xp, *xpb, *w, *wb, *out, *outb;
+    float *lossd, *lossbd, *xpd, *xpbd, *wd, *wbd, *outd, *outbd;
+};
+
+struct Dims {
+    int N, C, K, H, W, Hp, Wp, Kpad, Cpad;
+};
+
+int32_t check(int64_t N, int64_t C, int64_t K, int64_t H, int64_t W, const char* fn, Dims& d) {
+    if (N < 0 || C < 0 || K < 0 || H < 0 || W < 0) return set_error(STADE_HIP_EINVAL, "%s: negative size", fn);
+    const double lim = 2147483647.0;
+    if ((double)N * C * (H + 2) * (W + 2) > lim || (double)N * K * H * W > lim || 9.0 * C * K > lim ||
+        (double)N * ((K + 63) / 64) > 65535 || (double)N * ((C + 63) / 64) > 65535 || H > 200000 || W > 200000)
+        return set_error(STADE_HIP_ERANGE, "%s: sizes out of range", fn);
+    d.N = (int)N; d.C = (int)C; d.K = (int)K; d.H = (int)H; d.W = (int)W;
+    d.Hp = d.H + 2; d.Wp = d.W + 2;
+    d.Kpad = (d.K + 63) / 64 * 64;
+    d.Cpad = (d.C + 63) / 64 * 64;
+    const long tapblocks = (long)((d.W + TX - 1) / TX) * ((d.H + TY - 1) / TY) * d.N * (d.Kpad / 64);
+    if (tapblocks * 2 > kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: sizes out of range", fn);
+    return STADE_HIP_OK;
+}
+
+inline size_t up64(size_t n) { return (n + 63) / 64 * 64; }
+
+template <int MODE>
+hipError_t launch_tap(const TapArgs& a, const char* name, hipStream_t stream, unsigned& nblocks) {
+    dim3 grid((a.W + TX - 1) / TX, (a.H + TY - 1) / TY, a.N * (a.Rpad / RT));
+    nblocks = grid.x * grid.y * grid.z;
+    STADE_TIMED(name, stream, (tap_kernel<MODE><<<grid, NT, 0, stream>>>(a)));
+    return hipGetLastError();
+}
+
+template <int NPR>
+int32_t weight_grad(const Dims& d, const float* x0, const float* g0, const float* x1, const float* g1, float* part,
+                    int nsplit, float* wb, const char* name, hipStream_t stream) {
+    WgArgs a{};
+    a.x[0] = x0; a.g[0] = g0; a.x[1] = x1; a.g[1] = g1;
+    a.N = d.N; a.C = d.C; a.K = d.K; a.H = d.H; a.W = d.W;
+    a.ntx = (d.W + WTX - 1) / WTX;
+    a.nty = (d.H + WTY - 1) / WTY;
+    a.ntiles = a.ntx * a.nty * d.N;
+    a.part = part;
+    const int ctn = d.Cpad / 64, ktn = d.Kpad / 64;
+    dim3 grid(ctn * ktn, nsplit);
+    STADE_TIMED(name, stream, (wgrad_kernel<NPR><<<grid, NT, 0, stream>>>(a)));
+    STADE_LAUNCHED("conv3x3 wgrad_kernel");
+    const long nr = (long)ctn * ktn * 9 * 4096;
+    STADE_TIMED("conv_wreduce", stream,
+                (wreduce_kernel<<<(unsigned)((nr + NT - 1) / NT), NT, 0, stream>>>(part, nsplit, ctn * ktn, ktn, d.C, d.K, wb)));
+    STADE_LAUNCHED("conv3x3 wreduce_kernel");
+    return STADE_HIP_OK;
+}
+
+template <int MODE>
+int32_t run(const Ptrs& p, const Dims& d, hipStream_t stream) {
+    if (d.N == 0 || d.K == 0 || d.H == 0 || d.W == 0) return STADE_HIP_OK;
+    Workspace* ws = workspace();
+    if (!ws) return STADE_HIP_ENOMEM;
+    const size_t nwf = up64((size_t)d.C * 9 * d.Kpad), nwg = up64((size_t)d.K * 9 * d.Cpad);
+    const size_t nout = up64((size_t)d.N * d.K * d.H * d.W);
+    const int ctn = d.Cpad / 64, ktn = d.Kpad / 64;
+    const long ntiles = (long)((d.W + WTX - 1) / WTX) * ((d.H + WTY - 1) / WTY) * d.N;
+    // ctn is 0 when C = 0 (no weight gradient to form)
+    const int nsplit = ctn == 0 ? 0 : (int)std::max(1L, std::min(ntiles, (long)std::max(1, 256 / (ctn * ktn))));
+    const size_t npart = (MODE == TAN || d.C == 0) ? 0 : (size_t)nsplit * ctn * ktn * 9 * 4096;
+    const int two = MODE == ADJ ? 1 : 2;
+    const size_t total = two * nwf + (MODE == TAN ? 0 : two * nwg + two * nout) + npart;
+    float* base = (float*)scratch(sizeof(float) * total + 256);
+    if (!base) return STADE_HIP_ENOMEM;
+    float* wf0 = base;
+    float* wf1 = wf0 + nwf;
+    float* wg0 = wf0 + two * nwf;
+    float* wg1 = wg0 + nwg;
+    float* G = wg0 + (MODE == TAN ? 0 : two * nwg);
+    float* GD = G + nout;
+    float* part = G + (MODE == TAN ? 0 : two * nout);
+
+    // weights in tap-kernel layouts
+    {
+        const long n = (long)d.C * 9 * d.Kpad + (MODE == TAN ? 0 : (long)d.K * 9 * d.Cpad);
+        const unsigned nb = (unsigned)((n + NT - 1) / NT);
+        if (n > 0) {
+            STADE_TIMED("conv_prep", stream, (prep_kernel<<<nb, NT, 0, stream>>>(p.w, d.C, d.K, wf0, d.Kpad,
+                                                                                 MODE == TAN ? nullptr : wg0, d.Cpad)));
+            STADE_LAUNCHED("conv3x3 prep_kernel");
+            if (MODE != ADJ) {
+                STADE_TIMED("conv_prep", stream, (prep_kernel<<<nb, NT, 0, stream>>>(p.wd, d.C, d.K, wf1, d.Kpad,
+                                                                                     MODE == TAN ? nullptr : wg1, d.Cpad)));
+                STADE_LAUNCHED("conv3x3 prep_kernel");
+            }
+        }
+    }
+    // forward: out (and outd), loss (and lossd); adjoint seeds g (and gd), outb (and outbd) reset
+    {
+        TapArgs a{};
+        a.src[0] = p.xp; a.src[1] = p.xpd;
+        a.wt[0] = wf0; a.wt[1] = wf1;
+        a.Cin = d.C; a.R = d.K; a.Rpad = d.Kpad; a.N = d.N;
+        a.SH = d.Hp; a.SW = d.Wp; a.ofs = 0;
+        a.H = d.H; a.W = d.W;
+        a.o0 = p.out; a.o1 = p.outd;
+        a.OH = d.H; a.OW = d.W; a.oofs = 0;
+        a.g0 = G; a.g1 = GD; a.ob = p.outb; a.obd = p.outbd;
+        a.lossb = p.lossb; a.lossbd = p.lossbd;
+        a.partials = ws->partials;
+        unsigned nblocks = 0;
+        hipError_t e;
+        if (MODE == ADJ) e = launch_tap<FWD_B>(a, "conv_fwd", stream, nblocks);
+        else if (MODE == TAN) e = launch_tap<FWD_D>(a, "conv_fwd_d", stream, nblocks);
+        else e = launch_tap<FWD_HV>(a, "conv_fwd_hv", stream, nblocks);
+        if (e != hipSuccess) return check_hip(e, "conv3x3 tap_kernel (forward)");
+        if (MODE == ADJ) {
+            STADE_TIMED("conv_loss", stream, (loss_kernel<1><<<1, NT, 0, stream>>>(ws->partials, (int)nblocks, p.loss, nullptr)));
+        } else {
+            STADE_TIMED("conv_loss", stream, (loss_kernel<2><<<1, NT, 0, stream>>>(ws->partials, (int)nblocks, p.loss, p.lossd)));
+        }
+        STADE_LAUNCHED("conv3x3 loss_kernel");
+    }
+    if (MODE == TAN || d.C == 0) return STADE_HIP_OK;
+    // wb += sum xp g;  HVP: wbd += sum (xpd g + xp gd)
+    int32_t rc = weight_grad<1>(d, p.xp, G, nullptr, nullptr, part, nsplit, p.wb, "conv_wgrad", stream);
+    if (rc) return rc;
+    if (MODE == HVP) {
+        rc = weight_grad<2>(d, p.xpd, G, p.xp, GD, part, nsplit, p.wbd, "conv_wgrad2", stream);
+        if (rc) return rc;
+    }
+    // xpb interior += flipped taps over g;  HVP: xpbd += wd g + w gd
+    {
+        TapArgs a{};
+        a.src[0] = G; a.src[1] = GD;
+        a.wt[0] = wg0; a.wt[1] = wg1;
+        a.Cin = d.K; a.R = d.C; a.Rpad = d.Cpad; a.N = d.N;
+        a.SH = d.H; a.SW = d.W; a.ofs = -1;
+        a.H = d.H; a.W = d.W;
+        a.o0 = p.xpb; a.o1 = p.xpbd;
+        a.OH = d.Hp; a.OW = d.Wp; a.oofs = 1;
+        unsigned nblocks = 0;
+        hipError_t e = MODE == ADJ ? launch_tap<DG_B>(a, "conv_dgrad", stream, nblocks)
+                                   : launch_tap<DG_HV>(a, "conv_dgrad_hv", stream, nblocks);
+        if (e != hipSuccess) return check_hip(e, "conv3x3 tap_kernel (xpb)");
+    }
+    // xpb frame
+    {
+        BorderArgs b{p.w, p.wd, G, GD, p.xpb, p.xpbd, d.N, d.C, d.K, d.H, d.W};
+        const long n = (long)d.N * d.C * (2 * d.Wp + 2 * d.H);
+        const unsigned nb = (unsigned)((n + NT - 1) / NT);
+        if (MODE == ADJ) {
+            STADE_TIMED("conv_border", stream, (border_kernel<false><<<nb, NT, 0, stream>>>(b)));
+        } else {
+            STADE_TIMED("conv_border", stream, (border_kernel<true><<<nb, NT, 0, stream>>>(b)));
+        }
+        STADE_LAUNCHED("conv3x3 border_kernel");
+    }
+    return STADE_HIP_OK;
+}
+
+}  // namespace
+}  // namespace stade
+
+using namespace stade;
+
+extern "C" {
+
+int32_t stade_hip_conv3x3_b(float* loss, const float* lossb, const float* xp, float* xpb, const float* w, float* wb,
+                            float* out, float* outb, int64_t i_nb, int64_t i_c, int64_t i_k, int64_t i_h, int64_t i_w,
+                            hipStream_t stream) {
+    Dims d;
+    if (int32_t rc = check(i_nb, i_c, i_k, i_h, i_w, "stade_hip_conv3x3_b", d)) return rc;
+    Ptrs p{};
+    p.loss = loss; p.lossb = (float*)lossb; p.xp = (float*)xp; p.xpb = xpb; p.w = (float*)w; p.wb = wb; p.out = out; p.outb = outb;
+    return run<ADJ>(p, d, stream);
+}
+
+int32_t stade_hip_conv3x3_d(float* loss, float* lossd, const float* xp, const float* xpd, const float* w, const float* wd,
+                            float* out, float* outd, int64_t i_nb, int64_t i_c, int64_t i_k, int64_t i_h, int64_t i_w,
+                            hipStream_t stream) {
+    Dims d;
+    if (int32_t rc = check(i_nb, i_c, i_k, i_h, i_w, "stade_hip_conv3x3_d", d)) return rc;
+    Ptrs p{};
+    p.loss = loss; p.lossd = lossd; p.xp = (float*)xp; p.xpd = (float*)xpd; p.w = (float*)w; p.wd = (float*)wd;
+    p.out = out; p.outd = outd;
+    return run<TAN>(p, d, stream);
+}
+
+int32_t stade_hip_conv3x3_hv(float* loss, const float* lossb, const float* xp, float* xpb, const float* w, float* wb,
+                             float* out, float* outb, int64_t i_nb, int64_t i_c, int64_t i_k, int64_t i_h, int64_t i_w,
+                             float* lossd, const float* lossbd, const float* xpd, float* xpbd, const float* wd, float* wbd,
+                             float* outd, float* outbd, hipStream_t stream) {
+    Dims d;
+    if (int32_t rc = check(i_nb, i_c, i_k, i_h, i_w, "stade_hip_conv3x3_hv", d)) return rc;
+    Ptrs p{};
+    p.loss = loss; p.lossb = (float*)lossb; p.xp = (float*)xp; p.xpb = xpb; p.w = (float*)w; p.wb = wb; p.out = out; p.outb = outb;
+    p.lossd = lossd; p.lossbd = (float*)lossbd; p.xpd = (float*)xpd; p.xpbd = xpbd; p.wd = (float*)wd; p.wbd = wbd;
+    p.outd = outd; p.outbd = outbd;
+    return run<HVP>(p, d, stream);
+}
+
+}  // extern "C"

@@ -47,6 +47,9 @@ ENTRY_POINTS: dict[str, str] = {
     "stade_hip_mlp2_ce_b": "a" * 17 + "iiii",
     "stade_hip_mlp2_ce_d": "a" * 17 + "iiii",
     "stade_hip_mlp2_ce_hv": "a" * 17 + "iiii" + "a" * 16,
+    "stade_hip_conv3x3_b": "a" * 8 + "iiiii",
+    "stade_hip_conv3x3_d": "a" * 8 + "iiiii",
+    "stade_hip_conv3x3_hv": "a" * 8 + "iiiii" + "a" * 8,
 }
 
 _CT = {"a": P, "i": I64, "f": F64, "r": F64P}
@@ -368,3 +371,48 @@ def mlp2_ce_hv(loss, lossb, x, xb, lab, w1, w1b, b1, b1b, w2, w2b, b2, b2b, h1, 
          _arr("w2d", w2d, f, s["w2"]), _arr("w2bd", w2bd, f, s["w2"]), _arr("b2d", b2d, f, O), _arr("b2bd", b2bd, f, O),
          _arr("h1d", h1d, f, s["h1"]), _arr("h1bd", h1bd, f, s["h1"]), _arr("zd", zd, f, s["z"]), _arr("zbd", zbd, f, s["z"])]
     _call("stade_hip_mlp2_ce_hv", a, _stream_of(x))
+
+
+# ------------------------------------------------------------------------------------------
+# config 4: conv3x3(loss, xp, w, out, i_nb, i_c, i_k, i_h, i_w)   (Float32)
+# ------------------------------------------------------------------------------------------
+
+def _conv_sizes(i_nb, i_c, i_k, i_h, i_w):
+    N, C, K, H, W = (_int(n, v) for n, v in (("i_nb", i_nb), ("i_c", i_c), ("i_k", i_k), ("i_h", i_h), ("i_w", i_w)))
+    return N, C, K, H, W, dict(loss=1, xp=(W + 2) * (H + 2) * C * N, w=9 * C * K, out=W * H * K * N)
+
+
+def _conv_args(names, arrays, s):
+    """Validated pointers; a shadow (`<x>b`, `<x>d`, `<x>bd`) has the length of its primal `<x>`."""
+    f = _f32()
+
+    def primal(nm):
+        for suffix in ("bd", "b", "d"):
+            if nm.endswith(suffix) and nm[: -len(suffix)] in s:
+                return nm[: -len(suffix)]
+        return nm
+    return [_arr(nm, v, f, s[primal(nm)]) for nm, v in zip(names, arrays)]
+
+
+def conv3x3_b(loss, lossb, xp, xpb, w, wb, out, outb, i_nb, i_c, i_k, i_h, i_w):
+    """Adjoint of conv3x3 (corpus/conv3x3_b.jl); returns nothing."""
+    N, C, K, H, W, s = _conv_sizes(i_nb, i_c, i_k, i_h, i_w)
+    a = _conv_args(("loss", "lossb", "xp", "xpb", "w", "wb", "out", "outb"), (loss, lossb, xp, xpb, w, wb, out, outb), s)
+    _call("stade_hip_conv3x3_b", a + [N, C, K, H, W], _stream_of(xp))
+
+
+def conv3x3_d(loss, lossd, xp, xpd, w, wd, out, outd, i_nb, i_c, i_k, i_h, i_w):
+    """Tangent of conv3x3 (corpus/conv3x3_d.jl); returns nothing."""
+    N, C, K, H, W, s = _conv_sizes(i_nb, i_c, i_k, i_h, i_w)
+    a = _conv_args(("loss", "lossd", "xp", "xpd", "w", "wd", "out", "outd"), (loss, lossd, xp, xpd, w, wd, out, outd), s)
+    _call("stade_hip_conv3x3_d", a + [N, C, K, H, W], _stream_of(xp))
+
+
+def conv3x3_hv(loss, lossb, xp, xpb, w, wb, out, outb, i_nb, i_c, i_k, i_h, i_w,
+               lossd, lossbd, xpd, xpbd, wd, wbd, outd, outbd):
+    """HVP of conv3x3 (corpus/conv3x3_hv.jl); returns nothing."""
+    N, C, K, H, W, s = _conv_sizes(i_nb, i_c, i_k, i_h, i_w)
+    a = _conv_args(("loss", "lossb", "xp", "xpb", "w", "wb", "out", "outb"), (loss, lossb, xp, xpb, w, wb, out, outb), s)
+    t = _conv_args(("lossd", "lossbd", "xpd", "xpbd", "wd", "wbd", "outd", "outbd"),
+                   (lossd, lossbd, xpd, xpbd, wd, wbd, outd, outbd), s)
+    _call("stade_hip_conv3x3_hv", a + [N, C, K, H, W] + t, _stream_of(xp))

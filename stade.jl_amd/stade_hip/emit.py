@@ -114,6 +114,20 @@ KERNELS: dict[str, KernelSpec] = {
                        + _a("lossd", "lossbd", "xd", "xbd", "w1d", "w1bd", "b1d", "b1bd", "w2d", "w2bd", "b2d", "b2bd",
                             "h1d", "h1bd", "zd", "zbd")),
         }),
+    "conv3x3": KernelSpec(
+        "conv3x3", "Float32",
+        {
+            "b": Mode("stade_hip_conv3x3_b",
+                      _a("loss", "lossb", "xp", "xpb", "w", "wb", "out", "outb")
+                      + (("i_nb", "I"), ("i_c", "I"), ("i_k", "I"), ("i_h", "I"), ("i_w", "I"))),
+            "d": Mode("stade_hip_conv3x3_d",
+                      _a("loss", "lossd", "xp", "xpd", "w", "wd", "out", "outd")
+                      + (("i_nb", "I"), ("i_c", "I"), ("i_k", "I"), ("i_h", "I"), ("i_w", "I"))),
+            "hv": Mode("stade_hip_conv3x3_hv",
+                       _a("loss", "lossb", "xp", "xpb", "w", "wb", "out", "outb")
+                       + (("i_nb", "I"), ("i_c", "I"), ("i_k", "I"), ("i_h", "I"), ("i_w", "I"))
+                       + _a("lossd", "lossbd", "xpd", "xpbd", "wd", "wbd", "outd", "outbd")),
+        }),
 }
 
 

@@ -10,7 +10,7 @@ def _header_syms():
     return set(re.findall(r"\b(stade_hip_\w+)\s*\(", (ROOT / "include" / "stade_hip.h").read_text()))
 
 
-@pytest.mark.parametrize("name", ["affine_lsq", "diffusion2d", "burgers1d", "mlp2_ce"])
+@pytest.mark.parametrize("name", ["affine_lsq", "diffusion2d", "burgers1d", "mlp2_ce", "conv3x3"])
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
 def test_emit_generated_file(tmp_path, name, mode):
     from stade_hip import stade_hip_file
