@@ -618,6 +618,9 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--only", action="store_true", help="measure the headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a device-to-device copy of 1 GiB, 10 times (the reference kernel that scales "
+                         "FETCH_SIZE / WRITE_SIZE counters to bytes)")
     ap.add_argument("--configs", default="", help="comma-separated workloads to measure besides the headline "
                                                   "(default: all)")
     args = ap.parse_args()
@@ -630,6 +633,15 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = 1 << 27
+        src = torch.ones(n, dtype=torch.float64, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": 8 * n, "copy_bytes_written": 8 * n, "launches": 10}))
+        return
     head = WORKLOADS[args.workload]()
     res = measure(head, args.steps, args.warmup, dev)
     others = {}

@@ -7,74 +7,97 @@
 // launch per loop plus a host mapreduce for the loss (10519-10571) and the periodic
 // owner-computes gather (`cgen_gather_periodic_inverse` 7343-7529) for the adjoint scatter.
 //
-// Layout and work per launch:
-//   * 64 x 32 output tiles per 256-thread block: lane = i offset (one 512-byte row segment
-//     per wave load), wave = j offset modulo 4.  u is staged in LDS with a 2-cell periodic
-//     halo, unb with a 1-cell halo.  The adjoint needs the new state at the neighbours of a
-//     cell, so the block recomputes un on its 1-cell halo instead of reading it back.
-//   * adjoint, pass 1: un, loss, w = unb + (2 un) lossb on tile+halo, then the gather
+// Layout and work per launch (row streaming):
+//   * A 256-thread block owns a strip of 256 columns (i) and a chunk of CH rows (j); thread t
+//     owns column c0 + t.  It marches down its rows keeping ring buffers of whole strip rows
+//     in LDS (u: 5 rows, the new state's adjoint seed w: 3 rows), each row with a periodic
+//     halo of 2 columns a side.  Every array element of the chunk is loaded once (plus the
+//     2-row / 2-column halo), and the loads for two rows ahead are issued before the current
+//     row is computed (two register sets, the row loop unrolled by two), so each wave keeps
+//     reads in flight across the barriers.
+//   * adjoint, pass 1, for output row j: un on row j+1 (interior and the 1-column halo),
+//     w = unb + (2 un) lossb there, then the owner-computes gather
 //     ub[c] += w_c + 0.1 (w_E + w_W + w_N + w_S) + 4 (-(0.1 w_c)): each cell owns its ub, no
-//     atomics.  ub is prefetched into registers before the first barrier.  Pass 1 reads unb
-//     but never writes it, so the halo reads cannot race with the reset.  Pass 2 streams the
-//     reset unb = 0 and, in its first block, adds the per-block loss partials of pass 1 (the
-//     second stage of the grid sum).  HBM traffic = 48 B/cell, the algorithmic figure
-//     (u R, un W, unb R+W, ub R+W): 40 B/cell in pass 1, 8 B/cell in pass 2.
-//   * blockIdx -> tile is row-major over tiles with 64-cell-wide tiles along i, so the
-//     blocks that share a j-halo row are a multiple of 8 launches apart whenever the tile
-//     count along i is a multiple of 8, and land on the same XCD (round-robin dispatch).
+//     atomics.  Pass 1 reads unb but never writes it, so the halo reads cannot race with the
+//     reset.  Pass 2 streams the reset unb = 0 and, in its first block, adds the per-block
+//     loss partials of pass 1 (the second stage of the grid sum).  HBM traffic = 48 B/cell,
+//     the algorithmic figure (u R, un W, unb R+W, ub R+W): 40 B/cell in pass 1, 8 in pass 2.
+//   * tangent: un, und for row j from u, ud rows j-1..j+1 (3-row rings), loss partials.
+//   * blockIdx = chunk * strips + strip: the blocks that share a halo row are `strips`
+//     launches apart, on the same XCD (round-robin dispatch) when strips is a multiple of 8.
 #include "internal.hpp"
 #include "../../include/stade_hip.h"
 
 namespace stade {
 namespace {
 
-constexpr int TI = 64, TJ = 32, NT = 256, NW = NT / 64;
-constexpr int UI = TI + 4, UJ = TJ + 4;  // 2-cell halo
-constexpr int WI = TI + 2, WJ = TJ + 2;  // 1-cell halo
-constexpr int RPT = TJ / NW;             // owned rows per thread
+constexpr int SW = 256, NT = SW;  // strip width = threads per block
+constexpr int RW = SW + 4;        // LDS row: 2 halo columns each side (position k = column - c0 + 2)
+constexpr int CH = 32;            // rows per block (measured best of 16 / 32 / 64 at n = 4096)
 
-__device__ __forceinline__ int wrap_any(int x, int n, bool small) { return small ? wrapn(x, n) : wrap1(x, n); }
+// Column geometry of a strip: wi columns c0 .. c0+wi-1; LDS positions 0, 1 hold columns
+// c0-2, c0-1 and positions wi+2, wi+3 hold c0+wi, c0+wi+1 (periodic).
+struct Strip {
+    int c0, wi, j0, wj, n;
+    int hcol[4];  // the 4 halo columns (thread 0..3 loads hcol[t] into position hpos(t))
+    __device__ int hpos(int t) const { return t < 2 ? t : wi + t; }
+};
 
-// un at LDS position (b, a) in the operation order of the generated text:
+__device__ __forceinline__ Strip strip_of(int n, int strips) {
+    Strip s;
+    const int sx = blockIdx.x % strips, cy = blockIdx.x / strips;
+    s.c0 = sx * SW;
+    s.wi = min(SW, n - s.c0);
+    s.j0 = cy * CH;
+    s.wj = min(CH, n - s.j0);
+    s.n = n;
+    s.hcol[0] = wrapn(s.c0 - 2, n);
+    s.hcol[1] = wrapn(s.c0 - 1, n);
+    s.hcol[2] = wrapn(s.c0 + s.wi, n);
+    s.hcol[3] = wrapn(s.c0 + s.wi + 1, n);
+    return s;
+}
+
+// One strip row of an array: the thread's own column and (threads 0..3) a halo column.
+struct RowVal {
+    double own, halo;
+};
+
+// halo = 2: all four halo columns (u, ud of the adjoint: the new state is formed on a
+// 1-column halo); halo = 1: only columns c0-1 and c0+wi (threads 1 and 2)
+__device__ __forceinline__ RowVal load_row(const double* __restrict__ a, const Strip& s, int r, int halo) {
+    const int t = threadIdx.x;
+    const size_t base = (size_t)wrapn(s.j0 + r, s.n) * s.n;
+    RowVal v{0.0, 0.0};
+    if (t < s.wi) v.own = a[base + s.c0 + t];
+    if (halo == 2 ? t < 4 : (t == 1 || t == 2)) v.halo = a[base + s.hcol[t]];
+    return v;
+}
+
+__device__ __forceinline__ void put_row(double* row, const RowVal& v, const Strip& s) {
+    const int t = threadIdx.x;
+    if (t < s.wi) row[t + 2] = v.own;
+    if (t < 4) row[s.hpos(t)] = v.halo;
+}
+
+// un at LDS position k of the middle row, in the operation order of the generated text:
 // u + 0.1 * (u[W] + u[E] + u[S] + u[N] - 4.0 * u)
-template <int W>
-__device__ __forceinline__ double step5(const double (*s)[W], int b, int a) {
-    double c = s[b][a];
-    double t = s[b][a - 1] + s[b][a + 1];
-    t = t + s[b - 1][a];
-    t = t + s[b + 1][a];
+__device__ __forceinline__ double step5(const double* up, const double* uc, const double* dn, int k) {
+    const double c = uc[k];
+    double t = uc[k - 1] + uc[k + 1];
+    t = t + up[k];
+    t = t + dn[k];
     t = t - 4.0 * c;
     return c + 0.1 * t;
 }
 // tangent form: ud + 0.1 * ((((ud[W] + ud[E]) + ud[S]) + ud[N]) + -(4.0 * ud))
-template <int W>
-__device__ __forceinline__ double step5d(const double (*s)[W], int b, int a) {
-    double c = s[b][a];
-    double t = s[b][a - 1] + s[b][a + 1];
-    t = t + s[b - 1][a];
-    t = t + s[b + 1][a];
+__device__ __forceinline__ double step5d(const double* up, const double* uc, const double* dn, int k) {
+    const double c = uc[k];
+    double t = uc[k - 1] + uc[k + 1];
+    t = t + up[k];
+    t = t + dn[k];
     t = t + -(4.0 * c);
     return c + 0.1 * t;
-}
-
-// Stage a (TI + 2h) x (TJ + 2h) periodic tile of src into dst (row stride W), halo h:
-// the 64 interior columns one row per wave instruction, the 2h halo columns separately.
-template <int W>
-__device__ __forceinline__ void stage(double (*dst)[W], const double* __restrict__ src, int i0, int j0, int h, int n,
-                                      bool small) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rows = TJ + 2 * h;
-    const int gi = wrap_any(i0 + lane, n, small);
-    for (int b = wave; b < rows; b += NW) {
-        const int gj = wrap_any(j0 - h + b, n, small);
-        dst[b][lane + h] = src[(size_t)gj * n + gi];
-    }
-    for (int q = threadIdx.x; q < rows * 2 * h; q += NT) {
-        const int b = q / (2 * h), c = q % (2 * h);
-        const int col = c < h ? c : TI + c;  // 0..h-1 and TI+h..TI+2h-1
-        const int gj = wrap_any(j0 - h + b, n, small), gx = wrap_any(i0 - h + col, n, small);
-        dst[b][col] = src[(size_t)gj * n + gx];
-    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -82,30 +105,50 @@ __device__ __forceinline__ void stage(double (*dst)[W], const double* __restrict
 // ---------------------------------------------------------------------------------------
 __global__ __launch_bounds__(NT) void diffusion_d_kernel(const double* __restrict__ u, const double* __restrict__ ud,
                                                          double* __restrict__ un, double* __restrict__ und, int n,
-                                                         int tiles_i, double* partials) {
-    __shared__ double su[WJ][WI];
-    __shared__ double sud[WJ][WI];
+                                                         int strips, double* partials) {
+    __shared__ double su[3][RW];
+    __shared__ double sud[3][RW];
     __shared__ double red[32];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int i0 = (blockIdx.x % tiles_i) * TI, j0 = (blockIdx.x / tiles_i) * TJ;
-    const bool small = n < UJ;
-    stage<WI>(su, u, i0, j0, 1, n, small);
-    stage<WI>(sud, ud, i0, j0, 1, n, small);
-    __syncthreads();
+    const Strip s = strip_of(n, strips);
+    const int t = threadIdx.x, k = t + 2;
     double acc[2] = {0.0, 0.0};
-    const int gi = i0 + lane;
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        const int b = wave + NW * r, gj = j0 + b;
-        if (gi < n && gj < n) {
-            double v = step5<WI>(su, b + 1, lane + 1);
-            double vd = step5d<WI>(sud, b + 1, lane + 1);
-            size_t g = (size_t)gj * n + gi;
+    // rows -1, 0 staged; row 1 in flight
+    put_row(su[0], load_row(u, s, -1, 1), s);
+    put_row(sud[0], load_row(ud, s, -1, 1), s);
+    put_row(su[1], load_row(u, s, 0, 1), s);
+    put_row(sud[1], load_row(ud, s, 0, 1), s);
+    // row r+1 is staged at step r: sets q[0], q[1] hold the rows of the next even / odd step
+    struct Pref {
+        RowVal u, ud;
+    } q[2];
+    auto fetch = [&](Pref& p, int r) {
+        if (r < s.wj) {
+            p.u = load_row(u, s, r + 1, 1);
+            p.ud = load_row(ud, s, r + 1, 1);
+        }
+    };
+    fetch(q[0], 0);
+    fetch(q[1], 1);
+    auto step = [&](int r, Pref& p) {
+        const int sp = r % 3, sc = (r + 1) % 3, sn = (r + 2) % 3;  // rows r-1, r, r+1 (row q in slot (q+1) % 3)
+        put_row(su[sn], p.u, s);
+        put_row(sud[sn], p.ud, s);
+        fetch(p, r + 2);
+        __syncthreads();
+        if (t < s.wi) {
+            const double v = step5(su[sp], su[sc], su[sn], k);
+            const double vd = step5d(sud[sp], sud[sc], sud[sn], k);
+            const size_t g = (size_t)(s.j0 + r) * n + s.c0 + t;
             und[g] = vd;
             un[g] = v;
             acc[1] += (2.0 * v) * vd;
             acc[0] += v * v;
         }
+        __syncthreads();
+    };
+    for (int r = 0; r < s.wj; r += 2) {
+        step(r, q[0]);
+        if (r + 1 < s.wj) step(r + 1, q[1]);
     }
     block_partials<2>(acc, red, partials);
 }
@@ -120,89 +163,129 @@ __global__ __launch_bounds__(NT) void diffusion_b_kernel(const double* __restric
                                                          const double* __restrict__ unb, const double* __restrict__ unbd,
                                                          double* __restrict__ ub, double* __restrict__ ubd,
                                                          const double* __restrict__ lossb, const double* __restrict__ lossbd,
-                                                         int n, int tiles_i, double* partials) {
-    __shared__ double su[UJ][UI];
-    __shared__ double sw[WJ][WI];
-    __shared__ double sud[HV ? UJ : 1][HV ? UI : 1];
-    __shared__ double swd[HV ? WJ : 1][HV ? WI : 1];
+                                                         int n, int strips, double* partials) {
+    __shared__ double su[5][RW];
+    __shared__ double sw[3][RW];
+    __shared__ double sud[HV ? 5 : 1][HV ? RW : 1];
+    __shared__ double swd[HV ? 3 : 1][HV ? RW : 1];
     __shared__ double red[32];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int i0 = (blockIdx.x % tiles_i) * TI, j0 = (blockIdx.x / tiles_i) * TJ;
-    const bool small = n < UJ;
-    const int gi = i0 + lane;
-    // prefetch the owned ub (+ ubd): their latency overlaps the LDS phases
-    double pub[RPT], pubd[RPT];
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        const int gj = j0 + wave + NW * r;
-        const bool live = gi < n && gj < n;
-        pub[r] = live ? ub[(size_t)gj * n + gi] : 0.0;
-        pubd[r] = (HV && live) ? ubd[(size_t)gj * n + gi] : 0.0;
-    }
-    stage<UI>(su, u, i0, j0, 2, n, small);
-    stage<WI>(sw, unb, i0, j0, 1, n, small);
-    if constexpr (HV) {
-        stage<UI>(sud, ud, i0, j0, 2, n, small);
-        stage<WI>(swd, unbd, i0, j0, 1, n, small);
-    }
-    __syncthreads();
+    const Strip s = strip_of(n, strips);
+    const int t = threadIdx.x, k = t + 2;
     const double lb = lossb[0];
     const double lbd = HV ? lossbd[0] : 0.0;
     double acc[2] = {0.0, 0.0};
-    // un and w on the 1-cell halo region: interior columns by lane, then the two halo columns
-    for (int q = threadIdx.x; q < WJ * WI; q += NT) {
-        int b, a;
-        if (q < WJ * TI) {
-            b = q >> 6;
-            a = (q & 63) + 1;
-        } else {
-            int h = q - WJ * TI;
-            b = h >> 1;
-            a = (h & 1) ? WI - 1 : 0;
-        }
-        double v = step5<UI>(su, b + 1, a + 1);
-        double vd = 0.0;
-        if constexpr (HV) {
-            vd = step5d<UI>(sud, b + 1, a + 1);
-            swd[b][a] = swd[b][a] + (lb * (2.0 * vd) + (2.0 * v) * lbd);
-        }
-        sw[b][a] = sw[b][a] + (2.0 * v) * lb;
-        const int oi = i0 + a - 1, oj = j0 + b - 1;
-        if (a >= 1 && a <= TI && b >= 1 && b <= TJ && oi < n && oj < n) {
-            size_t g = (size_t)oj * n + oi;
-            if (HV) {
-                und[g] = vd;
-                acc[1] += (2.0 * v) * vd;
+
+    // un / w of strip row r (interior columns, then threads 0 and 1 the halo columns c0-1 and
+    // c0+wi) from the u rings (rows r-1, r, r+1 in slots (r+1)%5, (r+2)%5, (r+3)%5), into w
+    // slot (r+1)%3; the owned interior of rows 0..wj-1 is stored.  The unb halo values are
+    // held by threads 1 (column c0-1) and 2 (column c0+wi) and shuffled to threads 0 and 1
+    // by every lane, outside the branches.
+    auto new_state_all = [&](int r, const RowVal& nb, const RowVal& nbd) {
+        const double hb0 = __shfl(nb.halo, 1, 64), hb1 = __shfl(nb.halo, 2, 64);
+        const double hbd0 = HV ? __shfl(nbd.halo, 1, 64) : 0.0, hbd1 = HV ? __shfl(nbd.halo, 2, 64) : 0.0;
+        const int sp = (r + 1) % 5, sc = (r + 2) % 5, sn = (r + 3) % 5, sw_ = (r + 1) % 3;
+        const bool own_row = r >= 0 && r < s.wj;
+        auto one = [&](int kk, double b, double bd, bool store) {
+            const double v = step5(su[sp], su[sc], su[sn], kk);
+            double vd = 0.0;
+            if constexpr (HV) {
+                vd = step5d(sud[sp], sud[sc], sud[sn], kk);
+                swd[sw_][kk] = bd + (lb * (2.0 * vd) + (2.0 * v) * lbd);
             }
-            un[g] = v;
-            acc[0] += v * v;
-        }
+            sw[sw_][kk] = b + (2.0 * v) * lb;
+            if (store) {
+                const size_t g = (size_t)(s.j0 + r) * n + s.c0 + t;
+                if (HV) {
+                    und[g] = vd;
+                    acc[1] += (2.0 * v) * vd;
+                }
+                un[g] = v;
+                acc[0] += v * v;
+            }
+        };
+        if (t < s.wi) one(k, nb.own, nbd.own, own_row);
+        if (t == 0) one(1, hb0, hbd0, false);
+        if (t == 1) one(s.wi + 2, hb1, hbd1, false);
+    };
+
+    // prologue: u rows -2..1 and unb rows -1, 0 staged; w rows -1, 0 formed
+    for (int r = -2; r <= 1; ++r) {
+        put_row(su[(r + 2) % 5], load_row(u, s, r, 2), s);
+        if constexpr (HV) put_row(sud[(r + 2) % 5], load_row(ud, s, r, 2), s);
+    }
+    RowVal b_m1 = load_row(unb, s, -1, 1), b_0 = load_row(unb, s, 0, 1);
+    RowVal bd_m1{0.0, 0.0}, bd_0{0.0, 0.0};
+    if constexpr (HV) {
+        bd_m1 = load_row(unbd, s, -1, 1);
+        bd_0 = load_row(unbd, s, 0, 1);
     }
     __syncthreads();
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        const int b = wave + NW * r, gj = j0 + b;
-        if (gi >= n || gj >= n) continue;
-        const int A = lane + 1, B = b + 1;
-        double wc = sw[B][A];
-        double s = wc;
-        s = s + 0.1 * sw[B][A + 1];
-        s = s + 0.1 * sw[B][A - 1];
-        s = s + 0.1 * sw[B + 1][A];
-        s = s + 0.1 * sw[B - 1][A];
-        s = s + 4.0 * -(0.1 * wc);
-        size_t g = (size_t)gj * n + gi;
+    new_state_all(-1, b_m1, bd_m1);
+    new_state_all(0, b_0, bd_0);
+    // step r stages u row r+2 and uses unb row r+1 and ub row r: sets q[0], q[1] hold those
+    // of the next even / odd step, refilled two steps ahead
+    struct Pref {
+        RowVal u, ud, b, bd;
+        double ub, ubd;
+    } q[2];
+    auto fetch = [&](Pref& p, int r) {
+        if (r >= s.wj) return;
+        p.u = load_row(u, s, r + 2, 2);
+        p.b = load_row(unb, s, r + 1, 1);
+        if (t < s.wi) p.ub = ub[(size_t)(s.j0 + r) * n + s.c0 + t];
         if constexpr (HV) {
-            double wcd = swd[B][A];
-            double sd = wcd;
-            sd = sd + 0.1 * swd[B][A + 1];
-            sd = sd + 0.1 * swd[B][A - 1];
-            sd = sd + 0.1 * swd[B + 1][A];
-            sd = sd + 0.1 * swd[B - 1][A];
-            sd = sd + 4.0 * -(0.1 * wcd);
-            ubd[g] = pubd[r] + sd;
+            p.ud = load_row(ud, s, r + 2, 2);
+            p.bd = load_row(unbd, s, r + 1, 1);
+            if (t < s.wi) p.ubd = ubd[(size_t)(s.j0 + r) * n + s.c0 + t];
         }
-        ub[g] = pub[r] + s;
+    };
+    q[0].ud = q[0].bd = q[1].ud = q[1].bd = RowVal{0.0, 0.0};
+    q[0].ub = q[0].ubd = q[1].ub = q[1].ubd = 0.0;
+    fetch(q[0], 0);
+    fetch(q[1], 1);
+    auto step = [&](int r, Pref& p) {
+        // A: stage u row r+2; refill this set for step r+2
+        put_row(su[(r + 4) % 5], p.u, s);
+        if constexpr (HV) put_row(sud[(r + 4) % 5], p.ud, s);
+        const RowVal cb = p.b, cbd = p.bd;
+        const double cub = p.ub, cubd = p.ubd;
+        fetch(p, r + 2);
+        __syncthreads();
+        // B: un and w of row r+1
+        new_state_all(r + 1, cb, cbd);
+        __syncthreads();
+        // C: gather into ub of row r from w rows r-1, r, r+1
+        if (t < s.wi) {
+            const double* wm = sw[r % 3];
+            const double* wc = sw[(r + 1) % 3];
+            const double* wp = sw[(r + 2) % 3];
+            const double c = wc[k];
+            double a = c;
+            a = a + 0.1 * wc[k + 1];
+            a = a + 0.1 * wc[k - 1];
+            a = a + 0.1 * wp[k];
+            a = a + 0.1 * wm[k];
+            a = a + 4.0 * -(0.1 * c);
+            const size_t g = (size_t)(s.j0 + r) * n + s.c0 + t;
+            if constexpr (HV) {
+                const double* dm = swd[r % 3];
+                const double* dc = swd[(r + 1) % 3];
+                const double* dp = swd[(r + 2) % 3];
+                const double cd = dc[k];
+                double ad = cd;
+                ad = ad + 0.1 * dc[k + 1];
+                ad = ad + 0.1 * dc[k - 1];
+                ad = ad + 0.1 * dp[k];
+                ad = ad + 0.1 * dm[k];
+                ad = ad + 4.0 * -(0.1 * cd);
+                ubd[g] = cubd + ad;
+            }
+            ub[g] = cub + a;
+        }
+    };
+    for (int r = 0; r < s.wj; r += 2) {
+        step(r, q[0]);
+        if (r + 1 < s.wj) step(r + 1, q[1]);
     }
     if (HV) {
         block_partials<2>(acc, red, partials);
@@ -240,15 +323,22 @@ __global__ __launch_bounds__(NT) void zero2_kernel(double* __restrict__ a, doubl
 int32_t check_n(int64_t n, const char* fn) {
     if (n < 0) return set_error(STADE_HIP_EINVAL, "%s: n = %lld is negative", fn, (long long)n);
     if (n > 46340) return set_error(STADE_HIP_ERANGE, "%s: n = %lld exceeds 46340 (n*n must fit Int32 cell indices)", fn, (long long)n);
-    int64_t tiles = ((n + TI - 1) / TI) * ((n + TJ - 1) / TJ);
-    if (tiles * 2 > kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: n = %lld needs more reduction slots than the workspace holds", fn, (long long)n);
     return STADE_HIP_OK;
 }
 
+// two 16-byte stores per thread; measured fastest for a 128 MiB fill on MI355X
 unsigned zero_blocks(int64_t count) {
-    int64_t per = (int64_t)NT * 2 * 8;
+    int64_t per = (int64_t)NT * 2 * 2;
     int64_t blocks = (count + per - 1) / per;
     return (unsigned)(blocks > 65536 ? 65536 : (blocks < 1 ? 1 : blocks));
+}
+
+struct Grid {
+    int strips, blocks;
+};
+Grid grid_of(int64_t n) {
+    const int strips = (int)((n + SW - 1) / SW), chunks = (int)((n + CH - 1) / CH);
+    return Grid{strips, strips * chunks};
 }
 
 }  // namespace
@@ -265,11 +355,11 @@ int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, co
     if (!loss || !lossd || !u || !ud || !un || !und) return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_d: null pointer");
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
-    int ti = (int)((n + TI - 1) / TI), tj = (int)((n + TJ - 1) / TJ);
+    const Grid g = grid_of(n);
     STADE_TIMED("diffusion2d_d", stream,
-                diffusion_d_kernel<<<ti * tj, NT, 0, stream>>>(u, ud, un, und, (int)n, ti, ws->partials));
+                diffusion_d_kernel<<<g.blocks, NT, 0, stream>>>(u, ud, un, und, (int)n, g.strips, ws->partials));
     STADE_LAUNCHED("diffusion_d_kernel");
-    STADE_TIMED("finalize", stream, finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, ti * tj, SumOuts{{loss, lossd}}));
+    STADE_TIMED("finalize", stream, finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, g.blocks, SumOuts{{loss, lossd}}));
     STADE_LAUNCHED("finalize_kernel");
     return STADE_HIP_OK;
 }
@@ -281,13 +371,13 @@ int32_t stade_hip_diffusion2d_b(double* loss, const double* lossb, const double*
     if (!loss || !lossb || !u || !ub || !un || !unb) return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_b: null pointer");
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
-    int ti = (int)((n + TI - 1) / TI), tj = (int)((n + TJ - 1) / TJ);
+    const Grid g = grid_of(n);
     STADE_TIMED("diffusion2d_b", stream,
-                diffusion_b_kernel<false><<<ti * tj, NT, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr, lossb,
-                                                                      nullptr, (int)n, ti, ws->partials));
+                diffusion_b_kernel<false><<<g.blocks, NT, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr, lossb,
+                                                                       nullptr, (int)n, g.strips, ws->partials));
     STADE_LAUNCHED("diffusion_b_kernel");
     STADE_TIMED("zero", stream,
-                zero2_kernel<1><<<zero_blocks(n * n), NT, 0, stream>>>(unb, nullptr, (size_t)(n * n), ws->partials, ti * tj,
+                zero2_kernel<1><<<zero_blocks(n * n), NT, 0, stream>>>(unb, nullptr, (size_t)(n * n), ws->partials, g.blocks,
                                                                        SumOuts{{loss}}));
     STADE_LAUNCHED("zero2_kernel");
     return STADE_HIP_OK;
@@ -302,13 +392,13 @@ int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double
         return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_hv: null pointer");
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
-    int ti = (int)((n + TI - 1) / TI), tj = (int)((n + TJ - 1) / TJ);
+    const Grid g = grid_of(n);
     STADE_TIMED("diffusion2d_hv", stream,
-                diffusion_b_kernel<true><<<ti * tj, NT, 0, stream>>>(u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd, (int)n,
-                                                                     ti, ws->partials));
+                diffusion_b_kernel<true><<<g.blocks, NT, 0, stream>>>(u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd, (int)n,
+                                                                      g.strips, ws->partials));
     STADE_LAUNCHED("diffusion_b_kernel<hv>");
     STADE_TIMED("zero", stream,
-                zero2_kernel<2><<<zero_blocks(n * n), NT, 0, stream>>>(unb, unbd, (size_t)(n * n), ws->partials, ti * tj,
+                zero2_kernel<2><<<zero_blocks(n * n), NT, 0, stream>>>(unb, unbd, (size_t)(n * n), ws->partials, g.blocks,
                                                                        SumOuts{{loss, lossd}}));
     STADE_LAUNCHED("zero2_kernel");
     return STADE_HIP_OK;

@@ -8,13 +8,19 @@
 // Up to two segments accumulate into one tile, so a tangent product such as
 // W1d * X + W1 * Xd is one launch.
 //
-// Tiling: a 256-thread block (4 waves) computes a 128 x 128 tile of C; each wave a 64 x 64
-// quarter as 2 x 2 MFMA 32 x 32 tiles (64 accumulator registers per lane).  K advances 16 at
-// a time through two LDS buffers (one barrier per step: the next tile's global loads are
-// issued before the MFMAs of the current one and stored to the other buffer after them).
-// LDS rows are padded by 4 floats.  The MFMA operands are swapped (B tile as the matrix-core
-// A operand) so that the accumulator's lane index runs along m: each epilogue store of a
-// wave covers 32 consecutive rows of a column-major C, a 128-byte segment.
+// Tiling: a 256-thread block (4 waves) computes a 128 x BNT tile of C (BNT = 128 or 64);
+// each wave a 64 x BNT/2 part as 2 x BNT/64 MFMA 32 x 32 tiles.  K advances 16 at a time
+// through two LDS buffers (one barrier per step: the next tile's global loads are issued
+// before the MFMAs of the current one and stored to the other buffer after them).  LDS rows
+// are padded by 4 floats.  The MFMA operands are swapped (B tile as the matrix-core A
+// operand) so that the accumulator's lane index runs along m: each epilogue store of a wave
+// covers 32 consecutive rows of a column-major C, a 128-byte segment.
+//
+// Split K: with `ksplit` > 1 the K steps (of all segments, in order) are cut into ksplit
+// contiguous ranges, one per blockIdx.z; each writes its partial tile to a scratch slice
+// and a second kernel adds the slices in slice order and applies the epilogue.  The host
+// picks the narrow tile and the split so that small-M*N products still give every CU about
+// two blocks.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -24,8 +30,8 @@ namespace gemm {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, KT = 16, NT = 256, PAD = 4;
-constexpr int LDA_S = BM + PAD, LDB_S = BN + PAD;
+constexpr int BM = 128, KT = 16, NT = 256, PAD = 4;
+constexpr int LDA_S = BM + PAD;
 
 struct Seg {
     const float* A;
@@ -38,24 +44,28 @@ struct Args {
     Seg seg[2];
     int nseg;
     int M, N;
+    int ksplit;     // blockIdx.z ranges over ksplit slices of the K steps
+    float* part;    // ksplit > 1: partial tiles, slice z at part + z * M * N, column-major
 };
 
-// Registers holding one 128 x 16 operand tile between its global load and its LDS store.
+// Registers holding one ROWS x 16 operand tile between its global load and its LDS store.
+template <int ROWS>
 struct Stage {
-    float4 v[2];
+    float4 v[ROWS * KT / 4 / NT];
 };
 
-// A tile (m 0..127, k 0..15) of segment s at (m0, k0) into registers; zero outside M x K.
-template <bool KMAJ>
-__device__ __forceinline__ void load_tile(Stage& st, const float* __restrict__ P, long ld, int rows, int K, int r0, int k0,
-                                          bool vec) {
+// A tile (r 0..ROWS-1, k 0..15) at (r0, k0) into registers; zero outside rows x K.
+template <bool KMAJ, int ROWS>
+__device__ __forceinline__ void load_tile(Stage<ROWS>& st, const float* __restrict__ P, long ld, int rows, int K, int r0,
+                                          int k0, bool vec) {
+    constexpr int R4 = ROWS / 4;  // float4 per k row (KMAJ = false)
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
         const int f = threadIdx.x + NT * q;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (!KMAJ) {
-            // rows contiguous: f -> (k = f / 32, r4 = (f % 32) * 4)
-            const int kk = f >> 5, r4 = (f & 31) * 4;
+            // rows contiguous: f -> (k = f / R4, r4 = (f % R4) * 4)
+            const int kk = f / R4, r4 = (f % R4) * 4;
             const int k = k0 + kk, r = r0 + r4;
             if (k < K) {
                 const float* p = P + (long)r + (long)k * ld;
@@ -89,14 +99,15 @@ __device__ __forceinline__ void load_tile(Stage& st, const float* __restrict__ P
 }
 
 // Registers -> LDS tile S[k][r] (row stride LD)
-template <bool KMAJ, int LD>
-__device__ __forceinline__ void store_tile(const Stage& st, float* __restrict__ S) {
+template <bool KMAJ, int ROWS, int LD>
+__device__ __forceinline__ void store_tile(const Stage<ROWS>& st, float* __restrict__ S) {
+    constexpr int R4 = ROWS / 4;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
         const int f = threadIdx.x + NT * q;
         const float4 x = st.v[q];
         if (!KMAJ) {
-            const int kk = f >> 5, r4 = (f & 31) * 4;
+            const int kk = f / R4, r4 = (f % R4) * 4;
             *reinterpret_cast<float4*>(S + kk * LD + r4) = x;
         } else {
             const int rr = f >> 2, k4 = (f & 3) * 4;
@@ -108,100 +119,161 @@ __device__ __forceinline__ void store_tile(const Stage& st, float* __restrict__ 
     }
 }
 
-template <bool A_KM, bool B_KM, class Epi>
+template <bool A_KM, bool B_KM, int BNT, class Epi>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
+    constexpr int LDB_S = BNT + PAD, NJ = BNT / 64;
     __shared__ float As[2][KT * LDA_S];
     __shared__ float Bs[2][KT * LDB_S];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
-    const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BNT;
+    const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BNT / 2);
 
-    // the K steps of all segments, in order
+    // the K steps of all segments, in order; this block's slice of them
     int steps[2], total = 0;
     for (int s = 0; s < g.nseg; ++s) {
         steps[s] = (g.seg[s].K + KT - 1) / KT;
         total += steps[s];
     }
+    const int t_begin = (int)((long)total * blockIdx.z / g.ksplit);
+    const int t_end = (int)((long)total * (blockIdx.z + 1) / g.ksplit);
     auto locate = [&](int t, int& s, int& k0) {
         s = (t < steps[0]) ? 0 : 1;
         k0 = (s == 0 ? t : t - steps[0]) * KT;
     };
 
-    floatx16 acc[2][2];
+    floatx16 acc[2][NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    Stage sa, sb;
-    if (total > 0) {
+    Stage<BM> sa;
+    Stage<BNT> sb;
+    if (t_begin < t_end) {
         int s, k0;
-        locate(0, s, k0);
-        load_tile<A_KM>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
-        load_tile<B_KM>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
-        store_tile<A_KM, LDA_S>(sa, As[0]);
-        store_tile<B_KM, LDB_S>(sb, Bs[0]);
+        locate(t_begin, s, k0);
+        load_tile<A_KM, BM>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
+        load_tile<B_KM, BNT>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
+        store_tile<A_KM, BM, LDA_S>(sa, As[0]);
+        store_tile<B_KM, BNT, LDB_S>(sb, Bs[0]);
     }
     __syncthreads();
-    for (int t = 0; t < total; ++t) {
-        const int cur = t & 1;
-        const bool more = t + 1 < total;
+    for (int t = t_begin; t < t_end; ++t) {
+        const int cur = (t - t_begin) & 1;
+        const bool more = t + 1 < t_end;
         if (more) {
             int s, k0;
             locate(t + 1, s, k0);
-            load_tile<A_KM>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
-            load_tile<B_KM>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
+            load_tile<A_KM, BM>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
+            load_tile<B_KM, BNT>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
         }
         const float* A_ = As[cur];
         const float* B_ = Bs[cur];
 #pragma unroll
         for (int ks = 0; ks < KT / 2; ++ks) {
             const int kk = ks * 2 + (lane >> 5);
-            float a[2], b[2];
+            float a[2], b[NJ];
 #pragma unroll
             for (int i = 0; i < 2; ++i) a[i] = A_[kk * LDA_S + wm + i * 32 + (lane & 31)];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = B_[kk * LDB_S + wn + j * 32 + (lane & 31)];
+            for (int j = 0; j < NJ; ++j) b[j] = B_[kk * LDB_S + wn + j * 32 + (lane & 31)];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j], a[i], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < NJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j], a[i], acc[i][j], 0, 0, 0);
         }
         if (more) {
-            store_tile<A_KM, LDA_S>(sa, As[cur ^ 1]);
-            store_tile<B_KM, LDB_S>(sb, Bs[cur ^ 1]);
+            store_tile<A_KM, BM, LDA_S>(sa, As[cur ^ 1]);
+            store_tile<B_KM, BNT, LDB_S>(sb, Bs[cur ^ 1]);
         }
         __syncthreads();
     }
     // accumulator (i, j, r): m = m0 + wm + 32 i + lane % 32,  n = n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4
+    float* part = g.ksplit > 1 ? g.part + (long)blockIdx.z * g.M * g.N : nullptr;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int m = m0 + wm + i * 32 + (lane & 31);
         if (m >= g.M) continue;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (n < g.N) epi(m, n, acc[i][j][r]);
+                if (n < g.N) {
+                    if (part) part[m + (long)n * g.M] = acc[i][j][r];
+                    else epi(m, n, acc[i][j][r]);
+                }
             }
     }
 }
 
+// second stage of a split-K product: C(m, n) = sum over slices in order, then the epilogue
+template <class Epi>
+__global__ __launch_bounds__(NT) void splitk_reduce_kernel(const float* __restrict__ part, int ksplit, int M, int N, Epi epi) {
+    const long q = (long)blockIdx.x * NT + threadIdx.x;
+    const long mn = (long)M * N;
+    if (q >= mn) return;
+    float s = part[q];
+    for (int z = 1; z < ksplit; ++z) s += part[q + z * mn];
+    epi((int)(q % M), (int)(q / M), s);
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Launch; returns the hipError of the launch.
+// Tile width and K split for an M x N x K product on `cus` compute units: the wide tile
+// when it gives at least two blocks per CU, else the narrow one, split along K (slices of at
+// least 256) until there are about two blocks per CU.
+struct Plan {
+    int bnt, ksplit;
+};
+inline Plan plan(int M, int N, int Ktot, int cus) {
+    const long wide = (long)((M + BM - 1) / BM) * ((N + 127) / 128);
+    if (wide >= 2L * cus) return Plan{128, 1};
+    const long narrow = (long)((M + BM - 1) / BM) * ((N + 63) / 64);
+    int ks = 1;
+    while (narrow * ks < 2L * cus && Ktot / (ks * 2) >= 256 && ks < 16) ks *= 2;
+    return Plan{64, ks};
+}
+
+// Number of compute units of the current device (cached per process for device 0..15).
+inline int device_cus() {
+    static int cached[16] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+    if (!cached[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
+// Launch; returns the hipError of the launch.  `part` must hold ksplit * M * N floats when
+// the plan splits K (ask with plan() first); it may be null otherwise.
 template <bool A_KM, bool B_KM, class Epi>
-hipError_t launch(const Args& g, Epi epi, hipStream_t stream) {
+hipError_t launch(Args g, Epi epi, hipStream_t stream, const Plan& p) {
     if (g.M <= 0 || g.N <= 0) return hipSuccess;
     bool vec = true;
     for (int s = 0; s < g.nseg; ++s) {
         vec = vec && aligned16(g.seg[s].A) && aligned16(g.seg[s].B) && g.seg[s].lda % 4 == 0 && g.seg[s].ldb % 4 == 0;
     }
-    dim3 grid((g.M + BM - 1) / BM, (g.N + BN - 1) / BN);
-    gemm_kernel<A_KM, B_KM, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);
+    g.ksplit = p.ksplit;
+    if (p.ksplit > 1 && !g.part) return hipErrorInvalidValue;
+    if (p.bnt == 128) {
+        dim3 grid((g.M + BM - 1) / BM, (g.N + 127) / 128, p.ksplit);
+        gemm_kernel<A_KM, B_KM, 128, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);
+    } else {
+        dim3 grid((g.M + BM - 1) / BM, (g.N + 63) / 64, p.ksplit);
+        gemm_kernel<A_KM, B_KM, 64, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);
+    }
+    if (p.ksplit > 1) {
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const long mn = (long)g.M * g.N;
+        splitk_reduce_kernel<Epi><<<(unsigned)((mn + NT - 1) / NT), NT, 0, stream>>>(g.part, p.ksplit, g.M, g.N, epi);
+    }
     return hipGetLastError();
 }
 

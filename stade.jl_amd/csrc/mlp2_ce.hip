@@ -19,6 +19,8 @@
 // The tangent adds S1d = W1d X + W1 Xd (one two-segment GEMM, epilogue h1d = (1 - h1^2)(S1d +
 // b1d)); the HVP adds the tangents of every backward product as two-segment GEMMs.
 #include "internal.hpp"
+
+#include <algorithm>
 #include "gemm_f32.hpp"
 #include "../../include/stade_hip.h"
 
@@ -352,31 +354,55 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     const int nchunks = (B + SC - 1) / SC;
     const size_t nD1 = (size_t)H * B, nD2 = (size_t)O * B, nC = (size_t)nchunks * 2 * (O + 1) * H;
     const int hv = MODE == HVP ? 2 : 1;
-    float* D1 = (float*)scratch(sizeof(float) * (hv * (nD1 + nD2) + nC) + 256);
+    using namespace gemm;
+    // tile and K-split plans of the matrix-core products (two-segment launches have twice the K)
+    const int cus = device_cus();
+    const Plan p_s1 = plan(H, B, I, cus), p_s1d = plan(H, B, 2 * I, cus);
+    const Plan p_w1b = plan(H, I, B, cus), p_w1bd = plan(H, I, 2 * B, cus);
+    const Plan p_xb = plan(I, B, H, cus), p_xbd = plan(I, B, 2 * H, cus);
+    size_t npart = 0;
+    auto need = [&](const Plan& q, long M, long N) {
+        if (q.ksplit > 1) npart = std::max(npart, (size_t)q.ksplit * M * N);
+    };
+    need(p_s1, H, B);
+    if (MODE != ADJ) need(p_s1d, H, B);
+    if (MODE != TAN) {
+        need(p_w1b, H, I);
+        need(p_xb, I, B);
+    }
+    if (MODE == HVP) {
+        need(p_w1bd, H, I);
+        need(p_xbd, I, B);
+    }
+    npart = (npart + 63) / 64 * 64;
+    const size_t nlocal = hv * (nD1 + nD2) + nC;
+    float* D1 = (float*)scratch(sizeof(float) * ((nlocal + 63) / 64 * 64 + npart) + 256);
     if (!D1) return STADE_HIP_ENOMEM;
     float *D2 = D1 + nD1, *D1d = D2 + nD2, *D2d = D1d + (MODE == HVP ? nD1 : 0), *cpart = D2d + (MODE == HVP ? nD2 : 0);
+    float* kpart = D1 + (nlocal + 63) / 64 * 64;
     int* err = (int*)(ws->dscalars + 16);
-    using namespace gemm;
     // forward: h1 = tanh(W1 x + b1)
     {
         Args g{};
+        g.part = kpart;
         g.seg[0] = Seg{p.w1, p.x, H, I, I};
         g.nseg = 1;
         g.M = H;
         g.N = B;
         hipError_t e;
-        STADE_TIMED("mlp_gemm_s1", stream, e = (launch<false, true>(g, EpiTanh{p.h1, p.b1, H}, stream)));
+        STADE_TIMED("mlp_gemm_s1", stream, e = (launch<false, true>(g, EpiTanh{p.h1, p.b1, H}, stream, p_s1)));
         if (e != hipSuccess) return check_hip(e, "mlp gemm s1");
     }
     if (MODE != ADJ) {
         Args g{};
+        g.part = kpart;
         g.seg[0] = Seg{p.w1d, p.x, H, I, I};
         g.seg[1] = Seg{p.w1, p.xd, H, I, I};
         g.nseg = 2;
         g.M = H;
         g.N = B;
         hipError_t e;
-        STADE_TIMED("mlp_gemm_s1d", stream, e = (launch<false, true>(g, EpiTanhD{p.h1d, p.h1, p.b1d, H}, stream)));
+        STADE_TIMED("mlp_gemm_s1d", stream, e = (launch<false, true>(g, EpiTanhD{p.h1d, p.h1, p.b1d, H}, stream, p_s1d)));
         if (e != hipSuccess) return check_hip(e, "mlp gemm s1d");
     }
     HeadArgs h{};
@@ -405,36 +431,38 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     // W1b += d1 x'   (M = H, N = I, K = B);  HVP: W1bd += d1 xd' + d1d x'
     {
         Args g{};
+        g.part = kpart;
         g.seg[0] = Seg{D1, p.x, H, I, B};
         g.nseg = 1;
         g.M = H;
         g.N = I;
         hipError_t e;
-        STADE_TIMED("mlp_gemm_w1b", stream, e = (launch<false, false>(g, EpiAcc{p.w1b, H}, stream)));
+        STADE_TIMED("mlp_gemm_w1b", stream, e = (launch<false, false>(g, EpiAcc{p.w1b, H}, stream, p_w1b)));
         if (e != hipSuccess) return check_hip(e, "mlp gemm w1b");
         if (MODE == HVP) {
             g.seg[0] = Seg{D1, p.xd, H, I, B};
             g.seg[1] = Seg{D1d, p.x, H, I, B};
             g.nseg = 2;
-            STADE_TIMED("mlp_gemm_w1bd", stream, e = (launch<false, false>(g, EpiAcc{p.w1bd, H}, stream)));
+            STADE_TIMED("mlp_gemm_w1bd", stream, e = (launch<false, false>(g, EpiAcc{p.w1bd, H}, stream, p_w1bd)));
             if (e != hipSuccess) return check_hip(e, "mlp gemm w1bd");
         }
     }
     // Xb += W1' d1   (M = I, N = B, K = H);  HVP: Xbd += W1d' d1 + W1' d1d
     {
         Args g{};
+        g.part = kpart;
         g.seg[0] = Seg{p.w1, D1, H, H, H};
         g.nseg = 1;
         g.M = I;
         g.N = B;
         hipError_t e;
-        STADE_TIMED("mlp_gemm_xb", stream, e = (launch<true, true>(g, EpiAcc{p.xb, I}, stream)));
+        STADE_TIMED("mlp_gemm_xb", stream, e = (launch<true, true>(g, EpiAcc{p.xb, I}, stream, p_xb)));
         if (e != hipSuccess) return check_hip(e, "mlp gemm xb");
         if (MODE == HVP) {
             g.seg[0] = Seg{p.w1d, D1, H, H, H};
             g.seg[1] = Seg{p.w1, D1d, H, H, H};
             g.nseg = 2;
-            STADE_TIMED("mlp_gemm_xbd", stream, e = (launch<true, true>(g, EpiAcc{p.xbd, I}, stream)));
+            STADE_TIMED("mlp_gemm_xbd", stream, e = (launch<true, true>(g, EpiAcc{p.xbd, I}, stream, p_xbd)));
             if (e != hipSuccess) return check_hip(e, "mlp gemm xbd");
         }
     }
