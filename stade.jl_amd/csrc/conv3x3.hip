@@ -18,7 +18,8 @@
 // operands are read from the patch at tap-shifted offsets.
 //   tap_kernel    forward (and the tangent's two products) and the interior of xpb, which
 //                 is the same shifted product on g with flipped, transposed weights
-//   border_kernel the one-cell frame of xpb (taps that land on the zero padding)
+//   border_kernel the one-cell frame of xpb (taps that land on the zero padding): four 1-D
+//                 3-tap line correlations
 //   wgrad_kernel  split over pixel tiles, partial 9 x 64 x 64 weight gradients per block
 //   wreduce_kernel sums the partials in a fixed order into wb
 #include "internal.hpp"
@@ -275,9 +276,18 @@ __global__ __launch_bounds__(NT) void loss_kernel(const double* __restrict__ par
 }
 
 // ------------------------------------------------------------------------------------------
-// border of xpb: padded cells with yp in {0, Hp-1} or xq in {0, Wp-1}; only taps that land
-// inside the output image contribute.  One thread per (n, c, cell).
+// frame of xpb: padded cells with yp in {0, Hp-1} or xq in {0, Wp-1}.  On each edge only one
+// tap row (or column) lands inside the image, so an edge is a 1-D 3-tap full correlation
+// along one line of g:
+//   top    (yp = 0,    p = xq in 0..W+1):  sum_co sum_d w[co][c][0][d]  g[co][0][p - d]
+//   bottom (yp = Hp-1, p = xq):            sum_co sum_d w[co][c][2][d]  g[co][H-1][p - d]
+//   left   (xq = 0,    p = yp-1 in 0..H-1): sum_co sum_d w[co][c][d][0] g[co][p + 1 - d][0]
+//   right  (xq = Wp-1, p = yp-1):          sum_co sum_d w[co][c][d][2]  g[co][p + 1 - d][W-1]
+// (g zero outside the image).  Block: 64 cells of one edge x 16 channels c; output
+// channels advance 16 at a time through LDS (the g line segment and the weight slice).
 // ------------------------------------------------------------------------------------------
+constexpr int BSEG = 64, BKC = 16, BCG = 16;
+
 struct BorderArgs {
     const float* w;
     const float* wd;
@@ -290,49 +300,77 @@ struct BorderArgs {
 
 template <bool HV>
 __global__ __launch_bounds__(NT) void border_kernel(BorderArgs a) {
-    const int Wp = a.W + 2, Hp = a.H + 2;
-    const int nb = 2 * Wp + 2 * a.H;
-    const long q = (long)blockIdx.x * NT + threadIdx.x;
-    if (q >= (long)a.N * a.C * nb) return;
-    const int cell = (int)(q % nb);
-    const long plane = q / nb;
-    const int n = (int)(plane / a.C), c = (int)(plane % a.C);
-    int yp, xq;
-    if (cell < Wp) {
-        yp = 0;
-        xq = cell;
-    } else if (cell < 2 * Wp) {
-        yp = Hp - 1;
-        xq = cell - Wp;
-    } else if (cell < 2 * Wp + a.H) {
-        yp = cell - 2 * Wp + 1;
-        xq = 0;
-    } else {
-        yp = cell - 2 * Wp - a.H + 1;
-        xq = Wp - 1;
-    }
-    double s = 0.0, sd = 0.0;
-    for (int co = 0; co < a.K; ++co) {
-        const long wo = ((long)co * a.C + c) * 9;
-        const long go = (long)(n * a.K + co) * a.H;
-#pragma unroll
-        for (int ky = 0; ky < 3; ++ky) {
-            const int yy = yp - ky;
-            if (yy < 0 || yy >= a.H) continue;
-#pragma unroll
-            for (int kx = 0; kx < 3; ++kx) {
-                const int xx = xq - kx;
-                if (xx < 0 || xx >= a.W) continue;
-                const long gi = (go + yy) * a.W + xx;
-                const float wv = a.w[wo + 3 * ky + kx], gv = a.g[gi];
-                s += (double)wv * (double)gv;
-                if (HV) sd += (double)a.wd[wo + 3 * ky + kx] * (double)gv + (double)wv * (double)a.gd[gi];
+    constexpr int NG = HV ? 2 : 1;
+    __shared__ float gl[NG][BKC][BSEG + 2];
+    __shared__ float wv[NG][BKC][BCG][3];
+    const int e = blockIdx.y;
+    const int L = e < 2 ? a.W + 2 : a.H;
+    const int p0 = blockIdx.x * BSEG;
+    if (p0 >= L) return;  // whole block
+    const int ncg = (a.C + BCG - 1) / BCG;
+    const int n = blockIdx.z / ncg, c0 = (blockIdx.z % ncg) * BCG;
+    const int off = e < 2 ? 0 : 1;
+    const int fixed = (e == 0 || e == 2) ? 0 : 2;
+    const int lim = e < 2 ? a.W : a.H;
+    const int cell = threadIdx.x & 63, cg = threadIdx.x >> 6;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f}, accd[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < a.K; k0 += BKC) {
+        __syncthreads();
+        for (int f = threadIdx.x; f < BKC * (BSEG + 2); f += NT) {
+            const int kk = f / (BSEG + 2), i = f - kk * (BSEG + 2);
+            const int co = k0 + kk, q = p0 + off - 2 + i;
+            float v = 0.f, vd = 0.f;
+            if (co < a.K && q >= 0 && q < lim) {
+                const long plane = (long)(n * a.K + co) * a.H;
+                const long gi = e < 2 ? (plane + (e == 0 ? 0 : a.H - 1)) * a.W + q : (plane + q) * a.W + (e == 2 ? 0 : a.W - 1);
+                v = a.g[gi];
+                if (HV) vd = a.gd[gi];
             }
+            gl[0][kk][i] = v;
+            if (HV) gl[NG - 1][kk][i] = vd;
         }
+        for (int f = threadIdx.x; f < BKC * BCG * 3; f += NT) {
+            const int kk = f / (BCG * 3), r = f - kk * (BCG * 3);
+            const int cc = r / 3, d = r - cc * 3;
+            const int co = k0 + kk, c = c0 + cc;
+            float v = 0.f, vd = 0.f;
+            if (co < a.K && c < a.C) {
+                const int ky = e < 2 ? fixed : d, kx = e < 2 ? d : fixed;
+                const long wi = ((long)co * a.C + c) * 9 + 3 * ky + kx;
+                v = a.w[wi];
+                if (HV) vd = a.wd[wi];
+            }
+            wv[0][kk][cc][d] = v;
+            if (HV) wv[NG - 1][kk][cc][d] = vd;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int kk = 0; kk < BKC; ++kk)
+#pragma unroll
+            for (int d = 0; d < 3; ++d) {
+                const float gv = gl[0][kk][cell + 2 - d];
+                const float gvd = HV ? gl[NG - 1][kk][cell + 2 - d] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float wc = wv[0][kk][cg + 4 * i][d];
+                    acc[i] += wc * gv;
+                    if (HV) accd[i] += wv[NG - 1][kk][cg + 4 * i][d] * gv + wc * gvd;
+                }
+            }
     }
-    const long oi = (plane * Hp + yp) * Wp + xq;
-    a.xpb[oi] = (float)((double)a.xpb[oi] + s);
-    if (HV) a.xpbd[oi] = (float)((double)a.xpbd[oi] + sd);
+    const int p = p0 + cell;
+    if (p >= L) return;
+    const int Hp = a.H + 2, Wp = a.W + 2;
+    const int yp = e == 0 ? 0 : e == 1 ? Hp - 1 : p + 1;
+    const int xq = e < 2 ? p : (e == 2 ? 0 : Wp - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = c0 + cg + 4 * i;
+        if (c >= a.C) continue;
+        const long oi = ((long)(n * a.C + c) * Hp + yp) * Wp + xq;
+        a.xpb[oi] = a.xpb[oi] + acc[i];
+        if (HV) a.xpbd[oi] = a.xpbd[oi] + accd[i];
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -462,19 +500,28 @@ __global__ __launch_bounds__(NT) void wgrad_kernel(WgArgs a) {
         }
 }
 
-// wb[co][c][t] += sum over splits (in split order) of the partials
+// wb[co][c][t] += the sum of the partials over splits.  Block: 64 consecutive partial
+// elements x 4 split lanes; lane l sums splits l, l+4, ... in order, then the 4 lane sums
+// are added in lane order (a fixed order: the result does not depend on scheduling).
 __global__ __launch_bounds__(NT) void wreduce_kernel(const float* __restrict__ part, int nsplit, int nslab, int ktn, int C,
                                                      int K, float* __restrict__ wb) {
-    const long q = (long)blockIdx.x * NT + threadIdx.x;
-    if (q >= (long)nslab * 9 * 4096) return;
+    __shared__ double red[4][64];
+    const long total = (long)nslab * 9 * 4096;
+    const int el = threadIdx.x & 63, sl = threadIdx.x >> 6;
+    const long q = (long)blockIdx.x * 64 + el;
+    double s = 0.0;
+    if (q < total)
+        for (int sp = sl; sp < nsplit; sp += 4) s += part[(long)sp * total + q];
+    red[sl][el] = s;
+    __syncthreads();
+    if (sl != 0 || q >= total) return;
+    s = ((red[0][el] + red[1][el]) + red[2][el]) + red[3][el];
     const int co_l = (int)(q & 63), ci_l = (int)((q >> 6) & 63);
     const long rest = q >> 12;
     const int t = (int)(rest % 9), slab = (int)(rest / 9);
     const int ct = slab / ktn, kt = slab - ct * ktn;
     const int c = ct * 64 + ci_l, k = kt * 64 + co_l;
     if (c >= C || k >= K) return;
-    double s = 0.0;
-    for (int sp = 0; sp < nsplit; ++sp) s += part[((long)sp * nslab + slab) * 9 * 4096 + (long)t * 4096 + ci_l * 64 + co_l];
     const long wi = ((long)k * C + c) * 9 + t;
     wb[wi] = (float)((double)wb[wi] + s);
 }
@@ -497,7 +544,7 @@ int32_t check(int64_t N, int64_t C, int64_t K, int64_t H, int64_t W, const char*
     if (N < 0 || C < 0 || K < 0 || H < 0 || W < 0) return set_error(STADE_HIP_EINVAL, "%s: negative size", fn);
     const double lim = 2147483647.0;
     if ((double)N * C * (H + 2) * (W + 2) > lim || (double)N * K * H * W > lim || 9.0 * C * K > lim ||
-        (double)N * ((K + 63) / 64) > 65535 || (double)N * ((C + 63) / 64) > 65535 || H > 200000 || W > 200000)
+        (double)N * ((K + 63) / 64) > 65535 || (double)N * ((C + 15) / 16) > 65535 || H > 200000 || W > 200000)
         return set_error(STADE_HIP_ERANGE, "%s: sizes out of range", fn);
     d.N = (int)N; d.C = (int)C; d.K = (int)K; d.H = (int)H; d.W = (int)W;
     d.Hp = d.H + 2; d.Wp = d.W + 2;
@@ -534,7 +581,7 @@ int32_t weight_grad(const Dims& d, const float* x0, const float* g0, const float
     STADE_LAUNCHED("conv3x3 wgrad_kernel");
     const long nr = (long)ctn * ktn * 9 * 4096;
     STADE_TIMED("conv_wreduce", stream,
-                (wreduce_kernel<<<(unsigned)((nr + NT - 1) / NT), NT, 0, stream>>>(part, nsplit, ctn * ktn, ktn, d.C, d.K, wb)));
+                (wreduce_kernel<<<(unsigned)((nr + 63) / 64), NT, 0, stream>>>(part, nsplit, ctn * ktn, ktn, d.C, d.K, wb)));
     STADE_LAUNCHED("conv3x3 wreduce_kernel");
     return STADE_HIP_OK;
 }
@@ -630,12 +677,11 @@ int32_t run(const Ptrs& p, const Dims& d, hipStream_t stream) {
     // xpb frame
     {
         BorderArgs b{p.w, p.wd, G, GD, p.xpb, p.xpbd, d.N, d.C, d.K, d.H, d.W};
-        const long n = (long)d.N * d.C * (2 * d.Wp + 2 * d.H);
-        const unsigned nb = (unsigned)((n + NT - 1) / NT);
+        const dim3 grid((std::max(d.W + 2, d.H) + BSEG - 1) / BSEG, 4, d.N * ((d.C + BCG - 1) / BCG));
         if (MODE == ADJ) {
-            STADE_TIMED("conv_border", stream, (border_kernel<false><<<nb, NT, 0, stream>>>(b)));
+            STADE_TIMED("conv_border", stream, (border_kernel<false><<<grid, NT, 0, stream>>>(b)));
         } else {
-            STADE_TIMED("conv_border", stream, (border_kernel<true><<<nb, NT, 0, stream>>>(b)));
+            STADE_TIMED("conv_border", stream, (border_kernel<true><<<grid, NT, 0, stream>>>(b)));
         }
         STADE_LAUNCHED("conv3x3 border_kernel");
     }

@@ -62,8 +62,14 @@ struct EpiAcc {  // C += v (a shadow accumulated, as the generated code does)
 };
 
 // ---------------------------------------------------------------------------------------
-// head: one wave per sample
+// head: one wave per sample, 512-thread blocks.  With LDSW (the adjoint, i_h <= HLDS) the block first
+// copies W2 (and W2d) into LDS as [j][o] rows padded to OP = 17 floats: a lane's reads of
+// its columns j = lane + 64 q are one base register plus immediate offsets, and the odd row
+// stride keeps the 64 lanes on distinct banks.  Without it the weights are read from global
+// memory.
 // ---------------------------------------------------------------------------------------
+constexpr int HNT = 512, OP = OMAX + 1, HLDS = 1024;
+
 struct HeadArgs {
     const float *h1, *w2, *b2, *lossb;
     float *z, *zb, *h1b, *D1, *D2;
@@ -71,21 +77,34 @@ struct HeadArgs {
     float *zd, *zbd, *h1bd, *D1d, *D2d;
     const int64_t* lab;
     int B, H, O;
-    double* partials;  // per block: loss, lossd, b2b[O], b2bd[O]
+    double* partials;  // per block: loss, lossd
     int* err;          // set when a label is outside 1..O
 };
 
-template <int MODE, int HPL>
-__global__ __launch_bounds__(NT) void head_kernel(HeadArgs a) {
-    __shared__ double red[16 * (2 + 2 * OMAX)];
+template <int MODE, int HPL, bool LDSW>
+__global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
+    constexpr int NWS = LDSW ? (MODE == ADJ ? 1 : 2) : 0;
+    __shared__ double red[16 * 2];
+    __shared__ float w2s[NWS ? NWS * HLDS * OP : 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.H, O = a.O;
-    double acc[2 + 2 * OMAX];  // loss, lossd, b2b[0..O), b2bd[0..O)
+    if constexpr (LDSW) {
+        for (int q = threadIdx.x; q < O * H; q += HNT) {
+            const int j = q / O, o = q - j * O;
+            w2s[j * OP + o] = a.w2[q];
+            if (MODE != ADJ) w2s[HLDS * OP + j * OP + o] = a.w2d[q];
+        }
+        __syncthreads();
+    }
+    // W2(o, j), W2d(o, j)
+    auto W2 = [&](int o, int j) { return LDSW ? w2s[j * OP + o] : a.w2[(long)j * O + o]; };
+    auto W2d = [&](int o, int j) { return LDSW ? w2s[(NWS - 1) * HLDS * OP + j * OP + o] : a.w2d[(long)j * O + o]; };
+    double acc[2];  // loss, lossd
 #pragma unroll
-    for (int k = 0; k < 2 + 2 * OMAX; ++k) acc[k] = 0.0;
+    for (int k = 0; k < 2; ++k) acc[k] = 0.0;
     const float lb = (MODE == TAN) ? 0.f : a.lossb[0];
     const float lbd = (MODE == HVP) ? a.lossbd[0] : 0.f;
-    for (int s = blockIdx.x * (NT / 64) + wave; s < a.B; s += gridDim.x * (NT / 64)) {
+    for (int s = blockIdx.x * (HNT / 64) + wave; s < a.B; s += gridDim.x * (HNT / 64)) {
         const long hs = (long)s * H, os = (long)s * O;
         float hj[HPL], hdj[HPL];
 #pragma unroll
@@ -102,14 +121,17 @@ __global__ __launch_bounds__(NT) void head_kernel(HeadArgs a) {
         for (int q = 0; q < HPL; ++q) {
             const int j = lane + 64 * q;
             if (j >= H) continue;
-            const float* w2j = a.w2 + (long)j * O;
 #pragma unroll
             for (int o = 0; o < OMAX; ++o) {
                 if (o < O) {
-                    z[o] += w2j[o] * hj[q];
-                    if (MODE != ADJ) zd[o] += hj[q] * a.w2d[(long)j * O + o] + w2j[o] * hdj[q];
+                    const float w = W2(o, j);
+                    z[o] += w * hj[q];
+                    if (MODE != ADJ) zd[o] += hj[q] * W2d(o, j) + w * hdj[q];
                 }
             }
+            // one column block's weights live at a time (the scheduler would otherwise hoist
+            // every LDS read of the loop and spill)
+            if constexpr (LDSW) asm volatile("" ::: "memory");
         }
 #pragma unroll
         for (int o = 0; o < OMAX; ++o) {
@@ -171,11 +193,6 @@ __global__ __launch_bounds__(NT) void head_kernel(HeadArgs a) {
                     if (o == l) td = td + -lbd;
                     d2d[o] = td + (seb * (e[o] * zd[o]) + e[o] * sebd);
                 }
-                // every lane holds the same d2: lane 0 counts it once for b2b
-                if (lane == 0) {
-                    acc[2 + o] += (double)d2[o];
-                    if (MODE == HVP) acc[2 + OMAX + o] += (double)d2d[o];
-                }
             }
         }
         if (lane < O) {
@@ -195,16 +212,17 @@ __global__ __launch_bounds__(NT) void head_kernel(HeadArgs a) {
         for (int q = 0; q < HPL; ++q) {
             const int j = lane + 64 * q;
             if (j >= H) continue;
-            const float* w2j = a.w2 + (long)j * O;
             float t = a.h1b[hs + j];
             float td = (MODE == HVP) ? a.h1bd[hs + j] : 0.f;
 #pragma unroll
             for (int o = OMAX - 1; o >= 0; --o) {
                 if (o < O) {
-                    if (MODE == HVP) td = td + (d2[o] * a.w2d[(long)j * O + o] + w2j[o] * d2d[o]);
-                    t = t + w2j[o] * d2[o];
+                    const float w = W2(o, j);
+                    if (MODE == HVP) td = td + (d2[o] * W2d(o, j) + w * d2d[o]);
+                    t = t + w * d2[o];
                 }
             }
+            if constexpr (LDSW) asm volatile("" ::: "memory");
             const float h = hj[q];
             const float g = 1.0f - h * h;
             a.h1b[hs + j] = 0.f;
@@ -215,8 +233,8 @@ __global__ __launch_bounds__(NT) void head_kernel(HeadArgs a) {
             }
         }
     }
-    // block partials: loss, lossd, b2b[0..O), b2bd[0..O)
-    block_partials<2 + 2 * OMAX>(acc, red, a.partials);
+    // block partials: loss, lossd
+    block_partials<2>(acc, red, a.partials);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -226,58 +244,82 @@ __global__ __launch_bounds__(NT) void head_kernel(HeadArgs a) {
 constexpr int SC = 128;  // samples per chunk
 struct ColArgs {
     const float *h1, *D1, *D2, *h1d, *D1d, *D2d;
-    float* part;  // [chunk][2 * (O + 1)][H]
+    float* part;   // [chunk][2 * (O + 1)][H]
+    float* part2;  // [chunk][2 * OMAX]: sum over the chunk's samples of d2 (and d2d)
     int B, H, O;
 };
 
 template <int MODE>
 __global__ __launch_bounds__(NT) void colsum_kernel(ColArgs a) {
+    // block: 64 columns j x 4 sample lanes; lane sl takes samples s0 + sl, s0 + sl + 4, ...
+    // and the 4 lane sums are added in lane order
+    constexpr int NR = 2 * (OMAX + 1);
     __shared__ float d2s[SC * OMAX], d2ds[SC * OMAX];
-    const int j = blockIdx.x * NT + threadIdx.x, c = blockIdx.y;
+    __shared__ float red[4][NR][64];
+    const int jl = threadIdx.x & 63, sl = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + jl, c = blockIdx.y;
     const int s0 = c * SC, s1 = min(a.B, s0 + SC), O = a.O, H = a.H;
     for (int q = threadIdx.x; q < (s1 - s0) * O; q += NT) {
         d2s[q] = a.D2[(long)s0 * O + q];
         if (MODE == HVP) d2ds[q] = a.D2d[(long)s0 * O + q];
     }
     __syncthreads();
-    if (j >= H) return;
+    // b2b (+ b2bd) partials of the chunk: the column-independent sums of d2 over samples
+    if (blockIdx.x == 0 && threadIdx.x < 2 * OMAX) {
+        const int o = threadIdx.x % OMAX;
+        const bool dd = threadIdx.x >= OMAX;
+        double t = 0.0;
+        if (o < O && (!dd || MODE == HVP))
+            for (int q = 0; q < s1 - s0; ++q) t += (double)(dd ? d2ds[q * O + o] : d2s[q * O + o]);
+        a.part2[(long)c * 2 * OMAX + threadIdx.x] = (float)t;
+    }
     float w[OMAX], wd[OMAX], bsum = 0.f, bsumd = 0.f;
 #pragma unroll
     for (int o = 0; o < OMAX; ++o) w[o] = wd[o] = 0.f;
-    for (int s = s0; s < s1; ++s) {
-        const long k = (long)s * H + j;
-        const float h = a.h1[k];
-        const float hd = (MODE == HVP) ? a.h1d[k] : 0.f;
-        const float* d2 = d2s + (s - s0) * O;
-        const float* d2d = d2ds + (s - s0) * O;
+    if (j < H) {
+        for (int s = s0 + sl; s < s1; s += 4) {
+            const long k = (long)s * H + j;
+            const float h = a.h1[k];
+            const float hd = (MODE == HVP) ? a.h1d[k] : 0.f;
+            const float* d2 = d2s + (s - s0) * O;
+            const float* d2d = d2ds + (s - s0) * O;
 #pragma unroll
-        for (int o = 0; o < OMAX; ++o) {
-            if (o < O) {
-                w[o] += h * d2[o];
-                if (MODE == HVP) wd[o] += d2[o] * hd + h * d2d[o];
+            for (int o = 0; o < OMAX; ++o) {
+                if (o < O) {
+                    w[o] += h * d2[o];
+                    if (MODE == HVP) wd[o] += d2[o] * hd + h * d2d[o];
+                }
             }
+            bsum += a.D1[k];
+            if (MODE == HVP) bsumd += a.D1d[k];
         }
-        bsum += a.D1[k];
-        if (MODE == HVP) bsumd += a.D1d[k];
     }
-    float* p = a.part + (long)c * 2 * (O + 1) * H;
 #pragma unroll
     for (int o = 0; o < OMAX; ++o) {
-        if (o < O) {
-            p[(long)o * H + j] = w[o];
-            if (MODE == HVP) p[(long)(O + 1 + o) * H + j] = wd[o];
-        }
+        red[sl][o][jl] = w[o];
+        red[sl][OMAX + 1 + o][jl] = wd[o];
     }
-    p[(long)O * H + j] = bsum;
-    if (MODE == HVP) p[(long)(2 * O + 1) * H + j] = bsumd;
+    red[sl][OMAX][jl] = bsum;
+    red[sl][2 * OMAX + 1][jl] = bsumd;
+    __syncthreads();
+    if (j >= H) return;
+    float* p = a.part + (long)c * 2 * (O + 1) * H;
+    // rows of this thread's column: r = sl, sl + 4, ... of the 2 (O + 1) partial rows
+    for (int r = sl; r < 2 * (O + 1); r += 4) {
+        if (MODE != HVP && r > O) break;
+        const int src = r < O ? r : (r == O ? OMAX : (r < 2 * O + 1 ? OMAX + 1 + (r - O - 1) : 2 * OMAX + 1));
+        const float v = ((red[0][src][jl] + red[1][src][jl]) + red[2][src][jl]) + red[3][src][jl];
+        p[(long)r * H + j] = v;
+    }
 }
 
-// block 0: loss (+ lossd) and b2b (+ b2bd) from the head partials; the other blocks: W2b,
-// b1b (+ W2bd, b1bd) from the colsum chunk partials, chunks in order
+// block 0: loss (+ lossd) from the head partials and b2b (+ b2bd) from the colsum chunk sums;
+// the other blocks: W2b, b1b (+ W2bd, b1bd) from the colsum chunk partials, chunks in order
 struct FinalArgs {
     const double* hpart;
     int nhead;
     const float* cpart;
+    const float* c2part;
     int nchunks;
     float *loss, *lossd, *b2b, *b2bd, *w2b, *w2bd, *b1b, *b1bd;
     int H, O;
@@ -288,14 +330,17 @@ __global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
     __shared__ double red[16];
     const int O = f.O, H = f.H;
     if (blockIdx.x == 0) {
-        constexpr int NV = 2 + 2 * OMAX;
-        for (int k = 0; k < NV; ++k) {
+        for (int k = 0; k < 2 + 2 * OMAX; ++k) {
             if (k == 1 && MODE == ADJ) continue;
             if (k >= 2 && MODE == TAN) break;
             if (k >= 2 + O && k < 2 + OMAX) continue;
             if (k >= 2 + OMAX && (MODE != HVP || k >= 2 + OMAX + O)) continue;
             double v[1] = {0.0};
-            for (int b = threadIdx.x; b < f.nhead; b += NT) v[0] += f.hpart[(size_t)b * NV + k];
+            if (k < 2) {
+                for (int b = threadIdx.x; b < f.nhead; b += NT) v[0] += f.hpart[(size_t)b * 2 + k];
+            } else {
+                for (int c = threadIdx.x; c < f.nchunks; c += NT) v[0] += (double)f.c2part[(size_t)c * 2 * OMAX + (k - 2)];
+            }
             block_sum<1>(v, red);
             if (threadIdx.x == 0) {
                 float t = (float)v[0];
@@ -339,7 +384,15 @@ int32_t check(int64_t B, int64_t I, int64_t H, int64_t O, const char* fn) {
 
 template <int MODE, int HPL>
 void launch_head(const HeadArgs& h, unsigned blocks, hipStream_t stream) {
-    head_kernel<MODE, HPL><<<blocks, NT, 0, stream>>>(h);
+    // (the tangent and HVP forms keep W2, W2d in global memory: with both in LDS their
+    // register demand exceeds the 256 VGPRs a 512-thread block allows)
+    if constexpr (MODE == ADJ) {
+        if (h.H <= HLDS) {
+            head_kernel<MODE, HPL, true><<<blocks, HNT, 0, stream>>>(h);
+            return;
+        }
+    }
+    head_kernel<MODE, HPL, false><<<blocks, HNT, 0, stream>>>(h);
 }
 
 template <int MODE>
@@ -375,10 +428,11 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
         need(p_xbd, I, B);
     }
     npart = (npart + 63) / 64 * 64;
-    const size_t nlocal = hv * (nD1 + nD2) + nC;
+    const size_t nlocal = hv * (nD1 + nD2) + nC + (size_t)nchunks * 2 * OMAX;
     float* D1 = (float*)scratch(sizeof(float) * ((nlocal + 63) / 64 * 64 + npart) + 256);
     if (!D1) return STADE_HIP_ENOMEM;
     float *D2 = D1 + nD1, *D1d = D2 + nD2, *D2d = D1d + (MODE == HVP ? nD1 : 0), *cpart = D2d + (MODE == HVP ? nD2 : 0);
+    float* c2part = cpart + nC;
     float* kpart = D1 + (nlocal + 63) / 64 * 64;
     int* err = (int*)(ws->dscalars + 16);
     // forward: h1 = tanh(W1 x + b1)
@@ -409,20 +463,21 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     h.h1 = p.h1; h.w2 = p.w2; h.b2 = p.b2; h.lossb = p.lossb; h.z = p.z; h.zb = p.zb; h.h1b = p.h1b; h.D1 = D1; h.D2 = D2;
     h.h1d = p.h1d; h.w2d = p.w2d; h.b2d = p.b2d; h.lossbd = p.lossbd; h.zd = p.zd; h.zbd = p.zbd; h.h1bd = p.h1bd;
     h.D1d = D1d; h.D2d = D2d; h.lab = p.lab; h.B = B; h.H = H; h.O = O; h.partials = ws->partials; h.err = err;
-    const unsigned hb = (unsigned)((B + 4 * 4 - 1) / (4 * 4));  // 4 samples per wave
+    const unsigned hb = (unsigned)((B + 16 - 1) / 16);  // 8 waves, 2 samples per wave
     STADE_TIMED("mlp_head", stream, {
         if (H <= 256) launch_head<MODE, 4>(h, hb, stream);
         else if (H <= 1024) launch_head<MODE, 16>(h, hb, stream);
         else launch_head<MODE, 32>(h, hb, stream);
     });
     STADE_LAUNCHED("mlp head_kernel");
-    if (MODE != TAN && H > 0) {
-        ColArgs c{p.h1, D1, D2, p.h1d, D1d, D2d, cpart, B, H, O};
+    if (MODE != TAN) {
+        // (one column block even when i_h = 0: its first block forms the b2b chunk sums)
+        ColArgs c{p.h1, D1, D2, p.h1d, D1d, D2d, cpart, c2part, B, H, O};
         STADE_TIMED("mlp_colsum", stream,
-                    colsum_kernel<MODE><<<dim3((H + NT - 1) / NT, nchunks), NT, 0, stream>>>(c));
+                    colsum_kernel<MODE><<<dim3(std::max(1, (H + 63) / 64), nchunks), NT, 0, stream>>>(c));
         STADE_LAUNCHED("mlp colsum_kernel");
     }
-    FinalArgs f{ws->partials, (int)hb, cpart, nchunks, p.loss, p.lossd, p.b2b, p.b2bd, p.w2b, p.w2bd, p.b1b, p.b1bd, H, O};
+    FinalArgs f{ws->partials, (int)hb, cpart, c2part, nchunks, p.loss, p.lossd, p.b2b, p.b2bd, p.w2b, p.w2bd, p.b1b, p.b1bd, H, O};
     const long rows = (long)(MODE == HVP ? 2 : 1) * (O + 1) * H;
     const unsigned fb = 1 + (MODE == TAN ? 0 : (unsigned)((rows + NT - 1) / NT));
     STADE_TIMED("mlp_final", stream, final_kernel<MODE><<<fb, NT, 0, stream>>>(f));
