@@ -305,9 +305,10 @@ class Burgers(Workload):
 
 
 class Mlp(Workload):
-    """Config 3: x (784, 4096) ~ N(0,1), tanh hidden layer of 1024, 10-way softmax
-    cross-entropy, Float32; W1, W2 Glorot-scaled N(0,1), b ~ 0.1 N(0,1), labels uniform in
-    1..10 -- all from the seeded Xoshiro stream."""
+    """Config 3: x (784, 4096) ~ U[0,1], tanh hidden layer of 1024, 10-way softmax
+    cross-entropy, Float32; W1, W2 Glorot-uniform U(+-sqrt(6 / (fan_in + fan_out))),
+    b1 = b2 = 0, labels uniform in 1..10, HVP direction (xd, W1d, b1d, W2d, b2d) ~ N(0,1) --
+    all from the seeded Xoshiro stream."""
     dtype = "f32"
     bound = "mfma"
 
@@ -327,16 +328,15 @@ class Mlp(Workload):
         import stade_hip
         I, H, O = self.I, self.H, self.O
         rng = stade_hip.api.Rng(stade_hip.stable_seed("mlp2_ce"))
-        x = stade_hip.rng_normal(rng, I * B).astype(np.float32)
-        w1 = (stade_hip.rng_normal(rng, H * I) * np.sqrt(2.0 / (I + H))).astype(np.float32)
-        b1 = (0.1 * stade_hip.rng_normal(rng, H)).astype(np.float32)
-        w2 = (stade_hip.rng_normal(rng, O * H) * np.sqrt(2.0 / (H + O))).astype(np.float32)
-        b2 = (0.1 * stade_hip.rng_normal(rng, O)).astype(np.float32)
+        x = stade_hip.rng_uniform(rng, I * B, 0.0, 1.0).astype(np.float32)
+        a1, a2 = np.sqrt(6.0 / (I + H)), np.sqrt(6.0 / (H + O))
+        w1 = stade_hip.rng_uniform(rng, H * I, -a1, a1).astype(np.float32)
+        w2 = stade_hip.rng_uniform(rng, O * H, -a2, a2).astype(np.float32)
+        b1, b2 = np.zeros(H, dtype=np.float32), np.zeros(O, dtype=np.float32)
         lab = stade_hip.rng_int_range(rng, B, 1, O)
         rng2 = stade_hip.api.Rng(stade_hip.stable_seed("mlp2_ce") + 1)
-        d = {k: (stade_hip.rng_normal(rng2, n) * sc).astype(np.float32)
-             for k, n, sc in (("xd", I * B, 1.0), ("w1d", H * I, np.sqrt(2.0 / (I + H))), ("b1d", H, 0.1),
-                              ("w2d", O * H, np.sqrt(2.0 / (H + O))), ("b2d", O, 0.1))}
+        d = {k: stade_hip.rng_normal(rng2, n).astype(np.float32)
+             for k, n in (("xd", I * B), ("w1d", H * I), ("b1d", H), ("w2d", O * H), ("b2d", O))}
         return dict(x=x, w1=w1, b1=b1, w2=w2, b2=b2, lab=lab, **d)
 
     def setup(self, dev):
@@ -373,8 +373,8 @@ class Mlp(Workload):
         return sum(self.kernels.values()) * 1.0 + {"b": 2, "d": 2, "hv": 4}[self.mode] * 2.0 * O * H * B
 
     def config(self):
-        return {"workload": f"mlp2_ce_{self.mode}: x {self.I}x{self.B} fp32 -> tanh({self.H}) -> {self.O}-way softmax "
-                            f"cross-entropy summed over the batch",
+        return {"workload": f"mlp2_ce_{self.mode}: x {self.I}x{self.B} fp32 U[0,1] -> tanh({self.H}) -> {self.O}-way softmax "
+                            f"cross-entropy summed over the batch; Glorot-uniform weights, zero biases",
                 "batch": self.B, "widths": [self.I, self.H, self.O]}
 
     def cpu_sample(self):
@@ -404,7 +404,8 @@ class Mlp(Workload):
 
 class Conv(Workload):
     """Config 4: 8 images of 256 x 256, 64 -> 64 channels, 3 x 3, zero border held in xp,
-    Float32; xp interior ~ N(0,1), w ~ N(0,1)/sqrt(9 C), from the seeded Xoshiro stream."""
+    Float32; xp interior ~ N(0,1), w He-normal N(0, 2 / (9 C)); tangent / HVP direction
+    xpd (interior), wd the same laws -- from the seeded Xoshiro stream."""
     dtype = "f32"
     bound = "mfma"
 
@@ -424,11 +425,11 @@ class Conv(Workload):
         rng = stade_hip.api.Rng(stade_hip.stable_seed("conv3x3"))
         xp = np.zeros((N, C, H + 2, W + 2), dtype=np.float32)
         xp[:, :, 1:-1, 1:-1] = stade_hip.rng_normal(rng, N * C * H * W).reshape(N, C, H, W)
-        w = (stade_hip.rng_normal(rng, 9 * C * K) / np.sqrt(9.0 * C)).astype(np.float32)
+        w = (stade_hip.rng_normal(rng, 9 * C * K) * np.sqrt(2.0 / (9.0 * C))).astype(np.float32)
         rng2 = stade_hip.api.Rng(stade_hip.stable_seed("conv3x3") + 1)
         xpd = np.zeros_like(xp)
         xpd[:, :, 1:-1, 1:-1] = stade_hip.rng_normal(rng2, N * C * H * W).reshape(N, C, H, W)
-        wd = (stade_hip.rng_normal(rng2, 9 * C * K) / np.sqrt(9.0 * C)).astype(np.float32)
+        wd = (stade_hip.rng_normal(rng2, 9 * C * K) * np.sqrt(2.0 / (9.0 * C))).astype(np.float32)
         return dict(xp=xp.ravel(), w=w, xpd=xpd.ravel(), wd=wd)
 
     def setup(self, dev):
@@ -514,6 +515,18 @@ def _lib():
     return L
 
 
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from its committed counter summary
+    (profiles/<kernel>_traffic.md: FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what
+    the same counter reads for a 1 GiB copy), or None when there is none."""
+    import re
+    f = ROOT / "profiles" / f"{kernel}_traffic.md"
+    if not f.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read_text(), re.M)
+    return int(m.group(1)) if m else None
+
+
 def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
     import torch
     L = _lib()
@@ -555,7 +568,7 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
         if wl.bound == "hbm":
             ach = wl.kernel_bytes() / (k_ms * 1e-3) / 1e9
             out["roofline"] = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                               "frac": ach / HBM_PEAK_GBS, "traffic": None}
+                               "frac": ach / HBM_PEAK_GBS, "traffic": profiled_traffic(wl.kernel)}
         else:
             peak = FP32_PEAK_TFLOPS if wl.dtype == "f32" else FP64_PEAK_TFLOPS
             ach = wl.kernels[wl.kernel] / (k_ms * 1e-3) / 1e12
