@@ -29,6 +29,7 @@ namespace stade {
 namespace {
 
 constexpr int NT = 256, KMAX = 32;
+constexpr int BNT = 1024;  // threads of the forward and backward chunk kernels (16 waves per CU)
 
 struct Coef {
     double cadv, cdif, cadvd, cdifd;
@@ -50,7 +51,7 @@ __device__ __forceinline__ double step_ud(double um, double uc, double up, doubl
 // forward: `nk` steps starting at 0-based step t0, from src (+ srcd) to dst (+ dstd)
 // ---------------------------------------------------------------------------------------
 template <bool TAN, int S>
-__global__ __launch_bounds__(NT) void fwd_kernel(const double* __restrict__ src, const double* __restrict__ srcd,
+__global__ __launch_bounds__(BNT) void fwd_kernel(const double* __restrict__ src, const double* __restrict__ srcd,
                                                  double* __restrict__ dst, double* __restrict__ dstd,
                                                  double* __restrict__ tape, double* __restrict__ taped, int n, int64_t t0,
                                                  int nk, Coef c) {
@@ -60,7 +61,7 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const double* __restrict__ src,
     const int x0 = blockIdx.x * S;
     const int len = nk == 0 ? S : S + 2 * nk;  // extended region [x0 - nk, x0 + S + nk)
     const int own = min(S, n - x0);
-    for (int e = threadIdx.x; e < len; e += NT) {
+    for (int e = threadIdx.x; e < len; e += BNT) {
         int x = wrapn(x0 - nk + e, n);
         A[0][e] = src[x];
         if (TAN) D[0][e] = srcd[x];
@@ -70,12 +71,12 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const double* __restrict__ src,
     for (int k = 0; k < nk; ++k) {
         const size_t row = (size_t)(t0 + k) * (size_t)n;
         if (tape) {
-            for (int e = threadIdx.x; e < own; e += NT) {
+            for (int e = threadIdx.x; e < own; e += BNT) {
                 tape[row + x0 + e] = A[cur][nk + e];
                 if (TAN && taped) taped[row + x0 + e] = D[cur][nk + e];
             }
         }
-        for (int e = k + 1 + threadIdx.x; e < len - k - 1; e += NT) {
+        for (int e = k + 1 + threadIdx.x; e < len - k - 1; e += BNT) {
             double um = A[cur][e - 1], uc = A[cur][e], up = A[cur][e + 1];
             if (TAN) D[cur ^ 1][e] = step_ud(um, uc, up, D[cur][e - 1], D[cur][e], D[cur][e + 1], c);
             A[cur ^ 1][e] = step_u(um, uc, up, c);
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const double* __restrict__ src,
         __syncthreads();
         cur ^= 1;
     }
-    for (int e = threadIdx.x; e < own; e += NT) {
+    for (int e = threadIdx.x; e < own; e += BNT) {
         dst[x0 + e] = A[cur][nk + e];
         if (TAN) dstd[x0 + e] = D[cur][nk + e];
     }
@@ -141,35 +142,63 @@ __global__ __launch_bounds__(NT) void bwd_init_kernel(const double* __restrict__
 // the interior, with A/B/C the contributions a cell sends to its east/west neighbours)
 // ---------------------------------------------------------------------------------------
 template <bool HV, int S>
-__global__ __launch_bounds__(NT) void bwd_kernel(const double* __restrict__ win, const double* __restrict__ wind,
-                                                 double* __restrict__ vout, double* __restrict__ voutd,
-                                                 const double* __restrict__ tape, const double* __restrict__ taped, int n,
-                                                 int64_t t_hi, int nk, Coef c, double* partials) {
+__global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win, const double* __restrict__ wind,
+                                                  double* __restrict__ vout, double* __restrict__ voutd,
+                                                  const double* __restrict__ tape, const double* __restrict__ taped, int n,
+                                                  int64_t t_hi, int nk, Coef c, double* partials) {
     constexpr int L = S + 2 * KMAX;
+    constexpr int M = (L + BNT - 1) / BNT;  // extended-region positions per thread
     __shared__ double W[2][L];
     __shared__ double U[L];
     __shared__ double WD[HV ? 2 : 1][HV ? L : 1];
     __shared__ double UD[HV ? L : 1];
-    __shared__ double red[32];
+    __shared__ double red[16 * 4];
     const int x0 = blockIdx.x * S;
     const int len = S + 2 * nk;
     const int own = min(S, n - x0);
-    for (int e = threadIdx.x; e < len; e += NT) {
-        int x = wrapn(x0 - nk + e, n);
-        W[0][e] = win[x];
-        if (HV) WD[0][e] = wind[x];
+    // the thread's positions e = threadIdx.x + i * BNT and their (periodic) columns
+    int xcol[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = threadIdx.x + i * BNT;
+        xcol[i] = e < len ? wrapn(x0 - nk + e, n) : 0;
+        if (e < len) {
+            W[0][e] = win[xcol[i]];
+            if (HV) WD[0][e] = wind[xcol[i]];
+        }
     }
+    // tape row of backward step k (state at the start of step t_hi - k), on [k, len - k):
+    // held in registers from one step ahead
+    double pre[M], pred[M];
+    auto fetch = [&](int k) {
+        const size_t row = (size_t)(t_hi - k) * (size_t)n;
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const int e = threadIdx.x + i * BNT;
+            if (e >= k && e < len - k) {
+                pre[i] = tape[row + xcol[i]];
+                if (HV) pred[i] = taped[row + xcol[i]];
+            }
+        }
+    };
+    fetch(0);
     double acc[4] = {0.0, 0.0, 0.0, 0.0};  // cadvb, cdifb, cadvbd, cdifbd
     int cur = 0;
     for (int k = 0; k < nk; ++k) {
-        const size_t row = (size_t)(t_hi - k) * (size_t)n;
-        for (int e = k + threadIdx.x; e < len - k; e += NT) {
-            int x = wrapn(x0 - nk + e, n);
-            U[e] = tape[row + x];
-            if (HV) UD[e] = taped[row + x];
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const int e = threadIdx.x + i * BNT;
+            if (e >= k && e < len - k) {
+                U[e] = pre[i];
+                if (HV) UD[e] = pred[i];
+            }
         }
+        if (k + 1 < nk) fetch(k + 1);
         __syncthreads();
-        for (int e = k + 1 + threadIdx.x; e < len - k - 1; e += NT) {
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const int e = threadIdx.x + i * BNT;
+            if (e < k + 1 || e >= len - k - 1) continue;
             const double* Wc = W[cur];
             // contributions of the three cells e-1, e, e+1
             double um1 = U[e - 1], uc = U[e], up1 = U[e + 1];
@@ -222,7 +251,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const double* __restrict__ win,
         __syncthreads();
         cur ^= 1;
     }
-    for (int e = threadIdx.x; e < own; e += NT) {
+    for (int e = threadIdx.x; e < own; e += BNT) {
         vout[x0 + e] = W[cur][nk + e];
         if (HV) voutd[x0 + e] = WD[cur][nk + e];
     }
@@ -326,7 +355,7 @@ int32_t forward(const double* src, const double* srcd, double* fin, double* find
         double* d = last ? fin : (flip ? Q : P);
         double* dd = last ? find : (flip ? Qd : Pd);
         STADE_TIMED(TAN ? "burgers1d_fwd_hv" : "burgers1d_fwd", stream,
-                    fwd_kernel<TAN, S><<<nb, NT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c));
+                    fwd_kernel<TAN, S><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c));
         STADE_LAUNCHED("burgers1d fwd_kernel");
         cs = d;
         csd = dd;
@@ -368,7 +397,7 @@ int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, dou
         double* d = last ? ub : ow;
         double* dd = last ? ubd : owd;
         STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
-                    bwd_kernel<HV, S><<<nb, NT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, nk, c,
+                    bwd_kernel<HV, S><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, nk, c,
                                                              pbwd + (size_t)chunk * nb * NV));
         STADE_LAUNCHED("burgers1d bwd_kernel");
         ++chunk;
