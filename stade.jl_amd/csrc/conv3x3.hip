@@ -180,31 +180,39 @@ __global__ __launch_bounds__(NT) void tap_kernel(TapArgs a) {
         store();
         __syncthreads();
         if (ch + 1 < nchunks) load((ch + 1) * CC);
+        // k steps st = (channel pair qq, tap t); the fragments of step st+1 are read from LDS
+        // while the MFMAs of step st run (two register sets; the scheduling barriers keep
+        // the compiler from sinking each read to its use)
+        constexpr int NSTEP = CC / 2 * 9;
+        float pf[2][NP][2], wf[2][NP][2];
+        auto frag = [&](int st, int buf) {
+            const int qq = st / 9, t = st % 9, ky = t / 3, kx = t % 3;
 #pragma unroll
-        for (int qq = 0; qq < CC / 2; ++qq) {
+            for (int p = 0; p < NP; ++p)
 #pragma unroll
-            for (int t = 0; t < 9; ++t) {
-                const int ky = t / 3, kx = t % 3;
-                float pf[NP][2], wf[NP][2];
+                for (int j = 0; j < 2; ++j) pf[buf][p][j] = Ps[p * PSZ + pbase + 2 * qq * PPL + ky * PXW + kx + 32 * j];
 #pragma unroll
-                for (int p = 0; p < NP; ++p)
+            for (int p = 0; p < NP; ++p)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) pf[p][j] = Ps[p * PSZ + pbase + 2 * qq * PPL + ky * PXW + kx + 32 * j];
+                for (int i = 0; i < 2; ++i) wf[buf][p][i] = Ws[p * WSZ + wbase + (2 * qq * 9 + t) * RT + 32 * i];
+        };
+        frag(0, 0);
 #pragma unroll
-                for (int p = 0; p < NP; ++p)
+        for (int st = 0; st < NSTEP; ++st) {
+            const int b = st & 1;
+            if (st + 1 < NSTEP) frag(st + 1, b ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) wf[p][i] = Ws[p * WSZ + wbase + (2 * qq * 9 + t) * RT + 32 * i];
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        acc[0][i][j] = mfma(wf[0][i], pf[0][j], acc[0][i][j]);
-                        if constexpr (NP == 2) {
-                            acc[1][i][j] = mfma(wf[1][i], pf[0][j], acc[1][i][j]);
-                            acc[1][i][j] = mfma(wf[0][i], pf[1][j], acc[1][i][j]);
-                        }
+                for (int j = 0; j < 2; ++j) {
+                    acc[0][i][j] = mfma(wf[b][0][i], pf[b][0][j], acc[0][i][j]);
+                    if constexpr (NP == 2) {
+                        acc[1][i][j] = mfma(wf[b][1][i], pf[b][0][j], acc[1][i][j]);
+                        acc[1][i][j] = mfma(wf[b][0][i], pf[b][1][j], acc[1][i][j]);
                     }
-            }
+                }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
@@ -217,44 +225,65 @@ __global__ __launch_bounds__(NT) void tap_kernel(TapArgs a) {
     if constexpr (MODE == FWD_B || MODE == FWD_HV) lb = a.lossb[0];
     if constexpr (MODE == FWD_HV) lbd = a.lossbd[0];
     const int y = y0 + wave;
-    if (y < a.H) {
+    // The read-modify-write inputs (outb, outbd of the forward adjoint; xpb, xpbd of the
+    // interior) are all loaded before any store: the output arrays may alias as far as the
+    // compiler knows, so interleaving would serialise one HBM round trip per element.
+    constexpr bool RMW = MODE != FWD_D;
+    constexpr int NR = (MODE == FWD_HV || MODE == DG_HV) ? 2 : 1;
+    float pre[NR][2][2][16];
+    auto index = [&](int i, int j, int q, long& oi) {
+        const int x = x0 + 32 * j + l32;
+        const int r = rt * RT + 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
+        oi = ((long)(n * a.R + r) * a.OH + y + a.oofs) * a.OW + x + a.oofs;
+        return y < a.H && x < a.W && r < a.R;
+    };
+    if constexpr (RMW) {
+        const float* s0 = FWD ? a.ob : a.o0;
+        const float* s1 = FWD ? a.obd : a.o1;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int x = x0 + 32 * j + l32;
-                if (x >= a.W) continue;
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int q = 0; q < 16; ++q) {
-                    const int r = rt * RT + 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
-                    if (r >= a.R) continue;
-                    const long oi = ((long)(n * a.R + r) * a.OH + y + a.oofs) * a.OW + x + a.oofs;
-                    const float v = acc[0][i][j][q];
-                    if constexpr (FWD) {
-                        a.o0[oi] = v;
-                        ls[0] += 0.5 * (double)v * (double)v;
-                        if constexpr (MODE == FWD_B) {
-                            a.g0[oi] = a.ob[oi] + (0.5f * (2.0f * v)) * lb;
-                            a.ob[oi] = 0.f;
-                        } else {
-                            const float vd = acc[1][i][j][q];
-                            a.o1[oi] = vd;
-                            ls[1] += 0.5 * ((double)(2.0f * v) * (double)vd);
-                            if constexpr (MODE == FWD_HV) {
-                                const float c8 = 0.5f * (2.0f * v);
-                                a.g1[oi] = a.obd[oi] + (lb * (0.5f * (2.0f * vd)) + c8 * lbd);
-                                a.g0[oi] = a.ob[oi] + c8 * lb;
-                                a.ob[oi] = 0.f;
-                                a.obd[oi] = 0.f;
-                            }
-                        }
+                    long oi;
+                    const bool ok = index(i, j, q, oi);
+                    pre[0][i][j][q] = ok ? s0[oi] : 0.f;
+                    if constexpr (NR == 2) pre[NR - 1][i][j][q] = ok ? s1[oi] : 0.f;
+                }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                long oi;
+                if (!index(i, j, q, oi)) continue;
+                const float v = acc[0][i][j][q];
+                if constexpr (FWD) {
+                    a.o0[oi] = v;
+                    ls[0] += 0.5 * (double)v * (double)v;
+                    if constexpr (MODE == FWD_B) {
+                        a.g0[oi] = pre[0][i][j][q] + (0.5f * (2.0f * v)) * lb;
+                        a.ob[oi] = 0.f;
                     } else {
-                        a.o0[oi] = a.o0[oi] + v;
-                        if constexpr (MODE == DG_HV) a.o1[oi] = a.o1[oi] + acc[1][i][j][q];
+                        const float vd = acc[1][i][j][q];
+                        a.o1[oi] = vd;
+                        ls[1] += 0.5 * ((double)(2.0f * v) * (double)vd);
+                        if constexpr (MODE == FWD_HV) {
+                            const float c8 = 0.5f * (2.0f * v);
+                            a.g1[oi] = pre[NR - 1][i][j][q] + (lb * (0.5f * (2.0f * vd)) + c8 * lbd);
+                            a.g0[oi] = pre[0][i][j][q] + c8 * lb;
+                            a.ob[oi] = 0.f;
+                            a.obd[oi] = 0.f;
+                        }
                     }
+                } else {
+                    a.o0[oi] = pre[0][i][j][q] + v;
+                    if constexpr (MODE == DG_HV) a.o1[oi] = pre[NR - 1][i][j][q] + acc[1][i][j][q];
                 }
             }
-    }
     if constexpr (FWD) block_partials<NV>(ls, red, a.partials);
 }
 
@@ -472,21 +501,29 @@ __global__ __launch_bounds__(NT) void wgrad_kernel(WgArgs a) {
         store();
         __syncthreads();
         if (tile + (int)gridDim.y < a.ntiles) load(tile + gridDim.y);
+        // k steps s (pixel pairs 2s, 2s+1); step s+1's fragments are read during step s's MFMAs
+        constexpr int NSTEP = GPX / 2;
+        float gf[2][NPR], xf[2][NPR][9];
+        auto frag = [&](int st, int buf) {
+            const int py = (2 * st) / WTX, px = (2 * st) % WTX;
 #pragma unroll
-        for (int s = 0; s < GPX / 2; ++s) {
-            const int py = (2 * s) / WTX, px = (2 * s) % WTX;
-            float gf[NPR];
+            for (int p = 0; p < NPR; ++p) {
+                gf[buf][p] = Gs[p * GSZ + gb + 2 * st];
 #pragma unroll
-            for (int p = 0; p < NPR; ++p) gf[p] = Gs[p * GSZ + gb + 2 * s];
-#pragma unroll
-            for (int t = 0; t < 9; ++t) {
-                const int ky = t / 3, kx = t % 3;
-#pragma unroll
-                for (int p = 0; p < NPR; ++p) {
-                    const float xf = Xs[p * XSZ + xb + (py + ky) * XPX + px + kx];
-                    acc[t] = mfma(xf, gf[p], acc[t]);
-                }
+                for (int t = 0; t < 9; ++t) xf[buf][p][t] = Xs[p * XSZ + xb + (py + t / 3) * XPX + px + t % 3];
             }
+        };
+        frag(0, 0);
+#pragma unroll
+        for (int st = 0; st < NSTEP; ++st) {
+            const int b = st & 1;
+            if (st + 1 < NSTEP) frag(st + 1, b ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 9; ++t)
+#pragma unroll
+                for (int p = 0; p < NPR; ++p) acc[t] = mfma(xf[b][p][t], gf[b][p], acc[t]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     // accumulator (t, q): c = 32 wa + 8 (q / 4) + 4 h + q % 4, co = 32 wb + l32 (slab-local)

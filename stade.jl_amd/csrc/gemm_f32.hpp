@@ -1,6 +1,9 @@
 // fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32), with a fused per-element epilogue.
 //
-//   C(m, n) = sum over segments s of  sum_k A_s(m, k) * B_s(k, n),   epi(m, n, C(m, n))
+//   C(m, n) = sum over segments s of  sum_k A_s(m, k) * B_s(k, n),   epi(m, n, C(m, n), epi.load(m, n))
+//
+// An epilogue functor reads what it needs of the old output in load(m, n) (gathered for the
+// whole tile before any store) and writes in operator()(m, n, v, loaded).
 //
 // A_s is M x K_s and B_s is K_s x N, column-major (Julia) with either storage order:
 //   A_KM = false: A(m, k) at A[m + k * lda] (m contiguous);  A_KM = true: at A[k + m * lda]
@@ -54,11 +57,23 @@ struct Stage {
     float4 v[ROWS * KT / 4 / NT];
 };
 
-// A tile (r 0..ROWS-1, k 0..15) at (r0, k0) into registers; zero outside rows x K.
+// A tile (r 0..ROWS-1, k 0..15) at (r0, k0) into registers; zero outside rows x K.  A tile
+// that lies wholly inside the operand (the common case, decided per block) takes 16-byte
+// loads with no per-element test.
 template <bool KMAJ, int ROWS>
 __device__ __forceinline__ void load_tile(Stage<ROWS>& st, const float* __restrict__ P, long ld, int rows, int K, int r0,
                                           int k0, bool vec) {
     constexpr int R4 = ROWS / 4;  // float4 per k row (KMAJ = false)
+    if (vec && r0 + ROWS <= rows && k0 + KT <= K) {
+#pragma unroll
+        for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
+            const int f = threadIdx.x + NT * q;
+            const float* p = !KMAJ ? P + (long)(r0 + (f % R4) * 4) + (long)(k0 + f / R4) * ld
+                                   : P + (long)(k0 + (f & 3) * 4) + (long)(r0 + (f >> 2)) * ld;
+            st.v[q] = *reinterpret_cast<const float4*>(p);
+        }
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
         const int f = threadIdx.x + NT * q;
@@ -171,19 +186,26 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         }
         const float* A_ = As[cur];
         const float* B_ = Bs[cur];
+        // every fragment of the stage first (the LDS reads overlap each other), then the MFMAs
+        float a[KT / 2][2], b[KT / 2][NJ];
 #pragma unroll
         for (int ks = 0; ks < KT / 2; ++ks) {
             const int kk = ks * 2 + (lane >> 5);
-            float a[2], b[NJ];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = A_[kk * LDA_S + wm + i * 32 + (lane & 31)];
+            for (int i = 0; i < 2; ++i) a[ks][i] = A_[kk * LDA_S + wm + i * 32 + (lane & 31)];
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) b[j] = B_[kk * LDB_S + wn + j * 32 + (lane & 31)];
+            for (int j = 0; j < NJ; ++j) b[ks][j] = B_[kk * LDB_S + wn + j * 32 + (lane & 31)];
+        }
+        // keep the reads ahead of the MFMAs (the scheduler would sink each read to its use
+        // and expose the LDS latency at every k step)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KT / 2; ++ks)
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j], a[i], acc[i][j], 0, 0, 0);
-        }
+                for (int j = 0; j < NJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[ks][j], a[ks][i], acc[i][j], 0, 0, 0);
         if (more) {
             store_tile<A_KM, BM, LDA_S>(sa, As[cur ^ 1]);
             store_tile<B_KM, BNT, LDB_S>(sb, Bs[cur ^ 1]);
@@ -191,7 +213,36 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         __syncthreads();
     }
     // accumulator (i, j, r): m = m0 + wm + 32 i + lane % 32,  n = n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4
-    float* part = g.ksplit > 1 ? g.part + (long)blockIdx.z * g.M * g.N : nullptr;
+    if (g.ksplit > 1) {
+        float* part = g.part + (long)blockIdx.z * g.M * g.N;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int m = m0 + wm + i * 32 + (lane & 31);
+            if (m >= g.M) continue;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                    if (n < g.N) part[m + (long)n * g.M] = acc[i][j][r];
+                }
+        }
+        return;
+    }
+    // the epilogue's inputs (e.g. C of C += v) for the whole tile first, then the stores: the
+    // output may alias them as far as the compiler knows, and interleaving would serialise one
+    // memory round trip per element
+    float pre[2][NJ][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm + i * 32 + (lane & 31);
+                const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                pre[i][j][r] = (m < g.M && n < g.N) ? epi.load(m, n) : 0.f;
+            }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int m = m0 + wm + i * 32 + (lane & 31);
@@ -201,10 +252,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (n < g.N) {
-                    if (part) part[m + (long)n * g.M] = acc[i][j][r];
-                    else epi(m, n, acc[i][j][r]);
-                }
+                if (n < g.N) epi(m, n, acc[i][j][r], pre[i][j][r]);
             }
     }
 }
@@ -217,7 +265,8 @@ __global__ __launch_bounds__(NT) void splitk_reduce_kernel(const float* __restri
     if (q >= mn) return;
     float s = part[q];
     for (int z = 1; z < ksplit; ++z) s += part[q + z * mn];
-    epi((int)(q % M), (int)(q / M), s);
+    const int m = (int)(q % M), n = (int)(q / M);
+    epi(m, n, s, epi.load(m, n));
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

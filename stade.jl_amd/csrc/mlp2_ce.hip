@@ -39,26 +39,22 @@ struct EpiTanh {  // h1 = tanh(s1), s1 = b1 + W1 x
     float* h1;
     const float* b1;
     long ld;
-    __device__ void operator()(int m, int n, float v) const { h1[m + n * ld] = tanhf(v + b1[m]); }
+    __device__ float load(int m, int) const { return b1[m]; }
+    __device__ void operator()(int m, int n, float v, float b) const { h1[m + n * ld] = tanhf(v + b); }
 };
 struct EpiTanhD {  // h1d = (1.0 - h1^2) * s1d, s1d = b1d + W1d x + W1 xd
     float* h1d;
     const float* h1;
     const float* b1d;
     long ld;
-    __device__ void operator()(int m, int n, float v) const {
-        const long k = m + n * ld;
-        const float h = h1[k];
-        h1d[k] = (1.0f - h * h) * (v + b1d[m]);
-    }
+    __device__ float load(int m, int n) const { return h1[m + n * ld]; }
+    __device__ void operator()(int m, int n, float v, float h) const { h1d[m + n * ld] = (1.0f - h * h) * (v + b1d[m]); }
 };
 struct EpiAcc {  // C += v (a shadow accumulated, as the generated code does)
     float* C;
     long ld;
-    __device__ void operator()(int m, int n, float v) const {
-        const long k = m + n * ld;
-        C[k] = C[k] + v;
-    }
+    __device__ float load(int m, int n) const { return C[m + n * ld]; }
+    __device__ void operator()(int m, int n, float v, float c) const { C[m + n * ld] = c + v; }
 };
 
 // ---------------------------------------------------------------------------------------
