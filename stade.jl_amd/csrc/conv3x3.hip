@@ -94,11 +94,10 @@ struct TapArgs {
 };
 
 template <int MODE>
-__global__ __launch_bounds__(NT) void tap_kernel(TapArgs a) {
+__global__ __launch_bounds__(NT, (MODE == FWD_B || MODE == DG_B) ? 2 : 1) void tap_kernel(TapArgs a) {
     constexpr int NP = (MODE == FWD_B || MODE == DG_B) ? 1 : 2;  // sources = weight sets = outputs
     constexpr int CC = 16 / NP;
     constexpr int PSZ = CC * PPL, WSZ = CC * KW;
-    constexpr int PLD = (NP * PSZ + NT - 1) / NT;
     constexpr int WLD = NP * WSZ / 4 / NT;
     static_assert(NP * WSZ % (4 * NT) == 0, "weight stage");
     constexpr bool FWD = MODE == FWD_B || MODE == FWD_D || MODE == FWD_HV;
@@ -115,24 +114,27 @@ __global__ __launch_bounds__(NT) void tap_kernel(TapArgs a) {
     const int rtiles = a.Rpad / RT;
     const int n = blockIdx.z / rtiles, rt = blockIdx.z - n * rtiles;
 
-    float pr[PLD];
+    // Patch staging by rows: the NP * CC * PYH = 96 patch rows of PXW = 66 floats; wave w
+    // takes rows w, w + 4, ..., one column per lane (columns 0..63), so the channel, row and
+    // row bounds are wave-uniform (scalar) and a lane's address is a row base plus its lane;
+    // columns 64, 65 of every row go to threads 0..191, one element each.
+    constexpr int PROWS = NP * CC * PYH, RPW = PROWS / 4;
+    static_assert(PROWS % 4 == 0 && PXW == 66 && 2 * PROWS <= NT, "patch rows");
+    float pr[RPW + 1];
     float4 wr[WLD];
+    auto row_src = [&](int rr, int c0, int col, float& v) {
+        const int p = NP == 1 ? 0 : rr / (CC * PYH);
+        const int rem = rr - p * (CC * PYH);
+        const int cc = rem / PYH, ty = rem - cc * PYH;
+        const int c = c0 + cc, sy = y0 + ty + a.ofs, sx = x0 + col + a.ofs;
+        v = 0.f;
+        if (c < a.Cin && (unsigned)sy < (unsigned)a.SH && (unsigned)sx < (unsigned)a.SW)
+            v = a.src[p][((long)(n * a.Cin + c) * a.SH + sy) * a.SW + sx];
+    };
     auto load = [&](int c0) {
 #pragma unroll
-        for (int q = 0; q < PLD; ++q) {
-            const int f = threadIdx.x + q * NT;
-            float v = 0.f;
-            if (f < NP * PSZ) {
-                const int p = NP == 1 ? 0 : f / PSZ;
-                const int rem = f - p * PSZ;
-                const int cc = rem / PPL, e = rem - cc * PPL;
-                const int ty = e / PXW, tx = e - ty * PXW;
-                const int c = c0 + cc, sy = y0 + ty + a.ofs, sx = x0 + tx + a.ofs;
-                if (c < a.Cin && (unsigned)sy < (unsigned)a.SH && (unsigned)sx < (unsigned)a.SW)
-                    v = a.src[p][((long)(n * a.Cin + c) * a.SH + sy) * a.SW + sx];
-            }
-            pr[q] = v;
-        }
+        for (int i = 0; i < RPW; ++i) row_src(wave + 4 * i, c0, lane, pr[i]);
+        if (threadIdx.x < 2 * PROWS) row_src(threadIdx.x >> 1, c0, 64 + (threadIdx.x & 1), pr[RPW]);
 #pragma unroll
         for (int q = 0; q < WLD; ++q) {
             const int f = threadIdx.x + q * NT;  // float4 slot of [w][cc][t][r]
@@ -147,11 +149,10 @@ __global__ __launch_bounds__(NT) void tap_kernel(TapArgs a) {
         }
     };
     auto store = [&]() {
+        // patch row rr = (p, cc, ty) is at Ps + p * PSZ + cc * PPL + ty * PXW = Ps + rr * PXW
 #pragma unroll
-        for (int q = 0; q < PLD; ++q) {
-            const int f = threadIdx.x + q * NT;
-            if (f < NP * PSZ) Ps[f] = pr[q];
-        }
+        for (int i = 0; i < RPW; ++i) Ps[(wave + 4 * i) * PXW + lane] = pr[i];
+        if (threadIdx.x < 2 * PROWS) Ps[(threadIdx.x >> 1) * PXW + 64 + (threadIdx.x & 1)] = pr[RPW];
 #pragma unroll
         for (int q = 0; q < WLD; ++q) {
             const int f = threadIdx.x + q * NT;
