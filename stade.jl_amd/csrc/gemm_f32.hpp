@@ -28,6 +28,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 namespace stade {
 namespace gemm {
 
@@ -57,23 +59,11 @@ struct Stage {
     float4 v[ROWS * KT / 4 / NT];
 };
 
-// A tile (r 0..ROWS-1, k 0..15) at (r0, k0) into registers; zero outside rows x K.  A tile
-// that lies wholly inside the operand (the common case, decided per block) takes 16-byte
-// loads with no per-element test.
+// A tile (r 0..ROWS-1, k 0..15) at (r0, k0) into registers; zero outside rows x K.
 template <bool KMAJ, int ROWS>
 __device__ __forceinline__ void load_tile(Stage<ROWS>& st, const float* __restrict__ P, long ld, int rows, int K, int r0,
                                           int k0, bool vec) {
     constexpr int R4 = ROWS / 4;  // float4 per k row (KMAJ = false)
-    if (vec && r0 + ROWS <= rows && k0 + KT <= K) {
-#pragma unroll
-        for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
-            const int f = threadIdx.x + NT * q;
-            const float* p = !KMAJ ? P + (long)(r0 + (f % R4) * 4) + (long)(k0 + f / R4) * ld
-                                   : P + (long)(k0 + (f & 3) * 4) + (long)(r0 + (f >> 2)) * ld;
-            st.v[q] = *reinterpret_cast<const float4*>(p);
-        }
-        return;
-    }
 #pragma unroll
     for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
         const int f = threadIdx.x + NT * q;
@@ -113,6 +103,19 @@ __device__ __forceinline__ void load_tile(Stage<ROWS>& st, const float* __restri
     }
 }
 
+// The same for a tile known to lie inside the operand, with 16-byte aligned rows.
+template <bool KMAJ, int ROWS>
+__device__ __forceinline__ void load_tile_full(Stage<ROWS>& st, const float* __restrict__ P, long ld, int r0, int k0) {
+    constexpr int R4 = ROWS / 4;
+#pragma unroll
+    for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
+        const int f = threadIdx.x + NT * q;
+        const float* p = !KMAJ ? P + (long)(r0 + (f % R4) * 4) + (long)(k0 + f / R4) * ld
+                               : P + (long)(k0 + (f & 3) * 4) + (long)(r0 + (f >> 2)) * ld;
+        st.v[q] = *reinterpret_cast<const float4*>(p);
+    }
+}
+
 // Registers -> LDS tile S[k][r] (row stride LD)
 template <bool KMAJ, int ROWS, int LD>
 __device__ __forceinline__ void store_tile(const Stage<ROWS>& st, float* __restrict__ S) {
@@ -143,18 +146,26 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BNT;
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BNT / 2);
 
+    // Both segments' operands in registers (indexing g.seg[s] with a runtime s would reload
+    // them from the kernel-argument segment at every step).
+    const float* const A0 = g.seg[0].A;
+    const float* const B0 = g.seg[0].B;
+    const long lda0 = g.seg[0].lda, ldb0 = g.seg[0].ldb;
+    const int K0 = g.seg[0].K;
+    const bool two = g.nseg > 1;
+    const float* const A1 = two ? g.seg[1].A : A0;
+    const float* const B1 = two ? g.seg[1].B : B0;
+    const long lda1 = two ? g.seg[1].lda : lda0, ldb1 = two ? g.seg[1].ldb : ldb0;
+    const int K1 = two ? g.seg[1].K : 0;
+
     // the K steps of all segments, in order; this block's slice of them
-    int steps[2], total = 0;
-    for (int s = 0; s < g.nseg; ++s) {
-        steps[s] = (g.seg[s].K + KT - 1) / KT;
-        total += steps[s];
-    }
+    const int steps0 = (K0 + KT - 1) / KT;
+    const int total = steps0 + (K1 + KT - 1) / KT;
     const int t_begin = (int)((long)total * blockIdx.z / g.ksplit);
     const int t_end = (int)((long)total * (blockIdx.z + 1) / g.ksplit);
-    auto locate = [&](int t, int& s, int& k0) {
-        s = (t < steps[0]) ? 0 : 1;
-        k0 = (s == 0 ? t : t - steps[0]) * KT;
-    };
+    // a block whose tiles all lie inside the operands (M, N and every K step) loads with no
+    // per-element tests
+    const bool full = vec && m0 + BM <= g.M && n0 + BNT <= g.N && K0 % KT == 0 && K1 % KT == 0;
 
     floatx16 acc[2][NJ];
 #pragma unroll
@@ -166,52 +177,64 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 
     Stage<BM> sa;
     Stage<BNT> sb;
-    if (t_begin < t_end) {
-        int s, k0;
-        locate(t_begin, s, k0);
-        load_tile<A_KM, BM>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
-        load_tile<B_KM, BNT>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
-        store_tile<A_KM, BM, LDA_S>(sa, As[0]);
-        store_tile<B_KM, BNT, LDB_S>(sb, Bs[0]);
-    }
-    __syncthreads();
-    for (int t = t_begin; t < t_end; ++t) {
-        const int cur = (t - t_begin) & 1;
-        const bool more = t + 1 < t_end;
-        if (more) {
-            int s, k0;
-            locate(t + 1, s, k0);
-            load_tile<A_KM, BM>(sa, g.seg[s].A, g.seg[s].lda, g.M, g.seg[s].K, m0, k0, vec);
-            load_tile<B_KM, BNT>(sb, g.seg[s].B, g.seg[s].ldb, g.N, g.seg[s].K, n0, k0, vec);
+    auto load = [&](int t, bool fast) {
+        const bool s1 = t >= steps0;
+        const float* A = s1 ? A1 : A0;
+        const float* B = s1 ? B1 : B0;
+        const long lda = s1 ? lda1 : lda0, ldb = s1 ? ldb1 : ldb0;
+        const int K = s1 ? K1 : K0;
+        const int k0 = (s1 ? t - steps0 : t) * KT;
+        if (fast) {
+            load_tile_full<A_KM, BM>(sa, A, lda, m0, k0);
+            load_tile_full<B_KM, BNT>(sb, B, ldb, n0, k0);
+        } else {
+            load_tile<A_KM, BM>(sa, A, lda, g.M, K, m0, k0, vec);
+            load_tile<B_KM, BNT>(sb, B, ldb, g.N, K, n0, k0, vec);
         }
-        const float* A_ = As[cur];
-        const float* B_ = Bs[cur];
-        // every fragment of the stage first (the LDS reads overlap each other), then the MFMAs
-        float a[KT / 2][2], b[KT / 2][NJ];
-#pragma unroll
-        for (int ks = 0; ks < KT / 2; ++ks) {
-            const int kk = ks * 2 + (lane >> 5);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) a[ks][i] = A_[kk * LDA_S + wm + i * 32 + (lane & 31)];
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) b[ks][j] = B_[kk * LDB_S + wn + j * 32 + (lane & 31)];
-        }
-        // keep the reads ahead of the MFMAs (the scheduler would sink each read to its use
-        // and expose the LDS latency at every k step)
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ks = 0; ks < KT / 2; ++ks)
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[ks][j], a[ks][i], acc[i][j], 0, 0, 0);
-        if (more) {
-            store_tile<A_KM, BM, LDA_S>(sa, As[cur ^ 1]);
-            store_tile<B_KM, BNT, LDB_S>(sb, Bs[cur ^ 1]);
+    };
+    auto mainloop = [&](auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        if (t_begin < t_end) {
+            load(t_begin, FAST);
+            store_tile<A_KM, BM, LDA_S>(sa, As[0]);
+            store_tile<B_KM, BNT, LDB_S>(sb, Bs[0]);
         }
         __syncthreads();
-    }
+        for (int t = t_begin; t < t_end; ++t) {
+            const int cur = (t - t_begin) & 1;
+            const bool more = t + 1 < t_end;
+            if (more) load(t + 1, FAST);
+            const float* A_ = As[cur];
+            const float* B_ = Bs[cur];
+            // every fragment of the stage first (the LDS reads overlap each other), then the MFMAs
+            float a[KT / 2][2], b[KT / 2][NJ];
+#pragma unroll
+            for (int ks = 0; ks < KT / 2; ++ks) {
+                const int kk = ks * 2 + (lane >> 5);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) a[ks][i] = A_[kk * LDA_S + wm + i * 32 + (lane & 31)];
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) b[ks][j] = B_[kk * LDB_S + wn + j * 32 + (lane & 31)];
+            }
+            // keep the reads ahead of the MFMAs (the scheduler would sink each read to its use
+            // and expose the LDS latency at every k step)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < KT / 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[ks][j], a[ks][i], acc[i][j], 0, 0, 0);
+            if (more) {
+                store_tile<A_KM, BM, LDA_S>(sa, As[cur ^ 1]);
+                store_tile<B_KM, BNT, LDB_S>(sb, Bs[cur ^ 1]);
+            }
+            __syncthreads();
+        }
+    };
+    if (full) mainloop(std::true_type{});
+    else mainloop(std::false_type{});
     // accumulator (i, j, r): m = m0 + wm + 32 i + lane % 32,  n = n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4
     if (g.ksplit > 1) {
         float* part = g.part + (long)blockIdx.z * g.M * g.N;
