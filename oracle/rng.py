@@ -10,14 +10,21 @@ Pinned bit-for-bit against the known answers of
 * `val_normal(rng)`: Box-Muller, cosine branch, u1 = 1 - rand(), u2 = rand()
   (/root/reference/src/STADE.jl:16628-16637).
 
-Pure Python: for the small arrays the oracle tests use.  The product library has its
-own C++ copy (`stade_hip_rng_*` in libstade_hip.so); tests compare the two.
+The scalar draws are pure Python.  Array fills longer than `_C_FILL_MIN` run the same
+stream through `oracle/rng_fill.c` (gcc, built into `oracle/_gen/`), bit-identical to the
+scalar loop; the full-size parity tests need tens of millions of draws.  The product
+library has its own C++ copy (`stade_hip_rng_*` in libstade_hip.so); tests compare them.
 """
 from __future__ import annotations
 
+import ctypes
 import hashlib
 import math
+import os
 import struct
+import subprocess
+import threading
+from pathlib import Path
 
 import numpy as np
 
@@ -76,10 +83,54 @@ def val_normal(rng: Xoshiro) -> float:
     return math.sqrt(-2.0 * math.log(u1)) * math.cos(2.0 * math.pi * u2)
 
 
-def val_randn(rng: Xoshiro, n: int) -> np.ndarray:
+_C_FILL_MIN = 256
+_SRC = Path(__file__).resolve().parent / "rng_fill.c"
+_SO = Path(__file__).resolve().parent / "_gen" / "rng_fill.so"
+_fill_lib = None
+_fill_mu = threading.Lock()
+
+
+def fill_lib(rebuild: bool = False):
+    """Compile (when missing, stale, or `rebuild`) and load oracle/rng_fill.c."""
+    global _fill_lib
+    with _fill_mu:
+        if _fill_lib is not None and not rebuild:
+            return _fill_lib
+        stale = not _SO.exists() or _SO.stat().st_mtime < _SRC.stat().st_mtime
+        if rebuild or stale:
+            _SO.parent.mkdir(parents=True, exist_ok=True)
+            tmp = _SO.with_suffix(f".so.tmp{os.getpid()}")
+            subprocess.run(["gcc", "-O2", "-fno-fast-math", "-ffp-contract=off", "-fPIC", "-shared",
+                            "-o", str(tmp), str(_SRC), "-lm"], check=True)
+            os.replace(tmp, _SO)
+        lib = ctypes.CDLL(str(_SO))
+        st = ctypes.POINTER(ctypes.c_uint64)
+        dp = ctypes.POINTER(ctypes.c_double)
+        lib.oracle_rng_normal.argtypes = [st, dp, ctypes.c_int64]
+        lib.oracle_rng_normal.restype = None
+        lib.oracle_rng_uniform.argtypes = [st, dp, ctypes.c_int64, ctypes.c_double, ctypes.c_double]
+        lib.oracle_rng_uniform.restype = None
+        _fill_lib = lib
+        return lib
+
+
+def _c_fill(rng: Xoshiro, n: int, fn: str, *extra) -> np.ndarray:
+    out = np.empty(n, dtype=np.float64)
+    st = (ctypes.c_uint64 * 4)(*rng.s)
+    getattr(fill_lib(), fn)(st, out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), n, *extra)
+    rng.s = [int(v) for v in st]
+    return out
+
+
+def val_randn(rng: Xoshiro, n: int, c_fill: bool | None = None) -> np.ndarray:
+    """n draws of `val_normal(rng)` in order (`c_fill` forces or forbids the C fill)."""
+    if c_fill if c_fill is not None else n >= _C_FILL_MIN:
+        return _c_fill(rng, n, "oracle_rng_normal")
     return np.array([val_normal(rng) for _ in range(n)], dtype=np.float64)
 
 
-def rand_uniform(rng: Xoshiro, n: int, lo: float = 0.0, hi: float = 1.0) -> np.ndarray:
+def rand_uniform(rng: Xoshiro, n: int, lo: float = 0.0, hi: float = 1.0, c_fill: bool | None = None) -> np.ndarray:
     """`lo + (hi - lo) * rand(rng)`, n scalar draws in order."""
+    if c_fill if c_fill is not None else n >= _C_FILL_MIN:
+        return _c_fill(rng, n, "oracle_rng_uniform", float(lo), float(hi))
     return np.array([lo + (hi - lo) * rng.rand() for _ in range(n)], dtype=np.float64)

@@ -55,3 +55,18 @@ def test_library_rng_matches_oracle_and_known_answers():
     x = stade_hip.rng_uniform(stade_hip.api.Rng(big), 50, -1.0, 1.0)
     g = jrng.Xoshiro(big)
     assert np.array_equal(x, jrng.rand_uniform(g, 50, -1.0, 1.0))
+
+
+@pytest.mark.parametrize("seed", [5, 0, (1 << 64) - 12345, jrng.val_stable_seed("diffusion2d_hv")])
+def test_c_fill_matches_scalar_stream(seed):
+    """oracle/rng_fill.c continues the same stream bit for bit, for normals and uniforms, and
+    leaves the generator where the scalar loop would."""
+    g1, g2 = jrng.Xoshiro(seed), jrng.Xoshiro(seed)
+    a = jrng.val_randn(g1, 3000, c_fill=True)
+    b = jrng.val_randn(g2, 3000, c_fill=False)
+    assert np.array_equal(a, b)
+    assert g1.s == g2.s
+    u = jrng.rand_uniform(g1, 777, -1.0, 1.0, c_fill=True)
+    v = jrng.rand_uniform(g2, 777, -1.0, 1.0, c_fill=False)
+    assert np.array_equal(u, v)
+    assert g1.rand() == g2.rand()
