@@ -7,7 +7,12 @@
 // launch per loop plus a host mapreduce for the loss (10519-10571) and the periodic
 // owner-computes gather (`cgen_gather_periodic_inverse` 7343-7529) for the adjoint scatter.
 //
-// Layout and work per launch (row streaming):
+// Two kernel families:
+//   * wave-strip kernels (n a multiple of 64, the benchmark grids): one wavefront per strip of
+//     64 columns and a chunk of rows, no LDS and no barriers (described at their definition);
+//   * row-streaming kernels (every other n), described next.
+//
+// Row-streaming layout and work per launch:
 //   * A 256-thread block owns a strip of 256 columns (i) and a chunk of CH rows (j); thread t
 //     owns column c0 + t.  It marches down its rows keeping ring buffers of whole strip rows
 //     in LDS (u: 5 rows, the new state's adjoint seed w: 3 rows), each row with a periodic
@@ -36,25 +41,26 @@ constexpr int RW = SW + 4;        // LDS row: 2 halo columns each side (position
 constexpr int CH = 32;            // rows per block (measured best of 16 / 32 / 64 at n = 4096)
 
 // Column geometry of a strip: wi columns c0 .. c0+wi-1; LDS positions 0, 1 hold columns
-// c0-2, c0-1 and positions wi+2, wi+3 hold c0+wi, c0+wi+1 (periodic).
+// c0-2, c0-1 and positions wi+2, wi+3 hold c0+wi, c0+wi+1 (periodic).  Threads 0..3 each
+// carry one halo column (hcol) and its LDS position (hpos) in registers: a per-thread array
+// indexed by the thread id would live in scratch memory and cost a load per row.
 struct Strip {
     int c0, wi, j0, wj, n;
-    int hcol[4];  // the 4 halo columns (thread 0..3 loads hcol[t] into position hpos(t))
-    __device__ int hpos(int t) const { return t < 2 ? t : wi + t; }
+    int hcol, hpos;
 };
 
 __device__ __forceinline__ Strip strip_of(int n, int strips) {
     Strip s;
     const int sx = blockIdx.x % strips, cy = blockIdx.x / strips;
+    const int t = threadIdx.x;
     s.c0 = sx * SW;
     s.wi = min(SW, n - s.c0);
     s.j0 = cy * CH;
     s.wj = min(CH, n - s.j0);
     s.n = n;
-    s.hcol[0] = wrapn(s.c0 - 2, n);
-    s.hcol[1] = wrapn(s.c0 - 1, n);
-    s.hcol[2] = wrapn(s.c0 + s.wi, n);
-    s.hcol[3] = wrapn(s.c0 + s.wi + 1, n);
+    const int off = t < 2 ? t - 2 : s.wi + (t & 3) - 2;  // t = 0..3: c0-2, c0-1, c0+wi, c0+wi+1
+    s.hcol = wrapn(s.c0 + off, n);
+    s.hpos = t < 2 ? t : s.wi + (t & 3);
     return s;
 }
 
@@ -70,14 +76,14 @@ __device__ __forceinline__ RowVal load_row(const double* __restrict__ a, const S
     const size_t base = (size_t)wrapn(s.j0 + r, s.n) * s.n;
     RowVal v{0.0, 0.0};
     if (t < s.wi) v.own = a[base + s.c0 + t];
-    if (halo == 2 ? t < 4 : (t == 1 || t == 2)) v.halo = a[base + s.hcol[t]];
+    if (halo == 2 ? t < 4 : (t == 1 || t == 2)) v.halo = a[base + s.hcol];
     return v;
 }
 
 __device__ __forceinline__ void put_row(double* row, const RowVal& v, const Strip& s) {
     const int t = threadIdx.x;
     if (t < s.wi) row[t + 2] = v.own;
-    if (t < 4) row[s.hpos(t)] = v.halo;
+    if (t < 4) row[s.hpos] = v.halo;
 }
 
 // un at LDS position k of the middle row, in the operation order of the generated text:
@@ -320,6 +326,270 @@ __global__ __launch_bounds__(NT) void zero2_kernel(double* __restrict__ a, doubl
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Wave-strip kernels: the fast path when n is a multiple of 64 and of the chunk height.
+//
+// One wavefront owns a strip of 64 columns (lane l: column c0 + l) and a chunk of WCH rows,
+// and marches down it alone: no LDS, no barriers.  East / west neighbours come from the
+// adjacent lanes by DPP wavefront shifts; the strip's two edge columns come from a second
+// load per row ("halo" lanes 0..3 load columns c0-2, c0-1, c0+64, c0+65; lanes 4..63 repeat
+// lane 3's address, a cache line already being fetched) and are broadcast with readlane.
+// Rows above and below are held in registers.  The row loop is unrolled in full and every
+// load is unconditional, so the loads of the next WD rows stay in flight while a row is
+// computed (the compiler can count them exactly; a branch around a load would force it to
+// wait for all of them).
+// ---------------------------------------------------------------------------------------
+#ifndef STADE_DIFF_WCH
+#define STADE_DIFF_WCH 64
+#endif
+#ifndef STADE_DIFF_WCH_HV
+#define STADE_DIFF_WCH_HV 32
+#endif
+#ifndef STADE_DIFF_WD
+#define STADE_DIFF_WD 4
+#endif
+#ifndef STADE_DIFF_WD_HV
+#define STADE_DIFF_WD_HV 4
+#endif
+// rows per wave and rows of loads in flight ahead of the row being computed; measured at
+// n = 4096: 64 rows beat 32 for the adjoint and the tangent (fewer halo rows), while the
+// HVP, with twice the values per row, keeps 32 rows to stay in registers (at 64 it spills).
+// Depths 3..6 measured within 2 % of each other.
+constexpr int WS = 64;                      // columns per wave strip
+constexpr int WCH = STADE_DIFF_WCH;         // adjoint, tangent
+constexpr int WCH_HV = STADE_DIFF_WCH_HV;   // HVP
+constexpr int WD = STADE_DIFF_WD;
+constexpr int WD_HV = STADE_DIFF_WD_HV;
+static_assert(WS % WCH == 0 && WS % WCH_HV == 0, "the wave-strip path requires n % 64 == 0 to imply n % rows == 0");
+constexpr int kDppWaveShl1 = 0x130;   // lane l <- lane l+1
+constexpr int kDppWaveShr1 = 0x138;   // lane l <- lane l-1
+
+// v of the lane to the west (lane l-1); lane 0 gets `edge`
+__device__ __forceinline__ double from_west(double v, double edge) {
+    const int lo = __builtin_amdgcn_update_dpp(__double2loint(edge), __double2loint(v), kDppWaveShr1, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(__double2hiint(edge), __double2hiint(v), kDppWaveShr1, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+// v of the lane to the east (lane l+1); lane 63 gets `edge`
+__device__ __forceinline__ double from_east(double v, double edge) {
+    const int lo = __builtin_amdgcn_update_dpp(__double2loint(edge), __double2loint(v), kDppWaveShl1, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(__double2hiint(edge), __double2hiint(v), kDppWaveShl1, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+// v of lane l, in every lane
+__device__ __forceinline__ double lane_val(double v, int l) {
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), l), __builtin_amdgcn_readlane(__double2loint(v), l));
+}
+
+// the 5-point forms of step5 / step5d on values instead of LDS positions
+__device__ __forceinline__ double step5v(double up, double c, double dn, double w, double e) {
+    double t = w + e;
+    t = t + up;
+    t = t + dn;
+    t = t - 4.0 * c;
+    return c + 0.1 * t;
+}
+__device__ __forceinline__ double step5dv(double up, double c, double dn, double w, double e) {
+    double t = w + e;
+    t = t + up;
+    t = t + dn;
+    t = t + -(4.0 * c);
+    return c + 0.1 * t;
+}
+
+struct WaveGeom {
+    int c0, j0, oc, hc;
+};
+// wave `wid` = strip wid % nstrips, chunk wid / nstrips of `rows` rows
+__device__ __forceinline__ WaveGeom wave_geom(int wid, int n, int nstrips, int rows) {
+    const int lane = threadIdx.x & 63;
+    WaveGeom g;
+    g.c0 = (wid % nstrips) * WS;
+    g.j0 = (wid / nstrips) * rows;
+    g.oc = g.c0 + lane;
+    const int hoff = lane == 0 ? -2 : (lane == 1 ? -1 : (lane == 2 ? WS : WS + 1));
+    g.hc = wrap1(g.c0 + hoff, n);
+    return g;
+}
+
+// tangent: un, und of rows j0 .. j0+ROWS-1 from u, ud rows j0-1 .. j0+ROWS
+template <int ROWS, int D>
+__global__ __launch_bounds__(256) void diffusion_d_wave(const double* __restrict__ u, const double* __restrict__ ud,
+                                                        double* __restrict__ un, double* __restrict__ und, int n,
+                                                        int nstrips, int nwaves, double* partials) {
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= nwaves) return;  // whole waves only; the kernel has no barrier
+    const WaveGeom g = wave_geom(wid, n, nstrips, ROWS);
+    double U[ROWS + 2], H[ROWS + 2], UD[ROWS + 2], HD[ROWS + 2];  // row q at index q + 1
+    auto load = [&](int q) {
+        const size_t rb = (size_t)wrap1(g.j0 + q, n) * n;
+        U[q + 1] = u[rb + g.oc];
+        H[q + 1] = u[rb + g.hc];
+        UD[q + 1] = ud[rb + g.oc];
+        HD[q + 1] = ud[rb + g.hc];
+    };
+    load(-1);
+    load(0);
+#pragma unroll
+    for (int k = 1; k <= D; ++k) load(k);
+    double acc[2] = {0.0, 0.0};
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        if (r + D + 1 <= ROWS) load(r + D + 1);
+        const int i = r + 1;
+        const double v = step5v(U[i - 1], U[i], U[i + 1], from_west(U[i], lane_val(H[i], 1)), from_east(U[i], lane_val(H[i], 2)));
+        const double vd =
+            step5dv(UD[i - 1], UD[i], UD[i + 1], from_west(UD[i], lane_val(HD[i], 1)), from_east(UD[i], lane_val(HD[i], 2)));
+        const size_t gi = (size_t)(g.j0 + r) * n + g.oc;
+        und[gi] = vd;
+        un[gi] = v;
+        acc[1] += (2.0 * v) * vd;
+        acc[0] += v * v;
+    }
+    acc[0] = wave_sum(acc[0]);
+    acc[1] = wave_sum(acc[1]);
+    if ((threadIdx.x & 63) == 0) {
+        partials[(size_t)wid * 2] = acc[0];
+        partials[(size_t)wid * 2 + 1] = acc[1];
+    }
+}
+
+// adjoint pass 1 (HV = false) and its tangent (HV = true): un (+ und) of the wave's rows,
+// loss partials, and the gather of w = unb + (2 un) lossb (+ wd) into ub (+ ubd)
+template <bool HV, int ROWS, int D>
+__global__ __launch_bounds__(256) void diffusion_b_wave(const double* __restrict__ u, const double* __restrict__ ud,
+                                                        double* __restrict__ un, double* __restrict__ und,
+                                                        const double* __restrict__ unb, const double* __restrict__ unbd,
+                                                        double* __restrict__ ub, double* __restrict__ ubd,
+                                                        const double* __restrict__ lossb, const double* __restrict__ lossbd,
+                                                        int n, int nstrips, int nwaves, double* partials) {
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= nwaves) return;  // whole waves only; the kernel has no barrier
+    const WaveGeom g = wave_geom(wid, n, nstrips, ROWS);
+    const double lb = lossb[0];
+    const double lbd = HV ? lossbd[0] : 0.0;
+    // u rows -2 .. ROWS+1 at index q + 2; unb rows -1 .. ROWS at q + 1; ub rows 0 .. ROWS-1
+    double U[ROWS + 4], H[ROWS + 4], B[ROWS + 2], BH[ROWS + 2], UB[ROWS];
+    double UD[HV ? ROWS + 4 : 1], HD[HV ? ROWS + 4 : 1], BD[HV ? ROWS + 2 : 1], BHD[HV ? ROWS + 2 : 1], UBD[HV ? ROWS : 1];
+    auto rowb = [&](int q) { return (size_t)wrap1(g.j0 + q, n) * n; };
+    auto load_u = [&](int q) {
+        const size_t rb = rowb(q);
+        U[q + 2] = u[rb + g.oc];
+        H[q + 2] = u[rb + g.hc];
+        if constexpr (HV) {
+            UD[q + 2] = ud[rb + g.oc];
+            HD[q + 2] = ud[rb + g.hc];
+        }
+    };
+    auto load_b = [&](int q) {
+        const size_t rb = rowb(q);
+        B[q + 1] = unb[rb + g.oc];
+        BH[q + 1] = unb[rb + g.hc];
+        if constexpr (HV) {
+            BD[q + 1] = unbd[rb + g.oc];
+            BHD[q + 1] = unbd[rb + g.hc];
+        }
+    };
+    // the loads that step r consumes last: u row r+2, unb row r+1, ub row r
+    auto load_group = [&](int r) {
+        load_u(r + 2);
+        load_b(r + 1);
+        const size_t gi = (size_t)(g.j0 + r) * n + g.oc;
+        UB[r] = ub[gi];
+        if constexpr (HV) UBD[r] = ubd[gi];
+    };
+    // w of rows -1 .. ROWS (own column) and of the edge columns c0-1 (west) and c0+64 (east)
+    double Wo[ROWS + 2], Ww[ROWS + 2], We[ROWS + 2];
+    double WDo[HV ? ROWS + 2 : 1], WDw[HV ? ROWS + 2 : 1], WDe[HV ? ROWS + 2 : 1];
+    double acc[2] = {0.0, 0.0};
+    // un (+ und) and w (+ wd) of row q in the generated text's operation order; un stored
+    // for the wave's own rows
+    auto new_state = [&](int q) {
+        const int i = q + 2;
+        const double v = step5v(U[i - 1], U[i], U[i + 1], from_west(U[i], lane_val(H[i], 1)), from_east(U[i], lane_val(H[i], 2)));
+        const double vw = step5v(lane_val(H[i - 1], 1), lane_val(H[i], 1), lane_val(H[i + 1], 1), lane_val(H[i], 0), lane_val(U[i], 0));
+        const double ve = step5v(lane_val(H[i - 1], 2), lane_val(H[i], 2), lane_val(H[i + 1], 2), lane_val(U[i], 63), lane_val(H[i], 3));
+        const int b = q + 1;
+        Wo[b] = B[b] + (2.0 * v) * lb;
+        Ww[b] = lane_val(BH[b], 1) + (2.0 * vw) * lb;
+        We[b] = lane_val(BH[b], 2) + (2.0 * ve) * lb;
+        double vd = 0.0;
+        if constexpr (HV) {
+            vd = step5dv(UD[i - 1], UD[i], UD[i + 1], from_west(UD[i], lane_val(HD[i], 1)), from_east(UD[i], lane_val(HD[i], 2)));
+            const double vdw =
+                step5dv(lane_val(HD[i - 1], 1), lane_val(HD[i], 1), lane_val(HD[i + 1], 1), lane_val(HD[i], 0), lane_val(UD[i], 0));
+            const double vde =
+                step5dv(lane_val(HD[i - 1], 2), lane_val(HD[i], 2), lane_val(HD[i + 1], 2), lane_val(UD[i], 63), lane_val(HD[i], 3));
+            WDo[b] = BD[b] + (lb * (2.0 * vd) + (2.0 * v) * lbd);
+            WDw[b] = lane_val(BHD[b], 1) + (lb * (2.0 * vdw) + (2.0 * vw) * lbd);
+            WDe[b] = lane_val(BHD[b], 2) + (lb * (2.0 * vde) + (2.0 * ve) * lbd);
+        }
+        if (q >= 0 && q < ROWS) {
+            const size_t gi = (size_t)(g.j0 + q) * n + g.oc;
+            if constexpr (HV) {
+                und[gi] = vd;
+                acc[1] += (2.0 * v) * vd;
+            }
+            un[gi] = v;
+            acc[0] += v * v;
+        }
+    };
+    // ub[row r] += w_c + 0.1 w_E + 0.1 w_W + 0.1 w_S + 0.1 w_N + 4 (-(0.1 w_c))
+    auto gather = [&](int r) {
+        const int b = r + 1;
+        const double c = Wo[b];
+        double a = c;
+        a = a + 0.1 * from_east(c, We[b]);
+        a = a + 0.1 * from_west(c, Ww[b]);
+        a = a + 0.1 * Wo[b + 1];
+        a = a + 0.1 * Wo[b - 1];
+        a = a + 4.0 * -(0.1 * c);
+        const size_t gi = (size_t)(g.j0 + r) * n + g.oc;
+        if constexpr (HV) {
+            const double cd = WDo[b];
+            double ad = cd;
+            ad = ad + 0.1 * from_east(cd, WDe[b]);
+            ad = ad + 0.1 * from_west(cd, WDw[b]);
+            ad = ad + 0.1 * WDo[b + 1];
+            ad = ad + 0.1 * WDo[b - 1];
+            ad = ad + 4.0 * -(0.1 * cd);
+            ubd[gi] = UBD[r] + ad;
+        }
+        ub[gi] = UB[r] + a;
+    };
+#pragma unroll
+    for (int q = -2; q <= 1; ++q) load_u(q);
+    load_b(-1);
+    load_b(0);
+#pragma unroll
+    for (int k = 0; k < D; ++k) load_group(k);
+    new_state(-1);
+    new_state(0);
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        if (r + D < ROWS) load_group(r + D);
+        new_state(r + 1);
+        gather(r);
+    }
+    acc[0] = wave_sum(acc[0]);
+    if constexpr (HV) acc[1] = wave_sum(acc[1]);
+    if ((threadIdx.x & 63) == 0) {
+        partials[(size_t)wid * (HV ? 2 : 1)] = acc[0];
+        if constexpr (HV) partials[(size_t)wid * 2 + 1] = acc[1];
+    }
+}
+
+struct WaveGrid {
+    int nstrips, nwaves, blocks;
+};
+// the wave-strip path applies when n is a multiple of the strip width (and so of the rows
+// per wave)
+bool wave_path(int64_t n) { return n >= WS && n % WS == 0; }
+WaveGrid wave_grid_of(int64_t n, int rows) {
+    const int nstrips = (int)(n / WS), nwaves = nstrips * (int)(n / rows);
+    return WaveGrid{nstrips, nwaves, (nwaves + 3) / 4};
+}
+
 int32_t check_n(int64_t n, const char* fn) {
     if (n < 0) return set_error(STADE_HIP_EINVAL, "%s: n = %lld is negative", fn, (long long)n);
     if (n > 46340) return set_error(STADE_HIP_ERANGE, "%s: n = %lld exceeds 46340 (n*n must fit Int32 cell indices)", fn, (long long)n);
@@ -355,11 +625,21 @@ int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, co
     if (!loss || !lossd || !u || !ud || !un || !und) return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_d: null pointer");
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
-    const Grid g = grid_of(n);
-    STADE_TIMED("diffusion2d_d", stream,
-                diffusion_d_kernel<<<g.blocks, NT, 0, stream>>>(u, ud, un, und, (int)n, g.strips, ws->partials));
-    STADE_LAUNCHED("diffusion_d_kernel");
-    STADE_TIMED("finalize", stream, finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, g.blocks, SumOuts{{loss, lossd}}));
+    int nparts;
+    if (wave_path(n)) {
+        const WaveGrid w = wave_grid_of(n, WCH);
+        STADE_TIMED("diffusion2d_d", stream,
+                    diffusion_d_wave<WCH, WD><<<w.blocks, 256, 0, stream>>>(u, ud, un, und, (int)n, w.nstrips, w.nwaves, ws->partials));
+        STADE_LAUNCHED("diffusion_d_wave");
+        nparts = w.nwaves;
+    } else {
+        const Grid g = grid_of(n);
+        STADE_TIMED("diffusion2d_d", stream,
+                    diffusion_d_kernel<<<g.blocks, NT, 0, stream>>>(u, ud, un, und, (int)n, g.strips, ws->partials));
+        STADE_LAUNCHED("diffusion_d_kernel");
+        nparts = g.blocks;
+    }
+    STADE_TIMED("finalize", stream, finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, nparts, SumOuts{{loss, lossd}}));
     STADE_LAUNCHED("finalize_kernel");
     return STADE_HIP_OK;
 }
@@ -371,13 +651,25 @@ int32_t stade_hip_diffusion2d_b(double* loss, const double* lossb, const double*
     if (!loss || !lossb || !u || !ub || !un || !unb) return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_b: null pointer");
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
-    const Grid g = grid_of(n);
-    STADE_TIMED("diffusion2d_b", stream,
-                diffusion_b_kernel<false><<<g.blocks, NT, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr, lossb,
-                                                                       nullptr, (int)n, g.strips, ws->partials));
-    STADE_LAUNCHED("diffusion_b_kernel");
+    int nparts;
+    if (wave_path(n)) {
+        const WaveGrid w = wave_grid_of(n, WCH);
+        STADE_TIMED("diffusion2d_b", stream,
+                    diffusion_b_wave<false, WCH, WD><<<w.blocks, 256, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr,
+                                                                              lossb, nullptr, (int)n, w.nstrips, w.nwaves,
+                                                                              ws->partials));
+        STADE_LAUNCHED("diffusion_b_wave");
+        nparts = w.nwaves;
+    } else {
+        const Grid g = grid_of(n);
+        STADE_TIMED("diffusion2d_b", stream,
+                    diffusion_b_kernel<false><<<g.blocks, NT, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr,
+                                                                           lossb, nullptr, (int)n, g.strips, ws->partials));
+        STADE_LAUNCHED("diffusion_b_kernel");
+        nparts = g.blocks;
+    }
     STADE_TIMED("zero", stream,
-                zero2_kernel<1><<<zero_blocks(n * n), NT, 0, stream>>>(unb, nullptr, (size_t)(n * n), ws->partials, g.blocks,
+                zero2_kernel<1><<<zero_blocks(n * n), NT, 0, stream>>>(unb, nullptr, (size_t)(n * n), ws->partials, nparts,
                                                                        SumOuts{{loss}}));
     STADE_LAUNCHED("zero2_kernel");
     return STADE_HIP_OK;
@@ -392,13 +684,24 @@ int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double
         return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_hv: null pointer");
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
-    const Grid g = grid_of(n);
-    STADE_TIMED("diffusion2d_hv", stream,
-                diffusion_b_kernel<true><<<g.blocks, NT, 0, stream>>>(u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd, (int)n,
-                                                                      g.strips, ws->partials));
-    STADE_LAUNCHED("diffusion_b_kernel<hv>");
+    int nparts;
+    if (wave_path(n)) {
+        const WaveGrid w = wave_grid_of(n, WCH_HV);
+        STADE_TIMED("diffusion2d_hv", stream,
+                    diffusion_b_wave<true, WCH_HV, WD_HV><<<w.blocks, 256, 0, stream>>>(u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd,
+                                                                                (int)n, w.nstrips, w.nwaves, ws->partials));
+        STADE_LAUNCHED("diffusion_b_wave<hv>");
+        nparts = w.nwaves;
+    } else {
+        const Grid g = grid_of(n);
+        STADE_TIMED("diffusion2d_hv", stream,
+                    diffusion_b_kernel<true><<<g.blocks, NT, 0, stream>>>(u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd,
+                                                                          (int)n, g.strips, ws->partials));
+        STADE_LAUNCHED("diffusion_b_kernel<hv>");
+        nparts = g.blocks;
+    }
     STADE_TIMED("zero", stream,
-                zero2_kernel<2><<<zero_blocks(n * n), NT, 0, stream>>>(unb, unbd, (size_t)(n * n), ws->partials, g.blocks,
+                zero2_kernel<2><<<zero_blocks(n * n), NT, 0, stream>>>(unb, unbd, (size_t)(n * n), ws->partials, nparts,
                                                                        SumOuts{{loss, lossd}}));
     STADE_LAUNCHED("zero2_kernel");
     return STADE_HIP_OK;
