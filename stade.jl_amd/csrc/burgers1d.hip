@@ -141,6 +141,82 @@ __global__ __launch_bounds__(NT) void bwd_init_kernel(const double* __restrict__
 //   ub[y] = B(y+1) + C(y+1) + own(y) + A(y-1) + C(y-1)   (the generated statement order of
 // the interior, with A/B/C the contributions a cell sends to its east/west neighbours)
 // ---------------------------------------------------------------------------------------
+
+// One backward step k on the extended region: reads the tape row in U (+ UD) and the adjoint
+// state in Wc (+ WDc), writes the next adjoint state to Wn (+ WDn) on [k+1, len-k-1), and adds
+// the owned cells' coefficient-shadow terms to acc.
+template <bool HV, int M>
+__device__ __forceinline__ void bwd_step(int k, int len, int nk, int own, const double* U, const double* UD, const double* Wc,
+                                         const double* WDc, double* Wn, double* WDn, const Coef& c, double (&acc)[4]) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = threadIdx.x + i * BNT;
+        if (e < k + 1 || e >= len - k - 1) continue;
+        // contributions of the three cells e-1, e, e+1
+        double um1 = U[e - 1], uc = U[e], up1 = U[e + 1];
+        double wm = Wc[e - 1], wc = Wc[e], wp = Wc[e + 1];
+        // cell e+1 -> west neighbour e:  B = -(c5 * c4), C = cdif * w
+        double c4p = -wp, c5p = c.cadv * up1;
+        double Bp = -(c5p * c4p), Cp = c.cdif * wp;
+        // cell e-1 -> east neighbour e: A = c5 * c4
+        double c4m = -wm, c5m = c.cadv * um1;
+        double Am = c5m * c4m, Cm = c.cdif * wm;
+        // own: ucb = ((w + (cadv * c3) * c4) + 2.0 * -(cdif * w))
+        double c3 = up1 - um1, c4 = -wc;
+        double h7 = c.cadv * c3;
+        double c6 = c.cdif * wc;
+        double own_ = ((0.0 + wc) + h7 * c4) + 2.0 * -c6;
+        double s = ((((0.0 + Bp) + Cp) + own_) + Am) + Cm;
+        const bool owned = e >= nk && e < nk + own;
+        if (owned) {
+            acc[0] += (uc * c3) * c4;
+            acc[1] += ((up1 - 2.0 * uc) + um1) * wc;
+        }
+        if (HV) {
+            double dm1 = UD[e - 1], dc = UD[e], dp1 = UD[e + 1];
+            double wdm = WDc[e - 1], wdc = WDc[e], wdp = WDc[e + 1];
+            // east neighbour e+1's contributions to e
+            double c4pd = -wdp, c5pd = up1 * c.cadvd + c.cadv * dp1;
+            double h8p = c4p * c5pd + c5p * c4pd;
+            double Bpd = -h8p, Cpd = wp * c.cdifd + c.cdif * wdp;
+            // west neighbour e-1's contributions to e
+            double c4md = -wdm, c5md = um1 * c.cadvd + c.cadv * dm1;
+            double Amd = c4m * c5md + c5m * c4md, Cmd = wm * c.cdifd + c.cdif * wdm;
+            // own
+            double c3d = dp1 + -dm1, c4d = -wdc;
+            double c6d = wc * c.cdifd + c.cdif * wdc;
+            double ownd = ((0.0 + wdc) + (c4 * (c3 * c.cadvd + c.cadv * c3d) + h7 * c4d)) + 2.0 * -c6d;
+            WDn[e] = ((((0.0 + Bpd) + Cpd) + ownd) + Amd) + Cmd;
+            if (owned) {
+                double h6 = uc * c3;
+                acc[2] += c4 * (c3 * dc + uc * c3d) + h6 * c4d;
+                double h9 = (up1 - 2.0 * uc) + um1;
+                double h9d = (dp1 + -(2.0 * dc)) + dm1;
+                acc[3] += wc * h9d + h9 * wdc;
+            }
+        }
+        Wn[e] = s;
+    }
+}
+
+// the chunk's final adjoint state and its coefficient-shadow partials
+template <bool HV>
+__device__ __forceinline__ void bwd_finish(const double* Wc, const double* WDc, double* __restrict__ vout,
+                                           double* __restrict__ voutd, int x0, int nk, int own, double (&acc)[4], double* red,
+                                           double* partials) {
+    for (int e = threadIdx.x; e < own; e += BNT) {
+        vout[x0 + e] = Wc[nk + e];
+        if (HV) voutd[x0 + e] = WDc[nk + e];
+    }
+    if (HV) {
+        block_partials<4>(acc, red, partials);
+    } else {
+        double v[2] = {acc[0], acc[1]};
+        block_partials<2>(v, red, partials);
+    }
+}
+
+// any nk <= KMAX: the tape row of the next step is fetched one step ahead
 template <bool HV, int S>
 __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win, const double* __restrict__ wind,
                                                   double* __restrict__ vout, double* __restrict__ voutd,
@@ -195,72 +271,77 @@ __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win
         }
         if (k + 1 < nk) fetch(k + 1);
         __syncthreads();
-#pragma unroll
-        for (int i = 0; i < M; ++i) {
-            const int e = threadIdx.x + i * BNT;
-            if (e < k + 1 || e >= len - k - 1) continue;
-            const double* Wc = W[cur];
-            // contributions of the three cells e-1, e, e+1
-            double um1 = U[e - 1], uc = U[e], up1 = U[e + 1];
-            double wm = Wc[e - 1], wc = Wc[e], wp = Wc[e + 1];
-            // cell e+1 -> west neighbour e:  B = -(c5 * c4), C = cdif * w
-            double c4p = -wp, c5p = c.cadv * up1;
-            double Bp = -(c5p * c4p), Cp = c.cdif * wp;
-            // cell e-1 -> east neighbour e: A = c5 * c4
-            double c4m = -wm, c5m = c.cadv * um1;
-            double Am = c5m * c4m, Cm = c.cdif * wm;
-            // own: ucb = ((w + (cadv * c3) * c4) + 2.0 * -(cdif * w))
-            double c3 = up1 - um1, c4 = -wc;
-            double h7 = c.cadv * c3;
-            double c6 = c.cdif * wc;
-            double own_ = ((0.0 + wc) + h7 * c4) + 2.0 * -c6;
-            double s = ((((0.0 + Bp) + Cp) + own_) + Am) + Cm;
-            double sd = 0.0;
-            const bool owned = e >= nk && e < nk + own;
-            if (owned) {
-                acc[0] += (uc * c3) * c4;
-                acc[1] += ((up1 - 2.0 * uc) + um1) * wc;
-            }
-            if (HV) {
-                const double* WDc = WD[cur];
-                double dm1 = UD[e - 1], dc = UD[e], dp1 = UD[e + 1];
-                double wdm = WDc[e - 1], wdc = WDc[e], wdp = WDc[e + 1];
-                // east neighbour e+1's contributions to e
-                double c4pd = -wdp, c5pd = up1 * c.cadvd + c.cadv * dp1;
-                double h8p = c4p * c5pd + c5p * c4pd;
-                double Bpd = -h8p, Cpd = wp * c.cdifd + c.cdif * wdp;
-                // west neighbour e-1's contributions to e
-                double c4md = -wdm, c5md = um1 * c.cadvd + c.cadv * dm1;
-                double Amd = c4m * c5md + c5m * c4md, Cmd = wm * c.cdifd + c.cdif * wdm;
-                // own
-                double c3d = dp1 + -dm1, c4d = -wdc;
-                double c6d = wc * c.cdifd + c.cdif * wdc;
-                double ownd = ((0.0 + wdc) + (c4 * (c3 * c.cadvd + c.cadv * c3d) + h7 * c4d)) + 2.0 * -c6d;
-                sd = ((((0.0 + Bpd) + Cpd) + ownd) + Amd) + Cmd;
-                WD[cur ^ 1][e] = sd;
-                if (owned) {
-                    double h6 = uc * c3;
-                    acc[2] += c4 * (c3 * dc + uc * c3d) + h6 * c4d;
-                    double h9 = (up1 - 2.0 * uc) + um1;
-                    double h9d = (dp1 + -(2.0 * dc)) + dm1;
-                    acc[3] += wc * h9d + h9 * wdc;
-                }
-            }
-            W[cur ^ 1][e] = s;
-        }
+        bwd_step<HV, M>(k, len, nk, own, U, UD, W[cur], WD[HV ? cur : 0], W[cur ^ 1], WD[HV ? cur ^ 1 : 0], c, acc);
         __syncthreads();
         cur ^= 1;
     }
-    for (int e = threadIdx.x; e < own; e += BNT) {
-        vout[x0 + e] = W[cur][nk + e];
-        if (HV) voutd[x0 + e] = WD[cur][nk + e];
+    bwd_finish<HV>(W[cur], WD[HV ? cur : 0], vout, voutd, x0, nk, own, acc, red, partials);
+}
+
+// a full chunk of KMAX steps: the tape rows of the next PD steps are in flight while a step
+// is computed (the generic kernel above fetches one step ahead and measured 3.4 TB/s).  Every load is unconditional (positions past the extended region read column
+// 0; the last PD steps re-read the chunk's last row, an L2 hit), so the compiler can count the
+// loads still in flight instead of waiting for all of them.
+// PD: 4 rows ahead for the adjoint; 2 for the HVP, whose rows are twice as wide in registers
+template <bool HV, int S, int PD>
+__global__ __launch_bounds__(BNT) void bwd_full_kernel(const double* __restrict__ win, const double* __restrict__ wind,
+                                                       double* __restrict__ vout, double* __restrict__ voutd,
+                                                       const double* __restrict__ tape, const double* __restrict__ taped,
+                                                       int n, int64_t t_hi, Coef c, double* partials) {
+    static_assert(KMAX % PD == 0, "full chunks are whole rounds of the prefetch ring");
+    constexpr int nk = KMAX;
+    constexpr int L = S + 2 * KMAX, len = L;
+    constexpr int M = (L + BNT - 1) / BNT;
+    __shared__ double W[2][L];
+    __shared__ double U[L];
+    __shared__ double WD[HV ? 2 : 1][HV ? L : 1];
+    __shared__ double UD[HV ? L : 1];
+    __shared__ double red[16 * 4];
+    const int x0 = blockIdx.x * S;
+    const int own = min(S, n - x0);
+    int xcol[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = threadIdx.x + i * BNT;
+        xcol[i] = e < len ? wrapn(x0 - nk + e, n) : 0;
+        if (e < len) {
+            W[0][e] = win[xcol[i]];
+            if (HV) WD[0][e] = wind[xcol[i]];
+        }
     }
-    if (HV) {
-        block_partials<4>(acc, red, partials);
-    } else {
-        double v[2] = {acc[0], acc[1]};
-        block_partials<2>(v, red, partials);
+    double pre[PD][M], pred[HV ? PD : 1][M];
+    auto fetch = [&](int slot, int k) {
+        const size_t row = (size_t)(t_hi - (k < nk ? k : nk - 1)) * (size_t)n;
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            pre[slot][i] = tape[row + xcol[i]];
+            if constexpr (HV) pred[slot][i] = taped[row + xcol[i]];
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < PD; ++j) fetch(j, j);
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    int cur = 0;
+    for (int k0 = 0; k0 < nk; k0 += PD) {
+#pragma unroll
+        for (int j = 0; j < PD; ++j) {
+            const int k = k0 + j;
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                const int e = threadIdx.x + i * BNT;
+                if (e < len) {
+                    U[e] = pre[j][i];
+                    if constexpr (HV) UD[e] = pred[j][i];
+                }
+            }
+            fetch(j, k + PD);
+            __syncthreads();
+            bwd_step<HV, M>(k, len, nk, own, U, UD, W[cur], WD[HV ? cur : 0], W[cur ^ 1], WD[HV ? cur ^ 1 : 0], c, acc);
+            __syncthreads();
+            cur ^= 1;
+        }
     }
+    bwd_finish<HV>(W[cur], WD[HV ? cur : 0], vout, voutd, x0, nk, own, acc, red, partials);
 }
 
 // second stage of the reverse sweep's sums: block 0 the loss (init kernel's partials),
@@ -396,9 +477,15 @@ int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, dou
         bool last = t - nk < 0;
         double* d = last ? ub : ow;
         double* dd = last ? ubd : owd;
-        STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
-                    bwd_kernel<HV, S><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, nk, c,
-                                                             pbwd + (size_t)chunk * nb * NV));
+        if (nk == KMAX) {
+            STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
+                        bwd_full_kernel<HV, S, HV ? 2 : 4><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, c,
+                                                                      pbwd + (size_t)chunk * nb * NV));
+        } else {
+            STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
+                        bwd_kernel<HV, S><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, nk, c,
+                                                                 pbwd + (size_t)chunk * nb * NV));
+        }
         STADE_LAUNCHED("burgers1d bwd_kernel");
         ++chunk;
         *nparts = chunk * (int)nb;

@@ -51,6 +51,8 @@ struct Args {
     int M, N;
     int ksplit;     // blockIdx.z ranges over ksplit slices of the K steps
     float* part;    // ksplit > 1: partial tiles, slice z at part + z * M * N, column-major
+    bool bufok;     // set by launch(): every operand's byte extent fits 31 bits and the two
+                    // segments share lda and ldb, so whole tiles may use buffer loads
 };
 
 // Registers holding one ROWS x 16 operand tile between its global load and its LDS store.
@@ -103,16 +105,45 @@ __device__ __forceinline__ void load_tile(Stage<ROWS>& st, const float* __restri
     }
 }
 
-// The same for a tile known to lie inside the operand, with 16-byte aligned rows.
+// The same for a tile known to lie inside the operand, with 16-byte aligned rows, as buffer
+// loads: a scalar resource over the operand, this thread's constant byte offsets (tile_offsets)
+// and a scalar byte offset for the K step.  No per-step address arithmetic in vector
+// registers, so the loads' destination registers are not reused as address temporaries
+// while the loads are in flight.
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kBufWord3 = 0x00020000;  // gfx9-family buffer resource word 3 (raw, 32-bit data)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t operand_rsrc(const float* P) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(P), (short)0, 0x7fffffff, kBufWord3);
+}
+
 template <bool KMAJ, int ROWS>
-__device__ __forceinline__ void load_tile_full(Stage<ROWS>& st, const float* __restrict__ P, long ld, int r0, int k0) {
+struct TileOffsets {
+    uint32_t o[ROWS * KT / 4 / NT];
+};
+
+// byte offsets of this thread's float4s of the tile at rows r0.., k step 0
+template <bool KMAJ, int ROWS>
+__device__ __forceinline__ TileOffsets<KMAJ, ROWS> tile_offsets(long ld, int r0) {
     constexpr int R4 = ROWS / 4;
+    TileOffsets<KMAJ, ROWS> t;
 #pragma unroll
     for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
         const int f = threadIdx.x + NT * q;
-        const float* p = !KMAJ ? P + (long)(r0 + (f % R4) * 4) + (long)(k0 + f / R4) * ld
-                               : P + (long)(k0 + (f & 3) * 4) + (long)(r0 + (f >> 2)) * ld;
-        st.v[q] = *reinterpret_cast<const float4*>(p);
+        const long e = !KMAJ ? (long)(r0 + (f % R4) * 4) + (long)(f / R4) * ld : (long)((f & 3) * 4) + (long)(r0 + (f >> 2)) * ld;
+        t.o[q] = (uint32_t)(e * 4);
+    }
+    return t;
+}
+
+// soff: byte offset of K step k0 (k0 * ld * 4 for KMAJ = false, k0 * 4 for KMAJ = true)
+template <bool KMAJ, int ROWS>
+__device__ __forceinline__ void load_tile_full(Stage<ROWS>& st, __amdgpu_buffer_rsrc_t r, const TileOffsets<KMAJ, ROWS>& to,
+                                               uint32_t soff) {
+#pragma unroll
+    for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
+        const v4f x = __builtin_amdgcn_raw_buffer_load_b128(r, to.o[q], soff, 0);
+        st.v[q] = make_float4(x.x, x.y, x.z, x.w);
     }
 }
 
@@ -165,7 +196,13 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     const int t_end = (int)((long)total * (blockIdx.z + 1) / g.ksplit);
     // a block whose tiles all lie inside the operands (M, N and every K step) loads with no
     // per-element tests
-    const bool full = vec && m0 + BM <= g.M && n0 + BNT <= g.N && K0 % KT == 0 && K1 % KT == 0;
+    const bool full = vec && g.bufok && m0 + BM <= g.M && n0 + BNT <= g.N && K0 % KT == 0 && K1 % KT == 0;
+    // buffer resources of both segments' operands and this thread's offsets (the segments
+    // share lda and ldb when bufok is set)
+    const __amdgpu_buffer_rsrc_t rA0 = operand_rsrc(A0), rA1 = operand_rsrc(A1);
+    const __amdgpu_buffer_rsrc_t rB0 = operand_rsrc(B0), rB1 = operand_rsrc(B1);
+    const TileOffsets<A_KM, BM> offA = tile_offsets<A_KM, BM>(lda0, m0);
+    const TileOffsets<B_KM, BNT> offB = tile_offsets<B_KM, BNT>(ldb0, n0);
 
     floatx16 acc[2][NJ];
 #pragma unroll
@@ -175,9 +212,15 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    Stage<BM> sa;
-    Stage<BNT> sb;
-    auto load = [&](int t, bool fast) {
+    // two register stages: the global loads of step t+2 are issued at step t, and the stage
+    // holding step t+1 (loaded at step t-1) goes to LDS at the end of step t, so a load has
+    // two steps of matrix-core work to arrive.  Loads and stores are unconditional (a step
+    // past the slice reloads its last step, whose data is never read) so that the compiler
+    // waits only for the older stage.
+    Stage<BM> sa[2];
+    Stage<BNT> sb[2];
+    auto load = [&](int p, int t, bool fast) {
+        t = t < t_end ? t : t_end - 1;
         const bool s1 = t >= steps0;
         const float* A = s1 ? A1 : A0;
         const float* B = s1 ? B1 : B0;
@@ -185,25 +228,27 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         const int K = s1 ? K1 : K0;
         const int k0 = (s1 ? t - steps0 : t) * KT;
         if (fast) {
-            load_tile_full<A_KM, BM>(sa, A, lda, m0, k0);
-            load_tile_full<B_KM, BNT>(sb, B, ldb, n0, k0);
+            const uint32_t sa_off = (uint32_t)((A_KM ? (long)k0 : (long)k0 * lda0) * 4);
+            const uint32_t sb_off = (uint32_t)((B_KM ? (long)k0 : (long)k0 * ldb0) * 4);
+            load_tile_full<A_KM, BM>(sa[p], s1 ? rA1 : rA0, offA, sa_off);
+            load_tile_full<B_KM, BNT>(sb[p], s1 ? rB1 : rB0, offB, sb_off);
         } else {
-            load_tile<A_KM, BM>(sa, A, lda, g.M, K, m0, k0, vec);
-            load_tile<B_KM, BNT>(sb, B, ldb, g.N, K, n0, k0, vec);
+            load_tile<A_KM, BM>(sa[p], A, lda, g.M, K, m0, k0, vec);
+            load_tile<B_KM, BNT>(sb[p], B, ldb, g.N, K, n0, k0, vec);
         }
     };
     auto mainloop = [&](auto fast_tag) {
         constexpr bool FAST = decltype(fast_tag)::value;
-        if (t_begin < t_end) {
-            load(t_begin, FAST);
-            store_tile<A_KM, BM, LDA_S>(sa, As[0]);
-            store_tile<B_KM, BNT, LDB_S>(sb, Bs[0]);
-        }
+        if (t_begin >= t_end) return;
+        load(0, t_begin, FAST);
+        load(1, t_begin + 1, FAST);
+        store_tile<A_KM, BM, LDA_S>(sa[0], As[0]);
+        store_tile<B_KM, BNT, LDB_S>(sb[0], Bs[0]);
         __syncthreads();
-        for (int t = t_begin; t < t_end; ++t) {
-            const int cur = (t - t_begin) & 1;
-            const bool more = t + 1 < t_end;
-            if (more) load(t + 1, FAST);
+        // step t with p = (t - t_begin) % 2: LDS buffer p and register stage p
+        auto step = [&](int t, auto p_tag) {
+            constexpr int cur = decltype(p_tag)::value;
+            load(cur, t + 2, FAST);
             const float* A_ = As[cur];
             const float* B_ = Bs[cur];
             // every fragment of the stage first (the LDS reads overlap each other), then the MFMAs
@@ -226,11 +271,13 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 #pragma unroll
                     for (int j = 0; j < NJ; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[ks][j], a[ks][i], acc[i][j], 0, 0, 0);
-            if (more) {
-                store_tile<A_KM, BM, LDA_S>(sa, As[cur ^ 1]);
-                store_tile<B_KM, BNT, LDB_S>(sb, Bs[cur ^ 1]);
-            }
+            store_tile<A_KM, BM, LDA_S>(sa[cur ^ 1], As[cur ^ 1]);
+            store_tile<B_KM, BNT, LDB_S>(sb[cur ^ 1], Bs[cur ^ 1]);
             __syncthreads();
+        };
+        for (int t = t_begin; t < t_end; t += 2) {
+            step(t, std::integral_constant<int, 0>{});
+            if (t + 1 < t_end) step(t + 1, std::integral_constant<int, 1>{});
         }
     };
     if (full) mainloop(std::true_type{});
@@ -287,6 +334,7 @@ __global__ __launch_bounds__(NT) void splitk_reduce_kernel(const float* __restri
     const long mn = (long)M * N;
     if (q >= mn) return;
     float s = part[q];
+#pragma unroll 4
     for (int z = 1; z < ksplit; ++z) s += part[q + z * mn];
     const int m = (int)(q % M), n = (int)(q / M);
     epi(m, n, s, epi.load(m, n));
@@ -333,6 +381,14 @@ hipError_t launch(Args g, Epi epi, hipStream_t stream, const Plan& p) {
     }
     g.ksplit = p.ksplit;
     if (p.ksplit > 1 && !g.part) return hipErrorInvalidValue;
+    // byte extent of each operand: A spans K columns of lda (A_KM = false) or M columns,
+    // B spans N columns of ldb (B_KM = true) or K columns
+    g.bufok = g.nseg == 1 || (g.seg[0].lda == g.seg[1].lda && g.seg[0].ldb == g.seg[1].ldb);
+    for (int s = 0; s < g.nseg; ++s) {
+        const double ea = (double)g.seg[s].lda * (A_KM ? g.M : g.seg[s].K) * 4.0;
+        const double eb = (double)g.seg[s].ldb * (B_KM ? g.N : g.seg[s].K) * 4.0;
+        g.bufok = g.bufok && ea < 2147483648.0 && eb < 2147483648.0;
+    }
     if (p.bnt == 128) {
         dim3 grid((g.M + BM - 1) / BM, (g.N + 127) / 128, p.ksplit);
         gemm_kernel<A_KM, B_KM, 128, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);

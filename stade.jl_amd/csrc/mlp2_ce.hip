@@ -85,10 +85,26 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.H, O = a.O;
     if constexpr (LDSW) {
-        for (int q = threadIdx.x; q < O * H; q += HNT) {
-            const int j = q / O, o = q - j * O;
-            w2s[j * OP + o] = a.w2[q];
-            if (MODE != ADJ) w2s[HLDS * OP + j * OP + o] = a.w2d[q];
+        // CB loads in flight per thread, then their LDS stores (a load-store loop would wait
+        // out one global-memory round trip per element)
+        constexpr int CB = 8;
+        for (int q0 = 0; q0 < O * H; q0 += HNT * CB) {
+            float v[CB], vd[CB];
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const int q = q0 + c * HNT + threadIdx.x;
+                v[c] = q < O * H ? a.w2[q] : 0.f;
+                vd[c] = (MODE != ADJ && q < O * H) ? a.w2d[q] : 0.f;
+            }
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const int q = q0 + c * HNT + threadIdx.x;
+                if (q < O * H) {
+                    const int j = q / O, o = q - j * O;
+                    w2s[j * OP + o] = v[c];
+                    if (MODE != ADJ) w2s[HLDS * OP + j * OP + o] = vd[c];
+                }
+            }
         }
         __syncthreads();
     }
@@ -102,13 +118,24 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
     const float lbd = (MODE == HVP) ? a.lossbd[0] : 0.f;
     for (int s = blockIdx.x * (HNT / 64) + wave; s < a.B; s += gridDim.x * (HNT / 64)) {
         const long hs = (long)s * H, os = (long)s * O;
-        float hj[HPL], hdj[HPL];
+        // every global read of the sample first: h1 (+ h1d), then h1b (+ h1bd), zb (+ zbd) and
+        // the label, so one memory round trip covers them
+        float hj[HPL], hdj[HPL], hbj[HPL], hbdj[HPL];
 #pragma unroll
         for (int q = 0; q < HPL; ++q) {
             const int j = lane + 64 * q;
             hj[q] = j < H ? a.h1[hs + j] : 0.f;
             hdj[q] = (MODE != ADJ && j < H) ? a.h1d[hs + j] : 0.f;
         }
+#pragma unroll
+        for (int q = 0; q < HPL; ++q) {
+            const int j = lane + 64 * q;
+            hbj[q] = (MODE != TAN && j < H) ? a.h1b[hs + j] : 0.f;
+            hbdj[q] = (MODE == HVP && j < H) ? a.h1bd[hs + j] : 0.f;
+        }
+        const float zb_l = (MODE != TAN && lane < O) ? a.zb[os + lane] : 0.f;
+        const float zbd_l = (MODE == HVP && lane < O) ? a.zbd[os + lane] : 0.f;
+        const int64_t lab_s = a.lab[s];
         // z = b2 + W2 h1 (and zd = b2d + W2d h1 + W2 h1d)
         float z[OMAX], zd[OMAX];
 #pragma unroll
@@ -146,7 +173,7 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
                 se = se + e[o];
             }
         }
-        int l = (int)a.lab[s] - 1;
+        int l = (int)lab_s - 1;
         if (l < 0 || l >= O) {
             if (lane == 0) atomicExch(a.err, 1);
             l = -1;
@@ -181,11 +208,11 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
         for (int o = 0; o < OMAX; ++o) {
             d2[o] = d2d[o] = 0.f;
             if (o < O) {
-                float t = a.zb[os + o];
+                float t = __shfl(zb_l, o, 64);
                 if (o == l) t = t + -lb;
                 d2[o] = t + e[o] * seb;
                 if (MODE == HVP) {
-                    float td = a.zbd[os + o];
+                    float td = __shfl(zbd_l, o, 64);
                     if (o == l) td = td + -lbd;
                     d2d[o] = td + (seb * (e[o] * zd[o]) + e[o] * sebd);
                 }
@@ -208,8 +235,8 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
         for (int q = 0; q < HPL; ++q) {
             const int j = lane + 64 * q;
             if (j >= H) continue;
-            float t = a.h1b[hs + j];
-            float td = (MODE == HVP) ? a.h1bd[hs + j] : 0.f;
+            float t = hbj[q];
+            float td = hbdj[q];
 #pragma unroll
             for (int o = OMAX - 1; o >= 0; --o) {
                 if (o < O) {
@@ -234,10 +261,306 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
+// head, split form (i_h <= 1024, the form the launcher uses there), first half: z = W2 h1 + b2,
+// the cross-entropy, d2 = dloss/dz and the zb reset, per sample; the second half (D1, h1b
+// reset) is fused with the column sums in d1sum_kernel.  A 256-thread block stages W2 (+ W2d)
+// in LDS once as [j][o] rows of OP floats, zero-padded to OMAX outputs and 64 * HPL columns;
+// each wave takes SPW samples at a time with their reads of h1 (+ h1d) issued together, and
+// one LDS read of a weight serves the SPW samples.  Padded outputs carry zeros, so the o loops
+// have no branches.  Per sample the arithmetic is that of head_kernel, in the same order.
+// ---------------------------------------------------------------------------------------
+constexpr int H4NT = 256;
+constexpr int SC = 128;  // samples per chunk of the column sums
+
+template <int MODE, int HPL, int SPW>
+__global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
+    constexpr int NW = MODE == ADJ ? 1 : 2;
+    constexpr int JR = 64 * HPL;
+    __shared__ float w2s[NW * JR * OP];
+    __shared__ double red[16 * 2];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.H, O = a.O, B = a.B;
+    {
+        // padded element q = (j, o) with o fastest; CB loads in flight per thread
+        constexpr int CB = 8, TOTAL = JR * OMAX;
+        for (int q0 = 0; q0 < TOTAL; q0 += H4NT * CB) {
+            float v[CB], vd[CB];
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const int q = q0 + c * H4NT + threadIdx.x;
+                const int j = q / OMAX, o = q % OMAX;
+                const bool in = q < TOTAL && j < H && o < O;
+                v[c] = in ? a.w2[(long)j * O + o] : 0.f;
+                vd[c] = (MODE != ADJ && in) ? a.w2d[(long)j * O + o] : 0.f;
+            }
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const int q = q0 + c * H4NT + threadIdx.x;
+                if (q < TOTAL) {
+                    const int j = q / OMAX, o = q % OMAX;
+                    w2s[j * OP + o] = v[c];
+                    if (MODE != ADJ) w2s[JR * OP + j * OP + o] = vd[c];
+                }
+            }
+        }
+    }
+    const float lb = (MODE == TAN) ? 0.f : a.lossb[0];
+    const float lbd = (MODE == HVP) ? a.lossbd[0] : 0.f;
+    double acc[2] = {0.0, 0.0};  // loss, lossd
+    __syncthreads();
+    const float* W2s = w2s;
+    const float* W2ds = w2s + (NW - 1) * JR * OP;
+    const int nw = gridDim.x * (H4NT / 64);
+    for (int s0 = (blockIdx.x * (H4NT / 64) + wave) * SPW; s0 < B; s0 += nw * SPW) {
+        // every global read of the SPW samples first (a sample past B re-reads sample B-1)
+        float h[SPW][HPL], hd[SPW][HPL];
+        float zb_l[SPW], zbd_l[SPW];
+        int64_t lab[SPW];
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) {
+            const int s = min(s0 + i, B - 1);
+            const long hs = (long)s * H, os = (long)s * O;
+#pragma unroll
+            for (int q = 0; q < HPL; ++q) {
+                const int j = lane + 64 * q, jc = min(j, H - 1);
+                const float x = a.h1[hs + jc];
+                h[i][q] = j < H ? x : 0.f;
+                if (MODE != ADJ) {
+                    const float xd = a.h1d[hs + jc];
+                    hd[i][q] = j < H ? xd : 0.f;
+                }
+            }
+            const int oc = min(lane, O - 1);
+            zb_l[i] = (MODE != TAN) ? a.zb[os + oc] : 0.f;
+            zbd_l[i] = (MODE == HVP) ? a.zbd[os + oc] : 0.f;
+            lab[i] = a.lab[s];
+        }
+        // z = b2 + W2 h1 (zd = b2d + W2d h1 + W2 h1d): lane partial sums over its columns
+        float z[SPW][OMAX], zd[SPW][OMAX];
+#pragma unroll
+        for (int i = 0; i < SPW; ++i)
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) z[i][o] = zd[i][o] = 0.f;
+#pragma unroll
+        for (int q = 0; q < HPL; ++q) {
+            const int row = (lane + 64 * q) * OP;
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                const float w = W2s[row + o];
+                const float wd = (MODE != ADJ) ? W2ds[row + o] : 0.f;
+#pragma unroll
+                for (int i = 0; i < SPW; ++i) {
+                    z[i][o] += w * h[i][q];
+                    if (MODE != ADJ) zd[i][o] += h[i][q] * wd + w * hd[i][q];
+                }
+            }
+            // one column block's weights live at a time (the scheduler would otherwise hoist
+            // every LDS read of the loop)
+            asm volatile("" ::: "memory");
+        }
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) {
+            const int s = s0 + i;
+            const bool live = s < B;  // uniform over the wave
+            const long os = (long)min(s, B - 1) * O;
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                if (o < O) {
+                    z[i][o] = a.b2[o] + wave_sum(z[i][o]);
+                    if (MODE != ADJ) zd[i][o] = a.b2d[o] + wave_sum(zd[i][o]);
+                }
+            }
+            // softmax cross-entropy: loss += log(se) - z[l]
+            float se = 0.f, sed = 0.f, e[OMAX];
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                e[o] = 0.f;
+                if (o < O) {
+                    e[o] = expf(z[i][o]);
+                    if (MODE != ADJ) sed = sed + e[o] * zd[i][o];
+                    se = se + e[o];
+                }
+            }
+            int l = (int)lab[i] - 1;
+            if (l < 0 || l >= O) {
+                if (live && lane == 0) atomicExch(a.err, 1);
+                l = -1;
+            }
+            float zl = 0.f, zdl = 0.f, zo = 0.f, zdo = 0.f;
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                if (o == l) {
+                    zl = z[i][o];
+                    zdl = zd[i][o];
+                }
+                if (o == lane) {
+                    zo = z[i][o];
+                    zdo = zd[i][o];
+                }
+            }
+            if (live && lane == 0 && l >= 0) {
+                acc[0] += (double)(logf(se) - zl);
+                if (MODE != ADJ) acc[1] += (double)((1.0f / se) * sed + -zdl);
+            }
+            if (live && lane < O) {
+                if (MODE != ADJ) a.zd[os + lane] = zdo;
+                a.z[os + lane] = zo;
+            }
+            if (MODE == TAN) continue;
+            // reverse of the loss: d2 = zb + [o == l](-lb) + exp(z) seb, seb = (1 / se) lb
+            const float seb = (1.0f / se) * lb;
+            const float sebd = (MODE == HVP) ? (lb * (-(1.0f / (se * se)) * sed) + (1.0f / se) * lbd) : 0.f;
+            float d2o = 0.f, d2do = 0.f;
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                if (o < O) {
+                    float t = __shfl(zb_l[i], o, 64);
+                    if (o == l) t = t + -lb;
+                    const float d2 = t + e[o] * seb;
+                    float d2d = 0.f;
+                    if (MODE == HVP) {
+                        float td = __shfl(zbd_l[i], o, 64);
+                        if (o == l) td = td + -lbd;
+                        d2d = td + (seb * (e[o] * zd[i][o]) + e[o] * sebd);
+                    }
+                    if (o == lane) {
+                        d2o = d2;
+                        d2do = d2d;
+                    }
+                }
+            }
+            if (live && lane < O) {
+                a.zb[os + lane] = 0.f;
+                a.D2[os + lane] = d2o;
+                if (MODE == HVP) {
+                    a.zbd[os + lane] = 0.f;
+                    a.D2d[os + lane] = d2do;
+                }
+            }
+        }
+    }
+    block_partials<2>(acc, red, a.partials);
+}
+
+// ---------------------------------------------------------------------------------------
+// second half of the split head fused with the column sums (i_h <= 1024): per chunk of SC
+// samples and 64 columns j,
+//   d1 = (1 - h1^2) (h1b + sum_o w2[o, j] d2[o]) (o descending, as the generated loop), h1b = 0
+//   (HVP: d1d, h1bd = 0), and the chunk partials of W2b += d2 h1', b1b += sum_s d1 (+ W2bd,
+//   b1bd) and of b2b (+ b2bd), in colsum_kernel's layout and summation order.
+// A thread owns column j (its W2 column in registers) and the samples s0 + sl + 4 k.
+// ---------------------------------------------------------------------------------------
+struct D1Args {
+    const float *h1, *h1b_in, *w2, *D2, *h1d, *w2d, *D2d;
+    float *h1b, *D1, *h1bd, *D1d;
+    float* part;   // [chunk][2 * (O + 1)][H]
+    float* part2;  // [chunk][2 * OMAX]
+    int B, H, O;
+};
+
+template <int MODE>
+__global__ __launch_bounds__(NT) void d1sum_kernel(D1Args a) {
+    constexpr int NR = 2 * (OMAX + 1);
+    constexpr bool HV = MODE == HVP;
+    __shared__ float d2s[SC * OMAX];               // [s][o], zero past O
+    __shared__ float d2ds[HV ? SC * OMAX : 1];
+    __shared__ float red[4][NR][64];
+    const int jl = threadIdx.x & 63, sl = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + jl, c = blockIdx.y;
+    const int s0 = c * SC, s1 = min(a.B, s0 + SC), O = a.O, H = a.H;
+    const int jc = min(j, H - 1);
+    {
+        constexpr int CB = SC * OMAX / NT;
+        float v[CB], vd[CB];
+#pragma unroll
+        for (int k = 0; k < CB; ++k) {
+            const int q = k * NT + threadIdx.x;
+            const int ss = q / OMAX, o = q % OMAX;
+            const bool in = s0 + ss < s1 && o < O;
+            v[k] = in ? a.D2[(long)(s0 + ss) * O + o] : 0.f;
+            vd[k] = (HV && in) ? a.D2d[(long)(s0 + ss) * O + o] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < CB; ++k) {
+            d2s[k * NT + threadIdx.x] = v[k];
+            if (HV) d2ds[k * NT + threadIdx.x] = vd[k];
+        }
+    }
+    float w[OMAX], wd[OMAX];
+#pragma unroll
+    for (int o = 0; o < OMAX; ++o) {
+        w[o] = (j < H && o < O) ? a.w2[(long)jc * O + o] : 0.f;
+        wd[o] = (HV && j < H && o < O) ? a.w2d[(long)jc * O + o] : 0.f;
+    }
+    __syncthreads();
+    // b2b (+ b2bd) partials of the chunk: the column-independent sums of d2 over samples
+    if (blockIdx.x == 0 && threadIdx.x < 2 * OMAX) {
+        const int o = threadIdx.x % OMAX;
+        const bool dd = threadIdx.x >= OMAX;
+        double t = 0.0;
+        if (o < O && (!dd || HV))
+            for (int q = 0; q < s1 - s0; ++q) t += (double)(dd ? d2ds[q * OMAX + o] : d2s[q * OMAX + o]);
+        a.part2[(long)c * 2 * OMAX + threadIdx.x] = (float)t;
+    }
+    float wacc[OMAX], wdacc[OMAX], bsum = 0.f, bsumd = 0.f;
+#pragma unroll
+    for (int o = 0; o < OMAX; ++o) wacc[o] = wdacc[o] = 0.f;
+#pragma unroll 4
+    for (int s = s0 + sl; s < s1; s += 4) {
+        const long k = (long)s * H + jc;
+        const float h = a.h1[k];
+        const float hb = a.h1b_in[k];
+        const float hd = HV ? a.h1d[k] : 0.f;
+        const float hbd = HV ? a.h1bd[k] : 0.f;
+        const float* d2 = d2s + (s - s0) * OMAX;
+        const float* d2d = d2ds + (HV ? (s - s0) * OMAX : 0);
+        float t = hb, td = hbd;
+#pragma unroll
+        for (int o = OMAX - 1; o >= 0; --o) {
+            if (HV) td = td + (d2[o] * wd[o] + w[o] * d2d[o]);
+            t = t + w[o] * d2[o];
+        }
+        const float g = 1.0f - h * h;
+        const float d1 = g * t;
+        const float d1d = HV ? t * -((2.0f * h) * hd) + g * td : 0.f;
+        if (j < H) {
+            a.h1b[k] = 0.f;
+            a.D1[k] = d1;
+            if (HV) {
+                a.h1bd[k] = 0.f;
+                a.D1d[k] = d1d;
+            }
+        }
+#pragma unroll
+        for (int o = 0; o < OMAX; ++o) {
+            wacc[o] += h * d2[o];
+            if (HV) wdacc[o] += d2[o] * hd + h * d2d[o];
+        }
+        bsum += d1;
+        if (HV) bsumd += d1d;
+    }
+#pragma unroll
+    for (int o = 0; o < OMAX; ++o) {
+        red[sl][o][jl] = wacc[o];
+        red[sl][OMAX + 1 + o][jl] = wdacc[o];
+    }
+    red[sl][OMAX][jl] = bsum;
+    red[sl][2 * OMAX + 1][jl] = bsumd;
+    __syncthreads();
+    if (j >= H) return;
+    float* p = a.part + (long)c * 2 * (O + 1) * H;
+    for (int r = sl; r < 2 * (O + 1); r += 4) {
+        if (!HV && r > O) break;
+        const int src = r < O ? r : (r == O ? OMAX : (r < 2 * O + 1 ? OMAX + 1 + (r - O - 1) : 2 * OMAX + 1));
+        const float v = ((red[0][src][jl] + red[1][src][jl]) + red[2][src][jl]) + red[3][src][jl];
+        p[(long)r * H + j] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // colsum: per chunk of samples, W2b[o, j] += sum_s d2[o, s] h1[j, s], b1b[j] += sum_s d1[j, s]
 // (HVP: W2bd += d2 h1d + h1 d2d, b1bd += d1d); chunk partials reduced in order by final_kernel
 // ---------------------------------------------------------------------------------------
-constexpr int SC = 128;  // samples per chunk
 struct ColArgs {
     const float *h1, *D1, *D2, *h1d, *D1d, *D2d;
     float* part;   // [chunk][2 * (O + 1)][H]
@@ -255,9 +578,23 @@ __global__ __launch_bounds__(NT) void colsum_kernel(ColArgs a) {
     const int jl = threadIdx.x & 63, sl = threadIdx.x >> 6;
     const int j = blockIdx.x * 64 + jl, c = blockIdx.y;
     const int s0 = c * SC, s1 = min(a.B, s0 + SC), O = a.O, H = a.H;
-    for (int q = threadIdx.x; q < (s1 - s0) * O; q += NT) {
-        d2s[q] = a.D2[(long)s0 * O + q];
-        if (MODE == HVP) d2ds[q] = a.D2d[(long)s0 * O + q];
+    {
+        constexpr int CB = (SC * OMAX + NT - 1) / NT;  // every element of the chunk in one round trip
+        float v[CB], vd[CB];
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+            const int q = c * NT + threadIdx.x;
+            v[c] = q < (s1 - s0) * O ? a.D2[(long)s0 * O + q] : 0.f;
+            vd[c] = (MODE == HVP && q < (s1 - s0) * O) ? a.D2d[(long)s0 * O + q] : 0.f;
+        }
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+            const int q = c * NT + threadIdx.x;
+            if (q < (s1 - s0) * O) {
+                d2s[q] = v[c];
+                if (MODE == HVP) d2ds[q] = vd[c];
+            }
+        }
     }
     __syncthreads();
     // b2b (+ b2bd) partials of the chunk: the column-independent sums of d2 over samples
@@ -273,6 +610,8 @@ __global__ __launch_bounds__(NT) void colsum_kernel(ColArgs a) {
 #pragma unroll
     for (int o = 0; o < OMAX; ++o) w[o] = wd[o] = 0.f;
     if (j < H) {
+        // 8 samples' loads in flight (the per-sample sums keep their order)
+#pragma unroll 8
         for (int s = s0 + sl; s < s1; s += 4) {
             const long k = (long)s * H + j;
             const float h = a.h1[k];
@@ -354,6 +693,7 @@ __global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
     if (q >= (long)rows * H) return;
     const int r = (int)(q / H), j = (int)(q % H);
     float s = 0.f;
+#pragma unroll 8
     for (int c = 0; c < f.nchunks; ++c) s += f.cpart[(long)c * 2 * (O + 1) * H + (long)r * H + j];
     if (r < O) f.w2b[(long)j * O + r] = f.w2b[(long)j * O + r] + s;
     else if (r == O) f.b1b[j] = f.b1b[j] + s;
@@ -459,14 +799,22 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     h.h1 = p.h1; h.w2 = p.w2; h.b2 = p.b2; h.lossb = p.lossb; h.z = p.z; h.zb = p.zb; h.h1b = p.h1b; h.D1 = D1; h.D2 = D2;
     h.h1d = p.h1d; h.w2d = p.w2d; h.b2d = p.b2d; h.lossbd = p.lossbd; h.zd = p.zd; h.zbd = p.zbd; h.h1bd = p.h1bd;
     h.D1d = D1d; h.D2d = D2d; h.lab = p.lab; h.B = B; h.H = H; h.O = O; h.partials = ws->partials; h.err = err;
-    const unsigned hb = (unsigned)((B + 16 - 1) / 16);  // 8 waves, 2 samples per wave
+    // i_h <= 1024: the batched head, SPW samples per wave, at most one block per CU (each
+    // block stages W2 once); wider layers: one wave per sample, 8 waves and 16 samples a block
+    constexpr int SPW = MODE == ADJ ? 4 : 1;
+    const unsigned hb = H <= 1024 ? (unsigned)std::min<long>(((long)B + SPW * 4 - 1) / (SPW * 4), cus)
+                                  : (unsigned)((B + 16 - 1) / 16);
     STADE_TIMED("mlp_head", stream, {
-        if (H <= 256) launch_head<MODE, 4>(h, hb, stream);
-        else if (H <= 1024) launch_head<MODE, 16>(h, hb, stream);
+        if (H <= 256) head4_kernel<MODE, 4, SPW><<<hb, H4NT, 0, stream>>>(h);
+        else if (H <= 1024) head4_kernel<MODE, 16, SPW><<<hb, H4NT, 0, stream>>>(h);
         else launch_head<MODE, 32>(h, hb, stream);
     });
     STADE_LAUNCHED("mlp head_kernel");
-    if (MODE != TAN) {
+    if (MODE != TAN && H <= 1024 && H > 0) {
+        D1Args c{p.h1, p.h1b, p.w2, D2, p.h1d, p.w2d, D2d, p.h1b, D1, p.h1bd, D1d, cpart, c2part, B, H, O};
+        STADE_TIMED("mlp_colsum", stream, d1sum_kernel<MODE><<<dim3((H + 63) / 64, nchunks), NT, 0, stream>>>(c));
+        STADE_LAUNCHED("mlp d1sum_kernel");
+    } else if (MODE != TAN) {
         // (one column block even when i_h = 0: its first block forms the b2b chunk sums)
         ColArgs c{p.h1, D1, D2, p.h1d, D1d, D2d, cpart, c2part, B, H, O};
         STADE_TIMED("mlp_colsum", stream,

@@ -3,7 +3,9 @@
 the truth rule (fp64 oracle) where the two differ by more.
 
 Sizes cover tiny and odd widths, widths that are not multiples of the 128 x 128 matrix-core
-tile, and the benchmark widths 784 -> 1024 -> 10 on a reduced batch."""
+tile, an odd batch with the widest output layer (16) and a hidden width that is not a multiple
+of 64, a hidden layer wider than 1024 (the per-sample head), and the benchmark widths 784 ->
+1024 -> 10 on a reduced batch."""
 import numpy as np
 import pytest
 
@@ -11,7 +13,8 @@ from helpers import run_parity
 
 pytestmark = pytest.mark.gpu
 
-SIZES = [(8, 5, 7, 3), (64, 40, 48, 10), (130, 129, 131, 10), (256, 784, 1024, 10)]
+SIZES = [(8, 5, 7, 3), (64, 40, 48, 10), (130, 129, 131, 10), (33, 17, 300, 16), (16, 8, 1100, 4),
+         (256, 784, 1024, 10)]
 
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
