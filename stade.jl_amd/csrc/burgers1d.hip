@@ -19,7 +19,9 @@
 //   * backward init: w = unb + (ub + (2 u_T) lossb), loss += sum u_T^2, unb = 0 (pointwise).
 //   * backward chunk: K steps of the transposed stencil in gathered (owner-computes) form,
 //     reading tape rows; the scalar shadows of the two coefficients are per-thread sums over
-//     owned cells and steps, then a deterministic grid sum.
+//     owned cells and steps, then a deterministic grid sum.  Full chunks (K = 32 steps) keep
+//     the state in registers with DPP neighbours (bwd_reg_kernel); a shorter last chunk uses
+//     the LDS form (bwd_kernel).
 #include "internal.hpp"
 #include "../../include/stade_hip.h"
 
@@ -278,70 +280,166 @@ __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win
     bwd_finish<HV>(W[cur], WD[HV ? cur : 0], vout, voutd, x0, nk, own, acc, red, partials);
 }
 
-// a full chunk of KMAX steps: the tape rows of the next PD steps are in flight while a step
-// is computed (the generic kernel above fetches one step ahead and measured 3.4 TB/s).  Every load is unconditional (positions past the extended region read column
-// 0; the last PD steps re-read the chunk's last row, an L2 hit), so the compiler can count the
-// loads still in flight instead of waiting for all of them.
-// PD: 4 rows ahead for the adjoint; 2 for the HVP, whose rows are twice as wide in registers
+// ---------------------------------------------------------------------------------------
+// A full chunk of KMAX steps with the state in registers.  Thread t holds positions
+// e = t + i * BNT (slot i) of the extended region; its neighbours e -/+ 1 are the adjacent
+// lanes of the same slot, taken by DPP wavefront shifts.  Only a wave's two end lanes need a
+// value from another wave (lane 0: the previous wave's lane 63, or slot i-1's last lane for
+// wave 0; lane 63: the next wave's lane 0, or slot i+1's first lane for the last wave): every
+// wave publishes its end lanes' tape value and adjoint state in a small LDS array, double
+// buffered by step, so a step needs one barrier and almost no LDS traffic.  The tape row of
+// step k+1 is published at the end of step k, so the prefetch ring of PD rows keeps PD - 1
+// rows in flight.  The arithmetic per position is bwd_step's, in the same order.
+// ---------------------------------------------------------------------------------------
 template <bool HV, int S, int PD>
-__global__ __launch_bounds__(BNT) void bwd_full_kernel(const double* __restrict__ win, const double* __restrict__ wind,
-                                                       double* __restrict__ vout, double* __restrict__ voutd,
-                                                       const double* __restrict__ tape, const double* __restrict__ taped,
-                                                       int n, int64_t t_hi, Coef c, double* partials) {
+__global__ __launch_bounds__(BNT) void bwd_reg_kernel(const double* __restrict__ win, const double* __restrict__ wind,
+                                                      double* __restrict__ vout, double* __restrict__ voutd,
+                                                      const double* __restrict__ tape, const double* __restrict__ taped, int n,
+                                                      int64_t t_hi, Coef c, double* partials) {
+    constexpr int nk = KMAX, L = S + 2 * KMAX;
+    constexpr int M = (L + BNT - 1) / BNT, NWV = BNT / 64;
+    constexpr int NA = HV ? 4 : 2;  // exchanged arrays: u, w (+ ud, wd)
     static_assert(KMAX % PD == 0, "full chunks are whole rounds of the prefetch ring");
-    constexpr int nk = KMAX;
-    constexpr int L = S + 2 * KMAX, len = L;
-    constexpr int M = (L + BNT - 1) / BNT;
-    __shared__ double W[2][L];
-    __shared__ double U[L];
-    __shared__ double WD[HV ? 2 : 1][HV ? L : 1];
-    __shared__ double UD[HV ? L : 1];
+    static_assert(L - (M - 1) * BNT <= 64, "the last slot belongs to wave 0 alone");
+    __shared__ double edge[2][NA][M][NWV][2];
     __shared__ double red[16 * 4];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int x0 = blockIdx.x * S;
     const int own = min(S, n - x0);
-    int xcol[M];
+    // columns, ownership, and where an end lane finds its outside neighbour (slot, wave, side)
+    int xc[M], eo[M];
+    bool owned[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) {
         const int e = threadIdx.x + i * BNT;
-        xcol[i] = e < len ? wrapn(x0 - nk + e, n) : 0;
-        if (e < len) {
-            W[0][e] = win[xcol[i]];
-            if (HV) WD[0][e] = wind[xcol[i]];
+        xc[i] = wrapn(x0 - nk + min(e, L - 1), n);
+        owned[i] = e >= nk && e < nk + own;
+        int si, sv, ss;
+        if (lane == 0) {
+            ss = 1;
+            sv = wave > 0 ? wave - 1 : NWV - 1;
+            si = wave > 0 ? i : max(i - 1, 0);
+        } else {
+            ss = 0;
+            sv = wave < NWV - 1 ? wave + 1 : 0;
+            si = wave < NWV - 1 ? i : min(i + 1, M - 1);
         }
+        eo[i] = (si * NWV + sv) * 2 + ss;
     }
-    double pre[PD][M], pred[HV ? PD : 1][M];
+    auto edge_at = [&](int buf, int a, int i) { return (&edge[buf][a][0][0][0])[eo[i]]; };
+    double w[M], wd[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        w[i] = win[xc[i]];
+        wd[i] = HV ? wind[xc[i]] : 0.0;
+    }
+    double pu[PD][M], pud[HV ? PD : 1][M];
     auto fetch = [&](int slot, int k) {
         const size_t row = (size_t)(t_hi - (k < nk ? k : nk - 1)) * (size_t)n;
 #pragma unroll
         for (int i = 0; i < M; ++i) {
-            pre[slot][i] = tape[row + xcol[i]];
-            if constexpr (HV) pred[slot][i] = taped[row + xcol[i]];
+            pu[slot][i] = tape[row + xc[i]];
+            if constexpr (HV) pud[slot][i] = taped[row + xc[i]];
+        }
+    };
+    // the end lanes' adjoint state and the tape row of the next step (ring slot `nxt`)
+    auto publish = [&](int buf, int nxt) {
+        if (lane == 0 || lane == 63) {
+            const int side = lane == 63;
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                edge[buf][0][i][wave][side] = pu[nxt][i];
+                edge[buf][1][i][wave][side] = w[i];
+                if constexpr (HV) {
+                    edge[buf][2][i][wave][side] = pud[nxt][i];
+                    edge[buf][3][i][wave][side] = wd[i];
+                }
+            }
         }
     };
 #pragma unroll
     for (int j = 0; j < PD; ++j) fetch(j, j);
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    int cur = 0;
+    publish(0, 0);
+    __syncthreads();
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};  // cadvb, cdifb, cadvbd, cdifbd
     for (int k0 = 0; k0 < nk; k0 += PD) {
 #pragma unroll
         for (int j = 0; j < PD; ++j) {
-            const int k = k0 + j;
+            const int k = k0 + j, buf = k & 1;
+            double wn[M], wdn[M];
 #pragma unroll
             for (int i = 0; i < M; ++i) {
-                const int e = threadIdx.x + i * BNT;
-                if (e < len) {
-                    U[e] = pre[j][i];
-                    if constexpr (HV) UD[e] = pred[j][i];
+                wn[i] = w[i];
+                wdn[i] = wd[i];
+                if (i == M - 1 && wave != 0) continue;  // past the extended region (uniform)
+                const double uc = pu[j][i], eu = edge_at(buf, 0, i);
+                const double um1 = from_west(uc, eu), up1 = from_east(uc, eu);
+                const double wc = w[i], ew = edge_at(buf, 1, i);
+                const double wm = from_west(wc, ew), wp = from_east(wc, ew);
+                // cell e+1 -> west neighbour e:  B = -(c5 * c4), C = cdif * w
+                const double c4p = -wp, c5p = c.cadv * up1;
+                const double Bp = -(c5p * c4p), Cp = c.cdif * wp;
+                // cell e-1 -> east neighbour e: A = c5 * c4
+                const double c4m = -wm, c5m = c.cadv * um1;
+                const double Am = c5m * c4m, Cm = c.cdif * wm;
+                // own: ucb = ((w + (cadv * c3) * c4) + 2.0 * -(cdif * w))
+                const double c3 = up1 - um1, c4 = -wc;
+                const double h7 = c.cadv * c3;
+                const double c6 = c.cdif * wc;
+                const double own_ = ((0.0 + wc) + h7 * c4) + 2.0 * -c6;
+                wn[i] = ((((0.0 + Bp) + Cp) + own_) + Am) + Cm;
+                if (owned[i]) {
+                    acc[0] += (uc * c3) * c4;
+                    acc[1] += ((up1 - 2.0 * uc) + um1) * wc;
+                }
+                if constexpr (HV) {
+                    const double dc = pud[j][i], eud = edge_at(buf, 2, i);
+                    const double dm1 = from_west(dc, eud), dp1 = from_east(dc, eud);
+                    const double wdc = wd[i], ewd = edge_at(buf, 3, i);
+                    const double wdm = from_west(wdc, ewd), wdp = from_east(wdc, ewd);
+                    const double c4pd = -wdp, c5pd = up1 * c.cadvd + c.cadv * dp1;
+                    const double h8p = c4p * c5pd + c5p * c4pd;
+                    const double Bpd = -h8p, Cpd = wp * c.cdifd + c.cdif * wdp;
+                    const double c4md = -wdm, c5md = um1 * c.cadvd + c.cadv * dm1;
+                    const double Amd = c4m * c5md + c5m * c4md, Cmd = wm * c.cdifd + c.cdif * wdm;
+                    const double c3d = dp1 + -dm1, c4d = -wdc;
+                    const double c6d = wc * c.cdifd + c.cdif * wdc;
+                    const double ownd = ((0.0 + wdc) + (c4 * (c3 * c.cadvd + c.cadv * c3d) + h7 * c4d)) + 2.0 * -c6d;
+                    wdn[i] = ((((0.0 + Bpd) + Cpd) + ownd) + Amd) + Cmd;
+                    if (owned[i]) {
+                        const double h6 = uc * c3;
+                        acc[2] += c4 * (c3 * dc + uc * c3d) + h6 * c4d;
+                        const double h9 = (up1 - 2.0 * uc) + um1;
+                        const double h9d = (dp1 + -(2.0 * dc)) + dm1;
+                        acc[3] += wc * h9d + h9 * wdc;
+                    }
                 }
             }
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                w[i] = wn[i];
+                wd[i] = wdn[i];
+            }
+            publish(buf ^ 1, (j + 1) % PD);
             fetch(j, k + PD);
             __syncthreads();
-            bwd_step<HV, M>(k, len, nk, own, U, UD, W[cur], WD[HV ? cur : 0], W[cur ^ 1], WD[HV ? cur ^ 1 : 0], c, acc);
-            __syncthreads();
-            cur ^= 1;
         }
     }
-    bwd_finish<HV>(W[cur], WD[HV ? cur : 0], vout, voutd, x0, nk, own, acc, red, partials);
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = threadIdx.x + i * BNT;
+        if (owned[i]) {
+            vout[x0 + e - nk] = w[i];
+            if (HV) voutd[x0 + e - nk] = wd[i];
+        }
+    }
+    if (HV) {
+        block_partials<4>(acc, red, partials);
+    } else {
+        double v[2] = {acc[0], acc[1]};
+        block_partials<2>(v, red, partials);
+    }
 }
 
 // second stage of the reverse sweep's sums: block 0 the loss (init kernel's partials),
@@ -479,7 +577,7 @@ int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, dou
         double* dd = last ? ubd : owd;
         if (nk == KMAX) {
             STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
-                        bwd_full_kernel<HV, S, HV ? 2 : 4><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, c,
+                        bwd_reg_kernel<HV, S, HV ? 2 : 4><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, c,
                                                                       pbwd + (size_t)chunk * nb * NV));
         } else {
             STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,

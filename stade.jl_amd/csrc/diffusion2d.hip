@@ -361,26 +361,6 @@ constexpr int WCH_HV = STADE_DIFF_WCH_HV;   // HVP
 constexpr int WD = STADE_DIFF_WD;
 constexpr int WD_HV = STADE_DIFF_WD_HV;
 static_assert(WS % WCH == 0 && WS % WCH_HV == 0, "the wave-strip path requires n % 64 == 0 to imply n % rows == 0");
-constexpr int kDppWaveShl1 = 0x130;   // lane l <- lane l+1
-constexpr int kDppWaveShr1 = 0x138;   // lane l <- lane l-1
-
-// v of the lane to the west (lane l-1); lane 0 gets `edge`
-__device__ __forceinline__ double from_west(double v, double edge) {
-    const int lo = __builtin_amdgcn_update_dpp(__double2loint(edge), __double2loint(v), kDppWaveShr1, 0xF, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(__double2hiint(edge), __double2hiint(v), kDppWaveShr1, 0xF, 0xF, false);
-    return __hiloint2double(hi, lo);
-}
-// v of the lane to the east (lane l+1); lane 63 gets `edge`
-__device__ __forceinline__ double from_east(double v, double edge) {
-    const int lo = __builtin_amdgcn_update_dpp(__double2loint(edge), __double2loint(v), kDppWaveShl1, 0xF, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(__double2hiint(edge), __double2hiint(v), kDppWaveShl1, 0xF, 0xF, false);
-    return __hiloint2double(hi, lo);
-}
-// v of lane l, in every lane
-__device__ __forceinline__ double lane_val(double v, int l) {
-    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), l), __builtin_amdgcn_readlane(__double2loint(v), l));
-}
-
 // the 5-point forms of step5 / step5d on values instead of LDS positions
 __device__ __forceinline__ double step5v(double up, double c, double dn, double w, double e) {
     double t = w + e;

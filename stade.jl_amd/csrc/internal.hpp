@@ -89,6 +89,27 @@ constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm:[2,3,0,1]
 constexpr int kDppRowRor4 = 0x124;    // row_ror:4
 constexpr int kDppRowRor8 = 0x128;    // row_ror:8
 
+// DPP wavefront shifts (gfx9 family): neighbour values across the 64 lanes of a wave.
+constexpr int kDppWaveShl1 = 0x130;  // wave_shl:1, lane l <- lane l+1
+constexpr int kDppWaveShr1 = 0x138;  // wave_shr:1, lane l <- lane l-1
+
+// v of the lane to the west (lane l-1); lane 0 gets `edge`
+__device__ __forceinline__ double from_west(double v, double edge) {
+    const int lo = __builtin_amdgcn_update_dpp(__double2loint(edge), __double2loint(v), kDppWaveShr1, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(__double2hiint(edge), __double2hiint(v), kDppWaveShr1, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+// v of the lane to the east (lane l+1); lane 63 gets `edge`
+__device__ __forceinline__ double from_east(double v, double edge) {
+    const int lo = __builtin_amdgcn_update_dpp(__double2loint(edge), __double2loint(v), kDppWaveShl1, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(__double2hiint(edge), __double2hiint(v), kDppWaveShl1, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+// v of lane l, in every lane
+__device__ __forceinline__ double lane_val(double v, int l) {
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), l), __builtin_amdgcn_readlane(__double2loint(v), l));
+}
+
 // Sum over the 64 lanes; every lane gets the total.  Inside a 16-lane row: two quad
 // permutations and two row rotations (DPP, no LDS traffic); across rows: two xor shuffles.
 __device__ __forceinline__ double wave_sum(double v) {
