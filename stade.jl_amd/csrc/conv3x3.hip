@@ -295,13 +295,18 @@ __global__ __launch_bounds__(NT) void loss_kernel(const double* __restrict__ par
     double acc[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) acc[k] = 0.0;
+    // unrolled so that several partials' loads are in flight (the sums keep their order)
+#pragma unroll 8
     for (int b = threadIdx.x; b < nparts; b += NT)
 #pragma unroll
         for (int k = 0; k < NV; ++k) acc[k] += partials[(long)b * NV + k];
     block_sum<NV>(acc, red);
     if (threadIdx.x == 0) {
-        l0[0] = (float)((double)l0[0] + acc[0]);
-        if (NV == 2) l1[0] = (float)((double)l1[0] + acc[NV - 1]);
+        // both destinations read before either is written (they may alias as far as the
+        // compiler knows)
+        const float o0 = l0[0], o1 = NV == 2 ? l1[0] : 0.f;
+        l0[0] = (float)((double)o0 + acc[0]);
+        if (NV == 2) l1[0] = (float)((double)o1 + acc[NV - 1]);
     }
 }
 

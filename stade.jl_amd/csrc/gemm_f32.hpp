@@ -333,9 +333,14 @@ __global__ __launch_bounds__(NT) void splitk_reduce_kernel(const float* __restri
     const long q = (long)blockIdx.x * NT + threadIdx.x;
     const long mn = (long)M * N;
     if (q >= mn) return;
-    float s = part[q];
-#pragma unroll 4
-    for (int z = 1; z < ksplit; ++z) s += part[q + z * mn];
+    // every slice's value in flight at once (ksplit <= 16), added in slice order
+    float v[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) v[z] = z < ksplit ? part[q + z * mn] : 0.f;
+    float s = v[0];
+#pragma unroll
+    for (int z = 1; z < 16; ++z)
+        if (z < ksplit) s += v[z];
     const int m = (int)(q % M), n = (int)(q / M);
     epi(m, n, s, epi.load(m, n));
 }

@@ -187,14 +187,21 @@ __device__ __forceinline__ void finalize_partials(const double* partials, int np
     double acc[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) acc[k] = 0.0;
+    // unrolled so that several partials' loads are in flight (the sums keep their order)
+#pragma unroll 8
     for (int b = threadIdx.x; b < nparts; b += blockDim.x) {
 #pragma unroll
         for (int k = 0; k < NV; ++k) acc[k] += partials[(size_t)b * NV + k];
     }
     block_sum<NV>(acc, lds);
     if (threadIdx.x == 0) {
+        // every destination read before any is written (they may alias as far as the compiler
+        // knows, and interleaving would cost a memory round trip per destination)
+        double old[NV];
 #pragma unroll
-        for (int k = 0; k < NV; ++k) out.p[k][0] = out.p[k][0] + acc[k];
+        for (int k = 0; k < NV; ++k) old[k] = out.p[k][0];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) out.p[k][0] = old[k] + acc[k];
     }
 }
 

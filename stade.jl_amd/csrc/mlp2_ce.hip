@@ -272,35 +272,50 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
 constexpr int H4NT = 256;
 constexpr int SC = 128;  // samples per chunk of the column sums
 
+// sum over the 16 lanes of a DPP row (every lane of the row gets it)
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<kDppQuadSwap1>(v);
+    v += dpp_f32<kDppQuadSwap2>(v);
+    v += dpp_f32<kDppRowRor4>(v);
+    v += dpp_f32<kDppRowRor8>(v);
+    return v;
+}
+
 template <int MODE, int HPL, int SPW>
 __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
     constexpr int NW = MODE == ADJ ? 1 : 2;
     constexpr int JR = 64 * HPL;
+    // the adjoint reduces its lane partial sums through LDS: per wave a [64][ZW] array
+    constexpr int ZW = SPW * OMAX + 4;
+    static_assert(MODE != ADJ || SPW * OMAX <= 64, "one lane per (sample, output) of a wave");
     __shared__ float w2s[NW * JR * OP];
+    __shared__ float zt[MODE == ADJ ? (H4NT / 64) * 64 * ZW : 1];
     __shared__ double red[16 * 2];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.H, O = a.O, B = a.B;
     {
-        // padded element q = (j, o) with o fastest; CB loads in flight per thread
-        constexpr int CB = 8, TOTAL = JR * OMAX;
-        for (int q0 = 0; q0 < TOTAL; q0 += H4NT * CB) {
-            float v[CB], vd[CB];
+        // LDS row j, entry o: W2[o, j] for j < H and o < O, zero elsewhere; a thread takes whole
+        // rows j = threadIdx.x + H4NT c with every load in flight at once (no index division,
+        // and the padding is written with the data)
+        constexpr int RPT = JR / H4NT;
+        float v[RPT][OMAX], vd[RPT][OMAX];
 #pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                const int q = q0 + c * H4NT + threadIdx.x;
-                const int j = q / OMAX, o = q % OMAX;
-                const bool in = q < TOTAL && j < H && o < O;
-                v[c] = in ? a.w2[(long)j * O + o] : 0.f;
-                vd[c] = (MODE != ADJ && in) ? a.w2d[(long)j * O + o] : 0.f;
+        for (int c = 0; c < RPT; ++c) {
+            const int j = threadIdx.x + H4NT * c;
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                const bool in = j < H && o < O;
+                v[c][o] = in ? a.w2[(long)j * O + o] : 0.f;
+                vd[c][o] = (MODE != ADJ && in) ? a.w2d[(long)j * O + o] : 0.f;
             }
+        }
 #pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                const int q = q0 + c * H4NT + threadIdx.x;
-                if (q < TOTAL) {
-                    const int j = q / OMAX, o = q % OMAX;
-                    w2s[j * OP + o] = v[c];
-                    if (MODE != ADJ) w2s[JR * OP + j * OP + o] = vd[c];
-                }
+        for (int c = 0; c < RPT; ++c) {
+            const int j = threadIdx.x + H4NT * c;
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                w2s[j * OP + o] = v[c][o];
+                if (MODE != ADJ) w2s[JR * OP + j * OP + o] = vd[c][o];
             }
         }
     }
@@ -330,11 +345,19 @@ __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
                     hd[i][q] = j < H ? xd : 0.f;
                 }
             }
-            const int oc = min(lane, O - 1);
-            zb_l[i] = (MODE != TAN) ? a.zb[os + oc] : 0.f;
-            zbd_l[i] = (MODE == HVP) ? a.zbd[os + oc] : 0.f;
-            lab[i] = a.lab[s];
+            if (MODE != ADJ) {
+                const int oc = min(lane, O - 1);
+                zb_l[i] = (MODE != TAN) ? a.zb[os + oc] : 0.f;
+                zbd_l[i] = (MODE == HVP) ? a.zbd[os + oc] : 0.f;
+                lab[i] = a.lab[s];
+            }
         }
+        // the adjoint's lane L = 16 i + o: sample s0 + i, output o
+        const int li = lane >> 4, lo = lane & (OMAX - 1);
+        const int ls = min(s0 + li, B - 1);
+        const float zb_lane = (MODE == ADJ) ? a.zb[(long)ls * O + min(lo, O - 1)] : 0.f;
+        const float b2_lane = (MODE == ADJ) ? a.b2[min(lo, O - 1)] : 0.f;
+        const int64_t lab_lane = (MODE == ADJ) ? a.lab[ls] : 0;
         // z = b2 + W2 h1 (zd = b2d + W2d h1 + W2 h1d): lane partial sums over its columns
         float z[SPW][OMAX], zd[SPW][OMAX];
 #pragma unroll
@@ -357,6 +380,44 @@ __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
             // one column block's weights live at a time (the scheduler would otherwise hoist
             // every LDS read of the loop)
             asm volatile("" ::: "memory");
+        }
+        if constexpr (MODE == ADJ) {
+            // lane l writes its partial sums as row l of the wave's array; lane L = 16 i + o then
+            // adds column L over the 64 rows in lane order (a wave's LDS operations complete in
+            // issue order, so no barrier is needed between the writes and the reads)
+            float* zw = zt + (threadIdx.x >> 6) * 64 * ZW;
+#pragma unroll
+            for (int i = 0; i < SPW; ++i)
+#pragma unroll
+                for (int o = 0; o < OMAX; o += 4)
+                    *reinterpret_cast<float4*>(zw + lane * ZW + i * OMAX + o) =
+                        make_float4(z[i][o], z[i][o + 1], z[i][o + 2], z[i][o + 3]);
+            float zs = 0.f;
+            const int col = min(lane, SPW * OMAX - 1);
+#pragma unroll 16
+            for (int r = 0; r < 64; ++r) zs += zw[r * ZW + col];
+            asm volatile("" ::: "memory");
+            // softmax cross-entropy of sample s0 + li, output lo, over the lanes of its DPP row
+            const bool live = li < SPW && s0 + li < B, vo = lo < O;
+            const long os = (long)ls * O;
+            const float zv = vo ? b2_lane + zs : 0.f;
+            const float e = vo ? expf(zv) : 0.f;
+            const float se = row16_sum(e);
+            const int l = (int)lab_lane - 1;
+            const bool lok = l >= 0 && l < O;
+            if (live && lo == 0 && !lok) atomicExch(a.err, 1);
+            if (live && lok && lo == l) acc[0] += (double)(logf(se) - zv);
+            // reverse of the loss: d2 = zb + [o == l](-lb) + exp(z) seb, seb = (1 / se) lb
+            const float seb = (1.0f / se) * lb;
+            float t = zb_lane;
+            if (lo == l) t = t + -lb;
+            const float d2 = t + e * seb;
+            if (live && vo) {
+                a.z[os + lo] = zv;
+                a.zb[os + lo] = 0.f;
+                a.D2[os + lo] = d2;
+            }
+            continue;
         }
 #pragma unroll
         for (int i = 0; i < SPW; ++i) {
@@ -662,27 +723,43 @@ struct FinalArgs {
 
 template <int MODE>
 __global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
-    __shared__ double red[16];
+    constexpr int NV = 2 + 2 * OMAX;  // loss, lossd, b2b[OMAX], b2bd[OMAX]
+    __shared__ double red[16 * NV];
     const int O = f.O, H = f.H;
     if (blockIdx.x == 0) {
-        for (int k = 0; k < 2 + 2 * OMAX; ++k) {
-            if (k == 1 && MODE == ADJ) continue;
-            if (k >= 2 && MODE == TAN) break;
-            if (k >= 2 + O && k < 2 + OMAX) continue;
-            if (k >= 2 + OMAX && (MODE != HVP || k >= 2 + OMAX + O)) continue;
-            double v[1] = {0.0};
-            if (k < 2) {
-                for (int b = threadIdx.x; b < f.nhead; b += NT) v[0] += f.hpart[(size_t)b * 2 + k];
-            } else {
-                for (int c = threadIdx.x; c < f.nchunks; c += NT) v[0] += (double)f.c2part[(size_t)c * 2 * OMAX + (k - 2)];
+        // all the sums at once: per value a thread-strided sum in index order, then one block
+        // reduction of the NV values together
+        double v[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) v[k] = 0.0;
+        for (int b = threadIdx.x; b < f.nhead; b += NT) {
+            v[0] += f.hpart[(size_t)b * 2];
+            if (MODE != ADJ) v[1] += f.hpart[(size_t)b * 2 + 1];
+        }
+        if (MODE != TAN) {
+            for (int c = threadIdx.x; c < f.nchunks; c += NT) {
+#pragma unroll
+                for (int k = 0; k < 2 * OMAX; ++k) v[2 + k] += (double)f.c2part[(size_t)c * 2 * OMAX + k];
             }
-            block_sum<1>(v, red);
-            if (threadIdx.x == 0) {
-                float t = (float)v[0];
-                if (k == 0) f.loss[0] = f.loss[0] + t;
-                else if (k == 1) f.lossd[0] = f.lossd[0] + t;
-                else if (k < 2 + OMAX) f.b2b[k - 2] = f.b2b[k - 2] + t;
-                else f.b2bd[k - 2 - OMAX] = f.b2bd[k - 2 - OMAX] + t;
+        }
+        block_sum<NV>(v, red);
+        // every output read before any is written: the stores may alias the later reads as far
+        // as the compiler knows, and interleaving would cost a memory round trip per output
+        if (threadIdx.x == 0) {
+            float old[NV];
+            old[0] = f.loss[0];
+            old[1] = MODE != ADJ ? f.lossd[0] : 0.f;
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                old[2 + o] = (MODE != TAN && o < O) ? f.b2b[o] : 0.f;
+                old[2 + OMAX + o] = (MODE == HVP && o < O) ? f.b2bd[o] : 0.f;
+            }
+            f.loss[0] = old[0] + (float)v[0];
+            if (MODE != ADJ) f.lossd[0] = old[1] + (float)v[1];
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
+                if (MODE != TAN && o < O) f.b2b[o] = old[2 + o] + (float)v[2 + o];
+                if (MODE == HVP && o < O) f.b2bd[o] = old[2 + OMAX + o] + (float)v[2 + OMAX + o];
             }
         }
         return;
@@ -692,9 +769,17 @@ __global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
     const long q = (long)(blockIdx.x - 1) * NT + threadIdx.x;
     if (q >= (long)rows * H) return;
     const int r = (int)(q / H), j = (int)(q % H);
+    // 32 chunk partials in flight at a time, added in chunk order
     float s = 0.f;
-#pragma unroll 8
-    for (int c = 0; c < f.nchunks; ++c) s += f.cpart[(long)c * 2 * (O + 1) * H + (long)r * H + j];
+    for (int c0 = 0; c0 < f.nchunks; c0 += 32) {
+        float v[32];
+#pragma unroll
+        for (int c = 0; c < 32; ++c)
+            v[c] = c0 + c < f.nchunks ? f.cpart[(long)(c0 + c) * 2 * (O + 1) * H + (long)r * H + j] : 0.f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c)
+            if (c0 + c < f.nchunks) s += v[c];
+    }
     if (r < O) f.w2b[(long)j * O + r] = f.w2b[(long)j * O + r] + s;
     else if (r == O) f.b1b[j] = f.b1b[j] + s;
     else if (r < 2 * O + 1) f.w2bd[(long)j * O + (r - O - 1)] = f.w2bd[(long)j * O + (r - O - 1)] + s;
