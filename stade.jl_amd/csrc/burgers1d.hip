@@ -289,7 +289,10 @@ __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win
 // wave publishes its end lanes' tape value and adjoint state in a small LDS array, double
 // buffered by step, so a step needs one barrier and almost no LDS traffic.  The tape row of
 // step k+1 is published at the end of step k, so the prefetch ring of PD rows keeps PD - 1
-// rows in flight.  The arithmetic per position is bwd_step's, in the same order.
+// rows in flight.  The arithmetic per position is bwd_step's, in the same order.  A ring of 2
+// measured faster than 4 (537 against 526 adjoint evals/s); loading the tape shifted by -/+1
+// instead of taking neighbours by DPP needs more registers than a 1024-thread block allows
+// and ran at 392.
 // ---------------------------------------------------------------------------------------
 template <bool HV, int S, int PD>
 __global__ __launch_bounds__(BNT) void bwd_reg_kernel(const double* __restrict__ win, const double* __restrict__ wind,
@@ -577,7 +580,7 @@ int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, dou
         double* dd = last ? ubd : owd;
         if (nk == KMAX) {
             STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
-                        bwd_reg_kernel<HV, S, HV ? 2 : 4><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, c,
+                        bwd_reg_kernel<HV, S, 2><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, c,
                                                                       pbwd + (size_t)chunk * nb * NV));
         } else {
             STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
