@@ -427,7 +427,8 @@ struct WgArgs {
     const float* x[2];  // xp-shaped
     const float* g[2];  // out-shaped
     int N, C, K, H, W;
-    int ntx, nty, ntiles;
+    int ntx, nty, ntiles;  // pixel tiles of one (x, g) pair
+    int npairs;            // NPR = 1: tiles [p * ntiles, (p + 1) * ntiles) use pair p
     float* part;
 };
 
@@ -450,6 +451,11 @@ __global__ __launch_bounds__(NT) void wgrad_kernel(WgArgs a) {
 
     float xr[NPR][XLD], gr[NPR][GLD];
     auto load = [&](int tile) {
+        // NPR = 1 with two pairs: the pair is uniform over the block's tile
+        const int pr = NPR == 1 && tile >= a.ntiles ? 1 : 0;
+        tile -= pr * a.ntiles;
+        const float* xs[2] = {a.x[pr], a.x[1]};
+        const float* gs[2] = {a.g[pr], a.g[1]};
         const int xt = tile % a.ntx;
         const int rest = tile / a.ntx;
         const int yt = rest % a.nty, n = rest / a.nty;
@@ -462,14 +468,14 @@ __global__ __launch_bounds__(NT) void wgrad_kernel(WgArgs a) {
                 const int ci = f / XPL, e = f - ci * XPL;
                 const int ty = e / XPX, tx = e - ty * XPX;
                 const int c = c0 + ci, yy = y0 + ty, xx = x0 + tx;
-                xr[p][q] = (c < a.C && yy < Hp && xx < Wp) ? a.x[p][((long)(n * a.C + c) * Hp + yy) * Wp + xx] : 0.f;
+                xr[p][q] = (c < a.C && yy < Hp && xx < Wp) ? xs[p][((long)(n * a.C + c) * Hp + yy) * Wp + xx] : 0.f;
             }
 #pragma unroll
             for (int q = 0; q < GLD; ++q) {
                 const int f = threadIdx.x + q * NT;
                 const int co = f / GPX, px = f - co * GPX;
                 const int k = k0 + co, yy = y0 + px / WTX, xx = x0 + px % WTX;
-                gr[p][q] = (k < a.K && yy < a.H && xx < a.W) ? a.g[p][((long)(n * a.K + k) * a.H + yy) * a.W + xx] : 0.f;
+                gr[p][q] = (k < a.K && yy < a.H && xx < a.W) ? gs[p][((long)(n * a.K + k) * a.H + yy) * a.W + xx] : 0.f;
             }
         }
     };
@@ -500,13 +506,14 @@ __global__ __launch_bounds__(NT) void wgrad_kernel(WgArgs a) {
     // lane bases: patch channel 32 wa + l32, pixel + h;  g row 32 wb + l32, pixel + h
     const int xb = (32 * wa + l32) * XPP + h;
     const int gb = (32 * wb + l32) * GPP + h;
+    const int ntot = a.ntiles * a.npairs;
     int tile = blockIdx.y;
-    if (tile < a.ntiles) load(tile);
-    for (; tile < a.ntiles; tile += gridDim.y) {
+    if (tile < ntot) load(tile);
+    for (; tile < ntot; tile += gridDim.y) {
         __syncthreads();
         store();
         __syncthreads();
-        if (tile + (int)gridDim.y < a.ntiles) load(tile + gridDim.y);
+        if (tile + (int)gridDim.y < ntot) load(tile + gridDim.y);
         // k steps s (pixel pairs 2s, 2s+1); step s+1's fragments are read during step s's MFMAs
         constexpr int NSTEP = GPX / 2;
         float gf[2][NPR], xf[2][NPR][9];
@@ -553,8 +560,11 @@ __global__ __launch_bounds__(NT) void wreduce_kernel(const float* __restrict__ p
     const int el = threadIdx.x & 63, sl = threadIdx.x >> 6;
     const long q = (long)blockIdx.x * 64 + el;
     double s = 0.0;
-    if (q < total)
+    // unrolled so that several splits' loads are in flight (the sum keeps its order)
+    if (q < total) {
+#pragma unroll 8
         for (int sp = sl; sp < nsplit; sp += 4) s += part[(long)sp * total + q];
+    }
     red[sl][el] = s;
     __syncthreads();
     if (sl != 0 || q >= total) return;
@@ -617,6 +627,7 @@ int32_t weight_grad(const Dims& d, const float* x0, const float* g0, const float
     a.ntx = (d.W + WTX - 1) / WTX;
     a.nty = (d.H + WTY - 1) / WTY;
     a.ntiles = a.ntx * a.nty * d.N;
+    a.npairs = NPR == 1 && x1 ? 2 : 1;
     a.part = part;
     const int ctn = d.Cpad / 64, ktn = d.Kpad / 64;
     dim3 grid(ctn * ktn, nsplit);
@@ -699,7 +710,9 @@ int32_t run(const Ptrs& p, const Dims& d, hipStream_t stream) {
     int32_t rc = weight_grad<1>(d, p.xp, G, nullptr, nullptr, part, nsplit, p.wb, "conv_wgrad", stream);
     if (rc) return rc;
     if (MODE == HVP) {
-        rc = weight_grad<2>(d, p.xpd, G, p.xp, GD, part, nsplit, p.wbd, "conv_wgrad2", stream);
+        // both products of wbd through the single-pair kernel, over twice the tiles (holding
+        // two pairs' tiles at once spilled registers and ran at 64 TFLOP/s)
+        rc = weight_grad<1>(d, p.xpd, G, p.xp, GD, part, nsplit, p.wbd, "conv_wgrad2", stream);
         if (rc) return rc;
     }
     // xpb interior += flipped taps over g;  HVP: xpbd += wd g + w gd

@@ -353,12 +353,16 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 struct Plan {
     int bnt, ksplit;
 };
+#ifndef STADE_GEMM_BPC
+#define STADE_GEMM_BPC 2
+#endif
 inline Plan plan(int M, int N, int Ktot, int cus) {
+    constexpr long bpc = STADE_GEMM_BPC;  // blocks per CU the plan aims for
     const long wide = (long)((M + BM - 1) / BM) * ((N + 127) / 128);
-    if (wide >= 2L * cus) return Plan{128, 1};
+    if (wide >= bpc * cus) return Plan{128, 1};
     const long narrow = (long)((M + BM - 1) / BM) * ((N + 63) / 64);
     int ks = 1;
-    while (narrow * ks < 2L * cus && Ktot / (ks * 2) >= 256 && ks < 16) ks *= 2;
+    while (narrow * ks < bpc * cus && Ktot / (ks * 2) >= 256 && ks < 16) ks *= 2;
     return Plan{64, ks};
 }
 
