@@ -30,7 +30,9 @@ namespace stade {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int NT = 256;
+constexpr int kBufWord3 = 0x00020000;  // gfx9-family buffer resource word 3 (raw, 32-bit data)
 
 enum { FWD_B, FWD_D, FWD_HV, DG_B, DG_HV };
 
@@ -122,30 +124,60 @@ __global__ __launch_bounds__(NT, (MODE == FWD_B || MODE == DG_B) ? 2 : 1) void t
     static_assert(PROWS % 4 == 0 && PXW == 66 && 2 * PROWS <= NT, "patch rows");
     float pr[RPW + 1];
     float4 wr[WLD];
-    auto row_src = [&](int rr, int c0, int col, float& v) {
-        const int p = NP == 1 ? 0 : rr / (CC * PYH);
-        const int rem = rr - p * (CC * PYH);
-        const int cc = rem / PYH, ty = rem - cc * PYH;
-        const int c = c0 + cc, sy = y0 + ty + a.ofs, sx = x0 + col + a.ofs;
-        v = 0.f;
-        if (c < a.Cin && (unsigned)sy < (unsigned)a.SH && (unsigned)sx < (unsigned)a.SW)
-            v = a.src[p][((long)(n * a.Cin + c) * a.SH + sy) * a.SW + sx];
-    };
+    // Staging loads are buffer loads: a scalar resource per source image n (and per weight
+    // set), the row part of a patch address as a scalar offset (patch rows are wave-uniform)
+    // and the column as the lane's offset.  An element outside the source reads offset =
+    // the resource's size, which returns 0.  Vector registers hold no 64-bit addresses, so the
+    // staging fits two waves per SIMD without spilling.  (The host keeps one image of a
+    // source and a weight set under 2^31 bytes.)
+    const long plane = (long)a.SH * a.SW;
+    const uint32_t sbytes = (uint32_t)((long)a.Cin * plane * 4);
+    const uint32_t wbytes = (uint32_t)((long)a.Cin * 9 * a.Rpad * 4);
+    __amdgpu_buffer_rsrc_t rs[NP], rw[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        rs[p] = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.src[p] + (long)n * a.Cin * plane), (short)0, sbytes,
+                                                  kBufWord3);
+        rw[p] = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.wt[p] + rt * RT), (short)0, wbytes, kBufWord3);
+    }
+    const int sx_l = x0 + lane + a.ofs;
+    const uint32_t lane_col = (unsigned)sx_l < (unsigned)a.SW ? (uint32_t)sx_l * 4u : sbytes;
     auto load = [&](int c0) {
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) row_src(wave + 4 * i, c0, lane, pr[i]);
-        if (threadIdx.x < 2 * PROWS) row_src(threadIdx.x >> 1, c0, 64 + (threadIdx.x & 1), pr[RPW]);
+        for (int i = 0; i < RPW; ++i) {
+            const int rr = wave + 4 * i;  // wave-uniform patch row (p, cc, ty)
+            const int p = NP == 1 ? 0 : rr / (CC * PYH);
+            const int rem = rr - p * (CC * PYH);
+            const int cc = rem / PYH, ty = rem - cc * PYH;
+            const int c = c0 + cc, sy = y0 + ty + a.ofs;
+            const bool ok = c < a.Cin && (unsigned)sy < (unsigned)a.SH;
+            const uint32_t soff = ok ? (uint32_t)(((long)c * a.SH + sy) * a.SW * 4) : 0u;
+            const uint32_t voff = ok ? lane_col : sbytes;
+            pr[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(p ? rs[NP - 1] : rs[0], voff, soff, 0));
+        }
+        if (threadIdx.x < 2 * PROWS) {
+            // columns 64, 65: the row varies across a wave, so the whole offset is the lane's
+            const int rr = threadIdx.x >> 1, col = 64 + (threadIdx.x & 1);
+            const int p = NP == 1 ? 0 : rr / (CC * PYH);
+            const int rem = rr - p * (CC * PYH);
+            const int cc = rem / PYH, ty = rem - cc * PYH;
+            const int c = c0 + cc, sy = y0 + ty + a.ofs, sx = x0 + col + a.ofs;
+            float v = 0.f;
+            if (c < a.Cin && (unsigned)sy < (unsigned)a.SH && (unsigned)sx < (unsigned)a.SW)
+                v = a.src[p][((long)(n * a.Cin + c) * a.SH + sy) * a.SW + sx];
+            pr[RPW] = v;
+        }
+        const uint32_t wsoff = (uint32_t)((long)c0 * 9 * a.Rpad * 4);
 #pragma unroll
         for (int q = 0; q < WLD; ++q) {
             const int f = threadIdx.x + q * NT;  // float4 slot of [w][cc][t][r]
-            const int wi = NP == 1 ? 0 : f / (WSZ / 4);
+            const int wi = NP == 1 ? 0 : __builtin_amdgcn_readfirstlane(f / (WSZ / 4));  // uniform per wave
             const int rem = f - wi * (WSZ / 4);
             const int row = rem / (RT / 4), r4 = (rem - row * (RT / 4)) * 4;
             const int cc = row / 9, t = row - cc * 9;
-            const int c = c0 + cc;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (c < a.Cin) v = *reinterpret_cast<const float4*>(a.wt[wi] + ((long)c * 9 + t) * a.Rpad + rt * RT + r4);
-            wr[q] = v;
+            const uint32_t voff = c0 + cc < a.Cin ? (uint32_t)(((cc * 9 + t) * a.Rpad + r4) * 4) : wbytes;
+            const v4f x = __builtin_amdgcn_raw_buffer_load_b128(wi ? rw[NP - 1] : rw[0], voff, wsoff, 0);
+            wr[q] = make_float4(x.x, x.y, x.z, x.w);
         }
     };
     auto store = [&]() {
@@ -596,6 +628,10 @@ struct Dims {
 int32_t check(int64_t N, int64_t C, int64_t K, int64_t H, int64_t W, const char* fn, Dims& d) {
     if (N < 0 || C < 0 || K < 0 || H < 0 || W < 0) return set_error(STADE_HIP_EINVAL, "%s: negative size", fn);
     const double lim = 2147483647.0;
+    // one image of a source and one weight set are read through buffer resources: < 2^31 bytes
+    const double blim = 536870911.0;
+    if ((double)C * (H + 2) * (W + 2) > blim || (double)K * H * W > blim || 9.0 * (C + 64) * (K + 64) > blim)
+        return set_error(STADE_HIP_ERANGE, "%s: one image or the weights exceed 2^29 elements", fn);
     if ((double)N * C * (H + 2) * (W + 2) > lim || (double)N * K * H * W > lim || 9.0 * C * K > lim ||
         (double)N * ((K + 63) / 64) > 65535 || (double)N * ((C + 15) / 16) > 65535 || H > 200000 || W > 200000)
         return set_error(STADE_HIP_ERANGE, "%s: sizes out of range", fn);
