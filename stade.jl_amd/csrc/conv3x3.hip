@@ -353,7 +353,7 @@ __global__ __launch_bounds__(NT) void loss_kernel(const double* __restrict__ par
 // (g zero outside the image).  Block: 64 cells of one edge x 16 channels c; output
 // channels advance 16 at a time through LDS (the g line segment and the weight slice).
 // ------------------------------------------------------------------------------------------
-constexpr int BSEG = 64, BKC = 16, BCG = 16;
+constexpr int BSEG = 64, BKC = 64, BCG = 16;  // cells, output channels per staging round, input channels
 
 struct BorderArgs {
     const float* w;
@@ -369,7 +369,7 @@ template <bool HV>
 __global__ __launch_bounds__(NT) void border_kernel(BorderArgs a) {
     constexpr int NG = HV ? 2 : 1;
     __shared__ float gl[NG][BKC][BSEG + 2];
-    __shared__ float wv[NG][BKC][BCG][3];
+    __shared__ float4 wv[NG][BKC][3][BCG / 4];  // [kk][d][c]: a thread's 4 channels in one read
     const int e = blockIdx.y;
     const int L = e < 2 ? a.W + 2 : a.H;
     const int p0 = blockIdx.x * BSEG;
@@ -383,20 +383,28 @@ __global__ __launch_bounds__(NT) void border_kernel(BorderArgs a) {
     float acc[4] = {0.f, 0.f, 0.f, 0.f}, accd[4] = {0.f, 0.f, 0.f, 0.f};
     for (int k0 = 0; k0 < a.K; k0 += BKC) {
         __syncthreads();
-        for (int f = threadIdx.x; f < BKC * (BSEG + 2); f += NT) {
+        // every staging load of the round issued before any LDS store (one memory round trip)
+        constexpr int NGL = (BKC * (BSEG + 2) + NT - 1) / NT, NWL = BKC * BCG * 3 / NT;
+        static_assert(BKC * BCG * 3 % NT == 0, "weight staging");
+        float gv_[NGL], gvd_[NGL], wv_[NWL], wvd_[NWL];
+#pragma unroll
+        for (int u = 0; u < NGL; ++u) {
+            const int f = threadIdx.x + u * NT;
             const int kk = f / (BSEG + 2), i = f - kk * (BSEG + 2);
             const int co = k0 + kk, q = p0 + off - 2 + i;
             float v = 0.f, vd = 0.f;
-            if (co < a.K && q >= 0 && q < lim) {
+            if (f < BKC * (BSEG + 2) && co < a.K && q >= 0 && q < lim) {
                 const long plane = (long)(n * a.K + co) * a.H;
                 const long gi = e < 2 ? (plane + (e == 0 ? 0 : a.H - 1)) * a.W + q : (plane + q) * a.W + (e == 2 ? 0 : a.W - 1);
                 v = a.g[gi];
                 if (HV) vd = a.gd[gi];
             }
-            gl[0][kk][i] = v;
-            if (HV) gl[NG - 1][kk][i] = vd;
+            gv_[u] = v;
+            gvd_[u] = vd;
         }
-        for (int f = threadIdx.x; f < BKC * BCG * 3; f += NT) {
+#pragma unroll
+        for (int u = 0; u < NWL; ++u) {
+            const int f = threadIdx.x + u * NT;
             const int kk = f / (BCG * 3), r = f - kk * (BCG * 3);
             const int cc = r / 3, d = r - cc * 3;
             const int co = k0 + kk, c = c0 + cc;
@@ -407,8 +415,25 @@ __global__ __launch_bounds__(NT) void border_kernel(BorderArgs a) {
                 v = a.w[wi];
                 if (HV) vd = a.wd[wi];
             }
-            wv[0][kk][cc][d] = v;
-            if (HV) wv[NG - 1][kk][cc][d] = vd;
+            wv_[u] = v;
+            wvd_[u] = vd;
+        }
+#pragma unroll
+        for (int u = 0; u < NGL; ++u) {
+            const int f = threadIdx.x + u * NT;
+            if (f < BKC * (BSEG + 2)) {
+                const int kk = f / (BSEG + 2), i = f - kk * (BSEG + 2);
+                gl[0][kk][i] = gv_[u];
+                if (HV) gl[NG - 1][kk][i] = gvd_[u];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NWL; ++u) {
+            const int f = threadIdx.x + u * NT;
+            const int kk = f / (BCG * 3), r = f - kk * (BCG * 3);
+            const int cc = r / 3, d = r - cc * 3;
+            reinterpret_cast<float*>(&wv[0][kk][d][0])[cc] = wv_[u];
+            if (HV) reinterpret_cast<float*>(&wv[NG - 1][kk][d][0])[cc] = wvd_[u];
         }
         __syncthreads();
 #pragma unroll 4
@@ -417,11 +442,13 @@ __global__ __launch_bounds__(NT) void border_kernel(BorderArgs a) {
             for (int d = 0; d < 3; ++d) {
                 const float gv = gl[0][kk][cell + 2 - d];
                 const float gvd = HV ? gl[NG - 1][kk][cell + 2 - d] : 0.f;
+                const float4 w4 = wv[0][kk][d][cg];
+                const float4 wd4 = HV ? wv[NG - 1][kk][d][cg] : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float wc_[4] = {w4.x, w4.y, w4.z, w4.w}, wdc_[4] = {wd4.x, wd4.y, wd4.z, wd4.w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float wc = wv[0][kk][cg + 4 * i][d];
-                    acc[i] += wc * gv;
-                    if (HV) accd[i] += wv[NG - 1][kk][cg + 4 * i][d] * gv + wc * gvd;
+                    acc[i] += wc_[i] * gv;
+                    if (HV) accd[i] += wdc_[i] * gv + wc_[i] * gvd;
                 }
             }
     }
@@ -430,13 +457,23 @@ __global__ __launch_bounds__(NT) void border_kernel(BorderArgs a) {
     const int Hp = a.H + 2, Wp = a.W + 2;
     const int yp = e == 0 ? 0 : e == 1 ? Hp - 1 : p + 1;
     const int xq = e < 2 ? p : (e == 2 ? 0 : Wp - 1);
+    // every xpb (xpbd) value read before any is written (the arrays may alias as far as the
+    // compiler knows)
+    float old[4], oldd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int c = c0 + cg + 4 * i;
+        const int c = c0 + 4 * cg + i;
+        const long oi = ((long)(n * a.C + c) * Hp + yp) * Wp + xq;
+        old[i] = c < a.C ? a.xpb[oi] : 0.f;
+        oldd[i] = (HV && c < a.C) ? a.xpbd[oi] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = c0 + 4 * cg + i;
         if (c >= a.C) continue;
         const long oi = ((long)(n * a.C + c) * Hp + yp) * Wp + xq;
-        a.xpb[oi] = a.xpb[oi] + acc[i];
-        if (HV) a.xpbd[oi] = a.xpbd[oi] + accd[i];
+        a.xpb[oi] = old[i] + acc[i];
+        if (HV) a.xpbd[oi] = oldd[i] + accd[i];
     }
 }
 
