@@ -304,18 +304,24 @@ __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
             const int j = threadIdx.x + H4NT * c;
 #pragma unroll
             for (int o = 0; o < OMAX; ++o) {
-                const bool in = j < H && o < O;
-                v[c][o] = in ? a.w2[(long)j * O + o] : 0.f;
-                vd[c][o] = (MODE != ADJ && in) ? a.w2d[(long)j * O + o] : 0.f;
+                // clamped, unconditional loads (a load under a branch makes the compiler wait
+                // for every load in flight); the padding is applied after all are issued
+                const long q = (long)min(j, H - 1) * O + min(o, O - 1);
+                v[c][o] = a.w2[q];
+                vd[c][o] = MODE != ADJ ? a.w2d[q] : 0.f;
             }
         }
+        // keep every load above the first use (the scheduler would otherwise place each select
+        // right after its load and wait for it)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < RPT; ++c) {
             const int j = threadIdx.x + H4NT * c;
 #pragma unroll
             for (int o = 0; o < OMAX; ++o) {
-                w2s[j * OP + o] = v[c][o];
-                if (MODE != ADJ) w2s[JR * OP + j * OP + o] = vd[c][o];
+                const bool in = j < H && o < O;
+                w2s[j * OP + o] = in ? v[c][o] : 0.f;
+                if (MODE != ADJ) w2s[JR * OP + j * OP + o] = in ? vd[c][o] : 0.f;
             }
         }
     }
@@ -337,13 +343,9 @@ __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
             const long hs = (long)s * H, os = (long)s * O;
 #pragma unroll
             for (int q = 0; q < HPL; ++q) {
-                const int j = lane + 64 * q, jc = min(j, H - 1);
-                const float x = a.h1[hs + jc];
-                h[i][q] = j < H ? x : 0.f;
-                if (MODE != ADJ) {
-                    const float xd = a.h1d[hs + jc];
-                    hd[i][q] = j < H ? xd : 0.f;
-                }
+                const int jc = min(lane + 64 * q, H - 1);
+                h[i][q] = a.h1[hs + jc];
+                if (MODE != ADJ) hd[i][q] = a.h1d[hs + jc];
             }
             if (MODE != ADJ) {
                 const int oc = min(lane, O - 1);
@@ -358,6 +360,16 @@ __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
         const float zb_lane = (MODE == ADJ) ? a.zb[(long)ls * O + min(lo, O - 1)] : 0.f;
         const float b2_lane = (MODE == ADJ) ? a.b2[min(lo, O - 1)] : 0.f;
         const int64_t lab_lane = (MODE == ADJ) ? a.lab[ls] : 0;
+        // every read above stays ahead of the first use; columns past H then contribute zero
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < SPW; ++i)
+#pragma unroll
+            for (int q = 0; q < HPL; ++q) {
+                const bool in = lane + 64 * q < H;
+                h[i][q] = in ? h[i][q] : 0.f;
+                if (MODE != ADJ) hd[i][q] = in ? hd[i][q] : 0.f;
+            }
         // z = b2 + W2 h1 (zd = b2d + W2d h1 + W2 h1d): lane partial sums over its columns
         float z[SPW][OMAX], zd[SPW][OMAX];
 #pragma unroll
@@ -535,23 +547,36 @@ __global__ __launch_bounds__(NT) void d1sum_kernel(D1Args a) {
         float v[CB], vd[CB];
 #pragma unroll
         for (int k = 0; k < CB; ++k) {
+            // clamped, unconditional loads; the zero padding is applied after all are issued
             const int q = k * NT + threadIdx.x;
             const int ss = q / OMAX, o = q % OMAX;
-            const bool in = s0 + ss < s1 && o < O;
-            v[k] = in ? a.D2[(long)(s0 + ss) * O + o] : 0.f;
-            vd[k] = (HV && in) ? a.D2d[(long)(s0 + ss) * O + o] : 0.f;
+            const long qi = (long)min(s0 + ss, s1 - 1) * O + min(o, O - 1);
+            v[k] = a.D2[qi];
+            vd[k] = HV ? a.D2d[qi] : 0.f;
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < CB; ++k) {
-            d2s[k * NT + threadIdx.x] = v[k];
-            if (HV) d2ds[k * NT + threadIdx.x] = vd[k];
+            const int q = k * NT + threadIdx.x;
+            const bool in = s0 + q / OMAX < s1 && q % OMAX < O;
+            d2s[k * NT + threadIdx.x] = in ? v[k] : 0.f;
+            if (HV) d2ds[k * NT + threadIdx.x] = in ? vd[k] : 0.f;
         }
     }
     float w[OMAX], wd[OMAX];
 #pragma unroll
     for (int o = 0; o < OMAX; ++o) {
-        w[o] = (j < H && o < O) ? a.w2[(long)jc * O + o] : 0.f;
-        wd[o] = (HV && j < H && o < O) ? a.w2d[(long)jc * O + o] : 0.f;
+        // clamped, unconditional loads (see head4_kernel); the padding is applied below
+        const long q = (long)jc * O + min(o, O - 1);
+        w[o] = a.w2[q];
+        wd[o] = HV ? a.w2d[q] : 0.f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int o = 0; o < OMAX; ++o) {
+        const bool in = j < H && o < O;
+        w[o] = in ? w[o] : 0.f;
+        wd[o] = in ? wd[o] : 0.f;
     }
     __syncthreads();
     // b2b (+ b2bd) partials of the chunk: the column-independent sums of d2 over samples
