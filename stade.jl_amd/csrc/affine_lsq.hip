@@ -33,15 +33,27 @@ __global__ __launch_bounds__(NT) void rows_kernel(const double* __restrict__ w, 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int chunk = blockIdx.x, i = blockIdx.y * RT + lane;
     const int j0 = chunk * CT + wv * CW;
+    // the wave's 16 columns: every load issued (clamped, unconditional) before the first use;
+    // columns past n and rows past m contribute nothing
+    double wv_[CW], xv_[CW], wdv_[CW], xdv_[CW];
+    const int ic = min(i, m - 1);
+#pragma unroll
+    for (int jj = 0; jj < CW; ++jj) {
+        const int jc = min(j0 + jj, n - 1);
+        const size_t g = (size_t)jc * m + ic;
+        wv_[jj] = w[g];
+        xv_[jj] = x[jc];
+        wdv_[jj] = M != ADJ ? wd[g] : 0.0;
+        xdv_[jj] = M != ADJ ? xd[jc] : 0.0;
+    }
+    __builtin_amdgcn_sched_barrier(0);
     double s = 0.0, sd = 0.0;
     if (i < m) {
-#pragma unroll 4
+#pragma unroll
         for (int jj = 0; jj < CW; ++jj) {
-            int j = j0 + jj;
-            if (j >= n) break;
-            size_t g = (size_t)j * m + i;
-            double wij = w[g], xj = x[j];
-            if (M != ADJ) sd = sd + (xj * wd[g] + wij * xd[j]);
+            if (j0 + jj >= n) break;
+            const double wij = wv_[jj], xj = xv_[jj];
+            if (M != ADJ) sd = sd + (xj * wdv_[jj] + wij * xdv_[jj]);
             s = s + wij * xj;
         }
     }
@@ -69,9 +81,22 @@ __global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partia
         double s = a.b[i] - a.t[i];
         double sd = 0.0;
         if (M != ADJ) sd = a.bd[i] - a.td[i];
-        for (int c = 0; c < a.nchunks; ++c) {
-            s = s + a.P[(size_t)c * a.m + i];
-            if (M != ADJ) sd = sd + a.Pd[(size_t)c * a.m + i];
+        // chunk partials 16 at a time, all loads in flight, added in chunk order
+        for (int c0 = 0; c0 < a.nchunks; c0 += 16) {
+            double pv[16], pdv[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const size_t q = (size_t)min(c0 + c, a.nchunks - 1) * a.m + i;
+                pv[c] = a.P[q];
+                pdv[c] = M != ADJ ? a.Pd[q] : 0.0;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                if (c0 + c >= a.nchunks) break;
+                s = s + pv[c];
+                if (M != ADJ) sd = sd + pdv[c];
+            }
         }
         if (M != ADJ) {
             a.rd[i] = sd;
@@ -126,27 +151,49 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
     const int rtile = blockIdx.y, i = rtile * RT + lane;
     const int j0 = blockIdx.x * CT + wv * CW;
     const bool live = i < m;
-    const double si = live ? S[i] : 0.0;
-    const double sid = (M == HVP && live) ? Sd[i] : 0.0;
+    const int ic = min(i, m - 1);
+    // every read of the wave's 16 columns (w, wb, x and the tangents) issued before any use or
+    // store: clamped and unconditional, with dead rows and columns masked afterwards
+    double wv_[CW], wbv_[CW], xv_[CW], wdv_[CW], wbdv_[CW], xdv_[CW];
+#pragma unroll
     for (int jj = 0; jj < CW; ++jj) {
-        int j = j0 + jj;
-        if (j >= n) break;
-        double cx = 0.0, cxd = 0.0;
-        if (live) {
-            size_t g = (size_t)j * m + i;
-            double xj = x[j], wij = w[g];
-            if (M == HVP) {
-                wbd[g] = wbd[g] + (si * xd[j] + xj * sid);
-                cxd = si * wd[g] + wij * sid;
-            }
-            wb[g] = wb[g] + xj * si;
-            cx = wij * si;
+        const int jc = min(j0 + jj, n - 1);
+        const size_t g = (size_t)jc * m + ic;
+        wv_[jj] = w[g];
+        wbv_[jj] = wb[g];
+        xv_[jj] = x[jc];
+        wdv_[jj] = M == HVP ? wd[g] : 0.0;
+        wbdv_[jj] = M == HVP ? wbd[g] : 0.0;
+        xdv_[jj] = M == HVP ? xd[jc] : 0.0;
+    }
+    const double si = S[ic];
+    const double sid = M == HVP ? Sd[ic] : 0.0;
+    __builtin_amdgcn_sched_barrier(0);
+    double cx[CW], cxd[CW];
+#pragma unroll
+    for (int jj = 0; jj < CW; ++jj) {
+        const bool ok = live && j0 + jj < n;
+        const size_t g = (size_t)(j0 + jj) * m + i;
+        const double xj = xv_[jj], wij = wv_[jj];
+        cx[jj] = ok ? wij * si : 0.0;
+        cxd[jj] = (M == HVP && ok) ? si * wdv_[jj] + wij * sid : 0.0;
+        if (ok) {
+            if (M == HVP) wbd[g] = wbdv_[jj] + (si * xdv_[jj] + xj * sid);
+            wb[g] = wbv_[jj] + xj * si;
         }
-        cx = wave_sum(cx);
-        if (M == HVP) cxd = wave_sum(cxd);
-        if (lane == 0) {
-            XP[(size_t)rtile * n + j] = cx;
-            if (M == HVP) XPd[(size_t)rtile * n + j] = cxd;
+    }
+    // column sums over the tile's rows (DPP wave sums), all 16 columns at once
+#pragma unroll
+    for (int jj = 0; jj < CW; ++jj) {
+        cx[jj] = wave_sum(cx[jj]);
+        if (M == HVP) cxd[jj] = wave_sum(cxd[jj]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int jj = 0; jj < CW; ++jj) {
+            if (j0 + jj >= n) break;
+            XP[(size_t)rtile * n + j0 + jj] = cx[jj];
+            if (M == HVP) XPd[(size_t)rtile * n + j0 + jj] = cxd[jj];
         }
     }
 }
@@ -157,13 +204,29 @@ __global__ __launch_bounds__(NT) void xfinish_kernel(double* __restrict__ xb, do
                                                      int n, int mtiles) {
     const int j = blockIdx.x * NT + threadIdx.x;
     if (j >= n) return;
+    // row-tile partials 16 at a time, all loads in flight, added in tile order; xb (xbd) read
+    // before either is written
+    const double xb0 = xb[j];
+    const double xbd0 = M == HVP ? xbd[j] : 0.0;
     double s = 0.0, sd = 0.0;
-    for (int r = 0; r < mtiles; ++r) {
-        s += XP[(size_t)r * n + j];
-        if (M == HVP) sd += XPd[(size_t)r * n + j];
+    for (int r0 = 0; r0 < mtiles; r0 += 16) {
+        double pv[16], pdv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const size_t q = (size_t)min(r0 + r, mtiles - 1) * n + j;
+            pv[r] = XP[q];
+            pdv[r] = M == HVP ? XPd[q] : 0.0;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if (r0 + r >= mtiles) break;
+            s += pv[r];
+            if (M == HVP) sd += pdv[r];
+        }
     }
-    if (M == HVP) xbd[j] = xbd[j] + sd;
-    xb[j] = xb[j] + s;
+    if (M == HVP) xbd[j] = xbd0 + sd;
+    xb[j] = xb0 + s;
 }
 
 int32_t check_sizes(int64_t m, int64_t n, const char* fn) {

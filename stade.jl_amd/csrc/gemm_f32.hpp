@@ -333,16 +333,19 @@ __global__ __launch_bounds__(NT) void splitk_reduce_kernel(const float* __restri
     const long q = (long)blockIdx.x * NT + threadIdx.x;
     const long mn = (long)M * N;
     if (q >= mn) return;
-    // every slice's value in flight at once (ksplit <= 16), added in slice order
+    // every slice's value in flight at once (ksplit <= 16; indices past the last slice clamped
+    // to it and never added), added in slice order
+    const int m = (int)(q % M), n = (int)(q / M);
     float v[16];
 #pragma unroll
-    for (int z = 0; z < 16; ++z) v[z] = z < ksplit ? part[q + z * mn] : 0.f;
+    for (int z = 0; z < 16; ++z) v[z] = part[q + min(z, ksplit - 1) * mn];
+    const auto old = epi.load(m, n);
+    __builtin_amdgcn_sched_barrier(0);
     float s = v[0];
 #pragma unroll
     for (int z = 1; z < 16; ++z)
         if (z < ksplit) s += v[z];
-    const int m = (int)(q % M), n = (int)(q / M);
-    epi(m, n, s, epi.load(m, n));
+    epi(m, n, s, old);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

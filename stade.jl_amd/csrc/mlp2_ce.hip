@@ -794,21 +794,27 @@ __global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
     const long q = (long)(blockIdx.x - 1) * NT + threadIdx.x;
     if (q >= (long)rows * H) return;
     const int r = (int)(q / H), j = (int)(q % H);
-    // 32 chunk partials in flight at a time, added in chunk order
+    // the destination: W2b / b1b (HVP: W2bd / b1bd), read before the partial loads go out
+    float* dst;
+    if (r < O) dst = f.w2b + (long)j * O + r;
+    else if (r == O) dst = f.b1b + j;
+    else if (r < 2 * O + 1) dst = f.w2bd + (long)j * O + (r - O - 1);
+    else dst = f.b1bd + j;
+    const float old = *dst;
+    // 32 chunk partials in flight at a time (indices past the last chunk clamped to it and never
+    // added), added in chunk order
     float s = 0.f;
+    const long cstride = 2L * (O + 1) * H;
     for (int c0 = 0; c0 < f.nchunks; c0 += 32) {
         float v[32];
 #pragma unroll
-        for (int c = 0; c < 32; ++c)
-            v[c] = c0 + c < f.nchunks ? f.cpart[(long)(c0 + c) * 2 * (O + 1) * H + (long)r * H + j] : 0.f;
+        for (int c = 0; c < 32; ++c) v[c] = f.cpart[(long)min(c0 + c, f.nchunks - 1) * cstride + (long)r * H + j];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < 32; ++c)
             if (c0 + c < f.nchunks) s += v[c];
     }
-    if (r < O) f.w2b[(long)j * O + r] = f.w2b[(long)j * O + r] + s;
-    else if (r == O) f.b1b[j] = f.b1b[j] + s;
-    else if (r < 2 * O + 1) f.w2bd[(long)j * O + (r - O - 1)] = f.w2bd[(long)j * O + (r - O - 1)] + s;
-    else f.b1bd[j] = f.b1bd[j] + s;
+    *dst = old + s;
 }
 
 struct Ptrs {
