@@ -14,8 +14,9 @@
 // Tiling: a 256-thread block (4 waves) computes a 128 x BNT tile of C (BNT = 128 or 64);
 // each wave a 64 x BNT/2 part as 2 x BNT/64 MFMA 32 x 32 tiles.  K advances 16 at a time
 // through two LDS buffers (one barrier per step: the next tile's global loads are issued
-// before the MFMAs of the current one and stored to the other buffer after them).  LDS rows
-// are padded by 4 floats.  The MFMA operands are swapped (B tile as the matrix-core A
+// before the MFMAs of the current one and stored to the other buffer after them).  Operand
+// tiles sit in LDS in a k-quad layout (below), read as one 128-bit fragment per 4 MFMAs.
+// The MFMA operands are swapped (B tile as the matrix-core A
 // operand) so that the accumulator's lane index runs along m: each epilogue store of a wave
 // covers 32 consecutive rows of a column-major C, a 128-byte segment.
 //
@@ -35,8 +36,23 @@ namespace gemm {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, KT = 16, NT = 256, PAD = 4;
-constexpr int LDA_S = BM + PAD;
+#ifndef STADE_GEMM_KT
+#define STADE_GEMM_KT 16
+#endif
+constexpr int BM = 128, KT = STADE_GEMM_KT, NT = 256;
+constexpr int KQ = KT / 4;  // k-planes per step
+static_assert(KT == 16 || KT == 32, "K step of 16 or 32");
+
+// LDS operand tiles use a "quad" layout: element (k, r) of a ROWS x KT tile sits at
+// S[(k / 4) * ldq(ROWS) + r * 4 + k % 4], i.e. KT / 4 k-planes each holding, per row, that
+// row's four consecutive k values as one 16-byte cell.  A matrix-core fragment is then one
+// 128-bit LDS read per 32 rows and 4 k values.  The plane stride ROWS * 4 + 128 / KT floats
+// spreads the KT / 4 planes of a row over distinct 16-byte bank groups, so the 128-bit
+// stores of k-contiguous operands (eight lanes: 32 / KT rows x KT / 4 planes) do not conflict.
+template <int ROWS>
+constexpr int ldq() {
+    return ROWS * 4 + 128 / KT;
+}
 
 struct Seg {
     const float* A;
@@ -55,41 +71,40 @@ struct Args {
                     // segments share lda and ldb, so whole tiles may use buffer loads
 };
 
-// Registers holding one ROWS x 16 operand tile between its global load and its LDS store.
+// The cells (row, k-plane) of a ROWS x KT tile are shared out over the block: cell
+// e = threadIdx.x + NT * q of this thread is
+//   KMAJ (k contiguous in memory):    row e / KQ,   plane e % KQ   (one 16-byte load per cell;
+//                                     KQ threads read a row's 4 KT contiguous bytes)
+//   !KMAJ (rows contiguous in memory): row e % ROWS, plane e / ROWS (four 4-byte loads per
+//                                     cell, one per k; a wave reads 64 consecutive rows of a k)
 template <int ROWS>
 struct Stage {
-    float4 v[ROWS * KT / 4 / NT];
+    float4 v[ROWS * KQ / NT];
 };
 
-// A tile (r 0..ROWS-1, k 0..15) at (r0, k0) into registers; zero outside rows x K.
+template <bool KMAJ, int ROWS>
+__device__ __forceinline__ void cell_of(int e, int& r, int& kq) {
+    if (KMAJ) {
+        r = e / KQ;
+        kq = e % KQ;
+    } else {
+        r = e % ROWS;
+        kq = e / ROWS;
+    }
+}
+
+// A tile (r 0..ROWS-1, k 0..KT-1) at (r0, k0) into registers; zero outside rows x K.
 template <bool KMAJ, int ROWS>
 __device__ __forceinline__ void load_tile(Stage<ROWS>& st, const float* __restrict__ P, long ld, int rows, int K, int r0,
                                           int k0, bool vec) {
-    constexpr int R4 = ROWS / 4;  // float4 per k row (KMAJ = false)
 #pragma unroll
-    for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
-        const int f = threadIdx.x + NT * q;
+    for (int q = 0; q < ROWS * KQ / NT; ++q) {
+        int rr, kq;
+        cell_of<KMAJ, ROWS>(threadIdx.x + NT * q, rr, kq);
+        const int r = r0 + rr, k = k0 + 4 * kq;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (!KMAJ) {
-            // rows contiguous: f -> (k = f / R4, r4 = (f % R4) * 4)
-            const int kk = f / R4, r4 = (f % R4) * 4;
-            const int k = k0 + kk, r = r0 + r4;
-            if (k < K) {
-                const float* p = P + (long)r + (long)k * ld;
-                if (vec && r + 3 < rows) {
-                    x = *reinterpret_cast<const float4*>(p);
-                } else {
-                    if (r + 0 < rows) x.x = p[0];
-                    if (r + 1 < rows) x.y = p[1];
-                    if (r + 2 < rows) x.z = p[2];
-                    if (r + 3 < rows) x.w = p[3];
-                }
-            }
-        } else {
-            // k contiguous: f -> (r = f / 4, k4 = (f % 4) * 4)
-            const int rr = f >> 2, k4 = (f & 3) * 4;
-            const int r = r0 + rr, k = k0 + k4;
-            if (r < rows) {
+        if (r < rows) {
+            if (KMAJ) {
                 const float* p = P + (long)k + (long)r * ld;
                 if (vec && k + 3 < K) {
                     x = *reinterpret_cast<const float4*>(p);
@@ -99,6 +114,12 @@ __device__ __forceinline__ void load_tile(Stage<ROWS>& st, const float* __restri
                     if (k + 2 < K) x.z = p[2];
                     if (k + 3 < K) x.w = p[3];
                 }
+            } else {
+                const float* p = P + (long)r + (long)k * ld;
+                if (k + 0 < K) x.x = p[0];
+                if (k + 1 < K) x.y = p[ld];
+                if (k + 2 < K) x.z = p[2 * ld];
+                if (k + 3 < K) x.w = p[3 * ld];
             }
         }
         st.v[q] = x;
@@ -119,60 +140,58 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t operand_rsrc(const float* P) {
 
 template <bool KMAJ, int ROWS>
 struct TileOffsets {
-    uint32_t o[ROWS * KT / 4 / NT];
+    uint32_t o[ROWS * KQ / NT];
 };
 
-// byte offsets of this thread's float4s of the tile at rows r0.., k step 0
+// byte offsets of this thread's cells of the tile at rows r0.., k step 0
 template <bool KMAJ, int ROWS>
 __device__ __forceinline__ TileOffsets<KMAJ, ROWS> tile_offsets(long ld, int r0) {
-    constexpr int R4 = ROWS / 4;
     TileOffsets<KMAJ, ROWS> t;
 #pragma unroll
-    for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
-        const int f = threadIdx.x + NT * q;
-        const long e = !KMAJ ? (long)(r0 + (f % R4) * 4) + (long)(f / R4) * ld : (long)((f & 3) * 4) + (long)(r0 + (f >> 2)) * ld;
+    for (int q = 0; q < ROWS * KQ / NT; ++q) {
+        int rr, kq;
+        cell_of<KMAJ, ROWS>(threadIdx.x + NT * q, rr, kq);
+        const long e = KMAJ ? (long)(4 * kq) + (long)(r0 + rr) * ld : (long)(r0 + rr) + (long)(4 * kq) * ld;
         t.o[q] = (uint32_t)(e * 4);
     }
     return t;
 }
 
-// soff: byte offset of K step k0 (k0 * ld * 4 for KMAJ = false, k0 * 4 for KMAJ = true)
+// soff: byte offset of K step k0 (k0 * ld * 4 for KMAJ = false, k0 * 4 for KMAJ = true);
+// ld4 = ld * 4 (the byte stride between consecutive k of a rows-contiguous operand)
 template <bool KMAJ, int ROWS>
 __device__ __forceinline__ void load_tile_full(Stage<ROWS>& st, __amdgpu_buffer_rsrc_t r, const TileOffsets<KMAJ, ROWS>& to,
-                                               uint32_t soff) {
+                                               uint32_t soff, uint32_t ld4) {
 #pragma unroll
-    for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
-        const v4f x = __builtin_amdgcn_raw_buffer_load_b128(r, to.o[q], soff, 0);
-        st.v[q] = make_float4(x.x, x.y, x.z, x.w);
+    for (int q = 0; q < ROWS * KQ / NT; ++q) {
+        if (KMAJ) {
+            const v4f x = __builtin_amdgcn_raw_buffer_load_b128(r, to.o[q], soff, 0);
+            st.v[q] = make_float4(x.x, x.y, x.z, x.w);
+        } else {
+            st.v[q].x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, to.o[q], soff, 0));
+            st.v[q].y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, to.o[q], soff + ld4, 0));
+            st.v[q].z = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, to.o[q], soff + 2 * ld4, 0));
+            st.v[q].w = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, to.o[q], soff + 3 * ld4, 0));
+        }
     }
 }
 
-// Registers -> LDS tile S[k][r] (row stride LD)
-template <bool KMAJ, int ROWS, int LD>
+// Registers -> LDS tile in the quad layout (one 16-byte store per cell)
+template <bool KMAJ, int ROWS>
 __device__ __forceinline__ void store_tile(const Stage<ROWS>& st, float* __restrict__ S) {
-    constexpr int R4 = ROWS / 4;
 #pragma unroll
-    for (int q = 0; q < ROWS * KT / 4 / NT; ++q) {
-        const int f = threadIdx.x + NT * q;
-        const float4 x = st.v[q];
-        if (!KMAJ) {
-            const int kk = f / R4, r4 = (f % R4) * 4;
-            *reinterpret_cast<float4*>(S + kk * LD + r4) = x;
-        } else {
-            const int rr = f >> 2, k4 = (f & 3) * 4;
-            S[(k4 + 0) * LD + rr] = x.x;
-            S[(k4 + 1) * LD + rr] = x.y;
-            S[(k4 + 2) * LD + rr] = x.z;
-            S[(k4 + 3) * LD + rr] = x.w;
-        }
+    for (int q = 0; q < ROWS * KQ / NT; ++q) {
+        int rr, kq;
+        cell_of<KMAJ, ROWS>(threadIdx.x + NT * q, rr, kq);
+        *reinterpret_cast<float4*>(S + kq * ldq<ROWS>() + rr * 4) = st.v[q];
     }
 }
 
 template <bool A_KM, bool B_KM, int BNT, class Epi>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
-    constexpr int LDB_S = BNT + PAD, NJ = BNT / 64;
-    __shared__ float As[2][KT * LDA_S];
-    __shared__ float Bs[2][KT * LDB_S];
+    constexpr int NJ = BNT / 64, LQA = ldq<BM>(), LQB = ldq<BNT>();
+    __shared__ __attribute__((aligned(16))) float As[2][KQ * LQA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][KQ * LQB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BNT;
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BNT / 2);
@@ -230,8 +249,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         if (fast) {
             const uint32_t sa_off = (uint32_t)((A_KM ? (long)k0 : (long)k0 * lda0) * 4);
             const uint32_t sb_off = (uint32_t)((B_KM ? (long)k0 : (long)k0 * ldb0) * 4);
-            load_tile_full<A_KM, BM>(sa[p], s1 ? rA1 : rA0, offA, sa_off);
-            load_tile_full<B_KM, BNT>(sb[p], s1 ? rB1 : rB0, offB, sb_off);
+            load_tile_full<A_KM, BM>(sa[p], s1 ? rA1 : rA0, offA, sa_off, (uint32_t)(lda0 * 4));
+            load_tile_full<B_KM, BNT>(sb[p], s1 ? rB1 : rB0, offB, sb_off, (uint32_t)(ldb0 * 4));
         } else {
             load_tile<A_KM, BM>(sa[p], A, lda, g.M, K, m0, k0, vec);
             load_tile<B_KM, BNT>(sb[p], B, ldb, g.N, K, n0, k0, vec);
@@ -242,38 +261,60 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         if (t_begin >= t_end) return;
         load(0, t_begin, FAST);
         load(1, t_begin + 1, FAST);
-        store_tile<A_KM, BM, LDA_S>(sa[0], As[0]);
-        store_tile<B_KM, BNT, LDB_S>(sb[0], Bs[0]);
+        store_tile<A_KM, BM>(sa[0], As[0]);
+        store_tile<B_KM, BNT>(sb[0], Bs[0]);
         __syncthreads();
-        // step t with p = (t - t_begin) % 2: LDS buffer p and register stage p
-        auto step = [&](int t, auto p_tag) {
-            constexpr int cur = decltype(p_tag)::value;
-            load(cur, t + 2, FAST);
-            const float* A_ = As[cur];
-            const float* B_ = Bs[cur];
-            // every fragment of the stage first (the LDS reads overlap each other), then the MFMAs
-            float a[KT / 2][2], b[KT / 2][NJ];
+        // fragments of a step in registers: F[p] is read from LDS buffer p during the step
+        // before (after its barrier), so the LDS latency hides behind half a step of MFMAs.
+        // The MFMA's k index (lane / 32) selects the k-plane: MFMA 4 h + c of the step takes
+        // k = 4 (2 h + lane / 32) + c, the same for both operands, so the KT / 2 MFMAs cover
+        // the KT k of the step once each.
+        constexpr int NH = KT / 8;
+        v4f fa[2][NH][2], fb[2][NH][NJ];  // [buffer][plane pair][tile]
+        auto read_frags = [&](auto p_tag) {
+            constexpr int p = decltype(p_tag)::value;
 #pragma unroll
-            for (int ks = 0; ks < KT / 2; ++ks) {
-                const int kk = ks * 2 + (lane >> 5);
-#pragma unroll
-                for (int i = 0; i < 2; ++i) a[ks][i] = A_[kk * LDA_S + wm + i * 32 + (lane & 31)];
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) b[ks][j] = B_[kk * LDB_S + wn + j * 32 + (lane & 31)];
-            }
-            // keep the reads ahead of the MFMAs (the scheduler would sink each read to its use
-            // and expose the LDS latency at every k step)
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int ks = 0; ks < KT / 2; ++ks)
+            for (int h = 0; h < NH; ++h) {
+                const int kq = 2 * h + (lane >> 5);
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
+                    fa[p][h][i] = *reinterpret_cast<const v4f*>(As[p] + kq * LQA + (wm + i * 32 + (lane & 31)) * 4);
 #pragma unroll
-                    for (int j = 0; j < NJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[ks][j], a[ks][i], acc[i][j], 0, 0, 0);
-            store_tile<A_KM, BM, LDA_S>(sa[cur ^ 1], As[cur ^ 1]);
-            store_tile<B_KM, BNT, LDB_S>(sb[cur ^ 1], Bs[cur ^ 1]);
+                for (int j = 0; j < NJ; ++j)
+                    fb[p][h][j] = *reinterpret_cast<const v4f*>(Bs[p] + kq * LQB + (wn + j * 32 + (lane & 31)) * 4);
+            }
+        };
+        // the MFMAs of plane pairs [h0, h1) of fragments F[p]
+        auto mma = [&](auto p_tag, int h0, int h1) {
+            constexpr int p = decltype(p_tag)::value;
+#pragma unroll
+            for (int h = h0; h < h1; ++h)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[p][h][j][c], fa[p][h][i][c], acc[i][j], 0, 0, 0);
+        };
+        read_frags(std::integral_constant<int, 0>{});
+        // step t with p = (t - t_begin) % 2: LDS buffer p, register stage p, fragments F[p].
+        // First half of the MFMAs, the next stage to LDS and the barrier, the next step's
+        // fragments, second half.
+        auto step = [&](int t, auto p_tag) {
+            constexpr int cur = decltype(p_tag)::value;
+            constexpr std::integral_constant<int, cur ^ 1> nxt{};
+            load(cur, t + 2, FAST);
+            mma(p_tag, 0, NH / 2);
+            __builtin_amdgcn_sched_barrier(0);
+            store_tile<A_KM, BM>(sa[cur ^ 1], As[cur ^ 1]);
+            store_tile<B_KM, BNT>(sb[cur ^ 1], Bs[cur ^ 1]);
             __syncthreads();
+            // a step past the slice reads its clamped reload, never used
+            read_frags(nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(p_tag, NH / 2, NH);
+            __builtin_amdgcn_sched_barrier(0);
         };
         for (int t = t_begin; t < t_end; t += 2) {
             step(t, std::integral_constant<int, 0>{});
@@ -350,23 +391,40 @@ __global__ __launch_bounds__(NT) void splitk_reduce_kernel(const float* __restri
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Tile width and K split for an M x N x K product on `cus` compute units: the wide tile
-// when it gives at least two blocks per CU, else the narrow one, split along K (slices of at
-// least 256) until there are about two blocks per CU.
+// Tile width and K split for an M x N x K product on `cus` compute units, from a cost model
+// in microseconds: the CU with the most blocks sets the time (blocks per CU x K steps per
+// block x the time of one block step, about 0.7 us for a 128 x 64 x 16 step measured on
+// MI355X), a single resident block per CU runs at about 3/4 of the rate (one wave per SIMD
+// hides no latency), and a K split costs its partial tiles' round trip through memory
+// (8 bytes per element and slice at about 5 TB/s) plus the reduction launch.  Every K slice
+// keeps at least 8 steps.  Ties go to the narrow tile and the smaller split.
 struct Plan {
     int bnt, ksplit;
 };
-#ifndef STADE_GEMM_BPC
-#define STADE_GEMM_BPC 2
+#ifndef STADE_GEMM_STEP_US
+#define STADE_GEMM_STEP_US 0.7
 #endif
 inline Plan plan(int M, int N, int Ktot, int cus) {
-    constexpr long bpc = STADE_GEMM_BPC;  // blocks per CU the plan aims for
-    const long wide = (long)((M + BM - 1) / BM) * ((N + 127) / 128);
-    if (wide >= bpc * cus) return Plan{128, 1};
-    const long narrow = (long)((M + BM - 1) / BM) * ((N + 63) / 64);
-    int ks = 1;
-    while (narrow * ks < bpc * cus && Ktot / (ks * 2) >= 256 && ks < 16) ks *= 2;
-    return Plan{64, ks};
+    const long mt = (M + BM - 1) / BM;
+    const long steps = (Ktot + KT - 1) / KT;
+    Plan best{64, 1};
+    double best_cost = 0.0;
+    for (int bnt = 64; bnt <= 128; bnt *= 2) {
+        const long tiles = mt * ((N + bnt - 1) / bnt);
+        for (int ks = 1; ks <= 16; ++ks) {
+            if (ks > 1 && steps / ks < 8) break;
+            const long per_cu = (tiles * ks + cus - 1) / cus;
+            const long st = (steps + ks - 1) / ks;
+            double cost = (double)per_cu * st * STADE_GEMM_STEP_US * (KT / 16.0) * (bnt / 64);
+            if (per_cu < 2) cost /= 0.75;
+            if (ks > 1) cost += 8.0 * ks * (double)M * N / 5e6 + 3.0;
+            if (cost < best_cost || best_cost == 0.0) {
+                best_cost = cost;
+                best = Plan{bnt, ks};
+            }
+        }
+    }
+    return best;
 }
 
 // Number of compute units of the current device (cached per process for device 0..15).
