@@ -591,13 +591,30 @@ __global__ __launch_bounds__(NT) void d1sum_kernel(D1Args a) {
     float wacc[OMAX], wdacc[OMAX], bsum = 0.f, bsumd = 0.f;
 #pragma unroll
     for (int o = 0; o < OMAX; ++o) wacc[o] = wdacc[o] = 0.f;
-#pragma unroll 4
-    for (int s = s0 + sl; s < s1; s += 4) {
+    // the wave's samples s0 + sl, s0 + sl + 4, ... in batches of SB: every load of a batch
+    // (clamped, unconditional) issued before the batch's first store, since h1b (h1bd) is
+    // reset in place and the compiler must otherwise keep each load behind the previous store
+    constexpr int SB = HV ? 8 : 16;
+    for (int sb = s0 + sl; sb < s1; sb += 4 * SB) {
+    float hv_[SB], hbv_[SB], hdv_[SB], hbdv_[SB];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+        const long k = (long)min(sb + 4 * u, s1 - 1) * H + jc;
+        hv_[u] = a.h1[k];
+        hbv_[u] = a.h1b_in[k];
+        hdv_[u] = HV ? a.h1d[k] : 0.f;
+        hbdv_[u] = HV ? a.h1bd[k] : 0.f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+        const int s = sb + 4 * u;
+        if (s >= s1) break;
         const long k = (long)s * H + jc;
-        const float h = a.h1[k];
-        const float hb = a.h1b_in[k];
-        const float hd = HV ? a.h1d[k] : 0.f;
-        const float hbd = HV ? a.h1bd[k] : 0.f;
+        const float h = hv_[u];
+        const float hb = hbv_[u];
+        const float hd = hdv_[u];
+        const float hbd = hbdv_[u];
         const float* d2 = d2s + (s - s0) * OMAX;
         const float* d2d = d2ds + (HV ? (s - s0) * OMAX : 0);
         float t = hb, td = hbd;
@@ -624,6 +641,7 @@ __global__ __launch_bounds__(NT) void d1sum_kernel(D1Args a) {
         }
         bsum += d1;
         if (HV) bsumd += d1d;
+    }
     }
 #pragma unroll
     for (int o = 0; o < OMAX; ++o) {
