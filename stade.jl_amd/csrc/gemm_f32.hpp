@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
+#include <utility>
 
 namespace stade {
 namespace gemm {
@@ -187,6 +188,15 @@ __device__ __forceinline__ void store_tile(const Stage<ROWS>& st, float* __restr
     }
 }
 
+template <int... U, class F>
+__device__ __forceinline__ void unroll_seq(std::integer_sequence<int, U...>, F&& f) {
+    (f(std::integral_constant<int, U>{}), ...);
+}
+
+#ifndef STADE_GEMM_PF
+#define STADE_GEMM_PF 2
+#endif
+
 template <bool A_KM, bool B_KM, int BNT, class Epi>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     constexpr int NJ = BNT / 64, LQA = ldq<BM>(), LQB = ldq<BNT>();
@@ -231,13 +241,14 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // two register stages: the global loads of step t+2 are issued at step t, and the stage
-    // holding step t+1 (loaded at step t-1) goes to LDS at the end of step t, so a load has
-    // two steps of matrix-core work to arrive.  Loads and stores are unconditional (a step
-    // past the slice reloads its last step, whose data is never read) so that the compiler
-    // waits only for the older stage.
-    Stage<BM> sa[2];
-    Stage<BNT> sb[2];
+    // PF register stages: the global loads of step t+PF are issued at step t, and the stage
+    // holding step t+1 (loaded at step t+1-PF) goes to LDS in the middle of step t, so a load
+    // has PF - 1 steps of matrix-core work to arrive.  Loads and stores are unconditional (a
+    // step past the slice reloads its last step, whose data is never read) so that the
+    // compiler waits only for the oldest stage.
+    constexpr int PF = STADE_GEMM_PF;
+    Stage<BM> sa[PF];
+    Stage<BNT> sb[PF];
     auto load = [&](int p, int t, bool fast) {
         t = t < t_end ? t : t_end - 1;
         const bool s1 = t >= steps0;
@@ -259,8 +270,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     auto mainloop = [&](auto fast_tag) {
         constexpr bool FAST = decltype(fast_tag)::value;
         if (t_begin >= t_end) return;
-        load(0, t_begin, FAST);
-        load(1, t_begin + 1, FAST);
+#pragma unroll
+        for (int q = 0; q < PF; ++q) load(q, t_begin + q, FAST);
         store_tile<A_KM, BM>(sa[0], As[0]);
         store_tile<B_KM, BNT>(sb[0], Bs[0]);
         __syncthreads();
@@ -298,17 +309,17 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
                             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[p][h][j][c], fa[p][h][i][c], acc[i][j], 0, 0, 0);
         };
         read_frags(std::integral_constant<int, 0>{});
-        // step t with p = (t - t_begin) % 2: LDS buffer p, register stage p, fragments F[p].
-        // First half of the MFMAs, the next stage to LDS and the barrier, the next step's
-        // fragments, second half.
-        auto step = [&](int t, auto p_tag) {
-            constexpr int cur = decltype(p_tag)::value;
+        // step t with register stage rs = (t - t_begin) % PF and LDS buffer / fragments
+        // p = (t - t_begin) % 2: first half of the MFMAs, the next stage to LDS and the
+        // barrier, the next step's fragments, second half.
+        auto step = [&](int t, auto rs_tag, auto p_tag) {
+            constexpr int rs = decltype(rs_tag)::value, cur = decltype(p_tag)::value;
             constexpr std::integral_constant<int, cur ^ 1> nxt{};
-            load(cur, t + 2, FAST);
+            load(rs, t + PF, FAST);
             mma(p_tag, 0, NH / 2);
             __builtin_amdgcn_sched_barrier(0);
-            store_tile<A_KM, BM>(sa[cur ^ 1], As[cur ^ 1]);
-            store_tile<B_KM, BNT>(sb[cur ^ 1], Bs[cur ^ 1]);
+            store_tile<A_KM, BM>(sa[(rs + 1) % PF], As[cur ^ 1]);
+            store_tile<B_KM, BNT>(sb[(rs + 1) % PF], Bs[cur ^ 1]);
             __syncthreads();
             // a step past the slice reads its clamped reload, never used
             read_frags(nxt);
@@ -316,9 +327,14 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
             mma(p_tag, NH / 2, NH);
             __builtin_amdgcn_sched_barrier(0);
         };
-        for (int t = t_begin; t < t_end; t += 2) {
-            step(t, std::integral_constant<int, 0>{});
-            if (t + 1 < t_end) step(t + 1, std::integral_constant<int, 1>{});
+        // unrolled over a whole cycle of both rings, so every index is a compile-time constant
+        constexpr int UL = PF % 2 == 0 ? PF : 2 * PF;
+        for (int t = t_begin; t < t_end; t += UL) {
+            unroll_seq(std::make_integer_sequence<int, UL>{}, [&](auto u) {
+                constexpr int U = decltype(u)::value;
+                if (U == 0 || t + U < t_end)
+                    step(t + U, std::integral_constant<int, U % PF>{}, std::integral_constant<int, U % 2>{});
+            });
         }
     };
     if (full) mainloop(std::true_type{});
