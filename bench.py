@@ -673,7 +673,7 @@ def main():
                 continue
             wl = mk()
             heavy = nm.startswith(("burgers1d", "conv3x3", "mlp2_ce"))
-            others[nm] = measure(wl, 5 if heavy else max(5, args.steps // 2), 1 if heavy else max(2, args.warmup), dev)
+            others[nm] = measure(wl, 10 if heavy else max(5, args.steps // 2), 2 if heavy else max(2, args.warmup), dev)
             if not args.no_cpu_baseline:
                 others[nm]["cpu_baseline"] = cpu_baseline(wl, budget_s=4.0, max_runs=5)
             del wl
