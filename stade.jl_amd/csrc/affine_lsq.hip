@@ -28,7 +28,9 @@ enum Mode { ADJ = 0, TAN = 1, HVP = 2 };
 template <int M>
 __global__ __launch_bounds__(NT) void rows_kernel(const double* __restrict__ w, const double* __restrict__ wd,
                                                   const double* __restrict__ x, const double* __restrict__ xd,
-                                                  double* __restrict__ P, double* __restrict__ Pd, int m, int n) {
+                                                  double* __restrict__ P, double* __restrict__ Pd, int m, int n,
+                                                  double* __restrict__ rb, double* __restrict__ rbd, double* __restrict__ RBc,
+                                                  double* __restrict__ RBdc) {
     __shared__ double part[2][4][RT];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int chunk = blockIdx.x, i = blockIdx.y * RT + lane;
@@ -63,6 +65,18 @@ __global__ __launch_bounds__(NT) void rows_kernel(const double* __restrict__ w, 
     if (wv == 0 && i < m) {
         P[(size_t)chunk * m + i] = ((part[0][0][lane] + part[0][1][lane]) + part[0][2][lane]) + part[0][3][lane];
         if (M != ADJ) Pd[(size_t)chunk * m + i] = ((part[1][0][lane] + part[1][1][lane]) + part[1][2][lane]) + part[1][3][lane];
+        // the adjoint forms: rb (rbd) staged for the column kernel and reset here, the only
+        // reader of rb in this launch, so that every column block can read the staged value
+        if (M != TAN && RBc && chunk == 0) {
+            const double v = rb[i];
+            const double vd = M == HVP ? rbd[i] : 0.0;
+            RBc[i] = v;
+            rb[i] = 0.0;
+            if (M == HVP) {
+                RBdc[i] = vd;
+                rbd[i] = 0.0;
+            }
+        }
     }
 }
 
@@ -72,32 +86,39 @@ struct FinishArgs {
     int m, nchunks;
 };
 
+// r_i = (b_i - t_i) + the chunk partials of row i in chunk order (and its tangent): chunk
+// partials 16 at a time, all loads in flight
+template <int M>
+__device__ __forceinline__ void row_value(const FinishArgs& a, int i, double& s, double& sd) {
+    s = a.b[i] - a.t[i];
+    sd = M != ADJ ? a.bd[i] - a.td[i] : 0.0;
+    for (int c0 = 0; c0 < a.nchunks; c0 += 16) {
+        double pv[16], pdv[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const size_t q = (size_t)min(c0 + c, a.nchunks - 1) * a.m + i;
+            pv[c] = a.P[q];
+            pdv[c] = M != ADJ ? a.Pd[q] : 0.0;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            if (c0 + c >= a.nchunks) break;
+            s = s + pv[c];
+            if (M != ADJ) sd = sd + pdv[c];
+        }
+    }
+}
+
+// the tangent, and the adjoint forms with no columns (n = 0)
 template <int M>
 __global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partials) {
     __shared__ double red[32];
     const int i = blockIdx.x * NT + threadIdx.x;
     double acc[2] = {0.0, 0.0};
     if (i < a.m) {
-        double s = a.b[i] - a.t[i];
-        double sd = 0.0;
-        if (M != ADJ) sd = a.bd[i] - a.td[i];
-        // chunk partials 16 at a time, all loads in flight, added in chunk order
-        for (int c0 = 0; c0 < a.nchunks; c0 += 16) {
-            double pv[16], pdv[16];
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const size_t q = (size_t)min(c0 + c, a.nchunks - 1) * a.m + i;
-                pv[c] = a.P[q];
-                pdv[c] = M != ADJ ? a.Pd[q] : 0.0;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                if (c0 + c >= a.nchunks) break;
-                s = s + pv[c];
-                if (M != ADJ) sd = sd + pdv[c];
-            }
-        }
+        double s, sd;
+        row_value<M>(a, i, s, sd);
         if (M != ADJ) {
             a.rd[i] = sd;
             acc[1] = 0.5 * ((2.0 * s) * sd);
@@ -132,21 +153,17 @@ __global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partia
     }
 }
 
+// The adjoint forms with n > 0.  Every block recomputes the row values of its 64 rows from
+// the chunk partials (r, then sb = rb + (2 r / 2) lossb with rb as staged by rows_kernel),
+// and the blocks of column chunk 0 also write r, bb, tb (and the tangents) and the row
+// tile's loss partials.
 template <int M>
 __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, const double* __restrict__ wd,
                                                   double* __restrict__ wb, double* __restrict__ wbd,
-                                                  const double* __restrict__ x, const double* __restrict__ xd,
-                                                  const double* __restrict__ S, const double* __restrict__ Sd,
+                                                  const double* __restrict__ x, const double* __restrict__ xd, FinishArgs fa,
+                                                  const double* __restrict__ RBc, const double* __restrict__ RBdc,
                                                   double* __restrict__ XP, double* __restrict__ XPd, int m, int n,
-                                                  const double* partials, int nparts, SumOuts outs) {
-    __shared__ double red[32];
-    // second stage of the loss sums of finish_kernel, in the first block
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
-        if (M == ADJ)
-            finalize_partials<1>(partials, nparts, red, outs);
-        else
-            finalize_partials<2>(partials, nparts, red, outs);
-    }
+                                                  double* __restrict__ partials) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int rtile = blockIdx.y, i = rtile * RT + lane;
     const int j0 = blockIdx.x * CT + wv * CW;
@@ -166,8 +183,43 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
         wbdv_[jj] = M == HVP ? wbd[g] : 0.0;
         xdv_[jj] = M == HVP ? xd[jc] : 0.0;
     }
-    const double si = S[ic];
-    const double sid = M == HVP ? Sd[ic] : 0.0;
+    double rv, rvd;
+    row_value<M>(fa, ic, rv, rvd);
+    const double lb = fa.lossb[0];
+    const double rbv = RBc[ic];
+    double si, sid = 0.0;
+    if (M == ADJ) {
+        si = rbv + 0.5 * (2.0 * rv) * lb;
+    } else {
+        const double h4 = 0.5 * (2.0 * rv);
+        sid = RBdc[ic] + (lb * (0.5 * (2.0 * rvd)) + h4 * fa.lossbd[0]);
+        si = rbv + h4 * lb;
+    }
+    if (blockIdx.x == 0 && wv == 0) {
+        // every destination read before any is written
+        const double bb0 = fa.bb[ic], tb0 = fa.tb[ic];
+        const double bbd0 = M == HVP ? fa.bbd[ic] : 0.0, tbd0 = M == HVP ? fa.tbd[ic] : 0.0;
+        if (live) {
+            fa.r[i] = rv;
+            fa.bb[i] = bb0 + si;
+            fa.tb[i] = tb0 + -si;
+            if (M == HVP) {
+                fa.rd[i] = rvd;
+                fa.bbd[i] = bbd0 + sid;
+                fa.tbd[i] = tbd0 + -sid;
+            }
+        }
+        double l0 = wave_sum(live ? 0.5 * (rv * rv) : 0.0);
+        double l1 = M == HVP ? wave_sum(live ? 0.5 * ((2.0 * rv) * rvd) : 0.0) : 0.0;
+        if (lane == 0) {
+            if (M == ADJ) {
+                partials[rtile] = l0;
+            } else {
+                partials[2 * rtile] = l0;
+                partials[2 * rtile + 1] = l1;
+            }
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
     double cx[CW], cxd[CW];
 #pragma unroll
@@ -201,7 +253,15 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
 template <int M>
 __global__ __launch_bounds__(NT) void xfinish_kernel(double* __restrict__ xb, double* __restrict__ xbd,
                                                      const double* __restrict__ XP, const double* __restrict__ XPd,
-                                                     int n, int mtiles) {
+                                                     int n, int mtiles, const double* partials, SumOuts outs) {
+    __shared__ double red[32];
+    // second stage of the loss sums (the column kernel's row-tile partials), in the first block
+    if (blockIdx.x == 0) {
+        if (M == ADJ)
+            finalize_partials<1>(partials, mtiles, red, outs);
+        else
+            finalize_partials<2>(partials, mtiles, red, outs);
+    }
     const int j = blockIdx.x * NT + threadIdx.x;
     if (j >= n) return;
     // row-tile partials 16 at a time, all loads in flight, added in tile order; xb (xbd) read
@@ -233,7 +293,7 @@ int32_t check_sizes(int64_t m, int64_t n, const char* fn) {
     if (m < 0 || n < 0) return set_error(STADE_HIP_EINVAL, "%s: negative size (i_m = %lld, i_n = %lld)", fn, (long long)m, (long long)n);
     if (m > (1 << 26) || n > (1 << 26) || m * n > (int64_t)1 << 34)
         return set_error(STADE_HIP_ERANGE, "%s: size out of range (i_m = %lld, i_n = %lld)", fn, (long long)m, (long long)n);
-    if ((m + NT - 1) / NT * 2 > kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: i_m too large for the workspace", fn);
+    if ((m + RT - 1) / RT * 2 > kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: i_m too large for the workspace", fn);
     return STADE_HIP_OK;
 }
 
@@ -249,8 +309,13 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
     double* base = (double*)scratch(sizeof(double) * two * (nP + nS + nX) + 256);
     if (!base) return STADE_HIP_ENOMEM;
     double *P = base, *Pd = P + nP, *S = P + two * nP, *Sd = S + nS, *XP = S + two * nS, *XPd = XP + nX;
+    // the adjoint forms with columns: rows (+ rb staged in S), columns (row values recomputed
+    // per block), xb; otherwise rows, finish, the loss sum
+    const bool fused = M != TAN && n > 0;
     if (nchunks > 0) {
-        STADE_TIMED("affine_rows", stream, rows_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, x, xd, P, Pd, (int)m, (int)n));
+        STADE_TIMED("affine_rows", stream,
+                    rows_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, x, xd, P, Pd, (int)m, (int)n, fa.rb, fa.rbd,
+                                                                              fused ? S : nullptr, Sd));
         STADE_LAUNCHED("affine rows_kernel");
     }
     fa.P = P;
@@ -259,11 +324,11 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
     fa.Sd = Sd;
     fa.m = (int)m;
     fa.nchunks = nchunks;
-    const int nfin = (int)((m + NT - 1) / NT);
-    STADE_TIMED("affine_finish", stream, finish_kernel<M><<<(unsigned)nfin, NT, 0, stream>>>(fa, ws->partials));
-    STADE_LAUNCHED("affine finish_kernel");
     SumOuts outs{{fa.loss, fa.lossd}};
-    if (M == TAN || n == 0) {
+    if (!fused) {
+        const int nfin = (int)((m + NT - 1) / NT);
+        STADE_TIMED("affine_finish", stream, finish_kernel<M><<<(unsigned)nfin, NT, 0, stream>>>(fa, ws->partials));
+        STADE_LAUNCHED("affine finish_kernel");
         if (M == ADJ)
             finalize_kernel<1><<<1, NT, 0, stream>>>(ws->partials, nfin, outs);
         else
@@ -272,10 +337,12 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
         return STADE_HIP_OK;
     }
     STADE_TIMED("affine_cols", stream,
-                cols_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, S, Sd, XP, XPd, (int)m, (int)n,
-                                                                          ws->partials, nfin, outs));
+                cols_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, fa, S, Sd, XP, XPd, (int)m, (int)n,
+                                                                          ws->partials));
     STADE_LAUNCHED("affine cols_kernel");
-    STADE_TIMED("affine_xfinish", stream, xfinish_kernel<M><<<(unsigned)((n + NT - 1) / NT), NT, 0, stream>>>(xb, xbd, XP, XPd, (int)n, mtiles));
+    STADE_TIMED("affine_xfinish", stream,
+                xfinish_kernel<M><<<(unsigned)((n + NT - 1) / NT), NT, 0, stream>>>(xb, xbd, XP, XPd, (int)n, mtiles, ws->partials,
+                                                                                     outs));
     STADE_LAUNCHED("affine xfinish_kernel");
     return STADE_HIP_OK;
 }

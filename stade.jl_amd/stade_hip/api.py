@@ -131,13 +131,20 @@ def rng_int_range(rng: Rng, n: int, lo: int, hi: int) -> np.ndarray:
 # ------------------------------------------------------------------------------------------
 
 def _stream_of(t):
+    """The raw HIP stream that torch's current stream of t's device wraps (an int)."""
     import torch
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def _arr(name: str, t, dtype, numel: int | None):
-    """Device pointer of a flat contiguous GPU tensor of the given dtype and length."""
+    """Device pointer (an int) of a flat contiguous GPU tensor of the given dtype and length.
+    The accepted case is tested first in one expression (an evaluation passes a dozen arrays,
+    so the checks are a visible part of a small call); anything else falls through to the
+    checks that name what is wrong."""
     import torch
+    if (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype is dtype and t.is_contiguous()
+            and (numel is None or t.numel() == numel)):
+        return t.data_ptr()
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name}: expected a torch tensor on a GPU, got {type(t).__name__}")
     if t.device.type != "cuda":
@@ -148,7 +155,7 @@ def _arr(name: str, t, dtype, numel: int | None):
         raise ValueError(f"{name}: tensor must be contiguous (Julia column-major data, flat)")
     if numel is not None and t.numel() != numel:
         raise ValueError(f"{name}: length {t.numel()}, expected {numel}")
-    return ctypes.c_void_p(t.data_ptr())
+    return t.data_ptr()
 
 
 def _int(name: str, v) -> int:
