@@ -39,16 +39,20 @@ struct Coef {
     double cadv, cdif, cadvd, cdifd;
 };
 
+// The generated step  un = uc - cadv * uc * (u[ip] - u[im]) + cdif * (u[ip] - 2.0 * uc + u[im])
+// and its tangent (cadv, cdif and u all carry tangents), with fused multiply-adds: 6 and 11
+// fp64 operations instead of 8 and 19; results agree with the generated order to rounding.
 __device__ __forceinline__ double step_u(double um, double uc, double up, const Coef& c) {
-    // uc - cadv * uc * (u[ip] - u[im]) + cdif * (u[ip] - 2.0 * uc + u[im])
-    return (uc - (c.cadv * uc) * (up - um)) + c.cdif * ((up - 2.0 * uc) + um);
+    const double h1 = up - um, h2 = fma(-2.0, uc, up) + um;
+    return fma(c.cdif, h2, fma(-(c.cadv * uc), h1, uc));
 }
 
 __device__ __forceinline__ double step_ud(double um, double uc, double up, double dm, double dc, double dp, const Coef& c) {
-    double h1 = up - um;
-    double h2 = (up - 2.0 * uc) + um;
-    double t = ((uc * h1) * c.cadvd + (c.cadv * h1) * dc) + (c.cadv * uc) * (dp + -dm);
-    return (dc + -t) + (h2 * c.cdifd + c.cdif * ((dp + -(2.0 * dc)) + dm));
+    const double h1 = up - um, h2 = fma(-2.0, uc, up) + um;
+    const double dh1 = dp - dm, dh2 = fma(-2.0, dc, dp) + dm;
+    // t = d(cadv uc h1) = cadvd uc h1 + cadv (dc h1 + uc dh1)
+    const double t = fma(c.cadvd * uc, h1, c.cadv * fma(dc, h1, uc * dh1));
+    return fma(c.cdif, dh2, fma(c.cdifd, h2, dc - t));
 }
 
 // ---------------------------------------------------------------------------------------
