@@ -358,7 +358,8 @@ int32_t stade_hip_affine_lsq_b(double* loss, const double* lossb, const double* 
                                const double* b, double* bb, const double* t, double* tb, double* r, double* rb,
                                int64_t i_m, int64_t i_n, hipStream_t stream) {
     if (int32_t rc = check_sizes(i_m, i_n, "stade_hip_affine_lsq_b")) return rc;
-    if (i_m > 0 && (!loss || !lossb || !w || !wb || !x || !xb || !b || !bb || !t || !tb || !r || !rb))
+    // (arrays of no elements may be null: with i_n = 0 the matrix and x are never touched)
+    if (i_m > 0 && (!loss || !lossb || !b || !bb || !t || !tb || !r || !rb || (i_n > 0 && (!w || !wb || !x || !xb))))
         return set_error(STADE_HIP_EINVAL, "stade_hip_affine_lsq_b: null pointer");
     FinishArgs fa{};
     fa.b = b; fa.t = t; fa.lossb = lossb; fa.r = r; fa.rb = rb; fa.bb = bb; fa.tb = tb; fa.loss = loss;
@@ -369,7 +370,7 @@ int32_t stade_hip_affine_lsq_d(double* loss, double* lossd, const double* w, con
                                const double* b, const double* bd, const double* t, const double* td, double* r, double* rd,
                                int64_t i_m, int64_t i_n, hipStream_t stream) {
     if (int32_t rc = check_sizes(i_m, i_n, "stade_hip_affine_lsq_d")) return rc;
-    if (i_m > 0 && (!loss || !lossd || !w || !wd || !x || !xd || !b || !bd || !t || !td || !r || !rd))
+    if (i_m > 0 && (!loss || !lossd || !b || !bd || !t || !td || !r || !rd || (i_n > 0 && (!w || !wd || !x || !xd))))
         return set_error(STADE_HIP_EINVAL, "stade_hip_affine_lsq_d: null pointer");
     FinishArgs fa{};
     fa.b = b; fa.t = t; fa.bd = bd; fa.td = td; fa.r = r; fa.rd = rd; fa.loss = loss; fa.lossd = lossd;
@@ -382,8 +383,8 @@ int32_t stade_hip_affine_lsq_hv(double* loss, const double* lossb, const double*
                                 const double* xd, double* xbd, const double* bd, double* bbd, const double* td, double* tbd,
                                 double* rd, double* rbd, hipStream_t stream) {
     if (int32_t rc = check_sizes(i_m, i_n, "stade_hip_affine_lsq_hv")) return rc;
-    if (i_m > 0 && (!loss || !lossb || !w || !wb || !x || !xb || !b || !bb || !t || !tb || !r || !rb || !lossd || !lossbd ||
-                    !wd || !wbd || !xd || !xbd || !bd || !bbd || !td || !tbd || !rd || !rbd))
+    if (i_m > 0 && (!loss || !lossb || !b || !bb || !t || !tb || !r || !rb || !lossd || !lossbd || !bd || !bbd || !td || !tbd ||
+                    !rd || !rbd || (i_n > 0 && (!w || !wb || !x || !xb || !wd || !wbd || !xd || !xbd))))
         return set_error(STADE_HIP_EINVAL, "stade_hip_affine_lsq_hv: null pointer");
     FinishArgs fa{};
     fa.b = b; fa.t = t; fa.bd = bd; fa.td = td; fa.lossb = lossb; fa.lossbd = lossbd;

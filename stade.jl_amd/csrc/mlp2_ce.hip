@@ -849,6 +849,10 @@ int32_t check(int64_t B, int64_t I, int64_t H, int64_t O, const char* fn) {
     if (H > 2048) return set_error(STADE_HIP_ERANGE, "%s: i_h = %lld exceeds 2048", fn, (long long)H);
     if (B > (1 << 24) || I > (1 << 24) || (double)B * (double)(H > I ? H : I) > 2e9)
         return set_error(STADE_HIP_ERANGE, "%s: sizes out of range", fn);
+    // with samples, an empty output layer leaves every label out of range (the generated code
+    // throws a BoundsError), and an empty hidden layer is not supported by the head kernels
+    if (B > 0 && O == 0) return set_error(STADE_HIP_ERANGE, "%s: i_out = 0 with i_b = %lld samples: every label is out of range", fn, (long long)B);
+    if (B > 0 && H == 0) return set_error(STADE_HIP_ERANGE, "%s: i_h = 0 is not supported", fn);
     return STADE_HIP_OK;
 }
 
@@ -1014,8 +1018,9 @@ int32_t stade_hip_mlp2_ce_b(float* loss, const float* lossb, const float* x, flo
                             float* h1, float* h1b, float* z, float* zb, int64_t i_b, int64_t i_in, int64_t i_h, int64_t i_out,
                             hipStream_t stream) {
     if (int32_t rc = check(i_b, i_in, i_h, i_out, "stade_hip_mlp2_ce_b")) return rc;
-    if (i_b > 0 && (!loss || !lossb || !x || !xb || !lab || !w1 || !w1b || !b1 || !b1b || !w2 || !w2b || !b2 || !b2b || !h1 ||
-                    !h1b || !z || !zb))
+    // (with i_in = 0, x and W1 have no elements and may be null)
+    if (i_b > 0 && (!loss || !lossb || !lab || !b1 || !b1b || !w2 || !w2b || !b2 || !b2b || !h1 || !h1b || !z || !zb ||
+                    (i_in > 0 && (!x || !xb || !w1 || !w1b))))
         return set_error(STADE_HIP_EINVAL, "stade_hip_mlp2_ce_b: null pointer");
     Ptrs p{};
     p.loss = loss; p.x = (float*)x; p.w1 = (float*)w1; p.b1 = (float*)b1; p.w2 = (float*)w2; p.b2 = (float*)b2; p.h1 = h1; p.z = z;
@@ -1028,8 +1033,8 @@ int32_t stade_hip_mlp2_ce_d(float* loss, float* lossd, const float* x, const flo
                             const float* b2, const float* b2d, float* h1, float* h1d, float* z, float* zd, int64_t i_b,
                             int64_t i_in, int64_t i_h, int64_t i_out, hipStream_t stream) {
     if (int32_t rc = check(i_b, i_in, i_h, i_out, "stade_hip_mlp2_ce_d")) return rc;
-    if (i_b > 0 && (!loss || !lossd || !x || !xd || !lab || !w1 || !w1d || !b1 || !b1d || !w2 || !w2d || !b2 || !b2d || !h1 ||
-                    !h1d || !z || !zd))
+    if (i_b > 0 && (!loss || !lossd || !lab || !b1 || !b1d || !w2 || !w2d || !b2 || !b2d || !h1 || !h1d || !z || !zd ||
+                    (i_in > 0 && (!x || !xd || !w1 || !w1d))))
         return set_error(STADE_HIP_EINVAL, "stade_hip_mlp2_ce_d: null pointer");
     Ptrs p{};
     p.loss = loss; p.x = (float*)x; p.w1 = (float*)w1; p.b1 = (float*)b1; p.w2 = (float*)w2; p.b2 = (float*)b2; p.h1 = h1; p.z = z;
@@ -1045,9 +1050,9 @@ int32_t stade_hip_mlp2_ce_hv(float* loss, const float* lossb, const float* x, fl
                              const float* b1d, float* b1bd, const float* w2d, float* w2bd, const float* b2d, float* b2bd,
                              float* h1d, float* h1bd, float* zd, float* zbd, hipStream_t stream) {
     if (int32_t rc = check(i_b, i_in, i_h, i_out, "stade_hip_mlp2_ce_hv")) return rc;
-    if (i_b > 0 && (!loss || !lossb || !x || !xb || !lab || !w1 || !w1b || !b1 || !b1b || !w2 || !w2b || !b2 || !b2b || !h1 ||
-                    !h1b || !z || !zb || !lossd || !lossbd || !xd || !xbd || !w1d || !w1bd || !b1d || !b1bd || !w2d || !w2bd ||
-                    !b2d || !b2bd || !h1d || !h1bd || !zd || !zbd))
+    if (i_b > 0 && (!loss || !lossb || !lab || !b1 || !b1b || !w2 || !w2b || !b2 || !b2b || !h1 || !h1b || !z || !zb || !lossd ||
+                    !lossbd || !b1d || !b1bd || !w2d || !w2bd || !b2d || !b2bd || !h1d || !h1bd || !zd || !zbd ||
+                    (i_in > 0 && (!x || !xb || !w1 || !w1b || !xd || !xbd || !w1d || !w1bd))))
         return set_error(STADE_HIP_EINVAL, "stade_hip_mlp2_ce_hv: null pointer");
     Ptrs p{};
     p.loss = loss; p.x = (float*)x; p.w1 = (float*)w1; p.b1 = (float*)b1; p.w2 = (float*)w2; p.b2 = (float*)b2; p.h1 = h1; p.z = z;

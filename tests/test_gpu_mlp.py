@@ -14,7 +14,7 @@ from helpers import run_parity
 pytestmark = pytest.mark.gpu
 
 SIZES = [(8, 5, 7, 3), (64, 40, 48, 10), (130, 129, 131, 10), (33, 17, 300, 16), (16, 8, 1100, 4),
-         (256, 784, 1024, 10)]
+         (256, 784, 1024, 10), (8, 0, 7, 3), (0, 5, 7, 3)]
 
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
@@ -33,3 +33,18 @@ def test_mlp2_ce_parity(mode, size):
     print(f"mlp2_ce_{mode} B={B} I={I} H={H} O={O}", flush=True)
     run_parity("mlp2_ce", mode, shapes, dict(i_b=B, i_in=I, i_h=H, i_out=O), precision="f32",
                int_arrays=dict(lab=lab), scales=scales)
+
+
+@pytest.mark.parametrize("size", [(4, 3, 0, 2), (4, 3, 5, 0)])
+def test_mlp2_ce_degenerate_widths_rejected(size):
+    """An empty hidden or output layer with samples is refused with a named error before any
+    launch (i_out = 0 leaves every label out of range, a BoundsError in the generated code)."""
+    import torch
+    import stade_hip
+    B, I, H, O = size
+    print(f"mlp2_ce_b degenerate B={B} I={I} H={H} O={O}", flush=True)
+    f = lambda k: torch.zeros(k, dtype=torch.float32, device="cuda")
+    lab = torch.ones(B, dtype=torch.int64, device="cuda")
+    with pytest.raises(stade_hip.StadeHipError, match="i_h = 0|i_out = 0"):
+        stade_hip.mlp2_ce_b(f(1), f(1), f(I * B), f(I * B), lab, f(H * I), f(H * I), f(H), f(H), f(O * H), f(O * H),
+                            f(O), f(O), f(H * B), f(H * B), f(O * B), f(O * B), B, I, H, O)
