@@ -318,11 +318,11 @@ class Mlp(Workload):
         self.mode, self.B, self.I, self.H, self.O = mode, B, I, H, O
         self.name = f"mlp2_ce_{mode}"
         g = 2.0 * H * I * B
-        # flops per launch of each matrix-core kernel (a two-segment launch does two products)
+        # flops per launch of each matrix-core kernel: the tangent and HVP run each pair
+        # (s1, s1d), (W1b, W1bd), (xb, xbd) as one dual launch of three products
         self.kernels = {"b": {"mlp_gemm_s1": g, "mlp_gemm_w1b": g, "mlp_gemm_xb": g},
-                        "d": {"mlp_gemm_s1": g, "mlp_gemm_s1d": 2 * g},
-                        "hv": {"mlp_gemm_s1": g, "mlp_gemm_s1d": 2 * g, "mlp_gemm_w1b": g, "mlp_gemm_w1bd": 2 * g,
-                               "mlp_gemm_xb": g, "mlp_gemm_xbd": 2 * g}}[mode]
+                        "d": {"mlp_gemm_s1d": 3 * g},
+                        "hv": {"mlp_gemm_s1d": 3 * g, "mlp_gemm_w1bd": 3 * g, "mlp_gemm_xbd": 3 * g}}[mode]
         self.kernel = next(iter(self.kernels))
 
     def _host(self, B):

@@ -197,11 +197,18 @@ __device__ __forceinline__ void unroll_seq(std::integer_sequence<int, U...>, F&&
 #define STADE_GEMM_PF 2
 #endif
 
-template <bool A_KM, bool B_KM, int BNT, class Epi>
+// DUAL: the two segments share K and their operands are read in the same K steps, giving two
+// outputs from three products,
+//   P = A0 B0,   Q = A0 B1 + A1 B0,
+// (a tangent pair such as s1 = W1 x, s1d = W1 xd + W1d x) with each operand tile loaded once.
+// The epilogue then takes both: load(m, n) returns a float2 of old values and
+// operator()(m, n, p, q, old) writes.
+template <bool A_KM, bool B_KM, int BNT, class Epi, bool DUAL = false>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     constexpr int NJ = BNT / 64, LQA = ldq<BM>(), LQB = ldq<BNT>();
-    __shared__ __attribute__((aligned(16))) float As[2][KQ * LQA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][KQ * LQB];
+    constexpr int NOP = DUAL ? 2 : 1;  // operand pairs staged per step
+    __shared__ __attribute__((aligned(16))) float As[2][NOP][KQ * LQA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][NOP][KQ * LQB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BNT;
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BNT / 2);
@@ -218,9 +225,9 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     const long lda1 = two ? g.seg[1].lda : lda0, ldb1 = two ? g.seg[1].ldb : ldb0;
     const int K1 = two ? g.seg[1].K : 0;
 
-    // the K steps of all segments, in order; this block's slice of them
+    // the K steps of all segments, in order (DUAL: of the shared K); this block's slice of them
     const int steps0 = (K0 + KT - 1) / KT;
-    const int total = steps0 + (K1 + KT - 1) / KT;
+    const int total = DUAL ? steps0 : steps0 + (K1 + KT - 1) / KT;
     const int t_begin = (int)((long)total * blockIdx.z / g.ksplit);
     const int t_end = (int)((long)total * (blockIdx.z + 1) / g.ksplit);
     // a block whose tiles all lie inside the operands (M, N and every K step) loads with no
@@ -233,13 +240,15 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     const TileOffsets<A_KM, BM> offA = tile_offsets<A_KM, BM>(lda0, m0);
     const TileOffsets<B_KM, BNT> offB = tile_offsets<B_KM, BNT>(ldb0, n0);
 
-    floatx16 acc[2][NJ];
+    floatx16 acc[NOP][2][NJ];  // DUAL: [0] P, [1] Q
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int o = 0; o < NOP; ++o)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[o][i][j][r] = 0.f;
 
     // PF register stages: the global loads of step t+PF are issued at step t, and the stage
     // holding step t+1 (loaded at step t+1-PF) goes to LDS in the middle of step t, so a load
@@ -247,24 +256,48 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     // step past the slice reloads its last step, whose data is never read) so that the
     // compiler waits only for the oldest stage.
     constexpr int PF = STADE_GEMM_PF;
-    Stage<BM> sa[PF];
-    Stage<BNT> sb[PF];
+    Stage<BM> sa[PF][NOP];
+    Stage<BNT> sb[PF][NOP];
     auto load = [&](int p, int t, bool fast) {
         t = t < t_end ? t : t_end - 1;
-        const bool s1 = t >= steps0;
-        const float* A = s1 ? A1 : A0;
-        const float* B = s1 ? B1 : B0;
-        const long lda = s1 ? lda1 : lda0, ldb = s1 ? ldb1 : ldb0;
-        const int K = s1 ? K1 : K0;
-        const int k0 = (s1 ? t - steps0 : t) * KT;
-        if (fast) {
-            const uint32_t sa_off = (uint32_t)((A_KM ? (long)k0 : (long)k0 * lda0) * 4);
-            const uint32_t sb_off = (uint32_t)((B_KM ? (long)k0 : (long)k0 * ldb0) * 4);
-            load_tile_full<A_KM, BM>(sa[p], s1 ? rA1 : rA0, offA, sa_off, (uint32_t)(lda0 * 4));
-            load_tile_full<B_KM, BNT>(sb[p], s1 ? rB1 : rB0, offB, sb_off, (uint32_t)(ldb0 * 4));
+        if constexpr (DUAL) {
+            const int k0 = t * KT;
+            if (fast) {
+                const uint32_t sa_off = (uint32_t)((A_KM ? (long)k0 : (long)k0 * lda0) * 4);
+                const uint32_t sb_off = (uint32_t)((B_KM ? (long)k0 : (long)k0 * ldb0) * 4);
+                load_tile_full<A_KM, BM>(sa[p][0], rA0, offA, sa_off, (uint32_t)(lda0 * 4));
+                load_tile_full<A_KM, BM>(sa[p][1], rA1, offA, sa_off, (uint32_t)(lda0 * 4));
+                load_tile_full<B_KM, BNT>(sb[p][0], rB0, offB, sb_off, (uint32_t)(ldb0 * 4));
+                load_tile_full<B_KM, BNT>(sb[p][1], rB1, offB, sb_off, (uint32_t)(ldb0 * 4));
+            } else {
+                load_tile<A_KM, BM>(sa[p][0], A0, lda0, g.M, K0, m0, k0, vec);
+                load_tile<A_KM, BM>(sa[p][1], A1, lda1, g.M, K0, m0, k0, vec);
+                load_tile<B_KM, BNT>(sb[p][0], B0, ldb0, g.N, K0, n0, k0, vec);
+                load_tile<B_KM, BNT>(sb[p][1], B1, ldb1, g.N, K0, n0, k0, vec);
+            }
         } else {
-            load_tile<A_KM, BM>(sa[p], A, lda, g.M, K, m0, k0, vec);
-            load_tile<B_KM, BNT>(sb[p], B, ldb, g.N, K, n0, k0, vec);
+            const bool s1 = t >= steps0;
+            const float* A = s1 ? A1 : A0;
+            const float* B = s1 ? B1 : B0;
+            const long lda = s1 ? lda1 : lda0, ldb = s1 ? ldb1 : ldb0;
+            const int K = s1 ? K1 : K0;
+            const int k0 = (s1 ? t - steps0 : t) * KT;
+            if (fast) {
+                const uint32_t sa_off = (uint32_t)((A_KM ? (long)k0 : (long)k0 * lda0) * 4);
+                const uint32_t sb_off = (uint32_t)((B_KM ? (long)k0 : (long)k0 * ldb0) * 4);
+                load_tile_full<A_KM, BM>(sa[p][0], s1 ? rA1 : rA0, offA, sa_off, (uint32_t)(lda0 * 4));
+                load_tile_full<B_KM, BNT>(sb[p][0], s1 ? rB1 : rB0, offB, sb_off, (uint32_t)(ldb0 * 4));
+            } else {
+                load_tile<A_KM, BM>(sa[p][0], A, lda, g.M, K, m0, k0, vec);
+                load_tile<B_KM, BNT>(sb[p][0], B, ldb, g.N, K, n0, k0, vec);
+            }
+        }
+    };
+    auto store = [&](int rs, int buf) {
+#pragma unroll
+        for (int o = 0; o < NOP; ++o) {
+            store_tile<A_KM, BM>(sa[rs][o], As[buf][o]);
+            store_tile<B_KM, BNT>(sb[rs][o], Bs[buf][o]);
         }
     };
     auto mainloop = [&](auto fast_tag) {
@@ -272,8 +305,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         if (t_begin >= t_end) return;
 #pragma unroll
         for (int q = 0; q < PF; ++q) load(q, t_begin + q, FAST);
-        store_tile<A_KM, BM>(sa[0], As[0]);
-        store_tile<B_KM, BNT>(sb[0], Bs[0]);
+        store(0, 0);
         __syncthreads();
         // fragments of a step in registers: F[p] is read from LDS buffer p during the step
         // before (after its barrier), so the LDS latency hides behind half a step of MFMAs.
@@ -281,21 +313,25 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         // k = 4 (2 h + lane / 32) + c, the same for both operands, so the KT / 2 MFMAs cover
         // the KT k of the step once each.
         constexpr int NH = KT / 8;
-        v4f fa[2][NH][2], fb[2][NH][NJ];  // [buffer][plane pair][tile]
+        v4f fa[2][NH][NOP][2], fb[2][NH][NOP][NJ];  // [buffer][plane pair][operand][tile]
         auto read_frags = [&](auto p_tag) {
             constexpr int p = decltype(p_tag)::value;
 #pragma unroll
             for (int h = 0; h < NH; ++h) {
                 const int kq = 2 * h + (lane >> 5);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    fa[p][h][i] = *reinterpret_cast<const v4f*>(As[p] + kq * LQA + (wm + i * 32 + (lane & 31)) * 4);
+                for (int o = 0; o < NOP; ++o) {
 #pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    fb[p][h][j] = *reinterpret_cast<const v4f*>(Bs[p] + kq * LQB + (wn + j * 32 + (lane & 31)) * 4);
+                    for (int i = 0; i < 2; ++i)
+                        fa[p][h][o][i] = *reinterpret_cast<const v4f*>(As[p][o] + kq * LQA + (wm + i * 32 + (lane & 31)) * 4);
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        fb[p][h][o][j] = *reinterpret_cast<const v4f*>(Bs[p][o] + kq * LQB + (wn + j * 32 + (lane & 31)) * 4);
+                }
             }
         };
-        // the MFMAs of plane pairs [h0, h1) of fragments F[p]
+        // the MFMAs of plane pairs [h0, h1) of fragments F[p] (DUAL: P += A0 B0,
+        // Q += A0 B1 + A1 B0; the operands are swapped, B first)
         auto mma = [&](auto p_tag, int h0, int h1) {
             constexpr int p = decltype(p_tag)::value;
 #pragma unroll
@@ -305,8 +341,13 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
-                        for (int j = 0; j < NJ; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[p][h][j][c], fa[p][h][i][c], acc[i][j], 0, 0, 0);
+                        for (int j = 0; j < NJ; ++j) {
+                            acc[0][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[p][h][0][j][c], fa[p][h][0][i][c], acc[0][i][j], 0, 0, 0);
+                            if constexpr (DUAL) {
+                                acc[1][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[p][h][1][j][c], fa[p][h][0][i][c], acc[1][i][j], 0, 0, 0);
+                                acc[1][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[p][h][0][j][c], fa[p][h][1][i][c], acc[1][i][j], 0, 0, 0);
+                            }
+                        }
         };
         read_frags(std::integral_constant<int, 0>{});
         // step t with register stage rs = (t - t_begin) % PF and LDS buffer / fragments
@@ -318,8 +359,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
             load(rs, t + PF, FAST);
             mma(p_tag, 0, NH / 2);
             __builtin_amdgcn_sched_barrier(0);
-            store_tile<A_KM, BM>(sa[(rs + 1) % PF], As[cur ^ 1]);
-            store_tile<B_KM, BNT>(sb[(rs + 1) % PF], Bs[cur ^ 1]);
+            store((rs + 1) % PF, cur ^ 1);
             __syncthreads();
             // a step past the slice reads its clamped reload, never used
             read_frags(nxt);
@@ -341,7 +381,9 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     else mainloop(std::false_type{});
     // accumulator (i, j, r): m = m0 + wm + 32 i + lane % 32,  n = n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4
     if (g.ksplit > 1) {
-        float* part = g.part + (long)blockIdx.z * g.M * g.N;
+        // slice z at part + z * NOP * M * N (DUAL: P then Q)
+        const long mn = (long)g.M * g.N;
+        float* part = g.part + (long)blockIdx.z * NOP * mn;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int m = m0 + wm + i * 32 + (lane & 31);
@@ -351,7 +393,10 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                    if (n < g.N) part[m + (long)n * g.M] = acc[i][j][r];
+                    if (n < g.N) {
+#pragma unroll
+                        for (int o = 0; o < NOP; ++o) part[o * mn + m + (long)n * g.M] = acc[o][i][j][r];
+                    }
                 }
         }
         return;
@@ -359,7 +404,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     // the epilogue's inputs (e.g. C of C += v) for the whole tile first, then the stores: the
     // output may alias them as far as the compiler knows, and interleaving would serialise one
     // memory round trip per element
-    float pre[2][NJ][16];
+    using Pre = decltype(epi.load(0, 0));
+    Pre pre[2][NJ][16];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -368,7 +414,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm + i * 32 + (lane & 31);
                 const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                pre[i][j][r] = (m < g.M && n < g.N) ? epi.load(m, n) : 0.f;
+                pre[i][j][r] = (m < g.M && n < g.N) ? epi.load(m, n) : Pre{};
             }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -379,30 +425,46 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (n < g.N) epi(m, n, acc[i][j][r], pre[i][j][r]);
+                if (n < g.N) {
+                    if constexpr (DUAL)
+                        epi(m, n, acc[0][i][j][r], acc[NOP - 1][i][j][r], pre[i][j][r]);
+                    else
+                        epi(m, n, acc[0][i][j][r], pre[i][j][r]);
+                }
             }
     }
 }
 
 // second stage of a split-K product: C(m, n) = sum over slices in order, then the epilogue
-template <class Epi>
+// (DUAL: P and Q, each summed in slice order)
+template <class Epi, bool DUAL = false>
 __global__ __launch_bounds__(NT) void splitk_reduce_kernel(const float* __restrict__ part, int ksplit, int M, int N, Epi epi) {
+    constexpr int NOP = DUAL ? 2 : 1;
     const long q = (long)blockIdx.x * NT + threadIdx.x;
     const long mn = (long)M * N;
     if (q >= mn) return;
     // every slice's value in flight at once (ksplit <= 16; indices past the last slice clamped
     // to it and never added), added in slice order
     const int m = (int)(q % M), n = (int)(q / M);
-    float v[16];
+    float v[NOP][16];
 #pragma unroll
-    for (int z = 0; z < 16; ++z) v[z] = part[q + min(z, ksplit - 1) * mn];
+    for (int o = 0; o < NOP; ++o)
+#pragma unroll
+        for (int z = 0; z < 16; ++z) v[o][z] = part[(long)min(z, ksplit - 1) * NOP * mn + o * mn + q];
     const auto old = epi.load(m, n);
     __builtin_amdgcn_sched_barrier(0);
-    float s = v[0];
+    float s[NOP];
 #pragma unroll
-    for (int z = 1; z < 16; ++z)
-        if (z < ksplit) s += v[z];
-    epi(m, n, s, old);
+    for (int o = 0; o < NOP; ++o) {
+        s[o] = v[o][0];
+#pragma unroll
+        for (int z = 1; z < 16; ++z)
+            if (z < ksplit) s[o] += v[o][z];
+    }
+    if constexpr (DUAL)
+        epi(m, n, s[0], s[NOP - 1], old);
+    else
+        epi(m, n, s[0], old);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -420,20 +482,23 @@ struct Plan {
 #ifndef STADE_GEMM_STEP_US
 #define STADE_GEMM_STEP_US 0.7
 #endif
-inline Plan plan(int M, int N, int Ktot, int cus) {
+// nout = 2 plans a dual product (three products per step over shared loads, two outputs).
+inline Plan plan(int M, int N, int Ktot, int cus, int nout = 1) {
+    const double work = nout == 2 ? 2.5 : 1.0;  // block-step time relative to a single product
     const long mt = (M + BM - 1) / BM;
     const long steps = (Ktot + KT - 1) / KT;
     Plan best{64, 1};
     double best_cost = 0.0;
-    for (int bnt = 64; bnt <= 128; bnt *= 2) {
+    // (a dual product keeps the narrow tile: with the wide one its registers allow one wave per SIMD)
+    for (int bnt = 64; bnt <= (nout == 2 ? 64 : 128); bnt *= 2) {
         const long tiles = mt * ((N + bnt - 1) / bnt);
         for (int ks = 1; ks <= 16; ++ks) {
             if (ks > 1 && steps / ks < 8) break;
             const long per_cu = (tiles * ks + cus - 1) / cus;
             const long st = (steps + ks - 1) / ks;
-            double cost = (double)per_cu * st * STADE_GEMM_STEP_US * (KT / 16.0) * (bnt / 64);
+            double cost = (double)per_cu * st * STADE_GEMM_STEP_US * (KT / 16.0) * (bnt / 64) * work;
             if (per_cu < 2) cost /= 0.75;
-            if (ks > 1) cost += 8.0 * ks * (double)M * N / 5e6 + 3.0;
+            if (ks > 1) cost += 8.0 * ks * nout * (double)M * N / 5e6 + 3.0;
             if (cost < best_cost || best_cost == 0.0) {
                 best_cost = cost;
                 best = Plan{bnt, ks};
@@ -456,11 +521,13 @@ inline int device_cus() {
     return cached[dev];
 }
 
-// Launch; returns the hipError of the launch.  `part` must hold ksplit * M * N floats when
-// the plan splits K (ask with plan() first); it may be null otherwise.
-template <bool A_KM, bool B_KM, class Epi>
+// Launch; returns the hipError of the launch.  `part` must hold ksplit * M * N floats (DUAL:
+// twice that) when the plan splits K (ask with plan() first); it may be null otherwise.  A
+// dual product takes two segments of the same K.
+template <bool A_KM, bool B_KM, class Epi, bool DUAL = false>
 hipError_t launch(Args g, Epi epi, hipStream_t stream, const Plan& p) {
     if (g.M <= 0 || g.N <= 0) return hipSuccess;
+    if (DUAL && (g.nseg != 2 || g.seg[0].K != g.seg[1].K)) return hipErrorInvalidValue;
     bool vec = true;
     for (int s = 0; s < g.nseg; ++s) {
         vec = vec && aligned16(g.seg[s].A) && aligned16(g.seg[s].B) && g.seg[s].lda % 4 == 0 && g.seg[s].ldb % 4 == 0;
@@ -477,16 +544,16 @@ hipError_t launch(Args g, Epi epi, hipStream_t stream, const Plan& p) {
     }
     if (p.bnt == 128) {
         dim3 grid((g.M + BM - 1) / BM, (g.N + 127) / 128, p.ksplit);
-        gemm_kernel<A_KM, B_KM, 128, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);
+        gemm_kernel<A_KM, B_KM, 128, Epi, DUAL><<<grid, NT, 0, stream>>>(g, vec, epi);
     } else {
         dim3 grid((g.M + BM - 1) / BM, (g.N + 63) / 64, p.ksplit);
-        gemm_kernel<A_KM, B_KM, 64, Epi><<<grid, NT, 0, stream>>>(g, vec, epi);
+        gemm_kernel<A_KM, B_KM, 64, Epi, DUAL><<<grid, NT, 0, stream>>>(g, vec, epi);
     }
     if (p.ksplit > 1) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const long mn = (long)g.M * g.N;
-        splitk_reduce_kernel<Epi><<<(unsigned)((mn + NT - 1) / NT), NT, 0, stream>>>(g.part, p.ksplit, g.M, g.N, epi);
+        splitk_reduce_kernel<Epi, DUAL><<<(unsigned)((mn + NT - 1) / NT), NT, 0, stream>>>(g.part, p.ksplit, g.M, g.N, epi);
     }
     return hipGetLastError();
 }

@@ -42,13 +42,28 @@ struct EpiTanh {  // h1 = tanh(s1), s1 = b1 + W1 x
     __device__ float load(int m, int) const { return b1[m]; }
     __device__ void operator()(int m, int n, float v, float b) const { h1[m + n * ld] = tanhf(v + b); }
 };
-struct EpiTanhD {  // h1d = (1.0 - h1^2) * s1d, s1d = b1d + W1d x + W1 xd
-    float* h1d;
-    const float* h1;
-    const float* b1d;
+// dual forward (tangent and HVP): from P = W1 x and Q = W1 xd + W1d x in one launch,
+// h1 = tanh(P + b1) and h1d = (1.0 - h1^2) * (Q + b1d)
+struct EpiTanhPair {
+    float *h1, *h1d;
+    const float *b1, *b1d;
     long ld;
-    __device__ float load(int m, int n) const { return h1[m + n * ld]; }
-    __device__ void operator()(int m, int n, float v, float h) const { h1d[m + n * ld] = (1.0f - h * h) * (v + b1d[m]); }
+    __device__ float2 load(int m, int) const { return make_float2(b1[m], b1d[m]); }
+    __device__ void operator()(int m, int n, float p, float q, float2 b) const {
+        const float h = tanhf(p + b.x);
+        h1[m + n * ld] = h;
+        h1d[m + n * ld] = (1.0f - h * h) * (q + b.y);
+    }
+};
+// dual accumulation (HVP): C += P, Cd += Q
+struct EpiAccPair {
+    float *C, *Cd;
+    long ld;
+    __device__ float2 load(int m, int n) const { return make_float2(C[m + n * ld], Cd[m + n * ld]); }
+    __device__ void operator()(int m, int n, float p, float q, float2 c) const {
+        C[m + n * ld] = c.x + p;
+        Cd[m + n * ld] = c.y + q;
+    }
 };
 struct EpiAcc {  // C += v (a shadow accumulated, as the generated code does)
     float* C;
@@ -884,22 +899,25 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     using namespace gemm;
     // tile and K-split plans of the matrix-core products (two-segment launches have twice the K)
     const int cus = device_cus();
-    const Plan p_s1 = plan(H, B, I, cus), p_s1d = plan(H, B, 2 * I, cus);
-    const Plan p_w1b = plan(H, I, B, cus), p_w1bd = plan(H, I, 2 * B, cus);
-    const Plan p_xb = plan(I, B, H, cus), p_xbd = plan(I, B, 2 * H, cus);
+    // (the tangent and the HVP form s1 with s1d, the HVP W1b with W1bd and xb with xbd, as dual
+    // products: one launch each, operand tiles shared)
+    const Plan p_s1 = plan(H, B, I, cus), p_s1d = plan(H, B, I, cus, 2);
+    const Plan p_w1b = plan(H, I, B, cus), p_w1bd = plan(H, I, B, cus, 2);
+    const Plan p_xb = plan(I, B, H, cus), p_xbd = plan(I, B, H, cus, 2);
     size_t npart = 0;
     auto need = [&](const Plan& q, long M, long N) {
         if (q.ksplit > 1) npart = std::max(npart, (size_t)q.ksplit * M * N);
     };
-    need(p_s1, H, B);
-    if (MODE != ADJ) need(p_s1d, H, B);
-    if (MODE != TAN) {
+    if (MODE == ADJ) {
+        need(p_s1, H, B);
         need(p_w1b, H, I);
         need(p_xb, I, B);
+    } else {
+        need(p_s1d, 2L * H, B);  // dual products keep two partial planes per slice
     }
     if (MODE == HVP) {
-        need(p_w1bd, H, I);
-        need(p_xbd, I, B);
+        need(p_w1bd, 2L * H, I);
+        need(p_xbd, 2L * I, B);
     }
     npart = (npart + 63) / 64 * 64;
     const size_t nlocal = hv * (nD1 + nD2) + nC + (size_t)nchunks * 2 * OMAX;
@@ -909,8 +927,9 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     float* c2part = cpart + nC;
     float* kpart = D1 + (nlocal + 63) / 64 * 64;
     int* err = (int*)(ws->dscalars + 16);
-    // forward: h1 = tanh(W1 x + b1)
-    {
+    // forward: h1 = tanh(W1 x + b1); the tangent and HVP also h1d = (1 - h1^2)(W1 xd + W1d x + b1d),
+    // as one dual product
+    if (MODE == ADJ) {
         Args g{};
         g.part = kpart;
         g.seg[0] = Seg{p.w1, p.x, H, I, I};
@@ -920,18 +939,18 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
         hipError_t e;
         STADE_TIMED("mlp_gemm_s1", stream, e = (launch<false, true>(g, EpiTanh{p.h1, p.b1, H}, stream, p_s1)));
         if (e != hipSuccess) return check_hip(e, "mlp gemm s1");
-    }
-    if (MODE != ADJ) {
+    } else {
         Args g{};
         g.part = kpart;
-        g.seg[0] = Seg{p.w1d, p.x, H, I, I};
-        g.seg[1] = Seg{p.w1, p.xd, H, I, I};
+        g.seg[0] = Seg{p.w1, p.x, H, I, I};    // A0 = W1, B0 = x
+        g.seg[1] = Seg{p.w1d, p.xd, H, I, I};  // A1 = W1d, B1 = xd
         g.nseg = 2;
         g.M = H;
         g.N = B;
         hipError_t e;
-        STADE_TIMED("mlp_gemm_s1d", stream, e = (launch<false, true>(g, EpiTanhD{p.h1d, p.h1, p.b1d, H}, stream, p_s1d)));
-        if (e != hipSuccess) return check_hip(e, "mlp gemm s1d");
+        STADE_TIMED("mlp_gemm_s1d", stream,
+                    e = (launch<false, true, EpiTanhPair, true>(g, EpiTanhPair{p.h1, p.h1d, p.b1, p.b1d, H}, stream, p_s1d)));
+        if (e != hipSuccess) return check_hip(e, "mlp gemm s1 + s1d");
     }
     HeadArgs h{};
     h.h1 = p.h1; h.w2 = p.w2; h.b2 = p.b2; h.lossb = p.lossb; h.z = p.z; h.zb = p.zb; h.h1b = p.h1b; h.D1 = D1; h.D2 = D2;
@@ -965,43 +984,43 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     STADE_TIMED("mlp_final", stream, final_kernel<MODE><<<fb, NT, 0, stream>>>(f));
     STADE_LAUNCHED("mlp final_kernel");
     if (MODE == TAN || H == 0 || I == 0) return STADE_HIP_OK;
-    // W1b += d1 x'   (M = H, N = I, K = B);  HVP: W1bd += d1 xd' + d1d x'
+    // W1b += d1 x'   (M = H, N = I, K = B);  HVP with W1bd += d1 xd' + d1d x' as one dual product
     {
         Args g{};
         g.part = kpart;
-        g.seg[0] = Seg{D1, p.x, H, I, B};
-        g.nseg = 1;
+        g.seg[0] = Seg{D1, p.x, H, I, B};  // A0 = d1, B0 = x'
         g.M = H;
         g.N = I;
         hipError_t e;
-        STADE_TIMED("mlp_gemm_w1b", stream, e = (launch<false, false>(g, EpiAcc{p.w1b, H}, stream, p_w1b)));
-        if (e != hipSuccess) return check_hip(e, "mlp gemm w1b");
-        if (MODE == HVP) {
-            g.seg[0] = Seg{D1, p.xd, H, I, B};
-            g.seg[1] = Seg{D1d, p.x, H, I, B};
+        if (MODE == ADJ) {
+            g.nseg = 1;
+            STADE_TIMED("mlp_gemm_w1b", stream, e = (launch<false, false>(g, EpiAcc{p.w1b, H}, stream, p_w1b)));
+        } else {
+            g.seg[1] = Seg{D1d, p.xd, H, I, B};  // A1 = d1d, B1 = xd'
             g.nseg = 2;
-            STADE_TIMED("mlp_gemm_w1bd", stream, e = (launch<false, false>(g, EpiAcc{p.w1bd, H}, stream, p_w1bd)));
-            if (e != hipSuccess) return check_hip(e, "mlp gemm w1bd");
+            STADE_TIMED("mlp_gemm_w1bd", stream,
+                        e = (launch<false, false, EpiAccPair, true>(g, EpiAccPair{p.w1b, p.w1bd, H}, stream, p_w1bd)));
         }
+        if (e != hipSuccess) return check_hip(e, "mlp gemm w1b");
     }
-    // Xb += W1' d1   (M = I, N = B, K = H);  HVP: Xbd += W1d' d1 + W1' d1d
+    // Xb += W1' d1   (M = I, N = B, K = H);  HVP with Xbd += W1' d1d + W1d' d1 as one dual product
     {
         Args g{};
         g.part = kpart;
-        g.seg[0] = Seg{p.w1, D1, H, H, H};
-        g.nseg = 1;
+        g.seg[0] = Seg{p.w1, D1, H, H, H};  // A0 = W1', B0 = d1
         g.M = I;
         g.N = B;
         hipError_t e;
-        STADE_TIMED("mlp_gemm_xb", stream, e = (launch<true, true>(g, EpiAcc{p.xb, I}, stream, p_xb)));
-        if (e != hipSuccess) return check_hip(e, "mlp gemm xb");
-        if (MODE == HVP) {
-            g.seg[0] = Seg{p.w1d, D1, H, H, H};
-            g.seg[1] = Seg{p.w1, D1d, H, H, H};
+        if (MODE == ADJ) {
+            g.nseg = 1;
+            STADE_TIMED("mlp_gemm_xb", stream, e = (launch<true, true>(g, EpiAcc{p.xb, I}, stream, p_xb)));
+        } else {
+            g.seg[1] = Seg{p.w1d, D1d, H, H, H};  // A1 = W1d', B1 = d1d
             g.nseg = 2;
-            STADE_TIMED("mlp_gemm_xbd", stream, e = (launch<true, true>(g, EpiAcc{p.xbd, I}, stream, p_xbd)));
-            if (e != hipSuccess) return check_hip(e, "mlp gemm xbd");
+            STADE_TIMED("mlp_gemm_xbd", stream,
+                        e = (launch<true, true, EpiAccPair, true>(g, EpiAccPair{p.xb, p.xbd, I}, stream, p_xbd)));
         }
+        if (e != hipSuccess) return check_hip(e, "mlp gemm xb");
     }
     return STADE_HIP_OK;
 }
