@@ -393,15 +393,22 @@ __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
             for (int o = 0; o < OMAX; ++o) z[i][o] = zd[i][o] = 0.f;
 #pragma unroll
         for (int q = 0; q < HPL; ++q) {
+            // the column's weights (and their tangents) read together, then used: one LDS
+            // latency per column block (with one wave per SIMD nothing else hides it)
             const int row = (lane + 64 * q) * OP;
+            float wq[OMAX], wdq[OMAX];
 #pragma unroll
             for (int o = 0; o < OMAX; ++o) {
-                const float w = W2s[row + o];
-                const float wd = (MODE != ADJ) ? W2ds[row + o] : 0.f;
+                wq[o] = W2s[row + o];
+                wdq[o] = (MODE != ADJ) ? W2ds[row + o] : 0.f;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int o = 0; o < OMAX; ++o) {
 #pragma unroll
                 for (int i = 0; i < SPW; ++i) {
-                    z[i][o] += w * h[i][q];
-                    if (MODE != ADJ) zd[i][o] += h[i][q] * wd + w * hd[i][q];
+                    z[i][o] = fmaf(wq[o], h[i][q], z[i][o]);
+                    if (MODE != ADJ) zd[i][o] = fmaf(wq[o], hd[i][q], fmaf(h[i][q], wdq[o], zd[i][o]));
                 }
             }
             // one column block's weights live at a time (the scheduler would otherwise hoist
