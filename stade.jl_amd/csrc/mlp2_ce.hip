@@ -284,7 +284,12 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
 // one LDS read of a weight serves the SPW samples.  Padded outputs carry zeros, so the o loops
 // have no branches.  Per sample the arithmetic is that of head_kernel, in the same order.
 // ---------------------------------------------------------------------------------------
-constexpr int H4NT = 256;
+// threads of a head4 block: the adjoint's 4 waves (its per-wave LDS transpose arrays fill the
+// rest of the LDS), the tangent's and HVP's 8 (two waves per SIMD beside the staged weights)
+template <int MODE>
+constexpr int h4nt() {
+    return MODE == 0 ? 256 : 512;
+}
 constexpr int SC = 128;  // samples per chunk of the column sums
 
 // sum over the 16 lanes of a DPP row (every lane of the row gets it)
@@ -297,7 +302,8 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 template <int MODE, int HPL, int SPW>
-__global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
+__global__ __launch_bounds__(h4nt<MODE>()) void head4_kernel(HeadArgs a) {
+    constexpr int H4NT = h4nt<MODE>();
     constexpr int NW = MODE == ADJ ? 1 : 2;
     constexpr int JR = 64 * HPL;
     // the adjoint reduces its lane partial sums through LDS: per wave a [64][ZW] array
@@ -312,7 +318,7 @@ __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
         // LDS row j, entry o: W2[o, j] for j < H and o < O, zero elsewhere; a thread takes whole
         // rows j = threadIdx.x + H4NT c with every load in flight at once (no index division,
         // and the padding is written with the data)
-        constexpr int RPT = JR / H4NT;
+        constexpr int RPT = (JR + H4NT - 1) / H4NT;  // (threads past row JR - 1 load and store nothing new)
         float v[RPT][OMAX], vd[RPT][OMAX];
 #pragma unroll
         for (int c = 0; c < RPT; ++c) {
@@ -332,6 +338,7 @@ __global__ __launch_bounds__(H4NT) void head4_kernel(HeadArgs a) {
 #pragma unroll
         for (int c = 0; c < RPT; ++c) {
             const int j = threadIdx.x + H4NT * c;
+            if (JR % H4NT != 0 && j >= JR) continue;
 #pragma unroll
             for (int o = 0; o < OMAX; ++o) {
                 const bool in = j < H && o < O;
@@ -965,12 +972,12 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     h.D1d = D1d; h.D2d = D2d; h.lab = p.lab; h.B = B; h.H = H; h.O = O; h.partials = ws->partials; h.err = err;
     // i_h <= 1024: the batched head, SPW samples per wave, at most one block per CU (each
     // block stages W2 once); wider layers: one wave per sample, 8 waves and 16 samples a block
-    constexpr int SPW = MODE == ADJ ? 4 : 1;
-    const unsigned hb = H <= 1024 ? (unsigned)std::min<long>(((long)B + SPW * 4 - 1) / (SPW * 4), cus)
+    constexpr int SPW = MODE == ADJ ? 4 : 1, H4W = h4nt<MODE>() / 64;
+    const unsigned hb = H <= 1024 ? (unsigned)std::min<long>(((long)B + SPW * H4W - 1) / (SPW * H4W), cus)
                                   : (unsigned)((B + 16 - 1) / 16);
     STADE_TIMED("mlp_head", stream, {
-        if (H <= 256) head4_kernel<MODE, 4, SPW><<<hb, H4NT, 0, stream>>>(h);
-        else if (H <= 1024) head4_kernel<MODE, 16, SPW><<<hb, H4NT, 0, stream>>>(h);
+        if (H <= 256) head4_kernel<MODE, 4, SPW><<<hb, h4nt<MODE>(), 0, stream>>>(h);
+        else if (H <= 1024) head4_kernel<MODE, 16, SPW><<<hb, h4nt<MODE>(), 0, stream>>>(h);
         else launch_head<MODE, 32>(h, hb, stream);
     });
     STADE_LAUNCHED("mlp head_kernel");
