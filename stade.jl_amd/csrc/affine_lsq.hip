@@ -110,12 +110,16 @@ __device__ __forceinline__ void row_value(const FinishArgs& a, int i, double& s,
     }
 }
 
-// the tangent, and the adjoint forms with no columns (n = 0)
-template <int M>
-__global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partials) {
+// the tangent, and the adjoint forms with no columns (n = 0).  BT threads a block, RPB rows a
+// thread (rows i, i + BT * grid, ...).  A single block (m <= BT * RPB) adds the loss terms into
+// the outputs itself; otherwise each block writes partials for a second-stage sum.
+template <int M, int BT, int RPB>
+__global__ __launch_bounds__(BT) void finish_kernel(FinishArgs a, double* partials, SumOuts outs) {
     __shared__ double red[32];
-    const int i = blockIdx.x * NT + threadIdx.x;
     double acc[2] = {0.0, 0.0};
+#pragma unroll
+    for (int rr = 0; rr < RPB; ++rr) {
+    const int i = blockIdx.x * BT + threadIdx.x + rr * BT * gridDim.x;
     if (i < a.m) {
         double s, sd;
         row_value<M>(a, i, s, sd);
@@ -145,7 +149,17 @@ __global__ __launch_bounds__(NT) void finish_kernel(FinishArgs a, double* partia
             a.tb[i] = a.tb[i] + -rbt;
         }
     }
-    if (M == ADJ) {
+    }
+    if (gridDim.x == 1) {
+        // one block: the loss (and its tangent) straight into the outputs
+        block_sum<2>(acc, red);
+        if (threadIdx.x == 0) {
+            const double l0 = outs.p[0][0];
+            const double l1 = M != ADJ ? outs.p[1][0] : 0.0;
+            outs.p[0][0] = l0 + acc[0];
+            if (M != ADJ) outs.p[1][0] = l1 + acc[1];
+        }
+    } else if (M == ADJ) {
         double v[1] = {acc[0]};
         block_partials<1>(v, red, partials);
     } else {
@@ -326,8 +340,14 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
     fa.nchunks = nchunks;
     SumOuts outs{{fa.loss, fa.lossd}};
     if (!fused) {
+        if (m <= 4 * 1024) {
+            // one 1024-thread block, up to 4 rows a thread, sums the loss itself
+            STADE_TIMED("affine_finish", stream, finish_kernel<M, 1024, 4><<<1, 1024, 0, stream>>>(fa, ws->partials, outs));
+            STADE_LAUNCHED("affine finish_kernel");
+            return STADE_HIP_OK;
+        }
         const int nfin = (int)((m + NT - 1) / NT);
-        STADE_TIMED("affine_finish", stream, finish_kernel<M><<<(unsigned)nfin, NT, 0, stream>>>(fa, ws->partials));
+        STADE_TIMED("affine_finish", stream, finish_kernel<M, NT, 1><<<(unsigned)nfin, NT, 0, stream>>>(fa, ws->partials, outs));
         STADE_LAUNCHED("affine finish_kernel");
         if (M == ADJ)
             finalize_kernel<1><<<1, NT, 0, stream>>>(ws->partials, nfin, outs);

@@ -5,7 +5,8 @@ from helpers import run_parity
 
 pytestmark = pytest.mark.gpu
 
-SIZES = [(1, 1), (3, 5), (64, 64), (65, 130), (200, 77), (1, 300), (300, 1), (1024, 1024), (4, 0), (0, 3)]
+SIZES = [(1, 1), (3, 5), (64, 64), (65, 130), (200, 77), (1, 300), (300, 1), (1024, 1024), (4, 0), (0, 3),
+         (5000, 3), (5000, 0)]
 
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
