@@ -33,6 +33,7 @@ namespace stade {
 namespace {
 
 constexpr int NT = 256, KMAX = 32;
+constexpr int kInitBlockCells = NT * 8;  // cells per block of the backward init kernel
 constexpr int BNT = 1024;  // threads of the forward and backward chunk kernels (16 waves per CU)
 
 struct Coef {
@@ -114,26 +115,47 @@ __global__ __launch_bounds__(NT) void bwd_init_kernel(const double* __restrict__
     const double lb = lossb[0];
     const double lbd = HV ? lossbd[0] : 0.0;
     double acc[2] = {0.0, 0.0};
-    for (int x = blockIdx.x * NT + threadIdx.x; x < n; x += gridDim.x * NT) {
-        double u = uT[x];
-        acc[0] += u * u;
-        double g = ub[x] + (2.0 * u) * lb;
-        double gd = 0.0;
-        if (HV) {
-            double ud = udT[x];
-            acc[1] += (2.0 * u) * ud;
-            gd = ubd[x] + (lb * (2.0 * ud) + (2.0 * u) * lbd);
+    // the thread's cells x, x + stride, ... in groups of CPT: every read of a group (clamped,
+    // unconditional) before its first store, the sums in the same cell order
+    constexpr int CPT = kInitBlockCells / NT;
+    const int stride = gridDim.x * NT;
+    for (int x0 = blockIdx.x * NT + threadIdx.x; x0 < n; x0 += stride * CPT) {
+        double uv[CPT], ubv[CPT], unbv[CPT], udv[CPT], ubdv[CPT], unbdv[CPT];
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int xc = min(x0 + k * stride, n - 1);
+            uv[k] = uT[xc];
+            ubv[k] = ub[xc];
+            unbv[k] = ran ? unb[xc] : 0.0;
+            udv[k] = HV ? udT[xc] : 0.0;
+            ubdv[k] = HV ? ubd[xc] : 0.0;
+            unbdv[k] = (HV && ran) ? unbd[xc] : 0.0;
         }
-        if (ran) {
-            w[x] = unb[x] + g;
-            unb[x] = 0.0;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int x = x0 + k * stride;
+            if (x >= n) break;
+            const double u = uv[k];
+            acc[0] += u * u;
+            const double g = ubv[k] + (2.0 * u) * lb;
+            double gd = 0.0;
             if (HV) {
-                wd[x] = unbd[x] + gd;
-                unbd[x] = 0.0;
+                const double ud = udv[k];
+                acc[1] += (2.0 * u) * ud;
+                gd = ubdv[k] + (lb * (2.0 * ud) + (2.0 * u) * lbd);
             }
-        } else {
-            ub[x] = g;
-            if (HV) ubd[x] = gd;
+            if (ran) {
+                w[x] = unbv[k] + g;
+                unb[x] = 0.0;
+                if (HV) {
+                    wd[x] = unbdv[k] + gd;
+                    unbd[x] = 0.0;
+                }
+            } else {
+                ub[x] = g;
+                if (HV) ubd[x] = gd;
+            }
         }
     }
     if (HV) {
@@ -436,9 +458,11 @@ __global__ __launch_bounds__(BNT) void bwd_reg_kernel(const double* __restrict__
 }
 
 // second stage of the reverse sweep's sums: block 0 the loss (init kernel's partials),
-// block 1 the coefficient shadows (all backward chunks' partials, in chunk order)
+// block 1 the coefficient shadows (all backward chunks' partials, in chunk order); 1024
+// threads a block, so that a few partials a thread are all in flight at once
+constexpr int FNT = 1024;
 template <bool HV>
-__global__ __launch_bounds__(NT) void bwd_finalize_kernel(const double* pinit, int ninit, SumOuts loss_out,
+__global__ __launch_bounds__(FNT) void bwd_finalize_kernel(const double* pinit, int ninit, SumOuts loss_out,
                                                           const double* pbwd, int nbwd, SumOuts scal_out) {
     __shared__ double red[64];
     if (blockIdx.x == 0) {
@@ -538,7 +562,6 @@ int32_t forward(const double* src, const double* srcd, double* fin, double* find
 }
 
 // reduction partials: the init kernel's at offset 0, the backward chunks' after it
-constexpr int kInitBlockCells = NT * 8;
 int init_blocks(int64_t n) { return (int)grid_for((int)n, kInitBlockCells); }
 size_t bwd_offset(int64_t n) { return ((size_t)init_blocks(n) * 2 + 1023) / 1024 * 1024; }
 template <bool HV>
@@ -662,7 +685,7 @@ int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u
             if (int32_t rc = backward<false>(P, nullptr, Q, nullptr, ub, nullptr, u_stack, nullptr, (int)n, nrun, c, pbwd, &nparts, stream)) return rc;
         }
         STADE_TIMED("finalize", stream,
-                    bwd_finalize_kernel<false><<<2, NT, 0, stream>>>(ws->partials, gi, SumOuts{{loss}}, pbwd, nparts,
+                    bwd_finalize_kernel<false><<<2, FNT, 0, stream>>>(ws->partials, gi, SumOuts{{loss}}, pbwd, nparts,
                                                                      SumOuts{{ws->dscalars + 0, ws->dscalars + 1}}));
         STADE_LAUNCHED("burgers1d bwd_finalize_kernel");
         double* hs;
@@ -769,7 +792,7 @@ int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* 
             if (int32_t rc = backward<true>(P, Pd, Q, Qd, ub, ubd, u_stack, taped, (int)n, nrun, c, pbwd, &nparts, stream)) return rc;
         }
         STADE_TIMED("finalize", stream,
-                    bwd_finalize_kernel<true><<<2, NT, 0, stream>>>(ws->partials, gi, SumOuts{{loss, lossd}}, pbwd, nparts,
+                    bwd_finalize_kernel<true><<<2, FNT, 0, stream>>>(ws->partials, gi, SumOuts{{loss, lossd}}, pbwd, nparts,
                                                                     SumOuts{{ws->dscalars + 0, ws->dscalars + 1,
                                                                              ws->dscalars + 2, ws->dscalars + 3}}));
         STADE_LAUNCHED("burgers1d bwd_finalize_kernel");
