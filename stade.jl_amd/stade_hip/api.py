@@ -131,9 +131,13 @@ def rng_int_range(rng: Rng, n: int, lo: int, hi: int) -> np.ndarray:
 # ------------------------------------------------------------------------------------------
 
 def _stream_of(t):
-    """The raw HIP stream that torch's current stream of t's device wraps (an int)."""
+    """The raw HIP stream that torch's current stream of t's device wraps (an int).  torch's
+    raw-stream query is used where it exists (it skips building a Stream object per call)."""
     import torch
-    return torch._C._cuda_getCurrentRawStream(t.get_device())
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw(t.get_device())
+    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _arr(name: str, t, dtype, numel: int | None):
