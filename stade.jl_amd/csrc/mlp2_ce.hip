@@ -901,17 +901,14 @@ void launch_head(const HeadArgs& h, unsigned blocks, hipStream_t stream) {
 template <int MODE>
 int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipStream_t stream) {
     const int B = (int)B_, I = (int)I_, H = (int)H_, O = (int)O_;
-    if (B == 0 || H == 0) {
-        // no sample or no hidden unit: the loss loops still run over samples (with h1 empty)
-        if (B == 0) return STADE_HIP_OK;
-    }
+    if (B == 0) return STADE_HIP_OK;  // (i_h = 0 and i_out = 0 with samples are refused by check)
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
     const int nchunks = (B + SC - 1) / SC;
     const size_t nD1 = (size_t)H * B, nD2 = (size_t)O * B, nC = (size_t)nchunks * 2 * (O + 1) * H;
     const int hv = MODE == HVP ? 2 : 1;
     using namespace gemm;
-    // tile and K-split plans of the matrix-core products (two-segment launches have twice the K)
+    // tile and K-split plans of the matrix-core products
     const int cus = device_cus();
     // (the tangent and the HVP form s1 with s1d, the HVP W1b with W1bd and xb with xbd, as dual
     // products: one launch each, operand tiles shared)
