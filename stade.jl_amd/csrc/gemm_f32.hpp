@@ -9,22 +9,23 @@
 //   A_KM = false: A(m, k) at A[m + k * lda] (m contiguous);  A_KM = true: at A[k + m * lda]
 //   B_KM = true:  B(k, n) at B[k + n * ldb] (k contiguous);  B_KM = false: at B[n + k * ldb]
 // Up to two segments accumulate into one tile, so a tangent product such as
-// W1d * X + W1 * Xd is one launch.
+// W1d * X + W1 * Xd is one launch.  A dual launch instead reads both segments in the same K
+// steps and writes two outputs, P = A0 B0 and Q = A0 B1 + A1 B0 (a product with its tangent).
 //
 // Tiling: a 256-thread block (4 waves) computes a 128 x BNT tile of C (BNT = 128 or 64);
 // each wave a 64 x BNT/2 part as 2 x BNT/64 MFMA 32 x 32 tiles.  K advances 16 at a time
 // through two LDS buffers (one barrier per step: the next tile's global loads are issued
-// before the MFMAs of the current one and stored to the other buffer after them).  Operand
-// tiles sit in LDS in a k-quad layout (below), read as one 128-bit fragment per 4 MFMAs.
-// The MFMA operands are swapped (B tile as the matrix-core A
-// operand) so that the accumulator's lane index runs along m: each epilogue store of a wave
-// covers 32 consecutive rows of a column-major C, a 128-byte segment.
+// in the middle of the current one's MFMAs and stored to the other buffer, and the next
+// step's fragments are read right after the barrier).  Operand tiles sit in LDS in a k-quad
+// layout (below), read as one 128-bit fragment per 4 MFMAs.  The MFMA operands are swapped
+// (B tile as the matrix-core A operand) so that the accumulator's lane index runs along m:
+// each epilogue store of a wave covers 32 consecutive rows of a column-major C, a 128-byte
+// segment.
 //
 // Split K: with `ksplit` > 1 the K steps (of all segments, in order) are cut into ksplit
 // contiguous ranges, one per blockIdx.z; each writes its partial tile to a scratch slice
 // and a second kernel adds the slices in slice order and applies the epilogue.  The host
-// picks the narrow tile and the split so that small-M*N products still give every CU about
-// two blocks.
+// picks the tile width and the split from a cost model (plan()).
 #pragma once
 
 #include <hip/hip_runtime.h>
