@@ -14,9 +14,10 @@
 //
 // Tiling: a 256-thread block (4 waves) computes a 128 x BNT tile of C (BNT = 128 or 64);
 // each wave a 64 x BNT/2 part as 2 x BNT/64 MFMA 32 x 32 tiles.  K advances 16 at a time
-// through two LDS buffers (one barrier per step: the next tile's global loads are issued
-// in the middle of the current one's MFMAs and stored to the other buffer, and the next
-// step's fragments are read right after the barrier).  Operand tiles sit in LDS in a k-quad
+// through two LDS buffers (one barrier per step: a later step's global loads are issued as a
+// step starts, the next step's stage goes to the other buffer between the two halves of the
+// step's MFMAs, and the next step's fragments are read right after the barrier).  Operand
+// tiles sit in LDS in a k-quad
 // layout (below), read as one 128-bit fragment per 4 MFMAs.  The MFMA operands are swapped
 // (B tile as the matrix-core A operand) so that the accumulator's lane index runs along m:
 // each epilogue store of a wave covers 32 consecutive rows of a column-major C, a 128-byte
