@@ -17,8 +17,8 @@
 // through two LDS buffers (one barrier per step: a later step's global loads are issued as a
 // step starts, the next step's stage goes to the other buffer between the two halves of the
 // step's MFMAs, and the next step's fragments are read right after the barrier).  Operand
-// tiles sit in LDS in a k-quad
-// layout (below), read as one 128-bit fragment per 4 MFMAs.  The MFMA operands are swapped
+// tiles sit in LDS in a k-quad layout (below), read as one 128-bit fragment per 4 MFMAs.
+// The MFMA operands are swapped
 // (B tile as the matrix-core A operand) so that the accumulator's lane index runs along m:
 // each epilogue store of a wave covers 32 consecutive rows of a column-major C, a 128-byte
 // segment.
