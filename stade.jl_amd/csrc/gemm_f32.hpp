@@ -18,10 +18,9 @@
 // step starts, the next step's stage goes to the other buffer between the two halves of the
 // step's MFMAs, and the next step's fragments are read right after the barrier).  Operand
 // tiles sit in LDS in a k-quad layout (below), read as one 128-bit fragment per 4 MFMAs.
-// The MFMA operands are swapped
-// (B tile as the matrix-core A operand) so that the accumulator's lane index runs along m:
-// each epilogue store of a wave covers 32 consecutive rows of a column-major C, a 128-byte
-// segment.
+// The MFMA operands are swapped (B tile as the matrix-core A operand) so that the
+// accumulator's lane index runs along m: each epilogue store of a wave covers 32 consecutive
+// rows of a column-major C, a 128-byte segment.
 //
 // Split K: with `ksplit` > 1 the K steps (of all segments, in order) are cut into ksplit
 // contiguous ranges, one per blockIdx.z; each writes its partial tile to a scratch slice
