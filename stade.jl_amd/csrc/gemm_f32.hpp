@@ -333,6 +333,14 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
         };
         // the MFMAs of plane pairs [h0, h1) of fragments F[p] (DUAL: P += A0 B0,
         // Q += A0 B1 + A1 B0; the operands are swapped, B first)
+        // (a tile edge block skips the MFMAs of its 32 x 32 tiles that lie wholly past M or N:
+        // wave-uniform tests, compile-time true in whole blocks; those accumulators stay zero
+        // and are never stored)
+        bool live_i[2], live_j[NJ];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) live_i[i] = FAST || m0 + wm + 32 * i < g.M;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) live_j[j] = FAST || n0 + wn + 32 * j < g.N;
         auto mma = [&](auto p_tag, int h0, int h1) {
             constexpr int p = decltype(p_tag)::value;
 #pragma unroll
@@ -343,6 +351,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
                         for (int j = 0; j < NJ; ++j) {
+                            if (!(live_i[i] && live_j[j])) continue;
                             acc[0][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[p][h][0][j][c], fa[p][h][0][i][c], acc[0][i][j], 0, 0, 0);
                             if constexpr (DUAL) {
                                 acc[1][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[p][h][1][j][c], fa[p][h][0][i][c], acc[1][i][j], 0, 0, 0);
