@@ -8,8 +8,9 @@
 // owner-computes gather (`cgen_gather_periodic_inverse` 7343-7529) for the adjoint scatter.
 //
 // Two kernel families:
-//   * wave-strip kernels (n a multiple of 64, the benchmark grids): one wavefront per strip of
-//     64 columns and a chunk of rows, no LDS and no barriers (described at their definition);
+//   * wave-strip kernels: one wavefront per strip of 128 columns (n a multiple of 128, the
+//     benchmark grids; 16-byte accesses) or of 64 columns (n a multiple of 64 only) and a chunk
+//     of rows, no LDS and no barriers (described at their definition);
 //   * row-streaming kernels (every other n), described next.
 //
 // Row-streaming layout and work per launch:
@@ -351,6 +352,15 @@ __global__ __launch_bounds__(NT) void zero2_kernel(double* __restrict__ a, doubl
 #ifndef STADE_DIFF_WD_HV
 #define STADE_DIFF_WD_HV 4
 #endif
+#ifndef STADE_DIFF_WCH2
+#define STADE_DIFF_WCH2 64
+#endif
+#ifndef STADE_DIFF_WCH2_HV
+#define STADE_DIFF_WCH2_HV 64
+#endif
+#ifndef STADE_DIFF_WD2_HV
+#define STADE_DIFF_WD2_HV 2
+#endif
 // rows per wave and rows of loads in flight ahead of the row being computed; measured at
 // n = 4096: 64 rows beat 32 for the adjoint and the tangent (fewer halo rows), while the
 // HVP, with twice the values per row, keeps 32 rows to stay in registers (at 64 it spills).
@@ -559,6 +569,243 @@ __global__ __launch_bounds__(256) void diffusion_b_wave(const double* __restrict
     }
 }
 
+// 128-column strips: lane l owns columns c0 + 2l and c0 + 2l + 1 and moves them as one
+// 16-byte load or store, so a row of a strip is 1 KB (eight cache lines) and the strip's two
+// halo lines add a quarter instead of a half.  East / west of the pair come from the pair
+// itself and from the adjacent lane; the halo lanes are as in the 64-column kernels (columns
+// c0-2, c0-1, c0+128, c0+129).  Operation order per cell is the same as there.  The row loops
+// are unrolled by static_for: at 64 rows the bodies exceed the compiler's unroll threshold,
+// and a rolled loop would move the register arrays to scratch memory.
+constexpr int WS2 = 128;
+// rows per wave and rows of loads in flight, measured at n = 4096: the adjoint and the
+// tangent as on 64-column strips; the HVP, with twice the values per row, runs 64 rows with
+// two rows in flight (178 VGPRs, two waves a SIMD; four rows in flight take 256 VGPRs and one
+// wave a SIMD, 10 % slower)
+constexpr int WCH2 = STADE_DIFF_WCH2;        // adjoint, tangent
+constexpr int WCH2_HV = STADE_DIFF_WCH2_HV;  // HVP
+constexpr int WD2_HV = STADE_DIFF_WD2_HV;
+static_assert(WS2 % WCH2 == 0 && WS2 % WCH2_HV == 0, "n % 128 == 0 must imply n % rows == 0");
+
+struct WaveGeom2 {
+    int lane, c0, j0, oc, hc;
+};
+__device__ __forceinline__ WaveGeom2 wave_geom2(int wid, int n, int nstrips, int rows) {
+    WaveGeom2 g;
+    g.lane = threadIdx.x & 63;
+    g.c0 = (wid % nstrips) * WS2;
+    g.j0 = (wid / nstrips) * rows;
+    g.oc = g.c0 + 2 * g.lane;
+    g.hc = wrap1(g.c0 + (g.lane == 0 ? -2 : (g.lane == 1 ? -1 : (g.lane == 2 ? WS2 : WS2 + 1))), n);
+    return g;
+}
+// the pair holding element (row base rb, column oc) of a double array; rb and oc are even
+__device__ __forceinline__ size_t pair_of(size_t rb, int oc) { return (rb + oc) >> 1; }
+
+// 5-point step of the pair (x: column oc, y: oc + 1) from the rows above and below and the
+// halo columns hw (oc - 1 of lane 0) and he (oc + 2 of lane 63)
+template <bool TANGENT>
+__device__ __forceinline__ double2 step_pair(double2 up, double2 c, double2 dn, double hw, double he) {
+    double2 v;
+    if constexpr (TANGENT) {
+        v.x = step5dv(up.x, c.x, dn.x, from_west(c.y, hw), c.y);
+        v.y = step5dv(up.y, c.y, dn.y, c.x, from_east(c.x, he));
+    } else {
+        v.x = step5v(up.x, c.x, dn.x, from_west(c.y, hw), c.y);
+        v.y = step5v(up.y, c.y, dn.y, c.x, from_east(c.x, he));
+    }
+    return v;
+}
+
+// tangent: un, und of rows j0 .. j0+ROWS-1 from u, ud rows j0-1 .. j0+ROWS
+template <int ROWS, int D>
+__global__ __launch_bounds__(256) void diffusion_d_wave2(const double* __restrict__ u, const double* __restrict__ ud,
+                                                         double* __restrict__ un, double* __restrict__ und, int n,
+                                                         int nstrips, int nwaves, double* partials) {
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= nwaves) return;  // whole waves only; the kernel has no barrier
+    const WaveGeom2 g = wave_geom2(wid, n, nstrips, ROWS);
+    const double2* __restrict__ u2 = reinterpret_cast<const double2*>(u);
+    const double2* __restrict__ ud2 = reinterpret_cast<const double2*>(ud);
+    double2* __restrict__ un2 = reinterpret_cast<double2*>(un);
+    double2* __restrict__ und2 = reinterpret_cast<double2*>(und);
+    double2 U[ROWS + 2], UD[ROWS + 2];  // row q at index q + 1
+    double H[ROWS + 2], HD[ROWS + 2];
+    auto load = [&](int q) {
+        const size_t rb = (size_t)wrap1(g.j0 + q, n) * n;
+        U[q + 1] = u2[pair_of(rb, g.oc)];
+        H[q + 1] = u[rb + g.hc];
+        UD[q + 1] = ud2[pair_of(rb, g.oc)];
+        HD[q + 1] = ud[rb + g.hc];
+    };
+    load(-1);
+    load(0);
+#pragma unroll
+    for (int k = 1; k <= D; ++k) load(k);
+    double acc[2] = {0.0, 0.0};
+    static_for<ROWS>([&](auto rc) {
+        constexpr int r = decltype(rc)::value, i = r + 1;
+        if constexpr (r + D + 1 <= ROWS) load(r + D + 1);
+        const double2 v = step_pair<false>(U[i - 1], U[i], U[i + 1], lane_val(H[i], 1), lane_val(H[i], 2));
+        const double2 vd = step_pair<true>(UD[i - 1], UD[i], UD[i + 1], lane_val(HD[i], 1), lane_val(HD[i], 2));
+        const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
+        und2[gp] = vd;
+        un2[gp] = v;
+        acc[1] += (2.0 * v.x) * vd.x;
+        acc[0] += v.x * v.x;
+        acc[1] += (2.0 * v.y) * vd.y;
+        acc[0] += v.y * v.y;
+    });
+    acc[0] = wave_sum(acc[0]);
+    acc[1] = wave_sum(acc[1]);
+    if (g.lane == 0) {
+        partials[(size_t)wid * 2] = acc[0];
+        partials[(size_t)wid * 2 + 1] = acc[1];
+    }
+}
+
+// adjoint pass 1 (HV = false) and its tangent (HV = true): un (+ und) of the wave's rows,
+// loss partials, and the gather of w = unb + (2 un) lossb (+ wd) into ub (+ ubd)
+template <bool HV, int ROWS, int D>
+__global__ __launch_bounds__(256) void diffusion_b_wave2(const double* __restrict__ u, const double* __restrict__ ud,
+                                                         double* __restrict__ un, double* __restrict__ und,
+                                                         const double* __restrict__ unb, const double* __restrict__ unbd,
+                                                         double* __restrict__ ub, double* __restrict__ ubd,
+                                                         const double* __restrict__ lossb, const double* __restrict__ lossbd,
+                                                         int n, int nstrips, int nwaves, double* partials) {
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= nwaves) return;  // whole waves only; the kernel has no barrier
+    const WaveGeom2 g = wave_geom2(wid, n, nstrips, ROWS);
+    const double lb = lossb[0];
+    const double lbd = HV ? lossbd[0] : 0.0;
+    const double2* __restrict__ u2 = reinterpret_cast<const double2*>(u);
+    const double2* __restrict__ ud2 = reinterpret_cast<const double2*>(ud);
+    const double2* __restrict__ unb2 = reinterpret_cast<const double2*>(unb);
+    const double2* __restrict__ unbd2 = reinterpret_cast<const double2*>(unbd);
+    double2* __restrict__ un2 = reinterpret_cast<double2*>(un);
+    double2* __restrict__ und2 = reinterpret_cast<double2*>(und);
+    double2* __restrict__ ub2 = reinterpret_cast<double2*>(ub);
+    double2* __restrict__ ubd2 = reinterpret_cast<double2*>(ubd);
+    // u rows -2 .. ROWS+1 at index q + 2; unb rows -1 .. ROWS at q + 1; ub rows 0 .. ROWS-1
+    double2 U[ROWS + 4], B[ROWS + 2], UB[ROWS];
+    double H[ROWS + 4], BH[ROWS + 2];
+    double2 UD[HV ? ROWS + 4 : 1], BD[HV ? ROWS + 2 : 1], UBD[HV ? ROWS : 1];
+    double HD[HV ? ROWS + 4 : 1], BHD[HV ? ROWS + 2 : 1];
+    auto rowb = [&](int q) { return (size_t)wrap1(g.j0 + q, n) * n; };
+    auto load_u = [&](int q) {
+        const size_t rb = rowb(q);
+        U[q + 2] = u2[pair_of(rb, g.oc)];
+        H[q + 2] = u[rb + g.hc];
+        if constexpr (HV) {
+            UD[q + 2] = ud2[pair_of(rb, g.oc)];
+            HD[q + 2] = ud[rb + g.hc];
+        }
+    };
+    auto load_b = [&](int q) {
+        const size_t rb = rowb(q);
+        B[q + 1] = unb2[pair_of(rb, g.oc)];
+        BH[q + 1] = unb[rb + g.hc];
+        if constexpr (HV) {
+            BD[q + 1] = unbd2[pair_of(rb, g.oc)];
+            BHD[q + 1] = unbd[rb + g.hc];
+        }
+    };
+    // the loads that step r consumes last: u row r+2, unb row r+1, ub row r
+    auto load_group = [&](int r) {
+        load_u(r + 2);
+        load_b(r + 1);
+        const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
+        UB[r] = ub2[gp];
+        if constexpr (HV) UBD[r] = ubd2[gp];
+    };
+    // w of rows -1 .. ROWS (own pair) and of the edge columns c0-1 (west) and c0+128 (east)
+    double2 Wo[ROWS + 2], WDo[HV ? ROWS + 2 : 1];
+    double Ww[ROWS + 2], We[ROWS + 2], WDw[HV ? ROWS + 2 : 1], WDe[HV ? ROWS + 2 : 1];
+    double acc[2] = {0.0, 0.0};
+    // un (+ und) and w (+ wd) of row q in the generated text's operation order; un stored
+    // for the wave's own rows
+    auto new_state = [&](int q) {
+        const int i = q + 2, b = q + 1;
+        const double hw = lane_val(H[i], 1), he = lane_val(H[i], 2);
+        const double2 v = step_pair<false>(U[i - 1], U[i], U[i + 1], hw, he);
+        const double vw = step5v(lane_val(H[i - 1], 1), hw, lane_val(H[i + 1], 1), lane_val(H[i], 0), lane_val(U[i].x, 0));
+        const double ve = step5v(lane_val(H[i - 1], 2), he, lane_val(H[i + 1], 2), lane_val(U[i].y, 63), lane_val(H[i], 3));
+        Wo[b].x = B[b].x + (2.0 * v.x) * lb;
+        Wo[b].y = B[b].y + (2.0 * v.y) * lb;
+        Ww[b] = lane_val(BH[b], 1) + (2.0 * vw) * lb;
+        We[b] = lane_val(BH[b], 2) + (2.0 * ve) * lb;
+        double2 vd = make_double2(0.0, 0.0);
+        if constexpr (HV) {
+            const double hdw = lane_val(HD[i], 1), hde = lane_val(HD[i], 2);
+            vd = step_pair<true>(UD[i - 1], UD[i], UD[i + 1], hdw, hde);
+            const double vdw =
+                step5dv(lane_val(HD[i - 1], 1), hdw, lane_val(HD[i + 1], 1), lane_val(HD[i], 0), lane_val(UD[i].x, 0));
+            const double vde =
+                step5dv(lane_val(HD[i - 1], 2), hde, lane_val(HD[i + 1], 2), lane_val(UD[i].y, 63), lane_val(HD[i], 3));
+            WDo[b].x = BD[b].x + (lb * (2.0 * vd.x) + (2.0 * v.x) * lbd);
+            WDo[b].y = BD[b].y + (lb * (2.0 * vd.y) + (2.0 * v.y) * lbd);
+            WDw[b] = lane_val(BHD[b], 1) + (lb * (2.0 * vdw) + (2.0 * vw) * lbd);
+            WDe[b] = lane_val(BHD[b], 2) + (lb * (2.0 * vde) + (2.0 * ve) * lbd);
+        }
+        if (q >= 0 && q < ROWS) {
+            const size_t gp = pair_of((size_t)(g.j0 + q) * n, g.oc);
+            if constexpr (HV) {
+                und2[gp] = vd;
+                acc[1] += (2.0 * v.x) * vd.x;
+                acc[1] += (2.0 * v.y) * vd.y;
+            }
+            un2[gp] = v;
+            acc[0] += v.x * v.x;
+            acc[0] += v.y * v.y;
+        }
+    };
+    // ub[row r] += w_c + 0.1 w_E + 0.1 w_W + 0.1 w_S + 0.1 w_N + 4 (-(0.1 w_c))
+    auto gather1 = [](double c, double e, double w, double s, double nn) {
+        double a = c;
+        a = a + 0.1 * e;
+        a = a + 0.1 * w;
+        a = a + 0.1 * s;
+        a = a + 0.1 * nn;
+        a = a + 4.0 * -(0.1 * c);
+        return a;
+    };
+    auto gather = [&](int r) {
+        const int b = r + 1;
+        const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
+        if constexpr (HV) {
+            const double2 c = WDo[b];
+            double2 o;
+            o.x = UBD[r].x + gather1(c.x, c.y, from_west(c.y, WDw[b]), WDo[b + 1].x, WDo[b - 1].x);
+            o.y = UBD[r].y + gather1(c.y, from_east(c.x, WDe[b]), c.x, WDo[b + 1].y, WDo[b - 1].y);
+            ubd2[gp] = o;
+        }
+        const double2 c = Wo[b];
+        double2 o;
+        o.x = UB[r].x + gather1(c.x, c.y, from_west(c.y, Ww[b]), Wo[b + 1].x, Wo[b - 1].x);
+        o.y = UB[r].y + gather1(c.y, from_east(c.x, We[b]), c.x, Wo[b + 1].y, Wo[b - 1].y);
+        ub2[gp] = o;
+    };
+#pragma unroll
+    for (int q = -2; q <= 1; ++q) load_u(q);
+    load_b(-1);
+    load_b(0);
+#pragma unroll
+    for (int k = 0; k < D; ++k) load_group(k);
+    new_state(-1);
+    new_state(0);
+    static_for<ROWS>([&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+        if constexpr (r + D < ROWS) load_group(r + D);
+        new_state(r + 1);
+        gather(r);
+    });
+    acc[0] = wave_sum(acc[0]);
+    if constexpr (HV) acc[1] = wave_sum(acc[1]);
+    if (g.lane == 0) {
+        partials[(size_t)wid * (HV ? 2 : 1)] = acc[0];
+        if constexpr (HV) partials[(size_t)wid * 2 + 1] = acc[1];
+    }
+}
+
 struct WaveGrid {
     int nstrips, nwaves, blocks;
 };
@@ -606,7 +853,14 @@ int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, co
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
-    if (wave_path(n)) {
+    if (n % WS2 == 0) {
+        const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2);
+        STADE_TIMED("diffusion2d_d", stream,
+                    diffusion_d_wave2<WCH2, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(u, ud, un, und, (int)n, nstrips, nwaves,
+                                                                                    ws->partials));
+        STADE_LAUNCHED("diffusion_d_wave2");
+        nparts = nwaves;
+    } else if (wave_path(n)) {
         const WaveGrid w = wave_grid_of(n, WCH);
         STADE_TIMED("diffusion2d_d", stream,
                     diffusion_d_wave<WCH, WD><<<w.blocks, 256, 0, stream>>>(u, ud, un, und, (int)n, w.nstrips, w.nwaves, ws->partials));
@@ -632,7 +886,14 @@ int32_t stade_hip_diffusion2d_b(double* loss, const double* lossb, const double*
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
-    if (wave_path(n)) {
+    if (n % WS2 == 0) {
+        const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2);
+        STADE_TIMED("diffusion2d_b", stream,
+                    diffusion_b_wave2<false, WCH2, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(
+                        u, nullptr, un, nullptr, unb, nullptr, ub, nullptr, lossb, nullptr, (int)n, nstrips, nwaves, ws->partials));
+        STADE_LAUNCHED("diffusion_b_wave2");
+        nparts = nwaves;
+    } else if (wave_path(n)) {
         const WaveGrid w = wave_grid_of(n, WCH);
         STADE_TIMED("diffusion2d_b", stream,
                     diffusion_b_wave<false, WCH, WD><<<w.blocks, 256, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr,
@@ -665,7 +926,14 @@ int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
-    if (wave_path(n)) {
+    if (n % WS2 == 0) {
+        const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2_HV);
+        STADE_TIMED("diffusion2d_hv", stream,
+                    diffusion_b_wave2<true, WCH2_HV, WD2_HV><<<(nwaves + 3) / 4, 256, 0, stream>>>(
+                        u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd, (int)n, nstrips, nwaves, ws->partials));
+        STADE_LAUNCHED("diffusion_b_wave2<hv>");
+        nparts = nwaves;
+    } else if (wave_path(n)) {
         const WaveGrid w = wave_grid_of(n, WCH_HV);
         STADE_TIMED("diffusion2d_hv", stream,
                     diffusion_b_wave<true, WCH_HV, WD_HV><<<w.blocks, 256, 0, stream>>>(u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd,

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
+#include <utility>
 
 #define STADE_HIP_OK 0
 #define STADE_HIP_EINVAL (-1)
@@ -210,6 +211,18 @@ template <int NV>
 __global__ __launch_bounds__(256) void finalize_kernel(const double* partials, int nparts, SumOuts out) {
     __shared__ double lds[16 * NV];
     finalize_partials<NV>(partials, nparts, lds, out);
+}
+
+// f(std::integral_constant<int, I>{}) for I = 0 .. N-1 in order: an unroll that does not
+// depend on the compiler's unroll threshold (a long register-resident loop that stays rolled
+// moves its arrays to scratch memory)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
 // Periodic wrap of a coordinate that is at most one period outside [0, n).
