@@ -9,11 +9,15 @@
 //
 // Here: 64 x 64 tiles of w, one wave per 16 columns and one lane per row, so every wave
 // load is a 512-byte contiguous column segment.
-//   1. rows:    partial row sums  s_i = sum_j w[i,j] x[j]  per 64-column chunk (LDS tree)
-//   2. finish:  r = (b - t) + sum of chunk partials, loss (grid sum), rb reset, bb, tb, sb
-//   3. columns: wb[i,j] += x[j] sb_i (read-modify-write, the dominant traffic) and the
-//               per-tile column sums of w[i,j] sb_i (DPP wave sums), no atomics
-//   4. xb:      xb[j] += sum over row tiles of the column partials, in tile order
+//   1. rows:    partial row sums  s_i = sum_j w[i,j] x[j]  per 64-column chunk (LDS tree);
+//               the adjoint forms also stage rb and reset it
+//   2. columns: every block recomputes its rows' r = (b - t) + sum of chunk partials and
+//               sb, then wb[i,j] += x[j] sb_i (read-modify-write, the dominant traffic) and
+//               the per-tile column sums of w[i,j] sb_i (DPP wave sums), no atomics; the
+//               blocks of column chunk 0 write r, bb, tb and the row tiles' loss partials
+//   3. xb:      xb[j] += sum over row tiles of the column partials, in tile order, and the
+//               loss sum
+// The tangent (no columns to scatter) runs rows, then a finish kernel for r, rd and the loss.
 // Every reduction has a fixed order: results do not depend on scheduling.
 #include "internal.hpp"
 #include "../../include/stade_hip.h"
