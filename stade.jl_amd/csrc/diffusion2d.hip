@@ -32,6 +32,7 @@
 //   * blockIdx = chunk * strips + strip: the blocks that share a halo row are `strips`
 //     launches apart, on the same XCD (round-robin dispatch) when strips is a multiple of 8.
 #include "internal.hpp"
+#include <initializer_list>
 #include "../../include/stade_hip.h"
 
 namespace stade {
@@ -809,6 +810,14 @@ __global__ __launch_bounds__(256) void diffusion_b_wave2(const double* __restric
 struct WaveGrid {
     int nstrips, nwaves, blocks;
 };
+// the 128-column kernels move 16-byte pairs: every array they touch must be 16-byte aligned
+// (an array that is a view into a larger allocation may be 8-byte aligned only)
+bool pairs_ok(int64_t n, std::initializer_list<const void*> arrays) {
+    if (n % WS2 != 0) return false;
+    for (const void* p : arrays)
+        if (reinterpret_cast<uintptr_t>(p) & 15) return false;
+    return true;
+}
 // the wave-strip path applies when n is a multiple of the strip width (and so of the rows
 // per wave)
 bool wave_path(int64_t n) { return n >= WS && n % WS == 0; }
@@ -853,7 +862,7 @@ int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, co
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
-    if (n % WS2 == 0) {
+    if (pairs_ok(n, {u, ud, un, und})) {
         const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2);
         STADE_TIMED("diffusion2d_d", stream,
                     diffusion_d_wave2<WCH2, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(u, ud, un, und, (int)n, nstrips, nwaves,
@@ -886,7 +895,7 @@ int32_t stade_hip_diffusion2d_b(double* loss, const double* lossb, const double*
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
-    if (n % WS2 == 0) {
+    if (pairs_ok(n, {u, un, unb, ub})) {
         const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2);
         STADE_TIMED("diffusion2d_b", stream,
                     diffusion_b_wave2<false, WCH2, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(
@@ -926,7 +935,7 @@ int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double
     Workspace* ws = workspace();
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
-    if (n % WS2 == 0) {
+    if (pairs_ok(n, {u, ud, un, und, unb, unbd, ub, ubd})) {
         const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2_HV);
         STADE_TIMED("diffusion2d_hv", stream,
                     diffusion_b_wave2<true, WCH2_HV, WD2_HV><<<(nwaves + 3) / 4, 256, 0, stream>>>(

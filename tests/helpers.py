@@ -102,9 +102,13 @@ def make_args(lib, fname: str, shapes: dict, ints: dict, scalars: dict, seed: st
 
 def run_parity(name: str, mode: str, shapes: dict, ints: dict, scalars: dict | None = None,
                seed: str | None = None, precision: str = "f64", rtol: float | None = None,
-               stacks: tuple = (), int_arrays: dict | None = None, oracle=None, scales: dict | None = None):
+               stacks: tuple = (), int_arrays: dict | None = None, oracle=None, scales: dict | None = None,
+               offset: int = 0):
     """Run one generated function on the oracle and on libstade_hip with the same inputs;
-    compare every argument's final value and the returned scalars.  Returns the worst error."""
+    compare every argument's final value and the returned scalars.  Returns the worst error.
+
+    offset > 0 passes every device array as a view starting `offset` elements into a larger
+    allocation (so its address is only element-aligned)."""
     import stade_hip
     import torch
     scalars = scalars or {}
@@ -116,8 +120,15 @@ def run_parity(name: str, mode: str, shapes: dict, ints: dict, scalars: dict | N
     shp["__stacks__"] = tuple(s for s, _ in stacks)
     args = make_args(lib, fname, shp, ints, scalars, seed or f"{fname}-{ints}", fdt, int_arrays, scales)
     host = [v.copy(order="K") if isinstance(v, np.ndarray) else v for _, _, v in args]
-    dev = [torch.from_numpy(np.ascontiguousarray(v.ravel(order="F"))).to("cuda") if isinstance(v, np.ndarray) else v
-           for _, _, v in args]
+    def device_array(v):
+        t = torch.from_numpy(np.ascontiguousarray(v.ravel(order="F")))
+        if offset == 0:
+            return t.to("cuda")
+        buf = torch.zeros(t.numel() + offset, dtype=t.dtype, device="cuda")
+        buf[offset:] = t.to("cuda")
+        return buf[offset:]
+
+    dev = [device_array(v) if isinstance(v, np.ndarray) else v for _, _, v in args]
     stack_h, stack_d = [], []
     for sname, (length, kind) in stacks:
         if kind == "Ai":

@@ -24,3 +24,15 @@ def test_diffusion2d_parity(mode, n):
     shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
     print(f"diffusion2d_{mode} n={n}", flush=True)
     run_parity("diffusion2d", mode, shapes, dict(n=n))
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("n", [128, 384])
+def test_diffusion2d_element_aligned_views(mode, n):
+    """Arrays that are views one element into a larger allocation (8-byte aligned only): the
+    128-column kernels move 16-byte pairs, so such arrays must take the 64-column kernels."""
+    c = n * n
+    shapes = {k: c for k in ("u", "ub", "un", "unb", "ud", "und", "ubd", "unbd")}
+    shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
+    print(f"diffusion2d_{mode} n={n} offset=1", flush=True)
+    run_parity("diffusion2d", mode, shapes, dict(n=n), offset=1)
