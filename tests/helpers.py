@@ -133,10 +133,11 @@ def run_parity(name: str, mode: str, shapes: dict, ints: dict, scalars: dict | N
     for sname, (length, kind) in stacks:
         if kind == "Ai":
             stack_h.append(np.full(length, -7, dtype=np.int64))
-            stack_d.append(torch.full((length,), -7, dtype=torch.int64, device="cuda"))
+            stack_d.append(torch.full((length + offset,), -7, dtype=torch.int64, device="cuda")[offset:])
         else:
             stack_h.append(np.full(length, np.nan, dtype=fdt))
-            stack_d.append(torch.full((length,), float("nan"), dtype=torch.float64 if fdt == np.float64 else torch.float32, device="cuda"))
+            stack_d.append(torch.full((length + offset,), float("nan"), dtype=torch.float64 if fdt == np.float64 else torch.float32,
+                                      device="cuda")[offset:])
     ret_h = lib.call(fname, *host, *stack_h)
     for (a, kind, _), h in zip(args, host):
         if isinstance(h, np.ndarray) and kind == "Af":
