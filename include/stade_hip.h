@@ -13,7 +13,8 @@
  *     6750-6756: the adjoint list, then (xd, xbd) per float argument, then the stacks).
  *   - Arrays are device pointers to the caller's column-major, densely packed Julia arrays
  *     (the pointer of a ROCArray).  Indices keep Julia's meaning: element (i, j) of an
- *     (m, n) array is at offset (i-1) + (j-1)*m.
+ *     (m, n) array is at offset (i-1) + (j-1)*m.  Element alignment is enough: a view into a
+ *     larger array is accepted (16-byte vector paths check alignment and fall back).
  *   - Outputs are mutated in place exactly as the generated code does: primal outputs are
  *     overwritten, shadows are accumulated (not overwritten), statement resets zero the
  *     shadows the generated code zeroes, stacks are written by the forward sweep.
