@@ -34,7 +34,24 @@ namespace {
 
 constexpr int NT = 256, KMAX = 32;
 constexpr int kInitBlockCells = NT * 8;  // cells per block of the backward init kernel
-constexpr int BNT = 1024;  // threads of the forward and backward chunk kernels (16 waves per CU)
+constexpr int BNT = 1024;  // threads of the forward chunk kernel (16 waves per CU)
+#ifndef STADE_BURG_BT
+#define STADE_BURG_BT 512
+#endif
+#ifndef STADE_BURG_BS
+#define STADE_BURG_BS 2048
+#endif
+#ifndef STADE_BURG_BT_HV
+#define STADE_BURG_BT_HV 512
+#endif
+#ifndef STADE_BURG_BS_HV
+#define STADE_BURG_BS_HV 1024
+#endif
+// backward chunk kernels: threads and owned cells per block (adjoint; HVP).  Each step of a
+// chunk ends in a block barrier, and the step is bound by its chain of barrier, edge loads,
+// DPP moves and arithmetic: two 512-thread blocks per CU (two barrier domains, the same 16
+// waves) measured 2-3 % faster than one 1024-thread block.
+constexpr int BWD_T = STADE_BURG_BT, BWD_S = STADE_BURG_BS, BWD_T_HV = STADE_BURG_BT_HV, BWD_S_HV = STADE_BURG_BS_HV;
 
 struct Coef {
     double cadv, cdif, cadvd, cdifd;
@@ -175,12 +192,12 @@ __global__ __launch_bounds__(NT) void bwd_init_kernel(const double* __restrict__
 // One backward step k on the extended region: reads the tape row in U (+ UD) and the adjoint
 // state in Wc (+ WDc), writes the next adjoint state to Wn (+ WDn) on [k+1, len-k-1), and adds
 // the owned cells' coefficient-shadow terms to acc.
-template <bool HV, int M>
+template <bool HV, int M, int T>
 __device__ __forceinline__ void bwd_step(int k, int len, int nk, int own, const double* U, const double* UD, const double* Wc,
                                          const double* WDc, double* Wn, double* WDn, const Coef& c, double (&acc)[4]) {
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        const int e = threadIdx.x + i * BNT;
+        const int e = threadIdx.x + i * T;
         if (e < k + 1 || e >= len - k - 1) continue;
         // the update in its factored form (as in bwd_reg_kernel)
         const double um1 = U[e - 1], uc = U[e], up1 = U[e + 1];
@@ -216,11 +233,11 @@ __device__ __forceinline__ void bwd_step(int k, int len, int nk, int own, const 
 }
 
 // the chunk's final adjoint state and its coefficient-shadow partials
-template <bool HV>
+template <bool HV, int T>
 __device__ __forceinline__ void bwd_finish(const double* Wc, const double* WDc, double* __restrict__ vout,
                                            double* __restrict__ voutd, int x0, int nk, int own, double (&acc)[4], double* red,
                                            double* partials) {
-    for (int e = threadIdx.x; e < own; e += BNT) {
+    for (int e = threadIdx.x; e < own; e += T) {
         vout[x0 + e] = Wc[nk + e];
         if (HV) voutd[x0 + e] = WDc[nk + e];
     }
@@ -233,13 +250,13 @@ __device__ __forceinline__ void bwd_finish(const double* Wc, const double* WDc, 
 }
 
 // any nk <= KMAX: the tape row of the next step is fetched one step ahead
-template <bool HV, int S>
-__global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win, const double* __restrict__ wind,
+template <bool HV, int S, int T>
+__global__ __launch_bounds__(T) void bwd_kernel(const double* __restrict__ win, const double* __restrict__ wind,
                                                   double* __restrict__ vout, double* __restrict__ voutd,
                                                   const double* __restrict__ tape, const double* __restrict__ taped, int n,
                                                   int64_t t_hi, int nk, Coef c, double* partials) {
     constexpr int L = S + 2 * KMAX;
-    constexpr int M = (L + BNT - 1) / BNT;  // extended-region positions per thread
+    constexpr int M = (L + T - 1) / T;  // extended-region positions per thread
     __shared__ double W[2][L];
     __shared__ double U[L];
     __shared__ double WD[HV ? 2 : 1][HV ? L : 1];
@@ -248,11 +265,11 @@ __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win
     const int x0 = blockIdx.x * S;
     const int len = S + 2 * nk;
     const int own = min(S, n - x0);
-    // the thread's positions e = threadIdx.x + i * BNT and their (periodic) columns
+    // the thread's positions e = threadIdx.x + i * T and their (periodic) columns
     int xcol[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        const int e = threadIdx.x + i * BNT;
+        const int e = threadIdx.x + i * T;
         xcol[i] = e < len ? wrapn(x0 - nk + e, n) : 0;
         if (e < len) {
             W[0][e] = win[xcol[i]];
@@ -266,7 +283,7 @@ __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win
         const size_t row = (size_t)(t_hi - k) * (size_t)n;
 #pragma unroll
         for (int i = 0; i < M; ++i) {
-            const int e = threadIdx.x + i * BNT;
+            const int e = threadIdx.x + i * T;
             if (e >= k && e < len - k) {
                 pre[i] = tape[row + xcol[i]];
                 if (HV) pred[i] = taped[row + xcol[i]];
@@ -279,7 +296,7 @@ __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win
     for (int k = 0; k < nk; ++k) {
 #pragma unroll
         for (int i = 0; i < M; ++i) {
-            const int e = threadIdx.x + i * BNT;
+            const int e = threadIdx.x + i * T;
             if (e >= k && e < len - k) {
                 U[e] = pre[i];
                 if (HV) UD[e] = pred[i];
@@ -287,16 +304,16 @@ __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win
         }
         if (k + 1 < nk) fetch(k + 1);
         __syncthreads();
-        bwd_step<HV, M>(k, len, nk, own, U, UD, W[cur], WD[HV ? cur : 0], W[cur ^ 1], WD[HV ? cur ^ 1 : 0], c, acc);
+        bwd_step<HV, M, T>(k, len, nk, own, U, UD, W[cur], WD[HV ? cur : 0], W[cur ^ 1], WD[HV ? cur ^ 1 : 0], c, acc);
         __syncthreads();
         cur ^= 1;
     }
-    bwd_finish<HV>(W[cur], WD[HV ? cur : 0], vout, voutd, x0, nk, own, acc, red, partials);
+    bwd_finish<HV, T>(W[cur], WD[HV ? cur : 0], vout, voutd, x0, nk, own, acc, red, partials);
 }
 
 // ---------------------------------------------------------------------------------------
 // A full chunk of KMAX steps with the state in registers.  Thread t holds positions
-// e = t + i * BNT (slot i) of the extended region; its neighbours e -/+ 1 are the adjacent
+// e = t + i * T (slot i) of the extended region; its neighbours e -/+ 1 are the adjacent
 // lanes of the same slot, taken by DPP wavefront shifts.  Only a wave's two end lanes need a
 // value from another wave (lane 0: the previous wave's lane 63, or slot i-1's last lane for
 // wave 0; lane 63: the next wave's lane 0, or slot i+1's first lane for the last wave): every
@@ -305,19 +322,19 @@ __global__ __launch_bounds__(BNT) void bwd_kernel(const double* __restrict__ win
 // step k+1 is published at the end of step k, so the prefetch ring of PD rows keeps PD - 1
 // rows in flight.  The arithmetic per position is bwd_step's, in the same order.  A ring of 2
 // measured faster than 4 (537 against 526 adjoint evals/s); loading the tape shifted by -/+1
-// instead of taking neighbours by DPP needs more registers than a 1024-thread block allows
+// instead of taking neighbours by DPP needed more registers than a 1024-thread block allows
 // and ran at 392.
 // ---------------------------------------------------------------------------------------
-template <bool HV, int S, int PD>
-__global__ __launch_bounds__(BNT) void bwd_reg_kernel(const double* __restrict__ win, const double* __restrict__ wind,
+template <bool HV, int S, int PD, int T>
+__global__ __launch_bounds__(T) void bwd_reg_kernel(const double* __restrict__ win, const double* __restrict__ wind,
                                                       double* __restrict__ vout, double* __restrict__ voutd,
                                                       const double* __restrict__ tape, const double* __restrict__ taped, int n,
                                                       int64_t t_hi, Coef c, double* partials) {
     constexpr int nk = KMAX, L = S + 2 * KMAX;
-    constexpr int M = (L + BNT - 1) / BNT, NWV = BNT / 64;
+    constexpr int M = (L + T - 1) / T, NWV = T / 64;
     constexpr int NA = HV ? 4 : 2;  // exchanged arrays: u, w (+ ud, wd)
     static_assert(KMAX % PD == 0, "full chunks are whole rounds of the prefetch ring");
-    static_assert(L - (M - 1) * BNT <= 64, "the last slot belongs to wave 0 alone");
+    static_assert(L - (M - 1) * T <= 64, "the last slot belongs to wave 0 alone");
     __shared__ double edge[2][NA][M][NWV][2];
     __shared__ double red[16 * 4];
     const int lane = threadIdx.x & 63;
@@ -329,7 +346,7 @@ __global__ __launch_bounds__(BNT) void bwd_reg_kernel(const double* __restrict__
     bool owned[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        const int e = threadIdx.x + i * BNT;
+        const int e = threadIdx.x + i * T;
         xc[i] = wrapn(x0 - nk + min(e, L - 1), n);
         owned[i] = e >= nk && e < nk + own;
         int si, sv, ss;
@@ -443,7 +460,7 @@ __global__ __launch_bounds__(BNT) void bwd_reg_kernel(const double* __restrict__
     }
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        const int e = threadIdx.x + i * BNT;
+        const int e = threadIdx.x + i * T;
         if (owned[i]) {
             vout[x0 + e - nk] = w[i];
             if (HV) voutd[x0 + e - nk] = wd[i];
@@ -532,7 +549,7 @@ unsigned grid_for(int n, int per_block) { return (unsigned)((n + per_block - 1) 
 int32_t check(int64_t n, int64_t nsteps, const char* fn) {
     if (n < 0 || nsteps < 0) return set_error(STADE_HIP_EINVAL, "%s: negative size (n = %lld, nsteps = %lld)", fn, (long long)n, (long long)nsteps);
     if (n > (1LL << 30)) return set_error(STADE_HIP_ERANGE, "%s: n = %lld exceeds 2^30 cells", fn, (long long)n);
-    if (grid_for((int)n, 2048) * 4 > (unsigned)kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: n too large for the workspace", fn);
+    if (grid_for((int)n, BWD_S_HV) * 4 > (unsigned)kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: n too large for the workspace", fn);
     return STADE_HIP_OK;
 }
 
@@ -565,7 +582,7 @@ int32_t forward(const double* src, const double* srcd, double* fin, double* find
 int init_blocks(int64_t n) { return (int)grid_for((int)n, kInitBlockCells); }
 size_t bwd_offset(int64_t n) { return ((size_t)init_blocks(n) * 2 + 1023) / 1024 * 1024; }
 template <bool HV>
-int bwd_blocks(int64_t n) { return (int)grid_for((int)n, HV ? 2048 : 4096); }
+int bwd_blocks(int64_t n) { return (int)grid_for((int)n, HV ? BWD_S_HV : BWD_S); }
 template <bool HV>
 int32_t check_partials(int64_t n, int64_t nrun, const char* fn) {
     const int64_t chunks = (nrun + KMAX - 1) / KMAX;
@@ -580,7 +597,7 @@ int32_t check_partials(int64_t n, int64_t nrun, const char* fn) {
 template <bool HV>
 int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, double* ubd, const double* tape, const double* taped,
                  int n, int64_t nrun, const Coef& c, double* pbwd, int* nparts, hipStream_t stream) {
-    constexpr int S = HV ? 2048 : 4096;
+    constexpr int S = HV ? BWD_S_HV : BWD_S, T = HV ? BWD_T_HV : BWD_T;
     constexpr int NV = HV ? 4 : 2;
     const unsigned nb = grid_for(n, S);
     double *cw = w, *cwd = wd, *ow = W2, *owd = W2d;
@@ -593,11 +610,11 @@ int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, dou
         double* dd = last ? ubd : owd;
         if (nk == KMAX) {
             STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
-                        bwd_reg_kernel<HV, S, 2><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, c,
+                        bwd_reg_kernel<HV, S, 2, T><<<nb, T, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, c,
                                                                       pbwd + (size_t)chunk * nb * NV));
         } else {
             STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
-                        bwd_kernel<HV, S><<<nb, BNT, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, nk, c,
+                        bwd_kernel<HV, S, T><<<nb, T, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, nk, c,
                                                                  pbwd + (size_t)chunk * nb * NV));
         }
         STADE_LAUNCHED("burgers1d bwd_kernel");
