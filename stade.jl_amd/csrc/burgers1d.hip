@@ -659,7 +659,7 @@ int32_t stade_hip_initstacks_burgers1d_b(int64_t n, int64_t nsteps, int64_t** br
     STADE_TRY_HIP(hipMalloc((void**)branch_stack, (size_t)(len[0] > 0 ? len[0] : 1) * sizeof(int64_t)));
     hipError_t e = hipMalloc((void**)u_stack, (size_t)(len[1] > 0 ? len[1] : 1) * sizeof(double));
     if (e != hipSuccess) {
-        hipFree(*branch_stack);
+        (void)hipFree(*branch_stack);  // the allocation error is the one reported
         *branch_stack = nullptr;
         return check_hip(e, "hipMalloc(u_stack)");
     }
