@@ -57,7 +57,7 @@ __global__ __launch_bounds__(NT) void rows_kernel(const double* __restrict__ w, 
     if (i < m) {
 #pragma unroll
         for (int jj = 0; jj < CW; ++jj) {
-            if (j0 + jj >= n) break;
+            if (j0 + jj >= n) continue;  // columns past n (a guard, not an exit: the loop unrolls)
             const double wij = wv_[jj], xj = xv_[jj];
             if (M != ADJ) sd = sd + (xj * wdv_[jj] + wij * xdv_[jj]);
             s = s + wij * xj;
@@ -107,7 +107,7 @@ __device__ __forceinline__ void row_value(const FinishArgs& a, int i, double& s,
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            if (c0 + c >= a.nchunks) break;
+            if (c0 + c >= a.nchunks) continue;
             s = s + pv[c];
             if (M != ADJ) sd = sd + pdv[c];
         }
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
     if (lane == 0) {
 #pragma unroll
         for (int jj = 0; jj < CW; ++jj) {
-            if (j0 + jj >= n) break;
+            if (j0 + jj >= n) continue;
             XP[(size_t)rtile * n + j0 + jj] = cx[jj];
             if (M == HVP) XPd[(size_t)rtile * n + j0 + jj] = cxd[jj];
         }
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(NT) void xfinish_kernel(double* __restrict__ xb, do
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            if (r0 + r >= mtiles) break;
+            if (r0 + r >= mtiles) continue;
             s += pv[r];
             if (M == HVP) sd += pdv[r];
         }

@@ -638,7 +638,7 @@ __global__ __launch_bounds__(NT) void d1sum_kernel(D1Args a) {
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
         const int s = sb + 4 * u;
-        if (s >= s1) break;
+        if (s >= s1) continue;  // a guard, not an exit: the loop unrolls
         const long k = (long)s * H + jc;
         const float h = hv_[u];
         const float hb = hbv_[u];

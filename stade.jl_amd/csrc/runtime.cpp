@@ -65,8 +65,10 @@ void* scratch(size_t bytes) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     if (w->scratch_bytes < bytes) {
         if (w->scratch) {
-            hipDeviceSynchronize();
-            hipFree(w->scratch);
+            // wait for kernels still using the old buffer; a failure here is sticky and is
+            // reported by the next launch's status
+            (void)hipDeviceSynchronize();
+            (void)hipFree(w->scratch);
             w->scratch = nullptr;
             w->scratch_bytes = 0;
         }
@@ -101,7 +103,7 @@ static hipEvent_t ev_get() {
         return e;
     }
     hipEvent_t e = nullptr;
-    hipEventCreate(&e);
+    (void)hipEventCreate(&e);  // profiling only: a failed event records nothing
     return e;
 }
 
@@ -112,12 +114,12 @@ void prof_begin(const char* kernel, hipStream_t s) {
     g_open.name = kernel;
     g_open.a = ev_get();
     g_open.b = ev_get();
-    hipEventRecord(g_open.a, s);
+    (void)hipEventRecord(g_open.a, s);
 }
 
 void prof_end(hipStream_t s) {
     std::lock_guard<std::mutex> lk(g_prof_mu);
-    hipEventRecord(g_open.b, s);
+    (void)hipEventRecord(g_open.b, s);
     g_pending.push_back(g_open);
 }
 
