@@ -645,6 +645,10 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE counters to bytes)")
     ap.add_argument("--configs", default="", help="comma-separated workloads to measure besides the headline "
                                                   "(default: all)")
+    ap.add_argument("--stream-ceiling", action="store_true",
+                    help="run only torch's own elementwise kernels over the headline's bytes (4096^2 fp64: "
+                         "un = u, ub += unb; 40 B per cell) and print their rate, a practical ceiling for "
+                         "the adjoint pass's access mix")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU; the multi-GPU design is described, not run "
@@ -663,6 +667,30 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": 8 * n, "copy_bytes_written": 8 * n, "launches": 10}))
+        return
+    if args.stream_ceiling:
+        n = 4096 * 4096
+        u, unb, ub = (torch.randn(n, dtype=torch.float64, device=dev) for _ in range(3))
+        un = torch.empty_like(u)
+
+        def one():
+            un.copy_(u)
+            ub.add_(unb)
+
+        for _ in range(5):
+            one()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 50
+        t0.record()
+        for _ in range(reps):
+            one()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / reps
+        print(json.dumps({"stream_ceiling": "un = u (copy), ub += unb (add), torch kernels, 4096^2 fp64",
+                          "bytes": 40 * n, "us": round(us, 1), "TBps": round(40 * n / us / 1e6, 3),
+                          "frac_of_8TBps": round(40 * n / us / 1e6 / 8.0, 3)}))
         return
     head = WORKLOADS[args.workload]()
     res = measure(head, args.steps, args.warmup, dev)
