@@ -98,8 +98,9 @@ __global__ __launch_bounds__(BNT) void fwd_kernel(const double* __restrict__ src
         const size_t row = (size_t)(t0 + k) * (size_t)n;
         if (tape) {
             for (int e = threadIdx.x; e < own; e += BNT) {
-                tape[row + x0 + e] = A[cur][nk + e];
-                if (TAN && taped) taped[row + x0 + e] = D[cur][nk + e];
+                // streaming stores: a tape row is read back only by the reverse sweep
+                __builtin_nontemporal_store(A[cur][nk + e], &tape[row + x0 + e]);
+                if (TAN && taped) __builtin_nontemporal_store(D[cur][nk + e], &taped[row + x0 + e]);
             }
         }
         for (int e = k + 1 + threadIdx.x; e < len - k - 1; e += BNT) {
@@ -285,8 +286,8 @@ __global__ __launch_bounds__(T) void bwd_kernel(const double* __restrict__ win, 
         for (int i = 0; i < M; ++i) {
             const int e = threadIdx.x + i * T;
             if (e >= k && e < len - k) {
-                pre[i] = tape[row + xcol[i]];
-                if (HV) pred[i] = taped[row + xcol[i]];
+                pre[i] = __builtin_nontemporal_load(&tape[row + xcol[i]]);
+                if (HV) pred[i] = __builtin_nontemporal_load(&taped[row + xcol[i]]);
             }
         }
     };
@@ -373,8 +374,8 @@ __global__ __launch_bounds__(T) void bwd_reg_kernel(const double* __restrict__ w
         const size_t row = (size_t)(t_hi - (k < nk ? k : nk - 1)) * (size_t)n;
 #pragma unroll
         for (int i = 0; i < M; ++i) {
-            pu[slot][i] = tape[row + xc[i]];
-            if constexpr (HV) pud[slot][i] = taped[row + xc[i]];
+            pu[slot][i] = __builtin_nontemporal_load(&tape[row + xc[i]]);
+            if constexpr (HV) pud[slot][i] = __builtin_nontemporal_load(&taped[row + xc[i]]);
         }
     };
     // the end lanes' adjoint state and the tape row of the next step (ring slot `nxt`)
