@@ -195,10 +195,10 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
         const int jc = min(j0 + jj, n - 1);
         const size_t g = (size_t)jc * m + ic;
         wv_[jj] = w[g];
-        wbv_[jj] = wb[g];
+        wbv_[jj] = __builtin_nontemporal_load(&wb[g]);  // wb, wbd: streamed once
         xv_[jj] = x[jc];
         wdv_[jj] = M == HVP ? wd[g] : 0.0;
-        wbdv_[jj] = M == HVP ? wbd[g] : 0.0;
+        wbdv_[jj] = M == HVP ? __builtin_nontemporal_load(&wbd[g]) : 0.0;
         xdv_[jj] = M == HVP ? xd[jc] : 0.0;
     }
     double rv, rvd;
@@ -248,8 +248,8 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
         cx[jj] = ok ? wij * si : 0.0;
         cxd[jj] = (M == HVP && ok) ? si * wdv_[jj] + wij * sid : 0.0;
         if (ok) {
-            if (M == HVP) wbd[g] = wbdv_[jj] + (si * xdv_[jj] + xj * sid);
-            wb[g] = wbv_[jj] + xj * si;
+            if (M == HVP) __builtin_nontemporal_store(wbdv_[jj] + (si * xdv_[jj] + xj * sid), &wbd[g]);
+            __builtin_nontemporal_store(wbv_[jj] + xj * si, &wb[g]);
         }
     }
     // column sums over the tile's rows (DPP wave sums), all 16 columns at once

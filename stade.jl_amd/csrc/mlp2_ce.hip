@@ -40,7 +40,7 @@ struct EpiTanh {  // h1 = tanh(s1), s1 = b1 + W1 x
     const float* b1;
     long ld;
     __device__ float load(int m, int) const { return b1[m]; }
-    __device__ void operator()(int m, int n, float v, float b) const { h1[m + n * ld] = tanhf(v + b); }
+    __device__ void operator()(int m, int n, float v, float b) const { __builtin_nontemporal_store(tanhf(v + b), &h1[m + n * ld]); }
 };
 // dual forward (tangent and HVP): from P = W1 x and Q = W1 xd + W1d x in one launch,
 // h1 = tanh(P + b1) and h1d = (1.0 - h1^2) * (Q + b1d)
@@ -51,25 +51,27 @@ struct EpiTanhPair {
     __device__ float2 load(int m, int) const { return make_float2(b1[m], b1d[m]); }
     __device__ void operator()(int m, int n, float p, float q, float2 b) const {
         const float h = tanhf(p + b.x);
-        h1[m + n * ld] = h;
-        h1d[m + n * ld] = (1.0f - h * h) * (q + b.y);
+        __builtin_nontemporal_store(h, &h1[m + n * ld]);
+        __builtin_nontemporal_store((1.0f - h * h) * (q + b.y), &h1d[m + n * ld]);
     }
 };
 // dual accumulation (HVP): C += P, Cd += Q
 struct EpiAccPair {
     float *C, *Cd;
     long ld;
-    __device__ float2 load(int m, int n) const { return make_float2(C[m + n * ld], Cd[m + n * ld]); }
+    __device__ float2 load(int m, int n) const {
+        return make_float2(__builtin_nontemporal_load(&C[m + n * ld]), __builtin_nontemporal_load(&Cd[m + n * ld]));
+    }
     __device__ void operator()(int m, int n, float p, float q, float2 c) const {
-        C[m + n * ld] = c.x + p;
-        Cd[m + n * ld] = c.y + q;
+        __builtin_nontemporal_store(c.x + p, &C[m + n * ld]);
+        __builtin_nontemporal_store(c.y + q, &Cd[m + n * ld]);
     }
 };
 struct EpiAcc {  // C += v (a shadow accumulated, as the generated code does)
     float* C;
     long ld;
-    __device__ float load(int m, int n) const { return C[m + n * ld]; }
-    __device__ void operator()(int m, int n, float v, float c) const { C[m + n * ld] = c + v; }
+    __device__ float load(int m, int n) const { return __builtin_nontemporal_load(&C[m + n * ld]); }
+    __device__ void operator()(int m, int n, float v, float c) const { __builtin_nontemporal_store(c + v, &C[m + n * ld]); }
 };
 
 // ---------------------------------------------------------------------------------------
@@ -630,9 +632,9 @@ __global__ __launch_bounds__(NT) void d1sum_kernel(D1Args a) {
     for (int u = 0; u < SB; ++u) {
         const long k = (long)min(sb + 4 * u, s1 - 1) * H + jc;
         hv_[u] = a.h1[k];
-        hbv_[u] = a.h1b_in[k];
+        hbv_[u] = __builtin_nontemporal_load(&a.h1b_in[k]);
         hdv_[u] = HV ? a.h1d[k] : 0.f;
-        hbdv_[u] = HV ? a.h1bd[k] : 0.f;
+        hbdv_[u] = HV ? __builtin_nontemporal_load(&a.h1bd[k]) : 0.f;
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -656,10 +658,10 @@ __global__ __launch_bounds__(NT) void d1sum_kernel(D1Args a) {
         const float d1 = g * t;
         const float d1d = HV ? t * -((2.0f * h) * hd) + g * td : 0.f;
         if (j < H) {
-            a.h1b[k] = 0.f;
+            __builtin_nontemporal_store(0.f, &a.h1b[k]);
             a.D1[k] = d1;
             if (HV) {
-                a.h1bd[k] = 0.f;
+                __builtin_nontemporal_store(0.f, &a.h1bd[k]);
                 a.D1d[k] = d1d;
             }
         }
