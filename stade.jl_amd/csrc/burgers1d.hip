@@ -98,7 +98,8 @@ __global__ __launch_bounds__(BNT) void fwd_kernel(const double* __restrict__ src
         const size_t row = (size_t)(t0 + k) * (size_t)n;
         if (tape) {
             for (int e = threadIdx.x; e < own; e += BNT) {
-                // streaming stores: a tape row is read back only by the reverse sweep
+                // streaming stores: a tape row is read back only by the reverse sweep (plain
+                // stores measured 1 % slower over an evaluation, the reverse sweep's reads too)
                 __builtin_nontemporal_store(A[cur][nk + e], &tape[row + x0 + e]);
                 if (TAN && taped) __builtin_nontemporal_store(D[cur][nk + e], &taped[row + x0 + e]);
             }
