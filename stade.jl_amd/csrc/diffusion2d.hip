@@ -370,10 +370,10 @@ __global__ __launch_bounds__(NT) void zero2_kernel(double* __restrict__ a, doubl
 #define STADE_DIFF_WCH2 64
 #endif
 #ifndef STADE_DIFF_WCH2_HV
-#define STADE_DIFF_WCH2_HV 64
+#define STADE_DIFF_WCH2_HV 32
 #endif
 #ifndef STADE_DIFF_WD2_HV
-#define STADE_DIFF_WD2_HV 2
+#define STADE_DIFF_WD2_HV 4
 #endif
 // rows per wave and rows of loads in flight ahead of the row being computed; measured at
 // n = 4096: 64 rows beat 32 for the adjoint and the tangent (fewer halo rows), while the
@@ -592,9 +592,9 @@ __global__ __launch_bounds__(256) void diffusion_b_wave(const double* __restrict
 // and a rolled loop would move the register arrays to scratch memory.
 constexpr int WS2 = 128;
 // rows per wave and rows of loads in flight, measured at n = 4096: the adjoint and the
-// tangent as on 64-column strips; the HVP, with twice the values per row, runs 64 rows with
-// two rows in flight (178 VGPRs, two waves a SIMD; four rows in flight take 256 VGPRs and one
-// wave a SIMD, 10 % slower)
+// tangent as on 64-column strips; the HVP, with twice the values per row, 32 rows with four in
+// flight (256 VGPRs, one wave a SIMD), 3 % faster with the streaming hints than 64 rows with
+// two in flight (178 VGPRs, two waves a SIMD), which had been 10 % faster without them
 constexpr int WCH2 = STADE_DIFF_WCH2;        // adjoint, tangent
 constexpr int WCH2_HV = STADE_DIFF_WCH2_HV;  // HVP
 constexpr int WD2_HV = STADE_DIFF_WD2_HV;
