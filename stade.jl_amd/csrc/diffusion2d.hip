@@ -361,7 +361,7 @@ __global__ __launch_bounds__(NT) void zero2_kernel(double* __restrict__ a, doubl
 #define STADE_DIFF_WCH_HV 32
 #endif
 #ifndef STADE_DIFF_WD
-#define STADE_DIFF_WD 4
+#define STADE_DIFF_WD 3
 #endif
 #ifndef STADE_DIFF_WD_HV
 #define STADE_DIFF_WD_HV 4
@@ -378,7 +378,8 @@ __global__ __launch_bounds__(NT) void zero2_kernel(double* __restrict__ a, doubl
 // rows per wave and rows of loads in flight ahead of the row being computed; measured at
 // n = 4096: 64 rows beat 32 for the adjoint and the tangent (fewer halo rows), while the
 // HVP, with twice the values per row, keeps 32 rows to stay in registers (at 64 it spills).
-// Depths 3..6 measured within 2 % of each other.
+// Depths 3..6 measured within 2 % of each other; on the 128-column strips with streaming
+// hints 3 is 1.6 % faster than 4 for the adjoint (6 and 32-row chunks slower).
 constexpr int WS = 64;                      // columns per wave strip
 constexpr int WCH = STADE_DIFF_WCH;         // adjoint, tangent
 constexpr int WCH_HV = STADE_DIFF_WCH_HV;   // HVP
