@@ -41,22 +41,64 @@ FP64_PEAK_TFLOPS = 78.6
 
 
 def _tensor(a, dev):
+    """A flat device copy of a host array; a matrix is flattened in Julia's column-major order."""
     import numpy as np
     import torch
-    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    a = np.asarray(a)
+    return torch.from_numpy(np.ascontiguousarray(a.ravel(order="F") if a.ndim > 1 else a)).to(dev)
+
+
+def arg_names(family: str, mode: str) -> list[str]:
+    """The generated function's argument names, in order, stacks included (the C ABI's and
+    the Python mirror's order: `agen_signature_args` /root/reference/src/STADE.jl:3455-3464,
+    `tgen_signature_args` 3306-3315, `hvp_emit` 6750-6756)."""
+    from stade_hip.emit import KERNELS
+    spec = KERNELS[family]
+    names = [nm for nm, _ in spec.modes[mode].args]
+    if mode != "d":
+        names += [nm for nm, _, _ in spec.stacks]
+    return names
 
 
 class Workload:
-    name = ""
+    """One generated function of one config at the benchmark size.
+
+    `host_inputs()` returns every argument of the config's three generated functions by its
+    generated name (numpy arrays in Julia's column-major order, flattened; Python floats and
+    ints), seeded as the benchmark seeds them; the GPU run, the CPU baseline and the
+    full-size parity tests all take their inputs from it."""
+    family = ""
     kernel = ""           # dominant kernel (profiler name)
     bound = "hbm"
     dtype = "f64"
 
-    def setup(self, dev):
+    def __init__(self, mode: str):
+        self.mode = mode
+        self.name = f"{self.family}_{mode}"
+
+    def host_inputs(self) -> dict:
         raise NotImplementedError
 
+    def stack_lengths(self) -> list[tuple[int, str]]:
+        """(length, 'Ai' | 'Af') of each stack argument (adjoint and HVP only)."""
+        return []
+
+    def setup(self, dev):
+        import numpy as np
+        import torch
+        self.h = self.host_inputs()
+        self.t = {k: _tensor(v, dev) if isinstance(v, np.ndarray) else v for k, v in self.h.items()}
+        self.stacks = []
+        if self.mode != "d":
+            for length, kind in self.stack_lengths():
+                dt = torch.int64 if kind == "Ai" else (torch.float64 if self.dtype == "f64" else torch.float32)
+                self.stacks.append(torch.empty(length, dtype=dt, device=dev))
+        names = arg_names(self.family, self.mode)
+        self.argv = [self.t[a] for a in names[:len(names) - len(self.stacks)]] + self.stacks
+
     def step(self):
-        raise NotImplementedError
+        import stade_hip
+        getattr(stade_hip, self.name)(*self.argv)
 
     def algo_bytes(self) -> float:          # per evaluation
         return 0.0
@@ -64,54 +106,64 @@ class Workload:
     def kernel_bytes(self) -> float:        # per launch of the dominant kernel
         return 0.0
 
-    def kernel_flops(self) -> float:
-        return 0.0
-
     def config(self) -> dict:
         return {}
 
+    def sample(self):
+        """A smaller workload of the same family for the CPU baseline, and the share of one
+        full evaluation that it is (1.0: the full size)."""
+        return self, 1.0
+
+    def sample_desc(self) -> str:
+        return f"{self.name} at the full size"
+
     def cpu_sample(self):
-        """(callable running one evaluation of the oracle, description); None if unavailable."""
-        return None
+        """(callable running one evaluation of the oracle on `sample()`, description, share)."""
+        import numpy as np
+        from oracle import runner
+        wl, share = self.sample()
+        prec = "f32" if self.dtype == "f32" else "f64"
+        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"{self.name}.jl", precision=prec, bounds_check=False)
+        h = wl.host_inputs()
+        names = arg_names(self.family, self.mode)
+        nst = len(wl.stack_lengths()) if self.mode != "d" else 0
+        fdt = np.float64 if prec == "f64" else np.float32
+
+        def run():
+            argv = [h[a].copy(order="K") if isinstance(h[a], np.ndarray) else h[a] for a in names[:len(names) - nst]]
+            if nst:
+                argv += [np.empty(k, dtype=np.int64 if kind == "Ai" else fdt) for k, kind in wl.stack_lengths()]
+            lib.call(self.name, *argv)
+        desc = wl.sample_desc()
+        if share != 1.0:
+            desc += f" ({1 / share:.0f}x less work than one benchmark evaluation; the rate is scaled by that share)"
+        return run, desc, share
+
+
+def _rng(name: str, salt: int = 0):
+    import stade_hip
+    return stade_hip.api.Rng(stade_hip.stable_seed(name) + salt)
 
 
 class Diffusion(Workload):
+    """Config 2: one periodic 5-point step on n x n fp64, u ~ N(0,1), loss = sum(un^2);
+    tangent / HVP direction ud ~ N(0,1) from the next seed."""
+    family = "diffusion2d"
     dtype = "f64"
 
     def __init__(self, mode="b", n=4096):
-        self.mode, self.n = mode, n
-        self.name = f"diffusion2d_{mode}"
+        super().__init__(mode)
+        self.n = n
         self.kernel = f"diffusion2d_{mode}"
 
-    def setup(self, dev):
+    def host_inputs(self):
         import numpy as np
-        import torch
         import stade_hip
-        n = self.n
-        c = n * n
-        rng = stade_hip.api.Rng(stade_hip.stable_seed("diffusion2d"))
-        u = stade_hip.rng_normal(rng, c)
-        z = lambda: torch.zeros(c, dtype=torch.float64, device=dev)
-        self.t = dict(loss=torch.zeros(1, dtype=torch.float64, device=dev),
-                      lossb=torch.ones(1, dtype=torch.float64, device=dev),
-                      lossd=torch.zeros(1, dtype=torch.float64, device=dev),
-                      lossbd=torch.zeros(1, dtype=torch.float64, device=dev),
-                      u=_tensor(u, dev), ub=z(), un=z(), unb=z(), und=z(), unbd=z(), ubd=z())
-        if self.mode in ("d", "hv"):
-            rng2 = stade_hip.api.Rng(stade_hip.stable_seed("diffusion2d") + 1)
-            self.t["ud"] = _tensor(stade_hip.rng_normal(rng2, c), dev)
-        self.host_u = u
-
-    def step(self):
-        import stade_hip
-        t, n = self.t, self.n
-        if self.mode == "b":
-            stade_hip.diffusion2d_b(t["loss"], t["lossb"], t["u"], t["ub"], t["un"], t["unb"], n)
-        elif self.mode == "d":
-            stade_hip.diffusion2d_d(t["loss"], t["lossd"], t["u"], t["ud"], t["un"], t["und"], n)
-        else:
-            stade_hip.diffusion2d_hv(t["loss"], t["lossb"], t["u"], t["ub"], t["un"], t["unb"], n,
-                                     t["lossd"], t["lossbd"], t["ud"], t["ubd"], t["und"], t["unbd"])
+        c = self.n * self.n
+        z = lambda k: np.zeros(k)
+        return dict(loss=z(1), lossb=np.ones(1), lossd=z(1), lossbd=z(1),
+                    u=stade_hip.rng_normal(_rng("diffusion2d"), c), ub=z(c), un=z(c), unb=z(c),
+                    ud=stade_hip.rng_normal(_rng("diffusion2d", 1), c), ubd=z(c), und=z(c), unbd=z(c), n=self.n)
 
     def algo_bytes(self):
         per = {"b": 48, "d": 32, "hv": 96}[self.mode]
@@ -127,64 +179,35 @@ class Diffusion(Workload):
                             f"periodic 5-point step + sum(un^2), {self.n}x{self.n} fp64, u ~ N(0,1) from val_stable_seed",
                 "n": self.n, "cells": self.n * self.n}
 
-    def cpu_sample(self):
-        import numpy as np
-        from oracle import runner
-        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"diffusion2d_{self.mode}.jl", bounds_check=False)
-        n, c = self.n, self.n * self.n
-        u = self.host_u.copy()
-        z = lambda: np.zeros(c)
-        a = dict(ub=z(), un=z(), unb=z(), ud=np.ones(c), und=z(), ubd=z(), unbd=z())
-
-        def run():
-            if self.mode == "b":
-                lib.call("diffusion2d_b", np.zeros(1), np.ones(1), u, a["ub"], a["un"], a["unb"], n)
-            elif self.mode == "d":
-                lib.call("diffusion2d_d", np.zeros(1), np.zeros(1), u, a["ud"], a["un"], a["und"], n)
-            else:
-                lib.call("diffusion2d_hv", np.zeros(1), np.ones(1), u, a["ub"], a["un"], a["unb"], n,
-                         np.zeros(1), np.zeros(1), a["ud"], a["ubd"], a["und"], a["unbd"])
-        return run, f"diffusion2d_{self.mode} at the full {n}x{n} grid"
+    def sample_desc(self):
+        return f"diffusion2d_{self.mode} at the full {self.n}x{self.n} grid"
 
 
 class Affine(Workload):
+    """Config 1: loss = 0.5 sum((W x + b - t)^2), W m x n fp64 U[-1,1], x, b, t N(0,1);
+    direction (Wd, xd, bd, td) ~ N(0,1) from the next seed."""
+    family = "affine_lsq"
     dtype = "f64"
 
     def __init__(self, mode="b", m=1024, n=1024):
-        self.mode, self.m, self.n = mode, m, n
-        self.name = f"affine_lsq_{mode}"
+        super().__init__(mode)
+        self.m, self.n = m, n
         self.kernel = "affine_cols" if mode != "d" else "affine_rows"
 
-    def setup(self, dev):
-        import torch
+    def host_inputs(self):
+        import numpy as np
         import stade_hip
         m, n = self.m, self.n
-        rng = stade_hip.api.Rng(stade_hip.stable_seed("affine_lsq"))
+        rng = _rng("affine_lsq")
         w = stade_hip.rng_uniform(rng, m * n, -1.0, 1.0)
         x, b, t = (stade_hip.rng_normal(rng, k) for k in (n, m, m))
-        rng2 = stade_hip.api.Rng(stade_hip.stable_seed("affine_lsq") + 1)
+        rng2 = _rng("affine_lsq", 1)
         wd, xd, bd, td = (stade_hip.rng_normal(rng2, k) for k in (m * n, n, m, m))
-        f = lambda a: _tensor(a, dev)
-        z = lambda k: torch.zeros(k, dtype=torch.float64, device=dev)
-        self.t = dict(loss=z(1), lossb=f([1.0]), lossd=z(1), lossbd=z(1), w=f(w), wb=z(m * n), x=f(x), xb=z(n),
-                      b=f(b), bb=z(m), t=f(t), tb=z(m), r=z(m), rb=z(m), wd=f(wd), wbd=z(m * n), xd=f(xd), xbd=z(n),
-                      bd=f(bd), bbd=z(m), td=f(td), tbd=z(m), rd=z(m), rbd=z(m))
-
-    def step(self):
-        import stade_hip
-        t, m, n = self.t, self.m, self.n
-        base = [t[k] for k in ("loss",)]
-        if self.mode == "b":
-            stade_hip.affine_lsq_b(t["loss"], t["lossb"], t["w"], t["wb"], t["x"], t["xb"], t["b"], t["bb"], t["t"], t["tb"],
-                                   t["r"], t["rb"], m, n)
-        elif self.mode == "d":
-            stade_hip.affine_lsq_d(t["loss"], t["lossd"], t["w"], t["wd"], t["x"], t["xd"], t["b"], t["bd"], t["t"], t["td"],
-                                   t["r"], t["rd"], m, n)
-        else:
-            stade_hip.affine_lsq_hv(t["loss"], t["lossb"], t["w"], t["wb"], t["x"], t["xb"], t["b"], t["bb"], t["t"], t["tb"],
-                                    t["r"], t["rb"], m, n, t["lossd"], t["lossbd"], t["wd"], t["wbd"], t["xd"], t["xbd"],
-                                    t["bd"], t["bbd"], t["td"], t["tbd"], t["rd"], t["rbd"])
-        del base
+        z = lambda k: np.zeros(k)
+        mat = lambda a: np.asfortranarray(a.reshape((m, n), order="F"))   # w is an (i_m, i_n) Julia matrix
+        return dict(loss=z(1), lossb=np.ones(1), lossd=z(1), lossbd=z(1), w=mat(w), wb=mat(z(m * n)), x=x, xb=z(n),
+                    b=b, bb=z(m), t=t, tb=z(m), r=z(m), rb=z(m), wd=mat(wd), wbd=mat(z(m * n)), xd=xd, xbd=z(n),
+                    bd=bd, bbd=z(m), td=td, tbd=z(m), rd=z(m), rbd=z(m), i_m=m, i_n=n)
 
     def algo_bytes(self):
         mn, m, n = self.m * self.n, self.m, self.n
@@ -202,57 +225,42 @@ class Affine(Workload):
         return {"workload": f"affine_lsq_{self.mode}, loss = 0.5*sum((W*x+b-t)^2), W {self.m}x{self.n} fp64 U[-1,1]",
                 "m": self.m, "n": self.n}
 
+    def sample_desc(self):
+        return f"affine_lsq_{self.mode} at the full {self.m}x{self.n} size"
+
 
 class Burgers(Workload):
     """Config 5: 2^20 periodic cells, 500 guarded steps, nu = 1e-3, dx = 1/n, dt such that
     nu dt / dx^2 = 0.2; u0 = sin(2 pi x) + 0.1 N(0,1), x_i = (i - 1) / n; tend = 1 (every
-    step runs)."""
+    step runs); tangent / HVP direction ud ~ N(0,1) from the next seed and nud = 0.01."""
+    family = "burgers1d"
     dtype = "f64"
 
-    def __init__(self, mode="b", n=1 << 20, nsteps=500):
-        self.mode, self.n, self.T = mode, n, nsteps
-        self.name = f"burgers1d_{mode}"
-        self.kernel = {"b": "burgers1d_bwd", "d": "burgers1d_fwd_hv", "hv": "burgers1d_bwd_hv"}[mode]
+    def __init__(self, mode="b", n=1 << 20, nsteps=500, dx=None):
+        super().__init__(mode)
+        self.n, self.T = n, nsteps
+        self.kernel = {"b": "burgers1d_bwd", "d": "burgers1d_fwd_tan", "hv": "burgers1d_bwd_hv"}[mode]
         self.nu = 1e-3
-        self.dx = 1.0 / n
+        self.dx = 1.0 / n if dx is None else dx
         self.dt = 0.2 * self.dx * self.dx / self.nu
         self.tend = 1.0
 
-    def _u0(self):
+    def host_inputs(self):
         import numpy as np
         import stade_hip
         n = self.n
         x = np.arange(n, dtype=np.float64) / n
-        rng = stade_hip.api.Rng(stade_hip.stable_seed("burgers1d"))
-        return np.sin(2.0 * np.pi * x) + 0.1 * stade_hip.rng_normal(rng, n)
+        u = np.sin(2.0 * np.pi * x) + 0.1 * stade_hip.rng_normal(_rng("burgers1d"), n)
+        ud = stade_hip.rng_normal(_rng("burgers1d", 1), n)
+        z = lambda k: np.zeros(k)
+        return dict(loss=z(1), lossb=np.ones(1), lossd=z(1), lossbd=z(1), u=u, ub=z(n), un=z(n), unb=z(n),
+                    ud=ud, ubd=z(n), und=z(n), unbd=z(n),
+                    nu=self.nu, nub=0.0, dt=self.dt, dtb=0.0, dx=self.dx, dxb=0.0, tend=self.tend, tendb=0.0,
+                    nud=0.01, nubd=0.0, dtd=0.0, dtbd=0.0, dxd=0.0, dxbd=0.0, tendd=0.0, tendbd=0.0,
+                    n=n, nsteps=self.T)
 
-    def setup(self, dev):
-        import torch
-        import stade_hip
-        n = self.n
-        self.host_u = self._u0()
-        rng2 = stade_hip.api.Rng(stade_hip.stable_seed("burgers1d") + 1)
-        ud = stade_hip.rng_normal(rng2, n)
-        z = lambda: torch.zeros(n, dtype=torch.float64, device=dev)
-        self.t = dict(loss=torch.zeros(1, dtype=torch.float64, device=dev), lossb=torch.ones(1, dtype=torch.float64, device=dev),
-                      lossd=torch.zeros(1, dtype=torch.float64, device=dev), lossbd=torch.zeros(1, dtype=torch.float64, device=dev),
-                      u=_tensor(self.host_u, dev), ub=z(), un=z(), unb=z(), ud=_tensor(ud, dev), ubd=z(), und=z(), unbd=z())
-        if self.mode != "d":
-            self.stacks = stade_hip.initstacks_burgers1d_b(n, self.T, dev)
-
-    def step(self):
-        import stade_hip
-        t, n, T = self.t, self.n, self.T
-        if self.mode == "b":
-            stade_hip.burgers1d_b(t["loss"], t["lossb"], t["u"], t["ub"], t["un"], t["unb"], self.nu, 0.0, self.dt, 0.0,
-                                  self.dx, 0.0, self.tend, 0.0, n, T, *self.stacks)
-        elif self.mode == "d":
-            stade_hip.burgers1d_d(t["loss"], t["lossd"], t["u"], t["ud"], t["un"], t["und"], self.nu, 0.01, self.dt, 0.0,
-                                  self.dx, 0.0, self.tend, 0.0, n, T)
-        else:
-            stade_hip.burgers1d_hv(t["loss"], t["lossb"], t["u"], t["ub"], t["un"], t["unb"], self.nu, 0.0, self.dt, 0.0,
-                                   self.dx, 0.0, self.tend, 0.0, n, T, t["lossd"], t["lossbd"], t["ud"], t["ubd"], t["und"],
-                                   t["unbd"], 0.01, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, *self.stacks)
+    def stack_lengths(self):
+        return [(self.T, "Ai"), (self.T * self.n, "Af")]
 
     def _launches(self):
         return -(-self.T // 32)
@@ -280,30 +288,12 @@ class Burgers(Workload):
                             f"counted loop with a guard, nu=1e-3, u0=sin(2 pi x)+0.1 N(0,1), loss=sum(u_T^2)",
                 "n": self.n, "nsteps": self.T, "tape_bytes": 8 * self.T * self.n}
 
-    def cpu_sample(self):
-        import numpy as np
-        from oracle import runner
+    def sample(self):
         Ts = 20
-        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"burgers1d_{self.mode}.jl", bounds_check=False)
-        n = self.n
-        scale = Ts / self.T
+        return Burgers(self.mode, self.n, Ts), Ts / self.T
 
-        def run():
-            u = self.host_u.copy()
-            z = lambda: np.zeros(n)
-            if self.mode == "d":
-                lib.call("burgers1d_d", np.zeros(1), np.zeros(1), u, np.ones(n), z(), z(), self.nu, 0.01, self.dt, 0.0,
-                         self.dx, 0.0, self.tend, 0.0, n, Ts)
-            else:
-                st = lib.stacks("initstacks_burgers1d_b", n, Ts, fill_nan=False)
-                if self.mode == "b":
-                    lib.call("burgers1d_b", np.zeros(1), np.ones(1), u, z(), z(), z(), self.nu, 0.0, self.dt, 0.0, self.dx, 0.0,
-                             self.tend, 0.0, n, Ts, *st)
-                else:
-                    lib.call("burgers1d_hv", np.zeros(1), np.ones(1), u, z(), z(), z(), self.nu, 0.0, self.dt, 0.0, self.dx, 0.0,
-                             self.tend, 0.0, n, Ts, np.zeros(1), np.zeros(1), np.ones(n), z(), z(), z(), 0.01, 0.0, 0.0, 0.0,
-                             0.0, 0.0, 0.0, 0.0, *st)
-        return run, f"burgers1d_{self.mode} on {n} cells for {Ts} of the {self.T} steps (time x {1/scale:.0f})", scale
+    def sample_desc(self):
+        return f"burgers1d_{self.mode} on {self.n} cells for {self.T} steps"
 
 
 class Mlp(Workload):
@@ -311,12 +301,13 @@ class Mlp(Workload):
     cross-entropy, Float32; W1, W2 Glorot-uniform U(+-sqrt(6 / (fan_in + fan_out))),
     b1 = b2 = 0, labels uniform in 1..10, HVP direction (xd, W1d, b1d, W2d, b2d) ~ N(0,1) --
     all from the seeded Xoshiro stream."""
+    family = "mlp2_ce"
     dtype = "f32"
     bound = "mfma"
 
     def __init__(self, mode="b", B=4096, I=784, H=1024, O=10):
-        self.mode, self.B, self.I, self.H, self.O = mode, B, I, H, O
-        self.name = f"mlp2_ce_{mode}"
+        super().__init__(mode)
+        self.B, self.I, self.H, self.O = B, I, H, O
         g = 2.0 * H * I * B
         # flops per launch of each matrix-core kernel: the tangent and HVP run each pair
         # (s1, s1d), (W1b, W1bd), (xb, xbd) as one dual launch of three products
@@ -325,50 +316,26 @@ class Mlp(Workload):
                         "hv": {"mlp_gemm_s1d": 3 * g, "mlp_gemm_w1bd": 3 * g, "mlp_gemm_xbd": 3 * g}}[mode]
         self.kernel = next(iter(self.kernels))
 
-    def _host(self, B):
+    def host_inputs(self):
         import numpy as np
         import stade_hip
-        I, H, O = self.I, self.H, self.O
-        rng = stade_hip.api.Rng(stade_hip.stable_seed("mlp2_ce"))
-        x = stade_hip.rng_uniform(rng, I * B, 0.0, 1.0).astype(np.float32)
-        a1, a2 = np.sqrt(6.0 / (I + H)), np.sqrt(6.0 / (H + O))
-        w1 = stade_hip.rng_uniform(rng, H * I, -a1, a1).astype(np.float32)
-        w2 = stade_hip.rng_uniform(rng, O * H, -a2, a2).astype(np.float32)
-        b1, b2 = np.zeros(H, dtype=np.float32), np.zeros(O, dtype=np.float32)
-        lab = stade_hip.rng_int_range(rng, B, 1, O)
-        rng2 = stade_hip.api.Rng(stade_hip.stable_seed("mlp2_ce") + 1)
-        d = {k: stade_hip.rng_normal(rng2, n).astype(np.float32)
-             for k, n in (("xd", I * B), ("w1d", H * I), ("b1d", H), ("w2d", O * H), ("b2d", O))}
-        return dict(x=x, w1=w1, b1=b1, w2=w2, b2=b2, lab=lab, **d)
-
-    def setup(self, dev):
-        import torch
         B, I, H, O = self.B, self.I, self.H, self.O
-        h = self._host(B)
-        f = lambda a: _tensor(a, dev)
-        z = lambda k: torch.zeros(k, dtype=torch.float32, device=dev)
-        t = {k: f(v) for k, v in h.items()}
-        t.update(loss=z(1), lossb=f([1.0]).float(), lossd=z(1), lossbd=z(1))
+        f = lambda a: np.asarray(a, dtype=np.float32)
+        rng = _rng("mlp2_ce")
+        x = f(stade_hip.rng_uniform(rng, I * B, 0.0, 1.0))
+        a1, a2 = np.sqrt(6.0 / (I + H)), np.sqrt(6.0 / (H + O))
+        w1 = f(stade_hip.rng_uniform(rng, H * I, -a1, a1))
+        w2 = f(stade_hip.rng_uniform(rng, O * H, -a2, a2))
+        lab = stade_hip.rng_int_range(rng, B, 1, O)
+        rng2 = _rng("mlp2_ce", 1)
+        d = {k: f(stade_hip.rng_normal(rng2, n)) for k, n in (("xd", I * B), ("w1d", H * I), ("b1d", H), ("w2d", O * H), ("b2d", O))}
+        z = lambda k: np.zeros(k, dtype=np.float32)
+        h = dict(loss=z(1), lossb=np.ones(1, np.float32), lossd=z(1), lossbd=z(1), x=x, lab=lab, w1=w1, b1=z(H), w2=w2, b2=z(O),
+                 i_b=B, i_in=I, i_h=H, i_out=O, **d)
         for k, n in (("x", I * B), ("w1", H * I), ("b1", H), ("w2", O * H), ("b2", O), ("h1", H * B), ("z", O * B)):
             for suf in ("b", "bd") if k not in ("h1", "z") else ("", "b", "d", "bd"):
-                t.setdefault(k + suf, z(n))
-        self.t = t
-
-    def step(self):
-        import stade_hip
-        t = self.t
-        sz = (self.B, self.I, self.H, self.O)
-        if self.mode == "b":
-            stade_hip.mlp2_ce_b(*(t[k] for k in ("loss", "lossb", "x", "xb", "lab", "w1", "w1b", "b1", "b1b", "w2", "w2b",
-                                                "b2", "b2b", "h1", "h1b", "z", "zb")), *sz)
-        elif self.mode == "d":
-            stade_hip.mlp2_ce_d(*(t[k] for k in ("loss", "lossd", "x", "xd", "lab", "w1", "w1d", "b1", "b1d", "w2", "w2d",
-                                                "b2", "b2d", "h1", "h1d", "z", "zd")), *sz)
-        else:
-            stade_hip.mlp2_ce_hv(*(t[k] for k in ("loss", "lossb", "x", "xb", "lab", "w1", "w1b", "b1", "b1b", "w2", "w2b",
-                                                 "b2", "b2b", "h1", "h1b", "z", "zb")), *sz,
-                                 *(t[k] for k in ("lossd", "lossbd", "xd", "xbd", "w1d", "w1bd", "b1d", "b1bd", "w2d", "w2bd",
-                                                  "b2d", "b2bd", "h1d", "h1bd", "zd", "zbd")))
+                h.setdefault(k + suf, z(n))
+        return h
 
     def eval_flops(self):
         B, I, H, O = self.B, self.I, self.H, self.O
@@ -379,83 +346,48 @@ class Mlp(Workload):
                             f"cross-entropy summed over the batch; Glorot-uniform weights, zero biases",
                 "batch": self.B, "widths": [self.I, self.H, self.O]}
 
-    def cpu_sample(self):
-        import numpy as np
-        from oracle import runner
+    def sample(self):
         Bs = 128
-        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"mlp2_ce_{self.mode}.jl", precision="f32", bounds_check=False)
-        h = self._host(Bs)
-        I, H, O = self.I, self.H, self.O
-        z = lambda k: np.zeros(k, dtype=np.float32)
-        one = np.ones(1, dtype=np.float32)
+        return Mlp(self.mode, Bs, self.I, self.H, self.O), Bs / self.B
 
-        def run():
-            if self.mode == "b":
-                lib.call("mlp2_ce_b", z(1), one, h["x"], z(I * Bs), h["lab"], h["w1"], z(H * I), h["b1"], z(H), h["w2"],
-                         z(O * H), h["b2"], z(O), z(H * Bs), z(H * Bs), z(O * Bs), z(O * Bs), Bs, I, H, O)
-            elif self.mode == "d":
-                lib.call("mlp2_ce_d", z(1), z(1), h["x"], h["xd"], h["lab"], h["w1"], h["w1d"], h["b1"], h["b1d"], h["w2"],
-                         h["w2d"], h["b2"], h["b2d"], z(H * Bs), z(H * Bs), z(O * Bs), z(O * Bs), Bs, I, H, O)
-            else:
-                lib.call("mlp2_ce_hv", z(1), one, h["x"], z(I * Bs), h["lab"], h["w1"], z(H * I), h["b1"], z(H), h["w2"],
-                         z(O * H), h["b2"], z(O), z(H * Bs), z(H * Bs), z(O * Bs), z(O * Bs), Bs, I, H, O,
-                         z(1), z(1), h["xd"], z(I * Bs), h["w1d"], z(H * I), h["b1d"], z(H), h["w2d"], z(O * H), h["b2d"], z(O),
-                         z(H * Bs), z(H * Bs), z(O * Bs), z(O * Bs))
-        return run, f"mlp2_ce_{self.mode} on {Bs} of the {self.B} samples (time x {self.B // Bs})", Bs / self.B
+    def sample_desc(self):
+        return f"mlp2_ce_{self.mode} on a batch of {self.B}"
 
 
 class Conv(Workload):
     """Config 4: 8 images of 256 x 256, 64 -> 64 channels, 3 x 3, zero border held in xp,
     Float32; xp interior ~ N(0,1), w He-normal N(0, 2 / (9 C)); tangent / HVP direction
     xpd (interior), wd the same laws -- from the seeded Xoshiro stream."""
+    family = "conv3x3"
     dtype = "f32"
     bound = "mfma"
 
     def __init__(self, mode="b", N=8, C=64, K=64, H=256, W=256):
-        self.mode, self.N, self.C, self.K, self.H, self.W = mode, N, C, K, H, W
-        self.name = f"conv3x3_{mode}"
+        super().__init__(mode)
+        self.N, self.C, self.K, self.H, self.W = N, C, K, H, W
         g = 2.0 * N * K * H * W * 9 * C
         self.kernels = {"b": {"conv_fwd": g, "conv_wgrad": g, "conv_dgrad": g},
                         "d": {"conv_fwd_d": 3 * g},
                         "hv": {"conv_fwd_hv": 3 * g, "conv_wgrad": g, "conv_wgrad2": 2 * g, "conv_dgrad_hv": 3 * g}}[mode]
         self.kernel = next(iter(self.kernels))
 
-    def _host(self, N, H):
+    def host_inputs(self):
         import numpy as np
         import stade_hip
-        C, K, W = self.C, self.K, self.W
-        rng = stade_hip.api.Rng(stade_hip.stable_seed("conv3x3"))
+        N, C, K, H, W = self.N, self.C, self.K, self.H, self.W
+        rng = _rng("conv3x3")
         xp = np.zeros((N, C, H + 2, W + 2), dtype=np.float32)
         xp[:, :, 1:-1, 1:-1] = stade_hip.rng_normal(rng, N * C * H * W).reshape(N, C, H, W)
         w = (stade_hip.rng_normal(rng, 9 * C * K) * np.sqrt(2.0 / (9.0 * C))).astype(np.float32)
-        rng2 = stade_hip.api.Rng(stade_hip.stable_seed("conv3x3") + 1)
+        rng2 = _rng("conv3x3", 1)
         xpd = np.zeros_like(xp)
         xpd[:, :, 1:-1, 1:-1] = stade_hip.rng_normal(rng2, N * C * H * W).reshape(N, C, H, W)
         wd = (stade_hip.rng_normal(rng2, 9 * C * K) * np.sqrt(2.0 / (9.0 * C))).astype(np.float32)
-        return dict(xp=xp.ravel(), w=w, xpd=xpd.ravel(), wd=wd)
-
-    def setup(self, dev):
-        import torch
-        N, C, K, H, W = self.N, self.C, self.K, self.H, self.W
-        h = self._host(N, H)
-        f = lambda a: _tensor(a, dev)
-        z = lambda k: torch.zeros(k, dtype=torch.float32, device=dev)
         nx, nw, no = N * C * (H + 2) * (W + 2), 9 * C * K, N * K * H * W
-        self.t = {k: f(v) for k, v in h.items()}
-        self.t.update(loss=z(1), lossb=f([1.0]).float(), lossd=z(1), lossbd=z(1), xpb=z(nx), xpbd=z(nx), wb=z(nw), wbd=z(nw),
-                      out=z(no), outb=z(no), outd=z(no), outbd=z(no))
-
-    def step(self):
-        import stade_hip
-        t = self.t
-        sz = (self.N, self.C, self.K, self.H, self.W)
-        if self.mode == "b":
-            stade_hip.conv3x3_b(*(t[k] for k in ("loss", "lossb", "xp", "xpb", "w", "wb", "out", "outb")), *sz)
-        elif self.mode == "d":
-            stade_hip.conv3x3_d(*(t[k] for k in ("loss", "lossd", "xp", "xpd", "w", "wd", "out", "outd")), *sz)
-        else:
-            stade_hip.conv3x3_hv(*(t[k] for k in ("loss", "lossb", "xp", "xpb", "w", "wb", "out", "outb")), *sz,
-                                 *(t[k] for k in ("lossd", "lossbd", "xpd", "xpbd", "wd", "wbd", "outd", "outbd")))
+        z = lambda k: np.zeros(k, dtype=np.float32)
+        return dict(loss=z(1), lossb=np.ones(1, np.float32), lossd=z(1), lossbd=z(1), xp=xp.ravel(), xpb=z(nx), xpd=xpd.ravel(),
+                    xpbd=z(nx), w=w, wb=z(nw), wd=wd, wbd=z(nw), out=z(no), outb=z(no), outd=z(no), outbd=z(no),
+                    i_nb=N, i_c=C, i_k=K, i_h=H, i_w=W)
 
     def eval_flops(self):
         return sum(self.kernels.values()) * 1.0
@@ -465,29 +397,12 @@ class Conv(Workload):
                             f"held in xp), 3x3 {self.C}->{self.K}, loss = 0.5 sum(out^2)",
                 "batch": self.N, "channels": [self.C, self.K], "image": [self.H, self.W]}
 
-    def cpu_sample(self):
-        import numpy as np
-        from oracle import runner
+    def sample(self):
         Ns, Hs = 1, 32
-        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"conv3x3_{self.mode}.jl", precision="f32", bounds_check=False)
-        h = self._host(Ns, Hs)
-        C, K, W = self.C, self.K, self.W
-        nx, nw, no = Ns * C * (Hs + 2) * (W + 2), 9 * C * K, Ns * K * Hs * W
-        z = lambda k: np.zeros(k, dtype=np.float32)
-        one = np.ones(1, dtype=np.float32)
-        sz = (Ns, C, K, Hs, W)
+        return Conv(self.mode, Ns, self.C, self.K, Hs, self.W), (Ns * Hs) / (self.N * self.H)
 
-        def run():
-            if self.mode == "b":
-                lib.call("conv3x3_b", z(1), one, h["xp"], z(nx), h["w"], z(nw), z(no), z(no), *sz)
-            elif self.mode == "d":
-                lib.call("conv3x3_d", z(1), z(1), h["xp"], h["xpd"], h["w"], h["wd"], z(no), z(no), *sz)
-            else:
-                lib.call("conv3x3_hv", z(1), one, h["xp"], z(nx), h["w"], z(nw), z(no), z(no), *sz,
-                         z(1), z(1), h["xpd"], z(nx), h["wd"], z(nw), z(no), z(no))
-        share = (Ns * Hs) / (self.N * self.H)
-        return run, (f"conv3x3_{self.mode} on {Ns} of the {self.N} images, {Hs} of the {self.H} rows "
-                     f"(time x {1 / share:.0f})"), share
+    def sample_desc(self):
+        return f"conv3x3_{self.mode} on {self.N} image(s) of {self.H} x {self.W}"
 
 
 WORKLOADS = {

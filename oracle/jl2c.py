@@ -860,14 +860,21 @@ class CGen:
             if _is_int_literal(t):
                 return (f"((int64_t){int(t, 0)})", "i")
             if "f" in t and not t.startswith("0x"):
+                # a Float32 literal (`1.0f-8`): the decimal rounded once, to Float32
                 mant, ex_ = t.split("f")
-                return (f"((float){mant}e{ex_})", "f")
+                return (f"({mant}e{ex_}f)", "f")
             txt = t if ("." in t or "e" in t or "E" in t) else t + ".0"
             if txt.startswith("."):
                 txt = "0" + txt
             if txt.endswith("."):
                 txt += "0"
-            return (f"{txt}{self.lsfx}", "f")
+            if self.fp == "double":
+                return (txt, "f")
+            # a Float64 literal in another precision keeps its Float64 value and is then
+            # converted, as `cgen_convert_precision`'s T(expr) converts the parsed literal
+            # (/root/reference/src/STADE.jl:15353-15354): decimal -> Float64 -> Float32 rounds
+            # twice, which can differ from the single rounding of a C float literal
+            return (f"(({self.fp}){txt})", "f")
         if k == "var":
             t = ty.etype(e)
             if e[1] in ty.arrays:

@@ -319,7 +319,8 @@ template <int M>
 int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double* wbd, const double* x, const double* xd,
             double* xb, double* xbd, int64_t m, int64_t n, hipStream_t stream) {
     if (m == 0) return STADE_HIP_OK;
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     const int nchunks = (int)((n + CT - 1) / CT), mtiles = (int)((m + RT - 1) / RT);
     const int two = (M == ADJ) ? 1 : 2;

@@ -569,7 +569,7 @@ int32_t forward(const double* src, const double* srcd, double* fin, double* find
         bool last = t0 + nk >= nrun;
         double* d = last ? fin : (flip ? Q : P);
         double* dd = last ? find : (flip ? Qd : Pd);
-        STADE_TIMED(TAN ? "burgers1d_fwd_hv" : "burgers1d_fwd", stream,
+        STADE_TIMED(TAN ? "burgers1d_fwd_tan" : "burgers1d_fwd", stream,
                     fwd_kernel<TAN, S><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c));
         STADE_LAUNCHED("burgers1d fwd_kernel");
         cs = d;
@@ -680,7 +680,8 @@ int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u
     const int64_t nrun = taken_steps(dt, tend, nsteps);
     if (int32_t rc = check_partials<false>(n, nrun, "stade_hip_burgers1d_b")) return rc;
     Coef c{cadv, cdif, 0.0, 0.0};
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     if (nsteps > 0) {
         STADE_TIMED("burgers1d_branch", stream, branch_kernel<<<grid_for((int)(nsteps < (1 << 20) ? nsteps : (1 << 20)), NT), NT, 0, stream>>>(branch_stack, nsteps, nrun));
@@ -746,7 +747,8 @@ int32_t stade_hip_burgers1d_d(double* loss, double* lossd, double* u, double* ud
     Coef c{0.5 * dt / dx, nu * dt / c0, (0.5 * dtd) / dx + -((0.5 * dt) / (dx * dx)) * dxd,
            (dt * nud + nu * dtd) / c0 + -((nu * dt) / (c0 * c0)) * (dx * dxd + dx * dxd)};
     const int64_t nrun = taken_steps(dt, tend, nsteps);
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     double* P = (double*)scratch(sizeof(double) * 4 * (size_t)n);
     if (!P) return STADE_HIP_ENOMEM;
@@ -783,7 +785,8 @@ int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* 
            (dt * nud + nu * dtd) / c0 + -((nu * dt) / (c0 * c0)) * (dx * dxd + dx * dxd)};
     const int64_t nrun = taken_steps(dt, tend, nsteps);
     if (int32_t rc = check_partials<true>(n, nrun, "stade_hip_burgers1d_hv")) return rc;
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     if (nsteps > 0) {
         STADE_TIMED("burgers1d_branch", stream, branch_kernel<<<grid_for((int)(nsteps < (1 << 20) ? nsteps : (1 << 20)), NT), NT, 0, stream>>>(branch_stack, nsteps, nrun));

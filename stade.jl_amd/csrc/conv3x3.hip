@@ -716,7 +716,8 @@ int32_t weight_grad(const Dims& d, const float* x0, const float* g0, const float
 template <int MODE>
 int32_t run(const Ptrs& p, const Dims& d, hipStream_t stream) {
     if (d.N == 0 || d.K == 0 || d.H == 0 || d.W == 0) return STADE_HIP_OK;
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     const size_t nwf = up64((size_t)d.C * 9 * d.Kpad), nwg = up64((size_t)d.K * 9 * d.Cpad);
     const size_t nout = up64((size_t)d.N * d.K * d.H * d.W);

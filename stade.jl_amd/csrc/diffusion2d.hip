@@ -873,7 +873,8 @@ int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, co
     if (int32_t rc = check_n(n, "stade_hip_diffusion2d_d")) return rc;
     if (n == 0) return STADE_HIP_OK;
     if (!loss || !lossd || !u || !ud || !un || !und) return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_d: null pointer");
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
     if (pairs_ok(n, {u, ud, un, und})) {
@@ -906,7 +907,8 @@ int32_t stade_hip_diffusion2d_b(double* loss, const double* lossb, const double*
     if (int32_t rc = check_n(n, "stade_hip_diffusion2d_b")) return rc;
     if (n == 0) return STADE_HIP_OK;
     if (!loss || !lossb || !u || !ub || !un || !unb) return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_b: null pointer");
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
     if (pairs_ok(n, {u, un, unb, ub})) {
@@ -946,7 +948,8 @@ int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double
     if (n == 0) return STADE_HIP_OK;
     if (!loss || !lossb || !u || !ub || !un || !unb || !lossd || !lossbd || !ud || !ubd || !und || !unbd)
         return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_hv: null pointer");
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
     if (pairs_ok(n, {u, ud, un, und, unb, unbd, ub, ubd})) {

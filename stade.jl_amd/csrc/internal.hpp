@@ -49,8 +49,30 @@ constexpr int kDeviceScalars = 64;
 
 // Workspace of the current device; nullptr (with the error set) on failure.
 Workspace* workspace();
-// Scratch of at least `bytes`; nullptr (with the error set) on failure.
+// Scratch of at least `bytes`; nullptr (with the error set) on failure.  Only valid under a
+// WsCall of the current device.
 void* scratch(size_t bytes);
+
+// The workspace of the current device for one library call that enqueues on `stream`.
+// While the guard lives, the calling thread holds the device's library lock, so calls from
+// other host threads wait (scratch cannot be regrown under a call that is enqueuing into it).
+// If the previous call on the device used another stream, `stream` first waits for an event
+// that call recorded at its end, so calls on different streams that share the workspace run
+// one after the other on the device instead of racing.  The destructor records this call's
+// event on `stream` (a stream that may be destroyed later is never touched again).  A
+// stream under graph capture is neither ordered nor recorded: the caller's graph orders it.
+class WsCall {
+  public:
+    explicit WsCall(hipStream_t stream);
+    ~WsCall();
+    WsCall(const WsCall&) = delete;
+    WsCall& operator=(const WsCall&) = delete;
+    Workspace* ws;  // nullptr (with the error set) on failure
+  private:
+    int dev_;
+    hipStream_t stream_;
+    bool capturing_;
+};
 
 // ------------------------------------------------------------------------------------------
 // kernel timing: when enabled (stade_hip_profile_start), every launch made through

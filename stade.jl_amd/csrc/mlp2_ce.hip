@@ -904,7 +904,8 @@ template <int MODE>
 int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipStream_t stream) {
     const int B = (int)B_, I = (int)I_, H = (int)H_, O = (int)O_;
     if (B == 0) return STADE_HIP_OK;  // (i_h = 0 and i_out = 0 with samples are refused by check)
-    Workspace* ws = workspace();
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     const int nchunks = (B + SC - 1) / SC;
     const size_t nD1 = (size_t)H * B, nD2 = (size_t)O * B, nC = (size_t)nchunks * 2 * (O + 1) * H;

@@ -32,6 +32,16 @@ static std::mutex g_ws_mu;
 static Workspace g_ws[64];
 static bool g_ws_ready[64];
 
+// per device: the lock a library call holds while it enqueues, and the event the last call
+// recorded on its stream at its end
+static std::recursive_mutex g_call_mu[64];
+struct CallOrder {
+    hipStream_t last;
+    bool has_last;
+    hipEvent_t ev;
+};
+static CallOrder g_order[64];
+
 Workspace* workspace() {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -57,6 +67,50 @@ Workspace* workspace() {
         g_ws_ready[dev] = true;
     }
     return &g_ws[dev];
+}
+
+WsCall::WsCall(hipStream_t stream) : ws(nullptr), dev_(-1), stream_(stream), capturing_(false) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        check_hip(e, "hipGetDevice");
+        return;
+    }
+    if (dev < 0 || dev >= 64) {
+        set_error(STADE_HIP_ERANGE, "device ordinal %d out of range", dev);
+        return;
+    }
+    g_call_mu[dev].lock();
+    dev_ = dev;
+    Workspace* w = workspace();
+    if (!w) return;
+    CallOrder& o = g_order[dev];
+    // a stream under graph capture takes no dependency on work outside the capture: such
+    // calls are ordered by the graph the caller builds
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    capturing_ = hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    if (!capturing_ && o.has_last && o.last != stream && o.ev) {
+        if ((e = hipStreamWaitEvent(stream, o.ev, 0)) != hipSuccess) {
+            check_hip(e, "hipStreamWaitEvent (ordering after the previous call's stream)");
+            return;
+        }
+    }
+    ws = w;
+}
+
+WsCall::~WsCall() {
+    if (dev_ < 0) return;
+    if (ws && !capturing_) {
+        CallOrder& o = g_order[dev_];
+        hipError_t e = hipSuccess;
+        if (!o.ev) e = hipEventCreateWithFlags(&o.ev, hipEventDisableTiming);
+        // a failure leaves the next call on another stream unordered; it is reported by
+        // that call's own first HIP error, if any
+        if (e == hipSuccess) (void)hipEventRecord(o.ev, stream_);
+        o.last = stream_;
+        o.has_last = true;
+    }
+    g_call_mu[dev_].unlock();
 }
 
 void* scratch(size_t bytes) {
@@ -296,6 +350,8 @@ int32_t stade_hip_device_error(int32_t* flag) {
     if (!flag) return set_error(STADE_HIP_EINVAL, "stade_hip_device_error: null flag");
     Workspace* w = workspace();
     if (!w) return STADE_HIP_ENOMEM;
+    // every stream's kernels first (the flag may be raised by a call on any stream)
+    STADE_TRY_HIP(hipDeviceSynchronize());
     int32_t h = 0, z = 0;
     STADE_TRY_HIP(hipMemcpy(&h, (int32_t*)(w->dscalars + 16), sizeof h, hipMemcpyDeviceToHost));
     STADE_TRY_HIP(hipMemcpy((int32_t*)(w->dscalars + 16), &z, sizeof z, hipMemcpyHostToDevice));

@@ -19,6 +19,11 @@ class StadeHipError(RuntimeError):
         self.code = code
 
 
+class StadeHipBoundsError(IndexError):
+    """An index the generated code would reject with a BoundsError (a label outside
+    1..i_out), seen by a kernel and reported through the device error flag."""
+
+
 def lib_path() -> Path:
     return Path(os.environ.get("STADE_HIP_LIB", str(_DEFAULT_LIB)))
 
@@ -73,8 +78,9 @@ def lib():
         L.stade_hip_rng_uniform_f64.argtypes = [U64P, P, I64, F64, F64]
         L.stade_hip_rng_int_range.argtypes = [U64P, P, I64, I64, I64]
         for nm in ("stade_hip_rng_seed", "stade_hip_rng_normal_f64", "stade_hip_rng_uniform_f64",
-                   "stade_hip_rng_int_range", "stade_hip_free", "stade_hip_synchronize"):
+                   "stade_hip_rng_int_range", "stade_hip_free", "stade_hip_synchronize", "stade_hip_device_error"):
             getattr(L, nm).restype = ctypes.c_int32
+        L.stade_hip_device_error.argtypes = [ctypes.POINTER(ctypes.c_int32)]
         L.stade_hip_free.argtypes = [P]
         L.stade_hip_synchronize.argtypes = [P]
         for nm, kinds in ENTRY_POINTS.items():
@@ -170,6 +176,25 @@ def _int(name: str, v) -> int:
 
 def _call(fn: str, args: list, stream):
     _check(fn, getattr(lib(), fn)(*args, stream))
+
+
+def device_error() -> bool:
+    """Read and clear the device error flag (`stade_hip_device_error`): True if a kernel saw
+    an index the generated code would reject since the flag was last read.  Waits for the
+    device."""
+    flag = ctypes.c_int32(0)
+    _check("stade_hip_device_error", lib().stade_hip_device_error(ctypes.byref(flag)))
+    return bool(flag.value)
+
+
+def _bounds(fn: str, check: bool):
+    """`check=True` is the generated code's bounds checking (`stade_amdgpu_file(...;
+    inbounds=false)`, /root/reference/src/STADE.jl:18604-18605): the flag is read after the
+    call, at the cost of one synchronisation, and a raised flag is a BoundsError.  The default
+    matches the reference's GPU default, `inbounds=true`: no check, and an out-of-range label
+    contributes no term."""
+    if check and device_error():
+        raise StadeHipBoundsError(f"{fn}: a label is outside 1..i_out (the generated code raises a BoundsError)")
 
 
 # ------------------------------------------------------------------------------------------
@@ -340,8 +365,9 @@ def _mlp_sizes(i_b, i_in, i_h, i_out):
 
 
 
-def mlp2_ce_b(loss, lossb, x, xb, lab, w1, w1b, b1, b1b, w2, w2b, b2, b2b, h1, h1b, z, zb, i_b, i_in, i_h, i_out):
-    """Adjoint of mlp2_ce (corpus/mlp2_ce_b.jl); returns nothing."""
+def mlp2_ce_b(loss, lossb, x, xb, lab, w1, w1b, b1, b1b, w2, w2b, b2, b2b, h1, h1b, z, zb, i_b, i_in, i_h, i_out, check=False):
+    """Adjoint of mlp2_ce (corpus/mlp2_ce_b.jl); returns nothing.  check=True raises
+    StadeHipBoundsError for a label outside 1..i_out (one synchronisation)."""
     import torch
     B, I, H, O, s = _mlp_sizes(i_b, i_in, i_h, i_out)
     f = _f32()
@@ -351,10 +377,11 @@ def mlp2_ce_b(loss, lossb, x, xb, lab, w1, w1b, b1, b1b, w2, w2b, b2, b2b, h1, h
          _arr("b2", b2, f, O), _arr("b2b", b2b, f, O), _arr("h1", h1, f, s["h1"]), _arr("h1b", h1b, f, s["h1"]),
          _arr("z", z, f, s["z"]), _arr("zb", zb, f, s["z"]), B, I, H, O]
     _call("stade_hip_mlp2_ce_b", a, _stream_of(x))
+    _bounds("mlp2_ce_b", check)
 
 
-def mlp2_ce_d(loss, lossd, x, xd, lab, w1, w1d, b1, b1d, w2, w2d, b2, b2d, h1, h1d, z, zd, i_b, i_in, i_h, i_out):
-    """Tangent of mlp2_ce (corpus/mlp2_ce_d.jl); returns nothing."""
+def mlp2_ce_d(loss, lossd, x, xd, lab, w1, w1d, b1, b1d, w2, w2d, b2, b2d, h1, h1d, z, zd, i_b, i_in, i_h, i_out, check=False):
+    """Tangent of mlp2_ce (corpus/mlp2_ce_d.jl); returns nothing.  check as for mlp2_ce_b."""
     import torch
     B, I, H, O, s = _mlp_sizes(i_b, i_in, i_h, i_out)
     f = _f32()
@@ -364,11 +391,12 @@ def mlp2_ce_d(loss, lossd, x, xd, lab, w1, w1d, b1, b1d, w2, w2d, b2, b2d, h1, h
          _arr("b2", b2, f, O), _arr("b2d", b2d, f, O), _arr("h1", h1, f, s["h1"]), _arr("h1d", h1d, f, s["h1"]),
          _arr("z", z, f, s["z"]), _arr("zd", zd, f, s["z"]), B, I, H, O]
     _call("stade_hip_mlp2_ce_d", a, _stream_of(x))
+    _bounds("mlp2_ce_d", check)
 
 
 def mlp2_ce_hv(loss, lossb, x, xb, lab, w1, w1b, b1, b1b, w2, w2b, b2, b2b, h1, h1b, z, zb, i_b, i_in, i_h, i_out,
-               lossd, lossbd, xd, xbd, w1d, w1bd, b1d, b1bd, w2d, w2bd, b2d, b2bd, h1d, h1bd, zd, zbd):
-    """HVP of mlp2_ce (corpus/mlp2_ce_hv.jl); returns nothing."""
+               lossd, lossbd, xd, xbd, w1d, w1bd, b1d, b1bd, w2d, w2bd, b2d, b2bd, h1d, h1bd, zd, zbd, check=False):
+    """HVP of mlp2_ce (corpus/mlp2_ce_hv.jl); returns nothing.  check as for mlp2_ce_b."""
     import torch
     B, I, H, O, s = _mlp_sizes(i_b, i_in, i_h, i_out)
     f = _f32()
@@ -382,6 +410,7 @@ def mlp2_ce_hv(loss, lossb, x, xb, lab, w1, w1b, b1, b1b, w2, w2b, b2, b2b, h1, 
          _arr("w2d", w2d, f, s["w2"]), _arr("w2bd", w2bd, f, s["w2"]), _arr("b2d", b2d, f, O), _arr("b2bd", b2bd, f, O),
          _arr("h1d", h1d, f, s["h1"]), _arr("h1bd", h1bd, f, s["h1"]), _arr("zd", zd, f, s["z"]), _arr("zbd", zbd, f, s["z"])]
     _call("stade_hip_mlp2_ce_hv", a, _stream_of(x))
+    _bounds("mlp2_ce_hv", check)
 
 
 # ------------------------------------------------------------------------------------------

@@ -48,6 +48,8 @@ class KernelSpec:
     modes: dict                    # 'b' | 'd' | 'hv' -> Mode
     stacks: tuple = ()             # (name, eltype, julia size expression) of initstacks_<k>_b
     stack_args: tuple = ()         # initstacks_<k>_b arguments
+    device_checked: tuple = ()     # Int64 arrays whose values index other arrays on the device
+                                   # (an out-of-range value raises the device error flag)
 
 
 def _a(*names):
@@ -113,7 +115,8 @@ KERNELS: dict[str, KernelSpec] = {
                        + (("i_b", "I"), ("i_in", "I"), ("i_h", "I"), ("i_out", "I"))
                        + _a("lossd", "lossbd", "xd", "xbd", "w1d", "w1bd", "b1d", "b1bd", "w2d", "w2bd", "b2d", "b2bd",
                             "h1d", "h1bd", "zd", "zbd")),
-        }),
+        },
+        device_checked=("lab",)),
     "conv3x3": KernelSpec(
         "conv3x3", "Float32",
         {
@@ -180,7 +183,7 @@ def identify(text: str) -> tuple[KernelSpec, dict]:
                           f"(functions found: {names}; implemented: {', '.join(sorted(KERNELS))})")
 
 
-def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, str]]) -> str:
+def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, str]], inbounds: bool = True) -> str:
     T = spec.eltype
     sig, types, vals = [], [], []
     rets = []
@@ -222,6 +225,13 @@ def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, s
     lines.append(f"                     {', '.join(vals)})")
     lines.append("    end")
     lines.append(f"    __rc == 0 || error(\"{mode.entry}: \", unsafe_string(ccall((:stade_hip_last_error, libstade_hip), Cstring, ())))")
+    if not inbounds and spec.device_checked:
+        # bounds checking on (`inbounds=false`): the device flag, read after the launches,
+        # stands for the generated code's BoundsError on an out-of-range index value
+        lines.append("    __flag = Ref{Int32}(0)")
+        lines.append("    __rc = ccall((:stade_hip_device_error, libstade_hip), Int32, (Ref{Int32},), __flag)")
+        lines.append("    __rc == 0 || error(\"stade_hip_device_error: \", unsafe_string(ccall((:stade_hip_last_error, libstade_hip), Cstring, ())))")
+        lines.append(f"    __flag[] == 0 || throw(BoundsError({spec.device_checked[0]}))")
     if not rets:
         lines.append("    return nothing")
     elif len(rets) == 1:
@@ -232,11 +242,15 @@ def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, s
     return "\n".join(lines)
 
 
-def stade_hip_file(in_path, out_path, *, precision=None, lib_path: str | None = None) -> str:
+def stade_hip_file(in_path, out_path, *, precision=None, inbounds: bool = True, lib_path: str | None = None) -> str:
     """Write Julia host code for the generated functions of `in_path` into `out_path`.
 
     `precision` mirrors `stade_amdgpu_file`'s keyword: `None` keeps the kernel's element
     type; a precision the library does not implement for that kernel is refused.
+    `inbounds` mirrors it too: with `inbounds=false` the host functions read the device
+    error flag after the call (one synchronisation) and throw a `BoundsError` where an
+    index value held in an Int64 array (the MLP labels) is out of range; with the default
+    `true`, as in the reference's GPU code, nothing is checked.
     Returns the written text.
     """
     text = Path(in_path).read_text()
@@ -278,7 +292,7 @@ def stade_hip_file(in_path, out_path, *, precision=None, lib_path: str | None = 
                 if args != want:
                     raise StadeHipRefusal(f"{fname}: argument list {args} differs from the one libstade_hip implements {want}")
                 stacks = [(nm, et) for nm, et, _ in spec.stacks] if mode_key != "d" else []
-                out.append(_jl_call(spec, fname, mode, stacks))
+                out.append(_jl_call(spec, fname, mode, stacks, inbounds))
                 out.append("")
                 emitted += 1
     if emitted == 0:

@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import os
+import threading
 from pathlib import Path
 
 import numpy as np
@@ -100,117 +101,191 @@ def make_args(lib, fname: str, shapes: dict, ints: dict, scalars: dict, seed: st
     return out
 
 
+def _log_parity(record: dict):
+    """Append one JSON line per compared output to $STADE_PARITY_LOG (when set): the GPU's
+    error against the oracle and, where the truth rule decided, both errors against the truth."""
+    path = os.environ.get("STADE_PARITY_LOG")
+    if not path:
+        return
+    import json
+    Path(path).parent.mkdir(parents=True, exist_ok=True)
+    with open(path, "a") as f:
+        f.write(json.dumps(record) + "\n")
+
+
+class ParityCase:
+    """One generated function on the oracle and on libstade_hip with the same inputs.
+
+    The phases are separate so that a slow oracle run (seconds to minutes at the benchmark
+    sizes) can run in a worker thread while the GPU works on other cases: the oracle runs
+    in C through ctypes, which releases the GIL.
+
+    args: [(name, kind, value)] in the generated function's order, kind in
+    'i' (Int64), 'f' (Float scalar), 'Af' (Float array), 'Ai' (Int64 array); stacks:
+    [(name, (length, 'Ai' | 'Af'))] appended after the arguments (filled with NaN / -7 so a
+    slot read before it is written shows)."""
+
+    def __init__(self, name: str, mode: str, args: list, stacks=(), precision: str = "f64",
+                 rtol: float | None = None, offset: int = 0, label: str | None = None):
+        self.name, self.mode, self.fname = name, mode, f"{name}_{mode}"
+        self.args, self.stacks, self.precision, self.offset = args, tuple(stacks), precision, offset
+        self.fdt = np.float32 if precision == "f32" else np.float64
+        self.rtol = rtol if rtol is not None else RTOL[self.fdt]
+        self.label = label or self.fname
+        self.host = None
+        self._truth = None
+        self._truth_lock = threading.Lock()
+
+    # -- oracle (CPU) ---------------------------------------------------------------------
+    def run_oracle(self, lib=None):
+        lib = lib or oracle_lib(self.name, self.mode, self.precision)
+        host = [v.copy(order="K") if isinstance(v, np.ndarray) else v for _, _, v in self.args]
+        stack_h = [np.full(length, -7, dtype=np.int64) if kind == "Ai" else np.full(length, np.nan, dtype=self.fdt)
+                   for _, (length, kind) in self.stacks]
+        self.ret_h = lib.call(self.fname, *host, *stack_h)
+        for (a, kind, _), h in zip(self.args, host):
+            if isinstance(h, np.ndarray) and kind == "Af":
+                assert np.all(np.isfinite(h)), f"{self.fname}: the oracle's {a} is not finite: the case's inputs are out of range"
+        self.host, self.stack_h = host, stack_h
+        return self
+
+    def run_truth(self):
+        """The same generated text in a wider type: 80-bit extended for fp64 code, fp64 for
+        fp32 code."""
+        with self._truth_lock:
+            return self._truth_locked()
+
+    def _truth_locked(self):
+        if self._truth is None:
+            tprec, tdt = ("f80", np.longdouble) if self.precision == "f64" else ("f64", np.float64)
+            tl = oracle_lib(self.name, self.mode, tprec)
+            th = [v.astype(np.int64 if v.dtype == np.int64 else tdt, order="K") if isinstance(v, np.ndarray) else v
+                  for _, _, v in self.args]
+            ts = [np.full(length, -7, dtype=np.int64) if kind == "Ai" else np.full(length, np.nan, dtype=tdt)
+                  for _, (length, kind) in self.stacks]
+            tr = tl.call(self.fname, *th, *ts)
+            self._truth = dict(arrays=th, stacks=ts, ret=tr)
+        return self._truth
+
+    # -- GPU -------------------------------------------------------------------------------
+    def run_gpu(self):
+        import stade_hip
+        import torch
+        offset = self.offset
+
+        def device_array(v):
+            t = torch.from_numpy(np.ascontiguousarray(v.ravel(order="F")))
+            if offset == 0:
+                return t.to("cuda")
+            buf = torch.zeros(t.numel() + offset, dtype=t.dtype, device="cuda")
+            buf[offset:] = t.to("cuda")
+            return buf[offset:]
+
+        dev = [device_array(v) if isinstance(v, np.ndarray) else v for _, _, v in self.args]
+        stack_d = []
+        for _, (length, kind) in self.stacks:
+            if kind == "Ai":
+                stack_d.append(torch.full((length + offset,), -7, dtype=torch.int64, device="cuda")[offset:])
+            else:
+                stack_d.append(torch.full((length + offset,), float("nan"),
+                                          dtype=torch.float64 if self.fdt == np.float64 else torch.float32, device="cuda")[offset:])
+        ret_d = getattr(stade_hip, self.fname)(*dev, *stack_d)
+        torch.cuda.synchronize()
+        if ret_d is None:
+            ret_d = ()
+        elif not isinstance(ret_d, tuple):
+            ret_d = (ret_d,)
+        self.dev, self.stack_d, self.ret_d = dev, stack_d, ret_d
+        return self
+
+    # -- comparison ------------------------------------------------------------------------
+    def compare(self) -> float:
+        """Every output argument, stack and returned scalar of the GPU run against the oracle;
+        fails listing every output that differs.  Returns the worst error used for a verdict."""
+        assert self.host is not None, "run_oracle() first"
+        rtol, fname = self.rtol, self.fname
+        failures: list[str] = []
+
+        def verdict(label, got, cpu, tvalue):
+            """Pass if the GPU is within rtol of the oracle; else apply the reference's truth rule
+            (`val_truth_verdict_lines` /root/reference/src/STADE.jl:18915-18932) without its 1e-10
+            ceiling: GPU error <= max(rtol, 20 x the oracle's own error), both against the truth."""
+            e = rel_err(got, cpu)
+            rec = {"case": self.label, "output": label, "rtol": rtol, "gpu_vs_oracle": e}
+            if e <= rtol:
+                _log_parity(rec)
+                return e
+            t = np.asarray(tvalue(), dtype=np.longdouble)
+            eg = float(rel_err(np.asarray(got, np.longdouble), t))
+            ec = float(rel_err(np.asarray(cpu, np.longdouble), t))
+            rec.update(truth_rule=True, gpu_vs_truth=eg, oracle_vs_truth=ec, passed=eg <= max(rtol, 20.0 * ec))
+            _log_parity(rec)
+            print(f"truth rule: {self.label} {label}: GPU vs oracle {e:.3e} > {rtol:.0e}; vs truth GPU {eg:.3e}, "
+                  f"oracle {ec:.3e}", flush=True)
+            if not rec["passed"]:
+                failures.append(f"{label}: relative error {e:.3e} against the oracle; against the truth "
+                                f"GPU {eg:.3e}, oracle {ec:.3e} (bar max({rtol:.0e}, 20 x oracle))")
+            return eg
+
+        worst = 0.0
+        for idx, ((a, kind, _), h, d) in enumerate(zip(self.args, self.host, self.dev)):
+            if not isinstance(h, np.ndarray):
+                continue
+            got = to_host(d)
+            want = np.ravel(h, order="F")
+            if kind == "Ai":
+                if not np.array_equal(got, want):
+                    failures.append(f"{fname}: Int64 array {a} differs")
+                continue
+            if not np.any(want):
+                if np.any(got):
+                    failures.append(f"{fname}:{a}: expected exact zeros, max |got| = {np.max(np.abs(got))}")
+                continue
+            worst = max(worst, verdict(f"{fname}:{a}", got, want,
+                                       lambda idx=idx: np.ravel(self.run_truth()["arrays"][idx], order="F")))
+        for sk, ((sname, (length, kind)), h, d) in enumerate(zip(self.stacks, self.stack_h, self.stack_d)):
+            got = to_host(d)
+            if kind == "Ai":
+                assert np.array_equal(got, h), f"{fname}: stack {sname} differs"
+                continue
+            wn, gn = np.isnan(h), np.isnan(got)
+            assert np.array_equal(wn, gn), f"{fname}: stack {sname} written at different slots"
+            if not wn.any():
+                # every slot written: compare in place (a tape can hold 10^9 values)
+                worst = max(worst, verdict(f"{fname}:{sname}", got, h, lambda sk=sk: self.run_truth()["stacks"][sk]))
+            else:
+                worst = max(worst, verdict(f"{fname}:{sname}", got[~gn], h[~wn],
+                                           lambda sk=sk, wn=wn: self.run_truth()["stacks"][sk][~wn]))
+            del got
+        assert len(self.ret_h) == len(self.ret_d), f"{fname}: {len(self.ret_d)} returned values, expected {len(self.ret_h)}"
+        for k, (h, d) in enumerate(zip(self.ret_h, self.ret_d)):
+            if d == h:
+                continue
+            worst = max(worst, verdict(f"{fname}: returned value {k}", np.array([d]), np.array([h]),
+                                       lambda k=k: np.array([self.run_truth()["ret"][k]])))
+        assert not failures, "\n".join(failures)
+        return worst
+
+
 def run_parity(name: str, mode: str, shapes: dict, ints: dict, scalars: dict | None = None,
                seed: str | None = None, precision: str = "f64", rtol: float | None = None,
                stacks: tuple = (), int_arrays: dict | None = None, oracle=None, scales: dict | None = None,
                offset: int = 0):
-    """Run one generated function on the oracle and on libstade_hip with the same inputs;
-    compare every argument's final value and the returned scalars.  Returns the worst error.
+    """Run one generated function on the oracle and on libstade_hip with the same seeded
+    inputs; compare every argument's final value and the returned scalars.  Returns the
+    worst error.
 
     offset > 0 passes every device array as a view starting `offset` elements into a larger
     allocation (so its address is only element-aligned)."""
-    import stade_hip
-    import torch
     scalars = scalars or {}
     fdt = np.float32 if precision == "f32" else np.float64
-    rtol = rtol if rtol is not None else RTOL[fdt]
     lib = oracle or oracle_lib(name, mode, precision)
     fname = f"{name}_{mode}"
     shp = dict(shapes)
     shp["__stacks__"] = tuple(s for s, _ in stacks)
     args = make_args(lib, fname, shp, ints, scalars, seed or f"{fname}-{ints}", fdt, int_arrays, scales)
-    host = [v.copy(order="K") if isinstance(v, np.ndarray) else v for _, _, v in args]
-    def device_array(v):
-        t = torch.from_numpy(np.ascontiguousarray(v.ravel(order="F")))
-        if offset == 0:
-            return t.to("cuda")
-        buf = torch.zeros(t.numel() + offset, dtype=t.dtype, device="cuda")
-        buf[offset:] = t.to("cuda")
-        return buf[offset:]
-
-    dev = [device_array(v) if isinstance(v, np.ndarray) else v for _, _, v in args]
-    stack_h, stack_d = [], []
-    for sname, (length, kind) in stacks:
-        if kind == "Ai":
-            stack_h.append(np.full(length, -7, dtype=np.int64))
-            stack_d.append(torch.full((length + offset,), -7, dtype=torch.int64, device="cuda")[offset:])
-        else:
-            stack_h.append(np.full(length, np.nan, dtype=fdt))
-            stack_d.append(torch.full((length + offset,), float("nan"), dtype=torch.float64 if fdt == np.float64 else torch.float32,
-                                      device="cuda")[offset:])
-    ret_h = lib.call(fname, *host, *stack_h)
-    for (a, kind, _), h in zip(args, host):
-        if isinstance(h, np.ndarray) and kind == "Af":
-            assert np.all(np.isfinite(h)), f"{fname}: the oracle's {a} is not finite: the case's inputs are out of range"
-    ret_d = getattr(stade_hip, fname)(*dev, *stack_d)
-    torch.cuda.synchronize()
-    if ret_d is None:
-        ret_d = ()
-    elif not isinstance(ret_d, tuple):
-        ret_d = (ret_d,)
-
-    # The truth, computed only when a direct comparison fails: the same generated text in a
-    # wider type (80-bit extended for fp64 code, fp64 for fp32 code).
-    truth_cache = {}
-
-    def truth():
-        if not truth_cache:
-            tprec, tdt = ("f80", np.longdouble) if precision == "f64" else ("f64", np.float64)
-            tl = oracle_lib(name, mode, tprec)
-            th = [v.astype(np.int64 if v.dtype == np.int64 else tdt, order="K") if isinstance(v, np.ndarray) else v
-                  for _, _, v in args]
-            ts = [np.full(length, -7, dtype=np.int64) if kind == "Ai" else np.full(length, np.nan, dtype=tdt)
-                  for _, (length, kind) in stacks]
-            tr = tl.call(fname, *th, *ts)
-            truth_cache.update(arrays=th, stacks=ts, ret=tr)
-        return truth_cache
-
-    def verdict(label, got, cpu, tvalue):
-        """Pass if the GPU is within rtol of the oracle; else apply the reference's truth rule
-        (`val_truth_verdict_lines` /root/reference/src/STADE.jl:18915-18932) without its 1e-10
-        ceiling: GPU error <= max(rtol, 20 x the oracle's own error), both against the truth."""
-        e = rel_err(got, cpu)
-        if e <= rtol:
-            return e
-        t = np.asarray(tvalue(), dtype=np.longdouble)
-        eg = float(rel_err(np.asarray(got, np.longdouble), t))
-        ec = float(rel_err(np.asarray(cpu, np.longdouble), t))
-        if eg > max(rtol, 20.0 * ec):
-            failures.append(f"{label}: relative error {e:.3e} against the oracle; against the truth "
-                            f"GPU {eg:.3e}, oracle {ec:.3e} (bar max({rtol:.0e}, 20 x oracle))")
-        return eg
-
-    # every output is checked before failing, so one report names all that differ
-    failures: list[str] = []
-    worst = 0.0
-    for idx, ((a, kind, _), h, d) in enumerate(zip(args, host, dev)):
-        if not isinstance(h, np.ndarray):
-            continue
-        got = to_host(d)
-        want = np.ravel(h, order="F")
-        if kind == "Ai":
-            if not np.array_equal(got, want):
-                failures.append(f"{fname}: Int64 array {a} differs")
-            continue
-        if np.all(want == 0):
-            if not np.all(got == 0):
-                failures.append(f"{fname}:{a}: expected exact zeros, max |got| = {np.max(np.abs(got))}")
-            continue
-        worst = max(worst, verdict(f"{fname}:{a}", got, want, lambda idx=idx: np.ravel(truth()["arrays"][idx], order="F")))
-    for sk, ((sname, (length, kind)), h, d) in enumerate(zip(stacks, stack_h, stack_d)):
-        got = to_host(d)
-        if kind == "Ai":
-            assert np.array_equal(got, h), f"{fname}: stack {sname} differs"
-        else:
-            wn, gn = np.isnan(h), np.isnan(got)
-            assert np.array_equal(wn, gn), f"{fname}: stack {sname} written at different slots"
-            worst = max(worst, verdict(f"{fname}:{sname}", got[~gn], h[~wn],
-                                       lambda sk=sk, wn=wn: truth()["stacks"][sk][~wn]))
-    assert len(ret_h) == len(ret_d), f"{fname}: {len(ret_d)} returned values, expected {len(ret_h)}"
-    for k, (h, d) in enumerate(zip(ret_h, ret_d)):
-        if d == h:
-            continue
-        worst = max(worst, verdict(f"{fname}: returned value {k}", np.array([d]), np.array([h]),
-                                   lambda k=k: np.array([truth()["ret"][k]])))
-    assert not failures, "\n".join(failures)
-    return worst
+    label = f"{fname} {ints}" + (f" offset={offset}" if offset else "")
+    case = ParityCase(name, mode, args, stacks, precision, rtol, offset, label)
+    case.run_oracle(lib)
+    case.run_gpu()
+    return case.compare()

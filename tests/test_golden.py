@@ -144,4 +144,4 @@ def test_gpu_matches_golden(name, mode):
     torch.cuda.synchronize()
     ret = () if ret is None else (ret if isinstance(ret, tuple) else (ret,))
     arrays = {a: (d.cpu().numpy() if isinstance(d, torch.Tensor) else d) for (a, _), d in zip(args, dev)}
-    _check(name, mode, fx, arrays, ret, 2e-5 if fdt == np.float32 else 1e-10)
+    _check(name, mode, fx, arrays, ret, 1e-5 if fdt == np.float32 else 1e-10)
