@@ -102,6 +102,16 @@ int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, co
 int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
                                  int64_t n, double* lossd, const double* lossbd, const double* ud, double* ubd, double* und,
                                  double* unbd, hipStream_t stream);
+/* No counterpart in the reference: stade_hip_diffusion2d_b for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, effects and kernels; the pass-1 loss partials live in a static device array
+ * of 131072 doubles (1 MiB per GPU, held until the process ends) instead of the library
+ * workspace, and the call makes no allocation.  A grid needing more partials than that
+ * (n above 23168 in the worst case; 32768 when n is a multiple of 128 and the arrays are
+ * 16-byte aligned) is refused with STADE_HIP_ERANGE before any work.  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (different streams or threads) race. */
+int32_t stade_hip_diffusion2d_b_noalloc(double* loss, const double* lossb, const double* u, double* ub, double* un,
+                                        double* unb, int64_t n, hipStream_t stream);
 
 /* ---- config 5: burgers1d(loss, u, un, nu, dt, dx, tend, n, nsteps) ------------------------
  * explicit viscous Burgers on n periodic cells, at most nsteps steps, each taken while the

@@ -32,6 +32,8 @@
 //   * blockIdx = chunk * strips + strip: the blocks that share a halo row are `strips`
 //     launches apart, on the same XCD (round-robin dispatch) when strips is a multiple of 8.
 #include "internal.hpp"
+
+#include <mutex>
 #include <initializer_list>
 #include "../../include/stade_hip.h"
 
@@ -861,12 +863,98 @@ Grid grid_of(int64_t n) {
     return Grid{strips, strips * chunks};
 }
 
+// the adjoint's reduction partials: one per wave (block on the row-streaming path) of pass 1
+int64_t adjoint_partials(int64_t n, bool pairs) {
+    if (pairs) return (n / WS2) * (n / WCH2);
+    if (wave_path(n)) return (n / WS) * (n / WCH);
+    const Grid g = grid_of(n);
+    return g.blocks;
+}
+
+// the adjoint: pass 1 (un, the loss partials and the owner-computes gather into ub), then
+// pass 2 (the unb reset, with the loss sum of the partials); `partials` holds at least
+// adjoint_partials(n, pairs_ok(...)) doubles
+int32_t adjoint(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb, int64_t n,
+                double* partials, hipStream_t stream) {
+    int nparts;
+    if (pairs_ok(n, {u, un, unb, ub})) {
+        const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2);
+        STADE_TIMED("diffusion2d_b", stream,
+                    diffusion_b_wave2<false, WCH2, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(
+                        u, nullptr, un, nullptr, unb, nullptr, ub, nullptr, lossb, nullptr, (int)n, nstrips, nwaves, partials));
+        STADE_LAUNCHED("diffusion_b_wave2");
+        nparts = nwaves;
+    } else if (wave_path(n)) {
+        const WaveGrid w = wave_grid_of(n, WCH);
+        STADE_TIMED("diffusion2d_b", stream,
+                    diffusion_b_wave<false, WCH, WD><<<w.blocks, 256, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr,
+                                                                              lossb, nullptr, (int)n, w.nstrips, w.nwaves, partials));
+        STADE_LAUNCHED("diffusion_b_wave");
+        nparts = w.nwaves;
+    } else {
+        const Grid g = grid_of(n);
+        STADE_TIMED("diffusion2d_b", stream,
+                    diffusion_b_kernel<false><<<g.blocks, NT, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr,
+                                                                           lossb, nullptr, (int)n, g.strips, partials));
+        STADE_LAUNCHED("diffusion_b_kernel");
+        nparts = g.blocks;
+    }
+    STADE_TIMED("zero", stream,
+                zero2_kernel<1><<<zero_blocks(n * n), NT, 0, stream>>>(unb, nullptr, (size_t)(n * n), partials, nparts,
+                                                                       SumOuts{{loss}}));
+    STADE_LAUNCHED("zero2_kernel");
+    return STADE_HIP_OK;
+}
+
+// ------------------------------------------------------------------------------------------
+// Scratch of the allocation-free adjoint (stade_hip_diffusion2d_b_noalloc): the pass-1 loss
+// partials in a static device array, one copy per GPU, held until the process ends.  Host
+// code never passes `scratch` itself (in host code the name is a stand-in, not a device
+// address): each device's address is looked up once with hipGetSymbolAddress and kept.
+// ------------------------------------------------------------------------------------------
+constexpr int64_t kNoAllocPartials = 131072;  // 1 MiB of doubles
+static __device__ __align__(256) double scratch[kNoAllocPartials];
+static std::mutex g_scratch_mu;
+static double* g_scratch_ptr[64];
+
+int32_t noalloc_scratch(double** out) {
+    int dev = 0;
+    STADE_TRY_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return set_error(STADE_HIP_ERANGE, "device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        STADE_TRY_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) return set_error(STADE_HIP_ENOMEM, "hipGetSymbolAddress returned no address for the scratch array");
+        g_scratch_ptr[dev] = (double*)ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return STADE_HIP_OK;
+}
+
 }  // namespace
 }  // namespace stade
 
 using namespace stade;
 
 extern "C" {
+
+int32_t stade_hip_diffusion2d_b_noalloc(double* loss, const double* lossb, const double* u, double* ub, double* un,
+                                        double* unb, int64_t n, hipStream_t stream) {
+    if (int32_t rc = check_n(n, "stade_hip_diffusion2d_b_noalloc")) return rc;
+    if (n == 0) return STADE_HIP_OK;
+    if (!loss || !lossb || !u || !ub || !un || !unb)
+        return set_error(STADE_HIP_EINVAL, "stade_hip_diffusion2d_b_noalloc: null pointer");
+    const int64_t need = adjoint_partials(n, pairs_ok(n, {u, un, unb, ub}));
+    if (need > kNoAllocPartials)
+        return set_error(STADE_HIP_ERANGE,
+                         "stade_hip_diffusion2d_b_noalloc: n = %lld needs %lld partial sums, above the %lld of the static "
+                         "scratch (use stade_hip_diffusion2d_b)",
+                         (long long)n, (long long)need, (long long)kNoAllocPartials);
+    double* partials = nullptr;
+    if (int32_t rc = noalloc_scratch(&partials)) return rc;
+    return adjoint(loss, lossb, u, ub, un, unb, n, partials, stream);
+}
 
 int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, const double* ud, double* un, double* und,
                                 int64_t n, hipStream_t stream) {
@@ -910,35 +998,7 @@ int32_t stade_hip_diffusion2d_b(double* loss, const double* lossb, const double*
     WsCall call_(stream);
     Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
-    int nparts;
-    if (pairs_ok(n, {u, un, unb, ub})) {
-        const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2);
-        STADE_TIMED("diffusion2d_b", stream,
-                    diffusion_b_wave2<false, WCH2, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(
-                        u, nullptr, un, nullptr, unb, nullptr, ub, nullptr, lossb, nullptr, (int)n, nstrips, nwaves, ws->partials));
-        STADE_LAUNCHED("diffusion_b_wave2");
-        nparts = nwaves;
-    } else if (wave_path(n)) {
-        const WaveGrid w = wave_grid_of(n, WCH);
-        STADE_TIMED("diffusion2d_b", stream,
-                    diffusion_b_wave<false, WCH, WD><<<w.blocks, 256, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr,
-                                                                              lossb, nullptr, (int)n, w.nstrips, w.nwaves,
-                                                                              ws->partials));
-        STADE_LAUNCHED("diffusion_b_wave");
-        nparts = w.nwaves;
-    } else {
-        const Grid g = grid_of(n);
-        STADE_TIMED("diffusion2d_b", stream,
-                    diffusion_b_kernel<false><<<g.blocks, NT, 0, stream>>>(u, nullptr, un, nullptr, unb, nullptr, ub, nullptr,
-                                                                           lossb, nullptr, (int)n, g.strips, ws->partials));
-        STADE_LAUNCHED("diffusion_b_kernel");
-        nparts = g.blocks;
-    }
-    STADE_TIMED("zero", stream,
-                zero2_kernel<1><<<zero_blocks(n * n), NT, 0, stream>>>(unb, nullptr, (size_t)(n * n), ws->partials, nparts,
-                                                                       SumOuts{{loss}}));
-    STADE_LAUNCHED("zero2_kernel");
-    return STADE_HIP_OK;
+    return adjoint(loss, lossb, u, ub, un, unb, n, ws->partials, stream);
 }
 
 int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,

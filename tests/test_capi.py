@@ -60,3 +60,17 @@ def test_product_path_refuses_cpu_tensors():
         stade_hip.diffusion2d_b(t[:1], t[:1], t, t, t, t, 2)
     with pytest.raises(TypeError, match="Int64"):
         stade_hip.diffusion2d_b(t[:1], t[:1], t, t, t, t, 2.0)
+
+
+def test_noalloc_refuses_grids_beyond_its_scratch():
+    """n = 46336 (a multiple of 128, 16-byte aligned arrays) needs 362 x 724 = 262088
+    partial sums, above the static scratch's 131072: refused before any device work (the
+    pointers are never dereferenced)."""
+    L = _lib()
+    f = L.stade_hip_diffusion2d_b_noalloc
+    f.restype = ctypes.c_int32
+    f.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int64, ctypes.c_void_p]
+    fake = ctypes.c_void_p(1 << 20)   # 16-byte aligned, never dereferenced
+    rc = f(fake, fake, fake, fake, fake, fake, 46336, None)
+    assert rc == -3 and b"262088 partial sums" in L.stade_hip_last_error()
+    assert f(None, None, None, None, None, None, 0, None) == 0
