@@ -310,10 +310,11 @@ class Mlp(Workload):
         self.B, self.I, self.H, self.O = B, I, H, O
         g = 2.0 * H * I * B
         # flops per launch of each matrix-core kernel: the tangent and HVP run each pair
-        # (s1, s1d), (W1b, W1bd), (xb, xbd) as one dual launch of three products
-        self.kernels = {"b": {"mlp_gemm_s1": g, "mlp_gemm_w1b": g, "mlp_gemm_xb": g},
+        # (s1, s1d), (W1b, W1bd), (xb, xbd) as one dual launch of three products, and the two
+        # backward products (W1b and xb, or their dual forms) share one launch
+        self.kernels = {"b": {"mlp_gemm_s1": g, "mlp_gemm_bwd": 2 * g},
                         "d": {"mlp_gemm_s1d": 3 * g},
-                        "hv": {"mlp_gemm_s1d": 3 * g, "mlp_gemm_w1bd": 3 * g, "mlp_gemm_xbd": 3 * g}}[mode]
+                        "hv": {"mlp_gemm_s1d": 3 * g, "mlp_gemm_bwd2": 6 * g}}[mode]
         self.kernel = next(iter(self.kernels))
 
     def host_inputs(self):
@@ -639,7 +640,9 @@ def main():
         "roofline": res.get("roofline"),
         "cpu_baseline": cpu,
         "eval_hbm_frac": res.get("eval_hbm_frac"),
+        "eval_mfma_frac": res.get("eval_mfma_frac"),
         "kernel_ms": res.get("kernel_ms"),
+        "kernels": res.get("kernels"),
         "kernel_timing": "HIP event pair around each launch of the dominant kernel on its own stream, over a second "
                          "pass of the same K steps; value and ms_per_step come from the first, event-free pass",
         "configs": {k: {kk: vv for kk, vv in v.items() if kk != "config"} | {"workload": v["config"].get("workload")}

@@ -24,7 +24,10 @@
 //
 // Split K: with `ksplit` > 1 the K steps (of all segments, in order) are cut into ksplit
 // contiguous ranges, one per blockIdx.z; each writes its partial tile to a scratch slice
-// and a second kernel adds the slices in slice order and applies the epilogue.  The host
+// and a second kernel adds the slices in slice order and applies the epilogue.  An epilogue
+// that only accumulates (C += v: a shadow, as the generated adjoint code accumulates it)
+// can instead take the slices by atomic addition straight into C (`Epi::kAtomic`): no
+// partial tiles and no second kernel, with the slices' order left to the hardware.  The host
 // picks the tile width and the split from a cost model (plan()).
 #pragma once
 
@@ -68,7 +71,8 @@ struct Args {
     int nseg;
     int M, N;
     int ksplit;     // blockIdx.z ranges over ksplit slices of the K steps
-    float* part;    // ksplit > 1: partial tiles, slice z at part + z * M * N, column-major
+    bool atomic;    // ksplit > 1: slices added into the output by atomics (Epi::kAtomic)
+    float* part;    // ksplit > 1, !atomic: partial tiles, slice z at part + z * M * N, column-major
     bool bufok;     // set by launch(): every operand's byte extent fits 31 bits and the two
                     // segments share lda and ldb, so whole tiles may use buffer loads
 };
@@ -189,6 +193,13 @@ __device__ __forceinline__ void store_tile(const Stage<ROWS>& st, float* __restr
     }
 }
 
+// an epilogue that only accumulates declares `static constexpr bool kAtomic = true` and an
+// atomic(m, n, v) (dual: atomic(m, n, p, q)) adding into its output
+template <class E, class = void>
+struct has_atomic : std::false_type {};
+template <class E>
+struct has_atomic<E, std::void_t<decltype(E::kAtomic)>> : std::integral_constant<bool, E::kAtomic> {};
+
 template <int... U, class F>
 __device__ __forceinline__ void unroll_seq(std::integer_sequence<int, U...>, F&& f) {
     (f(std::integral_constant<int, U>{}), ...);
@@ -204,14 +215,21 @@ __device__ __forceinline__ void unroll_seq(std::integer_sequence<int, U...>, F&&
 // (a tangent pair such as s1 = W1 x, s1d = W1 xd + W1d x) with each operand tile loaded once.
 // The epilogue then takes both: load(m, n) returns a float2 of old values and
 // operator()(m, n, p, q, old) writes.
-template <bool A_KM, bool B_KM, int BNT, class Epi, bool DUAL = false>
-__global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
+// LDS floats of one block: two buffers of the A and B operand tiles (DUAL: two of each)
+template <int BNT, bool DUAL>
+constexpr int smem_floats() {
+    return 2 * (DUAL ? 2 : 1) * KQ * (ldq<BM>() + ldq<BNT>());
+}
+
+// One block of the product: the tile at (bx, by) of slice bz, with its LDS at smem.
+template <bool A_KM, bool B_KM, int BNT, class Epi, bool DUAL>
+__device__ __forceinline__ void gemm_block(const Args& g, bool vec, const Epi& epi, int bx, int by, int bz, float* smem) {
     constexpr int NJ = BNT / 64, LQA = ldq<BM>(), LQB = ldq<BNT>();
     constexpr int NOP = DUAL ? 2 : 1;  // operand pairs staged per step
-    __shared__ __attribute__((aligned(16))) float As[2][NOP][KQ * LQA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][NOP][KQ * LQB];
+    auto As = reinterpret_cast<float(*)[NOP][KQ * LQA]>(smem);
+    auto Bs = reinterpret_cast<float(*)[NOP][KQ * LQB]>(smem + 2 * NOP * KQ * LQA);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BNT;
+    const int m0 = bx * BM, n0 = by * BNT;
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BNT / 2);
 
     // Both segments' operands in registers (indexing g.seg[s] with a runtime s would reload
@@ -229,8 +247,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     // the K steps of all segments, in order (DUAL: of the shared K); this block's slice of them
     const int steps0 = (K0 + KT - 1) / KT;
     const int total = DUAL ? steps0 : steps0 + (K1 + KT - 1) / KT;
-    const int t_begin = (int)((long)total * blockIdx.z / g.ksplit);
-    const int t_end = (int)((long)total * (blockIdx.z + 1) / g.ksplit);
+    const int t_begin = (int)((long)total * bz / g.ksplit);
+    const int t_end = (int)((long)total * (bz + 1) / g.ksplit);
     // a block whose tiles all lie inside the operands (M, N and every K step) loads with no
     // per-element tests
     const bool full = vec && g.bufok && m0 + BM <= g.M && n0 + BNT <= g.N && K0 % KT == 0 && K1 % KT == 0;
@@ -390,10 +408,32 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     if (full) mainloop(std::true_type{});
     else mainloop(std::false_type{});
     // accumulator (i, j, r): m = m0 + wm + 32 i + lane % 32,  n = n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4
+    if constexpr (has_atomic<Epi>::value) {
+        if (g.ksplit > 1 && g.atomic) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int m = m0 + wm + i * 32 + (lane & 31);
+                if (m >= g.M) continue;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                        if (n < g.N) {
+                            if constexpr (DUAL)
+                                epi.atomic(m, n, acc[0][i][j][r], acc[NOP - 1][i][j][r]);
+                            else
+                                epi.atomic(m, n, acc[0][i][j][r]);
+                        }
+                    }
+            }
+            return;
+        }
+    }
     if (g.ksplit > 1) {
         // slice z at part + z * NOP * M * N (DUAL: P then Q)
         const long mn = (long)g.M * g.N;
-        float* part = g.part + (long)blockIdx.z * NOP * mn;
+        float* part = g.part + (long)bz * NOP * mn;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int m = m0 + wm + i * 32 + (lane & 31);
@@ -445,6 +485,56 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
     }
 }
 
+template <bool A_KM, bool B_KM, int BNT, class Epi, bool DUAL = false>
+__global__ __launch_bounds__(NT) void gemm_kernel(Args g, bool vec, Epi epi) {
+    __shared__ __attribute__((aligned(16))) float smem[smem_floats<BNT, DUAL>()];
+    gemm_block<A_KM, B_KM, BNT, Epi, DUAL>(g, vec, epi, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+}
+
+// Two products in one launch, each block one tile of one of them: blocks [0, nblocks(P0))
+// are P0's (m tiles fastest, then n tiles, then K slices), the rest P1's.  Neither may need a
+// second kernel (a K split adds by atomics).  The two share the CUs, so the tail of one is
+// filled by blocks of the other.
+template <bool A_KM, bool B_KM, class Epi>
+struct Part {
+    Args g;
+    bool vec;
+    Epi epi;
+    int gx, gy;  // tile grid: m tiles, n tiles (slices: g.ksplit)
+};
+//
+// X: independent work that rides along as x.count extra blocks at the front of the grid, each
+// calling x(block, smem) with NT threads and at least 1088 floats of LDS (NoExtra: none).
+struct NoExtra {
+    int count = 0;
+    __device__ __forceinline__ void operator()(int, float*) const {}
+};
+template <class X>
+__global__ __launch_bounds__(NT) void extra_kernel(X x) {
+    __shared__ __attribute__((aligned(16))) float smem[1088];
+    x(blockIdx.x, smem);
+}
+template <int BNT, bool DUAL, bool A0, bool B0, class E0, bool A1, bool B1, class E1, class X>
+__global__ __launch_bounds__(NT) void gemm_pair_kernel(Part<A0, B0, E0> p0, Part<A1, B1, E1> p1, X x) {
+    static_assert(smem_floats<BNT, DUAL>() >= 1088, "the extra blocks' LDS");
+    __shared__ __attribute__((aligned(16))) float smem[smem_floats<BNT, DUAL>()];
+    const int n0 = p0.gx * p0.gy * p0.g.ksplit;
+    int b = blockIdx.x;
+    if (b < x.count) {
+        x(b, smem);
+        return;
+    }
+    b -= x.count;
+    if (b < n0) {
+        const int per = p0.gx * p0.gy, r = b % per;
+        gemm_block<A0, B0, BNT, E0, DUAL>(p0.g, p0.vec, p0.epi, r % p0.gx, r / p0.gx, b / per, smem);
+    } else {
+        b -= n0;
+        const int per = p1.gx * p1.gy, r = b % per;
+        gemm_block<A1, B1, BNT, E1, DUAL>(p1.g, p1.vec, p1.epi, r % p1.gx, r / p1.gx, b / per, smem);
+    }
+}
+
 // second stage of a split-K product: C(m, n) = sum over slices in order, then the epilogue
 // (DUAL: P and Q, each summed in slice order)
 template <class Epi, bool DUAL = false>
@@ -482,22 +572,31 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Tile width and K split for an M x N x K product on `cus` compute units, from a cost model
 // in microseconds: the CU with the most blocks sets the time (blocks per CU x K steps per
 // block x the time of one block step, about 0.7 us for a 128 x 64 x 16 step measured on
-// MI355X), a single resident block per CU runs at about 3/4 of the rate (one wave per SIMD
-// hides no latency), and a K split costs its partial tiles' round trip through memory
-// (8 bytes per element and slice at about 5 TB/s) plus the reduction launch.  Every K slice
-// keeps at least 8 steps.  Ties go to the narrow tile and the smaller split.
+// MI355X at two resident blocks per CU), scaled by the rate at the CU's residency (one
+// block: 3/4, one wave per SIMD hides no latency; three: 1.08; four or more: 1.13, measured
+// on the MLP's products), and a K split costs its partial tiles' round trip through memory
+// (8 bytes per element and slice at about 5 TB/s) plus the reduction launch, or, by atomics,
+// their atomic traffic (4 bytes per element and slice, overlapped with the other blocks'
+// work: about 10 TB/s of issue).  Every K slice keeps at least 8 steps.  Ties go to the
+// narrow tile and the smaller split.
 struct Plan {
     int bnt, ksplit;
+    bool atomic;  // the slices are added into the output by atomics (an accumulate epilogue)
 };
 #ifndef STADE_GEMM_STEP_US
 #define STADE_GEMM_STEP_US 0.7
 #endif
 // nout = 2 plans a dual product (three products per step over shared loads, two outputs).
-inline Plan plan(int M, int N, int Ktot, int cus, int nout = 1) {
+// atomic_ok: the epilogue only accumulates, so a split may add its slices by atomics (no
+// partial tiles, no reduction launch).
+#ifndef STADE_GEMM_ATOMIC_GBS
+#define STADE_GEMM_ATOMIC_GBS 10000.0
+#endif
+inline Plan plan(int M, int N, int Ktot, int cus, int nout = 1, bool atomic_ok = false) {
     const double work = nout == 2 ? 2.5 : 1.0;  // block-step time relative to a single product
     const long mt = (M + BM - 1) / BM;
     const long steps = (Ktot + KT - 1) / KT;
-    Plan best{64, 1};
+    Plan best{64, 1, false};
     double best_cost = 0.0;
     // (a dual product keeps the narrow tile: with the wide one its registers allow one wave per SIMD)
     for (int bnt = 64; bnt <= (nout == 2 ? 64 : 128); bnt *= 2) {
@@ -506,12 +605,15 @@ inline Plan plan(int M, int N, int Ktot, int cus, int nout = 1) {
             if (ks > 1 && steps / ks < 8) break;
             const long per_cu = (tiles * ks + cus - 1) / cus;
             const long st = (steps + ks - 1) / ks;
+            // an atomic split is kept to one round of resident blocks (four per CU)
+            if (atomic_ok && ks > 1 && per_cu > 4) break;
             double cost = (double)per_cu * st * STADE_GEMM_STEP_US * (KT / 16.0) * (bnt / 64) * work;
-            if (per_cu < 2) cost /= 0.75;
-            if (ks > 1) cost += 8.0 * ks * nout * (double)M * N / 5e6 + 3.0;
+            cost /= per_cu < 2 ? 0.75 : per_cu == 2 ? 1.0 : per_cu == 3 ? 1.08 : 1.13;
+            if (ks > 1) cost += atomic_ok ? 4.0 * ks * nout * (double)M * N / (STADE_GEMM_ATOMIC_GBS * 1e3)
+                                          : 8.0 * ks * nout * (double)M * N / 5e6 + 3.0;
             if (cost < best_cost || best_cost == 0.0) {
                 best_cost = cost;
-                best = Plan{bnt, ks};
+                best = Plan{bnt, ks, atomic_ok && ks > 1};
             }
         }
     }
@@ -534,16 +636,18 @@ inline int device_cus() {
 // Launch; returns the hipError of the launch.  `part` must hold ksplit * M * N floats (DUAL:
 // twice that) when the plan splits K (ask with plan() first); it may be null otherwise.  A
 // dual product takes two segments of the same K.
-template <bool A_KM, bool B_KM, class Epi, bool DUAL = false>
-hipError_t launch(Args g, Epi epi, hipStream_t stream, const Plan& p) {
-    if (g.M <= 0 || g.N <= 0) return hipSuccess;
+// the launch-time fields of g (split, atomic, buffer-load eligibility); vec: every operand
+// 16-byte aligned with leading dimensions a multiple of 4
+template <bool A_KM, bool B_KM, class Epi, bool DUAL>
+hipError_t prepare(Args& g, bool& vec, const Plan& p) {
     if (DUAL && (g.nseg != 2 || g.seg[0].K != g.seg[1].K)) return hipErrorInvalidValue;
-    bool vec = true;
+    vec = true;
     for (int s = 0; s < g.nseg; ++s) {
         vec = vec && aligned16(g.seg[s].A) && aligned16(g.seg[s].B) && g.seg[s].lda % 4 == 0 && g.seg[s].ldb % 4 == 0;
     }
     g.ksplit = p.ksplit;
-    if (p.ksplit > 1 && !g.part) return hipErrorInvalidValue;
+    g.atomic = p.atomic && has_atomic<Epi>::value;
+    if (p.ksplit > 1 && !g.atomic && !g.part) return hipErrorInvalidValue;
     // byte extent of each operand: A spans K columns of lda (A_KM = false) or M columns,
     // B spans N columns of ldb (B_KM = true) or K columns
     g.bufok = g.nseg == 1 || (g.seg[0].lda == g.seg[1].lda && g.seg[0].ldb == g.seg[1].ldb);
@@ -552,6 +656,14 @@ hipError_t launch(Args g, Epi epi, hipStream_t stream, const Plan& p) {
         const double eb = (double)g.seg[s].ldb * (B_KM ? g.N : g.seg[s].K) * 4.0;
         g.bufok = g.bufok && ea < 2147483648.0 && eb < 2147483648.0;
     }
+    return hipSuccess;
+}
+
+template <bool A_KM, bool B_KM, class Epi, bool DUAL = false>
+hipError_t launch(Args g, Epi epi, hipStream_t stream, const Plan& p) {
+    if (g.M <= 0 || g.N <= 0) return hipSuccess;
+    bool vec = true;
+    if (hipError_t e = prepare<A_KM, B_KM, Epi, DUAL>(g, vec, p)) return e;
     if (p.bnt == 128) {
         dim3 grid((g.M + BM - 1) / BM, (g.N + 127) / 128, p.ksplit);
         gemm_kernel<A_KM, B_KM, 128, Epi, DUAL><<<grid, NT, 0, stream>>>(g, vec, epi);
@@ -559,12 +671,48 @@ hipError_t launch(Args g, Epi epi, hipStream_t stream, const Plan& p) {
         dim3 grid((g.M + BM - 1) / BM, (g.N + 63) / 64, p.ksplit);
         gemm_kernel<A_KM, B_KM, 64, Epi, DUAL><<<grid, NT, 0, stream>>>(g, vec, epi);
     }
-    if (p.ksplit > 1) {
+    if (p.ksplit > 1 && !g.atomic) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const long mn = (long)g.M * g.N;
         splitk_reduce_kernel<Epi, DUAL><<<(unsigned)((mn + NT - 1) / NT), NT, 0, stream>>>(g.part, p.ksplit, g.M, g.N, epi);
     }
+    return hipGetLastError();
+}
+
+// Dynamic LDS that caps a kernel using `static_bytes` of LDS per block at `blocks` resident
+// blocks per CU (160 KiB of LDS per CU on gfx950); 0 when blocks <= 0.
+inline size_t lds_cap_bytes(size_t static_bytes, int blocks) {
+    constexpr size_t kLdsPerCu = 160 * 1024;
+    if (blocks <= 0) return 0;
+    size_t per = kLdsPerCu / (size_t)(blocks + 1) + 1;  // more than a (blocks + 1)-th of the CU's LDS
+    per = (per + 255) / 256 * 256;
+    return per > static_bytes ? per - static_bytes : 0;
+}
+
+// Two products as one launch (gemm_pair_kernel) when both plans use the narrow tile and
+// neither needs a second kernel; otherwise one launch each.  Both are enqueued on `stream`.
+// max_blocks > 0 caps the paired launch at that many resident blocks per CU (by LDS).
+template <bool A0, bool B0, class E0, bool A1, bool B1, class E1, bool DUAL = false, class X = NoExtra>
+hipError_t launch_pair(Args g0, E0 e0, const Plan& p0, Args g1, E1 e1, const Plan& p1, hipStream_t stream, X x = X{},
+                       int max_blocks = 0) {
+    const bool one0 = p0.ksplit == 1 || (p0.atomic && has_atomic<E0>::value);
+    const bool one1 = p1.ksplit == 1 || (p1.atomic && has_atomic<E1>::value);
+    if (g0.M <= 0 || g0.N <= 0 || g1.M <= 0 || g1.N <= 0 || p0.bnt != 64 || p1.bnt != 64 || !one0 || !one1) {
+        if (x.count > 0) {
+            extra_kernel<X><<<(unsigned)x.count, NT, 0, stream>>>(x);
+            if (hipError_t e = hipGetLastError()) return e;
+        }
+        if (hipError_t e = launch<A0, B0, E0, DUAL>(g0, e0, stream, p0)) return e;
+        return launch<A1, B1, E1, DUAL>(g1, e1, stream, p1);
+    }
+    Part<A0, B0, E0> q0{g0, true, e0, (g0.M + BM - 1) / BM, (g0.N + 63) / 64};
+    Part<A1, B1, E1> q1{g1, true, e1, (g1.M + BM - 1) / BM, (g1.N + 63) / 64};
+    if (hipError_t e = prepare<A0, B0, E0, DUAL>(q0.g, q0.vec, p0)) return e;
+    if (hipError_t e = prepare<A1, B1, E1, DUAL>(q1.g, q1.vec, p1)) return e;
+    const long nb = (long)x.count + (long)q0.gx * q0.gy * p0.ksplit + (long)q1.gx * q1.gy * p1.ksplit;
+    const size_t dyn = lds_cap_bytes(sizeof(float) * smem_floats<64, DUAL>(), max_blocks);
+    gemm_pair_kernel<64, DUAL, A0, B0, E0, A1, B1, E1, X><<<(unsigned)nb, NT, dyn, stream>>>(q0, q1, x);
     return hipGetLastError();
 }
 

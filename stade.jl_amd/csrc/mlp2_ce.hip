@@ -66,12 +66,19 @@ struct EpiAccPair {
         __builtin_nontemporal_store(c.x + p, &C[m + n * ld]);
         __builtin_nontemporal_store(c.y + q, &Cd[m + n * ld]);
     }
+    static constexpr bool kAtomic = true;
+    __device__ void atomic(int m, int n, float p, float q) const {
+        unsafeAtomicAdd(&C[m + n * ld], p);
+        unsafeAtomicAdd(&Cd[m + n * ld], q);
+    }
 };
 struct EpiAcc {  // C += v (a shadow accumulated, as the generated code does)
     float* C;
     long ld;
     __device__ float load(int m, int n) const { return __builtin_nontemporal_load(&C[m + n * ld]); }
     __device__ void operator()(int m, int n, float v, float c) const { __builtin_nontemporal_store(c + v, &C[m + n * ld]); }
+    static constexpr bool kAtomic = true;
+    __device__ void atomic(int m, int n, float v) const { unsafeAtomicAdd(&C[m + n * ld], v); }
 };
 
 // ---------------------------------------------------------------------------------------
@@ -795,28 +802,33 @@ struct FinalArgs {
     int H, O;
 };
 
+constexpr int kFinalNV = 2 + 2 * OMAX;  // loss, lossd, b2b[OMAX], b2bd[OMAX]
+
+// block `bid` of the final sums, with `red` a block-shared array of 16 + kFinalNV doubles
 template <int MODE>
-__global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
-    constexpr int NV = 2 + 2 * OMAX;  // loss, lossd, b2b[OMAX], b2bd[OMAX]
-    __shared__ double red[16 * NV];
+__device__ __forceinline__ void final_block(const FinalArgs& f, int bid, double* red) {
+    constexpr int NV = kFinalNV;
     const int O = f.O, H = f.H;
-    if (blockIdx.x == 0) {
-        // all the sums at once: per value a thread-strided sum in index order, then one block
-        // reduction of the NV values together
-        double v[NV];
-#pragma unroll
-        for (int k = 0; k < NV; ++k) v[k] = 0.0;
-        for (int b = threadIdx.x; b < f.nhead; b += NT) {
-            v[0] += f.hpart[(size_t)b * 2];
-            if (MODE != ADJ) v[1] += f.hpart[(size_t)b * 2 + 1];
-        }
-        if (MODE != TAN) {
-            for (int c = threadIdx.x; c < f.nchunks; c += NT) {
-#pragma unroll
-                for (int k = 0; k < 2 * OMAX; ++k) v[2 + k] += (double)f.c2part[(size_t)c * 2 * OMAX + k];
+    if (bid == 0) {
+        // one value at a time (few registers: this block may ride along in a launch of
+        // matrix-core tiles): a thread-strided sum in index order, then a block reduction.
+        // Values: 0 loss, 1 lossd, 2 + o b2b[o], 2 + OMAX + o b2bd[o]
+        double* tot = red + 16;  // red[0..15]: the block reduction's wave slots
+#pragma unroll 1
+        for (int k = 0; k < NV; ++k) {
+            const bool need = k == 0 || (k == 1 && MODE != ADJ) || (k >= 2 && k < 2 + OMAX && MODE != TAN && k - 2 < O) ||
+                              (k >= 2 + OMAX && MODE == HVP && k - 2 - OMAX < O);
+            if (!need) continue;
+            double v[1] = {0.0};
+            if (k < 2) {
+                for (int b = threadIdx.x; b < f.nhead; b += NT) v[0] += f.hpart[(size_t)b * 2 + k];
+            } else {
+                for (int c = threadIdx.x; c < f.nchunks; c += NT) v[0] += (double)f.c2part[(size_t)c * 2 * OMAX + (k - 2)];
             }
+            block_sum<1>(v, red);
+            if (threadIdx.x == 0) tot[k] = v[0];
         }
-        block_sum<NV>(v, red);
+        __syncthreads();
         // every output read before any is written: the stores may alias the later reads as far
         // as the compiler knows, and interleaving would cost a memory round trip per output
         if (threadIdx.x == 0) {
@@ -828,19 +840,19 @@ __global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
                 old[2 + o] = (MODE != TAN && o < O) ? f.b2b[o] : 0.f;
                 old[2 + OMAX + o] = (MODE == HVP && o < O) ? f.b2bd[o] : 0.f;
             }
-            f.loss[0] = old[0] + (float)v[0];
-            if (MODE != ADJ) f.lossd[0] = old[1] + (float)v[1];
+            f.loss[0] = old[0] + (float)tot[0];
+            if (MODE != ADJ) f.lossd[0] = old[1] + (float)tot[1];
 #pragma unroll
             for (int o = 0; o < OMAX; ++o) {
-                if (MODE != TAN && o < O) f.b2b[o] = old[2 + o] + (float)v[2 + o];
-                if (MODE == HVP && o < O) f.b2bd[o] = old[2 + OMAX + o] + (float)v[2 + OMAX + o];
+                if (MODE != TAN && o < O) f.b2b[o] = old[2 + o] + (float)tot[2 + o];
+                if (MODE == HVP && o < O) f.b2bd[o] = old[2 + OMAX + o] + (float)tot[2 + OMAX + o];
             }
         }
         return;
     }
     if (MODE == TAN) return;
     const int rows = (MODE == HVP ? 2 : 1) * (O + 1);
-    const long q = (long)(blockIdx.x - 1) * NT + threadIdx.x;
+    const long q = (long)(bid - 1) * NT + threadIdx.x;
     if (q >= (long)rows * H) return;
     const int r = (int)(q / H), j = (int)(q % H);
     // the destination: W2b / b1b (HVP: W2bd / b1bd), read before the partial loads go out
@@ -865,6 +877,30 @@ __global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
     }
     *dst = old + s;
 }
+
+template <int MODE>
+__global__ __launch_bounds__(NT) void final_kernel(FinalArgs f) {
+    __shared__ double red[16 + kFinalNV];
+    final_block<MODE>(f, blockIdx.x, red);
+}
+
+// resident blocks per CU of the adjoint's paired backward launch (its registers would allow
+// four; three measured faster)
+#ifndef STADE_MLP_BWD_BLOCKS
+#define STADE_MLP_BWD_BLOCKS 3
+#endif
+constexpr int kBwdBlocksPerCu = STADE_MLP_BWD_BLOCKS;
+
+// the final sums as extra blocks of the backward products' launch (they read only the head
+// and column-sum partials, so they run beside the product tiles)
+template <int MODE>
+struct FinalBlocks {
+    FinalArgs f;
+    int count;
+    __device__ __forceinline__ void operator()(int b, float* smem) const {
+        final_block<MODE>(f, b, reinterpret_cast<double*>(smem));
+    }
+};
 
 struct Ptrs {
     float *loss, *x, *w1, *b1, *w2, *b2, *h1, *z;       // primal (loss, h1, z written)
@@ -916,8 +952,9 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     // (the tangent and the HVP form s1 with s1d, the HVP W1b with W1bd and xb with xbd, as dual
     // products: one launch each, operand tiles shared)
     const Plan p_s1 = plan(H, B, I, cus), p_s1d = plan(H, B, I, cus, 2);
-    const Plan p_w1b = plan(H, I, B, cus), p_w1bd = plan(H, I, B, cus, 2);
-    const Plan p_xb = plan(I, B, H, cus), p_xbd = plan(I, B, H, cus, 2);
+    // (the backward products only accumulate into shadows: their K splits may add by atomics)
+    const Plan p_w1b = plan(H, I, B, cus, 1, true), p_w1bd = plan(H, I, B, cus, 2, true);
+    const Plan p_xb = plan(I, B, H, cus, 1, true), p_xbd = plan(I, B, H, cus, 2, true);
     size_t npart = 0;
     auto need = [&](const Plan& q, long M, long N) {
         if (q.ksplit > 1) npart = std::max(npart, (size_t)q.ksplit * M * N);
@@ -995,46 +1032,40 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     FinalArgs f{ws->partials, (int)hb, cpart, c2part, nchunks, p.loss, p.lossd, p.b2b, p.b2bd, p.w2b, p.w2bd, p.b1b, p.b1bd, H, O};
     const long rows = (long)(MODE == HVP ? 2 : 1) * (O + 1) * H;
     const unsigned fb = 1 + (MODE == TAN ? 0 : (unsigned)((rows + NT - 1) / NT));
-    STADE_TIMED("mlp_final", stream, final_kernel<MODE><<<fb, NT, 0, stream>>>(f));
-    STADE_LAUNCHED("mlp final_kernel");
-    if (MODE == TAN || H == 0 || I == 0) return STADE_HIP_OK;
-    // W1b += d1 x'   (M = H, N = I, K = B);  HVP with W1bd += d1 xd' + d1d x' as one dual product
-    {
-        Args g{};
-        g.part = kpart;
-        g.seg[0] = Seg{D1, p.x, H, I, B};  // A0 = d1, B0 = x'
-        g.M = H;
-        g.N = I;
-        hipError_t e;
-        if (MODE == ADJ) {
-            g.nseg = 1;
-            STADE_TIMED("mlp_gemm_w1b", stream, e = (launch<false, false>(g, EpiAcc{p.w1b, H}, stream, p_w1b)));
-        } else {
-            g.seg[1] = Seg{D1d, p.xd, H, I, B};  // A1 = d1d, B1 = xd'
-            g.nseg = 2;
-            STADE_TIMED("mlp_gemm_w1bd", stream,
-                        e = (launch<false, false, EpiAccPair, true>(g, EpiAccPair{p.w1b, p.w1bd, H}, stream, p_w1bd)));
-        }
-        if (e != hipSuccess) return check_hip(e, "mlp gemm w1b");
+    if (MODE == TAN || H == 0 || I == 0) {
+        STADE_TIMED("mlp_final", stream, final_kernel<MODE><<<fb, NT, 0, stream>>>(f));
+        STADE_LAUNCHED("mlp final_kernel");
+        return STADE_HIP_OK;
     }
-    // Xb += W1' d1   (M = I, N = B, K = H);  HVP with Xbd += W1' d1d + W1d' d1 as one dual product
+    const FinalBlocks<MODE> fin{f, (int)fb};
+    // W1b += d1 x'   (M = H, N = I, K = B) and Xb += W1' d1   (M = I, N = B, K = H): two products
+    // that both read d1, run as one launch whose blocks share the CUs; the HVP's dual forms
+    // add W1bd += d1 xd' + d1d x' and Xbd += W1' d1d + W1d' d1
     {
-        Args g{};
-        g.part = kpart;
-        g.seg[0] = Seg{p.w1, D1, H, H, H};  // A0 = W1', B0 = d1
-        g.M = I;
-        g.N = B;
+        Args gw{}, gx{};
+        gw.part = kpart;
+        gw.seg[0] = Seg{D1, p.x, H, I, B};  // A0 = d1, B0 = x'
+        gw.M = H;
+        gw.N = I;
+        gx.part = kpart;
+        gx.seg[0] = Seg{p.w1, D1, H, H, H};  // A0 = W1', B0 = d1
+        gx.M = I;
+        gx.N = B;
         hipError_t e;
         if (MODE == ADJ) {
-            g.nseg = 1;
-            STADE_TIMED("mlp_gemm_xb", stream, e = (launch<true, true>(g, EpiAcc{p.xb, I}, stream, p_xb)));
+            gw.nseg = gx.nseg = 1;
+            STADE_TIMED("mlp_gemm_bwd", stream,
+                        e = (launch_pair<false, false, EpiAcc, true, true, EpiAcc>(gw, EpiAcc{p.w1b, H}, p_w1b, gx, EpiAcc{p.xb, I},
+                                                                                   p_xb, stream, fin, kBwdBlocksPerCu)));
         } else {
-            g.seg[1] = Seg{p.w1d, D1d, H, H, H};  // A1 = W1d', B1 = d1d
-            g.nseg = 2;
-            STADE_TIMED("mlp_gemm_xbd", stream,
-                        e = (launch<true, true, EpiAccPair, true>(g, EpiAccPair{p.xb, p.xbd, I}, stream, p_xbd)));
+            gw.seg[1] = Seg{D1d, p.xd, H, I, B};     // A1 = d1d, B1 = xd'
+            gx.seg[1] = Seg{p.w1d, D1d, H, H, H};    // A1 = W1d', B1 = d1d
+            gw.nseg = gx.nseg = 2;
+            STADE_TIMED("mlp_gemm_bwd2", stream,
+                        e = (launch_pair<false, false, EpiAccPair, true, true, EpiAccPair, true>(
+                            gw, EpiAccPair{p.w1b, p.w1bd, H}, p_w1bd, gx, EpiAccPair{p.xb, p.xbd, I}, p_xbd, stream, fin)));
         }
-        if (e != hipSuccess) return check_hip(e, "mlp gemm xb");
+        if (e != hipSuccess) return check_hip(e, "mlp gemm w1b + xb");
     }
     return STADE_HIP_OK;
 }
