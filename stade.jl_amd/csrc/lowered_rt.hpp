@@ -1,0 +1,121 @@
+// Device runtime of the kernels that the general lowering (stade_hip.lower) writes for
+// generated STADE text: Julia's arithmetic semantics and the accumulation primitives.
+//
+// Julia semantics kept (1-based indexing is applied by the generated code itself):
+//   mod floored (sign of the divisor), div truncated, `x^2` = x*x (Base.literal_pow),
+//   max / min on floats propagate NaN and order -0.0 < 0.0, sign(0) = 0.
+// Accumulation into a shadow array at an index that other threads may share:
+//   wave_add: if the whole wave is active and every lane adds into the same element, the
+//   wave's values are summed across lanes and one lane makes the atomic addition (the
+//   wave-aggregated atomic); otherwise each lane adds atomically.  Floating-point atomics
+//   use the hardware instructions (unsafeAtomicAdd): the order of the additions is left to
+//   the hardware, as the generated adjoint's `@atomic` leaves it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+namespace stade_lowered {
+
+__device__ __forceinline__ int64_t jl_mod(int64_t a, int64_t b) {
+    int64_t r = a % b;
+    return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r;
+}
+__device__ __forceinline__ double jl_mod(double a, double b) {
+    double r = fmod(a, b);
+    return (r != 0.0 && ((r < 0.0) != (b < 0.0))) ? r + b : r;
+}
+__device__ __forceinline__ float jl_mod(float a, float b) {
+    float r = fmodf(a, b);
+    return (r != 0.0f && ((r < 0.0f) != (b < 0.0f))) ? r + b : r;
+}
+__device__ __forceinline__ int64_t jl_fld(int64_t a, int64_t b) {
+    int64_t q = a / b;
+    return (q * b != a && ((a < 0) != (b < 0))) ? q - 1 : q;
+}
+__device__ __forceinline__ int64_t jl_cld(int64_t a, int64_t b) {
+    int64_t q = a / b;
+    return (q * b != a && ((a < 0) == (b < 0))) ? q + 1 : q;
+}
+// number of values of lo:step:hi
+__device__ __host__ __forceinline__ int64_t jl_trip(int64_t lo, int64_t step, int64_t hi) {
+    int64_t t = (hi - lo + step) / step;
+    return t > 0 ? t : 0;
+}
+
+template <class T>
+__device__ __forceinline__ T jl_maxf(T a, T b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == b) return signbit(a) ? b : a;  // max(-0.0, 0.0) = 0.0
+    return a > b ? a : b;
+}
+template <class T>
+__device__ __forceinline__ T jl_minf(T a, T b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == b) return signbit(a) ? a : b;
+    return a < b ? a : b;
+}
+__device__ __forceinline__ int64_t jl_max(int64_t a, int64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ int64_t jl_min(int64_t a, int64_t b) { return a < b ? a : b; }
+__device__ __forceinline__ double jl_max(double a, double b) { return jl_maxf(a, b); }
+__device__ __forceinline__ double jl_min(double a, double b) { return jl_minf(a, b); }
+__device__ __forceinline__ float jl_max(float a, float b) { return jl_maxf(a, b); }
+__device__ __forceinline__ float jl_min(float a, float b) { return jl_minf(a, b); }
+
+template <class T>
+__device__ __forceinline__ T jl_sign(T x) {
+    return x > T(0) ? T(1) : (x < T(0) ? T(-1) : x);
+}
+__device__ __forceinline__ int64_t jl_ipow(int64_t b, int64_t e) {
+    int64_t r = 1;
+    while (e > 0) {
+        if (e & 1) r *= b;
+        b *= b;
+        e >>= 1;
+    }
+    return r;
+}
+
+// ---- wave reductions (full wave, 64 lanes) ------------------------------------------------
+template <class T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ void atomic_add(double* p, double v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add(int64_t* p, int64_t v) {
+    atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
+}
+
+template <class T>
+__device__ __forceinline__ void wave_add(T* p, T v) {
+    const uint64_t active = __ballot(1);
+    if (active == ~0ull) {
+        const uint64_t u = reinterpret_cast<uint64_t>(p);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u), hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+        T* p0 = reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+        if (__ballot(p == p0) == ~0ull) {
+            v = wave_sum(v);
+            if ((threadIdx.x & 63) == 0) atomic_add(p0, v);
+            return;
+        }
+    }
+    atomic_add(p, v);
+}
+
+// LDS-privatised accumulation: the block's copy, then one global atomic per nonzero element
+template <class T>
+__device__ __forceinline__ void lds_add(T* p, T v) {
+    atomicAdd(p, v);
+}
+__device__ __forceinline__ void lds_add(int64_t* p, int64_t v) {
+    atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
+}
+
+}  // namespace stade_lowered

@@ -1,0 +1,1154 @@
+"""Code generation of the general lowering: one HIP source per generated file, one C entry
+point per generated function.
+
+Execution model (designed for one MI355X, not a translation of the reference's per-loop
+AMDGPU.jl kernels, `cgen_kernel_def` /root/reference/src/STADE.jl:11106-11126):
+
+* The function's scalars (arguments and locals) live in a per-function frame in device
+  memory, so the host never waits for a device value: scalar statements run in small
+  single-thread kernels, stream-ordered with the loops around them.
+* A loop that `analysis.classify` accepts runs one iteration per thread (a grid-stride loop
+  over the trip count, bounds read on the device).  Its index conditions (a nonzero stride,
+  non-negative `div`/`mod` operands) are checked by the kernel; if one fails, the kernel runs
+  the loop in order on one thread instead.  Iteration-private scalars are registers; sums
+  into scalars are per-thread partials, summed across the wave and added once per wave;
+  owned array elements are plain loads and stores; accumulations at shared indices are
+  wave-aggregated atomics, or, for a small target with many contributions, atomics into a
+  block-private LDS copy flushed once per block.
+* A loop that cannot run that way but contains such loops, and whose bounds the host can
+  evaluate (Int arguments, sizes, enclosing host loops), stays on the host (the time loop of
+  an explicit scheme, as `cgen_body` keeps it, 10613-10615); one without parallel loops inside
+  runs on one thread.
+* An `if` around loops is evaluated on the device into a frame flag; the kernels of its
+  branches test the flags (no host round trip).
+* Returned scalars are copied back at the end: the only synchronisation of a call.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+from .analysis import ArrayUse, ParallelLoop, Types, classify, infer_types, _reads_of, _thaw
+from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, If, LowerError, Nothing_, Num, Range,
+                     Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
+
+MAX_BLOCKS = 8192          # grid of a parallel loop whose trip count the host cannot evaluate
+PRIV_MAX_BYTES = 48 * 1024  # LDS-privatised accumulation target, at most
+PRIV_RATIO = 32            # and at least this many iterations per target element
+
+
+def cname(n: str) -> str:
+    return n.replace("!", "_bang_")
+
+
+# ------------------------------------------------------------------------------------------
+# plan
+# ------------------------------------------------------------------------------------------
+
+@dataclass
+class SerialOp:
+    stmts: list
+    pred: tuple
+    kid: int = 0
+
+
+@dataclass
+class ParOp:
+    pl: ParallelLoop
+    pred: tuple
+    kid: int = 0
+
+
+@dataclass
+class HostLoopOp:
+    loop: For
+    ops: list
+    slot: int = 0
+
+
+@dataclass
+class IfOp:
+    node: If
+    flags: list                # flag slot of each branch (and of else when present)
+    branches: list             # ops per branch (else last)
+    pred: tuple
+    kid: int = 0
+
+
+@dataclass
+class AllocOp:
+    name: str
+    alloc: Alloc
+
+
+@dataclass
+class ReturnOp:
+    value: object
+    pred: tuple
+    kid: int = 0
+
+
+class FuncLower:
+    def __init__(self, f: Func, precision: str, arg_types: dict | None = None):
+        self.f = f
+        self.precision = precision
+        self.T: Types = infer_types(f, arg_types, precision)
+        self.fty = "float" if precision == "f32" else "double"
+        self.arrays = self.T.arrays
+        self.scalars = {n: t for n, t in self.T.scalars.items() if n not in self.arrays}
+        self.loopvars = {s.var for s in walk_stmts(f.body) if isinstance(s, For)}
+        self.nflags = 0
+        self.nhl = 0
+        self.kernels: list[str] = []
+        self.reasons: list[str] = []
+        self.refuse_reasons()
+        self.ops = self.plan()
+
+    # -- refusals ---------------------------------------------------------------------------
+    def refuse_reasons(self):
+        for s in walk_stmts(self.f.body):
+            for e in stmt_exprs(s):
+                for x in walk_expr(e):
+                    if isinstance(x, Call) and x.fn in ("push!", "pop!"):
+                        raise LowerError(f"{self.f.name}: push!/pop! stacks are not lowered (generate with indexed stacks)")
+                    if isinstance(x, Ref) and x.name not in self.arrays:
+                        raise LowerError(f"{self.f.name}: {x.name} is indexed but not an array")
+            if isinstance(s, ExprStmt):
+                raise LowerError(f"{self.f.name}: a bare expression statement")
+            if isinstance(s, Assign) and isinstance(s.lhs, Var) and s.lhs.name in self.arrays and not isinstance(s.rhs, Alloc):
+                raise LowerError(f"{self.f.name}: array {s.lhs.name} rebound by assignment")
+
+    # -- host-evaluable expressions ----------------------------------------------------------
+    def host_ok(self, e, hl: set) -> bool:
+        assigned = {s.lhs.name for s in walk_stmts(self.f.body) if isinstance(s, Assign) and isinstance(s.lhs, Var)}
+        for x in walk_expr(e):
+            if isinstance(x, Var):
+                if x.name in hl:
+                    continue
+                if x.name in self.arrays:
+                    continue
+                if x.name not in self.f.args or x.name in assigned or self.scalars.get(x.name) != "i":
+                    return False
+            elif isinstance(x, Ref):
+                return False
+            elif isinstance(x, Call) and x.fn not in ("div", "mod", "max", "min", "abs", "length", "size"):
+                return False
+            elif isinstance(x, Num) and not x.is_int:
+                return False
+            elif isinstance(x, Bin) and x.op not in ("+", "-", "*"):
+                return False
+        return True
+
+    # -- planning ----------------------------------------------------------------------------
+    def plan(self):
+        body = self.f.body
+        rets = [s for s in walk_stmts(body) if isinstance(s, Return)]
+        tail_return = bool(body) and isinstance(body[-1], Return)
+        if any(r is not body[-1] for r in rets) or any(isinstance(s, (Break, Continue)) for s in body):
+            # a return before the end (or control flow at the top level): the whole function in
+            # order on one thread
+            return [SerialOp(list(body), ())]
+        stmts = body[:-1] if tail_return else body
+        ops = self.lower_block(stmts, (), set(), top=True)
+        if tail_return and body[-1].value is not None and not isinstance(body[-1].value, Nothing_):
+            ops.append(ReturnOp(body[-1].value, ()))
+        return ops
+
+    def _later_reads(self) -> set:
+        out = set()
+        for s in walk_stmts(self.f.body):
+            for e in stmt_exprs(s):
+                out |= _reads_of(e)
+        return out
+
+    def contains_parallel(self, body, hl) -> bool:
+        for s in walk_stmts(body):
+            if isinstance(s, For):
+                pl, _ = classify(s, self.T, self._reads_outside(s), set())
+                if pl is not None:
+                    return True
+        return False
+
+    def _parents(self):
+        if not hasattr(self, "_par"):
+            par = {}
+
+            def visit(block, enclosing):
+                for k, s in enumerate(block):
+                    par[id(s)] = (block, k, enclosing)
+                    for b in sub_blocks(s):
+                        visit(b, s)
+            visit(self.f.body, None)
+            self._par = par
+        return self._par
+
+    def _reads_outside(self, loop: For) -> set:
+        """The scalars the loop assigns that are live after it: read on some path from the
+        loop's exit before being assigned again (the statements after it, then after each
+        enclosing statement, and one more pass over every enclosing loop's body)."""
+        from .analysis import _assigned, _upward_exposed
+        par = self._parents()
+        cont = []
+        node = loop
+        while node is not None:
+            block, k, enclosing = par[id(node)]
+            cont += block[k + 1:]
+            if isinstance(enclosing, (For, While)):
+                cont += enclosing.body
+            node = enclosing
+        out = set()
+        for name in _assigned(loop.body):
+            if _upward_exposed(cont, name):
+                out.add(name)
+        return out
+
+    def lower_block(self, stmts, pred, hl: set, top=False):
+        ops = []
+        cur = []
+
+        def flush():
+            if cur:
+                ops.append(SerialOp(list(cur), pred))
+                cur.clear()
+        for s in stmts:
+            if isinstance(s, Assign) and isinstance(s.rhs, Alloc):
+                if not (top and isinstance(s.lhs, Var) and self.host_ok(s.rhs.n, hl)):
+                    raise LowerError(f"{self.f.name}: allocation of {s.lhs} needs a size the host can evaluate, "
+                                     f"at the top level of the function")
+                flush()
+                ops.append(AllocOp(s.lhs.name, s.rhs))
+                continue
+            if isinstance(s, For):
+                pl, why = classify(s, self.T, self._reads_outside(s), set())
+                if pl is not None:
+                    flush()
+                    ops.append(ParOp(pl, pred))
+                    continue
+                self.reasons.append(f"loop over {s.var}: {why}")
+                if self.contains_parallel(s.body, hl) and self.host_ok(s.rng, hl) and not any(
+                        isinstance(t, (Break, Continue, Return)) for t in walk_stmts(s.body)):
+                    flush()
+                    slot = self.nhl
+                    self.nhl += 1
+                    inner = self.lower_block(s.body, pred, hl | {s.var})
+                    ops.append(HostLoopOp(s, inner, slot))
+                    continue
+                cur.append(s)
+                continue
+            if isinstance(s, If) and self.contains_parallel([s], hl) and not any(
+                    isinstance(t, (Break, Continue, Return)) for t in walk_stmts([s])):
+                flush()
+                nb = len(s.branches) + (1 if s.orelse is not None else 0)
+                flags = list(range(self.nflags, self.nflags + nb))
+                self.nflags += nb
+                branches = []
+                for k, (_, b) in enumerate(s.branches):
+                    branches.append(self.lower_block(b, pred + (flags[k],), hl))
+                if s.orelse is not None:
+                    branches.append(self.lower_block(s.orelse, pred + (flags[-1],), hl))
+                ops.append(IfOp(s, flags, branches, pred))
+                continue
+            cur.append(s)
+        flush()
+        return ops
+
+    # -- names ---------------------------------------------------------------------------------
+    def cty(self, t: str) -> str:
+        return {"i": "int64_t", "b": "bool", "f": self.fty}[t]
+
+    def frame_scalars(self):
+        # every scalar (a name may be a loop variable in one place and a plain variable in
+        # another; unused slots cost nothing)
+        return sorted(self.scalars)
+
+    # -- expressions -----------------------------------------------------------------------------
+    def ex(self, e, ctx) -> tuple[str, str]:
+        """C code and type ('i', 'b', 'f' precision float, 'd' double) of an expression."""
+        if isinstance(e, Num):
+            if e.text in ("true", "false"):
+                return e.text, "b"
+            if e.is_int:
+                return f"((int64_t){int(e.text, 0)}LL)", "i"
+            if e.f32:
+                return f"({e.text}f)", "f" if self.fty == "float" else "F"
+            txt = e.text if ("." in e.text or "e" in e.text or "E" in e.text) else e.text + ".0"
+            if self.fty == "float":
+                return f"((float){txt})", "f"
+            return f"({txt})", "f"
+        if isinstance(e, Var):
+            return ctx.var(e.name), ctx.vtype(e.name)
+        if isinstance(e, Ref):
+            return ctx.ref(e), ("i" if self.arrays[e.name] == "i" else "f")
+        if isinstance(e, Un):
+            a, t = self.ex(e.a, ctx)
+            if e.op == "!":
+                return f"(!{a})", "b"
+            return f"(-{a})", t
+        if isinstance(e, Bin):
+            return self.binop(e, ctx)
+        if isinstance(e, Call):
+            return self.call(e, ctx)
+        raise LowerError(f"{self.f.name}: cannot lower expression {e!r}")
+
+    def binop(self, e, ctx):
+        op = e.op
+        if op == "^":
+            return self.power(e, ctx)
+        a, ta = self.ex(e.a, ctx)
+        b, tb = self.ex(e.b, ctx)
+        if op in ("&&", "||"):
+            return f"({a} {op} {b})", "b"
+        if op in ("==", "!=", "<", ">", "<=", ">="):
+            return f"({a} {op} {b})", "b"
+        if op == "/":
+            if ta == "i" and tb == "i":
+                return f"((double){a} / (double){b})", "d"
+            return f"({a} / {b})", self._join(ta, tb)
+        return f"({a} {op} {b})", self._join(ta, tb)
+
+    def _join(self, ta, tb):
+        if "d" in (ta, tb):
+            return "d"
+        if "f" in (ta, tb) or "F" in (ta, tb):
+            return "f" if self.fty == "float" or "f" in (ta, tb) and self.fty == "double" else "f"
+        if "b" in (ta, tb):
+            return "i"
+        return "i"
+
+    def power(self, e, ctx):
+        base, tb = self.ex(e.a, ctx)
+        pe = e.b
+        if isinstance(pe, Num) and pe.is_int:
+            p = int(pe.text, 0)
+            if tb == "i":
+                return f"stade_lowered::jl_ipow({base}, {p})", "i"
+            ct = "double" if tb == "d" else self.fty
+            if p == 2:
+                return f"([&]() {{ const {ct} _b = {base}; return _b * _b; }}())", tb
+            if p == 3:
+                return f"([&]() {{ const {ct} _b = {base}; return _b * _b * _b; }}())", tb
+            if p == 1:
+                return base, tb
+            if p == 0:
+                return f"(({ct})1)", tb
+            if p == -1:
+                return f"(({ct})1 / {base})", tb
+            if p == -2:
+                return f"([&]() {{ const {ct} _b = ({ct})1 / {base}; return _b * _b; }}())", tb
+            return f"pow({base}, ({ct}){p})", tb
+        x, tx = self.ex(pe, ctx)
+        if tb == "i" and tx == "i":
+            return f"stade_lowered::jl_ipow({base}, {x})", "i"
+        return f"pow({base}, {x})", self._join(tb, tx) if tb != "i" else (tx if tx != "i" else "d")
+
+    def call(self, e, ctx):
+        fn, args = e.fn, e.args
+        if fn == "length":
+            return ctx.length(args[0].name), "i"
+        if fn == "size":
+            d = int(args[1].text) if len(args) > 1 else 1
+            return ctx.dim(args[0].name, d - 1), "i"
+        xs = [self.ex(a, ctx) for a in args]
+        codes = [c for c, _ in xs]
+        tys = [t for _, t in xs]
+        if fn in ("div", "mod", "rem", "fld", "cld"):
+            a, b = codes
+            if all(t == "i" for t in tys):
+                return {"div": f"({a} / {b})", "rem": f"({a} % {b})", "mod": f"stade_lowered::jl_mod({a}, {b})",
+                        "fld": f"stade_lowered::jl_fld({a}, {b})", "cld": f"stade_lowered::jl_cld({a}, {b})"}[fn], "i"
+            t = self._join(*tys)
+            ct = "double" if t == "d" else self.fty
+            a, b = f"({ct}){a}", f"({ct}){b}"
+            if fn == "mod":
+                return f"stade_lowered::jl_mod({a}, {b})", t
+            if fn == "rem":
+                return f"fmod({a}, {b})", t
+            if fn == "div":
+                return f"trunc({a} / {b})", t
+            if fn == "fld":
+                return f"floor({a} / {b})", t
+            return f"ceil({a} / {b})", t
+        if fn in ("max", "min"):
+            t = "i" if all(t == "i" for t in tys) else self._join(*tys)
+            ct = {"i": "int64_t", "d": "double"}.get(t, self.fty)
+            out = f"(({ct}){codes[0]})"
+            for c in codes[1:]:
+                out = f"stade_lowered::jl_{fn}({out}, ({ct}){c})"
+            return out, t
+        if fn == "abs":
+            return (f"llabs({codes[0]})", "i") if tys[0] == "i" else (f"fabs({codes[0]})", tys[0])
+        if fn == "sign":
+            return f"stade_lowered::jl_sign({codes[0]})", tys[0]
+        if fn == "ifelse":
+            t = self._join(tys[1], tys[2]) if "i" not in (tys[1], tys[2]) or tys[1] != tys[2] else tys[1]
+            return f"(({codes[0]}) ? ({codes[1]}) : ({codes[2]}))", t
+        if fn in ("Float64", "float"):
+            return f"((double){codes[0]})", "d"
+        if fn == "Float32":
+            return f"((float){codes[0]})", "f" if self.fty == "float" else "F"
+        if fn in ("Int", "Int64"):
+            return f"((int64_t){codes[0]})", "i"
+        if fn in ("floor", "ceil", "round", "trunc"):
+            cfn = {"floor": "floor", "ceil": "ceil", "round": "rint", "trunc": "trunc"}[fn]
+            if len(args) == 2:   # floor(Int, x)
+                return f"((int64_t){cfn}({codes[1]}))", "i"
+            return f"{cfn}({codes[0]})", tys[0]
+        if fn == "inv":
+            return f"(1 / {codes[0]})", tys[0]
+        if fn in ("exp", "log", "tanh", "sin", "cos", "tan", "sqrt", "sinh", "cosh", "atan", "asin", "acos", "log10",
+                  "log2", "exp2", "expm1", "log1p", "cbrt"):
+            t = tys[0] if tys[0] != "i" else "d"
+            a = codes[0] if tys[0] != "i" else f"(double){codes[0]}"
+            return f"{fn}({a})", t
+        raise LowerError(f"{self.f.name}: call to unsupported function {fn}")
+
+
+# ------------------------------------------------------------------------------------------
+# emission contexts
+# ------------------------------------------------------------------------------------------
+
+class Ctx:
+    """How names read and write inside one kernel (or the host)."""
+
+    def __init__(self, fl: FuncLower, locals_: dict, hl_names: dict, acc: dict | None = None, serial_acc=True,
+                 reductions: dict | None = None, lds: str | None = None):
+        self.fl = fl
+        self.locals = locals_          # scalar -> C local name
+        self.hl = hl_names             # host loop var -> slot
+        self.acc = acc or {}           # array -> 'atomic' (accumulations through wave_add / lds)
+        self.serial_acc = serial_acc   # accumulations as plain read-modify-writes
+        self.reductions = reductions or {}
+        self.lds = lds                 # array privatised in LDS (its accumulations go to lds_priv)
+
+    def var(self, n):
+        if n in self.locals:
+            return self.locals[n]
+        if n in self.hl:
+            return f"a.hl[{self.hl[n]}]"
+        if n in self.fl.arrays:
+            raise LowerError(f"{self.fl.f.name}: array {n} used as a value")
+        return f"fr.v_{cname(n)}"
+
+    def vtype(self, n):
+        t = self.fl.scalars.get(n, "f")
+        return t
+
+    def dim(self, name, d):
+        return f"a.D_{cname(name)}[{d}]"
+
+    def length(self, name):
+        nd = self.fl.T.ndim.get(name, 1)
+        return "(" + " * ".join(f"a.D_{cname(name)}[{d}]" for d in range(nd)) + ")"
+
+    def lin(self, ref: Ref) -> str:
+        parts = []
+        stride = None
+        for d, i in enumerate(ref.idx):
+            c, t = self.fl.ex(i, self)
+            if t != "i":
+                c = f"(int64_t)({c})"
+            term = f"(({c}) - 1)"
+            parts.append(term if stride is None else f"{term} * {stride}")
+            s = f"a.D_{cname(ref.name)}[{d}]"
+            stride = s if stride is None else f"{stride} * {s}"
+        return " + ".join(parts)
+
+    def ref(self, ref: Ref) -> str:
+        # bounds-checked: an index outside the array raises the frame's flag (the call then
+        # reports Julia's BoundsError) and reads 0 instead of touching memory
+        return f"rd(a.A_{cname(ref.name)}, {self.lin(ref)}, a.N_{cname(ref.name)})"
+
+
+class Emitter:
+    def __init__(self, fl: FuncLower, ctx: Ctx):
+        self.fl, self.ctx = fl, ctx
+        # labels unique across the emitters of one function, numbered in emission order so the
+        # generated source (whose hash names the built library) is the same in every process
+        fl.n_emitters = getattr(fl, "n_emitters", 0) + 1
+        self.u = fl.n_emitters
+        self.lines: list[str] = []
+        self.ind = 1
+        self.loop_labels = []
+        self.nlabel = 0
+
+    def emit(self, s):
+        self.lines.append("    " * self.ind + s)
+
+    def block(self, stmts):
+        for s in stmts:
+            self.stmt(s)
+
+    def stmt(self, s):
+        fl, ctx = self.fl, self.ctx
+        if isinstance(s, Assign):
+            if isinstance(s.lhs, Var):
+                n = s.lhs.name
+                if n in ctx.reductions and isinstance(s.rhs, Bin):
+                    r = s.rhs
+                    if isinstance(r.a, Var) and r.a.name == n:
+                        c, _ = fl.ex(r.b, ctx)
+                        self.emit(f"{ctx.reductions[n]} {'+' if r.op == '+' else '-'}= {c};")
+                    else:
+                        c, _ = fl.ex(r.a, ctx)
+                        self.emit(f"{ctx.reductions[n]} += {c};")
+                    return
+                c, _ = fl.ex(s.rhs, ctx)
+                self.emit(f"{ctx.var(n)} = ({fl.cty(fl.scalars.get(n, 'f'))})({c});")
+                return
+            ref = s.lhs
+            et = "int64_t" if fl.arrays[ref.name] == "i" else fl.fty
+            if ref.name in ctx.acc and not ctx.serial_acc:
+                r = s.rhs
+                other, sign = (r.b, "+") if r.a == ref else (r.a, "+")
+                if r.op == "-":
+                    sign = "-"
+                c, _ = fl.ex(other, ctx)
+                val = f"({et})({c})" if sign == "+" else f"(-({et})({c}))"
+                nm = cname(ref.name)
+                self.emit(f"{{ const int64_t _i = {ctx.lin(ref)};")
+                if ctx.lds == ref.name:
+                    self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::lds_add(&lds_priv[_i], {val}); else oob(); }}")
+                else:
+                    self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::wave_add(&a.A_{nm}[_i], {val}); else oob(); }}")
+                return
+            c, _ = fl.ex(s.rhs, ctx)
+            self.emit(f"wr(a.A_{cname(ref.name)}, {ctx.lin(ref)}, a.N_{cname(ref.name)}, ({et})({c}));")
+            return
+        if isinstance(s, For):
+            lo, _ = fl.ex(s.rng.lo, ctx)
+            hi, _ = fl.ex(s.rng.hi, ctx)
+            st = "1" if s.rng.step is None else fl.ex(s.rng.step, ctx)[0]
+            v = f"l_{cname(s.var)}"
+            saved = ctx.locals.get(s.var)
+            k = self.nlabel
+            self.nlabel += 1
+            self.emit("{")
+            self.ind += 1
+            self.emit(f"const int64_t _lo{k} = {lo}, _st{k} = {st}, _n{k} = stade_lowered::jl_trip(_lo{k}, _st{k}, {hi});")
+            self.emit(f"for (int64_t _k{k} = 0; _k{k} < _n{k}; ++_k{k}) {{")
+            self.ind += 1
+            self.emit(f"const int64_t {v} = _lo{k} + _k{k} * _st{k};")
+            ctx.locals[s.var] = v
+            self.loop_labels.append(k)
+            self.block(s.body)
+            self.loop_labels.pop()
+            self.emit(f"_cont{self.u}_{k}:;")
+            self.ind -= 1
+            self.emit("}")
+            self.emit(f"_brk{self.u}_{k}:;")
+            self.ind -= 1
+            self.emit("}")
+            if saved is None:
+                ctx.locals.pop(s.var, None)
+            else:
+                ctx.locals[s.var] = saved
+            return
+        if isinstance(s, While):
+            k = self.nlabel
+            self.nlabel += 1
+            c, _ = fl.ex(s.cond, ctx)
+            self.emit(f"while ({c}) {{")
+            self.ind += 1
+            self.loop_labels.append(k)
+            self.block(s.body)
+            self.loop_labels.pop()
+            self.emit(f"_cont{self.u}_{k}:;")
+            self.ind -= 1
+            self.emit("}")
+            self.emit(f"_brk{self.u}_{k}:;")
+            return
+        if isinstance(s, If):
+            for j, (cond, body) in enumerate(s.branches):
+                c, _ = fl.ex(cond, ctx)
+                self.emit(("if" if j == 0 else "} else if") + f" ({c}) {{")
+                self.ind += 1
+                self.block(body)
+                self.ind -= 1
+            if s.orelse is not None:
+                self.emit("} else {")
+                self.ind += 1
+                self.block(s.orelse)
+                self.ind -= 1
+            self.emit("}")
+            return
+        if isinstance(s, Break):
+            self.emit(f"goto _brk{self.u}_{self.loop_labels[-1]};")
+            return
+        if isinstance(s, Continue):
+            if self.loop_labels:
+                self.emit(f"goto _cont{self.u}_{self.loop_labels[-1]};")
+            else:
+                self.emit(f"goto _next_iter{self.u};")
+            return
+        if isinstance(s, Return):
+            self.ret(s.value)
+            self.emit("goto _fn_end;")
+            return
+        raise LowerError(f"{fl.f.name}: cannot lower statement {s!r}")
+
+    def ret(self, value):
+        fl = self.fl
+        if value is None or isinstance(value, Nothing_):
+            return
+        items = value.items if isinstance(value, Tup) else (value,)
+        for k, it in enumerate(items):
+            c, t = fl.ex(it, self.ctx)
+            if t == "i":
+                self.emit(f"fr.ri[{k}] = {c}; fr.rk[{k}] = 1;")
+            else:
+                self.emit(f"fr.r[{k}] = (double)({c}); fr.rk[{k}] = 0;")
+        self.emit(f"fr.nret = {len(items)};")
+
+
+# ------------------------------------------------------------------------------------------
+# kernels and the entry point of one function
+# ------------------------------------------------------------------------------------------
+
+def _stmt_scalars(fl: FuncLower, stmts) -> tuple[set, set]:
+    """(scalars read, scalars assigned) by statements, excluding their own loop variables."""
+    reads, writes, inner = set(), set(), set()
+    for s in walk_stmts(stmts):
+        for e in stmt_exprs(s):
+            reads |= {n for n in _reads_of(e) if n not in fl.arrays}
+        if isinstance(s, Assign) and isinstance(s.lhs, Var):
+            writes.add(s.lhs.name)
+        if isinstance(s, For):
+            inner.add(s.var)
+    return reads - inner, writes - inner
+
+
+class FuncGen:
+    """HIP source of one lowered function: namespace gen_<name> with its frame, kernels and
+    the extern "C" entry point stade_hip_gen_<name>."""
+
+    def __init__(self, fl: FuncLower):
+        self.fl = fl
+        self.ns = f"gen_{cname(fl.f.name)}"
+        self.kern: list[str] = []
+        self.host: list[str] = []
+        self.nk = 0
+        self.hind = 1
+        self.nalloc = 0
+        self.hlv: dict[str, int] = {}   # host loop variables in scope -> their slot in Args.hl
+
+    def pred_code(self, pred) -> str:
+        return " && ".join(f"fr.flag[{k}]" for k in pred) if pred else "true"
+
+    def hemit(self, line):
+        self.host.append("    " * self.hind + line)
+
+    def launch(self, kname, grid="1", block="1", shmem="0", tmpl=""):
+        self.hemit(f"{kname}{tmpl}<<<{grid}, {block}, {shmem}, stream>>>(a);")
+        self.hemit(f"if ((_e = hipGetLastError()) != hipSuccess) return _fail(_e, \"{kname}\");")
+
+    # -- serial kernels ---------------------------------------------------------------------
+    def serial(self, stmts, pred, ret_value=None) -> None:
+        fl = self.fl
+        k = self.nk
+        self.nk += 1
+        reads, writes = _stmt_scalars(fl, stmts)
+        if ret_value is not None:
+            reads |= {n for n in _reads_of(ret_value) if n not in fl.arrays}
+        hl = self.hlv
+        names = sorted(n for n in (reads | writes) if n not in hl and n in fl.scalars)
+        ctx = Ctx(fl, {n: f"x_{cname(n)}" for n in names}, hl, serial_acc=True)
+        em = Emitter(fl, ctx)
+        em.emit(f"if (!({self.pred_code(pred)})) return;")
+        for n in names:
+            em.emit(f"{fl.cty(fl.scalars[n])} x_{cname(n)} = fr.v_{cname(n)};")
+        em.block(stmts)
+        if ret_value is not None:
+            em.ret(ret_value)
+        em.emit("goto _fn_end;")
+        em.emit("_fn_end:;")
+        for n in sorted(writes):
+            if n in names:
+                em.emit(f"fr.v_{cname(n)} = x_{cname(n)};")
+        self.kern.append(f"__global__ __launch_bounds__(1) void k{k}(const Args a) {{\n" + "\n".join(em.lines) + "\n}\n")
+        self.launch(f"k{k}")
+
+    # -- parallel loops -----------------------------------------------------------------------
+    def parallel(self, op: ParOp) -> None:
+        fl, pl = self.fl, op.pl
+        loop = pl.loop
+        k = self.nk
+        self.nk += 1
+        hl = self.hlv
+        v = loop.var
+        inner = {s.var for s in walk_stmts(loop.body) if isinstance(s, For)}
+        priv = [n for n in pl.private if n not in hl]
+        reds = {n: f"r_{cname(n)}" for n in pl.reductions}
+        inv = sorted(n for n in pl.reads if n not in priv and n not in reds and n not in hl and n != v and n in fl.scalars)
+        atomic = [n for n, u in pl.arrays.items() if u.kind == "atomic"]
+        # LDS-privatised variants: PRIV = c + 1 takes candidate c's accumulations into a
+        # block-private copy (the host picks the first candidate small enough, with enough
+        # iterations per element); PRIV = 0 uses wave-aggregated global atomics only
+        cands = sorted(atomic)
+        locals_ = {n: f"x_{cname(n)}" for n in priv + inv}
+        locals_[v] = f"l_{cname(v)}"
+
+        def body_lines(parallel: bool, lds: str | None) -> list[str]:
+            ctx = Ctx(fl, dict(locals_), hl, acc={n: "atomic" for n in atomic}, serial_acc=not parallel,
+                      reductions=reds, lds=lds)
+            em = Emitter(fl, ctx)
+            em.ind = 3
+            em.emit(f"const int64_t l_{cname(v)} = _lo + _k * _st;")
+            for n in priv:
+                ct = fl.cty(fl.scalars[n])
+                if n in pl.reset:
+                    c, _ = fl.ex(pl.reset[n], ctx)
+                    em.emit(f"{ct} x_{cname(n)} = _k == 0 ? f0_{cname(n)} : ({ct})({c});")
+                else:
+                    em.emit(f"{ct} x_{cname(n)} = ({ct})0;")
+            em.block(loop.body)
+            em.emit(f"goto _next_iter{em.u};")
+            em.emit(f"_next_iter{em.u}:;")
+            if pl.live_out:
+                em.emit("if (_k == _trip - 1) {")
+                for n in pl.live_out:
+                    em.emit(f"    wb.v_{cname(n)} = x_{cname(n)};")
+                em.emit("}")
+            return em.lines
+
+        ctx0 = Ctx(fl, dict(locals_), hl)
+        lo, _ = fl.ex(loop.rng.lo, ctx0)
+        hi, _ = fl.ex(loop.rng.hi, ctx0)
+        st = "1" if loop.rng.step is None else fl.ex(loop.rng.step, ctx0)[0]
+        guards = self.guard_code(pl, ctx0)
+        head = [f"    if (!({self.pred_code(op.pred)})) return;"]
+        for n in inv:
+            head.append(f"    const {fl.cty(fl.scalars[n])} x_{cname(n)} = fr.v_{cname(n)};")
+        for n in priv:
+            if n in pl.reset:
+                head.append(f"    const {fl.cty(fl.scalars[n])} f0_{cname(n)} = fr.v_{cname(n)};")
+        head.append(f"    const int64_t _lo = {lo}, _st = {st}, _trip = stade_lowered::jl_trip(_lo, _st, {hi});")
+        red_decl = [f"    {fl.cty(fl.scalars[n])} {r} = 0;" for n, r in reds.items()]
+        out = list(head)
+        out.append(f"    if (!({guards})) {{")
+        out.append("        // an index condition of the one-thread-per-iteration form fails: the loop in order")
+        out.append("        if (blockIdx.x != 0 || threadIdx.x != 0) return;")
+        out += ["    " + x for x in red_decl]
+        out.append("        for (int64_t _k = 0; _k < _trip; ++_k) {")
+        out += body_lines(False, None)
+        out.append("        }")
+        for n, r in reds.items():
+            out.append(f"        fr.v_{cname(n)} += {r};")
+        out.append("        return;")
+        out.append("    }")
+        out += red_decl
+
+        def et_of(n):
+            return "int64_t" if fl.arrays[n] == "i" else fl.fty
+        for c, n in enumerate(cands):
+            n_len = Ctx(fl, {}, hl).length(n)
+            out.append(f"    if constexpr (PRIV == {c + 1}) {{")
+            out.append(f"        {et_of(n)}* lds_priv = reinterpret_cast<{et_of(n)}*>(lds_raw);")
+            out.append(f"        for (int64_t _j = threadIdx.x; _j < {n_len}; _j += blockDim.x) lds_priv[_j] = ({et_of(n)})0;")
+            out.append("        __syncthreads();")
+            out.append("    }")
+        out.append("    for (int64_t _k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; _k < _trip; _k += (int64_t)gridDim.x * blockDim.x) {")
+        if cands:
+            out.append("        if constexpr (PRIV == 0) {")
+            out += ["    " + x for x in body_lines(True, None)]
+            for c, n in enumerate(cands):
+                out.append(f"        }} else if constexpr (PRIV == {c + 1}) {{")
+                out.append(f"            {et_of(n)}* lds_priv = reinterpret_cast<{et_of(n)}*>(lds_raw);")
+                out += ["    " + x for x in body_lines(True, n)]
+            out.append("        }")
+        else:
+            out += body_lines(True, None)
+        out.append("    }")
+        for c, n in enumerate(cands):
+            n_len = Ctx(fl, {}, hl).length(n)
+            out.append(f"    if constexpr (PRIV == {c + 1}) {{")
+            out.append(f"        {et_of(n)}* lds_priv = reinterpret_cast<{et_of(n)}*>(lds_raw);")
+            out.append("        __syncthreads();")
+            out.append(f"        for (int64_t _j = threadIdx.x; _j < {n_len}; _j += blockDim.x)")
+            out.append(f"            if (lds_priv[_j] != ({et_of(n)})0) stade_lowered::atomic_add(&a.A_{cname(n)}[_j], lds_priv[_j]);")
+            out.append("    }")
+        for n, r in reds.items():
+            out.append(f"    {r} = stade_lowered::wave_sum({r});")
+            out.append(f"    if ((threadIdx.x & 63) == 0 && {r} != 0) stade_lowered::atomic_add(&fr.v_{cname(n)}, {r});")
+        pre = "    extern __shared__ __align__(16) unsigned char lds_raw[];\n    (void)lds_raw;\n" if cands else ""
+        self.kern.append(f"template <int PRIV>\n__global__ __launch_bounds__(256) void k{k}(const Args a) {{\n" + pre +
+                         "\n".join(out) + "\n}\n")
+        # host: grid from the trip count when the host can evaluate it
+        if fl.host_ok(loop.rng, set(hl)):
+            hctx = HostCtx(fl, self.hlv)
+            hlo, hhi = hctx.ex(loop.rng.lo), hctx.ex(loop.rng.hi)
+            hst = "1" if loop.rng.step is None else hctx.ex(loop.rng.step)
+            self.hemit("{")
+            self.hind += 1
+            self.hemit(f"const int64_t _trip = stade_lowered::jl_trip({hlo}, {hst}, {hhi});")
+            self.hemit("if (_trip > 0) {")
+            self.hind += 1
+            self.hemit(f"const unsigned _g = (unsigned)std::min<int64_t>((_trip + 255) / 256, {MAX_BLOCKS});")
+            if cands:
+                self.hemit("int _priv = 0;")
+                self.hemit("size_t _lds = 0;")
+                for c, n in enumerate(cands):
+                    es = 8 if fl.arrays[n] == "i" or fl.fty == "double" else 4
+                    hlen = hctx.length(n)
+                    cond = f"{hlen} > 0 && {hlen} * {es} <= {PRIV_MAX_BYTES} && _trip >= {PRIV_RATIO} * {hlen}"
+                    self.hemit(("if" if c == 0 else "else if") + f" ({cond}) {{ _priv = {c + 1}; _lds = (size_t){hlen} * {es}; }}")
+                self.hemit("switch (_priv) {")
+                for c in range(len(cands) + 1):
+                    self.hemit(f"case {c}:")
+                    self.hind += 1
+                    self.launch(f"k{k}", "_g", "256", "_lds", f"<{c}>")
+                    self.hemit("break;")
+                    self.hind -= 1
+                self.hemit("}")
+            else:
+                self.launch(f"k{k}", "_g", "256", "0", "<0>")
+            self.hind -= 1
+            self.hemit("}")
+            self.hind -= 1
+            self.hemit("}")
+        else:
+            self.launch(f"k{k}", str(MAX_BLOCKS), "256", "0", "<0>")
+        if pl.live_out:
+            kc = self.nk
+            self.nk += 1
+            lines = [f"    if (!({self.pred_code(op.pred)})) return;"]
+            for n in inv:
+                lines.append(f"    const {fl.cty(fl.scalars[n])} x_{cname(n)} = fr.v_{cname(n)};")
+            lines.append(f"    const int64_t _lo = {lo}, _st = {st}, _trip = stade_lowered::jl_trip(_lo, _st, {hi});")
+            lines.append("    if (_trip <= 0) return;")
+            for n in pl.live_out:
+                lines.append(f"    fr.v_{cname(n)} = wb.v_{cname(n)};")
+            self.kern.append(f"__global__ __launch_bounds__(1) void k{kc}(const Args a) {{\n" + "\n".join(lines) + "\n}\n")
+            self.launch(f"k{kc}")
+
+    def guard_code(self, pl: ParallelLoop, ctx) -> str:
+        conds = []
+        for g in pl.guards:
+            kind = g[0]
+            if kind == "nonzero":
+                conds.append(f"({self.poly(g[1], ctx)}) != 0")
+            elif kind == "positive":
+                conds.append(f"({self.poly(g[1], ctx)}) > 0")
+            elif kind == "nonneg_over_range":
+                v = pl.loop.var
+                at_lo = self.poly(g[1], ctx, {v: "_lo"})
+                at_hi = self.poly(g[1], ctx, {v: "(_lo + (_trip - 1) * _st)"})
+                conds.append(f"(_trip <= 0 || (({at_lo}) >= 0 && ({at_hi}) >= 0))")
+        return " && ".join(conds) if conds else "true"
+
+    def poly(self, p: dict, ctx, subst: dict | None = None) -> str:
+        subst = subst or {}
+        if not p:
+            return "((int64_t)0)"
+        terms = []
+        for m, c in sorted(p.items()):
+            fs = [f"((int64_t){c}LL)"]
+            for a in m:
+                fs.append(self.atom(a, ctx, subst))
+            terms.append(" * ".join(fs))
+        return "(" + " + ".join(terms) + ")"
+
+    def atom(self, a, ctx, subst):
+        if a[0] == "v":
+            n = a[1]
+            if n in subst:
+                return subst[n]
+            if n.startswith("size(") or n.startswith("length("):
+                inner = n[n.index("(") + 1:-1].split(",")
+                if n.startswith("length("):
+                    return ctx.length(inner[0])
+                return ctx.dim(inner[0], int(inner[1]) - 1 if len(inner) > 1 else 0)
+            return ctx.var(n) if n not in ctx.locals else ctx.locals[n]
+        X, N = _thaw(a[1]), _thaw(a[2])
+        x, n = self.poly(X, ctx, subst), self.poly(N, ctx, subst)
+        return f"({x} / {n})" if a[0] == "div" else f"stade_lowered::jl_mod({x}, {n})"
+
+    # -- structure ------------------------------------------------------------------------------
+    def ops(self, ops):
+        fl = self.fl
+        for op in ops:
+            if isinstance(op, SerialOp):
+                self.serial(op.stmts, op.pred)
+            elif isinstance(op, ParOp):
+                self.parallel(op)
+            elif isinstance(op, ReturnOp):
+                self.serial([], op.pred, op.value)
+            elif isinstance(op, AllocOp):
+                hctx = HostCtx(fl, self.hlv)
+                et = 8 if fl.arrays[op.name] == "i" or fl.fty == "double" else 4
+                slot = self.nalloc
+                self.nalloc += 1
+                self.hemit(f"a.D_{cname(op.name)}[0] = std::max<int64_t>(0, {hctx.ex(op.alloc.n)});")
+                self.hemit(f"a.N_{cname(op.name)} = a.D_{cname(op.name)}[0];")
+                self.hemit(f"if (!(a.A_{cname(op.name)} = reinterpret_cast<decltype(a.A_{cname(op.name)})>("
+                           f"_buf({slot}, (size_t)a.D_{cname(op.name)}[0] * {et})))) return _fail(hipErrorOutOfMemory, \"{op.name}\");")
+            elif isinstance(op, HostLoopOp):
+                hctx = HostCtx(fl, self.hlv)
+                lo, hi = hctx.ex(op.loop.rng.lo), hctx.ex(op.loop.rng.hi)
+                st = "1" if op.loop.rng.step is None else hctx.ex(op.loop.rng.step)
+                self.hemit("{")
+                self.hind += 1
+                self.hemit(f"const int64_t _lo{op.slot} = {lo}, _st{op.slot} = {st}, "
+                           f"_n{op.slot} = stade_lowered::jl_trip(_lo{op.slot}, _st{op.slot}, {hi});")
+                self.hemit(f"for (int64_t _k{op.slot} = 0; _k{op.slot} < _n{op.slot}; ++_k{op.slot}) {{")
+                self.hind += 1
+                self.hemit(f"a.hl[{op.slot}] = _lo{op.slot} + _k{op.slot} * _st{op.slot};")
+                saved = dict(self.hlv)
+                self.hlv[op.loop.var] = op.slot
+                self.ops(op.ops)
+                self.hlv = saved
+                self.hind -= 1
+                self.hemit("}")
+                self.hind -= 1
+                self.hemit("}")
+            elif isinstance(op, IfOp):
+                k = self.nk
+                self.nk += 1
+                reads = set()
+                for c, _ in op.node.branches:
+                    reads |= {n for n in _reads_of(c) if n not in fl.arrays}
+                names = sorted(n for n in reads if n in fl.scalars and n not in self.hlv)
+                ctx = Ctx(fl, {n: f"x_{cname(n)}" for n in names}, self.hlv)
+                lines = [f"    if (!({self.pred_code(op.pred)})) return;"]
+                for n in names:
+                    lines.append(f"    const {fl.cty(fl.scalars[n])} x_{cname(n)} = fr.v_{cname(n)};")
+                for f in op.flags:
+                    lines.append(f"    fr.flag[{f}] = 0;")
+                for j, (c, _) in enumerate(op.node.branches):
+                    cc, _ = fl.ex(c, ctx)
+                    lines.append(("    if" if j == 0 else "    else if") + f" ({cc}) fr.flag[{op.flags[j]}] = 1;")
+                if op.node.orelse is not None:
+                    lines.append(f"    else fr.flag[{op.flags[-1]}] = 1;")
+                self.kern.append(f"__global__ __launch_bounds__(1) void k{k}(const Args a) {{\n" + "\n".join(lines) + "\n}\n")
+                self.launch(f"k{k}")
+                for b in op.branches:
+                    self.ops(b)
+
+    def source(self) -> str:
+        fl = self.fl
+        f = fl.f
+        fr_fields = []
+        for n in fl.frame_scalars():
+            fr_fields.append(f"    {fl.cty(fl.scalars[n])} v_{cname(n)};")
+        args_fields = []
+        for n in sorted(fl.arrays):
+            et = "int64_t" if fl.arrays[n] == "i" else fl.fty
+            args_fields.append(f"    {et}* A_{cname(n)};")
+            args_fields.append(f"    int64_t D_{cname(n)}[{fl.T.ndim.get(n, 1)}];")
+            args_fields.append(f"    int64_t N_{cname(n)};   // elements (the product of the dimensions)")
+        for n in f.args:
+            if n not in fl.arrays:
+                args_fields.append(f"    {fl.cty(fl.scalars.get(n, 'f'))} s_{cname(n)};")
+        args_fields.append(f"    int64_t hl[{max(1, fl.nhl)}];")
+        self.ops(fl.ops)
+        init = ["    fr.nret = 0;", "    fr.oob = 0;"] + [f"    fr.v_{cname(n)} = a.s_{cname(n)};" for n in f.args if n not in fl.arrays]
+        init += [f"    fr.flag[{k}] = 0;" for k in range(fl.nflags)]
+        params, fill = [], []
+        for n in f.args:   # (parameters prefixed: a Julia name may be any C identifier)
+            if n in fl.arrays:
+                et = "int64_t" if fl.arrays[n] == "i" else fl.fty
+                params.append(f"{et}* p_{cname(n)}")
+                fill.append(f"    a.A_{cname(n)} = p_{cname(n)};")
+                for d in range(fl.T.ndim.get(n, 1)):
+                    params.append(f"int64_t p_{cname(n)}_d{d}")
+                    fill.append(f"    a.D_{cname(n)}[{d}] = p_{cname(n)}_d{d};")
+                nd = fl.T.ndim.get(n, 1)
+                fill.append(f"    a.N_{cname(n)} = " + " * ".join(f"p_{cname(n)}_d{d}" for d in range(nd)) + ";")
+                fill.append(f"    if (a.N_{cname(n)} < 0) return _fail(hipErrorInvalidValue, \"negative dimension of {n}\");")
+            else:
+                params.append(f"{fl.cty(fl.scalars.get(n, 'f'))} p_{cname(n)}")
+                fill.append(f"    a.s_{cname(n)} = p_{cname(n)};")
+        params += ["double* ret", "int64_t* iret", "hipStream_t stream"]
+        nb = max(1, self.nalloc)
+        return "\n".join([
+            f"namespace {self.ns} {{",
+            "using namespace stade_lowered;",
+            "struct Frame {",
+            *fr_fields,
+            f"    int32_t flag[{max(1, fl.nflags)}];",
+            "    double r[16];",
+            "    int64_t ri[16];",
+            "    int32_t rk[16];",
+            "    int32_t nret;",
+            "    int32_t oob;      // an index was outside its array",
+            "};",
+            "__device__ Frame fr;   // the function's scalars (one per device: calls that overlap race)",
+            "__device__ Frame wb;   // values of the last iteration of a parallel loop, committed after it",
+            "__device__ __forceinline__ void oob() { fr.oob = 1; }",
+            "template <class T>",
+            "__device__ __forceinline__ T rd(const T* p, int64_t i, int64_t n) {",
+            "    if ((uint64_t)i < (uint64_t)n) return p[i];",
+            "    oob();",
+            "    return T(0);",
+            "}",
+            "template <class T>",
+            "__device__ __forceinline__ void wr(T* p, int64_t i, int64_t n, T v) {",
+            "    if ((uint64_t)i < (uint64_t)n) p[i] = v;",
+            "    else oob();",
+            "}",
+            "struct Args {",
+            *args_fields,
+            "};",
+            "__global__ __launch_bounds__(1) void kinit(const Args a) {",
+            *init,
+            "}",
+            *self.kern,
+            f"static void* g_buf[{nb}];",
+            f"static size_t g_bytes[{nb}];",
+            "// local arrays (allocated inside the generated function): kept per process, grown on demand",
+            "static void* _buf(int slot, size_t bytes) {",
+            "    if (g_bytes[slot] < bytes) {",
+            "        if (g_buf[slot]) { (void)hipDeviceSynchronize(); (void)hipFree(g_buf[slot]); g_buf[slot] = nullptr; g_bytes[slot] = 0; }",
+            "        if (hipMalloc(&g_buf[slot], bytes ? bytes : 8) != hipSuccess) return nullptr;",
+            "        g_bytes[slot] = bytes;",
+            "    }",
+            "    return g_buf[slot];",
+            "}",
+            "}  // namespace",
+            "",
+            f"extern \"C\" int32_t stade_hip_gen_{cname(f.name)}({', '.join(params)}) {{",
+            f"    using namespace {self.ns};",
+            "    Args a{};",
+            *fill,
+            "    hipError_t _e;",
+            "    kinit<<<1, 1, 0, stream>>>(a);",
+            "    if ((_e = hipGetLastError()) != hipSuccess) return _fail(_e, \"kinit\");",
+            *self.host,
+            "    Frame h;",
+            "    if ((_e = hipMemcpyFromSymbolAsync(&h, HIP_SYMBOL(fr), sizeof(Frame), 0, hipMemcpyDeviceToHost, stream)) != hipSuccess)",
+            "        return _fail(_e, \"returned values\");",
+            "    if ((_e = hipStreamSynchronize(stream)) != hipSuccess) return _fail(_e, \"hipStreamSynchronize\");",
+            f"    if (h.oob) return _bounds(\"{f.name}\");",
+            "    for (int k = 0; k < h.nret && k < 16; ++k) {",
+            "        if (ret) ret[k] = h.r[k];",
+            "        if (iret) iret[k] = h.ri[k];",
+            "    }",
+            "    return h.nret;",
+            "}",
+            "",
+        ])
+
+
+class HostCtx:
+    """Host-side C of an expression the host can evaluate (Int arguments, array sizes, host
+    loop variables in scope)."""
+
+    def __init__(self, fl: FuncLower, hlv: dict):
+        self.fl = fl
+        self.hlv = hlv
+
+    def length(self, name):
+        nd = self.fl.T.ndim.get(name, 1)
+        return "(" + " * ".join(f"a.D_{cname(name)}[{d}]" for d in range(nd)) + ")"
+
+    def ex(self, e) -> str:
+        fl = self.fl
+        if isinstance(e, Num):
+            return f"((int64_t){int(e.text, 0)}LL)"
+        if isinstance(e, Var):
+            if e.name in self.hlv:
+                return f"a.hl[{self.hlv[e.name]}]"
+            return f"a.s_{cname(e.name)}"
+        if isinstance(e, Un):
+            return f"(-{self.ex(e.a)})"
+        if isinstance(e, Bin):
+            return f"({self.ex(e.a)} {e.op} {self.ex(e.b)})"
+        if isinstance(e, Call):
+            if e.fn == "length":
+                return self.length(e.args[0].name)
+            if e.fn == "size":
+                d = int(e.args[1].text) if len(e.args) > 1 else 1
+                return f"a.D_{cname(e.args[0].name)}[{d - 1}]"
+            xs = [self.ex(x) for x in e.args]
+            if e.fn == "div":
+                return f"({xs[0]} / {xs[1]})"
+            if e.fn == "mod":
+                return f"stade_lowered::jl_mod_h({xs[0]}, {xs[1]})"
+            if e.fn in ("max", "min"):
+                out = xs[0]
+                for x in xs[1:]:
+                    out = f"std::{e.fn}<int64_t>({out}, {x})"
+                return out
+            if e.fn == "abs":
+                return f"std::llabs({xs[0]})"
+        raise LowerError(f"{fl.f.name}: the host cannot evaluate {e!r}")
+
+
+PRELUDE = r"""// Generated by stade_hip.lower from STADE-generated Julia text: HIP for gfx950.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <algorithm>
+#include <cstdlib>
+#include "lowered_rt.hpp"
+namespace stade_lowered {
+inline int64_t jl_mod_h(int64_t a, int64_t b) { int64_t r = a % b; return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r; }
+}
+static char g_gen_err[256];
+static int32_t _fail(hipError_t e, const char* what) {
+    snprintf(g_gen_err, sizeof g_gen_err, "%s: %s", what, hipGetErrorString(e));
+    return -(int32_t)(e > 0 ? e : 1) - 100;
+}
+static int32_t _bounds(const char* fn) {
+    snprintf(g_gen_err, sizeof g_gen_err, "%s: an array index out of bounds (Julia raises a BoundsError)", fn);
+    return -3;
+}
+extern "C" const char* stade_hip_gen_last_error(void) { return g_gen_err; }
+"""
+
+
+def generate(text: str, precision: str = "f64", arg_types: dict | None = None) -> tuple[str, dict]:
+    """HIP source for every generated function of `text` (the initstacks_* functions stay on
+    the host) and, per function, its signature: [(name, kind, ndim)] with kind 'Af', 'Ai',
+    'f', 'i'."""
+    from .syntax import parse
+    funcs = parse(text)
+    src = [PRELUDE]
+    sigs = {}
+    # the element types of the stacks that the file's initstacks_* allocate (Int64 branch and
+    # tripcount stacks, Float64 value stacks) type the stack arguments of its functions
+    stack_kinds = {}
+    for f in funcs:
+        if f.name.startswith("initstacks_"):
+            for s in walk_stmts(f.body):
+                if isinstance(s, Assign) and isinstance(s.lhs, Var) and isinstance(s.rhs, Alloc):
+                    stack_kinds[s.lhs.name] = "Ai" if s.rhs.eltype == "Int64" else "Af"
+    for f in funcs:
+        if f.name.startswith("initstacks_"):
+            continue
+        kinds = {a: k for a, k in stack_kinds.items() if a in f.args}
+        kinds.update((arg_types or {}).get(f.name) or {})
+        fl = FuncLower(f, precision, kinds)
+        src.append(FuncGen(fl).source())
+        sig = []
+        for n in f.args:
+            if n in fl.arrays:
+                sig.append((n, "Ai" if fl.arrays[n] == "i" else "Af", fl.T.ndim.get(n, 1)))
+            else:
+                sig.append((n, fl.scalars.get(n, "f"), 0))
+        sigs[f.name] = dict(args=sig, plan=describe(fl.ops), reasons=list(fl.reasons))
+    return "\n".join(src), sigs
+
+
+def describe(ops, depth=0) -> list[str]:
+    out = []
+    for op in ops:
+        pad = "  " * depth
+        if isinstance(op, SerialOp):
+            nloops = sum(1 for t in walk_stmts(op.stmts) if isinstance(t, (For, While)))
+            out.append(pad + f"serial ({len(op.stmts)} statements" + (f", {nloops} loops in order)" if nloops else ")"))
+        elif isinstance(op, ParOp):
+            pl = op.pl
+            kinds = ", ".join(f"{n}:{u.kind}" for n, u in sorted(pl.arrays.items()))
+            out.append(pad + f"parallel over {pl.loop.var} [{kinds}]"
+                       + (f" sums {sorted(pl.reductions)}" if pl.reductions else ""))
+        elif isinstance(op, HostLoopOp):
+            out.append(pad + f"host loop over {op.loop.var}")
+            out += describe(op.ops, depth + 1)
+        elif isinstance(op, IfOp):
+            out.append(pad + "device if")
+            for b in op.branches:
+                out += describe(b, depth + 1)
+        elif isinstance(op, AllocOp):
+            out.append(pad + f"allocate {op.name}")
+        elif isinstance(op, ReturnOp):
+            out.append(pad + "return")
+    return out

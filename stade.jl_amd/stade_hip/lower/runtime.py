@@ -1,0 +1,237 @@
+"""Building and calling the libraries that the general lowering writes.
+
+`lower(text_or_path, precision)` turns a generated `.jl` into HIP source (`hipgen.generate`),
+compiles it for gfx950 once (hipcc, the build flags of libstade_hip: floating-point
+contraction off, packed FP32 off) into `stade.jl_amd/lib/gen/<stem>_<hash>.so`, and returns a
+`LoweredLib`.  A library already built for the same source is loaded as it is, so the GPU
+box, which receives the tree with its built libraries, does not compile.
+
+`LoweredLib.call(name, *args)` runs one generated function with Julia's argument convention:
+arrays are flat, contiguous torch tensors on the GPU (a matrix argument passes its Julia
+dimensions through `shapes=`), mutated in place; Int64 and float scalars are passed by value;
+the function's returned scalars come back as a tuple.  There is no CPU path: a tensor that is
+not on a GPU raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import os
+import shutil
+import subprocess
+import threading
+from pathlib import Path
+
+from . import hipgen
+from .syntax import Alloc, Assign, Bin, Call, LowerError, Nothing_, Num, Return, Tup, Un, Var, parse
+
+PKG = Path(__file__).resolve().parent.parent.parent
+GEN_LIB = PKG / "lib" / "gen"
+CSRC = PKG / "csrc"
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+ARCH = os.environ.get("STADE_HIP_ARCH", "gfx950")
+FLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-label", "-Wno-unused-variable",
+         "-Wno-unused-command-line-argument", "-I", str(CSRC)]
+_lock = threading.Lock()
+_cache: dict[str, "LoweredLib"] = {}
+
+
+def _src_key(src: str) -> str:
+    return hashlib.sha256((src + " ".join(FLAGS[1:])).encode()).hexdigest()[:16]
+
+
+def build_source(src: str, stem: str) -> Path:
+    """Compile HIP source into the generated-library directory (once per source text)."""
+    GEN_LIB.mkdir(parents=True, exist_ok=True)
+    so = GEN_LIB / f"{stem}_{_src_key(src)}.so"
+    with _lock:
+        if so.exists():
+            return so
+        hip = so.with_suffix(".hip")
+        hip.write_text(src)
+        tmp = so.with_suffix(f".so.tmp{os.getpid()}")
+        r = subprocess.run([HIPCC, *FLAGS, "-o", str(tmp), str(hip)], capture_output=True, text=True)
+        if r.returncode != 0:
+            raise LowerError(f"hipcc failed on the lowered {stem}:\n{r.stderr[-3000:]}")
+        os.replace(tmp, so)
+    return so
+
+
+class LoweredLib:
+    def __init__(self, so: Path, sigs: dict, precision: str, text: str):
+        self.path = so
+        self.sigs = sigs
+        self.precision = precision
+        self.text = text
+        self.lib = ctypes.CDLL(str(so))
+        self.lib.stade_hip_gen_last_error.restype = ctypes.c_char_p
+        self._fns = {}
+
+    def plan(self, name: str) -> list[str]:
+        return self.sigs[name]["plan"]
+
+    def _fn(self, name):
+        if name not in self._fns:
+            f = getattr(self.lib, f"stade_hip_gen_{hipgen.cname(name)}")
+            f.restype = ctypes.c_int32
+            ft = ctypes.c_float if self.precision == "f32" else ctypes.c_double
+            at = []
+            for a, kind, nd in self.sigs[name]["args"]:
+                if kind in ("Af", "Ai"):
+                    at += [ctypes.c_void_p] + [ctypes.c_int64] * nd
+                elif kind == "i":
+                    at.append(ctypes.c_int64)
+                elif kind == "b":
+                    at.append(ctypes.c_bool)
+                else:
+                    at.append(ft)
+            at += [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p]
+            f.argtypes = at
+            self._fns[name] = f
+        return self._fns[name]
+
+    def call(self, name: str, *args, shapes: dict | None = None, stream=None):
+        import torch
+        sig = self.sigs[name]["args"]
+        if len(args) != len(sig):
+            raise TypeError(f"{name} takes {len(sig)} arguments, got {len(args)}")
+        shapes = shapes or {}
+        fdt = torch.float32 if self.precision == "f32" else torch.float64
+        cargs = []
+        dev = None
+        for (a, kind, nd), v in zip(sig, args):
+            if kind in ("Af", "Ai"):
+                want = torch.int64 if kind == "Ai" else fdt
+                if not isinstance(v, torch.Tensor) or not v.is_cuda:
+                    raise ValueError(f"{name}: {a} must be a torch tensor on a GPU (there is no CPU path)")
+                if v.dtype != want:
+                    raise TypeError(f"{name}: {a} has dtype {v.dtype}, expected {want}")
+                if not v.is_contiguous():
+                    raise ValueError(f"{name}: {a} must be contiguous")
+                dims = tuple(shapes.get(a, (v.numel(),)))
+                if len(dims) < nd:
+                    raise ValueError(f"{name}: {a} is indexed with {nd} subscripts; pass its Julia dimensions in shapes")
+                if len(dims) > nd:   # trailing dimensions fold into the last one used
+                    head = list(dims[:nd - 1])
+                    tail = 1
+                    for d in dims[nd - 1:]:
+                        tail *= d
+                    dims = tuple(head + [tail])
+                n = 1
+                for d in dims:
+                    n *= d
+                if n != v.numel():
+                    raise ValueError(f"{name}: {a} has {v.numel()} elements, dimensions {dims} need {n}")
+                cargs += [ctypes.c_void_p(v.data_ptr())] + [int(d) for d in dims]
+                dev = dev or v.device
+            elif kind == "i":
+                cargs.append(int(v))
+            elif kind == "b":
+                cargs.append(bool(v))
+            else:
+                cargs.append(float(v))
+        if stream is None:
+            stream = torch.cuda.current_stream(dev).cuda_stream if dev is not None else 0
+        ret = (ctypes.c_double * 16)()
+        iret = (ctypes.c_int64 * 16)()
+        rc = self._fn(name)(*cargs, ret, iret, ctypes.c_void_p(stream))
+        if rc < 0:
+            raise RuntimeError(f"{name}: {self.lib.stade_hip_gen_last_error().decode(errors='replace')}")
+        kinds = self.sigs[name].get("ret", [])
+        return tuple(int(iret[k]) if k < len(kinds) and kinds[k] == "i" else float(ret[k]) for k in range(rc))
+
+
+def _ret_kinds(text: str, precision: str, arg_types) -> dict:
+    out = {}
+    arg_types = dict(arg_types or {})
+    for f in parse(text):
+        if f.name.startswith("initstacks_"):
+            for s in f.body:
+                if isinstance(s, Assign) and isinstance(s.lhs, Var) and isinstance(s.rhs, Alloc):
+                    for g in parse(text):
+                        if s.lhs.name in g.args:
+                            arg_types.setdefault(g.name, {})[s.lhs.name] = "Ai" if s.rhs.eltype == "Int64" else "Af"
+    for f in parse(text):
+        if f.name.startswith("initstacks_"):
+            continue
+        if f.body and isinstance(f.body[-1], Return) and f.body[-1].value is not None \
+                and not isinstance(f.body[-1].value, Nothing_):
+            v = f.body[-1].value
+            items = v.items if isinstance(v, Tup) else (v,)
+            fl = hipgen.FuncLower(f, precision, (arg_types or {}).get(f.name))
+            out[f.name] = ["i" if fl.T.etype(x) == "i" else "f" for x in items]
+    return out
+
+
+def lower(src, precision: str = "f64", arg_types: dict | None = None, tag: str | None = None) -> LoweredLib:
+    """Lower a generated file (path or text), build it once, load it."""
+    p = Path(src) if not (isinstance(src, str) and "\n" in src) else None
+    text = p.read_text() if p is not None else str(src)
+    key = (text, precision, repr(sorted((arg_types or {}).items())))
+    ck = hashlib.sha256(repr(key).encode()).hexdigest()
+    if ck in _cache:
+        return _cache[ck]
+    hip, sigs = hipgen.generate(text, precision, arg_types)
+    for name, kinds in _ret_kinds(text, precision, arg_types).items():
+        sigs[name]["ret"] = kinds
+    so = build_source(hip, tag or (p.stem if p is not None else "inline"))
+    lib = LoweredLib(so, sigs, precision, text)
+    _cache[ck] = lib
+    return lib
+
+
+# ------------------------------------------------------------------------------------------
+# initstacks_* on the host: the stack sizes are Int arithmetic of the Int arguments
+# ------------------------------------------------------------------------------------------
+
+def _ival(e, env):
+    if isinstance(e, Num):
+        return int(e.text, 0)
+    if isinstance(e, Var):
+        return env[e.name]
+    if isinstance(e, Un) and e.op == "-":
+        return -_ival(e.a, env)
+    if isinstance(e, Bin):
+        a, b = _ival(e.a, env), _ival(e.b, env)
+        if e.op == "+":
+            return a + b
+        if e.op == "-":
+            return a - b
+        if e.op == "*":
+            return a * b
+    if isinstance(e, Call):
+        xs = [_ival(x, env) for x in e.args]
+        if e.fn == "div":
+            q = abs(xs[0]) // abs(xs[1])
+            return q if (xs[0] >= 0) == (xs[1] >= 0) else -q
+        if e.fn == "mod":
+            return xs[0] % xs[1]
+        if e.fn == "max":
+            return max(xs)
+        if e.fn == "min":
+            return min(xs)
+    raise LowerError(f"initstacks: cannot evaluate {e!r} on the host")
+
+
+def initstacks(text: str, name: str, *int_args) -> list[tuple[str, str, int]]:
+    """[(stack name, element type, length)] that `initstacks_<k>_b(int_args...)` allocates,
+    in the order it returns them (`agen_init_emit` /root/reference/src/STADE.jl:4011-4097)."""
+    f = next((g for g in parse(text) if g.name == name), None)
+    if f is None:
+        raise LowerError(f"no function {name}")
+    env = dict(zip(f.args, (int(v) for v in int_args)))
+    allocs = {}
+    ret = []
+    for s in f.body:
+        if isinstance(s, Assign) and isinstance(s.lhs, Var):
+            if isinstance(s.rhs, Alloc):
+                allocs[s.lhs.name] = (s.rhs.eltype, max(0, _ival(s.rhs.n, env)))
+            else:
+                env[s.lhs.name] = _ival(s.rhs, env)
+        elif isinstance(s, Return) and s.value is not None:
+            items = s.value.items if isinstance(s.value, Tup) else (s.value,)
+            for it in items:
+                if isinstance(it, Var) and it.name in allocs:
+                    ret.append((it.name, *allocs[it.name]))
+    return ret

@@ -126,9 +126,13 @@ class ParityCase:
     slot read before it is written shows)."""
 
     def __init__(self, name: str, mode: str, args: list, stacks=(), precision: str = "f64",
-                 rtol: float | None = None, offset: int = 0, label: str | None = None):
+                 rtol: float | None = None, offset: int = 0, label: str | None = None, runner=None, oracle_path=None):
         self.name, self.mode, self.fname = name, mode, f"{name}_{mode}"
         self.args, self.stacks, self.precision, self.offset = args, tuple(stacks), precision, offset
+        # runner(device args, device stacks) -> returned values: the GPU path under test (default:
+        # the stade_hip mirror of the hand-written entry point); oracle_path: the text's file
+        self.runner = runner
+        self.oracle_path = oracle_path
         self.fdt = np.float32 if precision == "f32" else np.float64
         self.rtol = rtol if rtol is not None else RTOL[self.fdt]
         self.label = label or self.fname
@@ -137,8 +141,14 @@ class ParityCase:
         self._truth_lock = threading.Lock()
 
     # -- oracle (CPU) ---------------------------------------------------------------------
+    def _oracle(self, precision):
+        if self.oracle_path is not None:
+            from oracle import runner
+            return runner.load(self.oracle_path, precision=precision)
+        return oracle_lib(self.name, self.mode, precision)
+
     def run_oracle(self, lib=None):
-        lib = lib or oracle_lib(self.name, self.mode, self.precision)
+        lib = lib or self._oracle(self.precision)
         host = [v.copy(order="K") if isinstance(v, np.ndarray) else v for _, _, v in self.args]
         stack_h = [np.full(length, -7, dtype=np.int64) if kind == "Ai" else np.full(length, np.nan, dtype=self.fdt)
                    for _, (length, kind) in self.stacks]
@@ -158,7 +168,7 @@ class ParityCase:
     def _truth_locked(self):
         if self._truth is None:
             tprec, tdt = ("f80", np.longdouble) if self.precision == "f64" else ("f64", np.float64)
-            tl = oracle_lib(self.name, self.mode, tprec)
+            tl = self._oracle(tprec)
             th = [v.astype(np.int64 if v.dtype == np.int64 else tdt, order="K") if isinstance(v, np.ndarray) else v
                   for _, _, v in self.args]
             ts = [np.full(length, -7, dtype=np.int64) if kind == "Ai" else np.full(length, np.nan, dtype=tdt)
@@ -189,7 +199,10 @@ class ParityCase:
             else:
                 stack_d.append(torch.full((length + offset,), float("nan"),
                                           dtype=torch.float64 if self.fdt == np.float64 else torch.float32, device="cuda")[offset:])
-        ret_d = getattr(stade_hip, self.fname)(*dev, *stack_d)
+        if self.runner is not None:
+            ret_d = self.runner(dev, stack_d)
+        else:
+            ret_d = getattr(stade_hip, self.fname)(*dev, *stack_d)
         torch.cuda.synchronize()
         if ret_d is None:
             ret_d = ()

@@ -1,0 +1,150 @@
+"""The general lowering (stade_hip.lower) on the GPU against the oracle.
+
+Every case lowers a generated text to HIP, runs the built library on the GPU through its C
+entry point, and compares every output argument, stack and returned scalar with the oracle
+(the same text transpiled to sequential C) on the same seeded inputs, to the parity bars
+(fp64 1e-12, fp32 1e-5, integers exact) with the truth rule where a sum's order decides.
+
+Texts: the three kernels of stade.jl_amd/corpus/generic (a flattened mat-vec with scatters
+in the primal and the adjoint, an overlapping-window correlation, a binned sum over Int64
+labels), and the five benchmark configs' own texts taken through the general path instead of
+their hand-written kernels.  Sizes include ones whose accumulation targets are small enough,
+with enough iterations, for the LDS-privatised atomics (binsum's bins, window1d's taps), and
+ragged and empty ones."""
+import numpy as np
+import pytest
+
+from helpers import CORPUS, ParityCase, make_args
+
+pytestmark = pytest.mark.gpu
+
+GENERIC = CORPUS / "generic"
+FP32 = {"mlp2_ce", "conv3x3"}
+
+
+def _lowered(path, precision):
+    from stade_hip import lower
+    return lower.lower(path, precision)
+
+
+def _case(path, name, mode, shapes, ints, scalars=None, int_arrays=None, stacks=(), precision="f64", scales=None,
+          label=None):
+    from oracle import runner
+    import torch
+    lib_o = runner.load(path, precision=precision)
+    fname = f"{name}_{mode}"
+    shp = dict(shapes)
+    shp["__stacks__"] = tuple(s for s, _ in stacks)
+    fdt = np.float32 if precision == "f32" else np.float64
+    args = make_args(lib_o, fname, shp, ints, scalars or {}, f"lowered-{fname}-{ints}", fdt, int_arrays, scales)
+    low = _lowered(path, precision)
+    dims = {a: v.shape for a, _, v in args if isinstance(v, np.ndarray) and v.ndim > 1}
+
+    def run(dev, stack_d):
+        return low.call(fname, *dev, *stack_d, shapes=dims)
+    case = ParityCase(name, mode, args, stacks, precision, label=label or f"lowered {fname} {ints}", runner=run,
+                      oracle_path=path)
+    case.run_oracle(lib_o)
+    return case, low
+
+
+def _check(case, low, fname):
+    print(f"{case.label}: plan {low.plan(fname)}", flush=True)
+    case.run_gpu()
+    print(f"{case.label}: worst {case.compare():.3e}", flush=True)
+
+
+# ---- the three generic kernels ---------------------------------------------------------
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("mn", [(1, 1), (5, 4), (300, 70), (2000, 513), (0, 3)])
+def test_lowered_matvec_scatter(mode, mn):
+    m, n = mn
+    shapes = {k + s: v for k, v in dict(loss=1, a=m * n, x=n, y=m).items() for s in ("", "b", "d", "bd")}
+    case, low = _case(GENERIC / f"matvec_scatter_{mode}.jl", "matvec_scatter", mode, shapes, dict(i_m=m, i_n=n))
+    _check(case, low, f"matvec_scatter_{mode}")
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("nk", [(1, 1), (9, 4), (1000, 7), (50000, 7), (3, 5)])
+def test_lowered_window1d(mode, nk):
+    n, k = nk
+    nout = max(0, n - k + 1)
+    shapes = {a + s: v for a, v in dict(loss=1, inp=n, w=k, out=nout).items() for s in ("", "b", "d", "bd")}
+    case, low = _case(GENERIC / f"window1d_{mode}.jl", "window1d", mode, shapes, dict(i_n=n, i_k=k))
+    _check(case, low, f"window1d_{mode}")
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("nb", [(1, 1), (13, 4), (100000, 16), (20000, 3000), (0, 5)])
+def test_lowered_binsum(mode, nb):
+    from oracle import rng as jrng
+    n, b = nb
+    shapes = {a + s: v for a, v in dict(loss=1, v=n, c=b).items() for s in ("", "b", "d", "bd")}
+    g = jrng.Xoshiro(41 + n)
+    bins = np.array([1 + int(g.rand() * b) for _ in range(n)], dtype=np.int64)
+    case, low = _case(GENERIC / f"binsum_{mode}.jl", "binsum", mode, shapes, dict(i_n=n, i_b=b), int_arrays=dict(bins=bins))
+    _check(case, low, f"binsum_{mode}")
+
+
+# ---- the benchmark configs' texts through the general path ------------------------------
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("n", [1, 3, 64, 257])
+def test_lowered_diffusion2d(mode, n):
+    shapes = {k: n * n for k in ("u", "ub", "un", "unb", "ud", "ubd", "und", "unbd")}
+    shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
+    case, low = _case(CORPUS / f"diffusion2d_{mode}.jl", "diffusion2d", mode, shapes, dict(n=n))
+    _check(case, low, f"diffusion2d_{mode}")
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("mn", [(1, 1), (65, 33), (256, 300)])
+def test_lowered_affine_lsq(mode, mn):
+    m, n = mn
+    shapes = {k: (m, n) for k in ("w", "wb", "wd", "wbd")}
+    shapes.update({k: n for k in ("x", "xb", "xd", "xbd")})
+    shapes.update({k: m for k in ("b", "bb", "bd", "bbd", "t", "tb", "td", "tbd", "r", "rb", "rd", "rbd")})
+    shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
+    case, low = _case(CORPUS / f"affine_lsq_{mode}.jl", "affine_lsq", mode, shapes, dict(i_m=m, i_n=n))
+    _check(case, low, f"affine_lsq_{mode}")
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("case_", [(7, 6, 0.007), (100, 12, 10.0), (4097, 9, 10.0), (5, 0, 10.0)])
+def test_lowered_burgers1d(mode, case_):
+    n, T, tend = case_
+    shapes = {k: n for k in ("u", "ub", "un", "unb", "ud", "ubd", "und", "unbd")}
+    shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
+    scalars = dict(nu=0.05, dt=0.002, dx=0.5, tend=tend, nud=0.3, dtd=-0.2, dxd=0.1, tendd=0.7)
+    stacks = () if mode == "d" else (("branch_stack", (T, "Ai")), ("u_stack", (T * n, "Af")))
+    case, low = _case(CORPUS / f"burgers1d_{mode}.jl", "burgers1d", mode, shapes, dict(n=n, nsteps=T), scalars=scalars,
+                      stacks=stacks)
+    _check(case, low, f"burgers1d_{mode}")
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("size", [(8, 5, 7, 3), (33, 17, 40, 10)])
+def test_lowered_mlp2_ce(mode, size):
+    from oracle import rng as jrng
+    B, I, H, O = size
+    sz = dict(loss=1, x=I * B, w1=H * I, b1=H, w2=O * H, b2=O, h1=H * B, z=O * B)
+    shapes = {k + s: v for k, v in sz.items() for s in ("", "b", "d", "bd")}
+    lab = np.array([1 + int(jrng.Xoshiro(17 + s).rand() * O) for s in range(B)], dtype=np.int64)
+    g1, g2 = np.sqrt(2.0 / (I + H)), np.sqrt(2.0 / (H + O))
+    scales = {"w1": g1, "w1d": g1, "w2": g2, "w2d": g2, "b1": 0.1, "b2": 0.1}
+    case, low = _case(CORPUS / f"mlp2_ce_{mode}.jl", "mlp2_ce", mode, shapes, dict(i_b=B, i_in=I, i_h=H, i_out=O),
+                      int_arrays=dict(lab=lab), precision="f32", scales=scales)
+    _check(case, low, f"mlp2_ce_{mode}")
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("size", [(1, 1, 1, 1, 1), (2, 3, 5, 7, 9)])
+def test_lowered_conv3x3(mode, size):
+    N, C, K, H, W = size
+    sz = dict(loss=1, xp=(W + 2) * (H + 2) * C * N, w=9 * C * K, out=W * H * K * N)
+    shapes = {k + s: v for k, v in sz.items() for s in ("", "b", "d", "bd")}
+    s = 1.0 / np.sqrt(9.0 * C)
+    case, low = _case(CORPUS / f"conv3x3_{mode}.jl", "conv3x3", mode, shapes, dict(i_nb=N, i_c=C, i_k=K, i_h=H, i_w=W),
+                      precision="f32", scales={"w": s, "wd": s})
+    _check(case, low, f"conv3x3_{mode}")
