@@ -71,6 +71,7 @@ class Workload:
     kernel = ""           # dominant kernel (profiler name)
     bound = "hbm"
     dtype = "f64"
+    graph_steps = 0       # > 0: the timed steps are replays of a HIP graph of this many steps
 
     def __init__(self, mode: str):
         self.mode = mode
@@ -188,6 +189,10 @@ class Affine(Workload):
     direction (Wd, xd, bd, td) ~ N(0,1) from the next seed."""
     family = "affine_lsq"
     dtype = "f64"
+    # launch-bound at 1024^2 (an evaluation is 2-3 dependent launches of a few microseconds):
+    # the steps are issued as a captured HIP graph, as a caller running it in a loop would,
+    # so that the host's per-launch cost is not what is measured
+    graph_steps = 10
 
     def __init__(self, mode="b", m=1024, n=1024):
         super().__init__(mode)
@@ -445,6 +450,59 @@ def profiled_traffic(kernel: str):
     return int(m.group(1)) if m else None
 
 
+def _graph_us(fn, per_graph: int = 20, replays: int = 25) -> float:
+    """GPU time of one fn() in microseconds, with the host's launch cost taken out: per_graph
+    calls captured in one HIP graph (torch.cuda.graph), the graph replayed `replays` times
+    between two events."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(replays):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e3 / (replays * per_graph)
+
+
+def launch_floor(dev) -> dict:
+    """What an evaluation of the affine config (1024^2 fp64, 25.3 MB) must pay on this GPU,
+    measured with graph replays so that the host's launch cost is out: torch's own kernels
+    moving the matrix bytes in one launch and in three dependent launches, chains of one-element
+    launches (the per-launch floor), and the library's affine evaluations themselves."""
+    import torch
+    n = 1024 * 1024
+    w, wb = (torch.randn(n, dtype=torch.float64, device=dev) for _ in range(2))
+    tiny = torch.zeros(1, dtype=torch.float64, device=dev)
+    thirds = [(k * n // 3, (k + 1) * n // 3) for k in range(3)]
+    cases = {
+        "one launch, wb += w (24 MiB)": lambda: wb.add_(w),
+        "three dependent launches, wb[k] += w[k] (8 MiB each)": lambda: [wb[a:b].add_(w[a:b]) for a, b in thirds],
+        "one launch of one element": lambda: tiny.add_(1.0),
+        "two dependent launches of one element": lambda: [tiny.add_(1.0) for _ in range(2)],
+        "three dependent launches of one element": lambda: [tiny.add_(1.0) for _ in range(3)],
+    }
+    out = {name: round(_graph_us(fn), 2) for name, fn in cases.items()}
+    for mode in ("b", "d", "hv"):
+        wl = Affine(mode)
+        wl.setup(dev)
+        out[f"affine_lsq_{mode} evaluation (library, {2 if mode == 'd' else 3} launches)"] = round(_graph_us(wl.step), 2)
+    return {"launch_floor_us": out, "graph_replayed": True,
+            "affine_roofline_us": {m: round(Affine(m).algo_bytes() / 8e6, 2) for m in ("b", "d", "hv")}}
+
+
 def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
     import torch
     L = _lib()
@@ -452,10 +510,34 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
     for _ in range(warmup):
         wl.step()
     torch.cuda.synchronize()
+    run = lambda k: [wl.step() for _ in range(k)]
+    if wl.graph_steps:
+        # K steps as replays of captured graphs of graph_steps steps (and one of the remainder)
+        graphs = {}
+        for k in {min(wl.graph_steps, steps), steps % wl.graph_steps} - {0}:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                wl.step()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                run(k)
+            g.replay()
+            torch.cuda.synchronize()
+            graphs[k] = g
+        full, rest = divmod(steps, wl.graph_steps)
+
+        def run(k):
+            assert k == steps
+            for _ in range(full):
+                graphs[wl.graph_steps].replay()
+            if rest:
+                graphs[rest].replay()
     # pass 1, the timed region: K steps with nothing added to the stream
     t0 = time.perf_counter()
-    for _ in range(steps):
-        wl.step()
+    run(steps)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     # pass 2: the same K steps with the library's profiler on (a HIP event pair around every
@@ -508,6 +590,8 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
         out["eval_GBps"] = wl.algo_bytes() / (ms_step * 1e-3) / 1e9
         out["eval_hbm_frac"] = out["eval_GBps"] / HBM_PEAK_GBS
     out["config"] = wl.config()
+    if wl.graph_steps:
+        out["config"]["launch"] = f"HIP graph of {wl.graph_steps} steps, replayed (torch.cuda.graph)"
     return out
 
 
@@ -561,6 +645,10 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE counters to bytes)")
     ap.add_argument("--configs", default="", help="comma-separated workloads to measure besides the headline "
                                                   "(default: all)")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="time, with torch's own kernels, what any evaluation of the affine config must pay at "
+                         "1024^2 fp64: one launch moving its 24 MiB matrix bytes (wb += w), the same bytes split "
+                         "over three dependent launches, and chains of 1 and 3 launches of one element each")
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="run only torch's own elementwise kernels over the headline's bytes (4096^2 fp64: "
                          "un = u, ub += unb; 40 B per cell) and print their rate, a practical ceiling for "
@@ -583,6 +671,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": 8 * n, "copy_bytes_written": 8 * n, "launches": 10}))
+        return
+    if args.launch_floor:
+        print(json.dumps(launch_floor(dev)))
         return
     if args.stream_ceiling:
         n = 4096 * 4096

@@ -129,10 +129,10 @@ __global__ __launch_bounds__(BT) void finish_kernel(FinishArgs a, double* partia
         row_value<M>(a, i, s, sd);
         if (M != ADJ) {
             a.rd[i] = sd;
-            acc[1] = 0.5 * ((2.0 * s) * sd);
+            acc[1] += 0.5 * ((2.0 * s) * sd);   // a thread's rows accumulate (RPB > 1)
         }
         a.r[i] = s;
-        acc[0] = 0.5 * (s * s);
+        acc[0] += 0.5 * (s * s);
         if (M == ADJ) {
             double rbt = a.rb[i] + 0.5 * (2.0 * s) * a.lossb[0];
             a.rb[i] = 0.0;
@@ -268,19 +268,96 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
     }
 }
 
+// The tangent (and the adjoint forms with n = 0) for m <= kTicketRows: one wave a block, RPB
+// rows a lane, at most kTicketBlocks blocks.  Each block writes its loss partials, makes them
+// visible (one device-scope fence a block: with this few blocks the L2 write-backs it costs
+// are a fraction of a launch) and takes a ticket; the last block adds the partials in block
+// order into the loss and resets the ticket counter for the next call.  Spreading the rows
+// over many CUs is what makes this faster than one 1024-thread block (one CU pulling every
+// chunk partial).
+constexpr int kTicketBlocks = 32, kTicketRows = 2 * 64 * kTicketBlocks;
+
+template <int M, int RPB>
+__global__ __launch_bounds__(64) void finish_ticket_kernel(FinishArgs a, double* partials, SumOuts outs,
+                                                           uint32_t* ticket) {
+    __shared__ uint32_t last;
+    double acc[2] = {0.0, 0.0};
+#pragma unroll
+    for (int rr = 0; rr < RPB; ++rr) {
+        const int i = (blockIdx.x * RPB + rr) * 64 + threadIdx.x;
+        if (i < a.m) {
+            double s, sd;
+            row_value<M>(a, i, s, sd);
+            if (M != ADJ) {
+                a.rd[i] = sd;
+                acc[1] += 0.5 * ((2.0 * s) * sd);
+            }
+            a.r[i] = s;
+            acc[0] += 0.5 * (s * s);
+            if (M == ADJ) {
+                double rbt = a.rb[i] + 0.5 * (2.0 * s) * a.lossb[0];
+                a.rb[i] = 0.0;
+                a.bb[i] = a.bb[i] + rbt;
+                a.tb[i] = a.tb[i] + -rbt;
+            } else if (M == HVP) {
+                double h3 = a.lossb[0], h4 = 0.5 * (2.0 * s);
+                double rbdt = a.rbd[i] + (h3 * (0.5 * (2.0 * sd)) + h4 * a.lossbd[0]);
+                double rbt = a.rb[i] + h4 * h3;
+                a.rbd[i] = 0.0;
+                a.rb[i] = 0.0;
+                a.bbd[i] = a.bbd[i] + rbdt;
+                a.bb[i] = a.bb[i] + rbt;
+                a.tbd[i] = a.tbd[i] + -rbdt;
+                a.tb[i] = a.tb[i] + -rbt;
+            }
+        }
+    }
+    acc[0] = wave_sum(acc[0]);
+    acc[1] = wave_sum(acc[1]);
+    if (threadIdx.x == 0) {
+        partials[2 * blockIdx.x] = acc[0];
+        partials[2 * blockIdx.x + 1] = acc[1];
+    }
+    __threadfence();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    // the blocks' partials in block order (lane b holds block b's; gridDim.x <= 64)
+    const int b = threadIdx.x;
+    const double p0 = b < (int)gridDim.x ? __hip_atomic_load(&partials[2 * b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0;
+    const double p1 = b < (int)gridDim.x ? __hip_atomic_load(&partials[2 * b + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0;
+    double t0 = 0.0, t1 = 0.0;
+    for (int k = 0; k < (int)gridDim.x; ++k) {
+        t0 += lane_val(p0, k);
+        t1 += lane_val(p1, k);
+    }
+    if (threadIdx.x == 0) {
+        const double l0 = outs.p[0][0];
+        const double l1 = M != ADJ ? outs.p[1][0] : 0.0;
+        outs.p[0][0] = l0 + t0;
+        if (M != ADJ) outs.p[1][0] = l1 + t1;
+        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// one-wave blocks (the column partials are latency-bound reads: spread over many CUs), the
+// last block taking the loss's second stage on its own
 template <int M>
-__global__ __launch_bounds__(NT) void xfinish_kernel(double* __restrict__ xb, double* __restrict__ xbd,
+__global__ __launch_bounds__(64) void xfinish_kernel(double* __restrict__ xb, double* __restrict__ xbd,
                                                      const double* __restrict__ XP, const double* __restrict__ XPd,
                                                      int n, int mtiles, const double* partials, SumOuts outs) {
     __shared__ double red[32];
-    // second stage of the loss sums (the column kernel's row-tile partials), in the first block
-    if (blockIdx.x == 0) {
+    // second stage of the loss sums (the column kernel's row-tile partials)
+    if (blockIdx.x == gridDim.x - 1) {
         if (M == ADJ)
             finalize_partials<1>(partials, mtiles, red, outs);
         else
             finalize_partials<2>(partials, mtiles, red, outs);
+        return;
     }
-    const int j = blockIdx.x * NT + threadIdx.x;
+    const int j = blockIdx.x * 64 + threadIdx.x;
     if (j >= n) return;
     // row-tile partials 16 at a time, all loads in flight, added in tile order; xb (xbd) read
     // before either is written
@@ -345,10 +422,18 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
     fa.nchunks = nchunks;
     SumOuts outs{{fa.loss, fa.lossd}};
     if (!fused) {
-        if (m <= 4 * 1024) {
-            // one 1024-thread block, up to 4 rows a thread, sums the loss itself
-            STADE_TIMED("affine_finish", stream, finish_kernel<M, 1024, 4><<<1, 1024, 0, stream>>>(fa, ws->partials, outs));
-            STADE_LAUNCHED("affine finish_kernel");
+        if (m <= kTicketRows) {
+            // up to kTicketBlocks one-wave blocks, the last of which sums the loss
+            if (m <= 64 * kTicketBlocks) {
+                STADE_TIMED("affine_finish", stream,
+                            finish_ticket_kernel<M, 1><<<(unsigned)((m + 63) / 64), 64, 0, stream>>>(fa, ws->partials, outs,
+                                                                                                   ws->sync));
+            } else {
+                STADE_TIMED("affine_finish", stream,
+                            finish_ticket_kernel<M, 2><<<(unsigned)((m + 127) / 128), 64, 0, stream>>>(fa, ws->partials, outs,
+                                                                                                     ws->sync));
+            }
+            STADE_LAUNCHED("affine finish_ticket_kernel");
             return STADE_HIP_OK;
         }
         const int nfin = (int)((m + NT - 1) / NT);
@@ -366,7 +451,7 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
                                                                           ws->partials));
     STADE_LAUNCHED("affine cols_kernel");
     STADE_TIMED("affine_xfinish", stream,
-                xfinish_kernel<M><<<(unsigned)((n + NT - 1) / NT), NT, 0, stream>>>(xb, xbd, XP, XPd, (int)n, mtiles, ws->partials,
+                xfinish_kernel<M><<<(unsigned)((n + 63) / 64 + 1), 64, 0, stream>>>(xb, xbd, XP, XPd, (int)n, mtiles, ws->partials,
                                                                                      outs));
     STADE_LAUNCHED("affine xfinish_kernel");
     return STADE_HIP_OK;

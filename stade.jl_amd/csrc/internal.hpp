@@ -41,11 +41,18 @@ int32_t check_hip(hipError_t e, const char* what);
 struct Workspace {
     double* partials;       // per-block partial sums, kPartialSlots doubles
     double* dscalars;       // small device scalars handed back to the host
+    uint32_t* sync;         // ticket counters (kSyncSlots), zero between calls: a kernel's last
+                            // block resets the one it used
     void* scratch;          // grows on demand
     size_t scratch_bytes;
 };
 constexpr int kPartialSlots = 1 << 22;
 constexpr int kDeviceScalars = 64;
+constexpr int kSyncSlots = 64;
+// the device error flag (an int32 in the device scalars), raised with kErrIndex by a kernel
+// that sees an index the generated code would reject
+constexpr int kErrFlagSlot = 16;
+constexpr int kErrIndex = 1;
 
 // Workspace of the current device; nullptr (with the error set) on failure.
 Workspace* workspace();
@@ -67,6 +74,7 @@ class WsCall {
     ~WsCall();
     WsCall(const WsCall&) = delete;
     WsCall& operator=(const WsCall&) = delete;
+    bool capturing() const { return capturing_; }
     Workspace* ws;  // nullptr (with the error set) on failure
   private:
     int dev_;

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(HNT) void head_kernel(HeadArgs a) {
         }
         int l = (int)lab_s - 1;
         if (l < 0 || l >= O) {
-            if (lane == 0) atomicExch(a.err, 1);
+            if (lane == 0) atomicOr(a.err, kErrIndex);
             l = -1;
         }
         float zl = 0.f, zdl = 0.f;
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(h4nt<MODE>()) void head4_kernel(HeadArgs a) {
             const float se = row16_sum(e);
             const int l = (int)lab_lane - 1;
             const bool lok = l >= 0 && l < O;
-            if (live && lo == 0 && !lok) atomicExch(a.err, 1);
+            if (live && lo == 0 && !lok) atomicOr(a.err, kErrIndex);
             if (live && lok && lo == l) acc[0] += (double)(logf(se) - zv);
             // reverse of the loss: d2 = zb + [o == l](-lb) + exp(z) seb, seb = (1 / se) lb
             const float seb = (1.0f / se) * lb;
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(h4nt<MODE>()) void head4_kernel(HeadArgs a) {
             }
             int l = (int)lab[i] - 1;
             if (l < 0 || l >= O) {
-                if (live && lane == 0) atomicExch(a.err, 1);
+                if (live && lane == 0) atomicOr(a.err, kErrIndex);
                 l = -1;
             }
             float zl = 0.f, zdl = 0.f, zo = 0.f, zdo = 0.f;
@@ -977,7 +977,7 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     float *D2 = D1 + nD1, *D1d = D2 + nD2, *D2d = D1d + (MODE == HVP ? nD1 : 0), *cpart = D2d + (MODE == HVP ? nD2 : 0);
     float* c2part = cpart + nC;
     float* kpart = D1 + (nlocal + 63) / 64 * 64;
-    int* err = (int*)(ws->dscalars + 16);
+    int* err = (int*)(ws->dscalars + kErrFlagSlot);
     // forward: h1 = tanh(W1 x + b1); the tangent and HVP also h1d = (1 - h1^2)(W1 xd + W1d x + b1d),
     // as one dual product
     if (MODE == ADJ) {

@@ -59,6 +59,8 @@ Workspace* workspace() {
         if ((e = hipMalloc(&w.partials, sizeof(double) * kPartialSlots)) != hipSuccess ||
             (e = hipMalloc(&w.dscalars, sizeof(double) * kDeviceScalars)) != hipSuccess ||
             (e = hipMemset(w.dscalars, 0, sizeof(double) * kDeviceScalars)) != hipSuccess ||
+            (e = hipMalloc(&w.sync, sizeof(uint32_t) * kSyncSlots)) != hipSuccess ||
+            (e = hipMemset(w.sync, 0, sizeof(uint32_t) * kSyncSlots)) != hipSuccess ||
             (e = hipDeviceSynchronize()) != hipSuccess) {
             check_hip(e, "workspace allocation");
             return nullptr;
@@ -353,8 +355,8 @@ int32_t stade_hip_device_error(int32_t* flag) {
     // every stream's kernels first (the flag may be raised by a call on any stream)
     STADE_TRY_HIP(hipDeviceSynchronize());
     int32_t h = 0, z = 0;
-    STADE_TRY_HIP(hipMemcpy(&h, (int32_t*)(w->dscalars + 16), sizeof h, hipMemcpyDeviceToHost));
-    STADE_TRY_HIP(hipMemcpy((int32_t*)(w->dscalars + 16), &z, sizeof z, hipMemcpyHostToDevice));
+    STADE_TRY_HIP(hipMemcpy(&h, (int32_t*)(w->dscalars + kErrFlagSlot), sizeof h, hipMemcpyDeviceToHost));
+    STADE_TRY_HIP(hipMemcpy((int32_t*)(w->dscalars + kErrFlagSlot), &z, sizeof z, hipMemcpyHostToDevice));
     *flag = h;
     return STADE_HIP_OK;
 }

@@ -60,10 +60,24 @@ ENTRY_POINTS: dict[str, str] = {
 _CT = {"a": P, "i": I64, "f": F64, "r": F64P}
 
 
+def hip_runtime_first():
+    """Load torch (and with it the HIP runtime it carries) before any library of this package.
+
+    The libraries link libamdhip64.so.7; loaded first, they would bring in /opt/rocm's copy,
+    and torch would then load its own next to it.  Two HIP runtimes in one process do not
+    share the device (the second one's launches fail with "no ROCm-capable device"), so the
+    runtime torch carries is loaded first and the libraries resolve to it."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib():
     """The loaded library; raises if it has not been built."""
     global _lib
     if _lib is None:
+        hip_runtime_first()
         path = lib_path()
         if not path.exists():
             raise RuntimeError(f"libstade_hip.so not found at {path}: build it with "
@@ -178,13 +192,13 @@ def _call(fn: str, args: list, stream):
     _check(fn, getattr(lib(), fn)(*args, stream))
 
 
-def device_error() -> bool:
-    """Read and clear the device error flag (`stade_hip_device_error`): True if a kernel saw
-    an index the generated code would reject since the flag was last read.  Waits for the
-    device."""
+def device_error() -> int:
+    """Read and clear the device error flag (`stade_hip_device_error`): nonzero if a kernel
+    saw an index the generated code would reject since the flag was last read.  Waits for
+    the device."""
     flag = ctypes.c_int32(0)
     _check("stade_hip_device_error", lib().stade_hip_device_error(ctypes.byref(flag)))
-    return bool(flag.value)
+    return int(flag.value)
 
 
 def _bounds(fn: str, check: bool):

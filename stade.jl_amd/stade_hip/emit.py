@@ -19,9 +19,17 @@ same return convention as the generated function (`agen_emit` 3672, `hvp_emit`
 
 The kernel is identified by its primal, which STADE copies verbatim into every generated
 file (the trailing `function <k>(...)` of each `_b/_d/_hv` file), compared after removing
-comments and blank lines with the primal of `stade.jl_amd/corpus/<k>.jl`.  A file whose
-primal matches no kernel the library implements is refused with the reason, as STADE
-refuses what it cannot port (e.g. 18532-18534).
+comments and blank lines with the primal of `stade.jl_amd/corpus/<k>.jl`.
+
+Any other generated file goes through the general lowering (`stade_hip.lower`): its
+functions are written as HIP, built once for gfx950 into `lib/gen/<stem>_<hash>.so`, and
+the host functions `ccall` that library's `stade_hip_gen_<name>` entry points.  Arrays
+pass a device pointer and their Julia dimensions (the last one folding any further
+dimensions), scalars pass by value, the returned scalars come back through two host
+buffers (Float64 and Int64 values), and an index outside its array, which every lowered
+access checks, throws `BoundsError` as the generated code would.  A file the lowering
+cannot take is refused with the reason, as STADE refuses what it cannot port (e.g.
+18532-18534).
 """
 from __future__ import annotations
 
@@ -242,7 +250,112 @@ def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, s
     return "\n".join(lines)
 
 
-def stade_hip_file(in_path, out_path, *, precision=None, inbounds: bool = True, lib_path: str | None = None) -> str:
+_ALLOC_RE = re.compile(r"\bVector\{(Float64|Float32|Int64)\}\(undef,")
+_ZEROS_RE = re.compile(r"(?<![\w.])zeros\((Float64|Float32|Int64),")
+
+
+def _lowered_initstacks(fname: str, body: str, eltype: str) -> str:
+    """The generated `initstacks_<k>_b` with its host vectors allocated on the device
+    (`cgen_stack_device_expr` /root/reference/src/STADE.jl:9798-9802); the size arithmetic
+    is kept as written."""
+    body = _ALLOC_RE.sub(lambda m: f"ROCArray{{{eltype if m.group(1) != 'Int64' else 'Int64'}}}(undef,", body)
+    body = _ZEROS_RE.sub(lambda m: f"AMDGPU.zeros({eltype if m.group(1) != 'Int64' else 'Int64'},", body)
+    body = re.sub(rf"^function\s+{re.escape(fname)}\s*\(", f"function {fname}_hip(", body, count=1, flags=re.M)
+    return body.rstrip()
+
+
+def _lowered_call(fname: str, sig: dict, cfun: str, eltype: str) -> str:
+    """Host function for one lowered function: one ccall into the generated library."""
+    types, vals, arrays = [], [], []
+    for nm, kind, nd in sig["args"]:
+        if kind in ("Af", "Ai"):
+            types.append("Ptr{Int64}" if kind == "Ai" else f"Ptr{{{eltype}}}")
+            vals.append(f"pointer({nm})")
+            arrays.append(nm)
+            if nd == 1:
+                types.append("Int64")
+                vals.append(f"length({nm})")
+            else:
+                for d in range(1, nd):
+                    types.append("Int64")
+                    vals.append(f"size({nm}, {d})")
+                types.append("Int64")
+                vals.append(f"prod(size({nm})[{nd}:end])")
+        elif kind == "i":
+            types.append("Int64")
+            vals.append(f"Int64({nm})")
+        elif kind == "b":
+            types.append("Bool")
+            vals.append(f"Bool({nm})")
+        else:
+            types.append(eltype)
+            vals.append(f"{eltype}({nm})")
+    types += ["Ptr{Float64}", "Ptr{Int64}", "Ptr{Cvoid}"]
+    vals += ["__ret", "__iret", "AMDGPU.stream().stream"]
+    args = [nm for nm, _, _ in sig["args"]]
+    lines = [f"function {fname}_hip({', '.join(args)})",
+             "    __ret = zeros(Float64, 16)",
+             "    __iret = zeros(Int64, 16)"]
+    lines.append(f"    GC.@preserve {' '.join(arrays + ['__ret', '__iret'])} begin")
+    lines.append(f"        __rc = ccall((:{cfun}, libstade_gen), Int32,")
+    lines.append(f"                     ({', '.join(types)},),")
+    lines.append(f"                     {', '.join(vals)})")
+    lines.append("    end")
+    lines.append("    __rc == -3 && throw(BoundsError())")
+    lines.append(f"    __rc >= 0 || error(\"{cfun}: \", unsafe_string(ccall((:stade_hip_gen_last_error, libstade_gen), Cstring, ())))")
+    kinds = sig.get("ret") or []
+    vals_ret = [f"__iret[{k + 1}]" if kd == "i" else (f"__ret[{k + 1}]" if eltype == "Float64" else f"{eltype}(__ret[{k + 1}])")
+                for k, kd in enumerate(kinds)]
+    if not vals_ret:
+        lines.append("    return nothing")
+    elif len(vals_ret) == 1:
+        lines.append(f"    return {vals_ret[0]}")
+    else:
+        lines.append("    return (" + ", ".join(vals_ret) + ")")
+    lines.append("end")
+    return "\n".join(lines)
+
+
+def _lowered_file(text: str, in_path, out_path, precision) -> str:
+    from .lower import LowerError, hipgen, lower
+    if precision in (None, "Float64", "f64"):
+        prec = "f32" if re.search(r"\bFloat32\b", text) and precision is None else "f64"
+    elif precision in ("Float32", "f32"):
+        prec = "f32"
+    else:
+        raise StadeHipRefusal(f"precision={precision}: the lowering writes Float64 or Float32 code")
+    eltype = "Float32" if prec == "f32" else "Float64"
+    try:
+        lib = lower(text, prec, tag=Path(in_path).stem)
+    except LowerError as e:
+        raise StadeHipRefusal(f"{Path(in_path).name}: the general lowering cannot take this file: {e}") from e
+    funcs = _split_functions(text)
+    out = [
+        f"# Generated by stade_hip_file from {Path(in_path).name} through the general lowering: host",
+        "# functions that run the lowered HIP library (MI355X, gfx950) through ccall.  Arguments,",
+        "# in-place effects and return values are those of the generated functions they stand for.",
+        "using AMDGPU",
+        f"const libstade_gen = \"{lib.path}\"",
+        "",
+    ]
+    for fname, (args, body) in funcs.items():
+        if fname.startswith("initstacks_"):
+            out.append(_lowered_initstacks(fname, body, eltype))
+        elif fname in lib.sigs:
+            sig = lib.sigs[fname]
+            if [a for a, _, _ in sig["args"]] != args:
+                raise StadeHipRefusal(f"{fname}: the lowered argument list differs from the generated one")
+            out.append(_lowered_call(fname, sig, f"stade_hip_gen_{hipgen.cname(fname)}", eltype))
+        else:
+            continue
+        out.append("")
+    result = "\n".join(out)
+    Path(out_path).write_text(result)
+    return result
+
+
+def stade_hip_file(in_path, out_path, *, precision=None, inbounds: bool = True, lib_path: str | None = None,
+                   general: bool = True) -> str:
     """Write Julia host code for the generated functions of `in_path` into `out_path`.
 
     `precision` mirrors `stade_amdgpu_file`'s keyword: `None` keeps the kernel's element
@@ -250,11 +363,19 @@ def stade_hip_file(in_path, out_path, *, precision=None, inbounds: bool = True, 
     `inbounds` mirrors it too: with `inbounds=false` the host functions read the device
     error flag after the call (one synchronisation) and throw a `BoundsError` where an
     index value held in an Int64 array (the MLP labels) is out of range; with the default
-    `true`, as in the reference's GPU code, nothing is checked.
+    `true`, as in the reference's GPU code, nothing is checked.  (Lowered files check every
+    access either way.)
+    `general=False` refuses, instead of lowering, a file whose primal matches none of the
+    library's hand-written kernels.
     Returns the written text.
     """
     text = Path(in_path).read_text()
-    spec, funcs = identify(text)
+    try:
+        spec, funcs = identify(text)
+    except StadeHipRefusal:
+        if not general:
+            raise
+        return _lowered_file(text, in_path, out_path, precision)
     if precision not in (None, spec.eltype):
         raise StadeHipRefusal(f"{spec.name}: libstade_hip implements {spec.eltype} only, precision={precision} requested")
     libp = lib_path or "libstade_hip"

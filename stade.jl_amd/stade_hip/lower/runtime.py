@@ -38,7 +38,12 @@ _cache: dict[str, "LoweredLib"] = {}
 
 
 def _src_key(src: str) -> str:
-    return hashlib.sha256((src + " ".join(FLAGS[1:])).encode()).hexdigest()[:16]
+    # the flags without the include directory's absolute path: the key (and so the library's
+    # file name) must not depend on where the tree sits, or a copied tree would rebuild
+    # (the device runtime header is part of the source)
+    flags = " ".join(f for f in FLAGS[1:] if f != str(CSRC))
+    rt = (CSRC / "lowered_rt.hpp").read_text()
+    return hashlib.sha256((src + flags + rt).encode()).hexdigest()[:16]
 
 
 def build_source(src: str, stem: str) -> Path:
@@ -64,9 +69,18 @@ class LoweredLib:
         self.sigs = sigs
         self.precision = precision
         self.text = text
-        self.lib = ctypes.CDLL(str(so))
-        self.lib.stade_hip_gen_last_error.restype = ctypes.c_char_p
+        self._lib = None
         self._fns = {}
+
+    @property
+    def lib(self):
+        """The library, loaded at first use (after torch's HIP runtime: `hip_runtime_first`)."""
+        if self._lib is None:
+            from ..api import hip_runtime_first
+            hip_runtime_first()
+            self._lib = ctypes.CDLL(str(self.path))
+            self._lib.stade_hip_gen_last_error.restype = ctypes.c_char_p
+        return self._lib
 
     def plan(self, name: str) -> list[str]:
         return self.sigs[name]["plan"]

@@ -33,7 +33,7 @@ def _prototypes() -> dict[str, tuple[str, list[str]]]:
 JL2C = {
     "Ptr{Float64}": "double*", "Ptr{Float32}": "float*", "Ref{Float64}": "double*", "Ptr{Int64}": "int64_t*",
     "Int64": "int64_t", "Float64": "double", "Ptr{Cvoid}": "hipStream_t", "Ref{Int32}": "int32_t*",
-    "Int32": "int32_t", "Cstring": "char*",
+    "Int32": "int32_t", "Cstring": "char*", "Float32": "float", "Bool": "bool",
 }
 
 
@@ -64,7 +64,7 @@ def _ccalls(text: str):
             depth += {"(": 1, ")": -1}.get(text[i], 0)
             i += 1
         parts = _split_top(text[m.end():i - 1])
-        sym = re.match(r"\(:(\w+), libstade_hip\)", parts[0]).group(1)
+        sym = re.match(r"\(:(\w+), (libstade_hip|libstade_gen)\)", parts[0]).group(1)
         types = parts[2].strip()
         assert types.startswith("(") and types.endswith(")"), types
         out.append((sym, parts[1], _split_top(types[1:-1]), parts[3:]))
@@ -125,21 +125,105 @@ def test_emitted_bounds_check_for_labels(tmp_path):
     assert "stade_hip_device_error" not in stade_hip_file(CORPUS / "mlp2_ce_b.jl", tmp_path / "p.jl")
 
 
-def test_refuses_unknown_kernel(tmp_path):
+def test_unknown_kernel_refused_without_the_general_path(tmp_path):
     from stade_hip import stade_hip_file
     from stade_hip.emit import StadeHipRefusal
     src = tmp_path / "other_b.jl"
     src.write_text((CORPUS / "diffusion2d_b.jl").read_text().replace("0.1 * (u[(j - 1) * n + im]", "0.2 * (u[(j - 1) * n + im]"))
     with pytest.raises(StadeHipRefusal, match="no kernel implemented"):
-        stade_hip_file(src, tmp_path / "o.jl")
+        stade_hip_file(src, tmp_path / "o.jl", general=False)
 
 
 @pytest.mark.skipif(not REF_CORPUS.exists(), reason="reference corpus not mounted")
-def test_refuses_reference_corpus_kernel(tmp_path):
+def test_reference_corpus_kernel_refused_without_the_general_path(tmp_path):
     from stade_hip import stade_hip_file
     from stade_hip.emit import StadeHipRefusal
     with pytest.raises(StadeHipRefusal):
-        stade_hip_file(REF_CORPUS / "affine_loss_b.jl", tmp_path / "o.jl")
+        stade_hip_file(REF_CORPUS / "affine_loss_b.jl", tmp_path / "o.jl", general=False)
+
+
+def test_lowering_refusal_names_the_cause(tmp_path):
+    from stade_hip import stade_hip_file
+    from stade_hip.emit import StadeHipRefusal
+    src = tmp_path / "odd_b.jl"
+    src.write_text("function odd_b(x, xb, n)\n    for i = 1:n\n        xb[i] = xb[i] + frobnicate(x[i])\n    end\n"
+                   "    return nothing\nend\n")
+    with pytest.raises(StadeHipRefusal, match="general lowering cannot take"):
+        stade_hip_file(src, tmp_path / "o.jl")
+
+
+def _gen_prototypes(text: str) -> dict[str, tuple[str, list[str]]]:
+    """name -> (return type, [parameter types]) of the extern "C" functions in lowered HIP source."""
+    from stade_hip.lower import hipgen
+    src, _ = hipgen.generate(text)
+    out = {}
+    for m in re.finditer(r'extern "C" (?:const )?([\w*]+\*?)\s+(stade_hip_gen_\w+)\(([^)]*)\)', src):
+        types = []
+        for prm in m.group(3).split(","):
+            prm = " ".join(prm.split())
+            if not prm or prm == "void":
+                continue
+            types.append(re.match(r"(.*?)\s*\w+$", prm).group(1).replace("const ", "").replace(" *", "*"))
+        out[m.group(2)] = (m.group(1), types)
+    return out
+
+
+GENERIC_FILES = [f"{k}_{m}" for k in ("matvec_scatter", "window1d", "binsum") for m in ("b", "d", "hv")]
+
+
+def _check_lowered(text: str, gen_text: str) -> list[str]:
+    protos = _gen_prototypes(gen_text)
+    protos["stade_hip_gen_last_error"] = ("char*", [])
+    bad = []
+    for sym, ret, jtypes, vals in _ccalls(text):
+        cret, ctys = protos[sym]
+        if JL2C[ret] != cret:
+            bad.append(f"{sym}: returns {cret}, ccall says {ret}")
+        if len(jtypes) != len(ctys) or len(vals) != len(jtypes):
+            bad.append(f"{sym}: {len(ctys)} parameters, ccall {len(jtypes)} types and {len(vals)} values")
+            continue
+        bad += [f"{sym} parameter {k}: C {ct}, ccall {jt}" for k, (jt, ct) in enumerate(zip(jtypes, ctys)) if JL2C[jt] != ct]
+    return bad
+
+
+@pytest.mark.parametrize("name", GENERIC_FILES)
+def test_lowered_emission_ccall_types(tmp_path, name):
+    """A file no hand-written kernel implements goes through the general lowering: one host
+    function per generated function, keeping its argument list, whose ccall into the lowered
+    library matches the generated C prototype type by type (arrays: pointer and Julia
+    dimensions; Int64, Float64 by value; two host return buffers; the stream)."""
+    from stade_hip import stade_hip_file
+    src = CORPUS / "generic" / f"{name}.jl"
+    text = stade_hip_file(src, tmp_path / "o.jl")
+    assert "const libstade_gen = " in text
+    gen = src.read_text()
+    for fn, args in re.findall(r"^function (\w+)\(([^)]*)\)", gen, re.M):
+        h = re.search(rf"^function {fn}_hip\(([^)]*)\)", text, re.M)
+        assert h and h.group(1) == args, fn
+    lines = text.splitlines()
+    assert sum(ln.startswith("function ") for ln in lines) == sum(ln == "end" for ln in lines)
+    calls = _ccalls(text)
+    assert len(calls) == text.count("ccall(("), "a ccall the checker could not parse"
+    assert _check_lowered(text, gen) == []
+
+
+def test_lowered_ccall_checker_catches_a_wrong_type(tmp_path, monkeypatch):
+    """The check above fails on a planted mistake: Float64 arrays emitted as Ptr{Float32}."""
+    from stade_hip import emit, stade_hip_file
+    real = emit._lowered_call
+    monkeypatch.setattr(emit, "_lowered_call", lambda f, sig, c, et: real(f, sig, c, "Float32"))
+    src = CORPUS / "generic" / "window1d_b.jl"
+    text = stade_hip_file(src, tmp_path / "o.jl")
+    assert any("Ptr{Float32}" in b for b in _check_lowered(text, src.read_text()))
+
+
+def test_lowered_initstacks_allocate_on_the_device(tmp_path):
+    from stade_hip.emit import _lowered_initstacks
+    body = (CORPUS / "burgers1d_b.jl").read_text().split("\nend\n")[0] + "\nend"
+    out = _lowered_initstacks("initstacks_burgers1d_b", body, "Float64")
+    assert "function initstacks_burgers1d_b_hip(n, nsteps)" in out
+    assert "branch_stack = ROCArray{Int64}(undef, max(0, div(nsteps - 1, 1) + 1))" in out
+    assert "u_stack = ROCArray{Float64}(undef, " in out and "Vector{" not in out
 
 
 def test_ccall_checker_catches_a_wrong_type(tmp_path, monkeypatch):
@@ -151,3 +235,15 @@ def test_ccall_checker_catches_a_wrong_type(tmp_path, monkeypatch):
     protos = _prototypes()
     sym, ret, jtypes, vals = next(c for c in _ccalls(text) if c[0] == "stade_hip_mlp2_ce_b")
     assert any(JL2C[jt] != ct for jt, ct in zip(jtypes, protos[sym][1]))
+
+
+@pytest.mark.parametrize("src", [f"{k}_{m}" for k in NAMES for m in ("b", "d", "hv")] + [f"generic/{g}" for g in GENERIC_FILES])
+@pytest.mark.parametrize("inbounds", [True, False])
+def test_emitted_lines_are_forms_the_gpu_tests_execute(tmp_path, src, inbounds):
+    """Every statement of the emitted host functions is one of the forms tests/jlhost.py
+    executes on the GPU, so those tests run the emitted text as written."""
+    from jlhost import JlHost
+    from stade_hip import stade_hip_file
+    host = JlHost(stade_hip_file(CORPUS / f"{src}.jl", tmp_path / "o.jl", inbounds=inbounds))
+    assert host.funcs
+    assert host.unknown_lines() == []

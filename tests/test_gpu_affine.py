@@ -6,7 +6,7 @@ from helpers import run_parity
 pytestmark = pytest.mark.gpu
 
 SIZES = [(1, 1), (3, 5), (64, 64), (65, 130), (200, 77), (1, 300), (300, 1), (1024, 1024), (4, 0), (0, 3),
-         (5000, 3), (5000, 0)]
+         (5000, 3), (5000, 0), (2048, 2048), (1000, 3000)]
 
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
@@ -24,3 +24,4 @@ def test_affine_lsq_parity(mode, mn):
         shapes[k] = 1
     print(f"affine_lsq_{mode} m={m} n={n}", flush=True)
     run_parity("affine_lsq", mode, shapes, dict(i_m=m, i_n=n))
+
