@@ -301,6 +301,39 @@ class Burgers(Workload):
         return f"burgers1d_{self.mode} on {self.n} cells for {self.T} steps"
 
 
+class BurgersCkpt(Burgers):
+    """Config 5 under the checkpoint tape policy (stade_hip_burgers1d_{b,hv}_ckpt): the state
+    of every `every`-th step is kept and each segment is recomputed in the reverse sweep.
+    Same inputs and outputs as Burgers; the tape the caller holds is 1/every of the full one."""
+
+    def __init__(self, mode="b", n=1 << 20, nsteps=500, every=32):
+        super().__init__(mode, n, nsteps)
+        self.every = every
+        self.name = f"burgers1d_{mode}_ckpt"
+
+    def stack_lengths(self):
+        return [(self.T, "Ai"), (-(-self.T // self.every) * self.n, "Af")]
+
+    def step(self):
+        import stade_hip
+        getattr(stade_hip, f"burgers1d_{self.mode}_ckpt")(*self.argv, self.every)
+
+    def config(self):
+        c = super().config()
+        c["workload"] = c["workload"].replace(f"burgers1d_{self.mode}:", f"burgers1d_{self.mode} (checkpoint policy, "
+                                              f"every {self.every} steps):")
+        c["tape_bytes"] = 8 * (-(-self.T // self.every)) * self.n
+        c["every"] = self.every
+        return c
+
+    def sample(self):
+        Ts = 20
+        return Burgers(self.mode, self.n, Ts), Ts / self.T
+
+    def sample_desc(self):
+        return f"burgers1d_{self.mode} (tape form: the same CPU code) on {self.n} cells for 20 steps"
+
+
 class Mlp(Workload):
     """Config 3: x (784, 4096) ~ U[0,1], tanh hidden layer of 1024, 10-way softmax
     cross-entropy, Float32; W1, W2 Glorot-uniform U(+-sqrt(6 / (fan_in + fan_out))),
@@ -421,6 +454,8 @@ WORKLOADS = {
     "burgers1d_b": lambda: Burgers("b"),
     "burgers1d_d": lambda: Burgers("d"),
     "burgers1d_hv": lambda: Burgers("hv"),
+    "burgers1d_b_ckpt": lambda: BurgersCkpt("b"),
+    "burgers1d_hv_ckpt": lambda: BurgersCkpt("hv"),
     "mlp2_ce_b": lambda: Mlp("b"),
     "mlp2_ce_d": lambda: Mlp("d"),
     "mlp2_ce_hv": lambda: Mlp("hv"),

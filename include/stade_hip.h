@@ -136,6 +136,29 @@ int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* 
                                double* dxbd, double tendd, double* tendbd, int64_t* branch_stack, double* u_stack,
                                hipStream_t stream);
 
+/* Tape policy: checkpoints and segment recompute.  The generated functions keep the state of
+ * every step (u_stack, nsteps * n values; the HVP's u_stack_d as many again).  Under this
+ * policy the caller passes u_ckpt instead, the state at the start of every `every`-th step
+ * (ceil(nsteps / every) * n values, stade_hip_burgers1d_ckpt_lengths); the reverse sweep
+ * recomputes each segment of `every` steps from its checkpoint into an `every`-row tape in
+ * library scratch and sweeps it back.  Every other output (loss, ub, un, unb, branch_stack,
+ * the scalar shadows, and for the HVP their tangents) is that of stade_hip_burgers1d_b / _hv;
+ * u_ckpt row k equals u_stack row k * every.  The reference's counterpart is a generator
+ * policy, not an ABI: its `ii_` recompute planning (/root/reference/src/STADE.jl:19314-20273)
+ * and rematerialised restores (`agen_remat_*` 5687-5899) rewrite the generated text so that
+ * values are recomputed in the reverse sweep instead of stored. */
+int32_t stade_hip_burgers1d_ckpt_lengths(int64_t n, int64_t nsteps, int64_t every, int64_t lengths[2]);
+int32_t stade_hip_burgers1d_b_ckpt(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                                   double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend,
+                                   double* tendb, int64_t n, int64_t nsteps, int64_t* branch_stack, double* u_ckpt, int64_t every,
+                                   hipStream_t stream);
+int32_t stade_hip_burgers1d_hv_ckpt(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                                    double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
+                                    int64_t n, int64_t nsteps, double* lossd, const double* lossbd, const double* ud, double* ubd,
+                                    double* und, double* unbd, double nud, double* nubd, double dtd, double* dtbd, double dxd,
+                                    double* dxbd, double tendd, double* tendbd, int64_t* branch_stack, double* u_ckpt, int64_t every,
+                                    hipStream_t stream);
+
 /* ---- config 3: mlp2_ce(loss, x, lab, w1, b1, w2, b2, h1, z, i_b, i_in, i_h, i_out) --------
  * tanh hidden layer, softmax cross-entropy summed over the batch, Float32 arrays (STADE's
  * precision=Float32, `cgen_convert_precision` /root/reference/src/STADE.jl:15351-15365),

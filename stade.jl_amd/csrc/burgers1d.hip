@@ -29,6 +29,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 namespace stade {
 namespace {
 
@@ -80,7 +82,7 @@ template <bool TAN, int S>
 __global__ __launch_bounds__(BNT) void fwd_kernel(const double* __restrict__ src, const double* __restrict__ srcd,
                                                  double* __restrict__ dst, double* __restrict__ dstd,
                                                  double* __restrict__ tape, double* __restrict__ taped, int n, int64_t t0,
-                                                 int nk, Coef c) {
+                                                 int nk, Coef c, int64_t row0, int every) {
     constexpr int L = S + 2 * KMAX;
     __shared__ double A[2][L];
     __shared__ double D[TAN ? 2 : 1][TAN ? L : 1];
@@ -95,8 +97,11 @@ __global__ __launch_bounds__(BNT) void fwd_kernel(const double* __restrict__ src
     __syncthreads();
     int cur = 0;
     for (int k = 0; k < nk; ++k) {
-        const size_t row = (size_t)(t0 + k) * (size_t)n;
-        if (tape) {
+        // the state at the start of step t0 + k goes to tape row (t0 + k - row0) / every when
+        // every divides t0 + k - row0 (every = 1, row0 = 0: the generated stack's layout)
+        const int64_t tr = t0 + k - row0;
+        const size_t row = (size_t)(tr / every) * (size_t)n;
+        if (tape && tr % every == 0) {
             for (int e = threadIdx.x; e < own; e += BNT) {
                 // streaming stores: a tape row is read back only by the reverse sweep (plain
                 // stores measured 1 % slower over an evaluation, the reverse sweep's reads too)
@@ -256,7 +261,7 @@ template <bool HV, int S, int T>
 __global__ __launch_bounds__(T) void bwd_kernel(const double* __restrict__ win, const double* __restrict__ wind,
                                                   double* __restrict__ vout, double* __restrict__ voutd,
                                                   const double* __restrict__ tape, const double* __restrict__ taped, int n,
-                                                  int64_t t_hi, int nk, Coef c, double* partials) {
+                                                  int64_t t_hi, int nk, Coef c, double* partials, int64_t row0) {
     constexpr int L = S + 2 * KMAX;
     constexpr int M = (L + T - 1) / T;  // extended-region positions per thread
     __shared__ double W[2][L];
@@ -282,7 +287,7 @@ __global__ __launch_bounds__(T) void bwd_kernel(const double* __restrict__ win, 
     // held in registers from one step ahead
     double pre[M], pred[M];
     auto fetch = [&](int k) {
-        const size_t row = (size_t)(t_hi - k) * (size_t)n;
+        const size_t row = (size_t)(t_hi - k - row0) * (size_t)n;
 #pragma unroll
         for (int i = 0; i < M; ++i) {
             const int e = threadIdx.x + i * T;
@@ -331,7 +336,7 @@ template <bool HV, int S, int PD, int T>
 __global__ __launch_bounds__(T) void bwd_reg_kernel(const double* __restrict__ win, const double* __restrict__ wind,
                                                       double* __restrict__ vout, double* __restrict__ voutd,
                                                       const double* __restrict__ tape, const double* __restrict__ taped, int n,
-                                                      int64_t t_hi, Coef c, double* partials) {
+                                                      int64_t t_hi, Coef c, double* partials, int64_t row0) {
     constexpr int nk = KMAX, L = S + 2 * KMAX;
     constexpr int M = (L + T - 1) / T, NWV = T / 64;
     constexpr int NA = HV ? 4 : 2;  // exchanged arrays: u, w (+ ud, wd)
@@ -372,7 +377,7 @@ __global__ __launch_bounds__(T) void bwd_reg_kernel(const double* __restrict__ w
     }
     double pu[PD][M], pud[HV ? PD : 1][M];
     auto fetch = [&](int slot, int k) {
-        const size_t row = (size_t)(t_hi - (k < nk ? k : nk - 1)) * (size_t)n;
+        const size_t row = (size_t)(t_hi - (k < nk ? k : nk - 1) - row0) * (size_t)n;
 #pragma unroll
         for (int i = 0; i < M; ++i) {
             pu[slot][i] = __builtin_nontemporal_load(&tape[row + xc[i]]);
@@ -555,22 +560,24 @@ int32_t check(int64_t n, int64_t nsteps, const char* fn) {
     return STADE_HIP_OK;
 }
 
-// forward sweep over steps [0, nrun): src (+d) -> final state in fin (+d); tape rows written
+// forward sweep over steps [t_begin, t_end): src (+d) -> final state in fin (+d); the state at
+// the start of step t goes to tape row (t - row0) / every when every divides t - row0
 template <bool TAN>
 int32_t forward(const double* src, const double* srcd, double* fin, double* find, double* tape, double* taped, int n,
-                int64_t nrun, const Coef& c, double* P, double* Q, double* Pd, double* Qd, hipStream_t stream) {
+                int64_t t_begin, int64_t t_end, const Coef& c, double* P, double* Q, double* Pd, double* Qd, hipStream_t stream,
+                int64_t row0 = 0, int every = 1) {
     constexpr int S = 4096;
     const unsigned nb = grid_for(n, S);
     const double *cs = src, *csd = srcd;
-    int64_t t0 = 0;
+    int64_t t0 = t_begin;
     int flip = 0;
-    while (t0 < nrun) {
-        int nk = (int)((nrun - t0) < KMAX ? (nrun - t0) : KMAX);
-        bool last = t0 + nk >= nrun;
+    while (t0 < t_end) {
+        int nk = (int)((t_end - t0) < KMAX ? (t_end - t0) : KMAX);
+        bool last = t0 + nk >= t_end;
         double* d = last ? fin : (flip ? Q : P);
         double* dd = last ? find : (flip ? Qd : Pd);
         STADE_TIMED(TAN ? "burgers1d_fwd_tan" : "burgers1d_fwd", stream,
-                    fwd_kernel<TAN, S><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c));
+                    fwd_kernel<TAN, S><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c, row0, every));
         STADE_LAUNCHED("burgers1d fwd_kernel");
         cs = d;
         csd = dd;
@@ -585,50 +592,89 @@ int init_blocks(int64_t n) { return (int)grid_for((int)n, kInitBlockCells); }
 size_t bwd_offset(int64_t n) { return ((size_t)init_blocks(n) * 2 + 1023) / 1024 * 1024; }
 template <bool HV>
 int bwd_blocks(int64_t n) { return (int)grid_for((int)n, HV ? BWD_S_HV : BWD_S); }
+// (every > 1: the checkpoint policy's reverse sweep, whose segments of `every` steps are
+// chunked separately)
 template <bool HV>
-int32_t check_partials(int64_t n, int64_t nrun, const char* fn) {
-    const int64_t chunks = (nrun + KMAX - 1) / KMAX;
+int32_t check_partials(int64_t n, int64_t nrun, const char* fn, int64_t every = 1) {
+    const int64_t chunks = every > 1 ? (nrun + every - 1) / every * ((every + KMAX - 1) / KMAX) : (nrun + KMAX - 1) / KMAX;
     const int64_t need = (int64_t)bwd_offset(n) + chunks * bwd_blocks<HV>(n) * (HV ? 4 : 2);
     if (need > kPartialSlots)
         return set_error(STADE_HIP_ERANGE, "%s: n * nsteps too large for the reduction workspace (%lld slots needed)", fn, (long long)need);
     return STADE_HIP_OK;
 }
 
-// reverse sweep over steps nrun..1 from w (+d); the final state goes to ub (+d); returns the
-// number of partial blocks written at pbwd
+// The reverse sweep's state: the adjoint state (+d) in cw, the other buffer of the pair in ow,
+// and the chunks done so far (each writes nb * NV partials).
+struct BwdState {
+    double *cw, *cwd, *ow, *owd;
+    int chunk;
+};
+
+// reverse sweep over steps t_hi, t_hi - 1, ..., t_lo, reading tape row t - row0 for step t;
+// when `final` the last chunk writes its state to ub (+d); *nparts = partial blocks so far
 template <bool HV>
-int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, double* ubd, const double* tape, const double* taped,
-                 int n, int64_t nrun, const Coef& c, double* pbwd, int* nparts, hipStream_t stream) {
+int32_t backward_range(BwdState& st, double* ub, double* ubd, const double* tape, const double* taped, int n, int64_t t_hi,
+                       int64_t t_lo, int64_t row0, bool final, const Coef& c, double* pbwd, int* nparts, hipStream_t stream) {
     constexpr int S = HV ? BWD_S_HV : BWD_S, T = HV ? BWD_T_HV : BWD_T;
     constexpr int NV = HV ? 4 : 2;
     const unsigned nb = grid_for(n, S);
-    double *cw = w, *cwd = wd, *ow = W2, *owd = W2d;
-    int64_t t = nrun - 1;
-    int chunk = 0;
-    while (t >= 0) {
-        int nk = (int)((t + 1) < KMAX ? (t + 1) : KMAX);
-        bool last = t - nk < 0;
-        double* d = last ? ub : ow;
-        double* dd = last ? ubd : owd;
+    int64_t t = t_hi;
+    while (t >= t_lo) {
+        int nk = (int)((t - t_lo + 1) < KMAX ? (t - t_lo + 1) : KMAX);
+        bool last = final && t - nk < t_lo;
+        double* d = last ? ub : st.ow;
+        double* dd = last ? ubd : st.owd;
         if (nk == KMAX) {
             STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
-                        bwd_reg_kernel<HV, S, 2, T><<<nb, T, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, c,
-                                                                      pbwd + (size_t)chunk * nb * NV));
+                        bwd_reg_kernel<HV, S, 2, T><<<nb, T, 0, stream>>>(st.cw, st.cwd, d, dd, tape, taped, n, t, c,
+                                                                      pbwd + (size_t)st.chunk * nb * NV, row0));
         } else {
             STADE_TIMED(HV ? "burgers1d_bwd_hv" : "burgers1d_bwd", stream,
-                        bwd_kernel<HV, S, T><<<nb, T, 0, stream>>>(cw, cwd, d, dd, tape, taped, n, t, nk, c,
-                                                                 pbwd + (size_t)chunk * nb * NV));
+                        bwd_kernel<HV, S, T><<<nb, T, 0, stream>>>(st.cw, st.cwd, d, dd, tape, taped, n, t, nk, c,
+                                                                 pbwd + (size_t)st.chunk * nb * NV, row0));
         }
         STADE_LAUNCHED("burgers1d bwd_kernel");
-        ++chunk;
-        *nparts = chunk * (int)nb;
-        double* tmp = cw;
-        cw = ow;
-        ow = tmp;
-        tmp = cwd;
-        cwd = owd;
-        owd = tmp;
+        ++st.chunk;
+        *nparts = st.chunk * (int)nb;
+        std::swap(st.cw, st.ow);
+        std::swap(st.cwd, st.owd);
         t -= nk;
+    }
+    return STADE_HIP_OK;
+}
+
+// reverse sweep over steps nrun..1 from w (+d) with the whole tape; the final state goes to
+// ub (+d); returns the number of partial blocks written at pbwd
+template <bool HV>
+int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, double* ubd, const double* tape, const double* taped,
+                 int n, int64_t nrun, const Coef& c, double* pbwd, int* nparts, hipStream_t stream) {
+    BwdState st{w, wd, W2, W2d, 0};
+    return backward_range<HV>(st, ub, ubd, tape, taped, n, nrun - 1, 0, 0, true, c, pbwd, nparts, stream);
+}
+
+// The reverse sweep under the checkpoint policy: the forward kept the state at the start of
+// every `every`-th step (rows ck, and ckd for the HVP); each segment [s0, s1), last first, is
+// recomputed from its checkpoint into the segment tape seg (+ segd, `every` rows), then swept
+// back.  The recomputed states are those the full forward produced (the same kernels, the
+// same steps), so the reverse sweep reads the tape it would have read.
+template <bool HV>
+int32_t backward_ckpt(double* w, double* wd, double* W2, double* W2d, double* ub, double* ubd, const double* ck,
+                      const double* ckd, double* seg, double* segd, double* R, int n, int64_t nrun, int every, const Coef& c,
+                      double* pbwd, int* nparts, hipStream_t stream) {
+    BwdState st{w, wd, W2, W2d, 0};
+    double *R1 = R, *R2 = R + n, *R1d = R + 2 * (size_t)n, *R2d = R + 3 * (size_t)n, *Rf = R + 4 * (size_t)n,
+           *Rfd = R + 5 * (size_t)n;
+    const int64_t nseg = (nrun + every - 1) / every;
+    for (int64_t k = nseg - 1; k >= 0; --k) {
+        const int64_t s0 = k * every, s1 = std::min<int64_t>(s0 + every, nrun);
+        const double* src = ck + (size_t)k * n;
+        const double* srcd = HV ? ckd + (size_t)k * n : nullptr;
+        if (int32_t rc = forward<HV>(src, srcd, Rf, HV ? Rfd : nullptr, seg, HV ? segd : nullptr, n, s0, s1, c, R1, R2,
+                                     HV ? R1d : nullptr, HV ? R2d : nullptr, stream, s0, 1))
+            return rc;
+        if (int32_t rc = backward_range<HV>(st, ub, ubd, seg, HV ? segd : nullptr, n, s1 - 1, s0, s0, k == 0, c, pbwd, nparts,
+                                            stream))
+            return rc;
     }
     return STADE_HIP_OK;
 }
@@ -638,47 +684,21 @@ int32_t backward(double* w, double* wd, double* W2, double* W2d, double* ub, dou
 
 using namespace stade;
 
-extern "C" {
+namespace stade {
+namespace {
 
-int32_t stade_hip_burgers1d_stack_lengths(int64_t n, int64_t nsteps, int64_t lengths[2]) {
-    // initstacks_burgers1d_b: branch_stack max(0, div(nsteps - 1, 1) + 1),
-    // u_stack max(0, div(nsteps - 1, 1) + 1) * max(0, div(n - 1, 1) + 1)   (Julia div truncates)
-    if (!lengths) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_stack_lengths: null lengths");
-    int64_t a = (nsteps - 1) / 1 + 1, b = (n - 1) / 1 + 1;
-    a = a > 0 ? a : 0;
-    b = b > 0 ? b : 0;
-    lengths[0] = a;
-    lengths[1] = a * b;
-    return STADE_HIP_OK;
-}
-
-int32_t stade_hip_initstacks_burgers1d_b(int64_t n, int64_t nsteps, int64_t** branch_stack, double** u_stack) {
-    int64_t len[2];
-    if (int32_t rc = stade_hip_burgers1d_stack_lengths(n, nsteps, len)) return rc;
-    if (!branch_stack || !u_stack) return set_error(STADE_HIP_EINVAL, "stade_hip_initstacks_burgers1d_b: null output");
-    *branch_stack = nullptr;
-    *u_stack = nullptr;
-    STADE_TRY_HIP(hipMalloc((void**)branch_stack, (size_t)(len[0] > 0 ? len[0] : 1) * sizeof(int64_t)));
-    hipError_t e = hipMalloc((void**)u_stack, (size_t)(len[1] > 0 ? len[1] : 1) * sizeof(double));
-    if (e != hipSuccess) {
-        (void)hipFree(*branch_stack);  // the allocation error is the one reported
-        *branch_stack = nullptr;
-        return check_hip(e, "hipMalloc(u_stack)");
-    }
-    return STADE_HIP_OK;
-}
-
-int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+template <bool CK>
+int32_t adjoint_impl(const char* fn, int64_t every, double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
                               double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
                               int64_t n, int64_t nsteps, int64_t* branch_stack, double* u_stack, hipStream_t stream) {
-    if (int32_t rc = check(n, nsteps, "stade_hip_burgers1d_b")) return rc;
-    if (!nub || !dtb || !dxb || !tendb) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_b: null scalar shadow");
+    if (int32_t rc = check(n, nsteps, fn)) return rc;
+    if (!nub || !dtb || !dxb || !tendb) return set_error(STADE_HIP_EINVAL, "%s: null scalar shadow", fn);
     if ((n > 0 && (!loss || !lossb || !u || !ub || !un || !unb)) || (nsteps > 0 && (!branch_stack || (n > 0 && !u_stack))))
-        return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_b: null pointer");
+        return set_error(STADE_HIP_EINVAL, "%s: null pointer", fn);
     const double cadv = 0.5 * dt / dx;
     const double cdif = nu * dt / (dx * dx);
     const int64_t nrun = taken_steps(dt, tend, nsteps);
-    if (int32_t rc = check_partials<false>(n, nrun, "stade_hip_burgers1d_b")) return rc;
+    if (int32_t rc = check_partials<false>(n, nrun, fn, CK ? every : 1)) return rc;
     Coef c{cadv, cdif, 0.0, 0.0};
     WsCall call_(stream);
     Workspace* ws = call_.ws;
@@ -689,10 +709,16 @@ int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u
     }
     double cadvb = 0.0, cdifb = 0.0;
     if (n > 0) {
-        double* P = (double*)scratch(sizeof(double) * 2 * (size_t)n);
+        // checkpoint policy: the segment tape (`every` rows) and the recompute states follow
+        const size_t seg_len = CK ? (size_t)every * (size_t)n : 0;
+        double* P = (double*)scratch(sizeof(double) * (2 * (size_t)n + (CK ? seg_len + 6 * (size_t)n : 0)));
         if (!P) return STADE_HIP_ENOMEM;
         double* Q = P + n;
-        if (int32_t rc = forward<false>(u, nullptr, un, nullptr, u_stack, nullptr, (int)n, nrun, c, P, Q, nullptr, nullptr, stream)) return rc;
+        double* seg = Q + n;
+        double* R = seg + seg_len;
+        if (int32_t rc = forward<false>(u, nullptr, un, nullptr, u_stack, nullptr, (int)n, 0, nrun, c, P, Q, nullptr, nullptr, stream,
+                                        0, CK ? (int)every : 1))
+            return rc;
         const double* uT = nrun > 0 ? un : u;
         const int gi = init_blocks(n);
         STADE_TIMED("burgers1d_init", stream,
@@ -702,7 +728,11 @@ int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u
         int nparts = 0;
         double* pbwd = ws->partials + bwd_offset(n);
         if (nrun > 0) {
-            if (int32_t rc = backward<false>(P, nullptr, Q, nullptr, ub, nullptr, u_stack, nullptr, (int)n, nrun, c, pbwd, &nparts, stream)) return rc;
+            int32_t rc = CK ? backward_ckpt<false>(P, nullptr, Q, nullptr, ub, nullptr, u_stack, nullptr, seg, nullptr, R, (int)n, nrun,
+                                                   (int)every, c, pbwd, &nparts, stream)
+                            : backward<false>(P, nullptr, Q, nullptr, ub, nullptr, u_stack, nullptr, (int)n, nrun, c, pbwd, &nparts,
+                                              stream);
+            if (rc) return rc;
         }
         STADE_TIMED("finalize", stream,
                     bwd_finalize_kernel<false><<<2, FNT, 0, stream>>>(ws->partials, gi, SumOuts{{loss}}, pbwd, nparts,
@@ -736,55 +766,25 @@ int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u
     return STADE_HIP_OK;
 }
 
-int32_t stade_hip_burgers1d_d(double* loss, double* lossd, double* u, double* ud, double* un, double* und, double nu, double nud,
-                              double dt, double dtd, double dx, double dxd, double tend, double tendd, int64_t n, int64_t nsteps,
-                              hipStream_t stream) {
-    (void)tendd;
-    if (int32_t rc = check(n, nsteps, "stade_hip_burgers1d_d")) return rc;
-    if (n == 0) return STADE_HIP_OK;
-    if (!loss || !lossd || !u || !ud || !un || !und) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_d: null pointer");
-    const double c0 = dx * dx;
-    Coef c{0.5 * dt / dx, nu * dt / c0, (0.5 * dtd) / dx + -((0.5 * dt) / (dx * dx)) * dxd,
-           (dt * nud + nu * dtd) / c0 + -((nu * dt) / (c0 * c0)) * (dx * dxd + dx * dxd)};
-    const int64_t nrun = taken_steps(dt, tend, nsteps);
-    WsCall call_(stream);
-    Workspace* ws = call_.ws;
-    if (!ws) return STADE_HIP_ENOMEM;
-    double* P = (double*)scratch(sizeof(double) * 4 * (size_t)n);
-    if (!P) return STADE_HIP_ENOMEM;
-    double *Q = P + n, *Pd = Q + n, *Qd = Pd + n;
-    if (nrun > 0) {
-        if (int32_t rc = forward<true>(u, ud, un, und, nullptr, nullptr, (int)n, nrun, c, P, Q, Pd, Qd, stream)) return rc;
-        STADE_TIMED("burgers1d_copy", stream, copy2_kernel<<<grid_for((int)n, NT * 8), NT, 0, stream>>>(un, u, und, ud, (int)n));
-        STADE_LAUNCHED("burgers1d copy2_kernel");
-    }
-    // loss and lossd from the final state, now in u and ud
-    const int gl = init_blocks(n);
-    STADE_TIMED("burgers1d_loss", stream, loss2_kernel<<<gl, NT, 0, stream>>>(u, ud, (int)n, ws->partials));
-    STADE_LAUNCHED("burgers1d loss2_kernel");
-    STADE_TIMED("finalize", stream, finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, gl, SumOuts{{loss, lossd}}));
-    STADE_LAUNCHED("burgers1d finalize_kernel");
-    return STADE_HIP_OK;
-}
-
-int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+template <bool CK>
+int32_t hvp_impl(const char* fn, int64_t every, double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
                                double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
                                int64_t n, int64_t nsteps, double* lossd, const double* lossbd, const double* ud, double* ubd,
                                double* und, double* unbd, double nud, double* nubd, double dtd, double* dtbd, double dxd,
                                double* dxbd, double tendd, double* tendbd, int64_t* branch_stack, double* u_stack,
                                hipStream_t stream) {
     (void)tendd;
-    if (int32_t rc = check(n, nsteps, "stade_hip_burgers1d_hv")) return rc;
+    if (int32_t rc = check(n, nsteps, fn)) return rc;
     if (!nub || !dtb || !dxb || !tendb || !nubd || !dtbd || !dxbd || !tendbd)
-        return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_hv: null scalar shadow");
+        return set_error(STADE_HIP_EINVAL, "%s: null scalar shadow", fn);
     if ((n > 0 && (!loss || !lossb || !u || !ub || !un || !unb || !lossd || !lossbd || !ud || !ubd || !und || !unbd)) ||
         (nsteps > 0 && (!branch_stack || (n > 0 && !u_stack))))
-        return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_hv: null pointer");
+        return set_error(STADE_HIP_EINVAL, "%s: null pointer", fn);
     const double c0 = dx * dx;
     Coef c{0.5 * dt / dx, nu * dt / c0, (0.5 * dtd) / dx + -((0.5 * dt) / (dx * dx)) * dxd,
            (dt * nud + nu * dtd) / c0 + -((nu * dt) / (c0 * c0)) * (dx * dxd + dx * dxd)};
     const int64_t nrun = taken_steps(dt, tend, nsteps);
-    if (int32_t rc = check_partials<true>(n, nrun, "stade_hip_burgers1d_hv")) return rc;
+    if (int32_t rc = check_partials<true>(n, nrun, fn, CK ? every : 1)) return rc;
     WsCall call_(stream);
     Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
@@ -796,11 +796,18 @@ int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* 
     if (n > 0) {
         // u_stack_d: allocated inside the generated _hv (Vector{Float64}(undef, length(u_stack)));
         // here a library scratch region, reused across calls
-        size_t tape_len = (size_t)nrun * (size_t)n;
-        double* P = (double*)scratch(sizeof(double) * (4 * (size_t)n + tape_len));
+        // (checkpoint policy: u_stack_d holds the checkpoints of ud, and the two segment tapes
+        // and the recompute states follow)
+        const size_t rows = CK ? (size_t)((nrun + every - 1) / every) : (size_t)nrun;
+        const size_t tape_len = rows * (size_t)n;
+        const size_t seg_len = CK ? (size_t)every * (size_t)n : 0;
+        double* P = (double*)scratch(sizeof(double) * (4 * (size_t)n + tape_len + (CK ? 2 * seg_len + 6 * (size_t)n : 0)));
         if (!P) return STADE_HIP_ENOMEM;
         double *Q = P + n, *Pd = Q + n, *Qd = Pd + n, *taped = Qd + n;
-        if (int32_t rc = forward<true>(u, ud, un, und, u_stack, taped, (int)n, nrun, c, P, Q, Pd, Qd, stream)) return rc;
+        double *seg = taped + tape_len, *segd = seg + seg_len, *R = segd + seg_len;
+        if (int32_t rc = forward<true>(u, ud, un, und, u_stack, taped, (int)n, 0, nrun, c, P, Q, Pd, Qd, stream, 0,
+                                       CK ? (int)every : 1))
+            return rc;
         const double* uT = nrun > 0 ? un : u;
         const double* udT = nrun > 0 ? und : ud;
         const int gi = init_blocks(n);
@@ -811,7 +818,10 @@ int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* 
         int nparts = 0;
         double* pbwd = ws->partials + bwd_offset(n);
         if (nrun > 0) {
-            if (int32_t rc = backward<true>(P, Pd, Q, Qd, ub, ubd, u_stack, taped, (int)n, nrun, c, pbwd, &nparts, stream)) return rc;
+            int32_t rc = CK ? backward_ckpt<true>(P, Pd, Q, Qd, ub, ubd, u_stack, taped, seg, segd, R, (int)n, nrun, (int)every, c,
+                                                  pbwd, &nparts, stream)
+                            : backward<true>(P, Pd, Q, Qd, ub, ubd, u_stack, taped, (int)n, nrun, c, pbwd, &nparts, stream);
+            if (rc) return rc;
         }
         STADE_TIMED("finalize", stream,
                     bwd_finalize_kernel<true><<<2, FNT, 0, stream>>>(ws->partials, gi, SumOuts{{loss, lossd}}, pbwd, nparts,
@@ -864,6 +874,118 @@ int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* 
     *dxb = xb_;
     *dxbd = xbd_;
     return STADE_HIP_OK;
+}
+
+}  // namespace
+}  // namespace stade
+
+extern "C" {
+
+int32_t stade_hip_burgers1d_stack_lengths(int64_t n, int64_t nsteps, int64_t lengths[2]) {
+    // initstacks_burgers1d_b: branch_stack max(0, div(nsteps - 1, 1) + 1),
+    // u_stack max(0, div(nsteps - 1, 1) + 1) * max(0, div(n - 1, 1) + 1)   (Julia div truncates)
+    if (!lengths) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_stack_lengths: null lengths");
+    int64_t a = (nsteps - 1) / 1 + 1, b = (n - 1) / 1 + 1;
+    a = a > 0 ? a : 0;
+    b = b > 0 ? b : 0;
+    lengths[0] = a;
+    lengths[1] = a * b;
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_initstacks_burgers1d_b(int64_t n, int64_t nsteps, int64_t** branch_stack, double** u_stack) {
+    int64_t len[2];
+    if (int32_t rc = stade_hip_burgers1d_stack_lengths(n, nsteps, len)) return rc;
+    if (!branch_stack || !u_stack) return set_error(STADE_HIP_EINVAL, "stade_hip_initstacks_burgers1d_b: null output");
+    *branch_stack = nullptr;
+    *u_stack = nullptr;
+    STADE_TRY_HIP(hipMalloc((void**)branch_stack, (size_t)(len[0] > 0 ? len[0] : 1) * sizeof(int64_t)));
+    hipError_t e = hipMalloc((void**)u_stack, (size_t)(len[1] > 0 ? len[1] : 1) * sizeof(double));
+    if (e != hipSuccess) {
+        (void)hipFree(*branch_stack);  // the allocation error is the one reported
+        *branch_stack = nullptr;
+        return check_hip(e, "hipMalloc(u_stack)");
+    }
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_burgers1d_b(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                              double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
+                              int64_t n, int64_t nsteps, int64_t* branch_stack, double* u_stack, hipStream_t stream) {
+    return adjoint_impl<false>("stade_hip_burgers1d_b", 1, loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, tendb, n,
+                               nsteps, branch_stack, u_stack, stream);
+}
+
+int32_t stade_hip_burgers1d_ckpt_lengths(int64_t n, int64_t nsteps, int64_t every, int64_t lengths[2]) {
+    if (!lengths) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_ckpt_lengths: null lengths");
+    if (every < 1 || every > (1 << 20)) return set_error(STADE_HIP_ERANGE, "stade_hip_burgers1d_ckpt_lengths: every = %lld out of range", (long long)every);
+    const int64_t a = nsteps > 0 ? nsteps : 0, b = n > 0 ? n : 0;
+    lengths[0] = a;
+    lengths[1] = (a + every - 1) / every * b;
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_burgers1d_b_ckpt(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                                   double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend,
+                                   double* tendb, int64_t n, int64_t nsteps, int64_t* branch_stack, double* u_ckpt, int64_t every,
+                                   hipStream_t stream) {
+    if (every < 1 || every > (1 << 20)) return set_error(STADE_HIP_ERANGE, "stade_hip_burgers1d_b_ckpt: every = %lld out of range", (long long)every);
+    return adjoint_impl<true>("stade_hip_burgers1d_b_ckpt", every, loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend,
+                              tendb, n, nsteps, branch_stack, u_ckpt, stream);
+}
+
+int32_t stade_hip_burgers1d_d(double* loss, double* lossd, double* u, double* ud, double* un, double* und, double nu, double nud,
+                              double dt, double dtd, double dx, double dxd, double tend, double tendd, int64_t n, int64_t nsteps,
+                              hipStream_t stream) {
+    (void)tendd;
+    if (int32_t rc = check(n, nsteps, "stade_hip_burgers1d_d")) return rc;
+    if (n == 0) return STADE_HIP_OK;
+    if (!loss || !lossd || !u || !ud || !un || !und) return set_error(STADE_HIP_EINVAL, "stade_hip_burgers1d_d: null pointer");
+    const double c0 = dx * dx;
+    Coef c{0.5 * dt / dx, nu * dt / c0, (0.5 * dtd) / dx + -((0.5 * dt) / (dx * dx)) * dxd,
+           (dt * nud + nu * dtd) / c0 + -((nu * dt) / (c0 * c0)) * (dx * dxd + dx * dxd)};
+    const int64_t nrun = taken_steps(dt, tend, nsteps);
+    WsCall call_(stream);
+    Workspace* ws = call_.ws;
+    if (!ws) return STADE_HIP_ENOMEM;
+    double* P = (double*)scratch(sizeof(double) * 4 * (size_t)n);
+    if (!P) return STADE_HIP_ENOMEM;
+    double *Q = P + n, *Pd = Q + n, *Qd = Pd + n;
+    if (nrun > 0) {
+        if (int32_t rc = forward<true>(u, ud, un, und, nullptr, nullptr, (int)n, 0, nrun, c, P, Q, Pd, Qd, stream)) return rc;
+        STADE_TIMED("burgers1d_copy", stream, copy2_kernel<<<grid_for((int)n, NT * 8), NT, 0, stream>>>(un, u, und, ud, (int)n));
+        STADE_LAUNCHED("burgers1d copy2_kernel");
+    }
+    // loss and lossd from the final state, now in u and ud
+    const int gl = init_blocks(n);
+    STADE_TIMED("burgers1d_loss", stream, loss2_kernel<<<gl, NT, 0, stream>>>(u, ud, (int)n, ws->partials));
+    STADE_LAUNCHED("burgers1d loss2_kernel");
+    STADE_TIMED("finalize", stream, finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, gl, SumOuts{{loss, lossd}}));
+    STADE_LAUNCHED("burgers1d finalize_kernel");
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_burgers1d_hv(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                               double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
+                               int64_t n, int64_t nsteps, double* lossd, const double* lossbd, const double* ud, double* ubd,
+                               double* und, double* unbd, double nud, double* nubd, double dtd, double* dtbd, double dxd,
+                               double* dxbd, double tendd, double* tendbd, int64_t* branch_stack, double* u_stack,
+                               hipStream_t stream) {
+    return hvp_impl<false>("stade_hip_burgers1d_hv", 1, loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, tendb, n, nsteps,
+                           lossd, lossbd, ud, ubd, und, unbd, nud, nubd, dtd, dtbd, dxd, dxbd, tendd, tendbd, branch_stack, u_stack,
+                           stream);
+}
+
+int32_t stade_hip_burgers1d_hv_ckpt(double* loss, const double* lossb, const double* u, double* ub, double* un, double* unb,
+                                    double nu, double* nub, double dt, double* dtb, double dx, double* dxb, double tend, double* tendb,
+                                    int64_t n, int64_t nsteps, double* lossd, const double* lossbd, const double* ud, double* ubd,
+                                    double* und, double* unbd, double nud, double* nubd, double dtd, double* dtbd, double dxd,
+                                    double* dxbd, double tendd, double* tendbd, int64_t* branch_stack, double* u_ckpt, int64_t every,
+                                    hipStream_t stream) {
+    if (every < 1 || every > (1 << 20)) return set_error(STADE_HIP_ERANGE, "stade_hip_burgers1d_hv_ckpt: every = %lld out of range", (long long)every);
+    return hvp_impl<true>("stade_hip_burgers1d_hv_ckpt", every, loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, tendb, n,
+                          nsteps, lossd, lossbd, ud, ubd, und, unbd, nud, nubd, dtd, dtbd, dxd, dxbd, tendd, tendbd, branch_stack,
+                          u_ckpt, stream);
 }
 
 }  // extern "C"

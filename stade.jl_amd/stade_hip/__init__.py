@@ -27,6 +27,7 @@ from .api import (  # noqa: F401
     affine_lsq_b, affine_lsq_d, affine_lsq_hv,
     diffusion2d_b, diffusion2d_d, diffusion2d_hv,
     burgers1d_b, burgers1d_d, burgers1d_hv, initstacks_burgers1d_b, burgers1d_stack_lengths,
+    burgers1d_b_ckpt, burgers1d_hv_ckpt, burgers1d_ckpt_lengths,
     mlp2_ce_b, mlp2_ce_d, mlp2_ce_hv,
     conv3x3_b, conv3x3_d, conv3x3_hv,
     rng_normal, rng_uniform, rng_int_range, stable_seed,

@@ -49,6 +49,8 @@ ENTRY_POINTS: dict[str, str] = {
     "stade_hip_burgers1d_b": "aaaaaa" + "frfrfrfr" + "ii" + "aa",
     "stade_hip_burgers1d_d": "aaaaaa" + "ffffffff" + "ii",
     "stade_hip_burgers1d_hv": "aaaaaa" + "frfrfrfr" + "ii" + "aaaaaa" + "frfrfrfr" + "aa",
+    "stade_hip_burgers1d_b_ckpt": "aaaaaa" + "frfrfrfr" + "ii" + "aa" + "i",
+    "stade_hip_burgers1d_hv_ckpt": "aaaaaa" + "frfrfrfr" + "ii" + "aaaaaa" + "frfrfrfr" + "aa" + "i",
     "stade_hip_mlp2_ce_b": "a" * 17 + "iiii",
     "stade_hip_mlp2_ce_d": "a" * 17 + "iiii",
     "stade_hip_mlp2_ce_hv": "a" * 17 + "iiii" + "a" * 16,
@@ -361,6 +363,59 @@ def burgers1d_hv(loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, t
          float(tendd), ctypes.byref(rd[3]),
          _arr("branch_stack", branch_stack, torch.int64, lb), _arr("u_stack", u_stack, d, lu)]
     _call("stade_hip_burgers1d_hv", a, _stream_of(u))
+    return (rs[0].value, rd[0].value, rs[1].value, rd[1].value, rs[2].value, rd[2].value, rs[3].value, rd[3].value)
+
+
+def burgers1d_ckpt_lengths(n: int, nsteps: int, every: int) -> tuple[int, int]:
+    """Lengths of (branch_stack, u_ckpt) under the checkpoint policy (every `every`-th state)."""
+    L = lib()
+    out = (ctypes.c_int64 * 2)()
+    L.stade_hip_burgers1d_ckpt_lengths.argtypes = [I64, I64, I64, ctypes.POINTER(ctypes.c_int64)]
+    _check("stade_hip_burgers1d_ckpt_lengths",
+           L.stade_hip_burgers1d_ckpt_lengths(_int("n", n), _int("nsteps", nsteps), _int("every", every), out))
+    return int(out[0]), int(out[1])
+
+
+def burgers1d_b_ckpt(loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, tendb, n, nsteps, branch_stack, u_ckpt,
+                     every):
+    """burgers1d_b under the checkpoint tape policy: u_ckpt (every `every`-th state) instead of
+    u_stack, the segments recomputed in the reverse sweep; the other outputs are burgers1d_b's.
+    Returns (nub, dtb, dxb, tendb)."""
+    import torch
+    n, T, every = _int("n", n), _int("nsteps", nsteps), _int("every", every)
+    lb, lc = burgers1d_ckpt_lengths(n, T, every)
+    d = _f64()
+    rs = [_r(v) for v in (nub, dtb, dxb, tendb)]
+    a = [_arr("loss", loss, d, 1), _arr("lossb", lossb, d, 1), _arr("u", u, d, n), _arr("ub", ub, d, n),
+         _arr("un", un, d, n), _arr("unb", unb, d, n),
+         float(nu), ctypes.byref(rs[0]), float(dt), ctypes.byref(rs[1]), float(dx), ctypes.byref(rs[2]),
+         float(tend), ctypes.byref(rs[3]), n, T,
+         _arr("branch_stack", branch_stack, torch.int64, lb), _arr("u_ckpt", u_ckpt, d, lc), every]
+    _call("stade_hip_burgers1d_b_ckpt", a, _stream_of(u))
+    return tuple(r.value for r in rs)
+
+
+def burgers1d_hv_ckpt(loss, lossb, u, ub, un, unb, nu, nub, dt, dtb, dx, dxb, tend, tendb, n, nsteps,
+                      lossd, lossbd, ud, ubd, und, unbd, nud, nubd, dtd, dtbd, dxd, dxbd, tendd, tendbd,
+                      branch_stack, u_ckpt, every):
+    """burgers1d_hv under the checkpoint tape policy (see burgers1d_b_ckpt).  Returns (nub, nubd,
+    dtb, dtbd, dxb, dxbd, tendb, tendbd)."""
+    import torch
+    n, T, every = _int("n", n), _int("nsteps", nsteps), _int("every", every)
+    lb, lc = burgers1d_ckpt_lengths(n, T, every)
+    d = _f64()
+    rs = [_r(v) for v in (nub, dtb, dxb, tendb)]
+    rd = [_r(v) for v in (nubd, dtbd, dxbd, tendbd)]
+    a = [_arr("loss", loss, d, 1), _arr("lossb", lossb, d, 1), _arr("u", u, d, n), _arr("ub", ub, d, n),
+         _arr("un", un, d, n), _arr("unb", unb, d, n),
+         float(nu), ctypes.byref(rs[0]), float(dt), ctypes.byref(rs[1]), float(dx), ctypes.byref(rs[2]),
+         float(tend), ctypes.byref(rs[3]), n, T,
+         _arr("lossd", lossd, d, 1), _arr("lossbd", lossbd, d, 1), _arr("ud", ud, d, n), _arr("ubd", ubd, d, n),
+         _arr("und", und, d, n), _arr("unbd", unbd, d, n),
+         float(nud), ctypes.byref(rd[0]), float(dtd), ctypes.byref(rd[1]), float(dxd), ctypes.byref(rd[2]),
+         float(tendd), ctypes.byref(rd[3]),
+         _arr("branch_stack", branch_stack, torch.int64, lb), _arr("u_ckpt", u_ckpt, d, lc), every]
+    _call("stade_hip_burgers1d_hv_ckpt", a, _stream_of(u))
     return (rs[0].value, rd[0].value, rs[1].value, rd[1].value, rs[2].value, rd[2].value, rs[3].value, rd[3].value)
 
 
