@@ -597,3 +597,70 @@ def classify(loop: For, types: Types, later_reads: set, frame_written_outside: s
     reads_all |= bound_reads
     frame_reads = {n for n in reads_all if n not in types.arrays and n != v and n not in inner_vars}
     return ParallelLoop(loop, private, reset, reductions, arrays, guards, live_out, frame_reads), ""
+
+
+# ------------------------------------------------------------------------------------------
+# narrow outputs: lanes that share one iteration's inner loop
+# ------------------------------------------------------------------------------------------
+
+def split_loops(pl: ParallelLoop, types: Types) -> dict:
+    """The inner loops of a parallel loop's body that the lanes of a wave can share when the
+    loop has few iterations and long inner loops (the narrow-output twin, `cgen_split_*`
+    /root/reference/src/STADE.jl:13155-13200, redone for 64-lane waves).
+
+    Returns {id(inner For): [sum targets]} for the direct children of the body that qualify:
+    every scalar the inner body assigns is either a sum target (only `s = s + e` / `s = e + s`
+    / `s = s - e` updates of a scalar declared outside, combined across lanes after the loop)
+    or local to an inner iteration (defined before it is read, not read after the loop, not
+    carried to the next outer iteration); the inner body writes only accumulate-only arrays
+    (order-free, so lanes add atomically); no break or return.  Empty when the body reads an
+    element of an array after a statement that stores into that array (the stores are made
+    by one lane of the wave; the other lanes would not see them)."""
+    body = pl.loop.body
+    owned = {n for n, u in pl.arrays.items() if u.kind == "owned"}
+    written = set()
+    for s in walk_stmts(body):     # statements in program order (owned stores are never in inner loops)
+        for e in stmt_exprs(s):
+            if any(isinstance(x, Ref) and x.name in written for x in walk_expr(e)):
+                return {}
+        if isinstance(s, Assign) and isinstance(s.lhs, Ref) and s.lhs.name in owned:
+            written.add(s.lhs.name)
+    out = {}
+    for k, L in enumerate(body):
+        if not isinstance(L, For):
+            continue
+        if any(isinstance(t, (Break, Return)) for t in walk_stmts(L.body)):
+            continue
+        inner_vars = {t.var for t in walk_stmts(L.body) if isinstance(t, For)} | {L.var}
+        assigned = _assigned(L.body) - inner_vars
+        after_reads = set()
+        for t in body[k + 1:]:
+            for e in stmt_exprs(t):
+                after_reads |= _reads_of(e)
+            for u in walk_stmts([t]):
+                for e in stmt_exprs(u):
+                    after_reads |= _reads_of(e)
+        targets, ok = [], True
+        for name in sorted(assigned):
+            occ = [t for t in walk_stmts(L.body) if any(name in _reads_of(e) for e in stmt_exprs(t))
+                   or (isinstance(t, Assign) and isinstance(t.lhs, Var) and t.lhs.name == name)]
+            if occ and all(_is_sum_update(t, name) for t in occ) and types.scalars.get(name) in ("f", "i"):
+                if name in pl.reductions:
+                    continue          # the parallel loop's own sum: per-lane partials already
+                targets.append(name)
+                continue
+            if (_upward_exposed(L.body, name) or name in after_reads or name in pl.reset or name in pl.live_out
+                    or name in pl.reductions):
+                ok = False
+                break
+        if not ok:
+            continue
+        for t in walk_stmts(L.body):
+            if isinstance(t, Assign) and isinstance(t.lhs, Ref):
+                u = pl.arrays.get(t.lhs.name)
+                if u is None or u.kind != "atomic":
+                    ok = False
+                    break
+        if ok:
+            out[id(L)] = targets
+    return out

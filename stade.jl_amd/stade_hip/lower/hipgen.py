@@ -27,13 +27,17 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
-from .analysis import ArrayUse, ParallelLoop, Types, classify, infer_types, _reads_of, _thaw
+from .analysis import ArrayUse, ParallelLoop, Types, classify, infer_types, split_loops, _reads_of, _thaw
 from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, If, LowerError, Nothing_, Num, Range,
                      Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
 MAX_BLOCKS = 8192          # grid of a parallel loop whose trip count the host cannot evaluate
 PRIV_MAX_BYTES = 48 * 1024  # LDS-privatised accumulation target, at most
 PRIV_RATIO = 32            # and at least this many iterations per target element
+SPLIT_MAX_TRIP = 16384     # a parallel loop with at most this many iterations (64 blocks of 256 threads)
+SPLIT_MIN_INNER = 256      # whose shared inner loop runs at least this many iterations (when the host
+SPLIT_MAX_TRIP_UNKNOWN = 4096  # can evaluate it; otherwise at most this many outer iterations) gives
+                               # each iteration a wave
 
 
 def cname(n: str) -> str:
@@ -56,6 +60,7 @@ class ParOp:
     pl: ParallelLoop
     pred: tuple
     kid: int = 0
+    types: Types | None = None
 
 
 @dataclass
@@ -221,7 +226,7 @@ class FuncLower:
                 pl, why = classify(s, self.T, self._reads_outside(s), set())
                 if pl is not None:
                     flush()
-                    ops.append(ParOp(pl, pred))
+                    ops.append(ParOp(pl, pred, types=self.T))
                     continue
                 self.reasons.append(f"loop over {s.var}: {why}")
                 if self.contains_parallel(s.body, hl) and self.host_ok(s.rng, hl) and not any(
@@ -469,6 +474,15 @@ class Emitter:
         self.ind = 1
         self.loop_labels = []
         self.nlabel = 0
+        # the split form (a wave per iteration): inner loops shared by the lanes, their sum
+        # targets' per-lane partials, and stores made by lane 0 outside those loops
+        self.split_loops: dict = {}
+        self.partials: dict = {}
+        self.lane0 = False
+        self.in_split = 0
+
+    def one_lane(self) -> bool:
+        return self.lane0 and not self.in_split
 
     def emit(self, s):
         self.lines.append("    " * self.ind + s)
@@ -482,14 +496,19 @@ class Emitter:
         if isinstance(s, Assign):
             if isinstance(s.lhs, Var):
                 n = s.lhs.name
-                if n in ctx.reductions and isinstance(s.rhs, Bin):
+                acc_name = self.partials.get(n) if self.in_split else None
+                if acc_name is None and n in ctx.reductions:
+                    acc_name = ctx.reductions[n]
+                if acc_name is not None and isinstance(s.rhs, Bin):
                     r = s.rhs
                     if isinstance(r.a, Var) and r.a.name == n:
                         c, _ = fl.ex(r.b, ctx)
-                        self.emit(f"{ctx.reductions[n]} {'+' if r.op == '+' else '-'}= {c};")
+                        line = f"{acc_name} {'+' if r.op == '+' else '-'}= {c};"
                     else:
                         c, _ = fl.ex(r.a, ctx)
-                        self.emit(f"{ctx.reductions[n]} += {c};")
+                        line = f"{acc_name} += {c};"
+                    # (a sum of the parallel loop outside the shared inner loops: lane 0's)
+                    self.emit(f"if (_lane == 0) {{ {line} }}" if self.one_lane() and n in ctx.reductions else line)
                     return
                 c, _ = fl.ex(s.rhs, ctx)
                 self.emit(f"{ctx.var(n)} = ({fl.cty(fl.scalars.get(n, 'f'))})({c});")
@@ -504,14 +523,18 @@ class Emitter:
                 c, _ = fl.ex(other, ctx)
                 val = f"({et})({c})" if sign == "+" else f"(-({et})({c}))"
                 nm = cname(ref.name)
-                self.emit(f"{{ const int64_t _i = {ctx.lin(ref)};")
+                self.emit(("if (_lane == 0) " if self.one_lane() else "") + f"{{ const int64_t _i = {ctx.lin(ref)};")
                 if ctx.lds == ref.name:
                     self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::lds_add(&lds_priv[_i], {val}); else oob(); }}")
                 else:
                     self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::wave_add(&a.A_{nm}[_i], {val}); else oob(); }}")
                 return
             c, _ = fl.ex(s.rhs, ctx)
-            self.emit(f"wr(a.A_{cname(ref.name)}, {ctx.lin(ref)}, a.N_{cname(ref.name)}, ({et})({c}));")
+            self.emit(("if (_lane == 0) " if self.one_lane() else "") +
+                      f"wr(a.A_{cname(ref.name)}, {ctx.lin(ref)}, a.N_{cname(ref.name)}, ({et})({c}));")
+            return
+        if isinstance(s, For) and id(s) in self.split_loops:
+            self.split_for(s)
             return
         if isinstance(s, For):
             lo, _ = fl.ex(s.rng.lo, ctx)
@@ -584,6 +607,50 @@ class Emitter:
             self.emit("goto _fn_end;")
             return
         raise LowerError(f"{fl.f.name}: cannot lower statement {s!r}")
+
+    def split_for(self, s: For):
+        """An inner loop shared by the lanes of the wave: lane l runs iterations l, l + 64, ...;
+        each sum target gets a per-lane partial, added to the target (the same value in every
+        lane) after the loop.  The last bits of such a sum differ from the loop in order."""
+        fl, ctx = self.fl, self.ctx
+        lo, _ = fl.ex(s.rng.lo, ctx)
+        hi, _ = fl.ex(s.rng.hi, ctx)
+        st = "1" if s.rng.step is None else fl.ex(s.rng.step, ctx)[0]
+        v = f"l_{cname(s.var)}"
+        saved = ctx.locals.get(s.var)
+        k = self.nlabel
+        self.nlabel += 1
+        targets = self.split_loops[id(s)]
+        self.emit("{")
+        self.ind += 1
+        saved_partials = dict(self.partials)
+        for t in targets:
+            pn = f"p{k}_{cname(t)}"
+            self.emit(f"{fl.cty(fl.scalars[t])} {pn} = 0;")
+            self.partials[t] = pn
+        self.emit(f"const int64_t _lo{k} = {lo}, _st{k} = {st}, _n{k} = stade_lowered::jl_trip(_lo{k}, _st{k}, {hi});")
+        self.emit(f"for (int64_t _k{k} = _lane; _k{k} < _n{k}; _k{k} += 64) {{")
+        self.ind += 1
+        self.emit(f"const int64_t {v} = _lo{k} + _k{k} * _st{k};")
+        ctx.locals[s.var] = v
+        self.loop_labels.append(k)
+        self.in_split += 1
+        self.block(s.body)
+        self.in_split -= 1
+        self.loop_labels.pop()
+        self.emit(f"_cont{self.u}_{k}:;")
+        self.ind -= 1
+        self.emit("}")
+        self.emit(f"_brk{self.u}_{k}:;")
+        for t in targets:
+            self.emit(f"{ctx.var(t)} = {ctx.var(t)} + stade_lowered::wave_sum({self.partials[t]});")
+        self.partials = saved_partials
+        self.ind -= 1
+        self.emit("}")
+        if saved is None:
+            ctx.locals.pop(s.var, None)
+        else:
+            ctx.locals[s.var] = saved
 
     def ret(self, value):
         fl = self.fl
@@ -686,10 +753,15 @@ class FuncGen:
         locals_ = {n: f"x_{cname(n)}" for n in priv + inv}
         locals_[v] = f"l_{cname(v)}"
 
-        def body_lines(parallel: bool, lds: str | None) -> list[str]:
+        split = split_loops(pl, fl.T)
+
+        def body_lines(parallel: bool, lds: str | None, wave: bool = False) -> list[str]:
             ctx = Ctx(fl, dict(locals_), hl, acc={n: "atomic" for n in atomic}, serial_acc=not parallel,
                       reductions=reds, lds=lds)
             em = Emitter(fl, ctx)
+            if wave:
+                em.split_loops = split
+                em.lane0 = True
             em.ind = 3
             em.emit(f"const int64_t l_{cname(v)} = _lo + _k * _st;")
             for n in priv:
@@ -771,6 +843,29 @@ class FuncGen:
         pre = "    extern __shared__ __align__(16) unsigned char lds_raw[];\n    (void)lds_raw;\n" if cands else ""
         self.kern.append(f"template <int PRIV>\n__global__ __launch_bounds__(256) void k{k}(const Args a) {{\n" + pre +
                          "\n".join(out) + "\n}\n")
+        if split:
+            # the narrow-output form: a wave per iteration, its lanes sharing the inner loops
+            sp = list(head)
+            sp.append(f"    if (!({guards})) {{")
+            sp.append("        if (blockIdx.x != 0 || threadIdx.x != 0) return;")
+            sp += ["    " + x for x in red_decl]
+            sp.append("        for (int64_t _k = 0; _k < _trip; ++_k) {")
+            sp += body_lines(False, None)
+            sp.append("        }")
+            for n, r in reds.items():
+                sp.append(f"        fr.v_{cname(n)} += {r};")
+            sp.append("        return;")
+            sp.append("    }")
+            sp += red_decl
+            sp.append("    const int _lane = threadIdx.x & 63;")
+            sp.append("    for (int64_t _k = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; _k < _trip;"
+                      " _k += ((int64_t)gridDim.x * blockDim.x) >> 6) {")
+            sp += body_lines(True, None, wave=True)
+            sp.append("    }")
+            for n, r in reds.items():
+                sp.append(f"    {r} = stade_lowered::wave_sum({r});")
+                sp.append(f"    if ((threadIdx.x & 63) == 0 && {r} != 0) stade_lowered::atomic_add(&fr.v_{cname(n)}, {r});")
+            self.kern.append(f"__global__ __launch_bounds__(256) void k{k}s(const Args a) {{\n" + "\n".join(sp) + "\n}\n")
         # host: grid from the trip count when the host can evaluate it
         if fl.host_ok(loop.rng, set(hl)):
             hctx = HostCtx(fl, self.hlv)
@@ -779,6 +874,21 @@ class FuncGen:
             self.hemit("{")
             self.hind += 1
             self.hemit(f"const int64_t _trip = stade_lowered::jl_trip({hlo}, {hst}, {hhi});")
+            if split:
+                # few iterations with long inner loops: a wave per iteration
+                first = next(t for t in walk_stmts(loop.body) if isinstance(t, For) and id(t) in split)
+                if fl.host_ok(first.rng, set(hl)):
+                    ilo, ihi = hctx.ex(first.rng.lo), hctx.ex(first.rng.hi)
+                    ist = "1" if first.rng.step is None else hctx.ex(first.rng.step)
+                    cond = (f"_trip > 0 && _trip <= {SPLIT_MAX_TRIP} && "
+                            f"stade_lowered::jl_trip({ilo}, {ist}, {ihi}) >= {SPLIT_MIN_INNER}")
+                else:
+                    cond = f"_trip > 0 && _trip <= {SPLIT_MAX_TRIP_UNKNOWN}"
+                self.hemit(f"if ({cond}) {{")
+                self.hind += 1
+                self.launch(f"k{k}s", f"(unsigned)std::min<int64_t>((_trip + 3) / 4, {MAX_BLOCKS})", "256", "0")
+                self.hind -= 1
+                self.hemit("} else")
             self.hemit("if (_trip > 0) {")
             self.hind += 1
             self.hemit(f"const unsigned _g = (unsigned)std::min<int64_t>((_trip + 255) / 256, {MAX_BLOCKS});")
@@ -1138,8 +1248,10 @@ def describe(ops, depth=0) -> list[str]:
         elif isinstance(op, ParOp):
             pl = op.pl
             kinds = ", ".join(f"{n}:{u.kind}" for n, u in sorted(pl.arrays.items()))
+            nsplit = len(split_loops(pl, op.types)) if getattr(op, "types", None) is not None else 0
             out.append(pad + f"parallel over {pl.loop.var} [{kinds}]"
-                       + (f" sums {sorted(pl.reductions)}" if pl.reductions else ""))
+                       + (f" sums {sorted(pl.reductions)}" if pl.reductions else "")
+                       + (f"; with few iterations a wave each, lanes sharing {nsplit} inner loop(s)" if nsplit else ""))
         elif isinstance(op, HostLoopOp):
             out.append(pad + f"host loop over {op.loop.var}")
             out += describe(op.ops, depth + 1)

@@ -148,3 +148,31 @@ def test_lowered_conv3x3(mode, size):
     case, low = _case(CORPUS / f"conv3x3_{mode}.jl", "conv3x3", mode, shapes, dict(i_nb=N, i_c=C, i_k=K, i_h=H, i_w=W),
                       precision="f32", scales={"w": s, "wd": s})
     _check(case, low, f"conv3x3_{mode}")
+
+
+# ---- narrow outputs: few iterations with long inner loops (a wave per iteration) ---------
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("nk", [(20000, 19990), (60000, 59000), (3000, 2700)])
+def test_lowered_window1d_narrow(mode, nk):
+    """11, 1001 and 301 outputs of 19990-, 59000- and 2700-tap correlations: the lanes of a wave
+    share each output's tap loop (the sum's order changes, within the fp64 bar)."""
+    n, k = nk
+    nout = n - k + 1
+    shapes = {a + s: v for a, v in dict(loss=1, inp=n, w=k, out=nout).items() for s in ("", "b", "d", "bd")}
+    case, low = _case(GENERIC / f"window1d_{mode}.jl", "window1d", mode, shapes, dict(i_n=n, i_k=k))
+    _check(case, low, f"window1d_{mode}")
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("mn", [(4, 200000), (16, 50000), (100, 5000)])
+def test_lowered_affine_lsq_narrow(mode, mn):
+    """Few rows and long rows: the row sums, and the adjoint's row loop with its accumulations
+    into wb and xb, shared by the lanes of a wave."""
+    m, n = mn
+    shapes = {k: (m, n) for k in ("w", "wb", "wd", "wbd")}
+    shapes.update({k: n for k in ("x", "xb", "xd", "xbd")})
+    shapes.update({k: m for k in ("b", "bb", "bd", "bbd", "t", "tb", "td", "tbd", "r", "rb", "rd", "rbd")})
+    shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
+    case, low = _case(CORPUS / f"affine_lsq_{mode}.jl", "affine_lsq", mode, shapes, dict(i_m=m, i_n=n))
+    _check(case, low, f"affine_lsq_{mode}")
