@@ -124,17 +124,19 @@ class Workload:
         from oracle import runner
         wl, share = self.sample()
         prec = "f32" if self.dtype == "f32" else "f64"
-        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"{self.name}.jl", precision=prec, bounds_check=False)
+        # the sample runs the generated text of its own function (a policy variant such as the
+        # checkpointed Burgers adjoint samples the tape form's text: the same CPU code)
+        lib = runner.load(ROOT / "stade.jl_amd" / "corpus" / f"{wl.name}.jl", precision=prec, bounds_check=False)
         h = wl.host_inputs()
-        names = arg_names(self.family, self.mode)
-        nst = len(wl.stack_lengths()) if self.mode != "d" else 0
+        names = arg_names(wl.family, wl.mode)
+        nst = len(wl.stack_lengths()) if wl.mode != "d" else 0
         fdt = np.float64 if prec == "f64" else np.float32
 
         def run():
             argv = [h[a].copy(order="K") if isinstance(h[a], np.ndarray) else h[a] for a in names[:len(names) - nst]]
             if nst:
                 argv += [np.empty(k, dtype=np.int64 if kind == "Ai" else fdt) for k, kind in wl.stack_lengths()]
-            lib.call(self.name, *argv)
+            lib.call(wl.name, *argv)
         desc = wl.sample_desc()
         if share != 1.0:
             desc += f" ({1 / share:.0f}x less work than one benchmark evaluation; the rate is scaled by that share)"
