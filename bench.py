@@ -247,6 +247,12 @@ class Burgers(Workload):
         super().__init__(mode)
         self.n, self.T = n, nsteps
         self.kernel = {"b": "burgers1d_bwd", "d": "burgers1d_fwd_tan", "hv": "burgers1d_bwd_hv"}[mode]
+        if mode == "d":
+            # no tape: the tangent is bound by its fp64 arithmetic (the state stays in LDS for 32
+            # steps a launch).  Algorithmic flops: the text's 26 operations per cell and step
+            # (__cse_1 1, __cse_2 3, und 17, un 5), averaged over the launches
+            self.bound = "valu"
+            self.kernels = {self.kernel: self.TAN_FLOPS * n * nsteps / max(1, self._launches())}
         self.nu = 1e-3
         self.dx = 1.0 / n if dx is None else dx
         self.dt = 0.2 * self.dx * self.dx / self.nu
@@ -269,8 +275,13 @@ class Burgers(Workload):
     def stack_lengths(self):
         return [(self.T, "Ai"), (self.T * self.n, "Af")]
 
+    TAN_FLOPS = 26   # fp64 operations per cell and step of burgers1d_d as written
+
     def _launches(self):
         return -(-self.T // 32)
+
+    def eval_flops(self):
+        return self.TAN_FLOPS * self.n * self.T
 
     def algo_bytes(self):
         n, T = self.n, self.T
@@ -616,13 +627,13 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
         else:
             peak = FP32_PEAK_TFLOPS if wl.dtype == "f32" else FP64_PEAK_TFLOPS
             ach = wl.kernels[wl.kernel] / (k_ms * 1e-3) / 1e12
-            out["roofline"] = {"bound": "mfma", "achieved": ach, "peak": peak, "unit": "TFLOP/s",
+            out["roofline"] = {"bound": wl.bound, "achieved": ach, "peak": peak, "unit": "TFLOP/s",
                                "frac": ach / peak, "traffic": None}
     if per_kernel:
         out["kernels"] = per_kernel
-    if wl.bound == "mfma":
+    if wl.bound in ("mfma", "valu"):
         out["eval_TFLOPs"] = wl.eval_flops() / (ms_step * 1e-3) / 1e12
-        out["eval_mfma_frac"] = out["eval_TFLOPs"] / FP32_PEAK_TFLOPS
+        out[f"eval_{wl.bound}_frac"] = out["eval_TFLOPs"] / (FP32_PEAK_TFLOPS if wl.dtype == "f32" else FP64_PEAK_TFLOPS)
     if wl.bound == "hbm" and wl.algo_bytes():
         out["eval_GBps"] = wl.algo_bytes() / (ms_step * 1e-3) / 1e9
         out["eval_hbm_frac"] = out["eval_GBps"] / HBM_PEAK_GBS
@@ -769,6 +780,7 @@ def main():
         "cpu_baseline": cpu,
         "eval_hbm_frac": res.get("eval_hbm_frac"),
         "eval_mfma_frac": res.get("eval_mfma_frac"),
+        "kernel": res.get("kernel"),
         "kernel_ms": res.get("kernel_ms"),
         "kernels": res.get("kernels"),
         "kernel_timing": "HIP event pair around each launch of the dominant kernel on its own stream, over a second "
