@@ -688,6 +688,9 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--only", action="store_true", help="measure the headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", type=int, default=None,
+                    help="issue the measured workload's timed steps as replays of a captured HIP graph of this many "
+                         "steps (0: eager launches; default: the workload's own choice)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a device-to-device copy of 1 GiB, 10 times (the reference kernel that scales "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -748,6 +751,8 @@ def main():
                           "frac_of_8TBps": round(40 * n / us / 1e6 / 8.0, 3)}))
         return
     head = WORKLOADS[args.workload]()
+    if args.graph is not None:
+        head.graph_steps = args.graph
     res = measure(head, args.steps, args.warmup, dev)
     others = {}
     if not args.only:

@@ -14,10 +14,11 @@
 //   head (per sample)    z = W2 h1 + b2, CE, d2 = dloss/dz, zb reset,
 //                        d1 = (1 - h1^2) (h1b + W2' d2), h1b reset    (one wave per sample)
 //   colsum               W2b += d2 h1', b1b += sum_s d1, b2b         (deterministic partials)
-//   W1b += d1 X'                                                       (H x I, K = B)
-//   Xb  += W1' d1                                                      (I x B, K = H)
-// The tangent adds S1d = W1d X + W1 Xd (one two-segment GEMM, epilogue h1d = (1 - h1^2)(S1d +
-// b1d)); the HVP adds the tangents of every backward product as two-segment GEMMs.
+//   W1b += d1 X'  and  Xb += W1' d1                                    (one paired launch:
+//                        H x I with K = B, I x B with K = H; the final sums ride along)
+// The adjoint (i_h <= 1024) forms head and column sums in one pass over h1 (headd1_kernel);
+// the tangent adds S1d = W1d X + W1 Xd (one dual GEMM, epilogue h1d = (1 - h1^2)(S1d + b1d));
+// the HVP adds the tangents of every backward product in dual launches.
 #include "internal.hpp"
 
 #include <algorithm>
@@ -554,13 +555,23 @@ __global__ __launch_bounds__(h4nt<MODE>()) void head4_kernel(HeadArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// second half of the split head fused with the column sums (i_h <= 1024): per chunk of SC
-// samples and 64 columns j,
-//   d1 = (1 - h1^2) (h1b + sum_o w2[o, j] d2[o]) (o descending, as the generated loop), h1b = 0
-//   (HVP: d1d, h1bd = 0), and the chunk partials of W2b += d2 h1', b1b += sum_s d1 (+ W2bd,
-//   b1bd) and of b2b (+ b2bd), in colsum_kernel's layout and summation order.
-// A thread owns column j (its W2 column in registers) and the samples s0 + sl + 4 k.
+// The adjoint's whole head in one pass over h1 (i_h <= 1024): a block of HDB = 16 waves
+// takes 16 consecutive samples.
+//  A. Wave w, sample s0 + w: lane l loads h1 of its columns j = l + 64 q; W2 is staged in LDS
+//     as rows [j][opl] (opl = i_out rounded up to odd: conflict-free row reads; zero past i_out
+//     and i_h).  z = b2 + W2 h1: the lane's 16 output partial sums are reduced across the
+//     wave by a reduce-scatter butterfly (xor shuffles 8, 4, 2, 1 within each 16-lane row, each
+//     halving the values a lane holds, then 16 and 32), after which lane l holds z of output
+//     l & 15.  Softmax cross-entropy, d2 = dloss/dz and the zb reset as in head4_kernel.  d2
+//     and the sample's h1 go to LDS.
+//  B. Thread t owns column j = t: for the block's samples in order,
+//     d1 = (1 - h1^2) (h1b + sum_o w2[o, j] d2[o]) (o descending, as the generated loop),
+//     the h1b reset, and the column's sums of W2b += d2 h1' and b1b, written as the block's
+//     partials in d1sum_kernel's layout (the block is the chunk); b2b and the loss likewise.
+// h1 and h1b are read once, D1 and the h1b reset written once (the split form read h1 twice,
+// in two launches), with four waves per SIMD.  Every sum has a fixed order.
 // ---------------------------------------------------------------------------------------
+// (the arguments of the column-sum kernels: d1sum_kernel, and headd1_kernel's step B)
 struct D1Args {
     const float *h1, *h1b_in, *w2, *D2, *h1d, *w2d, *D2d;
     float *h1b, *D1, *h1bd, *D1d;
@@ -569,6 +580,186 @@ struct D1Args {
     int B, H, O;
 };
 
+constexpr int HDB = 16, HDNT = 64 * HDB;
+
+__host__ __device__ constexpr int hd_opl(int O) { return O | 1; }
+
+// LDS of headd1_kernel, in floats: red (32 doubles), W2 rows [JR][opl], d2 [HDB][OMAX],
+// h1 [HDB][JR]
+__host__ __device__ constexpr int hd_lds_floats(int JR, int O) {
+    return 64 + JR * hd_opl(O) + HDB * OMAX + HDB * JR;
+}
+
+// A block barrier that waits only for the wave's LDS operations: __syncthreads() also waits
+// for every global load in flight, which would expose the step-B loads issued at the start.
+#ifndef STADE_HD_RAW_BARRIER
+#define STADE_HD_RAW_BARRIER 1
+#endif
+__device__ __forceinline__ void lds_barrier() {
+#if STADE_HD_RAW_BARRIER
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
+    __builtin_amdgcn_s_barrier();
+#else
+    __syncthreads();
+#endif
+}
+
+template <int HPL, int OM>
+__global__ __launch_bounds__(HDNT) void headd1_kernel(HeadArgs a, D1Args c) {
+    static_assert(OM <= OMAX, "output slots");
+    constexpr int JR = 64 * HPL;
+    static_assert(JR <= HDNT, "a column per thread in step B");
+    // (static, sized for i_out = OMAX)
+    __shared__ float hd_smem[hd_lds_floats(JR, OMAX)];
+    const int H = a.H, O = a.O, B = a.B;
+    constexpr int opl = hd_opl(OM);  // (i_out <= OM: rows of OM outputs, zero past i_out)
+    double* red = reinterpret_cast<double*>(hd_smem);
+    float* w2s = hd_smem + 64;
+    float* d2s = w2s + JR * opl;
+    float* hs = d2s + HDB * OMAX;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sb0 = blockIdx.x * HDB, s = sb0 + wave;
+    const bool live = s < B;
+    const int sc = min(s, B - 1);
+    // every global read first, in the order of use (loads complete in order): W2 (row
+    // j = threadIdx.x), the sample's h1 and the lane values (step A), then h1b of column j for
+    // the block's samples (step B), still in flight through step A (the barriers wait for
+    // LDS operations only)
+    const int j = threadIdx.x;
+    const int jc = min(j, H - 1);
+    float w2v[opl];
+#pragma unroll
+    for (int o = 0; o < opl; ++o) w2v[o] = a.w2[(long)jc * O + min(o, O - 1)];
+    // (row pointers are wave-uniform and column offsets 32-bit: scalar-base addressing)
+    const float* hrow = a.h1 + (long)sc * H;
+    float h[HPL];
+#pragma unroll
+    for (int q = 0; q < HPL; ++q) h[q] = hrow[min(lane + 64 * q, H - 1)];
+    const int lo = lane & (OMAX - 1);
+    const float zb_lane = a.zb[(long)sc * O + min(lo, O - 1)];
+    const float b2_lane = a.b2[min(lo, O - 1)];
+    const int64_t lab_s = a.lab[sc];
+    const float lb = a.lossb[0];
+    float hbv[HDB];
+#pragma unroll
+    for (int k = 0; k < HDB; ++k) hbv[k] = __builtin_nontemporal_load(&(a.h1b + (long)min(sb0 + k, B - 1) * H)[jc]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j < JR) {
+#pragma unroll
+        for (int o = 0; o < opl; ++o) w2s[j * opl + o] = (j < H && o < O) ? w2v[o] : 0.f;
+    }
+    lds_barrier();
+    // columns past i_h contribute nothing (a dead sample's values are never stored or used)
+#pragma unroll
+    for (int q = 0; q < HPL; ++q) h[q] = lane + 64 * q < H ? h[q] : 0.f;
+    float v[OMAX];
+#pragma unroll
+    for (int o = 0; o < OMAX; ++o) v[o] = 0.f;
+#pragma unroll
+    for (int q = 0; q < HPL; ++q) {
+        const int row = (lane + 64 * q) * opl;
+        float wq[OM];
+#pragma unroll
+        for (int o = 0; o < OM; ++o) wq[o] = w2s[row + o];
+#pragma unroll
+        for (int o = 0; o < OM; ++o) v[o] = fmaf(wq[o], h[q], v[o]);
+    }
+    // reduce-scatter within the 16-lane rows, then across them: lane l ends with output l & 15
+#pragma unroll
+    for (int half = 8; half >= 1; half >>= 1) {
+        // keep / send by a bit select on the values (a select on the array index would make
+        // the compiler index the register array dynamically: a compare and select chain)
+        const int m = (lane & half) ? -1 : 0;
+#pragma unroll
+        for (int p = 0; p < half; ++p) {
+            const int lo_ = __float_as_int(v[p]), hi_ = __float_as_int(v[p + half]);
+            const float keep = __int_as_float((hi_ & m) | (lo_ & ~m));
+            const float send = __int_as_float((lo_ & m) | (hi_ & ~m));
+            v[p] = keep + __shfl_xor(send, half, 64);
+        }
+    }
+    v[0] += __shfl_xor(v[0], 16, 64);
+    v[0] += __shfl_xor(v[0], 32, 64);
+    // softmax cross-entropy of the sample over the lanes of a DPP row (every row the same)
+    double acc[2] = {0.0, 0.0};
+    {
+        const bool vo = lo < O;
+        const long os = (long)sc * O;
+        const float zv = vo ? b2_lane + v[0] : 0.f;
+        const float e = vo ? expf(zv) : 0.f;
+        const float se = row16_sum(e);
+        const int l = (int)lab_s - 1;
+        const bool lok = l >= 0 && l < O;
+        if (live && lane == 0 && !lok) atomicOr(a.err, kErrIndex);
+        if (live && lok && lane == l) acc[0] += (double)(logf(se) - zv);
+        // reverse of the loss: d2 = zb + [o == l](-lb) + exp(z) seb, seb = (1 / se) lb
+        const float seb = (1.0f / se) * lb;
+        float t = zb_lane;
+        if (lo == l) t = t + -lb;
+        const float d2 = t + e * seb;
+        if (live && lane < O) {
+            a.z[os + lane] = zv;
+            a.zb[os + lane] = 0.f;
+        }
+        if (lane < OMAX) d2s[wave * OMAX + lane] = (live && vo) ? d2 : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < HPL; ++q) hs[wave * JR + lane + 64 * q] = h[q];
+    lds_barrier();
+    // step B: column j over the block's samples
+    const int ns = min(HDB, B - sb0);
+    if (j < JR) {
+        float wc[OM];
+#pragma unroll
+        for (int o = 0; o < OM; ++o) wc[o] = w2s[j * opl + o];
+        float w2acc[OM];
+#pragma unroll
+        for (int o = 0; o < OM; ++o) w2acc[o] = 0.f;
+        float b1acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < HDB; ++k) {
+            if (k >= ns) continue;  // a guard, not an exit: the loop unrolls
+            const float hv = hs[k * JR + j];
+            const float* d2 = d2s + k * OMAX;
+            float t = hbv[k];
+#pragma unroll
+            for (int o = OM - 1; o >= 0; --o) t = t + wc[o] * d2[o];
+            const float d1 = (1.0f - hv * hv) * t;
+            if (j < H) {
+                const long r0 = (long)(sb0 + k) * H;
+                __builtin_nontemporal_store(0.f, &(a.h1b + r0)[j]);
+                (a.D1 + r0)[j] = d1;
+            }
+            // (a sum over the block's samples, in a different order from the generated loop's
+            // anyway: fused multiply-adds)
+#pragma unroll
+            for (int o = 0; o < OM; ++o) w2acc[o] = fmaf(hv, d2[o], w2acc[o]);
+            b1acc += d1;
+        }
+        if (j < H) {
+            float* p = c.part + (long)blockIdx.x * 2 * (O + 1) * H;
+#pragma unroll
+            for (int o = 0; o < OM; ++o)
+                if (o < O) p[(long)o * H + j] = w2acc[o];
+            p[(long)O * H + j] = b1acc;
+        }
+    }
+    if (threadIdx.x < OMAX) {
+        double t = 0.0;
+        for (int k = 0; k < HDB; ++k) t += (double)d2s[k * OMAX + threadIdx.x];
+        c.part2[(long)blockIdx.x * 2 * OMAX + threadIdx.x] = threadIdx.x < O ? (float)t : 0.f;
+    }
+    block_partials<2>(acc, red, a.partials);
+}
+
+// ---------------------------------------------------------------------------------------
+// second half of the split head fused with the column sums (i_h <= 1024): per chunk of SC
+// samples and 64 columns j,
+//   d1 = (1 - h1^2) (h1b + sum_o w2[o, j] d2[o]) (o descending, as the generated loop), h1b = 0
+//   (HVP: d1d, h1bd = 0), and the chunk partials of W2b += d2 h1', b1b += sum_s d1 (+ W2bd,
+//   b1bd) and of b2b (+ b2bd), in colsum_kernel's layout and summation order.
+// A thread owns column j (its W2 column in registers) and the samples s0 + sl + 4 k.
+// ---------------------------------------------------------------------------------------
 template <int MODE>
 __global__ __launch_bounds__(NT) void d1sum_kernel(D1Args a) {
     constexpr int NR = 2 * (OMAX + 1);
@@ -943,7 +1134,11 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     WsCall call_(stream);
     Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
-    const int nchunks = (B + SC - 1) / SC;
+    // the adjoint with i_h <= 1024 runs its head in one pass (headd1_kernel), a chunk of the
+    // column sums per block of HDB samples; the other forms split it (head4 / head, then
+    // d1sum / colsum over chunks of SC samples)
+    const bool fused_head = MODE == ADJ && H > 0 && H <= 1024;
+    const int nchunks = fused_head ? (B + HDB - 1) / HDB : (B + SC - 1) / SC;
     const size_t nD1 = (size_t)H * B, nD2 = (size_t)O * B, nC = (size_t)nchunks * 2 * (O + 1) * H;
     const int hv = MODE == HVP ? 2 : 1;
     using namespace gemm;
@@ -1010,15 +1205,30 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     // i_h <= 1024: the batched head, SPW samples per wave, at most one block per CU (each
     // block stages W2 once); wider layers: one wave per sample, 8 waves and 16 samples a block
     constexpr int SPW = MODE == ADJ ? 4 : 1, H4W = h4nt<MODE>() / 64;
-    const unsigned hb = H <= 1024 ? (unsigned)std::min<long>(((long)B + SPW * H4W - 1) / (SPW * H4W), cus)
-                                  : (unsigned)((B + 16 - 1) / 16);
-    STADE_TIMED("mlp_head", stream, {
-        if (H <= 256) head4_kernel<MODE, 4, SPW><<<hb, h4nt<MODE>(), 0, stream>>>(h);
-        else if (H <= 1024) head4_kernel<MODE, 16, SPW><<<hb, h4nt<MODE>(), 0, stream>>>(h);
-        else launch_head<MODE, 32>(h, hb, stream);
-    });
-    STADE_LAUNCHED("mlp head_kernel");
-    if (MODE != TAN && H <= 1024 && H > 0) {
+    const unsigned hb = fused_head ? (unsigned)nchunks
+                        : H <= 1024 ? (unsigned)std::min<long>(((long)B + SPW * H4W - 1) / (SPW * H4W), cus)
+                                    : (unsigned)((B + 16 - 1) / 16);
+    if (fused_head) {
+        D1Args c{p.h1, p.h1b, p.w2, D2, p.h1d, p.w2d, D2d, p.h1b, D1, p.h1bd, D1d, cpart, c2part, B, H, O};
+        STADE_TIMED("mlp_head", stream, {
+            // (output rows of 10 slots for i_out <= 10, else 16)
+            if (H <= 256 && O <= 10) headd1_kernel<4, 10><<<hb, HDNT, 0, stream>>>(h, c);
+            else if (H <= 256) headd1_kernel<4, OMAX><<<hb, HDNT, 0, stream>>>(h, c);
+            else if (O <= 10) headd1_kernel<16, 10><<<hb, HDNT, 0, stream>>>(h, c);
+            else headd1_kernel<16, OMAX><<<hb, HDNT, 0, stream>>>(h, c);
+        });
+        STADE_LAUNCHED("mlp headd1_kernel");
+    } else {
+        STADE_TIMED("mlp_head", stream, {
+            if (H <= 256) head4_kernel<MODE, 4, SPW><<<hb, h4nt<MODE>(), 0, stream>>>(h);
+            else if (H <= 1024) head4_kernel<MODE, 16, SPW><<<hb, h4nt<MODE>(), 0, stream>>>(h);
+            else launch_head<MODE, 32>(h, hb, stream);
+        });
+        STADE_LAUNCHED("mlp head_kernel");
+    }
+    if (fused_head) {
+        // (the column sums were formed by headd1_kernel)
+    } else if (MODE != TAN && H <= 1024 && H > 0) {
         D1Args c{p.h1, p.h1b, p.w2, D2, p.h1d, p.w2d, D2d, p.h1b, D1, p.h1bd, D1d, cpart, c2part, B, H, O};
         STADE_TIMED("mlp_colsum", stream, d1sum_kernel<MODE><<<dim3((H + 63) / 64, nchunks), NT, 0, stream>>>(c));
         STADE_LAUNCHED("mlp d1sum_kernel");
