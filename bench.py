@@ -486,12 +486,14 @@ def _lib():
     return L
 
 
-def profiled_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from its committed counter summary
-    (profiles/<kernel>_traffic.md: FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what
-    the same counter reads for a 1 GiB copy), or None when there is none."""
+def profiled_traffic(workload: str):
+    """HBM bytes per launch of the workload's dominant kernel from its committed counter
+    summary (profiles/<workload>_traffic.md: FETCH_SIZE and WRITE_SIZE per dispatch, each
+    scaled by what the same counter reads for a 1 GiB copy), or None when there is none.
+    rocprofv3 counter passes cannot run inside the timed process, so the figure comes from
+    the committed summary of a separate run of the same command."""
     import re
-    f = ROOT / "profiles" / f"{kernel}_traffic.md"
+    f = ROOT / "profiles" / f"{workload}_traffic.md"
     if not f.exists():
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read_text(), re.M)
@@ -623,7 +625,7 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
         if wl.bound == "hbm":
             ach = wl.kernel_bytes() / (k_ms * 1e-3) / 1e9
             out["roofline"] = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                               "frac": ach / HBM_PEAK_GBS, "traffic": profiled_traffic(wl.kernel)}
+                               "frac": ach / HBM_PEAK_GBS, "traffic": profiled_traffic(wl.name)}
         else:
             peak = FP32_PEAK_TFLOPS if wl.dtype == "f32" else FP64_PEAK_TFLOPS
             ach = wl.kernels[wl.kernel] / (k_ms * 1e-3) / 1e12
