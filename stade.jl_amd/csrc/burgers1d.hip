@@ -36,7 +36,17 @@ namespace {
 
 constexpr int NT = 256, KMAX = 32;
 constexpr int kInitBlockCells = NT * 8;  // cells per block of the backward init kernel
-constexpr int BNT = 1024;  // threads of the forward chunk kernel (16 waves per CU)
+#ifndef STADE_BURG_FT
+#define STADE_BURG_FT 1024
+#endif
+#ifndef STADE_BURG_FS
+#define STADE_BURG_FS 4096
+#endif
+// forward chunk kernel: threads and owned cells per block.  512 / 2048, 256 / 1024 and
+// 1024 / 2048 measured within 1 % of 1024 / 4096 for the adjoint, tangent and HVP (as did
+// backward HVP blocks of 256 / 1024, 1024 / 2048 and 512 / 2048 against 512 / 1024)
+constexpr int BNT = STADE_BURG_FT;
+constexpr int FWD_S = STADE_BURG_FS;
 #ifndef STADE_BURG_BT
 #define STADE_BURG_BT 512
 #endif
@@ -566,7 +576,7 @@ template <bool TAN>
 int32_t forward(const double* src, const double* srcd, double* fin, double* find, double* tape, double* taped, int n,
                 int64_t t_begin, int64_t t_end, const Coef& c, double* P, double* Q, double* Pd, double* Qd, hipStream_t stream,
                 int64_t row0 = 0, int every = 1) {
-    constexpr int S = 4096;
+    constexpr int S = FWD_S;
     const unsigned nb = grid_for(n, S);
     const double *cs = src, *csd = srcd;
     int64_t t0 = t_begin;
