@@ -72,6 +72,7 @@ class Workload:
     bound = "hbm"
     dtype = "f64"
     graph_steps = 0       # > 0: the timed steps are replays of a HIP graph of this many steps
+    lowered = False       # True: the general lowering's library runs the generated text
 
     def __init__(self, mode: str):
         self.mode = mode
@@ -98,8 +99,21 @@ class Workload:
         self.argv = [self.t[a] for a in names[:len(names) - len(self.stacks)]] + self.stacks
 
     def step(self):
+        if self.lowered:
+            self._low.call(self.name, *self.argv, shapes=self._dims)
+            return
         import stade_hip
         getattr(stade_hip, self.name)(*self.argv)
+
+    def use_lowered(self):
+        """Run the config's generated text through the general lowering (stade_hip.lower)
+        instead of its hand-written entry point: the same inputs, the same outputs."""
+        import numpy as np
+        from stade_hip import lower
+        self.lowered = True
+        path = ROOT / "stade.jl_amd" / "corpus" / f"{self.name}.jl"
+        self._low = lower.lower(path, "f32" if self.dtype == "f32" else "f64")
+        self._dims = {a: v.shape for a, v in self.host_inputs().items() if isinstance(v, np.ndarray) and v.ndim > 1}
 
     def algo_bytes(self) -> float:          # per evaluation
         return 0.0
@@ -642,6 +656,8 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
     out["config"] = wl.config()
     if wl.graph_steps:
         out["config"]["launch"] = f"HIP graph of {wl.graph_steps} steps, replayed (torch.cuda.graph)"
+    if wl.lowered:
+        out["config"]["path"] = "general lowering (stade_hip.lower) of the generated text"
     return out
 
 
@@ -690,6 +706,9 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--only", action="store_true", help="measure the headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--lowered", action="store_true",
+                    help="run every measured workload's generated text through the general lowering (stade_hip.lower) "
+                         "instead of its hand-written kernels (the checkpointed Burgers forms have no text and are skipped)")
     ap.add_argument("--graph", type=int, default=None,
                     help="issue the measured workload's timed steps as replays of a captured HIP graph of this many "
                          "steps (0: eager launches; default: the workload's own choice)")
@@ -755,6 +774,8 @@ def main():
     head = WORKLOADS[args.workload]()
     if args.graph is not None:
         head.graph_steps = args.graph
+    if args.lowered:
+        head.use_lowered()
     res = measure(head, args.steps, args.warmup, dev)
     others = {}
     if not args.only:
@@ -762,6 +783,10 @@ def main():
             if nm == args.workload or (args.configs and nm not in args.configs.split(",")):
                 continue
             wl = mk()
+            if args.lowered:
+                if nm.endswith("_ckpt"):
+                    continue
+                wl.use_lowered()
             heavy = nm.startswith(("burgers1d", "conv3x3", "mlp2_ce"))
             others[nm] = measure(wl, 10 if heavy else max(5, args.steps // 2), 2 if heavy else max(2, args.warmup), dev)
             if not args.no_cpu_baseline:
