@@ -111,6 +111,7 @@ class Workload:
         import numpy as np
         from stade_hip import lower
         self.lowered = True
+        self.graph_steps = 0   # (a lowered call synchronises to check its error flag: no capture)
         path = ROOT / "stade.jl_amd" / "corpus" / f"{self.name}.jl"
         self._low = lower.lower(path, "f32" if self.dtype == "f32" else "f64")
         self._dims = {a: v.shape for a, v in self.host_inputs().items() if isinstance(v, np.ndarray) and v.ndim > 1}

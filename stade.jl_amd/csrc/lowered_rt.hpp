@@ -10,6 +10,9 @@
 //   wave-aggregated atomic); otherwise each lane adds atomically.  Floating-point atomics
 //   use the hardware instructions (unsafeAtomicAdd): the order of the additions is left to
 //   the hardware, as the generated adjoint's `@atomic` leaves it.
+//   block_add: a value a thread has summed in a register over its iterations (a loop's sum
+//   into a scalar, or into an array element whose index does not change over the loop: the
+//   reference's hoisted atomic), added once per block.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -107,6 +110,25 @@ __device__ __forceinline__ void wave_add(T* p, T v) {
         }
     }
     atomic_add(p, v);
+}
+
+// One atomic addition per block of the block's values (a loop's sum into a scalar, or its
+// accumulations into one array element at an index that does not change over the loop): the
+// wave's DPP-free butterfly sum, the waves' sums in order through `lds` (one slot per wave),
+// then thread 0 adds the total if it is nonzero.  Every thread of the block must call it;
+// `p` may be null only when the block's values are all zero.
+template <class T>
+__device__ __forceinline__ void block_add(T* p, T v, T* lds) {
+    v = wave_sum(v);
+    const int nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        T s = lds[0];
+        for (int w = 1; w < nw; ++w) s += lds[w];
+        if (s != (T)0 && p) atomic_add(p, s);
+    }
+    __syncthreads();
 }
 
 // LDS-privatised accumulation: the block's copy, then one global atomic per nonzero element

@@ -343,7 +343,8 @@ def linear_in(p: dict, name: str):
 class ArrayUse:
     name: str
     kind: str                  # 'read' | 'owned' | 'acc' | 'atomic'
-    index: object = None       # the common index expression (owned / injective acc)
+    index: object = None       # the common index expression (owned / injective acc; hoisted atomic)
+    hoist: bool = False        # atomic at one index that no iteration changes: summed in a register
 
 
 @dataclass
@@ -579,6 +580,14 @@ def classify(loop: For, types: Types, later_reads: set, frame_written_outside: s
                         arrays[name] = ArrayUse(name, "owned", writes[0][0])
                         guards += g
                         continue
+                # every accumulation at one index expression that no iteration changes (the
+                # loss of a reduction loop, a bias gradient): a register sum per thread,
+                # added once per block (`cgen_hoistable_atomic_keys` 11501-11519)
+                varying = assigned | inner_vars | {v}
+                if len(idxs) == 1 and all(not isinstance(x, (Ref, Call)) and not (isinstance(x, Var) and x.name in varying)
+                                          for e in writes[0][0].idx for x in walk_expr(e)):
+                    arrays[name] = ArrayUse(name, "atomic", writes[0][0], hoist=True)
+                    continue
                 arrays[name] = ArrayUse(name, "atomic")
                 continue
         # owned: one index expression for every access, injective in the loop variable

@@ -32,6 +32,7 @@ from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, F
                      Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
 MAX_BLOCKS = 8192          # grid of a parallel loop whose trip count the host cannot evaluate
+RED_MAX_BLOCKS = 2048      # at most, for a loop with sums (each block adds its sums once)
 PRIV_MAX_BYTES = 48 * 1024  # LDS-privatised accumulation target, at most
 PRIV_RATIO = 32            # and at least this many iterations per target element
 SPLIT_MAX_TRIP = 16384     # a parallel loop with at most this many iterations (64 blocks of 256 threads)
@@ -415,8 +416,9 @@ class Ctx:
     """How names read and write inside one kernel (or the host)."""
 
     def __init__(self, fl: FuncLower, locals_: dict, hl_names: dict, acc: dict | None = None, serial_acc=True,
-                 reductions: dict | None = None, lds: str | None = None):
+                 reductions: dict | None = None, lds: str | None = None, hoist: dict | None = None):
         self.fl = fl
+        self.hoist = hoist or {}       # array -> register summing its accumulations (one index)
         self.locals = locals_          # scalar -> C local name
         self.hl = hl_names             # host loop var -> slot
         self.acc = acc or {}           # array -> 'atomic' (accumulations through wave_add / lds)
@@ -523,6 +525,10 @@ class Emitter:
                 c, _ = fl.ex(other, ctx)
                 val = f"({et})({c})" if sign == "+" else f"(-({et})({c}))"
                 nm = cname(ref.name)
+                if ref.name in ctx.hoist:
+                    self.emit(f"{{ const int64_t _i = {ctx.lin(ref)};")
+                    self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) {ctx.hoist[ref.name]} += {val}; else oob(); }}")
+                    return
                 self.emit(("if (_lane == 0) " if self.one_lane() else "") + f"{{ const int64_t _i = {ctx.lin(ref)};")
                 if ctx.lds == ref.name:
                     self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::lds_add(&lds_priv[_i], {val}); else oob(); }}")
@@ -746,10 +752,13 @@ class FuncGen:
         reds = {n: f"r_{cname(n)}" for n in pl.reductions}
         inv = sorted(n for n in pl.reads if n not in priv and n not in reds and n not in hl and n != v and n in fl.scalars)
         atomic = [n for n, u in pl.arrays.items() if u.kind == "atomic"]
+        # accumulations at one index no iteration changes: a register per thread, added once
+        # per block after the loop (not in the narrow-output form, whose lanes share the work)
+        hoist = {n: f"h_{cname(n)}" for n, u in sorted(pl.arrays.items()) if u.kind == "atomic" and u.hoist}
         # LDS-privatised variants: PRIV = c + 1 takes candidate c's accumulations into a
         # block-private copy (the host picks the first candidate small enough, with enough
         # iterations per element); PRIV = 0 uses wave-aggregated global atomics only
-        cands = sorted(atomic)
+        cands = sorted(n for n in atomic if n not in hoist)
         locals_ = {n: f"x_{cname(n)}" for n in priv + inv}
         locals_[v] = f"l_{cname(v)}"
 
@@ -757,7 +766,7 @@ class FuncGen:
 
         def body_lines(parallel: bool, lds: str | None, wave: bool = False) -> list[str]:
             ctx = Ctx(fl, dict(locals_), hl, acc={n: "atomic" for n in atomic}, serial_acc=not parallel,
-                      reductions=reds, lds=lds)
+                      reductions=reds, lds=lds, hoist=hoist if parallel and not wave else None)
             em = Emitter(fl, ctx)
             if wave:
                 em.split_loops = split
@@ -810,6 +819,7 @@ class FuncGen:
 
         def et_of(n):
             return "int64_t" if fl.arrays[n] == "i" else fl.fty
+        out += [f"    {et_of(n)} {r} = 0;" for n, r in hoist.items()]
         for c, n in enumerate(cands):
             n_len = Ctx(fl, {}, hl).length(n)
             out.append(f"    if constexpr (PRIV == {c + 1}) {{")
@@ -837,10 +847,17 @@ class FuncGen:
             out.append(f"        for (int64_t _j = threadIdx.x; _j < {n_len}; _j += blockDim.x)")
             out.append(f"            if (lds_priv[_j] != ({et_of(n)})0) stade_lowered::atomic_add(&a.A_{cname(n)}[_j], lds_priv[_j]);")
             out.append("    }")
+        # the block's sums: one atomic addition per block
         for n, r in reds.items():
-            out.append(f"    {r} = stade_lowered::wave_sum({r});")
-            out.append(f"    if ((threadIdx.x & 63) == 0 && {r} != 0) stade_lowered::atomic_add(&fr.v_{cname(n)}, {r});")
+            out.append(f"    stade_lowered::block_add(&fr.v_{cname(n)}, {r}, reinterpret_cast<{fl.cty(fl.scalars[n])}*>(_blk));")
+        for n, r in hoist.items():
+            ref = pl.arrays[n].index
+            out.append(f"    {{ const int64_t _i = {Ctx(fl, dict(locals_), hl).lin(ref)};")
+            out.append(f"      stade_lowered::block_add((uint64_t)_i < (uint64_t)a.N_{cname(n)} ? &a.A_{cname(n)}[_i] : nullptr, {r}, "
+                       f"reinterpret_cast<{et_of(n)}*>(_blk)); }}")
         pre = "    extern __shared__ __align__(16) unsigned char lds_raw[];\n    (void)lds_raw;\n" if cands else ""
+        if reds or hoist:
+            pre += "    __shared__ double _blk[16];  // the waves' sums of block_add\n"
         self.kern.append(f"template <int PRIV>\n__global__ __launch_bounds__(256) void k{k}(const Args a) {{\n" + pre +
                          "\n".join(out) + "\n}\n")
         if split:
@@ -891,7 +908,8 @@ class FuncGen:
                 self.hemit("} else")
             self.hemit("if (_trip > 0) {")
             self.hind += 1
-            self.hemit(f"const unsigned _g = (unsigned)std::min<int64_t>((_trip + 255) / 256, {MAX_BLOCKS});")
+            cap = RED_MAX_BLOCKS if (reds or hoist) else MAX_BLOCKS
+            self.hemit(f"const unsigned _g = (unsigned)std::min<int64_t>((_trip + 255) / 256, {cap});")
             if cands:
                 self.hemit("int _priv = 0;")
                 self.hemit("size_t _lds = 0;")
