@@ -167,6 +167,20 @@ def infer_types(f: Func, arg_types: dict | None = None, precision: str = "f64") 
     for a in int_arrays:
         if a in T.arrays and arg_types.get(a) != "Af":
             T.arrays[a] = "i"
+    # a shadow or tangent argument has its primal's shape even where the body never indexes it
+    # (an input the loss does not depend on): the generated signatures follow each float
+    # argument with its shadow (`agen_signature_args` /root/reference/src/STADE.jl:3455-3464,
+    # x, xb), tangent (`tgen_signature_args` 3306-3315, x, xd) and HVP pair (`hvp_emit`
+    # 6750-6756, xd, xbd)
+    for a in f.args:
+        if a in T.arrays or arg_types.get(a) in ("f", "i"):
+            continue
+        for suf in ("bd", "b", "d"):
+            p0 = a[:-len(suf)]
+            if a.endswith(suf) and p0 in f.args and T.arrays.get(p0) == "f":
+                T.arrays[a] = "f"
+                T.ndim[a] = T.ndim.get(p0, 1)
+                break
     # scalars: fixed point over assignments; a name in an Int context, or assigned only Ints, is an Int
     assigns: dict[str, list] = {}
     for s in walk_stmts(f.body):

@@ -1,0 +1,140 @@
+"""Fixtures for the GPU parity of the general lowering on the reference's own generated code.
+
+For each sized kernel of tests/test_oracle_corpus.py (the reference's committed generated
+adjoint, tangent and HVP files under /root/reference/test/val-corpus) and two sizes each:
+the seeds of the inputs, the oracle's outputs (the generated text transpiled to sequential C,
+in Float64) and the truth where it differs (the same text in 80-bit extended precision,
+rounded to Float64).  The lowering's library is built from the same file into
+stade.jl_amd/lib/gen/ with an index of libraries and signatures (build products, not
+committed; `build()` makes them where the reference is mounted).  tests/test_gpu_ref_corpus.py runs that library on the GPU on these
+inputs: the reference's text is read here, never on the GPU box, and nothing of it is stored
+but the inputs, outputs and argument lists.
+
+    python tests/golden/make_ref_corpus.py        # writes tests/golden/ref_corpus.{json,npz}
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+for p in (ROOT, ROOT / "stade.jl_amd", ROOT / "tests"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+REF_CORPUS = Path("/root/reference/test/val-corpus")
+
+# (ints, array shapes) per kernel: the oracle tests' small sizes, and larger ones that spread
+# the loops over many GPU threads (the index relations of each kernel kept)
+SIZES = {
+    "affine_loss": [(dict(i_n=7), dict(loss=1, u=7, a=7, b=7, v=7)),
+                    (dict(i_n=1000), dict(loss=1, u=1000, a=1000, b=1000, v=1000))],
+    "matvec_loss": [(dict(i_m=5, i_n=4), dict(loss=1, a=(5, 4), u=4, v=5)),
+                    (dict(i_m=90, i_n=70), dict(loss=1, a=(90, 70), u=70, v=90))],
+    "stencil_loss": [(dict(i_n=9), dict(loss=1, u=9, w=9)),
+                     (dict(i_n=1500), dict(loss=1, u=1500, w=1500))],
+    "dotprod": [(dict(i_n=6), dict(loss=1, u=6, v=6)),
+                (dict(i_n=1500), dict(loss=1, u=1500, v=1500))],
+    "advection": [(dict(i_nstep=3, i_nnode=8), dict(u=8, du=8)),
+                  (dict(i_nstep=12, i_nnode=300), dict(u=300, du=300))],
+    "mlp1d": [(dict(n_h=4), dict(loss=1, x=1, y=1, w1=4, b1=4, w2=16, b2=4, w3=4, b3=1, h1=4, h2=4, o=1)),
+              (dict(n_h=30), dict(loss=1, x=1, y=1, w1=30, b1=30, w2=900, b2=30, w3=30, b3=1, h1=30, h2=30, o=1))],
+    "fixed_sweeps": [(dict(i_n=5), dict(y=5, x=5)),
+                     (dict(i_n=400), dict(y=400, x=400))],
+    "bnd_branch": [(dict(i_n=6, i_m=4), dict(x=6, flag=6, out=6))],
+    "selfrace_conv": [(dict(i_n=6, i_nc=3), dict(x=9, w=3, z=6, loss=1)),
+                      (dict(i_n=800, i_nc=7), dict(x=807, w=7, z=800, loss=1))],
+    "relu_field": [(dict(i_n=8), dict(loss=1, u=8, v=8)),
+                   (dict(i_n=1200), dict(loss=1, u=1200, v=1200))],
+    "clamped_sumsq": [(dict(i_n=8), dict(loss=1, u=8)),
+                      (dict(i_n=1200), dict(loss=1, u=1200))],
+    "geomrecur": [(dict(i_n=6), dict(loss=1, u=6))],
+    "sumsq_shifted": [(dict(i_n=5), dict(loss=1, u=5)),
+                      (dict(i_n=800), dict(loss=1, u=800))],
+    "two_field_loss": [(dict(i_n=5), dict(loss=1, u=5, v=5, p=5, q=5)),
+                       (dict(i_n=1000), dict(loss=1, u=1000, v=1000, p=1000, q=1000))],
+    "bilinear": [(dict(i_m=4, i_n=3), dict(loss=1, x=4, a=(4, 3), y=3)),
+                 (dict(i_m=30, i_n=25), dict(loss=1, x=30, a=(30, 25), y=25))],
+}
+MODES = ("b", "d", "hv")
+
+
+def _shapes_all(shapes: dict) -> dict:
+    out = {}
+    for k, v in shapes.items():
+        for suf in ("", "b", "d", "bd"):
+            out[k + suf] = v
+    return out
+
+
+def main() -> None:
+    from helpers import ParityCase, make_args
+    from oracle import runner
+    from stade_hip import lower
+
+    meta, arrays = [], {}
+    for name, sizes in SIZES.items():
+        for mode in MODES:
+            path = REF_CORPUS / f"{name}_{mode}.jl"
+            text = path.read_text()
+            low = lower.lower(path, "f64", tag=f"ref_{name}_{mode}")
+            lib_o = runner.load(path, precision="f64")
+            fname = f"{name}_{mode}"
+            stack_fn = f"initstacks_{name}_b"
+            for si, (ints, shapes) in enumerate(sizes):
+                stacks = []
+                if mode != "d" and stack_fn in lib_o.infos:
+                    sargs = [ints[a] for a, _ in lib_o.infos[stack_fn].args]
+                    stacks = [(s, (n, "Ai" if et == "Int64" else "Af"))
+                              for s, et, n in lower.initstacks(text, stack_fn, *sargs)]
+                shp = _shapes_all(shapes)
+                shp["__stacks__"] = tuple(s for s, _ in stacks)
+                args = make_args(lib_o, fname, shp, ints, {}, f"refcorpus-{fname}-{si}", np.float64)
+                case = ParityCase(name, mode, args, stacks, "f64", oracle_path=path)
+                try:
+                    case.run_oracle(lib_o)
+                    truth = case.run_truth()
+                except (AssertionError, RuntimeError) as e:   # a size outside the kernel's index relations
+                    print(f"skip {fname} size {si}: {e}", file=sys.stderr)
+                    continue
+                key = f"{fname}/{si}"
+                # inputs are not stored: the test draws them again from the seed
+                # (helpers.seeded_inputs); an output equal to its input is not stored either, and
+                # the truth only where it differs from the Float64 oracle's result
+                outs = []
+                for (a, kind, v), h, t in zip(args, case.host, truth["arrays"]):
+                    if not isinstance(v, np.ndarray):
+                        continue
+                    if kind == "Ai":
+                        arrays[f"{key}/in/{a}"] = v
+                    if np.array_equal(np.ravel(v, order="F"), np.ravel(h, order="F")):
+                        continue
+                    outs.append(a)
+                    arrays[f"{key}/out/{a}"] = np.ravel(h, order="F")
+                    tt = np.ravel(np.asarray(t, dtype=np.float64) if kind == "Af" else t, order="F")
+                    if not np.array_equal(tt, arrays[f"{key}/out/{a}"]):
+                        arrays[f"{key}/truth/{a}"] = tt
+                for (s_, _), h, t in zip(stacks, case.stack_h, truth["stacks"]):
+                    arrays[f"{key}/out/{s_}"] = h
+                    tt = np.asarray(t, dtype=np.float64) if h.dtype != np.int64 else t
+                    if not np.array_equal(tt, h, equal_nan=True):
+                        arrays[f"{key}/truth/{s_}"] = tt
+                pos = {a: k for k, (a, _) in enumerate(lib_o.infos[fname].args)}
+                meta.append(dict(
+                    key=key, name=name, mode=mode, fname=fname, ints=ints, seed=f"refcorpus-{fname}-{si}",
+                    args=[[a, kind, (list(v.shape) if isinstance(v, np.ndarray) else v), pos[a]] for a, kind, v in args],
+                    outs=outs, stacks=[[s_, n, k] for s_, (n, k) in stacks],
+                    ret=[float(x) for x in case.ret_h], ret_truth=[float(x) for x in truth["ret"]],
+                    ))
+                print(f"{key}: {len(args)} arguments, {len(stacks)} stacks, plan {low.plan(fname)}")
+    (HERE / "ref_corpus.json").write_text(json.dumps(meta, indent=1))
+    np.savez_compressed(HERE / "ref_corpus.npz", **arrays)
+    print(f"{len(meta)} cases")
+
+
+if __name__ == "__main__":
+    main()

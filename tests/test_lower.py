@@ -3,6 +3,7 @@ inference, index analysis, loop plans, host-side initstacks, and the libraries i
 The GPU runs are tests/test_gpu_lowered.py."""
 import re
 import subprocess
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -193,3 +194,32 @@ def test_generic_texts_pinned(name):
     assert checks.fd_adjoint(ld, lb, k, base, s) <= 1e-3
     assert checks.fd_tangent(ld, ld, k, base, s) <= 1e-3
     assert checks.fd_hvp(lb, lh, k, base, s) <= 1e-3
+
+
+@pytest.mark.skipif(not REF_CORPUS.exists(), reason="reference corpus not mounted")
+def test_ref_corpus_fixture_inputs_reproduce():
+    """tests/test_gpu_ref_corpus.py draws its inputs again from the fixtures' seeds
+    (helpers.seeded_inputs); they must be the inputs the fixtures' oracle run used
+    (helpers.make_args on the generated text), and the stored oracle outputs must be what the
+    oracle computes from them now."""
+    import json
+    from helpers import ParityCase, make_args, seeded_inputs
+    from oracle import runner
+    gold = Path(__file__).resolve().parent / "golden"
+    meta = json.loads((gold / "ref_corpus.json").read_text())
+    z = np.load(gold / "ref_corpus.npz")
+    for case in meta[::7]:
+        lib_o = runner.load(REF_CORPUS / f"{case['fname']}.jl")
+        ia = {a: z[f"{case['key']}/in/{a}"] for a, kind, _, _ in case["args"] if kind == "Ai"}
+        got = seeded_inputs(case["args"], case["ints"], case["seed"], ia)
+        shapes = {a: tuple(s) for a, kind, s, _ in case["args"] if kind == "Af"}
+        shapes["__stacks__"] = tuple(s for s, _, _ in case["stacks"])
+        want = make_args(lib_o, case["fname"], shapes, case["ints"], {}, case["seed"], np.float64, ia)
+        assert [a for a, _, _ in got] == [a for a, _, _ in want]
+        for (a, _, g), (_, _, w) in zip(got, want):
+            assert np.array_equal(np.asarray(g), np.asarray(w)), f"{case['key']}: input {a} differs"
+        pc = ParityCase(case["name"], case["mode"], want, [(s, (n, k)) for s, n, k in case["stacks"]], "f64").run_oracle(lib_o)
+        for (a, _, v), h in zip(want, pc.host):
+            k = f"{case['key']}/out/{a}"
+            if k in z:
+                assert np.array_equal(np.ravel(h, order="F"), z[k]), f"{case['key']}: oracle output {a} differs"
