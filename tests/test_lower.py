@@ -1,6 +1,7 @@
 """The general lowering (stade_hip.lower) on the CPU: its parser's Julia semantics, type
 inference, index analysis, loop plans, host-side initstacks, and the libraries it builds.
 The GPU runs are tests/test_gpu_lowered.py."""
+import os
 import re
 import subprocess
 from pathlib import Path
@@ -223,3 +224,23 @@ def test_ref_corpus_fixture_inputs_reproduce():
             k = f"{case['key']}/out/{a}"
             if k in z:
                 assert np.array_equal(np.ravel(h, order="F"), z[k]), f"{case['key']}: oracle output {a} differs"
+
+
+@pytest.mark.skipif(not REF_CORPUS.exists() or os.environ.get("STADE_FULL_CORPUS") != "1",
+                    reason="compiles all 417 reference files (about 20 minutes on 8 cores): STADE_FULL_CORPUS=1")
+def test_reference_corpus_compiles(tmp_path):
+    """Every generated file of the reference's corpus lowers and compiles for gfx950."""
+    import concurrent.futures as cf
+    from stade_hip.lower import hipgen, runtime
+    files = sorted(p for p in REF_CORPUS.glob("*_*.jl") if re.search(r"_(b|d|hv)\.jl$", p.name))
+
+    def one(p):
+        src, _ = hipgen.generate(p.read_text())
+        h = tmp_path / f"{p.stem}.hip"
+        h.write_text(src)
+        r = subprocess.run([runtime.HIPCC, *runtime.FLAGS, "-o", str(h.with_suffix(".so")), str(h)],
+                           capture_output=True, text=True)
+        return None if r.returncode == 0 else (p.name, r.stderr[-300:])
+    with cf.ThreadPoolExecutor(8) as ex:
+        bad = [r for r in ex.map(one, files) if r]
+    assert len(files) >= 400 and not bad, bad
