@@ -493,6 +493,16 @@ WORKLOADS = {
 }
 HEADLINE = "diffusion2d_b"
 
+# bench.py --sizes: (workload, label) around each benchmark size
+SIZE_SWEEP = (
+    [(lambda n=n, m=m: Diffusion(m, n=n), f"diffusion2d_{m} n={n}") for m in ("b", "d", "hv")
+     for n in (512, 1024, 2048, 4096, 8192)]
+    + [(lambda n=n: Affine("b", m=n, n=n), f"affine_lsq_b {n}x{n}") for n in (256, 1024, 4096, 8192)]
+    + [(lambda n=n: Burgers("b", n=n), f"burgers1d_b n={n} T=500") for n in (1 << 16, 1 << 18, 1 << 20, 1 << 22)]
+    + [(lambda b=b: Mlp("b", B=b), f"mlp2_ce_b batch={b}") for b in (512, 1024, 4096, 16384)]
+    + [(lambda k=k: Conv("b", N=k), f"conv3x3_b {k} images") for k in (1, 2, 8, 16)]
+)
+
 
 def _lib():
     import stade_hip
@@ -707,6 +717,9 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--only", action="store_true", help="measure the headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sizes", action="store_true",
+                    help="time each config's adjoint (and the headline's tangent and HVP) over a range of sizes around "
+                         "the benchmark's and print one JSON line per size (evals/s and the roofline fraction)")
     ap.add_argument("--lowered", action="store_true",
                     help="run every measured workload's generated text through the general lowering (stade_hip.lower) "
                          "instead of its hand-written kernels (the checkpointed Burgers forms have no text and are skipped)")
@@ -771,6 +784,20 @@ def main():
         print(json.dumps({"stream_ceiling": "un = u (copy), ub += unb (add), torch kernels, 4096^2 fp64",
                           "bytes": 40 * n, "us": round(us, 1), "TBps": round(40 * n / us / 1e6, 3),
                           "frac_of_8TBps": round(40 * n / us / 1e6 / 8.0, 3)}))
+        return
+    if args.sizes:
+        for mk, label in SIZE_SWEEP:
+            wl = mk()
+            heavy = wl.family in ("burgers1d", "conv3x3", "mlp2_ce")
+            r = measure(wl, 10 if heavy else 30, 2 if heavy else 5, dev)
+            rf = r.get("roofline") or {}
+            print(json.dumps({"size": label, "function": wl.name, "evals_per_s": r["evals_per_s"],
+                              "ms_per_step": r["ms_per_step"], "kernel_ms": r.get("kernel_ms"),
+                              "kernel_frac": rf.get("frac"), "bound": rf.get("bound"),
+                              "eval_frac": r.get("eval_hbm_frac") or r.get("eval_mfma_frac") or r.get("eval_valu_frac")}),
+                  flush=True)
+            del wl
+            torch.cuda.empty_cache()
         return
     head = WORKLOADS[args.workload]()
     if args.graph is not None:
