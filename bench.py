@@ -496,7 +496,7 @@ HEADLINE = "diffusion2d_b"
 # bench.py --sizes: (workload, label) around each benchmark size
 SIZE_SWEEP = (
     [(lambda n=n, m=m: Diffusion(m, n=n), f"diffusion2d_{m} n={n}") for m in ("b", "d", "hv")
-     for n in (512, 1024, 2048, 4096, 8192)]
+     for n in (512, 1024, 2048, 3072, 4096, 6144, 8192, 12288)]
     + [(lambda n=n: Affine("b", m=n, n=n), f"affine_lsq_b {n}x{n}") for n in (256, 1024, 4096, 8192)]
     + [(lambda n=n: Burgers("b", n=n), f"burgers1d_b n={n} T=500") for n in (1 << 16, 1 << 18, 1 << 20, 1 << 22)]
     + [(lambda b=b: Mlp("b", B=b), f"mlp2_ce_b batch={b}") for b in (512, 1024, 4096, 16384)]
@@ -717,9 +717,10 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--only", action="store_true", help="measure the headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--sizes", action="store_true",
+    ap.add_argument("--sizes", nargs="?", const="all", default=None, metavar="FAMILIES",
                     help="time each config's adjoint (and the headline's tangent and HVP) over a range of sizes around "
-                         "the benchmark's and print one JSON line per size (evals/s and the roofline fraction)")
+                         "the benchmark's and print one JSON line per size (evals/s and the roofline fraction); "
+                         "optionally only the comma-separated families named")
     ap.add_argument("--lowered", action="store_true",
                     help="run every measured workload's generated text through the general lowering (stade_hip.lower) "
                          "instead of its hand-written kernels (the checkpointed Burgers forms have no text and are skipped)")
@@ -786,7 +787,10 @@ def main():
                           "frac_of_8TBps": round(40 * n / us / 1e6 / 8.0, 3)}))
         return
     if args.sizes:
+        keep = None if args.sizes == "all" else set(args.sizes.split(","))
         for mk, label in SIZE_SWEEP:
+            if keep is not None and label.split(" ")[0].rsplit("_", 1)[0] not in keep:
+                continue
             wl = mk()
             heavy = wl.family in ("burgers1d", "conv3x3", "mlp2_ce")
             r = measure(wl, 10 if heavy else 30, 2 if heavy else 5, dev)

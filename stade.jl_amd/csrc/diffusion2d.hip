@@ -35,6 +35,7 @@
 
 #include <mutex>
 #include <initializer_list>
+#include <type_traits>
 #include "../../include/stade_hip.h"
 
 namespace stade {
@@ -368,12 +369,6 @@ __global__ __launch_bounds__(NT) void zero2_kernel(double* __restrict__ a, doubl
 #ifndef STADE_DIFF_WD_HV
 #define STADE_DIFF_WD_HV 4
 #endif
-#ifndef STADE_DIFF_WCH2
-#define STADE_DIFF_WCH2 64
-#endif
-#ifndef STADE_DIFF_WCH2_HV
-#define STADE_DIFF_WCH2_HV 32
-#endif
 #ifndef STADE_DIFF_WD2_HV
 #define STADE_DIFF_WD2_HV 4
 #endif
@@ -594,14 +589,32 @@ __global__ __launch_bounds__(256) void diffusion_b_wave(const double* __restrict
 // are unrolled by static_for: at 64 rows the bodies exceed the compiler's unroll threshold,
 // and a rolled loop would move the register arrays to scratch memory.
 constexpr int WS2 = 128;
-// rows per wave and rows of loads in flight, measured at n = 4096: the adjoint and the
-// tangent as on 64-column strips; the HVP, with twice the values per row, 32 rows with four in
-// flight (256 VGPRs, one wave a SIMD), 3 % faster with the streaming hints than 64 rows with
-// two in flight (178 VGPRs, two waves a SIMD), which had been 10 % faster without them
-constexpr int WCH2 = STADE_DIFF_WCH2;        // adjoint, tangent
-constexpr int WCH2_HV = STADE_DIFF_WCH2_HV;  // HVP
+// Rows per wave (16, 32 or 64; each divides 128, so n % 128 == 0 implies n % rows == 0),
+// chosen by n from timings of the three heights on MI355X at n = 1024 .. 16384.  16 rows are
+// within a few per cent of the best almost everywhere, and the only choice that holds up at
+// large n: at n = 8192 the adjoint ran at 71 % of the HBM peak with 16 rows, 60 % with 32 and
+// 48 % with 64 (power-of-two strides: a 64-row chunk of 64 KB rows starts 4 MB after the one
+// above), and at 16384 68 / 60 / 58 %.  Two ranges measured faster with taller chunks: around
+// n = 2048 (32 rows; 16-row chunks leave 20 % of each wave's rows to the halo) and, for the
+// adjoint, n = 4096, where 64 rows make a grid of exactly two blocks a CU, all resident at
+// once (77-81 % against 74 % with 16 rows).  The HVP, with twice the values per row, keeps
+// four rows in flight (256 VGPRs, one wave a SIMD; 64 rows would spill) and takes the
+// tangent's heights: 16 rows measured 1-7 points above 32 from n = 6144 to 12288 and 15 points
+// above at n <= 1024, and within 2 points either way from 2048 to 4096.
 constexpr int WD2_HV = STADE_DIFF_WD2_HV;
-static_assert(WS2 % WCH2 == 0 && WS2 % WCH2_HV == 0, "n % 128 == 0 must imply n % rows == 0");
+int rows_b2(int64_t n) { return n == 4096 ? 64 : (n >= 1536 && n <= 2560) ? 32 : 16; }
+int rows_d2(int64_t n) { return (n >= 2048 && n <= 4096) ? 32 : 16; }
+int rows_hv2(int64_t n) { return rows_d2(n); }
+// calls f with the chunk height as a compile-time constant (heights above MAXR are not
+// instantiated)
+template <int MAXR, typename F>
+void with_rows(int rows, F&& f) {
+    if constexpr (MAXR >= 64) {
+        if (rows == 64) return f(std::integral_constant<int, 64>{});
+    }
+    if (rows == 32) return f(std::integral_constant<int, 32>{});
+    f(std::integral_constant<int, 16>{});
+}
 
 struct WaveGeom2 {
     int lane, c0, j0, oc, hc;
@@ -638,46 +651,44 @@ template <int ROWS, int D>
 __global__ __launch_bounds__(256) void diffusion_d_wave2(const double* __restrict__ u, const double* __restrict__ ud,
                                                          double* __restrict__ un, double* __restrict__ und, int n,
                                                          int nstrips, int nwaves, double* partials) {
+    __shared__ double red[4 * 2];
     const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wid >= nwaves) return;  // whole waves only; the kernel has no barrier
-    const WaveGeom2 g = wave_geom2(wid, n, nstrips, ROWS);
-    const double2* __restrict__ u2 = reinterpret_cast<const double2*>(u);
-    const double2* __restrict__ ud2 = reinterpret_cast<const double2*>(ud);
-    double2* __restrict__ un2 = reinterpret_cast<double2*>(un);
-    double2* __restrict__ und2 = reinterpret_cast<double2*>(und);
-    double2 U[ROWS + 2], UD[ROWS + 2];  // row q at index q + 1
-    double H[ROWS + 2], HD[ROWS + 2];
-    auto load = [&](int q) {
-        const size_t rb = (size_t)wrap1(g.j0 + q, n) * n;
-        U[q + 1] = u2[pair_of(rb, g.oc)];
-        H[q + 1] = u[rb + g.hc];
-        UD[q + 1] = ud2[pair_of(rb, g.oc)];
-        HD[q + 1] = ud[rb + g.hc];
-    };
-    load(-1);
-    load(0);
-#pragma unroll
-    for (int k = 1; k <= D; ++k) load(k);
     double acc[2] = {0.0, 0.0};
-    static_for<ROWS>([&](auto rc) {
-        constexpr int r = decltype(rc)::value, i = r + 1;
-        if constexpr (r + D + 1 <= ROWS) load(r + D + 1);
-        const double2 v = step_pair<false>(U[i - 1], U[i], U[i + 1], lane_val(H[i], 1), lane_val(H[i], 2));
-        const double2 vd = step_pair<true>(UD[i - 1], UD[i], UD[i + 1], lane_val(HD[i], 1), lane_val(HD[i], 2));
-        const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
-        nt_store2(vd, &und2[gp]);
-        nt_store2(v, &un2[gp]);
-        acc[1] += (2.0 * v.x) * vd.x;
-        acc[0] += v.x * v.x;
-        acc[1] += (2.0 * v.y) * vd.y;
-        acc[0] += v.y * v.y;
-    });
-    acc[0] = wave_sum(acc[0]);
-    acc[1] = wave_sum(acc[1]);
-    if (g.lane == 0) {
-        partials[(size_t)wid * 2] = acc[0];
-        partials[(size_t)wid * 2 + 1] = acc[1];
+    if (wid < nwaves) {  // whole waves; the four of a block meet at the barrier below
+        const WaveGeom2 g = wave_geom2(wid, n, nstrips, ROWS);
+        const double2* __restrict__ u2 = reinterpret_cast<const double2*>(u);
+        const double2* __restrict__ ud2 = reinterpret_cast<const double2*>(ud);
+        double2* __restrict__ un2 = reinterpret_cast<double2*>(un);
+        double2* __restrict__ und2 = reinterpret_cast<double2*>(und);
+        double2 U[ROWS + 2], UD[ROWS + 2];  // row q at index q + 1
+        double H[ROWS + 2], HD[ROWS + 2];
+        auto load = [&](int q) {
+            const size_t rb = (size_t)wrap1(g.j0 + q, n) * n;
+            U[q + 1] = u2[pair_of(rb, g.oc)];
+            H[q + 1] = u[rb + g.hc];
+            UD[q + 1] = ud2[pair_of(rb, g.oc)];
+            HD[q + 1] = ud[rb + g.hc];
+        };
+        load(-1);
+        load(0);
+#pragma unroll
+        for (int k = 1; k <= D; ++k) load(k);
+        static_for<ROWS>([&](auto rc) {
+            constexpr int r = decltype(rc)::value, i = r + 1;
+            if constexpr (r + D + 1 <= ROWS) load(r + D + 1);
+            const double2 v = step_pair<false>(U[i - 1], U[i], U[i + 1], lane_val(H[i], 1), lane_val(H[i], 2));
+            const double2 vd = step_pair<true>(UD[i - 1], UD[i], UD[i + 1], lane_val(HD[i], 1), lane_val(HD[i], 2));
+            const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
+            nt_store2(vd, &und2[gp]);
+            nt_store2(v, &un2[gp]);
+            acc[1] += (2.0 * v.x) * vd.x;
+            acc[0] += v.x * v.x;
+            acc[1] += (2.0 * v.y) * vd.y;
+            acc[0] += v.y * v.y;
+        });
     }
+    // one partial pair per block: its four waves' sums added in wave order
+    block_partials<2>(acc, red, partials);
 }
 
 // adjoint pass 1 (HV = false) and its tangent (HV = true): un (+ und) of the wave's rows,
@@ -689,137 +700,140 @@ __global__ __launch_bounds__(256) void diffusion_b_wave2(const double* __restric
                                                          double* __restrict__ ub, double* __restrict__ ubd,
                                                          const double* __restrict__ lossb, const double* __restrict__ lossbd,
                                                          int n, int nstrips, int nwaves, double* partials) {
+    __shared__ double red[4 * (HV ? 2 : 1)];
     const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wid >= nwaves) return;  // whole waves only; the kernel has no barrier
-    const WaveGeom2 g = wave_geom2(wid, n, nstrips, ROWS);
-    const double lb = lossb[0];
-    const double lbd = HV ? lossbd[0] : 0.0;
-    const double2* __restrict__ u2 = reinterpret_cast<const double2*>(u);
-    const double2* __restrict__ ud2 = reinterpret_cast<const double2*>(ud);
-    const double2* __restrict__ unb2 = reinterpret_cast<const double2*>(unb);
-    const double2* __restrict__ unbd2 = reinterpret_cast<const double2*>(unbd);
-    double2* __restrict__ un2 = reinterpret_cast<double2*>(un);
-    double2* __restrict__ und2 = reinterpret_cast<double2*>(und);
-    double2* __restrict__ ub2 = reinterpret_cast<double2*>(ub);
-    double2* __restrict__ ubd2 = reinterpret_cast<double2*>(ubd);
-    // u rows -2 .. ROWS+1 at index q + 2; unb rows -1 .. ROWS at q + 1; ub rows 0 .. ROWS-1
-    double2 U[ROWS + 4], B[ROWS + 2], UB[ROWS];
-    double H[ROWS + 4], BH[ROWS + 2];
-    double2 UD[HV ? ROWS + 4 : 1], BD[HV ? ROWS + 2 : 1], UBD[HV ? ROWS : 1];
-    double HD[HV ? ROWS + 4 : 1], BHD[HV ? ROWS + 2 : 1];
-    auto rowb = [&](int q) { return (size_t)wrap1(g.j0 + q, n) * n; };
-    auto load_u = [&](int q) {
-        const size_t rb = rowb(q);
-        U[q + 2] = u2[pair_of(rb, g.oc)];
-        H[q + 2] = u[rb + g.hc];
-        if constexpr (HV) {
-            UD[q + 2] = ud2[pair_of(rb, g.oc)];
-            HD[q + 2] = ud[rb + g.hc];
-        }
-    };
-    auto load_b = [&](int q) {
-        const size_t rb = rowb(q);
-        B[q + 1] = unb2[pair_of(rb, g.oc)];
-        BH[q + 1] = unb[rb + g.hc];
-        if constexpr (HV) {
-            BD[q + 1] = unbd2[pair_of(rb, g.oc)];
-            BHD[q + 1] = unbd[rb + g.hc];
-        }
-    };
-    // the loads that step r consumes last: u row r+2, unb row r+1, ub row r
-    auto load_group = [&](int r) {
-        load_u(r + 2);
-        load_b(r + 1);
-        const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
-        UB[r] = nt_load2(&ub2[gp]);
-        if constexpr (HV) UBD[r] = nt_load2(&ubd2[gp]);
-    };
-    // w of rows -1 .. ROWS (own pair) and of the edge columns c0-1 (west) and c0+128 (east)
-    double2 Wo[ROWS + 2], WDo[HV ? ROWS + 2 : 1];
-    double Ww[ROWS + 2], We[ROWS + 2], WDw[HV ? ROWS + 2 : 1], WDe[HV ? ROWS + 2 : 1];
     double acc[2] = {0.0, 0.0};
-    // un (+ und) and w (+ wd) of row q in the generated text's operation order; un stored
-    // for the wave's own rows
-    auto new_state = [&](int q) {
-        const int i = q + 2, b = q + 1;
-        const double hw = lane_val(H[i], 1), he = lane_val(H[i], 2);
-        const double2 v = step_pair<false>(U[i - 1], U[i], U[i + 1], hw, he);
-        const double vw = step5v(lane_val(H[i - 1], 1), hw, lane_val(H[i + 1], 1), lane_val(H[i], 0), lane_val(U[i].x, 0));
-        const double ve = step5v(lane_val(H[i - 1], 2), he, lane_val(H[i + 1], 2), lane_val(U[i].y, 63), lane_val(H[i], 3));
-        Wo[b].x = B[b].x + (2.0 * v.x) * lb;
-        Wo[b].y = B[b].y + (2.0 * v.y) * lb;
-        Ww[b] = lane_val(BH[b], 1) + (2.0 * vw) * lb;
-        We[b] = lane_val(BH[b], 2) + (2.0 * ve) * lb;
-        double2 vd = make_double2(0.0, 0.0);
-        if constexpr (HV) {
-            const double hdw = lane_val(HD[i], 1), hde = lane_val(HD[i], 2);
-            vd = step_pair<true>(UD[i - 1], UD[i], UD[i + 1], hdw, hde);
-            const double vdw =
-                step5dv(lane_val(HD[i - 1], 1), hdw, lane_val(HD[i + 1], 1), lane_val(HD[i], 0), lane_val(UD[i].x, 0));
-            const double vde =
-                step5dv(lane_val(HD[i - 1], 2), hde, lane_val(HD[i + 1], 2), lane_val(UD[i].y, 63), lane_val(HD[i], 3));
-            WDo[b].x = BD[b].x + (lb * (2.0 * vd.x) + (2.0 * v.x) * lbd);
-            WDo[b].y = BD[b].y + (lb * (2.0 * vd.y) + (2.0 * v.y) * lbd);
-            WDw[b] = lane_val(BHD[b], 1) + (lb * (2.0 * vdw) + (2.0 * vw) * lbd);
-            WDe[b] = lane_val(BHD[b], 2) + (lb * (2.0 * vde) + (2.0 * ve) * lbd);
-        }
-        if (q >= 0 && q < ROWS) {
-            const size_t gp = pair_of((size_t)(g.j0 + q) * n, g.oc);
+    if (wid < nwaves) {  // whole waves; the four of a block meet at the barrier below
+        const WaveGeom2 g = wave_geom2(wid, n, nstrips, ROWS);
+        const double lb = lossb[0];
+        const double lbd = HV ? lossbd[0] : 0.0;
+        const double2* __restrict__ u2 = reinterpret_cast<const double2*>(u);
+        const double2* __restrict__ ud2 = reinterpret_cast<const double2*>(ud);
+        const double2* __restrict__ unb2 = reinterpret_cast<const double2*>(unb);
+        const double2* __restrict__ unbd2 = reinterpret_cast<const double2*>(unbd);
+        double2* __restrict__ un2 = reinterpret_cast<double2*>(un);
+        double2* __restrict__ und2 = reinterpret_cast<double2*>(und);
+        double2* __restrict__ ub2 = reinterpret_cast<double2*>(ub);
+        double2* __restrict__ ubd2 = reinterpret_cast<double2*>(ubd);
+        // u rows -2 .. ROWS+1 at index q + 2; unb rows -1 .. ROWS at q + 1; ub rows 0 .. ROWS-1
+        double2 U[ROWS + 4], B[ROWS + 2], UB[ROWS];
+        double H[ROWS + 4], BH[ROWS + 2];
+        double2 UD[HV ? ROWS + 4 : 1], BD[HV ? ROWS + 2 : 1], UBD[HV ? ROWS : 1];
+        double HD[HV ? ROWS + 4 : 1], BHD[HV ? ROWS + 2 : 1];
+        auto rowb = [&](int q) { return (size_t)wrap1(g.j0 + q, n) * n; };
+        auto load_u = [&](int q) {
+            const size_t rb = rowb(q);
+            U[q + 2] = u2[pair_of(rb, g.oc)];
+            H[q + 2] = u[rb + g.hc];
             if constexpr (HV) {
-                nt_store2(vd, &und2[gp]);
-                acc[1] += (2.0 * v.x) * vd.x;
-                acc[1] += (2.0 * v.y) * vd.y;
+                UD[q + 2] = ud2[pair_of(rb, g.oc)];
+                HD[q + 2] = ud[rb + g.hc];
             }
-            nt_store2(v, &un2[gp]);
-            acc[0] += v.x * v.x;
-            acc[0] += v.y * v.y;
-        }
-    };
-    // ub[row r] += w_c + 0.1 w_E + 0.1 w_W + 0.1 w_S + 0.1 w_N + 4 (-(0.1 w_c))
-    auto gather1 = [](double c, double e, double w, double s, double nn) {
-        double a = c;
-        a = a + 0.1 * e;
-        a = a + 0.1 * w;
-        a = a + 0.1 * s;
-        a = a + 0.1 * nn;
-        a = a + 4.0 * -(0.1 * c);
-        return a;
-    };
-    auto gather = [&](int r) {
-        const int b = r + 1;
-        const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
-        if constexpr (HV) {
-            const double2 c = WDo[b];
+        };
+        auto load_b = [&](int q) {
+            const size_t rb = rowb(q);
+            B[q + 1] = unb2[pair_of(rb, g.oc)];
+            BH[q + 1] = unb[rb + g.hc];
+            if constexpr (HV) {
+                BD[q + 1] = unbd2[pair_of(rb, g.oc)];
+                BHD[q + 1] = unbd[rb + g.hc];
+            }
+        };
+        // the loads that step r consumes last: u row r+2, unb row r+1, ub row r
+        auto load_group = [&](int r) {
+            load_u(r + 2);
+            load_b(r + 1);
+            const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
+            UB[r] = nt_load2(&ub2[gp]);
+            if constexpr (HV) UBD[r] = nt_load2(&ubd2[gp]);
+        };
+        // w of rows -1 .. ROWS (own pair) and of the edge columns c0-1 (west) and c0+128 (east)
+        double2 Wo[ROWS + 2], WDo[HV ? ROWS + 2 : 1];
+        double Ww[ROWS + 2], We[ROWS + 2], WDw[HV ? ROWS + 2 : 1], WDe[HV ? ROWS + 2 : 1];
+        // un (+ und) and w (+ wd) of row q in the generated text's operation order; un stored
+        // for the wave's own rows
+        auto new_state = [&](int q) {
+            const int i = q + 2, b = q + 1;
+            const double hw = lane_val(H[i], 1), he = lane_val(H[i], 2);
+            const double2 v = step_pair<false>(U[i - 1], U[i], U[i + 1], hw, he);
+            const double vw = step5v(lane_val(H[i - 1], 1), hw, lane_val(H[i + 1], 1), lane_val(H[i], 0), lane_val(U[i].x, 0));
+            const double ve = step5v(lane_val(H[i - 1], 2), he, lane_val(H[i + 1], 2), lane_val(U[i].y, 63), lane_val(H[i], 3));
+            Wo[b].x = B[b].x + (2.0 * v.x) * lb;
+            Wo[b].y = B[b].y + (2.0 * v.y) * lb;
+            Ww[b] = lane_val(BH[b], 1) + (2.0 * vw) * lb;
+            We[b] = lane_val(BH[b], 2) + (2.0 * ve) * lb;
+            double2 vd = make_double2(0.0, 0.0);
+            if constexpr (HV) {
+                const double hdw = lane_val(HD[i], 1), hde = lane_val(HD[i], 2);
+                vd = step_pair<true>(UD[i - 1], UD[i], UD[i + 1], hdw, hde);
+                const double vdw =
+                    step5dv(lane_val(HD[i - 1], 1), hdw, lane_val(HD[i + 1], 1), lane_val(HD[i], 0), lane_val(UD[i].x, 0));
+                const double vde =
+                    step5dv(lane_val(HD[i - 1], 2), hde, lane_val(HD[i + 1], 2), lane_val(UD[i].y, 63), lane_val(HD[i], 3));
+                WDo[b].x = BD[b].x + (lb * (2.0 * vd.x) + (2.0 * v.x) * lbd);
+                WDo[b].y = BD[b].y + (lb * (2.0 * vd.y) + (2.0 * v.y) * lbd);
+                WDw[b] = lane_val(BHD[b], 1) + (lb * (2.0 * vdw) + (2.0 * vw) * lbd);
+                WDe[b] = lane_val(BHD[b], 2) + (lb * (2.0 * vde) + (2.0 * ve) * lbd);
+            }
+            if (q >= 0 && q < ROWS) {
+                const size_t gp = pair_of((size_t)(g.j0 + q) * n, g.oc);
+                if constexpr (HV) {
+                    nt_store2(vd, &und2[gp]);
+                    acc[1] += (2.0 * v.x) * vd.x;
+                    acc[1] += (2.0 * v.y) * vd.y;
+                }
+                nt_store2(v, &un2[gp]);
+                acc[0] += v.x * v.x;
+                acc[0] += v.y * v.y;
+            }
+        };
+        // ub[row r] += w_c + 0.1 w_E + 0.1 w_W + 0.1 w_S + 0.1 w_N + 4 (-(0.1 w_c))
+        auto gather1 = [](double c, double e, double w, double s, double nn) {
+            double a = c;
+            a = a + 0.1 * e;
+            a = a + 0.1 * w;
+            a = a + 0.1 * s;
+            a = a + 0.1 * nn;
+            a = a + 4.0 * -(0.1 * c);
+            return a;
+        };
+        auto gather = [&](int r) {
+            const int b = r + 1;
+            const size_t gp = pair_of((size_t)(g.j0 + r) * n, g.oc);
+            if constexpr (HV) {
+                const double2 c = WDo[b];
+                double2 o;
+                o.x = UBD[r].x + gather1(c.x, c.y, from_west(c.y, WDw[b]), WDo[b + 1].x, WDo[b - 1].x);
+                o.y = UBD[r].y + gather1(c.y, from_east(c.x, WDe[b]), c.x, WDo[b + 1].y, WDo[b - 1].y);
+                nt_store2(o, &ubd2[gp]);
+            }
+            const double2 c = Wo[b];
             double2 o;
-            o.x = UBD[r].x + gather1(c.x, c.y, from_west(c.y, WDw[b]), WDo[b + 1].x, WDo[b - 1].x);
-            o.y = UBD[r].y + gather1(c.y, from_east(c.x, WDe[b]), c.x, WDo[b + 1].y, WDo[b - 1].y);
-            nt_store2(o, &ubd2[gp]);
-        }
-        const double2 c = Wo[b];
-        double2 o;
-        o.x = UB[r].x + gather1(c.x, c.y, from_west(c.y, Ww[b]), Wo[b + 1].x, Wo[b - 1].x);
-        o.y = UB[r].y + gather1(c.y, from_east(c.x, We[b]), c.x, Wo[b + 1].y, Wo[b - 1].y);
-        nt_store2(o, &ub2[gp]);
-    };
+            o.x = UB[r].x + gather1(c.x, c.y, from_west(c.y, Ww[b]), Wo[b + 1].x, Wo[b - 1].x);
+            o.y = UB[r].y + gather1(c.y, from_east(c.x, We[b]), c.x, Wo[b + 1].y, Wo[b - 1].y);
+            nt_store2(o, &ub2[gp]);
+        };
 #pragma unroll
-    for (int q = -2; q <= 1; ++q) load_u(q);
-    load_b(-1);
-    load_b(0);
+        for (int q = -2; q <= 1; ++q) load_u(q);
+        load_b(-1);
+        load_b(0);
 #pragma unroll
-    for (int k = 0; k < D; ++k) load_group(k);
-    new_state(-1);
-    new_state(0);
-    static_for<ROWS>([&](auto rc) {
-        constexpr int r = decltype(rc)::value;
-        if constexpr (r + D < ROWS) load_group(r + D);
-        new_state(r + 1);
-        gather(r);
-    });
-    acc[0] = wave_sum(acc[0]);
-    if constexpr (HV) acc[1] = wave_sum(acc[1]);
-    if (g.lane == 0) {
-        partials[(size_t)wid * (HV ? 2 : 1)] = acc[0];
-        if constexpr (HV) partials[(size_t)wid * 2 + 1] = acc[1];
+        for (int k = 0; k < D; ++k) load_group(k);
+        new_state(-1);
+        new_state(0);
+        static_for<ROWS>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            if constexpr (r + D < ROWS) load_group(r + D);
+            new_state(r + 1);
+            gather(r);
+        });
+    }
+    // one partial (pair) per block: its four waves' sums added in wave order
+    if constexpr (HV) {
+        block_partials<2>(acc, red, partials);
+    } else {
+        double v1[1] = {acc[0]};
+        block_partials<1>(v1, red, partials);
     }
 }
 
@@ -863,9 +877,10 @@ Grid grid_of(int64_t n) {
     return Grid{strips, strips * chunks};
 }
 
-// the adjoint's reduction partials: one per wave (block on the row-streaming path) of pass 1
+// the adjoint's reduction partials: one per block of pass 1 (one per wave on the 64-column
+// strips)
 int64_t adjoint_partials(int64_t n, bool pairs) {
-    if (pairs) return (n / WS2) * (n / WCH2);
+    if (pairs) return ((n / WS2) * (n / rows_b2(n)) + 3) / 4;
     if (wave_path(n)) return (n / WS) * (n / WCH);
     const Grid g = grid_of(n);
     return g.blocks;
@@ -878,12 +893,13 @@ int32_t adjoint(double* loss, const double* lossb, const double* u, double* ub, 
                 double* partials, hipStream_t stream) {
     int nparts;
     if (pairs_ok(n, {u, un, unb, ub})) {
-        const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2);
-        STADE_TIMED("diffusion2d_b", stream,
-                    diffusion_b_wave2<false, WCH2, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(
-                        u, nullptr, un, nullptr, unb, nullptr, ub, nullptr, lossb, nullptr, (int)n, nstrips, nwaves, partials));
+        const int rows = rows_b2(n), nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / rows);
+        STADE_TIMED("diffusion2d_b", stream, with_rows<64>(rows, [&](auto rc) {
+                        diffusion_b_wave2<false, decltype(rc)::value, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(
+                            u, nullptr, un, nullptr, unb, nullptr, ub, nullptr, lossb, nullptr, (int)n, nstrips, nwaves, partials);
+                    }));
         STADE_LAUNCHED("diffusion_b_wave2");
-        nparts = nwaves;
+        nparts = (nwaves + 3) / 4;
     } else if (wave_path(n)) {
         const WaveGrid w = wave_grid_of(n, WCH);
         STADE_TIMED("diffusion2d_b", stream,
@@ -966,12 +982,13 @@ int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, co
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
     if (pairs_ok(n, {u, ud, un, und})) {
-        const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2);
-        STADE_TIMED("diffusion2d_d", stream,
-                    diffusion_d_wave2<WCH2, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(u, ud, un, und, (int)n, nstrips, nwaves,
-                                                                                    ws->partials));
+        const int rows = rows_d2(n), nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / rows);
+        STADE_TIMED("diffusion2d_d", stream, with_rows<32>(rows, [&](auto rc) {
+                        diffusion_d_wave2<decltype(rc)::value, WD><<<(nwaves + 3) / 4, 256, 0, stream>>>(
+                            u, ud, un, und, (int)n, nstrips, nwaves, ws->partials);
+                    }));
         STADE_LAUNCHED("diffusion_d_wave2");
-        nparts = nwaves;
+        nparts = (nwaves + 3) / 4;
     } else if (wave_path(n)) {
         const WaveGrid w = wave_grid_of(n, WCH);
         STADE_TIMED("diffusion2d_d", stream,
@@ -985,7 +1002,7 @@ int32_t stade_hip_diffusion2d_d(double* loss, double* lossd, const double* u, co
         STADE_LAUNCHED("diffusion_d_kernel");
         nparts = g.blocks;
     }
-    STADE_TIMED("finalize", stream, finalize_kernel<2><<<1, NT, 0, stream>>>(ws->partials, nparts, SumOuts{{loss, lossd}}));
+    STADE_TIMED("finalize", stream, finalize_kernel<2, 1024><<<1, 1024, 0, stream>>>(ws->partials, nparts, SumOuts{{loss, lossd}}));
     STADE_LAUNCHED("finalize_kernel");
     return STADE_HIP_OK;
 }
@@ -1013,12 +1030,13 @@ int32_t stade_hip_diffusion2d_hv(double* loss, const double* lossb, const double
     if (!ws) return STADE_HIP_ENOMEM;
     int nparts;
     if (pairs_ok(n, {u, ud, un, und, unb, unbd, ub, ubd})) {
-        const int nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / WCH2_HV);
-        STADE_TIMED("diffusion2d_hv", stream,
-                    diffusion_b_wave2<true, WCH2_HV, WD2_HV><<<(nwaves + 3) / 4, 256, 0, stream>>>(
-                        u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd, (int)n, nstrips, nwaves, ws->partials));
+        const int rows = rows_hv2(n), nstrips = (int)(n / WS2), nwaves = nstrips * (int)(n / rows);
+        STADE_TIMED("diffusion2d_hv", stream, with_rows<32>(rows, [&](auto rc) {
+                        diffusion_b_wave2<true, decltype(rc)::value, WD2_HV><<<(nwaves + 3) / 4, 256, 0, stream>>>(
+                            u, ud, un, und, unb, unbd, ub, ubd, lossb, lossbd, (int)n, nstrips, nwaves, ws->partials);
+                    }));
         STADE_LAUNCHED("diffusion_b_wave2<hv>");
-        nparts = nwaves;
+        nparts = (nwaves + 3) / 4;
     } else if (wave_path(n)) {
         const WaveGrid w = wave_grid_of(n, WCH_HV);
         STADE_TIMED("diffusion2d_hv", stream,

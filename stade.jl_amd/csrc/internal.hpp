@@ -236,9 +236,11 @@ __device__ __forceinline__ void finalize_partials(const double* partials, int np
     }
 }
 
-// Stage 2 as its own launch (one block), for a producer with no follow-on kernel.
-template <int NV>
-__global__ __launch_bounds__(256) void finalize_kernel(const double* partials, int nparts, SumOuts out) {
+// Stage 2 as its own launch (one block of THREADS, at most 1024), for a producer with no
+// follow-on kernel.  More threads keep more partials' loads in flight: a 1024-thread block
+// reads tens of thousands of partials in a few microseconds.
+template <int NV, int THREADS = 256>
+__global__ __launch_bounds__(THREADS) void finalize_kernel(const double* partials, int nparts, SumOuts out) {
     __shared__ double lds[16 * NV];
     finalize_partials<NV>(partials, nparts, lds, out);
 }

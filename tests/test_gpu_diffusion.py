@@ -3,9 +3,11 @@
 Sizes cover the degenerate periodic grids (n = 1, 2: coincident neighbours), grids smaller
 than a tile, ragged tiles (the LDS row-streaming kernels), multiples of 128 (the 128-column
 wave strips: one strip whose halo wraps onto itself at n = 128, three strips and a partly
-empty block at 384), multiples of 64 only (the 64-column wave strips: one strip at n = 64,
-strip counts that leave a block partly empty at 192 and 320), and the benchmark grid
-n = 4096."""
+empty block at 384; each chunk height the launch picks by n: adjoint and tangent 16 rows at
+128, 384 and 4224, 32 at 2048 (the adjoint also at 1536), the adjoint 64 and the tangent 32 at
+4096; the HVP as the tangent), multiples of 64 only (the 64-column wave
+strips: one strip at n = 64, strip counts that leave a block partly empty at 192 and 320), and
+the benchmark grid n = 4096."""
 import numpy as np
 import pytest
 
@@ -13,7 +15,7 @@ from helpers import run_parity
 
 pytestmark = pytest.mark.gpu
 
-SIZES = [1, 2, 3, 5, 35, 36, 64, 65, 100, 128, 129, 192, 257, 320, 384, 4096]
+SIZES = [1, 2, 3, 5, 35, 36, 64, 65, 100, 128, 129, 192, 257, 320, 384, 1536, 2048, 4096, 4224]
 
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])

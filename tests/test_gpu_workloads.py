@@ -17,7 +17,7 @@ the same seeds, scales, zero shadows and Burgers scalars):
    module starts; each test then waits for its own.
 
 2. Size-independent properties at the full benchmark size of every config (conv: all 8
-   images), on the GPU alone:
+   images), and for diffusion2d also at 8192 x 8192, on the GPU alone:
    - the adjoint's defining identity <yb, J xd> = <J^T yb, xd> between the `_d` and `_b`
      entry points over the whole in-place state, with random yb and xd
      (`val_validate_dotprod` /root/reference/src/STADE.jl:17108-17131, with its scale
@@ -185,6 +185,8 @@ FULL = {
     "mlp2_ce": lambda b: b.Mlp("b"),
     "conv3x3": lambda b: b.Conv("b"),
     "burgers1d": lambda b: b.Burgers("b"),
+    # a grid above the benchmark's: the 16-row chunks every mode takes at large n
+    "diffusion2d_8192": lambda b: b.Diffusion("b", n=8192),
 }
 
 
@@ -198,8 +200,8 @@ def test_dotprod_identity_full_size(family):
     base = _dev_state(wl)
     g = torch.Generator(device="cuda")
     g.manual_seed(20261202)
-    bp = _pairs(family, "b", "b")
-    dp = _pairs(family, "d", "d")
+    bp = _pairs(wl.family, "b", "b")
+    dp = _pairs(wl.family, "d", "d")
     assert [p for p, _, _ in bp] == [p for p, _, _ in dp]
     xd, yb = {}, {}
     for p, _, kind in bp:
@@ -251,7 +253,7 @@ def test_hessian_symmetry_full_size(family):
     g = torch.Generator(device="cuda")
     g.manual_seed(7)
     # the HVP's argument list is the adjoint's, then (xd, xbd) per float argument
-    bp = _pairs(family, "b", "b")
+    bp = _pairs(wl.family, "b", "b")
     dirs = []
     for _ in range(2):
         v = {}
