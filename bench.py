@@ -497,7 +497,8 @@ HEADLINE = "diffusion2d_b"
 SIZE_SWEEP = (
     [(lambda n=n, m=m: Diffusion(m, n=n), f"diffusion2d_{m} n={n}") for m in ("b", "d", "hv")
      for n in (512, 1024, 2048, 3072, 4096, 6144, 8192, 12288)]
-    + [(lambda n=n: Affine("b", m=n, n=n), f"affine_lsq_b {n}x{n}") for n in (256, 1024, 4096, 8192)]
+    + [(lambda n=n, m=m: Affine(m, m=n, n=n), f"affine_lsq_{m} {n}x{n}") for m in ("b", "d", "hv")
+       for n in (256, 1024, 2048, 4096, 8192)]
     + [(lambda n=n: Burgers("b", n=n), f"burgers1d_b n={n} T=500") for n in (1 << 16, 1 << 18, 1 << 20, 1 << 22)]
     + [(lambda b=b: Mlp("b", B=b), f"mlp2_ce_b batch={b}") for b in (512, 1024, 4096, 16384)]
     + [(lambda k=k: Conv("b", N=k), f"conv3x3_b {k} images") for k in (1, 2, 8, 16)]

@@ -26,41 +26,46 @@ namespace stade {
 namespace {
 
 constexpr int RT = 64, CT = 64, CW = 16, NT = 256;  // rows per tile, columns per tile, columns per wave
+constexpr int kMaxChunks = 16;                      // row-sum partials per row
 
 enum Mode { ADJ = 0, TAN = 1, HVP = 2 };
 
 template <int M>
 __global__ __launch_bounds__(NT) void rows_kernel(const double* __restrict__ w, const double* __restrict__ wd,
                                                   const double* __restrict__ x, const double* __restrict__ xd,
-                                                  double* __restrict__ P, double* __restrict__ Pd, int m, int n,
+                                                  double* __restrict__ P, double* __restrict__ Pd, int m, int n, int tpc,
                                                   double* __restrict__ rb, double* __restrict__ rbd, double* __restrict__ RBc,
                                                   double* __restrict__ RBdc) {
     __shared__ double part[2][4][RT];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int chunk = blockIdx.x, i = blockIdx.y * RT + lane;
-    const int j0 = chunk * CT + wv * CW;
-    // the wave's 16 columns: every load issued (clamped, unconditional) before the first use;
-    // columns past n and rows past m contribute nothing
-    double wv_[CW], xv_[CW], wdv_[CW], xdv_[CW];
     const int ic = min(i, m - 1);
-#pragma unroll
-    for (int jj = 0; jj < CW; ++jj) {
-        const int jc = min(j0 + jj, n - 1);
-        const size_t g = (size_t)jc * m + ic;
-        wv_[jj] = w[g];
-        xv_[jj] = x[jc];
-        wdv_[jj] = M != ADJ ? wd[g] : 0.0;
-        xdv_[jj] = M != ADJ ? xd[jc] : 0.0;
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    const int t_end = min((chunk + 1) * tpc, (n + CT - 1) / CT);
     double s = 0.0, sd = 0.0;
-    if (i < m) {
+    // the chunk's column tiles in order; per tile, the wave's 16 columns: every load issued
+    // (clamped, unconditional) before the first use; columns past n and rows past m
+    // contribute nothing
+    for (int tile = chunk * tpc; tile < t_end; ++tile) {
+        const int j0 = tile * CT + wv * CW;
+        double wv_[CW], xv_[CW], wdv_[CW], xdv_[CW];
 #pragma unroll
         for (int jj = 0; jj < CW; ++jj) {
-            if (j0 + jj >= n) continue;  // columns past n (a guard, not an exit: the loop unrolls)
-            const double wij = wv_[jj], xj = xv_[jj];
-            if (M != ADJ) sd = sd + (xj * wdv_[jj] + wij * xdv_[jj]);
-            s = s + wij * xj;
+            const int jc = min(j0 + jj, n - 1);
+            const size_t g = (size_t)jc * m + ic;
+            wv_[jj] = w[g];
+            xv_[jj] = x[jc];
+            wdv_[jj] = M != ADJ ? wd[g] : 0.0;
+            xdv_[jj] = M != ADJ ? xd[jc] : 0.0;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < m) {
+#pragma unroll
+            for (int jj = 0; jj < CW; ++jj) {
+                if (j0 + jj >= n) continue;  // columns past n (a guard, not an exit: the loop unrolls)
+                const double wij = wv_[jj], xj = xv_[jj];
+                if (M != ADJ) sd = sd + (xj * wdv_[jj] + wij * xdv_[jj]);
+                s = s + wij * xj;
+            }
         }
     }
     part[0][wv][lane] = s;
@@ -183,8 +188,10 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
                                                   double* __restrict__ XP, double* __restrict__ XPd, int m, int n,
                                                   double* __restrict__ partials) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int rtile = blockIdx.y, i = rtile * RT + lane;
-    const int j0 = blockIdx.x * CT + wv * CW;
+    // row tiles along x: blocks dispatched together stream consecutive segments of the same
+    // columns (measured 6-20 % faster at 4096^2-8192^2 than column tiles along x)
+    const int rtile = blockIdx.x, i = rtile * RT + lane;
+    const int j0 = blockIdx.y * CT + wv * CW;
     const bool live = i < m;
     const int ic = min(i, m - 1);
     // every read of the wave's 16 columns (w, wb, x and the tangents) issued before any use or
@@ -213,7 +220,7 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
         sid = RBdc[ic] + (lb * (0.5 * (2.0 * rvd)) + h4 * fa.lossbd[0]);
         si = rbv + h4 * lb;
     }
-    if (blockIdx.x == 0 && wv == 0) {
+    if (blockIdx.y == 0 && wv == 0) {
         // every destination read before any is written
         const double bb0 = fa.bb[ic], tb0 = fa.tb[ic];
         const double bbd0 = M == HVP ? fa.bbd[ic] : 0.0, tbd0 = M == HVP ? fa.tbd[ic] : 0.0;
@@ -389,6 +396,9 @@ int32_t check_sizes(int64_t m, int64_t n, const char* fn) {
     if (m > (1 << 26) || n > (1 << 26) || m * n > (int64_t)1 << 34)
         return set_error(STADE_HIP_ERANGE, "%s: size out of range (i_m = %lld, i_n = %lld)", fn, (long long)m, (long long)n);
     if ((m + RT - 1) / RT * 2 > kPartialSlots) return set_error(STADE_HIP_ERANGE, "%s: i_m too large for the workspace", fn);
+    // row tiles are the rows kernel's grid y dimension, column tiles the column kernel's
+    if ((m + RT - 1) / RT > 65535) return set_error(STADE_HIP_ERANGE, "%s: i_m = %lld exceeds 65535 row tiles of 64", fn, (long long)m);
+    if ((n + CT - 1) / CT > 65535) return set_error(STADE_HIP_ERANGE, "%s: i_n = %lld exceeds 65535 column tiles of 64", fn, (long long)n);
     return STADE_HIP_OK;
 }
 
@@ -399,7 +409,11 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
     WsCall call_(stream);
     Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
-    const int nchunks = (int)((n + CT - 1) / CT), mtiles = (int)((m + RT - 1) / RT);
+    // column tiles of 64, grouped into at most kMaxChunks chunks of tpc tiles for the row sums,
+    // so that each row's value is the sum of at most kMaxChunks partials (one round of loads
+    // wherever it is recomputed)
+    const int ntiles = (int)((n + CT - 1) / CT), mtiles = (int)((m + RT - 1) / RT);
+    const int tpc = (ntiles + kMaxChunks - 1) / kMaxChunks, nchunks = ntiles > 0 ? (ntiles + tpc - 1) / tpc : 0;
     const int two = (M == ADJ) ? 1 : 2;
     size_t nP = (size_t)nchunks * m, nS = (size_t)m, nX = (size_t)mtiles * n;
     double* base = (double*)scratch(sizeof(double) * two * (nP + nS + nX) + 256);
@@ -410,7 +424,7 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
     const bool fused = M != TAN && n > 0;
     if (nchunks > 0) {
         STADE_TIMED("affine_rows", stream,
-                    rows_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, x, xd, P, Pd, (int)m, (int)n, fa.rb, fa.rbd,
+                    rows_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, x, xd, P, Pd, (int)m, (int)n, tpc, fa.rb, fa.rbd,
                                                                               fused ? S : nullptr, Sd));
         STADE_LAUNCHED("affine rows_kernel");
     }
@@ -447,7 +461,7 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
         return STADE_HIP_OK;
     }
     STADE_TIMED("affine_cols", stream,
-                cols_kernel<M><<<dim3(nchunks, mtiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, fa, S, Sd, XP, XPd, (int)m, (int)n,
+                cols_kernel<M><<<dim3(mtiles, ntiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, fa, S, Sd, XP, XPd, (int)m, (int)n,
                                                                           ws->partials));
     STADE_LAUNCHED("affine cols_kernel");
     STADE_TIMED("affine_xfinish", stream,

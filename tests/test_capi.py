@@ -46,6 +46,11 @@ def test_argument_errors_before_device_work():
     assert rc == -3 and b"46340" in L.stade_hip_last_error()
     rc = L.stade_hip_affine_lsq_b(*([null] * 12), -2, 3, null)
     assert rc == -1 and b"negative" in L.stade_hip_last_error()
+    # 65536 row tiles of 64 would exceed the grid's y dimension
+    rc = L.stade_hip_affine_lsq_b(*([null] * 12), ctypes.c_int64(65536 * 64), ctypes.c_int64(1), null)
+    assert rc == -3 and b"65535 row tiles" in L.stade_hip_last_error()
+    rc = L.stade_hip_affine_lsq_b(*([null] * 12), ctypes.c_int64(1), ctypes.c_int64(65536 * 64), null)
+    assert rc == -3 and b"65535 column tiles" in L.stade_hip_last_error()
     # zero-trip: n = 0 runs no loop and needs no device
     assert L.stade_hip_diffusion2d_b(null, null, null, null, null, null, 0, null) == 0
     assert L.stade_hip_affine_lsq_d(*([null] * 12), 0, 5, null) == 0
