@@ -1123,9 +1123,10 @@ class FuncGen:
             f"static size_t g_bytes[{nb}];",
             "// local arrays (allocated inside the generated function): kept per process, grown on demand",
             "static void* _buf(int slot, size_t bytes) {",
+            "    if (bytes == 0) bytes = 8;   // an empty array still gets an address (nothing reads it)",
             "    if (g_bytes[slot] < bytes) {",
             "        if (g_buf[slot]) { (void)hipDeviceSynchronize(); (void)hipFree(g_buf[slot]); g_buf[slot] = nullptr; g_bytes[slot] = 0; }",
-            "        if (hipMalloc(&g_buf[slot], bytes ? bytes : 8) != hipSuccess) return nullptr;",
+            "        if (hipMalloc(&g_buf[slot], bytes) != hipSuccess) return nullptr;",
             "        g_bytes[slot] = bytes;",
             "    }",
             "    return g_buf[slot];",

@@ -46,11 +46,17 @@ def _src_key(src: str) -> str:
     return hashlib.sha256((src + flags + rt).encode()).hexdigest()[:16]
 
 
+_so_locks: dict = {}
+
+
 def build_source(src: str, stem: str) -> Path:
-    """Compile HIP source into the generated-library directory (once per source text)."""
+    """Compile HIP source into the generated-library directory (once per source text; one
+    lock per library, so that different sources compile in parallel threads)."""
     GEN_LIB.mkdir(parents=True, exist_ok=True)
     so = GEN_LIB / f"{stem}_{_src_key(src)}.so"
     with _lock:
+        lk = _so_locks.setdefault(so, threading.Lock())
+    with lk:
         if so.exists():
             return so
         hip = so.with_suffix(".hip")

@@ -1,10 +1,17 @@
 """Fixtures for the GPU parity of the general lowering on the reference's own generated code.
 
-For each sized kernel of tests/test_oracle_corpus.py (the reference's committed generated
-adjoint, tangent and HVP files under /root/reference/test/val-corpus) and two sizes each:
-the seeds of the inputs, the oracle's outputs (the generated text transpiled to sequential C,
-in Float64) and the truth where it differs (the same text in 80-bit extended precision,
-rounded to Float64).  The lowering's library is built from the same file into
+For every kernel of the reference's validation corpus (its committed generated adjoint,
+tangent and HVP files under /root/reference/test/val-corpus): the seeds of the inputs, the
+oracle's outputs (the generated text transpiled to sequential C, in Float64) and the truth
+where it differs (the same text in 80-bit extended precision, rounded to Float64).  The
+kernels of tests/test_oracle_corpus.py take two hand-chosen sizes each (the oracle tests'
+small ones and larger ones that spread the loops over many GPU threads); every other kernel
+is sized the way the reference's validator sizes it (`val_generate_baseline` and
+`val_grow_shapes`, /root/reference/src/STADE.jl:16701-16790): Int64 arguments drawn from
+3..5, every array N along each of its dimensions with N = 4, 8, 16, ... until the tangent runs
+without an index out of bounds (Int64 arrays hold indices drawn from 1..cap, cap = 4, 8, ...
+in the outer loop), and a draw rejected when its results are not finite, exceed 1e6 in
+magnitude or leave every output unchanged (nothing exercised).  The lowering's library is built from the same file into
 stade.jl_amd/lib/gen/ with an index of libraries and signatures (build products, not
 committed; `build()` makes them where the reference is mounted).  tests/test_gpu_ref_corpus.py runs that library on the GPU on these
 inputs: the reference's text is read here, never on the GPU box, and nothing of it is stored
@@ -61,6 +68,7 @@ SIZES = {
                  (dict(i_m=30, i_n=25), dict(loss=1, x=30, a=(30, 25), y=25))],
 }
 MODES = ("b", "d", "hv")
+MAX_ELEMS = 1 << 20   # per array: caps N for arrays of three or more dimensions
 
 
 def _shapes_all(shapes: dict) -> dict:
@@ -71,69 +79,159 @@ def _shapes_all(shapes: dict) -> dict:
     return out
 
 
-def main() -> None:
+def _ndims(text: str, fname: str) -> dict:
+    """Dimensions of every array argument, as the general lowering reads them from the text."""
+    from stade_hip.lower import hipgen
+    _, sigs = hipgen.generate(text, "f64")
+    return {a: nd for a, _, nd in sigs[fname]["args"]}
+
+
+def auto_size(name: str):
+    """(ints, shapes, int arrays) for a kernel without hand-chosen sizes, found on the tangent
+    (no stacks to size); None when the kernel has no tangent file or no draw works."""
+    from helpers import make_args
+    from oracle import rng as jrng
+    from oracle import runner
+    path = REF_CORPUS / f"{name}_d.jl"
+    if not path.exists():
+        return None
+    fname = f"{name}_d"
+    lib = runner.load(path, precision="f64")
+    info = lib.infos[fname]
+    nd = _ndims(path.read_text(), fname)
+    int_names = [a for a, k in info.args if k == "i"]
+    arrays = [(a, k) for a, k in info.args if k in ("Af", "Ai")]
+    base = jrng.val_stable_seed(f"refcorpus-size-{name}")
+    for attempt in range(24):
+        rs = np.random.default_rng(base + attempt)
+        ints = {a: int(rs.integers(3, 6)) for a in int_names}
+        cap, verdict = 4, None
+        while cap <= 512 and verdict is None:
+            n = 4
+            while n <= 512 and verdict is None:
+                shp = {a: (n,) * max(1, nd[a]) for a, _ in arrays}
+                if any(n ** len(v) > MAX_ELEMS for v in shp.values()):
+                    break
+                shapes = {a: (v if len(v) > 1 else v[0]) for a, v in shp.items()}
+                ia = {a: np.asfortranarray(rs.integers(1, cap + 1, size=shp[a]).astype(np.int64)) for a, k in arrays if k == "Ai"}
+                args = make_args(lib, fname, shapes, ints, {}, f"refcorpus-{fname}-0", np.float64, int_arrays=ia)
+                host = [v.copy(order="K") if isinstance(v, np.ndarray) else v for _, _, v in args]
+                try:
+                    ret = lib.call(fname, *host)
+                except IndexError:
+                    n *= 2
+                    continue
+                outs = [h for (_, k, v), h in zip(args, host) if k == "Af"]
+                changed = any(not np.array_equal(h, v) for (_, k, v), h in zip(args, host) if k == "Af")
+                changed = changed or any(isinstance(r, float) and r != 0.0 for r in ret)
+                big = max([float(np.max(np.abs(h))) for h in outs if h.size] + [0.0])
+                verdict = "ok" if (changed and np.isfinite(big) and big <= 1e6) else "reject"
+                if verdict == "ok":
+                    return ints, shapes, ia
+            cap *= 2
+    return None
+
+
+def corpus_names() -> list:
+    """Kernels of the corpus: the primal files (a name with a generated _d, _b or _hv beside it)."""
+    return sorted(p.stem for p in REF_CORPUS.glob("*.jl")
+                  if not p.stem.endswith(("_b", "_d", "_hv")) and any((REF_CORPUS / f"{p.stem}_{m}.jl").exists() for m in MODES))
+
+
+def one_kernel(name: str):
+    """Meta entries, fixture arrays and log lines of one kernel (every mode, every size)."""
     from helpers import ParityCase, make_args
     from oracle import runner
     from stade_hip import lower
-
-    meta, arrays = [], {}
-    for name, sizes in SIZES.items():
-        for mode in MODES:
-            path = REF_CORPUS / f"{name}_{mode}.jl"
-            text = path.read_text()
-            low = lower.lower(path, "f64", tag=f"ref_{name}_{mode}")
+    meta, arrays, log = [], {}, []
+    if name in SIZES:
+        sizes = [(ints, shapes, {}) for ints, shapes in SIZES[name]]
+    else:
+        try:
+            found = auto_size(name)
+        except Exception as e:  # noqa: BLE001 -- a kernel the oracle cannot size is reported, not fatal
+            log.append(f"skip {name}: sizing failed: {str(e)[:160]}")
+            return meta, arrays, log
+        if found is None:
+            log.append(f"skip {name}: no working size")
+            return meta, arrays, log
+        sizes = [found]
+    for mode in MODES:
+        path = REF_CORPUS / f"{name}_{mode}.jl"
+        if not path.exists():
+            continue
+        text = path.read_text()
+        fname = f"{name}_{mode}"
+        stack_fn = f"initstacks_{name}_b"
+        try:
             lib_o = runner.load(path, precision="f64")
-            fname = f"{name}_{mode}"
-            stack_fn = f"initstacks_{name}_b"
-            for si, (ints, shapes) in enumerate(sizes):
+        except Exception as e:  # noqa: BLE001
+            log.append(f"skip {fname}: oracle: {str(e)[:160]}")
+            continue
+        for si, (ints, shapes, int_arrays) in enumerate(sizes):
+            try:
                 stacks = []
                 if mode != "d" and stack_fn in lib_o.infos:
                     sargs = [ints[a] for a, _ in lib_o.infos[stack_fn].args]
-                    stacks = [(s, (n, "Ai" if et == "Int64" else "Af"))
-                              for s, et, n in lower.initstacks(text, stack_fn, *sargs)]
+                    stacks = [(s_, (n, "Ai" if et == "Int64" else "Af"))
+                              for s_, et, n in lower.initstacks(text, stack_fn, *sargs)]
                 shp = _shapes_all(shapes)
-                shp["__stacks__"] = tuple(s for s, _ in stacks)
-                args = make_args(lib_o, fname, shp, ints, {}, f"refcorpus-{fname}-{si}", np.float64)
+                shp["__stacks__"] = tuple(s_ for s_, _ in stacks)
+                args = make_args(lib_o, fname, shp, ints, {}, f"refcorpus-{fname}-{si}", np.float64,
+                                 int_arrays=int_arrays)
                 case = ParityCase(name, mode, args, stacks, "f64", oracle_path=path)
-                try:
-                    case.run_oracle(lib_o)
-                    truth = case.run_truth()
-                except (AssertionError, RuntimeError) as e:   # a size outside the kernel's index relations
-                    print(f"skip {fname} size {si}: {e}", file=sys.stderr)
+                case.run_oracle(lib_o)
+                truth = case.run_truth()
+            except (AssertionError, RuntimeError, IndexError, KeyError, TypeError, ValueError, lower.LowerError) as e:
+                # a size outside the kernel's index relations, or a text the harness cannot run
+                log.append(f"skip {fname} size {si}: {type(e).__name__}: {str(e)[:160]}")
+                continue
+            key = f"{fname}/{si}"
+            # inputs are not stored: the test draws them again from the seed
+            # (helpers.seeded_inputs); an output equal to its input is not stored either, and
+            # the truth only where it differs from the Float64 oracle's result
+            outs = []
+            for (a, kind, v), h, t in zip(args, case.host, truth["arrays"]):
+                if not isinstance(v, np.ndarray):
                     continue
-                key = f"{fname}/{si}"
-                # inputs are not stored: the test draws them again from the seed
-                # (helpers.seeded_inputs); an output equal to its input is not stored either, and
-                # the truth only where it differs from the Float64 oracle's result
-                outs = []
-                for (a, kind, v), h, t in zip(args, case.host, truth["arrays"]):
-                    if not isinstance(v, np.ndarray):
-                        continue
-                    if kind == "Ai":
-                        arrays[f"{key}/in/{a}"] = v
-                    if np.array_equal(np.ravel(v, order="F"), np.ravel(h, order="F")):
-                        continue
-                    outs.append(a)
-                    arrays[f"{key}/out/{a}"] = np.ravel(h, order="F")
-                    tt = np.ravel(np.asarray(t, dtype=np.float64) if kind == "Af" else t, order="F")
-                    if not np.array_equal(tt, arrays[f"{key}/out/{a}"]):
-                        arrays[f"{key}/truth/{a}"] = tt
-                for (s_, _), h, t in zip(stacks, case.stack_h, truth["stacks"]):
-                    arrays[f"{key}/out/{s_}"] = h
-                    tt = np.asarray(t, dtype=np.float64) if h.dtype != np.int64 else t
-                    if not np.array_equal(tt, h, equal_nan=True):
-                        arrays[f"{key}/truth/{s_}"] = tt
-                pos = {a: k for k, (a, _) in enumerate(lib_o.infos[fname].args)}
-                meta.append(dict(
-                    key=key, name=name, mode=mode, fname=fname, ints=ints, seed=f"refcorpus-{fname}-{si}",
-                    args=[[a, kind, (list(v.shape) if isinstance(v, np.ndarray) else v), pos[a]] for a, kind, v in args],
-                    outs=outs, stacks=[[s_, n, k] for s_, (n, k) in stacks],
-                    ret=[float(x) for x in case.ret_h], ret_truth=[float(x) for x in truth["ret"]],
-                    ))
-                print(f"{key}: {len(args)} arguments, {len(stacks)} stacks, plan {low.plan(fname)}")
+                if kind == "Ai":
+                    arrays[f"{key}/in/{a}"] = v
+                if np.array_equal(np.ravel(v, order="F"), np.ravel(h, order="F")):
+                    continue
+                outs.append(a)
+                arrays[f"{key}/out/{a}"] = np.ravel(h, order="F")
+                tt = np.ravel(np.asarray(t, dtype=np.float64) if kind == "Af" else t, order="F")
+                if not np.array_equal(tt, arrays[f"{key}/out/{a}"]):
+                    arrays[f"{key}/truth/{a}"] = tt
+            for (s_, _), h, t in zip(stacks, case.stack_h, truth["stacks"]):
+                arrays[f"{key}/out/{s_}"] = h
+                tt = np.asarray(t, dtype=np.float64) if h.dtype != np.int64 else t
+                if not np.array_equal(tt, h, equal_nan=True):
+                    arrays[f"{key}/truth/{s_}"] = tt
+            pos = {a: k for k, (a, _) in enumerate(lib_o.infos[fname].args)}
+            meta.append(dict(
+                key=key, name=name, mode=mode, fname=fname, ints=ints, seed=f"refcorpus-{fname}-{si}",
+                args=[[a, kind, (list(v.shape) if isinstance(v, np.ndarray) else v), pos[a]] for a, kind, v in args],
+                outs=outs, stacks=[[s_, n, k] for s_, (n, k) in stacks],
+                ret=[float(x) for x in case.ret_h], ret_truth=[float(x) for x in truth["ret"]],
+                ))
+            log.append(f"{key}: {len(args)} arguments, {len(stacks)} stacks")
+    return meta, arrays, log
+
+
+def main() -> None:
+    import concurrent.futures as cf
+    names = corpus_names()
+    meta, arrays = [], {}
+    with cf.ThreadPoolExecutor(8) as ex:
+        for name, (m, a, log) in zip(names, ex.map(one_kernel, names)):
+            meta += m
+            arrays.update(a)
+            for line in log:
+                print(line, flush=True)
     (HERE / "ref_corpus.json").write_text(json.dumps(meta, indent=1))
     np.savez_compressed(HERE / "ref_corpus.npz", **arrays)
-    print(f"{len(meta)} cases")
+    print(f"{len(meta)} cases from {len({m['name'] for m in meta})} of {len(names)} kernels")
 
 
 if __name__ == "__main__":

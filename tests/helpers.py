@@ -65,7 +65,7 @@ def seeded_inputs(specs, ints: dict, seed: str, int_arrays: dict | None = None, 
         elif kind == "f":
             out.append((a, kind, float(jrng.val_normal(jrng.Xoshiro(base + pos)))))
         elif kind == "Ai":
-            out.append((a, kind, np.asarray(int_arrays[a], dtype=np.int64).copy()))
+            out.append((a, kind, np.array(int_arrays[a], dtype=np.int64, order="F")))
         else:
             shp = tuple(shp)
             v = jrng.val_randn(jrng.Xoshiro(base + pos), int(np.prod(shp))).astype(fdt)
@@ -113,7 +113,7 @@ def make_args(lib, fname: str, shapes: dict, ints: dict, scalars: dict, seed: st
             else:
                 out.append((a, kind, float(jrng.val_normal(jrng.Xoshiro(base + pos)))))
         elif kind == "Ai":
-            out.append((a, kind, np.asarray(int_arrays[a], dtype=np.int64).copy()))
+            out.append((a, kind, np.array(int_arrays[a], dtype=np.int64, order="F")))
         else:
             shp = shapes[a]
             shp = shp if isinstance(shp, tuple) else (shp,)

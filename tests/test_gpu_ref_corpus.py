@@ -1,11 +1,11 @@
 """The general lowering on the reference's own generated code, on the GPU.
 
 The reference's committed generated files (/root/reference/test/val-corpus: adjoint, tangent
-and HVP of 15 kernels covering flattened nests, div/mod indices, scatter-accumulate, stencils,
-indexed stacks, branch stacks and scalar returns; the oracle tests' set) are lowered by
-`build()` where the reference is mounted, into stade.jl_amd/lib/gen/ with an index of their
-entry points.  The expected results are fixtures (tests/golden/make_ref_corpus.py): the
-oracle's outputs on seeded inputs at two sizes per kernel, and the 80-bit truth where it
+and HVP of every kernel the fixture script can size and run, 352 files of 138 kernels) are
+lowered by `build()` where the reference is mounted, into stade.jl_amd/lib/gen/ with an index
+of their entry points.  The expected results are fixtures (tests/golden/make_ref_corpus.py):
+the oracle's outputs on seeded inputs (two sizes for the kernels the oracle tests size, the
+size the reference's validator rule finds for the others), and the 80-bit truth where it
 differs.  Each case draws the same inputs from the seed, runs the lowered library through its C
 entry point, and compares every output argument, stack and returned scalar with the parity
 bars (fp64 1e-12, integers exact) and the truth rule.  The reference's text is not read here."""
