@@ -31,7 +31,10 @@ semantics for the subset STADE emits (the kernel language of
 
 Type inference follows the four shapes of STADE's `shape_infer` (/root/reference/src/
 STADE.jl:936): Float, Int, Array{Float}, Array{Int}, decided from use (index
-positions, loop bounds, `div`/`mod` operands and integer literals make Int).
+positions, loop bounds, `div`/`mod` operands and integer literals make Int; a local assigned
+only Ints, itself included, is an Int, as Julia types `c = 0; c = c + 1`).  What a file's
+`initstacks_*` returns types the trailing arguments of its `_b` / `_hv` functions (arrays
+with their element type, counts as Int), also where the body never reads them.
 """
 from __future__ import annotations
 
@@ -689,8 +692,15 @@ class FuncTypes:
             for nm, rhss in assigns.items():
                 if nm in self.fixed or nm in self.arrays:
                     continue
-                ts = {self.etype(r) for r in rhss}
                 cur = self.scalars.get(nm, "?")
+                # a counter (`c = 0`, then `c = c + 1`) is an Int in Julia: while its type is
+                # open, its own reads count as Int (the type only widens, so this settles)
+                if cur == "?":
+                    self.scalars[nm] = "i"
+                    ts = {self.etype(r) for r in rhss}
+                    self.scalars[nm] = cur
+                else:
+                    ts = {self.etype(r) for r in rhss}
                 if "f" in ts:
                     new = "f"
                 elif ts <= {"i"}:
@@ -1178,11 +1188,25 @@ def transpile(src: str, precision: str = "f64", bounds_check: bool = False,
     arg_types = arg_types or {}
     # stacks allocated by initstacks_* keep their element type when they are arguments of *_b / *_hv
     known: dict[str, str] = {}
+    # everything initstacks_* returns is a trailing argument of *_b / *_hv: arrays with their
+    # element type, and Int64 counts (`__tot_*`, `__len_*`), typed so even where unread
+    init_ret: dict[str, str] = {}
     for f in funcs:
         if f.name.startswith("initstacks_"):
             ft = FuncTypes(f)
             for a, t in ft.allocs.items():
                 known[a] = t
+            for st in f.body:
+                if st[0] == "return" and st[1] is not None:
+                    items = st[1][1] if st[1][0] == "tuple" else [st[1]]
+                    for it in items:
+                        if it[0] != "var":
+                            continue
+                        nm = it[1]
+                        if nm in ft.arrays:
+                            init_ret[nm] = "A" + ft.arrays[nm]
+                        else:
+                            init_ret[nm] = ft.scalars.get(nm, "i")
     # a shadow argument (`xd`, `xb`, `xbd`) has the shape of its primal even where the derivative
     # code never touches it (a dead tangent): first pass collects every array name in the file
     arrays_by_name: dict[str, str] = dict(known)
@@ -1198,6 +1222,10 @@ def transpile(src: str, precision: str = "f64", bounds_check: bool = False,
             continue
         seen.add(f.name)
         hints = dict(arg_types.get(f.name) or {})
+        if not f.name.startswith("initstacks_"):
+            for a in f.args:
+                if a in init_ret and a not in hints:
+                    hints[a] = init_ret[a]
         probe = FuncTypes(f, known_arrays=known, arg_types=hints)
         for a in f.args:
             if a in probe.arrays or a in hints:

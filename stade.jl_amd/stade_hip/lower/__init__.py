@@ -8,5 +8,5 @@ the reference's `cgen_body` / `cgen_device_assign` / `cgen_emit` pipeline
 (/root/reference/src/STADE.jl:10409-12111), redesigned around one MI355X; the five benchmark
 kernels keep their hand-written entry points in libstade_hip.so.
 """
-from .runtime import LoweredLib, build_source, initstacks, lower  # noqa: F401
+from .runtime import LoweredLib, build_source, initstacks, initstacks_returns, lower, run_initstacks  # noqa: F401
 from .syntax import LowerError  # noqa: F401

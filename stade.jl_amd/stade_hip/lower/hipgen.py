@@ -1240,6 +1240,14 @@ def generate(text: str, precision: str = "f64", arg_types: dict | None = None) -
             for s in walk_stmts(f.body):
                 if isinstance(s, Assign) and isinstance(s.lhs, Var) and isinstance(s.rhs, Alloc):
                     stack_kinds[s.lhs.name] = "Ai" if s.rhs.eltype == "Int64" else "Af"
+            # what it returns besides arrays are Int64 counts (`__tot_*`, `__mult_*`, `__len_*`),
+            # passed on as the trailing arguments even where the body never reads them
+            ti = infer_types(f, None, precision)
+            for s in walk_stmts(f.body):
+                if isinstance(s, Return) and s.value is not None:
+                    for it in (s.value.items if isinstance(s.value, Tup) else (s.value,)):
+                        if isinstance(it, Var) and it.name not in stack_kinds and it.name not in ti.arrays:
+                            stack_kinds[it.name] = ti.scalars.get(it.name, "i")
     for f in funcs:
         if f.name.startswith("initstacks_"):
             continue

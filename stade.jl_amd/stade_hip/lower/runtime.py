@@ -23,7 +23,8 @@ import threading
 from pathlib import Path
 
 from . import hipgen
-from .syntax import Alloc, Assign, Bin, Call, LowerError, Nothing_, Num, Return, Tup, Un, Var, parse
+from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, If, LowerError, Nothing_, Num, Ref,
+                     Return, Tup, Un, Var, While, parse)
 
 PKG = Path(__file__).resolve().parent.parent.parent
 GEN_LIB = PKG / "lib" / "gen"
@@ -255,3 +256,228 @@ def initstacks(text: str, name: str, *int_args) -> list[tuple[str, str, int]]:
                 if isinstance(it, Var) and it.name in allocs:
                     ret.append((it.name, *allocs[it.name]))
     return ret
+
+
+# ------------------------------------------------------------------------------------------
+# initstacks_* run on the host in full: loops, branches, index arrays and scalar returns
+# ------------------------------------------------------------------------------------------
+
+class _Return(Exception):
+    def __init__(self, value):
+        self.value = value
+
+
+class _Break(Exception):
+    pass
+
+
+class _Continue(Exception):
+    pass
+
+
+def initstacks_returns(text: str, name: str) -> list[str]:
+    """Names of what `initstacks_<k>_b` returns, in order: the trailing arguments of the
+    generated `<k>_b` / `<k>_hv` (stacks, then any index arrays and Int64 counts)."""
+    f = next((g for g in parse(text) if g.name == name), None)
+    if f is None:
+        raise LowerError(f"no function {name}")
+    for st in f.body:
+        if isinstance(st, Return) and st.value is not None and not isinstance(st.value, Nothing_):
+            items = st.value.items if isinstance(st.value, Tup) else (st.value,)
+            if not all(isinstance(it, Var) for it in items):
+                raise LowerError(f"{name}: returns an expression, not named values")
+            return [it.name for it in items]
+    return []
+
+
+def run_initstacks(text: str, name: str, args: dict, max_iters: int = 1 << 26) -> list[tuple[str, object]]:
+    """Run `initstacks_<k>_b` on the host with its arguments' values (`args`: Int64 and float
+    scalars by name, arrays as numpy arrays where it takes their `length`), and return its
+    returned values [(name, value)] in order: stacks as zero-filled numpy arrays (the
+    generated code writes every slot before reading it), index arrays (`prefix_*`, `val_*`)
+    with the values it computed, Int64 counts as ints.  Julia's semantics for what these
+    functions use: Int64 and Float64 arithmetic, `div` (truncating), `mod` (the divisor's
+    sign), `max`, `min`, `length`, 1-based element stores, counted loops, `if`/`elseif`.
+    Same role as the generated function in the reference (`agen_init_emit`
+    /root/reference/src/STADE.jl:4011-4097); its calls run there in Julia on the host."""
+    import numpy as np
+    f = next((g for g in parse(text) if g.name == name), None)
+    if f is None:
+        raise LowerError(f"no function {name}")
+    missing = [a for a in f.args if a not in args]
+    if missing:
+        raise LowerError(f"{name}: no value for {', '.join(missing)}")
+    env = {a: args[a] for a in f.args}
+    budget = [max_iters]
+
+    def num(e: Num):
+        if e.text in ("true", "false"):
+            return e.text == "true"
+        t = e.text.replace("_", "")
+        return int(t, 0) if e.is_int else float(t)
+
+    def idiv(a, b):
+        if isinstance(a, int) and isinstance(b, int):
+            q = abs(a) // abs(b)
+            return q if (a >= 0) == (b >= 0) else -q
+        import math
+        return math.trunc(a / b)
+
+    def call(e: Call):
+        fn = e.fn
+        if fn == "length":
+            return int(np.size(ev(e.args[0])))
+        if fn == "size":
+            return int(np.shape(ev(e.args[0]))[ev(e.args[1]) - 1])
+        xs = [ev(x) for x in e.args]
+        if fn == "div":
+            return idiv(*xs)
+        if fn == "mod":
+            return xs[0] % xs[1]
+        if fn == "rem":
+            return xs[0] - idiv(xs[0], xs[1]) * xs[1]
+        if fn in ("max", "min"):
+            return (max if fn == "max" else min)(xs)
+        if fn == "abs":
+            return abs(xs[0])
+        if fn in ("Int", "Int64") and len(xs) == 1:
+            v = xs[0]
+            if isinstance(v, float) and not v.is_integer():
+                raise LowerError(f"{name}: InexactError converting {v} to Int64")
+            return int(v)
+        if fn in ("floor", "ceil", "round", "trunc"):
+            import math
+            v = xs[-1]
+            r = {"floor": math.floor, "ceil": math.ceil, "trunc": math.trunc,
+                 "round": lambda x: int(np.round(x))}[fn](v)
+            return int(r) if len(xs) == 2 else float(r)
+        if fn in ("Float64", "float"):
+            return float(xs[0])
+        raise LowerError(f"{name}: cannot run {fn}(...) on the host")
+
+    def ev(e):
+        if isinstance(e, Num):
+            return num(e)
+        if isinstance(e, Var):
+            if e.name not in env:
+                raise LowerError(f"{name}: {e.name} is read before it is set")
+            return env[e.name]
+        if isinstance(e, Ref):
+            a = env[e.name]
+            ix = [ev(x) for x in e.idx]
+            return a.ravel(order="F")[_linear(a, ix)].item()
+        if isinstance(e, Un):
+            v = ev(e.a)
+            return (not v) if e.op == "!" else -v
+        if isinstance(e, Bin):
+            if e.op == "&&":
+                return bool(ev(e.a)) and bool(ev(e.b))
+            if e.op == "||":
+                return bool(ev(e.a)) or bool(ev(e.b))
+            x, y = ev(e.a), ev(e.b)
+            op = e.op
+            if op == "+":
+                return x + y
+            if op == "-":
+                return x - y
+            if op == "*":
+                return x * y
+            if op == "/":
+                return x / y
+            if op == "^":
+                return x ** y
+            return {"==": x == y, "!=": x != y, "<": x < y, ">": x > y, "<=": x <= y, ">=": x >= y}[op]
+        if isinstance(e, Call):
+            return call(e)
+        if isinstance(e, Alloc):
+            n = ev(e.n)
+            return np.zeros(max(0, int(n)), dtype=np.int64 if e.eltype == "Int64" else np.float64)
+        if isinstance(e, Tup):
+            return tuple(ev(x) for x in e.items)
+        if isinstance(e, Nothing_):
+            return None
+        raise LowerError(f"{name}: cannot evaluate {type(e).__name__} on the host")
+
+    def _linear(a, ix):
+        k, stride = 0, 1
+        shape = a.shape if a.ndim else (1,)
+        for d, i in enumerate(ix):
+            ext = shape[d] if d < len(shape) else 1
+            if not 1 <= i <= (ext if d < len(ix) - 1 else int(np.prod(shape[d:]))):
+                raise LowerError(f"{name}: index {i} out of bounds for {a.shape}")
+            k += (i - 1) * stride
+            stride *= ext
+        return k
+
+    def tick():
+        budget[0] -= 1
+        if budget[0] < 0:
+            raise LowerError(f"{name}: more than {max_iters} loop iterations")
+
+    def run(stmts):
+        for st in stmts:
+            if isinstance(st, Assign):
+                v = ev(st.rhs)
+                if isinstance(st.lhs, Var):
+                    env[st.lhs.name] = v
+                else:
+                    a = env[st.lhs.name]
+                    ix = [ev(x) for x in st.lhs.idx]
+                    flat = a.reshape(-1, order="F")
+                    if not np.shares_memory(flat, a):
+                        raise LowerError(f"{name}: {st.lhs.name} is not contiguous")
+                    flat[_linear(a, ix)] = v
+            elif isinstance(st, For):
+                r = st.rng
+                lo, hi = ev(r.lo), ev(r.hi)
+                step = 1 if r.step is None else ev(r.step)
+                i = lo
+                while (step > 0 and i <= hi) or (step < 0 and i >= hi):
+                    tick()
+                    env[st.var] = i
+                    try:
+                        run(st.body)
+                    except _Continue:
+                        pass
+                    except _Break:
+                        break
+                    i += step
+            elif isinstance(st, While):
+                while ev(st.cond):
+                    tick()
+                    try:
+                        run(st.body)
+                    except _Continue:
+                        pass
+                    except _Break:
+                        break
+            elif isinstance(st, If):
+                for cond, body in st.branches:
+                    if ev(cond):
+                        run(body)
+                        break
+                else:
+                    if st.orelse:
+                        run(st.orelse)
+            elif isinstance(st, Return):
+                raise _Return(None if st.value is None else ev(st.value))
+            elif isinstance(st, Break):
+                raise _Break()
+            elif isinstance(st, Continue):
+                raise _Continue()
+            elif isinstance(st, ExprStmt):
+                ev(st.e)
+            else:
+                raise LowerError(f"{name}: cannot run {type(st).__name__} on the host")
+
+    try:
+        run(f.body)
+        value = None
+    except _Return as r:
+        value = r.value
+    names = initstacks_returns(text, name)
+    vals = value if isinstance(value, tuple) else (() if value is None else (value,))
+    if len(vals) != len(names):
+        raise LowerError(f"{name}: returned {len(vals)} values for {len(names)} names")
+    return list(zip(names, vals))
+

@@ -168,17 +168,31 @@ def one_kernel(name: str):
         except Exception as e:  # noqa: BLE001
             log.append(f"skip {fname}: oracle: {str(e)[:160]}")
             continue
-        for si, (ints, shapes, int_arrays) in enumerate(sizes):
+        for si, (ints0, shapes, int_arrays) in enumerate(sizes):
             try:
-                stacks = []
-                if mode != "d" and stack_fn in lib_o.infos:
-                    sargs = [ints[a] for a, _ in lib_o.infos[stack_fn].args]
-                    stacks = [(s_, (n, "Ai" if et == "Int64" else "Af"))
-                              for s_, et, n in lower.initstacks(text, stack_fn, *sargs)]
+                ints, zeros = dict(ints0), []
                 shp = _shapes_all(shapes)
-                shp["__stacks__"] = tuple(s_ for s_, _ in stacks)
+                trailing = lower.initstacks_returns(text, stack_fn) if mode != "d" and stack_fn in lib_o.infos else []
+                shp["__stacks__"] = tuple(trailing)
                 args = make_args(lib_o, fname, shp, ints, {}, f"refcorpus-{fname}-{si}", np.float64,
                                  int_arrays=int_arrays)
+                if trailing:
+                    # what initstacks returns (stacks, index arrays, Int64 counts) are the trailing
+                    # arguments: run it on the host with the case's own values, stacks zero-filled
+                    vals = {a: v for a, _, v in args}
+                    sargs = {a: ints.get(a, vals.get(a)) for a, _ in lib_o.infos[stack_fn].args}
+                    for nm, v in lower.run_initstacks(text, stack_fn, sargs):
+                        if isinstance(v, np.ndarray):
+                            kind = "Ai" if v.dtype == np.int64 else "Af"
+                            if kind == "Af":
+                                zeros.append(nm)
+                            args.append((nm, kind, v))
+                        else:
+                            ints[nm] = int(v)
+                            args.append((nm, "i", int(v)))
+                if [a for a, _, _ in args] != [a for a, _ in lib_o.infos[fname].args]:
+                    raise TypeError(f"{fname}: the arguments do not line up with the signature")
+                stacks = []
                 case = ParityCase(name, mode, args, stacks, "f64", oracle_path=path)
                 case.run_oracle(lib_o)
                 truth = case.run_truth()
@@ -210,7 +224,7 @@ def one_kernel(name: str):
                     arrays[f"{key}/truth/{s_}"] = tt
             pos = {a: k for k, (a, _) in enumerate(lib_o.infos[fname].args)}
             meta.append(dict(
-                key=key, name=name, mode=mode, fname=fname, ints=ints, seed=f"refcorpus-{fname}-{si}",
+                key=key, name=name, mode=mode, fname=fname, ints=ints, zeros=zeros, seed=f"refcorpus-{fname}-{si}",
                 args=[[a, kind, (list(v.shape) if isinstance(v, np.ndarray) else v), pos[a]] for a, kind, v in args],
                 outs=outs, stacks=[[s_, n, k] for s_, (n, k) in stacks],
                 ret=[float(x) for x in case.ret_h], ret_truth=[float(x) for x in truth["ret"]],

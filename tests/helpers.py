@@ -51,11 +51,13 @@ def normal(seed_name: str, n: int, salt: int = 0) -> np.ndarray:
     return jrng.val_randn(g, n)
 
 
-def seeded_inputs(specs, ints: dict, seed: str, int_arrays: dict | None = None, fdt=np.float64) -> list:
+def seeded_inputs(specs, ints: dict, seed: str, int_arrays: dict | None = None, fdt=np.float64,
+                  zeros=()) -> list:
     """The inputs `make_args` draws, from stored argument specs [(name, kind, shape or value,
     position in the generated signature)]: N(0,1) from Julia's Xoshiro stream seeded with
-    val_stable_seed(seed) + position.  Used where the generated text (and so the oracle's
-    argument table) is not available, with fixtures written by make_args."""
+    val_stable_seed(seed) + position; the float arrays named in `zeros` (stacks) zero-filled.
+    Used where the generated text (and so the oracle's argument table) is not available, with
+    fixtures written by make_args."""
     from oracle import rng as jrng
     base = jrng.val_stable_seed(seed)
     out = []
@@ -66,6 +68,8 @@ def seeded_inputs(specs, ints: dict, seed: str, int_arrays: dict | None = None, 
             out.append((a, kind, float(jrng.val_normal(jrng.Xoshiro(base + pos)))))
         elif kind == "Ai":
             out.append((a, kind, np.array(int_arrays[a], dtype=np.int64, order="F")))
+        elif a in zeros:
+            out.append((a, kind, np.zeros(tuple(shp), dtype=fdt, order="F")))
         else:
             shp = tuple(shp)
             v = jrng.val_randn(jrng.Xoshiro(base + pos), int(np.prod(shp))).astype(fdt)

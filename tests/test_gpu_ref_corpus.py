@@ -1,7 +1,7 @@
 """The general lowering on the reference's own generated code, on the GPU.
 
 The reference's committed generated files (/root/reference/test/val-corpus: adjoint, tangent
-and HVP of every kernel the fixture script can size and run, 352 files of 138 kernels) are
+and HVP of every kernel the fixture script can size and run, 414 files of 138 kernels) are
 lowered by `build()` where the reference is mounted, into stade.jl_amd/lib/gen/ with an index
 of their entry points.  The expected results are fixtures (tests/golden/make_ref_corpus.py):
 the oracle's outputs on seeded inputs (two sizes for the kernels the oracle tests size, the
@@ -51,7 +51,7 @@ def test_lowered_reference_kernel(case):
     sig["args"] = [tuple(x) for x in sig["args"]]
     low = LoweredLib(GEN / entry["lib"], {fname: sig}, "f64", None)
     ia = {a: z[f"{key}/in/{a}"] for a, kind, _, _ in case["args"] if kind == "Ai"}
-    args = seeded_inputs(case["args"], case["ints"], case["seed"], ia)
+    args = seeded_inputs(case["args"], case["ints"], case["seed"], ia, zeros=case.get("zeros", ()))
     stacks = [(s, (n, k)) for s, n, k in case["stacks"]]
     dims = {a: v.shape for a, _, v in args if isinstance(v, np.ndarray) and v.ndim > 1}
     print(f"reference {key}: {len(args)} arguments, plan {sig.get('plan')}", flush=True)

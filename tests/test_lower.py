@@ -212,10 +212,12 @@ def test_ref_corpus_fixture_inputs_reproduce():
     for case in meta[::7]:
         lib_o = runner.load(REF_CORPUS / f"{case['fname']}.jl")
         ia = {a: z[f"{case['key']}/in/{a}"] for a, kind, _, _ in case["args"] if kind == "Ai"}
-        got = seeded_inputs(case["args"], case["ints"], case["seed"], ia)
+        got = seeded_inputs(case["args"], case["ints"], case["seed"], ia, zeros=case.get("zeros", ()))
         shapes = {a: tuple(s) for a, kind, s, _ in case["args"] if kind == "Af"}
         shapes["__stacks__"] = tuple(s for s, _, _ in case["stacks"])
         want = make_args(lib_o, case["fname"], shapes, case["ints"], {}, case["seed"], np.float64, ia)
+        # the stacks initstacks returns are zero-filled
+        want = [(a, k, np.zeros_like(v, order="F") if a in case.get("zeros", ()) else v) for a, k, v in want]
         assert [a for a, _, _ in got] == [a for a, _, _ in want]
         for (a, _, g), (_, _, w) in zip(got, want):
             assert np.array_equal(np.asarray(g), np.asarray(w)), f"{case['key']}: input {a} differs"
