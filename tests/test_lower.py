@@ -246,3 +246,30 @@ def test_reference_corpus_compiles(tmp_path):
     with cf.ThreadPoolExecutor(8) as ex:
         bad = [r for r in ex.map(one, files) if r]
     assert len(files) >= 400 and not bad, bad
+
+
+@pytest.mark.skipif(not REF_CORPUS.exists(), reason="reference corpus not mounted")
+@pytest.mark.parametrize("name, args", [
+    ("advection", dict(i_nnode=8, i_nstep=3)),
+    ("coarsen_retire", dict(levels=4, n=9)),
+    ("windowed_relax_retire", dict(dx=0.25, num_passes=5, w0=6)),
+    ("cascadic_mg_prolong", dict(h_coarse=0.5, nu=3, num_levels=4)),
+])
+def test_run_initstacks_matches_the_oracle(name, args):
+    """lower.run_initstacks (initstacks_* run on the host with loops, branches, prefix index
+    arrays and Int64 counts) against the same function transpiled by the oracle: every
+    returned array's length and every returned count."""
+    from oracle import runner
+    from stade_hip import lower
+    path = REF_CORPUS / f"{name}_b.jl"
+    fn = f"initstacks_{name}_b"
+    got = lower.run_initstacks(path.read_text(), fn, args)
+    lib = runner.load(path)
+    want = lib.call(fn, *(args[a] for a, _ in lib.infos[fn].args))
+    assert len(got) == len(want) and len(got) > 0
+    for (nm, v), w in zip(got, want):
+        if isinstance(w, tuple):
+            assert isinstance(v, np.ndarray) and v.size == w[0], (nm, v, w)
+            assert (v.dtype == np.int64) == (w[1] == "Ai"), (nm, v.dtype, w)
+        else:
+            assert v == w, (nm, v, w)
