@@ -13,9 +13,10 @@
 // steps are a prefix 1..nrun of the loop.
 //
 // Kernels (one block owns S consecutive cells and carries a K-cell halo on each side):
-//   * forward chunk: K time steps in LDS (the valid region shrinks by one cell per step), the
-//     owned part of every state written to the tape; HBM traffic is the tape rows (written
-//     once) plus one state read and write per chunk.
+//   * forward chunk: K time steps with the state in registers and neighbours by DPP (the
+//     valid region shrinks by one cell per step), the owned part of every state written to
+//     the tape; HBM traffic is the tape rows (written once) plus one state read and write per
+//     chunk.
 //   * backward init: w = unb + (ub + (2 u_T) lossb), loss += sum u_T^2, unb = 0 (pointwise).
 //   * backward chunk: K steps of the transposed stencil in gathered (owner-computes) form,
 //     reading tape rows.  The generated per-cell update is evaluated in a factored form with
@@ -37,16 +38,22 @@ namespace {
 constexpr int NT = 256, KMAX = 32;
 constexpr int kInitBlockCells = NT * 8;  // cells per block of the backward init kernel
 #ifndef STADE_BURG_FT
-#define STADE_BURG_FT 1024
+#define STADE_BURG_FT 512
 #endif
 #ifndef STADE_BURG_FS
 #define STADE_BURG_FS 4096
 #endif
-// forward chunk kernel: threads and owned cells per block.  512 / 2048, 256 / 1024 and
-// 1024 / 2048 measured within 1 % of 1024 / 4096 for the adjoint, tangent and HVP (as did
-// backward HVP blocks of 256 / 1024, 1024 / 2048 and 512 / 2048 against 512 / 1024)
+#ifndef STADE_BURG_FS_NOTAPE
+#define STADE_BURG_FS_NOTAPE 1024
+#endif
+// forward chunk kernel (register form): threads and owned cells per block.  With a tape to
+// write (adjoint, HVP, checkpoints) 512 / 4096: against the LDS form it replaced (1024 /
+// 4096), the HVP 3-6 % faster and the adjoint 0-2 %; 1024 / 4096, 256 / 4096 and 512 / 2048
+// measured between the two.  The tangent, which writes no tape and is bound by its fp64
+// arithmetic, 512 / 1024: 20 % faster than the LDS form (512 / 2048 17 %, 1024 / 4096 13 %).
 constexpr int BNT = STADE_BURG_FT;
 constexpr int FWD_S = STADE_BURG_FS;
+constexpr int FWD_S_NOTAPE = STADE_BURG_FS_NOTAPE;
 #ifndef STADE_BURG_BT
 #define STADE_BURG_BT 512
 #endif
@@ -86,50 +93,111 @@ __device__ __forceinline__ double step_ud(double um, double uc, double up, doubl
 }
 
 // ---------------------------------------------------------------------------------------
-// forward: `nk` steps starting at 0-based step t0, from src (+ srcd) to dst (+ dstd)
+// forward: `nk` steps starting at 0-based step t0, from src (+ srcd) to dst (+ dstd), with the
+// state in registers.  Thread t holds positions e = t + i * T (slot i) of the extended region [x0 - KMAX, x0 + S + KMAX);
+// the neighbours e -/+ 1 are the adjacent lanes (DPP wavefront shifts), and a wave's two end
+// lanes take theirs from the end lanes the waves publish in a small LDS array, double
+// buffered by step: one barrier a step and no LDS traffic for the interior.  Any nk <= KMAX
+// (the owned cells stay valid for KMAX steps; the region's ends go stale one cell a step).
 // ---------------------------------------------------------------------------------------
-template <bool TAN, int S>
-__global__ __launch_bounds__(BNT) void fwd_kernel(const double* __restrict__ src, const double* __restrict__ srcd,
-                                                 double* __restrict__ dst, double* __restrict__ dstd,
-                                                 double* __restrict__ tape, double* __restrict__ taped, int n, int64_t t0,
-                                                 int nk, Coef c, int64_t row0, int every) {
+template <bool TAN, int S, int T>
+__global__ __launch_bounds__(T) void fwd_reg_kernel(const double* __restrict__ src, const double* __restrict__ srcd,
+                                                    double* __restrict__ dst, double* __restrict__ dstd,
+                                                    double* __restrict__ tape, double* __restrict__ taped, int n, int64_t t0,
+                                                    int nk, Coef c, int64_t row0, int every) {
     constexpr int L = S + 2 * KMAX;
-    __shared__ double A[2][L];
-    __shared__ double D[TAN ? 2 : 1][TAN ? L : 1];
+    constexpr int M = (L + T - 1) / T, NWV = T / 64;
+    constexpr int NA = TAN ? 2 : 1;  // exchanged arrays: u (+ ud)
+    static_assert(L - (M - 1) * T <= 64, "the last slot belongs to wave 0 alone");
+    __shared__ double edge[2][NA][M][NWV][2];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int x0 = blockIdx.x * S;
-    const int len = nk == 0 ? S : S + 2 * nk;  // extended region [x0 - nk, x0 + S + nk)
     const int own = min(S, n - x0);
-    for (int e = threadIdx.x; e < len; e += BNT) {
-        int x = wrapn(x0 - nk + e, n);
-        A[0][e] = src[x];
-        if (TAN) D[0][e] = srcd[x];
+    int xc[M], eo[M];
+    bool owned[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = threadIdx.x + i * T;
+        xc[i] = wrapn(x0 - KMAX + min(e, L - 1), n);
+        owned[i] = e >= KMAX && e < KMAX + own;
+        int si, sv, ss;
+        if (lane == 0) {
+            ss = 1;
+            sv = wave > 0 ? wave - 1 : NWV - 1;
+            si = wave > 0 ? i : max(i - 1, 0);
+        } else {
+            ss = 0;
+            sv = wave < NWV - 1 ? wave + 1 : 0;
+            si = wave < NWV - 1 ? i : min(i + 1, M - 1);
+        }
+        eo[i] = (si * NWV + sv) * 2 + ss;
     }
-    __syncthreads();
-    int cur = 0;
-    for (int k = 0; k < nk; ++k) {
-        // the state at the start of step t0 + k goes to tape row (t0 + k - row0) / every when
-        // every divides t0 + k - row0 (every = 1, row0 = 0: the generated stack's layout)
-        const int64_t tr = t0 + k - row0;
-        const size_t row = (size_t)(tr / every) * (size_t)n;
-        if (tape && tr % every == 0) {
-            for (int e = threadIdx.x; e < own; e += BNT) {
-                // streaming stores: a tape row is read back only by the reverse sweep (plain
-                // stores measured 1 % slower over an evaluation, the reverse sweep's reads too)
-                __builtin_nontemporal_store(A[cur][nk + e], &tape[row + x0 + e]);
-                if (TAN && taped) __builtin_nontemporal_store(D[cur][nk + e], &taped[row + x0 + e]);
+    auto edge_at = [&](int buf, int a, int i) { return (&edge[buf][a][0][0][0])[eo[i]]; };
+    double u[M], ud[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        u[i] = src[xc[i]];
+        ud[i] = TAN ? srcd[xc[i]] : 0.0;
+    }
+    auto publish = [&](int buf) {
+        if (lane == 0 || lane == 63) {
+            const int side = lane == 63;
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                edge[buf][0][i][wave][side] = u[i];
+                if constexpr (TAN) edge[buf][1][i][wave][side] = ud[i];
             }
         }
-        for (int e = k + 1 + threadIdx.x; e < len - k - 1; e += BNT) {
-            double um = A[cur][e - 1], uc = A[cur][e], up = A[cur][e + 1];
-            if (TAN) D[cur ^ 1][e] = step_ud(um, uc, up, D[cur][e - 1], D[cur][e], D[cur][e + 1], c);
-            A[cur ^ 1][e] = step_u(um, uc, up, c);
+    };
+    publish(0);
+    __syncthreads();
+    for (int k = 0; k < nk; ++k) {
+        const int buf = k & 1;
+        // the state at the start of step t0 + k goes to tape row (t0 + k - row0) / every when
+        // every divides t0 + k - row0 (every = 1, row0 = 0: the generated stack's layout);
+        // streaming stores: a tape row is read back only by the reverse sweep
+        const int64_t tr = t0 + k - row0;
+        if (tape && tr % every == 0) {
+            const size_t row = (size_t)(tr / every) * (size_t)n + (size_t)(x0 - KMAX);
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                if (owned[i]) {
+                    const size_t g = row + (size_t)(threadIdx.x + i * T);
+                    __builtin_nontemporal_store(u[i], &tape[g]);
+                    if (TAN && taped) __builtin_nontemporal_store(ud[i], &taped[g]);
+                }
+            }
         }
+        double un[M], udn[M];
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            un[i] = u[i];
+            udn[i] = ud[i];
+            if (i == M - 1 && wave != 0) continue;  // past the extended region (uniform)
+            const double uc = u[i], eu = edge_at(buf, 0, i);
+            const double um = from_west(uc, eu), up = from_east(uc, eu);
+            if constexpr (TAN) {
+                const double dc = ud[i], ed = edge_at(buf, 1, i);
+                udn[i] = step_ud(um, uc, up, from_west(dc, ed), dc, from_east(dc, ed), c);
+            }
+            un[i] = step_u(um, uc, up, c);
+        }
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            u[i] = un[i];
+            ud[i] = udn[i];
+        }
+        publish(buf ^ 1);
         __syncthreads();
-        cur ^= 1;
     }
-    for (int e = threadIdx.x; e < own; e += BNT) {
-        dst[x0 + e] = A[cur][nk + e];
-        if (TAN) dstd[x0 + e] = D[cur][nk + e];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        if (owned[i]) {
+            const int x = x0 + threadIdx.x + i * T - KMAX;
+            dst[x] = u[i];
+            if (TAN) dstd[x] = ud[i];
+        }
     }
 }
 
@@ -576,8 +644,8 @@ template <bool TAN>
 int32_t forward(const double* src, const double* srcd, double* fin, double* find, double* tape, double* taped, int n,
                 int64_t t_begin, int64_t t_end, const Coef& c, double* P, double* Q, double* Pd, double* Qd, hipStream_t stream,
                 int64_t row0 = 0, int every = 1) {
-    constexpr int S = FWD_S;
-    const unsigned nb = grid_for(n, S);
+    const bool notape = tape == nullptr;
+    const unsigned nb = grid_for(n, notape ? FWD_S_NOTAPE : FWD_S);
     const double *cs = src, *csd = srcd;
     int64_t t0 = t_begin;
     int flip = 0;
@@ -586,9 +654,16 @@ int32_t forward(const double* src, const double* srcd, double* fin, double* find
         bool last = t0 + nk >= t_end;
         double* d = last ? fin : (flip ? Q : P);
         double* dd = last ? find : (flip ? Qd : Pd);
-        STADE_TIMED(TAN ? "burgers1d_fwd_tan" : "burgers1d_fwd", stream,
-                    fwd_kernel<TAN, S><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c, row0, every));
-        STADE_LAUNCHED("burgers1d fwd_kernel");
+        if (notape) {
+            STADE_TIMED(TAN ? "burgers1d_fwd_tan" : "burgers1d_fwd", stream,
+                        fwd_reg_kernel<TAN, FWD_S_NOTAPE, BNT><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c,
+                                                                                        row0, every));
+        } else {
+            STADE_TIMED(TAN ? "burgers1d_fwd_tan" : "burgers1d_fwd", stream,
+                        fwd_reg_kernel<TAN, FWD_S, BNT><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c, row0,
+                                                                                 every));
+        }
+        STADE_LAUNCHED("burgers1d fwd_reg_kernel");
         cs = d;
         csd = dd;
         flip ^= 1;
