@@ -250,16 +250,45 @@ def _jl_call(spec: KernelSpec, fname: str, mode: Mode, stacks: list[tuple[str, s
     return "\n".join(lines)
 
 
-_ALLOC_RE = re.compile(r"\bVector\{(Float64|Float32|Int64)\}\(undef,")
-_ZEROS_RE = re.compile(r"(?<![\w.])zeros\((Float64|Float32|Int64),")
+_ALLOC_LINE_RE = re.compile(r"^(\s*)(\w+)\s*=\s*Vector\{(Float64|Float32|Int64|Int)\}\(undef,", re.M)
+_ZEROS_LINE_RE = re.compile(r"^(\s*)(\w+)\s*=\s*zeros\((Float64|Float32|Int64|Int),", re.M)
+_ELEM_WRITE_RE = re.compile(r"^\s*(\w+)\[[^\n=]*\]\s*(?:=|\+=|-=|\*=|/=)(?!=)", re.M)
 
 
 def _lowered_initstacks(fname: str, body: str, eltype: str) -> str:
-    """The generated `initstacks_<k>_b` with its host vectors allocated on the device
+    """The generated `initstacks_<k>_b` with its stacks allocated on the device
     (`cgen_stack_device_expr` /root/reference/src/STADE.jl:9798-9802); the size arithmetic
-    is kept as written."""
-    body = _ALLOC_RE.sub(lambda m: f"ROCArray{{{eltype if m.group(1) != 'Int64' else 'Int64'}}}(undef,", body)
-    body = _ZEROS_RE.sub(lambda m: f"AMDGPU.zeros({eltype if m.group(1) != 'Int64' else 'Int64'},", body)
+    is kept as written.  An array the function fills element by element (the prefix offsets
+    `prefix_*` and saved loop values `val_*` of indexed stacks) is filled in a host `Vector`,
+    as written, and uploaded where the function returns it: a device array cannot be written
+    element by element from the host, and the lowered kernels take device memory only."""
+    written = set(_ELEM_WRITE_RE.findall(body))
+
+    def dev_type(t: str) -> str:
+        return "Int64" if t in ("Int64", "Int") else eltype
+
+    def alloc(m):
+        ind, nm, t = m.group(1), m.group(2), m.group(3)
+        if nm in written:
+            return m.group(0)
+        return f"{ind}{nm} = ROCArray{{{dev_type(t)}}}(undef,"
+
+    def zeros_(m):
+        ind, nm, t = m.group(1), m.group(2), m.group(3)
+        if nm in written:
+            return m.group(0)
+        return f"{ind}{nm} = AMDGPU.zeros({dev_type(t)},"
+    body = _ALLOC_LINE_RE.sub(alloc, body)
+    body = _ZEROS_LINE_RE.sub(zeros_, body)
+    if written:
+        def ret(m):
+            items = [x.strip() for x in m.group(2).split(",")]
+            items = [f"ROCArray({x})" if x in written else x for x in items]
+            return f"{m.group(1)}return ({', '.join(items)})"
+        body = re.sub(r"^(\s*)return \((.*)\)\s*$", ret, body, flags=re.M)
+        body = re.sub(r"^(\s*)return (\w+)\s*$",
+                      lambda m: f"{m.group(1)}return ROCArray({m.group(2)})" if m.group(2) in written else m.group(0),
+                      body, flags=re.M)
     body = re.sub(rf"^function\s+{re.escape(fname)}\s*\(", f"function {fname}_hip(", body, count=1, flags=re.M)
     return body.rstrip()
 

@@ -226,6 +226,25 @@ def test_lowered_initstacks_allocate_on_the_device(tmp_path):
     assert "u_stack = ROCArray{Float64}(undef, " in out and "Vector{" not in out
 
 
+@pytest.mark.skipif(not REF_CORPUS.exists(), reason="reference corpus not mounted")
+def test_lowered_initstacks_fill_index_arrays_on_the_host():
+    """An initstacks_* that fills index arrays element by element (indexed stacks: prefix
+    offsets and saved loop values) keeps them host Vectors while it fills them and uploads them
+    where it returns them; its stacks are allocated on the device; its counts pass through."""
+    from stade_hip import emit
+    text = (REF_CORPUS / "windowed_relax_retire_b.jl").read_text()
+    _, body = emit._split_functions(text)["initstacks_windowed_relax_retire_b"]
+    out = emit._lowered_initstacks("initstacks_windowed_relax_retire_b", body, "Float64")
+    assert out.startswith("function initstacks_windowed_relax_retire_b_hip(dx, num_passes, w0)")
+    for nm in ("prefix_branch_stack_1", "prefix_left_stack_1", "val_w_1"):
+        assert re.search(rf"^\s*{nm} = Vector\{{Int(64)?\}}\(undef,", out, re.M), nm
+        assert f"ROCArray({nm})" in out, nm
+    for nm, t in (("branch_stack", "Int64"), ("left_stack", "Float64"), ("right_stack", "Float64")):
+        assert re.search(rf"^\s*{nm} = ROCArray\{{{t}\}}\(undef,", out, re.M), nm
+    ret = [ln for ln in out.splitlines() if ln.strip().startswith("return")][0]
+    assert "__tot_branch_stack_1," in ret and "ROCArray(__tot" not in ret
+
+
 def test_ccall_checker_catches_a_wrong_type(tmp_path, monkeypatch):
     """The check above fails on a planted mistake: the MLP's arrays emitted as Float64."""
     import dataclasses
