@@ -25,6 +25,8 @@ AMDGPU.jl kernels, `cgen_kernel_def` /root/reference/src/STADE.jl:11106-11126):
 """
 from __future__ import annotations
 
+import re
+
 from dataclasses import dataclass, field
 
 from .analysis import ArrayUse, ParallelLoop, Types, classify, infer_types, split_loops, _reads_of, _thaw
@@ -702,6 +704,7 @@ class FuncGen:
         self.hind = 1
         self.nalloc = 0
         self.hlv: dict[str, int] = {}   # host loop variables in scope -> their slot in Args.hl
+        self.serial_kernels: set[str] = set()
 
     def pred_code(self, pred) -> str:
         return " && ".join(f"fr.flag[{k}]" for k in pred) if pred else "true"
@@ -736,8 +739,45 @@ class FuncGen:
         for n in sorted(writes):
             if n in names:
                 em.emit(f"fr.v_{cname(n)} = x_{cname(n)};")
-        self.kern.append(f"__global__ __launch_bounds__(1) void k{k}(const Args a) {{\n" + "\n".join(em.lines) + "\n}\n")
+        self.one_thread_kernel(k, em.lines)
         self.launch(f"k{k}")
+
+    def one_thread_kernel(self, k: int, lines: list) -> None:
+        """A one-thread kernel k<k>, its body a device function, so that launches of
+        consecutive one-thread kernels can be merged into one (merge_serial_launches)."""
+        self.kern.append(f"__device__ __forceinline__ void k{k}_body(const Args& a) {{\n" + "\n".join(lines) + "\n}\n"
+                         f"__global__ __launch_bounds__(1) void k{k}(const Args a) {{ k{k}_body(a); }}\n")
+        self.serial_kernels.add(f"k{k}")
+
+    def merge_serial_launches(self) -> None:
+        """Launches of one-thread kernels that follow each other with no host
+        statement between them become one launch of a kernel that runs their bodies in order:
+        the same statements in the same order on the same thread, with the same arguments
+        (`a` changes only at host statements), one kernel boundary instead of several."""
+        launch_re = re.compile(r"^(\s*)(k\d+)<<<1, 1, 0, stream>>>\(a\);$")
+        out, i, h = [], 0, self.host
+        while i < len(h):
+            m = launch_re.match(h[i])
+            run = []
+            j = i
+            while j + 1 < len(h):
+                mj = launch_re.match(h[j])
+                if not (mj and mj.group(2) in self.serial_kernels and (not run or mj.group(1) == m.group(1))
+                        and h[j + 1].strip().startswith("if ((_e = hipGetLastError())")):
+                    break
+                run.append(mj.group(2))
+                j += 2
+            if len(run) >= 2:
+                name = "km" + "_".join(r[1:] for r in run)
+                self.kern.append(f"__global__ __launch_bounds__(1) void {name}(const Args a) {{ "
+                                 + " ".join(f"{r}_body(a);" for r in run) + " }\n")
+                out.append(f"{m.group(1)}{name}<<<1, 1, 0, stream>>>(a);")
+                out.append(f"{m.group(1)}if ((_e = hipGetLastError()) != hipSuccess) return _fail(_e, \"{name}\");")
+                i = j
+            else:
+                out.append(h[i])
+                i += 1
+        self.host = out
 
     # -- parallel loops -----------------------------------------------------------------------
     def parallel(self, op: ParOp) -> None:
@@ -944,7 +984,7 @@ class FuncGen:
             lines.append("    if (_trip <= 0) return;")
             for n in pl.live_out:
                 lines.append(f"    fr.v_{cname(n)} = wb.v_{cname(n)};")
-            self.kern.append(f"__global__ __launch_bounds__(1) void k{kc}(const Args a) {{\n" + "\n".join(lines) + "\n}\n")
+            self.one_thread_kernel(kc, lines)
             self.launch(f"k{kc}")
 
     def guard_code(self, pl: ParallelLoop, ctx) -> str:
@@ -1045,7 +1085,7 @@ class FuncGen:
                     lines.append(("    if" if j == 0 else "    else if") + f" ({cc}) fr.flag[{op.flags[j]}] = 1;")
                 if op.node.orelse is not None:
                     lines.append(f"    else fr.flag[{op.flags[-1]}] = 1;")
-                self.kern.append(f"__global__ __launch_bounds__(1) void k{k}(const Args a) {{\n" + "\n".join(lines) + "\n}\n")
+                self.one_thread_kernel(k, lines)
                 self.launch(f"k{k}")
                 for b in op.branches:
                     self.ops(b)
@@ -1067,6 +1107,7 @@ class FuncGen:
                 args_fields.append(f"    {fl.cty(fl.scalars.get(n, 'f'))} s_{cname(n)};")
         args_fields.append(f"    int64_t hl[{max(1, fl.nhl)}];")
         self.ops(fl.ops)
+        self.merge_serial_launches()
         init = ["    fr.nret = 0;", "    fr.oob = 0;"] + [f"    fr.v_{cname(n)} = a.s_{cname(n)};" for n in f.args if n not in fl.arrays]
         init += [f"    fr.flag[{k}] = 0;" for k in range(fl.nflags)]
         params, fill = [], []
