@@ -25,11 +25,13 @@ AMDGPU.jl kernels, `cgen_kernel_def` /root/reference/src/STADE.jl:11106-11126):
 """
 from __future__ import annotations
 
+import os
 import re
 
 from dataclasses import dataclass, field
 
 from .analysis import ArrayUse, ParallelLoop, Types, classify, infer_types, split_loops, _reads_of, _thaw
+from . import gather
 from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, If, LowerError, Nothing_, Num, Range,
                      Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
@@ -97,6 +99,10 @@ class ReturnOp:
 
 class FuncLower:
     def __init__(self, f: Func, precision: str, arg_types: dict | None = None):
+        # periodic scatters into owner-computes gathers where the index maps are bijections
+        # (gather.py); STADE_LOWER_GATHER=0 keeps every loop as written
+        if os.environ.get("STADE_LOWER_GATHER", "1") != "0":
+            f = Func(f.name, f.args, gather.transform(f.body), f.annot)
         self.f = f
         self.precision = precision
         self.T: Types = infer_types(f, arg_types, precision)

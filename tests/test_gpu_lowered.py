@@ -90,7 +90,7 @@ def test_lowered_binsum(mode, nb):
 # ---- the benchmark configs' texts through the general path ------------------------------
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
-@pytest.mark.parametrize("n", [1, 3, 64, 257])
+@pytest.mark.parametrize("n", [1, 2, 3, 64, 257])
 def test_lowered_diffusion2d(mode, n):
     shapes = {k: n * n for k in ("u", "ub", "un", "unb", "ud", "ubd", "und", "unbd")}
     shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
@@ -111,7 +111,7 @@ def test_lowered_affine_lsq(mode, mn):
 
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
-@pytest.mark.parametrize("case_", [(7, 6, 0.007), (100, 12, 10.0), (4097, 9, 10.0), (5, 0, 10.0)])
+@pytest.mark.parametrize("case_", [(7, 6, 0.007), (100, 12, 10.0), (4097, 9, 10.0), (5, 0, 10.0), (2, 4, 10.0)])
 def test_lowered_burgers1d(mode, case_):
     n, T, tend = case_
     shapes = {k: n for k in ("u", "ub", "un", "unb", "ud", "ubd", "und", "unbd")}

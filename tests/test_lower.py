@@ -78,7 +78,9 @@ def test_a_shared_index_is_not_injective():
 
 PLANS = {
     # (text, function): (loop variable, array, kind) that the plan must contain
-    ("diffusion2d_b", "diffusion2d_b"): [("idx", "un", "owned"), ("idx", "ub", "atomic"), ("k", "loss", "atomic")],
+    # (the periodic scatter into ub taken as an owner-computes gather, the unb reset deferred)
+    ("diffusion2d_b", "diffusion2d_b"): [("idx", "un", "owned"), ("idx", "ub", "owned"), ("idx", "unb", "read"),
+                                         ("idx", "unb", "owned"), ("k", "loss", "atomic")],
     ("mlp2_ce_b", "mlp2_ce_b"): [("idx", "h1", "owned"), ("idx", "w1b", "atomic"), ("idx", "xb", "atomic")],
     ("conv3x3_b", "conv3x3_b"): [("idx", "out", "owned"), ("idx", "wb", "atomic"), ("idx", "xpb", "atomic")],
     ("generic/binsum_b", "binsum_b"): [("i", "c", "atomic"), ("i", "vb", "owned")],
@@ -273,3 +275,52 @@ def test_run_initstacks_matches_the_oracle(name, args):
             assert (v.dtype == np.int64) == (w[1] == "Ai"), (nm, v.dtype, w)
         else:
             assert v == w, (nm, v, w)
+
+
+def _gathered(text: str, fname: str) -> int:
+    from stade_hip.lower import gather
+    from stade_hip.lower.syntax import parse
+    f = next(g for g in parse(text) if g.name == fname)
+    n = [0]
+    gather.transform(f.body, n)
+    return n[0]
+
+
+def test_periodic_scatter_becomes_a_gather():
+    """The Burgers reverse loop's neighbour scatters into ub (periodic shifts of i_x) run as
+    an owner-computes gather, its unb reset deferred to a loop of its own."""
+    from stade_hip.lower import hipgen
+    _, sigs = hipgen.generate((CORPUS / "burgers1d_b.jl").read_text())
+    plan = " | ".join(sigs["burgers1d_b"]["plan"])
+    assert re.search(r"parallel over i_x \[u:read, ub:owned, unb:read\] sums", plan), plan
+    assert re.search(r"parallel over i_x \[unb:owned\]", plan), plan
+    assert "ub:atomic" not in plan.split("host loop over i_t")[2], plan
+
+
+_SCATTER = """function s_b(x, xb, y, yb, n)
+    for i = 1:n
+        ip = mod(i, n) + 1
+        old = yb[i]
+        yb[i] = 0.0
+        xb[ip] = xb[ip] + WHAT
+    end
+    return nothing
+end
+"""
+
+
+@pytest.mark.parametrize("what, expect", [
+    ("2.0 * old", 1),                 # a periodic shift: rewritten
+    ("old * x[ip]", 1),               # reads an array the loop never writes
+    ("old * yb[ip]", 0),              # reads the array the loop resets, at a neighbour
+])
+def test_gather_only_where_exact(what, expect):
+    assert _gathered(_SCATTER.replace("WHAT", what), "s_b") == expect
+
+
+def test_no_gather_for_a_map_that_is_not_a_bijection():
+    text = _SCATTER.replace("ip = mod(i, n) + 1", "ip = mod(i, 2) + 1").replace("WHAT", "old")
+    assert _gathered(text, "s_b") == 0
+    # a shift whose extent is not the loop's
+    text = _SCATTER.replace("ip = mod(i, n) + 1", "ip = mod(i, n - 1) + 1").replace("WHAT", "old")
+    assert _gathered(text, "s_b") == 0
