@@ -31,7 +31,7 @@ import re
 from dataclasses import dataclass, field
 
 from .analysis import ArrayUse, ParallelLoop, Types, classify, infer_types, split_loops, _reads_of, _thaw
-from . import gather
+from . import fuse, gather
 from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, If, LowerError, Nothing_, Num, Range,
                      Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
@@ -106,6 +106,11 @@ class FuncLower:
         self.f = f
         self.precision = precision
         self.T: Types = infer_types(f, arg_types, precision)
+        # adjacent parallel loops over the same iterations as one loop (fuse.py);
+        # STADE_LOWER_FUSE=0 keeps them apart
+        if os.environ.get("STADE_LOWER_FUSE", "1") != "0":
+            f = self._fused(f)
+            self.f = f
         self.fty = "float" if precision == "f32" else "double"
         self.arrays = self.T.arrays
         self.scalars = {n: t for n, t in self.T.scalars.items() if n not in self.arrays}
@@ -116,6 +121,22 @@ class FuncLower:
         self.reasons: list[str] = []
         self.refuse_reasons()
         self.ops = self.plan()
+
+    def _fused(self, f: Func) -> Func:
+        from .analysis import _upward_exposed
+
+        def is_parallel(loop: For) -> bool:
+            # (live-out scalars: every scalar the loop assigns that is read anywhere else in
+            # the function, a superset of what the planner computes)
+            outside = set()
+            for s in walk_stmts(f.body):
+                if s is loop or any(t is s for t in walk_stmts(loop.body)):
+                    continue
+                for e in stmt_exprs(s):
+                    outside |= _reads_of(e)
+            pl, _ = classify(loop, self.T, outside, set())
+            return pl is not None
+        return Func(f.name, f.args, fuse.transform(f.body, self.T, is_parallel), f.annot)
 
     # -- refusals ---------------------------------------------------------------------------
     def refuse_reasons(self):

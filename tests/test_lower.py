@@ -78,9 +78,10 @@ def test_a_shared_index_is_not_injective():
 
 PLANS = {
     # (text, function): (loop variable, array, kind) that the plan must contain
-    # (the periodic scatter into ub taken as an owner-computes gather, the unb reset deferred)
+    # (the periodic scatter into ub taken as an owner-computes gather, the unb reset deferred;
+    # the forward, loss and seed loops over the same cells fused into one)
     ("diffusion2d_b", "diffusion2d_b"): [("idx", "un", "owned"), ("idx", "ub", "owned"), ("idx", "unb", "read"),
-                                         ("idx", "unb", "owned"), ("k", "loss", "atomic")],
+                                         ("idx", "unb", "owned"), ("idx", "loss", "atomic")],
     ("mlp2_ce_b", "mlp2_ce_b"): [("idx", "h1", "owned"), ("idx", "w1b", "atomic"), ("idx", "xb", "atomic")],
     ("conv3x3_b", "conv3x3_b"): [("idx", "out", "owned"), ("idx", "wb", "atomic"), ("idx", "xpb", "atomic")],
     ("generic/binsum_b", "binsum_b"): [("i", "c", "atomic"), ("i", "vb", "owned")],
@@ -324,3 +325,38 @@ def test_no_gather_for_a_map_that_is_not_a_bijection():
     # a shift whose extent is not the loop's
     text = _SCATTER.replace("ip = mod(i, n) + 1", "ip = mod(i, n - 1) + 1").replace("WHAT", "old")
     assert _gathered(text, "s_b") == 0
+
+
+def test_adjacent_loops_over_the_same_cells_fuse():
+    """The diffusion adjoint's forward loop, loss loop (k = 1:n*n) and seed loop
+    (k = n*n:-1:1) become one parallel loop: un written and read at the iteration's own index."""
+    from stade_hip.lower import hipgen
+    _, sigs = hipgen.generate((CORPUS / "diffusion2d_b.jl").read_text())
+    par = [p for p in sigs["diffusion2d_b"]["plan"] if p.startswith("parallel")]
+    assert len(par) == 3, par
+    assert par[0].startswith("parallel over idx [loss:atomic, lossb:read, u:read, un:owned, unb:owned]"), par
+
+
+_FUSE = """function f_b(x, y, z, s, n)
+    for i = 1:n
+        y[i] = 2.0 * x[i]
+    end
+    for k = n:-1:1
+        BODY
+    end
+    return nothing
+end
+"""
+
+
+@pytest.mark.parametrize("body, fused", [
+    ("z[k] = y[k] + 1.0", True),             # reads what the first loop wrote, at its own index
+    ("z[k] = y[mod(k, n) + 1]", False),       # reads another iteration's value
+    ("s[1] = s[1] + y[k]", True),             # a sum of own-index values
+])
+def test_fusion_only_where_iterations_stay_independent(body, fused):
+    from stade_hip.lower import hipgen
+    _, sigs = hipgen.generate(_FUSE.replace("BODY", body))
+    par = [p for p in sigs["f_b"]["plan"] if p.startswith("parallel")]
+    assert (len(par) == 1) == fused, par
+
