@@ -52,10 +52,11 @@ def normal(seed_name: str, n: int, salt: int = 0) -> np.ndarray:
 
 
 def seeded_inputs(specs, ints: dict, seed: str, int_arrays: dict | None = None, fdt=np.float64,
-                  zeros=()) -> list:
+                  zeros=(), scales: dict | None = None) -> list:
     """The inputs `make_args` draws, from stored argument specs [(name, kind, shape or value,
     position in the generated signature)]: N(0,1) from Julia's Xoshiro stream seeded with
-    val_stable_seed(seed) + position; the float arrays named in `zeros` (stacks) zero-filled.
+    val_stable_seed(seed) + position, times `scales[name]` where given; the float arrays named
+    in `zeros` (stacks) zero-filled.
     Used where the generated text (and so the oracle's argument table) is not available, with
     fixtures written by make_args."""
     from oracle import rng as jrng
@@ -72,7 +73,8 @@ def seeded_inputs(specs, ints: dict, seed: str, int_arrays: dict | None = None, 
             out.append((a, kind, np.zeros(tuple(shp), dtype=fdt, order="F")))
         else:
             shp = tuple(shp)
-            v = jrng.val_randn(jrng.Xoshiro(base + pos), int(np.prod(shp))).astype(fdt)
+            v = jrng.val_randn(jrng.Xoshiro(base + pos), int(np.prod(shp)))
+            v = (v * (scales or {}).get(a, 1.0)).astype(fdt)
             out.append((a, kind, np.asfortranarray(v.reshape(shp, order="F")) if len(shp) > 1 else v))
     return out
 

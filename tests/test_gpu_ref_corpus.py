@@ -1,12 +1,12 @@
 """The general lowering on the reference's own generated code, on the GPU.
 
 The reference's committed generated files (/root/reference/test/val-corpus: adjoint, tangent
-and HVP of every kernel the fixture script can size and run, 414 files of 138 kernels) are
+and HVP of every kernel: 417 files of 139 kernels) are
 lowered by `build()` where the reference is mounted, into stade.jl_amd/lib/gen/ with an index
 of their entry points.  The expected results are fixtures (tests/golden/make_ref_corpus.py):
-the oracle's outputs on seeded inputs (two sizes for the kernels the oracle tests size, the
-size the reference's validator rule finds for the others), and the 80-bit truth where it
-differs.  Each case draws the same inputs from the seed, runs the lowered library through its C
+the oracle's outputs on seeded inputs (two hand-chosen sizes for the kernels the oracle tests
+size and for one whose recurrence needs scaled inputs, the size the reference's validator rule
+finds for the others), and the 80-bit truth where it differs.  Each case draws the same inputs from the seed, runs the lowered library through its C
 entry point, and compares every output argument, stack and returned scalar with the parity
 bars (fp64 1e-12, integers exact) and the truth rule.  The reference's text is not read here."""
 from __future__ import annotations
@@ -51,7 +51,8 @@ def test_lowered_reference_kernel(case):
     sig["args"] = [tuple(x) for x in sig["args"]]
     low = LoweredLib(GEN / entry["lib"], {fname: sig}, "f64", None)
     ia = {a: z[f"{key}/in/{a}"] for a, kind, _, _ in case["args"] if kind == "Ai"}
-    args = seeded_inputs(case["args"], case["ints"], case["seed"], ia, zeros=case.get("zeros", ()))
+    args = seeded_inputs(case["args"], case["ints"], case["seed"], ia, zeros=case.get("zeros", ()),
+                         scales=case.get("scales"))
     stacks = [(s, (n, k)) for s, n, k in case["stacks"]]
     dims = {a: v.shape for a, _, v in args if isinstance(v, np.ndarray) and v.ndim > 1}
     print(f"reference {key}: {len(args)} arguments, plan {sig.get('plan')}", flush=True)

@@ -212,13 +212,16 @@ def test_ref_corpus_fixture_inputs_reproduce():
     gold = Path(__file__).resolve().parent / "golden"
     meta = json.loads((gold / "ref_corpus.json").read_text())
     z = np.load(gold / "ref_corpus.npz")
-    for case in meta[::7]:
+    # every seventh case, and every case drawn at scaled inputs
+    for case in [c for k, c in enumerate(meta) if k % 7 == 0 or c.get("scales")]:
         lib_o = runner.load(REF_CORPUS / f"{case['fname']}.jl")
         ia = {a: z[f"{case['key']}/in/{a}"] for a, kind, _, _ in case["args"] if kind == "Ai"}
-        got = seeded_inputs(case["args"], case["ints"], case["seed"], ia, zeros=case.get("zeros", ()))
+        got = seeded_inputs(case["args"], case["ints"], case["seed"], ia, zeros=case.get("zeros", ()),
+                            scales=case.get("scales"))
         shapes = {a: tuple(s) for a, kind, s, _ in case["args"] if kind == "Af"}
         shapes["__stacks__"] = tuple(s for s, _, _ in case["stacks"])
-        want = make_args(lib_o, case["fname"], shapes, case["ints"], {}, case["seed"], np.float64, ia)
+        want = make_args(lib_o, case["fname"], shapes, case["ints"], {}, case["seed"], np.float64, ia,
+                         case.get("scales"))
         # the stacks initstacks returns are zero-filled
         want = [(a, k, np.zeros_like(v, order="F") if a in case.get("zeros", ()) else v) for a, k, v in want]
         assert [a for a, _, _ in got] == [a for a, _, _ in want]
