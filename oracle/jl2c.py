@@ -924,12 +924,14 @@ class CGen:
         b, tb = self.ex(e[3])
         if op == "/":
             if ta == "i" and tb == "i":
-                return (f"(({self.fp if self.fp != 'float' else 'double'}){a} / ({self.fp if self.fp != 'float' else 'double'}){b})", "f")
+                # Julia: Int64 / Int64 is a Float64 quotient in every precision mode (the
+                # reference's BigFloat rerun keeps it so too: only inputs are promoted)
+                return (f"((double){a} / (double){b})", "f")
             return (f"({self.tofp(a, ta)} / {self.tofp(b, tb)})", "f")
         if op == "%":
             if ta == "i" and tb == "i":
                 return (f"({a} % {b})", "i")
-            return (f"fmod({a}, {b})", "f")
+            return (f"fmod{self.msfx}({self.tofp(a, ta)}, {self.tofp(b, tb)})", "f")
         rt = "f" if "f" in (ta, tb) else "i"
         if rt == "f":
             a, b = self.tofp(a, ta), self.tofp(b, tb)
@@ -1006,6 +1008,10 @@ class CGen:
         if fn in math1:
             if len(args) != 1:
                 raise SyntaxError(f"{fn} takes one argument")
+            if ts[0] == "i" and self.fp == "long double":
+                # Julia: sqrt(::Int64), exp(::Int64), ... return Float64; the reference's
+                # BigFloat rerun promotes inputs only, so that value stays a Float64
+                return (f"((long double){fn}((double){txt[0]}))", "f")
             return (f"{fn}{sfx}({self.tofp(txt[0], ts[0])})", "f")
         raise SyntaxError(f"call to unsupported function {fn}")
 

@@ -46,6 +46,14 @@ class JlArr(ctypes.Structure):
 _DT = {"Af": None, "Ai": np.int64}
 
 
+def _ld_from_buffer(buf, n):
+    """The first n values of a ctypes c_longdouble array as numpy long doubles.  Indexing the
+    ctypes array itself would return Python floats and drop the 80-bit values' last 11 bits (and
+    Int64 values above 2^53)."""
+    assert ctypes.sizeof(ctypes.c_longdouble) == np.dtype(np.longdouble).itemsize
+    return np.frombuffer(buf, dtype=np.longdouble, count=max(n, 0))
+
+
 class OracleLib:
     def __init__(self, so_path: Path, infos: dict, precision: str):
         self.path = so_path
@@ -97,7 +105,11 @@ class OracleLib:
                 elif self.precision == "f32":
                     c = ctypes.c_float(float(v))
                 elif self.precision == "f80":
-                    c = ctypes.c_longdouble(v)
+                    # through a numpy buffer: ctypes.c_longdouble(v) converts v via a Python float
+                    c = np.array([v], dtype=np.longdouble)
+                    keep.append(c)
+                    argv[j] = ctypes.c_void_p(c.ctypes.data)
+                    continue
                 else:
                     c = ctypes.c_double(float(v))
                 keep.append(c)
@@ -106,15 +118,16 @@ class OracleLib:
         n = self._fn(name)(argv, ret)
         if self.lib.jl_get_bounds_error():
             raise IndexError(f"{name}: out-of-bounds array access (see stderr)")
+        rv = _ld_from_buffer(ret, n)
         out = []
         for k in range(n):
             kind = info.ret[k] if k < len(info.ret) else "f"
             if kind == "i":
-                out.append(int(ret[k]))
+                out.append(int(rv[k]))
             elif kind.startswith("A"):
-                out.append((int(ret[k]), kind))
+                out.append((int(rv[k]), kind))
             else:
-                out.append(self.fdt(ret[k]) if self.precision == "f80" else float(self.fdt(ret[k])))
+                out.append(self.fdt(rv[k]) if self.precision == "f80" else float(self.fdt(rv[k])))
         return tuple(out)
 
     def stacks(self, name: str, *args, fill_nan: bool = True):

@@ -3,7 +3,7 @@
 For every kernel of the reference's validation corpus (its committed generated adjoint,
 tangent and HVP files under /root/reference/test/val-corpus): the seeds of the inputs, the
 oracle's outputs (the generated text transpiled to sequential C, in Float64) and the truth
-where it differs (the same text in 80-bit extended precision, rounded to Float64).  The
+where it differs (the same text in 80-bit extended precision, kept as long double).  The
 kernels of tests/test_oracle_corpus.py take two hand-chosen sizes each (the oracle tests'
 small ones and larger ones that spread the loops over many GPU threads); every other kernel
 is sized the way the reference's validator sizes it (`val_generate_baseline` and
@@ -12,7 +12,7 @@ is sized the way the reference's validator sizes it (`val_generate_baseline` and
 without an index out of bounds (Int64 arrays hold indices drawn from 1..cap, cap = 4, 8, ...
 in the outer loop), and a draw rejected when its results are not finite, exceed 1e6 in
 magnitude or leave every output unchanged (nothing exercised).  The lowering's library is built from the same file into
-stade.jl_amd/lib/gen/ with an index of libraries and signatures (build products, not
+tests/_build/ref_corpus/ with an index of libraries and signatures (test build products, not
 committed; `build()` makes them where the reference is mounted).  tests/test_gpu_ref_corpus.py runs that library on the GPU on these
 inputs: the reference's text is read here, never on the GPU box, and nothing of it is stored
 but the inputs, outputs and argument lists.
@@ -218,12 +218,14 @@ def one_kernel(name: str):
                     continue
                 outs.append(a)
                 arrays[f"{key}/out/{a}"] = np.ravel(h, order="F")
-                tt = np.ravel(np.asarray(t, dtype=np.float64) if kind == "Af" else t, order="F")
+                # the 80-bit truth kept as long double (the format of the box's numpy, the
+                # same image): rounding it to Float64 would drop the bits that make it a truth
+                tt = np.ravel(np.asarray(t, dtype=np.longdouble) if kind == "Af" else t, order="F")
                 if not np.array_equal(tt, arrays[f"{key}/out/{a}"]):
                     arrays[f"{key}/truth/{a}"] = tt
             for (s_, _), h, t in zip(stacks, case.stack_h, truth["stacks"]):
                 arrays[f"{key}/out/{s_}"] = h
-                tt = np.asarray(t, dtype=np.float64) if h.dtype != np.int64 else t
+                tt = np.asarray(t, dtype=np.longdouble) if h.dtype != np.int64 else t
                 if not np.array_equal(tt, h, equal_nan=True):
                     arrays[f"{key}/truth/{s_}"] = tt
             pos = {a: k for k, (a, _) in enumerate(lib_o.infos[fname].args)}
@@ -232,7 +234,10 @@ def one_kernel(name: str):
                 **({"scales": scales} if scales else {}),
                 args=[[a, kind, (list(v.shape) if isinstance(v, np.ndarray) else v), pos[a]] for a, kind, v in args],
                 outs=outs, stacks=[[s_, n, k] for s_, (n, k) in stacks],
-                ret=[float(x) for x in case.ret_h], ret_truth=[float(x) for x in truth["ret"]],
+                ret=[float(x) for x in case.ret_h],
+                # returned truths as the shortest decimal that reads back to the same long double
+                ret_truth=[np.format_float_scientific(np.longdouble(x), unique=True) if isinstance(x, np.floating)
+                           else x for x in truth["ret"]],
                 ))
             log.append(f"{key}: {len(args)} arguments, {len(stacks)} stacks")
     return meta, arrays, log

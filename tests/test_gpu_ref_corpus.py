@@ -2,7 +2,7 @@
 
 The reference's committed generated files (/root/reference/test/val-corpus: adjoint, tangent
 and HVP of every kernel: 417 files of 139 kernels) are
-lowered by `build()` where the reference is mounted, into stade.jl_amd/lib/gen/ with an index
+lowered by `build()` where the reference is mounted, into tests/_build/ref_corpus/ with an index
 of their entry points.  The expected results are fixtures (tests/golden/make_ref_corpus.py):
 the oracle's outputs on seeded inputs (two hand-chosen sizes for the kernels the oracle tests
 size and for one whose recurrence needs scaled inputs, the size the reference's validator rule
@@ -22,7 +22,7 @@ from helpers import ParityCase, seeded_inputs
 pytestmark = pytest.mark.gpu
 
 GOLD = Path(__file__).resolve().parent / "golden"
-GEN = Path(__file__).resolve().parent.parent / "stade.jl_amd" / "lib" / "gen"
+GEN = Path(__file__).resolve().parent / "_build" / "ref_corpus"
 META = json.loads((GOLD / "ref_corpus.json").read_text())
 _Z = {}
 
@@ -72,6 +72,7 @@ def test_lowered_reference_kernel(case):
     pc.stack_h = [z[f"{key}/out/{s}"] for s, _ in stacks]
     pc.ret_h = tuple(case["ret"])
     pc._truth = dict(arrays=th, stacks=[z[f"{key}/truth/{s}"] if f"{key}/truth/{s}" in z else z[f"{key}/out/{s}"]
-                                        for s, _ in stacks], ret=tuple(case["ret_truth"]))
+                                        for s, _ in stacks],
+                     ret=tuple(np.longdouble(x) if isinstance(x, str) else x for x in case["ret_truth"]))
     pc.run_gpu()
     print(f"reference {key}: worst {pc.compare():.3e}", flush=True)
