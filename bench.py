@@ -824,9 +824,12 @@ def main():
             others[nm] = measure(wl, 10 if heavy else max(5, args.steps // 2), 2 if heavy else max(2, args.warmup), dev)
             if not args.no_cpu_baseline:
                 others[nm]["cpu_baseline"] = cpu_baseline(wl, budget_s=4.0, max_runs=5)
+            # the full record of each function on a line of its own; the last line keeps a summary
+            print(json.dumps({"detail": nm, **others[nm]}), flush=True)
             del wl
             torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline(head)
+    print(json.dumps({"detail": args.workload, **res, "cpu_baseline": cpu}), flush=True)
     line = {
         "metric": "gradient evals/sec per config",
         "value": res["evals_per_s"],
@@ -847,13 +850,25 @@ def main():
         "eval_mfma_frac": res.get("eval_mfma_frac"),
         "kernel": res.get("kernel"),
         "kernel_ms": res.get("kernel_ms"),
-        "kernels": res.get("kernels"),
         "kernel_timing": "HIP event pair around each launch of the dominant kernel on its own stream, over a second "
                          "pass of the same K steps; value and ms_per_step come from the first, event-free pass",
-        "configs": {k: {kk: vv for kk, vv in v.items() if kk != "config"} | {"workload": v["config"].get("workload")}
-                    for k, v in others.items()},
+        # per function: evals/s, ms per evaluation, the evaluation's fraction of its roofline
+        # (HBM bytes, fp32 matrix-core or fp64 flops), the dominant kernel's fraction, the CPU
+        # baseline's evals/s; each function's full record is on its own "detail" line above
+        "configs": {k: _summary(v) for k, v in others.items()},
     }
     print(json.dumps(line))
+
+
+def _sig(x, d=4):
+    return None if x is None else float(f"{x:.{d}g}")
+
+
+def _summary(r: dict) -> dict:
+    frac = r.get("eval_hbm_frac") or r.get("eval_mfma_frac") or r.get("eval_valu_frac")
+    return {"evals_per_s": _sig(r["evals_per_s"]), "ms": _sig(r["ms_per_step"]), "eval_frac": _sig(frac, 3),
+            "kernel_frac": _sig((r.get("roofline") or {}).get("frac"), 3),
+            "cpu_evals_per_s": _sig((r.get("cpu_baseline") or {}).get("value"), 3)}
 
 
 if __name__ == "__main__":

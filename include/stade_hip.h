@@ -26,8 +26,17 @@
  *   - Return value: 0 on success; a positive hipError_t code or a negative STADE_HIP_E*
  *     code on failure, with a message in stade_hip_last_error().  Argument errors are
  *     reported before any work is enqueued.
- *   - Calls on one device share a library workspace (reduction partials and tickets):
- *     calls that overlap on one device, on different streams, race.
+ *   - Calls on one device share a library workspace (reduction partials, device scalars and
+ *     scratch).  Calls are serialised per device: a host thread holds the device's lock while
+ *     it enqueues, and a call on a stream other than the previous call's first waits
+ *     (hipStreamWaitEvent) for the event that call recorded at its end, so calls on different
+ *     streams run one after the other instead of racing.
+ *   - Graph capture: a call on a capturing stream takes no dependency outside the capture, and
+ *     the workspace does not grow under capture (STADE_HIP_ESTATE): make one eager call of the
+ *     largest size first.  Replays are not ordered against eager calls on other streams (the
+ *     caller orders them, as any graph); they share the workspace with those calls.  A scratch
+ *     buffer that a captured graph may hold is never freed: a later, larger eager call retires
+ *     it and allocates another, so earlier graphs stay valid.
  */
 #ifndef STADE_HIP_H
 #define STADE_HIP_H
@@ -43,6 +52,7 @@ extern "C" {
 #define STADE_HIP_EINVAL (-1)
 #define STADE_HIP_ENOMEM (-2)
 #define STADE_HIP_ERANGE (-3)
+#define STADE_HIP_ESTATE (-4)   /* not possible in the library's current state (e.g. workspace growth under graph capture) */
 
 /* ---- library ------------------------------------------------------------------------ */
 const char* stade_hip_last_error(void);
@@ -53,6 +63,11 @@ int32_t stade_hip_synchronize(hipStream_t stream);
  * such as a label outside 1..i_out): 1 if raised since the last read, then cleared.
  * Synchronous. */
 int32_t stade_hip_device_error(int32_t* flag);
+
+/* Library workspace of the current device (no counterpart in the reference: the generated
+ * code allocates per call): the bytes of scratch held, and the number of scratch buffers
+ * retired because a captured graph may still use them (kept until the process ends). */
+int32_t stade_hip_workspace_info(int64_t* scratch_bytes, int64_t* retired);
 
 /* ---- kernel timing (no counterpart in the reference; its timings come from an external
  * bench kit, /root/reference/claude/manual-stade-dev.md:2040).  While enabled, every kernel

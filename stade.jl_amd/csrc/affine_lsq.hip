@@ -417,7 +417,7 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
     const int two = (M == ADJ) ? 1 : 2;
     size_t nP = (size_t)nchunks * m, nS = (size_t)m, nX = (size_t)mtiles * n;
     double* base = (double*)scratch(sizeof(double) * two * (nP + nS + nX) + 256);
-    if (!base) return STADE_HIP_ENOMEM;
+    if (!base) return scratch_error();
     double *P = base, *Pd = P + nP, *S = P + two * nP, *Sd = S + nS, *XP = S + two * nS, *XPd = XP + nX;
     // the adjoint forms with columns: rows (+ rb staged in S), columns (row values recomputed
     // per block), xb; otherwise rows, finish, the loss sum

@@ -797,7 +797,7 @@ int32_t adjoint_impl(const char* fn, int64_t every, double* loss, const double* 
         // checkpoint policy: the segment tape (`every` rows) and the recompute states follow
         const size_t seg_len = CK ? (size_t)every * (size_t)n : 0;
         double* P = (double*)scratch(sizeof(double) * (2 * (size_t)n + (CK ? seg_len + 6 * (size_t)n : 0)));
-        if (!P) return STADE_HIP_ENOMEM;
+        if (!P) return scratch_error();
         double* Q = P + n;
         double* seg = Q + n;
         double* R = seg + seg_len;
@@ -887,7 +887,7 @@ int32_t hvp_impl(const char* fn, int64_t every, double* loss, const double* loss
         const size_t tape_len = rows * (size_t)n;
         const size_t seg_len = CK ? (size_t)every * (size_t)n : 0;
         double* P = (double*)scratch(sizeof(double) * (4 * (size_t)n + tape_len + (CK ? 2 * seg_len + 6 * (size_t)n : 0)));
-        if (!P) return STADE_HIP_ENOMEM;
+        if (!P) return scratch_error();
         double *Q = P + n, *Pd = Q + n, *Qd = Pd + n, *taped = Qd + n;
         double *seg = taped + tape_len, *segd = seg + seg_len, *R = segd + seg_len;
         if (int32_t rc = forward<true>(u, ud, un, und, u_stack, taped, (int)n, 0, nrun, c, P, Q, Pd, Qd, stream, 0,
@@ -1034,7 +1034,7 @@ int32_t stade_hip_burgers1d_d(double* loss, double* lossd, double* u, double* ud
     Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
     double* P = (double*)scratch(sizeof(double) * 4 * (size_t)n);
-    if (!P) return STADE_HIP_ENOMEM;
+    if (!P) return scratch_error();
     double *Q = P + n, *Pd = Q + n, *Qd = Pd + n;
     if (nrun > 0) {
         if (int32_t rc = forward<true>(u, ud, un, und, nullptr, nullptr, (int)n, 0, nrun, c, P, Q, Pd, Qd, stream)) return rc;

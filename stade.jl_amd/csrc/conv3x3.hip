@@ -729,7 +729,7 @@ int32_t run(const Ptrs& p, const Dims& d, hipStream_t stream) {
     const int two = MODE == ADJ ? 1 : 2;
     const size_t total = two * nwf + (MODE == TAN ? 0 : two * nwg + two * nout) + npart;
     float* base = (float*)scratch(sizeof(float) * total + 256);
-    if (!base) return STADE_HIP_ENOMEM;
+    if (!base) return scratch_error();
     float* wf0 = base;
     float* wf1 = wf0 + nwf;
     float* wg0 = wf0 + two * nwf;

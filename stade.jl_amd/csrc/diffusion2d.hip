@@ -942,6 +942,9 @@ int32_t noalloc_scratch(double** out) {
         void* ptr = nullptr;
         STADE_TRY_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
         if (!ptr) return set_error(STADE_HIP_ENOMEM, "hipGetSymbolAddress returned no address for the scratch array");
+        // the event that orders calls on different streams, made here once so that no call
+        // creates anything
+        if (int32_t rc = call_order_setup()) return rc;
         g_scratch_ptr[dev] = (double*)ptr;
     }
     *out = g_scratch_ptr[dev];
@@ -969,6 +972,11 @@ int32_t stade_hip_diffusion2d_b_noalloc(double* loss, const double* lossb, const
                          (long long)n, (long long)need, (long long)kNoAllocPartials);
     double* partials = nullptr;
     if (int32_t rc = noalloc_scratch(&partials)) return rc;
+    // ordered like every other call (the device's lock while enqueueing, then a wait for the
+    // previous call's stream), without the allocating workspace: calls on different streams
+    // run one after the other; a replay of a captured call is ordered by the caller
+    WsCall call_(stream, false);
+    if (!call_.ok()) return call_.error();
     return adjoint(loss, lossb, u, ub, un, unb, n, partials, stream);
 }
 

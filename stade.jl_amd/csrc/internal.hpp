@@ -45,6 +45,7 @@ struct Workspace {
                             // block resets the one it used
     void* scratch;          // grows on demand
     size_t scratch_bytes;
+    bool scratch_captured;  // a graph captured since `scratch` was allocated may hold its address
 };
 constexpr int kPartialSlots = 1 << 22;
 constexpr int kDeviceScalars = 64;
@@ -57,8 +58,12 @@ constexpr int kErrIndex = 1;
 // Workspace of the current device; nullptr (with the error set) on failure.
 Workspace* workspace();
 // Scratch of at least `bytes`; nullptr (with the error set) on failure.  Only valid under a
-// WsCall of the current device.
+// WsCall of the current device.  Under graph capture it does not grow (the graph would keep
+// the address of a buffer the growth replaces): it fails with STADE_HIP_ESTATE.  A buffer a
+// graph may still use is never freed; a growth outside capture retires it instead.
 void* scratch(size_t bytes);
+// The code of the last scratch() failure on this thread (STADE_HIP_ENOMEM or STADE_HIP_ESTATE).
+int32_t scratch_error();
 
 // The workspace of the current device for one library call that enqueues on `stream`.
 // While the guard lives, the calling thread holds the device's library lock, so calls from
@@ -70,7 +75,11 @@ void* scratch(size_t bytes);
 // stream under graph capture is neither ordered nor recorded: the caller's graph orders it.
 class WsCall {
   public:
-    explicit WsCall(hipStream_t stream);
+    // with_workspace = false: the lock and the ordering only (the allocation-free entry
+    // point); `ws` then stays null and ok() tells success
+    explicit WsCall(hipStream_t stream, bool with_workspace = true);
+    bool ok() const { return ok_; }
+    int32_t error() const { return err_; }   // the failure's code when !ok()
     ~WsCall();
     WsCall(const WsCall&) = delete;
     WsCall& operator=(const WsCall&) = delete;
@@ -80,7 +89,12 @@ class WsCall {
     int dev_;
     hipStream_t stream_;
     bool capturing_;
+    bool ok_;
+    int32_t err_;
 };
+// Create the current device's call-order event now (the allocation-free entry point's
+// one-time set-up, so that its calls create nothing); 0 or a hipError_t.
+int32_t call_order_setup();
 
 // ------------------------------------------------------------------------------------------
 // kernel timing: when enabled (stade_hip_profile_start), every launch made through

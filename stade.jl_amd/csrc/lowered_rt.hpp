@@ -96,8 +96,24 @@ __device__ __forceinline__ void atomic_add(int64_t* p, int64_t v) {
     atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
 }
 
+// Path statistics (optional; `st` is null unless a caller asked for them, see the
+// `_set_stats` entry point of a lowered function): a 64-bit counter per accumulation path,
+// counted once per wave or block, so that a test can tell which path a launch took.
+enum : int {
+    ST_WAVE_AGG = 0,     // wave_add calls that made one atomic for the whole wave
+    ST_WAVE_LANE = 1,    // wave_add calls that made one atomic per lane
+    ST_PRIV_BLOCK = 2,   // blocks that accumulated into an LDS-privatised copy
+    ST_SPLIT_BLOCK = 3,  // blocks of the wave-per-iteration (narrow-output) form
+    ST_BLOCK_ADD = 4,    // block_add calls that added a nonzero block total
+    ST_N = 8,
+};
+
+__device__ __forceinline__ void count(unsigned long long* st, int k) {
+    if (st) atomicAdd(&st[k], 1ull);
+}
+
 template <class T>
-__device__ __forceinline__ void wave_add(T* p, T v) {
+__device__ __forceinline__ void wave_add(T* p, T v, unsigned long long* st) {
     const uint64_t active = __ballot(1);
     if (active == ~0ull) {
         const uint64_t u = reinterpret_cast<uint64_t>(p);
@@ -105,11 +121,15 @@ __device__ __forceinline__ void wave_add(T* p, T v) {
         T* p0 = reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
         if (__ballot(p == p0) == ~0ull) {
             v = wave_sum(v);
-            if ((threadIdx.x & 63) == 0) atomic_add(p0, v);
+            if ((threadIdx.x & 63) == 0) {
+                atomic_add(p0, v);
+                count(st, ST_WAVE_AGG);
+            }
             return;
         }
     }
     atomic_add(p, v);
+    if (st && (threadIdx.x & 63) == (unsigned)__builtin_ctzll(active)) count(st, ST_WAVE_LANE);
 }
 
 // One atomic addition per block of the block's values (a loop's sum into a scalar, or its
@@ -118,7 +138,7 @@ __device__ __forceinline__ void wave_add(T* p, T v) {
 // then thread 0 adds the total if it is nonzero.  Every thread of the block must call it;
 // `p` may be null only when the block's values are all zero.
 template <class T>
-__device__ __forceinline__ void block_add(T* p, T v, T* lds) {
+__device__ __forceinline__ void block_add(T* p, T v, T* lds, unsigned long long* st) {
     v = wave_sum(v);
     const int nw = blockDim.x >> 6;
     if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
@@ -126,7 +146,10 @@ __device__ __forceinline__ void block_add(T* p, T v, T* lds) {
     if (threadIdx.x == 0) {
         T s = lds[0];
         for (int w = 1; w < nw; ++w) s += lds[w];
-        if (s != (T)0 && p) atomic_add(p, s);
+        if (s != (T)0 && p) {
+            atomic_add(p, s);
+            count(st, ST_BLOCK_ADD);
+        }
     }
     __syncthreads();
 }

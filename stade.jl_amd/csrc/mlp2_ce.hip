@@ -1168,7 +1168,7 @@ int32_t run(const Ptrs& p, int64_t B_, int64_t I_, int64_t H_, int64_t O_, hipSt
     npart = (npart + 63) / 64 * 64;
     const size_t nlocal = hv * (nD1 + nD2) + nC + (size_t)nchunks * 2 * OMAX;
     float* D1 = (float*)scratch(sizeof(float) * ((nlocal + 63) / 64 * 64 + npart) + 256);
-    if (!D1) return STADE_HIP_ENOMEM;
+    if (!D1) return scratch_error();
     float *D2 = D1 + nD1, *D1d = D2 + nD2, *D2d = D1d + (MODE == HVP ? nD1 : 0), *cpart = D2d + (MODE == HVP ? nD2 : 0);
     float* c2part = cpart + nC;
     float* kpart = D1 + (nlocal + 63) / 64 * 64;

@@ -41,6 +41,13 @@ struct CallOrder {
     hipEvent_t ev;
 };
 static CallOrder g_order[64];
+// whether the library call running on this thread enqueues under graph capture
+static thread_local bool tl_capturing = false;
+static thread_local int32_t tl_scratch_code = STADE_HIP_ENOMEM;
+// scratch buffers replaced while a captured graph may still hold their addresses: kept for
+// the life of the process (each retirement follows a growth, so they total less than the
+// largest scratch ever requested times two)
+static std::vector<void*> g_retired;
 
 Workspace* workspace() {
     int dev = 0;
@@ -71,38 +78,58 @@ Workspace* workspace() {
     return &g_ws[dev];
 }
 
-WsCall::WsCall(hipStream_t stream) : ws(nullptr), dev_(-1), stream_(stream), capturing_(false) {
+WsCall::WsCall(hipStream_t stream, bool with_workspace)
+    : ws(nullptr), dev_(-1), stream_(stream), capturing_(false), ok_(false), err_(STADE_HIP_ENOMEM) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) {
-        check_hip(e, "hipGetDevice");
+        err_ = check_hip(e, "hipGetDevice");
         return;
     }
     if (dev < 0 || dev >= 64) {
-        set_error(STADE_HIP_ERANGE, "device ordinal %d out of range", dev);
+        err_ = set_error(STADE_HIP_ERANGE, "device ordinal %d out of range", dev);
         return;
     }
     g_call_mu[dev].lock();
     dev_ = dev;
-    Workspace* w = workspace();
-    if (!w) return;
+    Workspace* w = with_workspace ? workspace() : nullptr;
+    if (with_workspace && !w) {
+        err_ = STADE_HIP_ENOMEM;
+        return;
+    }
     CallOrder& o = g_order[dev];
     // a stream under graph capture takes no dependency on work outside the capture: such
     // calls are ordered by the graph the caller builds
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     capturing_ = hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    tl_capturing = capturing_;
+    if (capturing_ && w) w->scratch_captured = true;
     if (!capturing_ && o.has_last && o.last != stream && o.ev) {
         if ((e = hipStreamWaitEvent(stream, o.ev, 0)) != hipSuccess) {
-            check_hip(e, "hipStreamWaitEvent (ordering after the previous call's stream)");
+            err_ = check_hip(e, "hipStreamWaitEvent (ordering after the previous call's stream)");
             return;
         }
     }
     ws = w;
+    ok_ = true;
+}
+
+int32_t call_order_setup() {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return check_hip(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return set_error(STADE_HIP_ERANGE, "device ordinal %d out of range", dev);
+    std::lock_guard<std::recursive_mutex> lk(g_call_mu[dev]);
+    CallOrder& o = g_order[dev];
+    if (!o.ev && (e = hipEventCreateWithFlags(&o.ev, hipEventDisableTiming)) != hipSuccess)
+        return check_hip(e, "hipEventCreateWithFlags (call order)");
+    return 0;
 }
 
 WsCall::~WsCall() {
     if (dev_ < 0) return;
-    if (ws && !capturing_) {
+    tl_capturing = false;
+    if (ok_ && !capturing_) {
         CallOrder& o = g_order[dev_];
         hipError_t e = hipSuccess;
         if (!o.ev) e = hipEventCreateWithFlags(&o.ev, hipEventDisableTiming);
@@ -120,23 +147,39 @@ void* scratch(size_t bytes) {
     if (!w) return nullptr;
     std::lock_guard<std::mutex> lk(g_ws_mu);
     if (w->scratch_bytes < bytes) {
+        if (tl_capturing) {
+            tl_scratch_code = STADE_HIP_ESTATE;
+            set_error(STADE_HIP_ESTATE,
+                      "the library workspace cannot grow under graph capture (%zu bytes needed, %zu held): "
+                      "make one eager call of the largest size before capturing", bytes, w->scratch_bytes);
+            return nullptr;
+        }
         if (w->scratch) {
-            // wait for kernels still using the old buffer; a failure here is sticky and is
-            // reported by the next launch's status
-            (void)hipDeviceSynchronize();
-            (void)hipFree(w->scratch);
+            if (w->scratch_captured) {
+                // a captured graph may replay with this address: keep the buffer
+                g_retired.push_back(w->scratch);
+            } else {
+                // wait for kernels still using the old buffer; a failure here is sticky and is
+                // reported by the next launch's status
+                (void)hipDeviceSynchronize();
+                (void)hipFree(w->scratch);
+            }
             w->scratch = nullptr;
             w->scratch_bytes = 0;
         }
         hipError_t e = hipMalloc(&w->scratch, bytes);
         if (e != hipSuccess) {
+            tl_scratch_code = STADE_HIP_ENOMEM;
             check_hip(e, "scratch allocation");
             return nullptr;
         }
         w->scratch_bytes = bytes;
+        w->scratch_captured = false;
     }
     return w->scratch;
 }
+
+int32_t scratch_error() { return tl_scratch_code; }
 
 // ------------------------------------------------------------------------------------------
 // kernel timing
@@ -358,6 +401,16 @@ int32_t stade_hip_device_error(int32_t* flag) {
     STADE_TRY_HIP(hipMemcpy(&h, (int32_t*)(w->dscalars + kErrFlagSlot), sizeof h, hipMemcpyDeviceToHost));
     STADE_TRY_HIP(hipMemcpy((int32_t*)(w->dscalars + kErrFlagSlot), &z, sizeof z, hipMemcpyHostToDevice));
     *flag = h;
+    return STADE_HIP_OK;
+}
+
+int32_t stade_hip_workspace_info(int64_t* scratch_bytes, int64_t* retired) {
+    if (!scratch_bytes || !retired) return set_error(STADE_HIP_EINVAL, "stade_hip_workspace_info: null output");
+    Workspace* w = workspace();
+    if (!w) return STADE_HIP_ENOMEM;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    *scratch_bytes = (int64_t)w->scratch_bytes;
+    *retired = (int64_t)g_retired.size();
     return STADE_HIP_OK;
 }
 

@@ -23,7 +23,7 @@ import os
 from pathlib import Path
 
 from .api import (  # noqa: F401
-    StadeHipError, StadeHipBoundsError, lib, lib_path, ENTRY_POINTS, device_error,
+    StadeHipError, StadeHipBoundsError, lib, lib_path, ENTRY_POINTS, device_error, workspace_info,
     affine_lsq_b, affine_lsq_d, affine_lsq_hv,
     diffusion2d_b, diffusion2d_d, diffusion2d_hv,
     burgers1d_b, burgers1d_d, burgers1d_hv, initstacks_burgers1d_b, burgers1d_stack_lengths,

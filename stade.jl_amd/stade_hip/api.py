@@ -98,6 +98,7 @@ def lib():
             getattr(L, nm).restype = ctypes.c_int32
         L.stade_hip_device_error.argtypes = [ctypes.POINTER(ctypes.c_int32)]
         L.stade_hip_free.argtypes = [P]
+        L.stade_hip_workspace_info.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
         L.stade_hip_synchronize.argtypes = [P]
         for nm, kinds in ENTRY_POINTS.items():
             f = getattr(L, nm)
@@ -201,6 +202,15 @@ def device_error() -> int:
     flag = ctypes.c_int32(0)
     _check("stade_hip_device_error", lib().stade_hip_device_error(ctypes.byref(flag)))
     return int(flag.value)
+
+
+def workspace_info() -> tuple[int, int]:
+    """(bytes of scratch held, scratch buffers retired) of the current device's library
+    workspace (`stade_hip_workspace_info`): a buffer is retired, not freed, when a larger call
+    needs more scratch after a graph captured a call that used it."""
+    b, r = ctypes.c_int64(0), ctypes.c_int64(0)
+    _check("stade_hip_workspace_info", lib().stade_hip_workspace_info(ctypes.byref(b), ctypes.byref(r)))
+    return int(b.value), int(r.value)
 
 
 def _bounds(fn: str, check: bool):

@@ -313,6 +313,12 @@ def _gather(loop: For, n_loop: int):
                 raise _No
         if need & {n for n in defs if n not in single}:
             raise _No
+        # every body scalar the value reads is computed by the slice, before the statement: a
+        # name the body assigns only later carries the previous iteration's value, which the
+        # source iteration's recomputation would not reproduce (sums and end-of-iteration
+        # resets elsewhere in the body keep their order in the rewritten loop)
+        if (need & set(defs)) - {body[kk].lhs.name for kk in sl}:
+            raise _No
         tag = f"__g{n_loop}_{q}"
         # the source iteration: t's coordinates shifted back
         src_c = {}

@@ -562,7 +562,7 @@ class Emitter:
                 if ctx.lds == ref.name:
                     self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::lds_add(&lds_priv[_i], {val}); else oob(); }}")
                 else:
-                    self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::wave_add(&a.A_{nm}[_i], {val}); else oob(); }}")
+                    self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::wave_add(&a.A_{nm}[_i], {val}, a.st); else oob(); }}")
                 return
             c, _ = fl.ex(s.rhs, ctx)
             self.emit(("if (_lane == 0) " if self.one_lane() else "") +
@@ -692,6 +692,9 @@ class Emitter:
         if value is None or isinstance(value, Nothing_):
             return
         items = value.items if isinstance(value, Tup) else (value,)
+        if len(items) > 16:
+            # the frame holds 16 returned values (r, ri, rk) and the host copies back as many
+            raise LowerError(f"{fl.f.name}: returns {len(items)} values; the lowering returns at most 16")
         for k, it in enumerate(items):
             c, t = fl.ex(it, self.ctx)
             if t == "i":
@@ -913,15 +916,16 @@ class FuncGen:
             out.append("        __syncthreads();")
             out.append(f"        for (int64_t _j = threadIdx.x; _j < {n_len}; _j += blockDim.x)")
             out.append(f"            if (lds_priv[_j] != ({et_of(n)})0) stade_lowered::atomic_add(&a.A_{cname(n)}[_j], lds_priv[_j]);")
+            out.append("        if (threadIdx.x == 0) stade_lowered::count(a.st, stade_lowered::ST_PRIV_BLOCK);")
             out.append("    }")
         # the block's sums: one atomic addition per block
         for n, r in reds.items():
-            out.append(f"    stade_lowered::block_add(&fr.v_{cname(n)}, {r}, reinterpret_cast<{fl.cty(fl.scalars[n])}*>(_blk));")
+            out.append(f"    stade_lowered::block_add(&fr.v_{cname(n)}, {r}, reinterpret_cast<{fl.cty(fl.scalars[n])}*>(_blk), a.st);")
         for n, r in hoist.items():
             ref = pl.arrays[n].index
             out.append(f"    {{ const int64_t _i = {Ctx(fl, dict(locals_), hl).lin(ref)};")
             out.append(f"      stade_lowered::block_add((uint64_t)_i < (uint64_t)a.N_{cname(n)} ? &a.A_{cname(n)}[_i] : nullptr, {r}, "
-                       f"reinterpret_cast<{et_of(n)}*>(_blk)); }}")
+                       f"reinterpret_cast<{et_of(n)}*>(_blk), a.st); }}")
         pre = "    extern __shared__ __align__(16) unsigned char lds_raw[];\n    (void)lds_raw;\n" if cands else ""
         if reds or hoist:
             pre += "    __shared__ double _blk[16];  // the waves' sums of block_add\n"
@@ -942,6 +946,7 @@ class FuncGen:
             sp.append("    }")
             sp += red_decl
             sp.append("    const int _lane = threadIdx.x & 63;")
+            sp.append("    if (threadIdx.x == 0) stade_lowered::count(a.st, stade_lowered::ST_SPLIT_BLOCK);")
             sp.append("    for (int64_t _k = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; _k < _trip;"
                       " _k += ((int64_t)gridDim.x * blockDim.x) >> 6) {")
             sp += body_lines(True, None, wave=True)
@@ -1133,6 +1138,7 @@ class FuncGen:
             if n not in fl.arrays:
                 args_fields.append(f"    {fl.cty(fl.scalars.get(n, 'f'))} s_{cname(n)};")
         args_fields.append(f"    int64_t hl[{max(1, fl.nhl)}];")
+        args_fields.append("    unsigned long long* st;   // path statistics (null: not counted)")
         self.ops(fl.ops)
         self.merge_serial_launches()
         init = ["    fr.nret = 0;", "    fr.oob = 0;"] + [f"    fr.v_{cname(n)} = a.s_{cname(n)};" for n in f.args if n not in fl.arrays]
@@ -1199,11 +1205,20 @@ class FuncGen:
             "    }",
             "    return g_buf[slot];",
             "}",
+            "// where the kernels count their accumulation paths (stade_lowered::ST_*; null: nowhere)",
+            "static unsigned long long* g_stats = nullptr;",
             "}  // namespace",
+            "",
+            "// Test hook, not part of the generated function's ABI: until it is called again with null,",
+            "// every call of this function adds its path counts into stats[0..ST_N) (device memory).",
+            f"extern \"C\" void stade_hip_gen_{cname(f.name)}_set_stats(unsigned long long* stats) {{",
+            f"    {self.ns}::g_stats = stats;",
+            "}",
             "",
             f"extern \"C\" int32_t stade_hip_gen_{cname(f.name)}({', '.join(params)}) {{",
             f"    using namespace {self.ns};",
             "    Args a{};",
+            "    a.st = g_stats;",
             *fill,
             "    hipError_t _e;",
             "    kinit<<<1, 1, 0, stream>>>(a);",

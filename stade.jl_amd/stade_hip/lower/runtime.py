@@ -50,11 +50,12 @@ def _src_key(src: str) -> str:
 _so_locks: dict = {}
 
 
-def build_source(src: str, stem: str) -> Path:
-    """Compile HIP source into the generated-library directory (once per source text; one
-    lock per library, so that different sources compile in parallel threads)."""
-    GEN_LIB.mkdir(parents=True, exist_ok=True)
-    so = GEN_LIB / f"{stem}_{_src_key(src)}.so"
+def build_source(src: str, stem: str, out_dir: Path | None = None) -> Path:
+    """Compile HIP source into the generated-library directory (or `out_dir`), once per source
+    text; one lock per library, so that different sources compile in parallel threads."""
+    out_dir = Path(out_dir) if out_dir is not None else GEN_LIB
+    out_dir.mkdir(parents=True, exist_ok=True)
+    so = out_dir / f"{stem}_{_src_key(src)}.so"
     with _lock:
         lk = _so_locks.setdefault(so, threading.Lock())
     with lk:
@@ -91,6 +92,25 @@ class LoweredLib:
 
     def plan(self, name: str) -> list[str]:
         return self.sigs[name]["plan"]
+
+    def set_stats(self, name: str, counters=None):
+        """Count the accumulation paths of function `name`'s launches into `counters` (an int64
+        CUDA tensor of at least 8 elements, added to, never cleared) until called with None.
+        Slots: 0 wave-aggregated atomics (one per wave), 1 per-lane atomics (one per wave), 2
+        blocks of an LDS-privatised variant, 3 blocks of the wave-per-iteration form, 4 block
+        sums added (`csrc/lowered_rt.hpp`, ST_*).  A test hook: the calls of the generated
+        function are unchanged."""
+        f = getattr(self.lib, f"stade_hip_gen_{hipgen.cname(name)}_set_stats")
+        f.restype = None
+        f.argtypes = [ctypes.c_void_p]
+        if counters is None:
+            f(None)
+            return
+        import torch
+        if not (isinstance(counters, torch.Tensor) and counters.is_cuda and counters.dtype == torch.int64
+                and counters.is_contiguous() and counters.numel() >= 8):
+            raise ValueError("counters must be a contiguous int64 CUDA tensor of at least 8 elements")
+        f(ctypes.c_void_p(counters.data_ptr()))
 
     def _fn(self, name):
         if name not in self._fns:
@@ -185,18 +205,20 @@ def _ret_kinds(text: str, precision: str, arg_types) -> dict:
     return out
 
 
-def lower(src, precision: str = "f64", arg_types: dict | None = None, tag: str | None = None) -> LoweredLib:
-    """Lower a generated file (path or text), build it once, load it."""
+def lower(src, precision: str = "f64", arg_types: dict | None = None, tag: str | None = None,
+          out_dir: Path | None = None) -> LoweredLib:
+    """Lower a generated file (path or text), build it once (into stade.jl_amd/lib/gen, or
+    `out_dir`), load it."""
     p = Path(src) if not (isinstance(src, str) and "\n" in src) else None
     text = p.read_text() if p is not None else str(src)
-    key = (text, precision, repr(sorted((arg_types or {}).items())))
+    key = (text, precision, repr(sorted((arg_types or {}).items())), str(out_dir))
     ck = hashlib.sha256(repr(key).encode()).hexdigest()
     if ck in _cache:
         return _cache[ck]
     hip, sigs = hipgen.generate(text, precision, arg_types)
     for name, kinds in _ret_kinds(text, precision, arg_types).items():
         sigs[name]["ret"] = kinds
-    so = build_source(hip, tag or (p.stem if p is not None else "inline"))
+    so = build_source(hip, tag or (p.stem if p is not None else "inline"), out_dir)
     lib = LoweredLib(so, sigs, precision, text)
     _cache[ck] = lib
     return lib

@@ -176,3 +176,83 @@ def test_lowered_affine_lsq_narrow(mode, mn):
     shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
     case, low = _case(CORPUS / f"affine_lsq_{mode}.jl", "affine_lsq", mode, shapes, dict(i_m=m, i_n=n))
     _check(case, low, f"affine_lsq_{mode}")
+
+
+# ---- which accumulation path ran: the kernels' path counters -------------------------------
+
+def _paths(case, low, fname):
+    """Run a case (checked against the oracle as above) with the lowered function's path
+    counters on; returns them by name (`LoweredLib.set_stats`)."""
+    import torch
+    st = torch.zeros(8, dtype=torch.int64, device="cuda")
+    low.set_stats(fname, st)
+    try:
+        _check(case, low, fname)
+    finally:
+        low.set_stats(fname, None)
+    c = st.cpu().tolist()
+    print(f"{case.label}: paths agg={c[0]} lane={c[1]} priv={c[2]} split={c[3]} block={c[4]}", flush=True)
+    return dict(agg=c[0], lane=c[1], priv=c[2], split=c[3], block=c[4])
+
+
+def _matvec_b(m, n):
+    shapes = {k + s: v for k, v in dict(loss=1, a=m * n, x=n, y=m).items() for s in ("", "b", "d", "bd")}
+    return _case(GENERIC / "matvec_scatter_b.jl", "matvec_scatter", "b", shapes, dict(i_m=m, i_n=n),
+                 label=f"paths matvec_scatter_b m={m} n={n}")
+
+
+def _binsum_b(n, b):
+    from oracle import rng as jrng
+    shapes = {a + s: v for a, v in dict(loss=1, v=n, c=b).items() for s in ("", "b", "d", "bd")}
+    g = jrng.Xoshiro(41 + n)
+    bins = np.array([1 + int(g.rand() * b) for _ in range(n)], dtype=np.int64)
+    return _case(GENERIC / "binsum_b.jl", "binsum", "b", shapes, dict(i_n=n, i_b=b), int_arrays=dict(bins=bins),
+                 label=f"paths binsum_b n={n} bins={b}")
+
+
+def test_paths_every_lane_shares_the_target():
+    """xb[j] at j = div(idx - 1, 128) + 1: the 64 lanes of every wave add into one element, and
+    xb (8192 doubles, 64 KiB) is too large for the LDS copy, so every wave of the adjoint loop
+    takes the aggregated branch: exactly 128 * 8192 / 64 single atomics, none per lane.  The
+    forward loop's y (128 doubles, 8192 iterations per element) takes the LDS-privatised
+    variant, and the loss sum one block total per block."""
+    case, low = _matvec_b(128, 8192)
+    p = _paths(case, low, "matvec_scatter_b")
+    assert p["agg"] == 128 * 8192 // 64 and p["lane"] == 0
+    assert p["priv"] > 0 and p["block"] > 0
+
+
+def test_paths_no_lane_shares_the_target():
+    """One row: every lane of a wave adds into its own xb[j] (70000 doubles, beyond the LDS
+    copy), so the wave-aggregated branch never fires and every wave of the adjoint loop adds
+    per lane (1093 full waves and a partial one).  The forward loop's y has one element and
+    70000 iterations: its LDS-privatised variant runs."""
+    case, low = _matvec_b(1, 70000)
+    p = _paths(case, low, "matvec_scatter_b")
+    assert p["agg"] == 0 and p["lane"] == -(-70000 // 64) and p["priv"] > 0
+
+
+def test_paths_lds_privatised_bins():
+    """16 bins and 100000 samples (6250 per bin): the LDS-privatised variant, and no global
+    per-lane or per-wave atomics into the bins."""
+    case, low = _binsum_b(100000, 16)
+    p = _paths(case, low, "binsum_b")
+    assert p["priv"] > 0 and p["lane"] == 0 and p["agg"] == 0
+
+
+def test_paths_global_atomics_for_sparse_bins():
+    """3000 bins and 20000 samples (under 32 per bin): no LDS copy; random bins, so waves add
+    per lane."""
+    case, low = _binsum_b(20000, 3000)
+    p = _paths(case, low, "binsum_b")
+    assert p["priv"] == 0 and p["lane"] > 0
+
+
+def test_paths_narrow_output_form():
+    """11 outputs of a 19990-tap correlation: the wave-per-iteration kernel runs."""
+    n, k = 20000, 19990
+    shapes = {a + s: v for a, v in dict(loss=1, inp=n, w=k, out=n - k + 1).items() for s in ("", "b", "d", "bd")}
+    case, low = _case(GENERIC / "window1d_d.jl", "window1d", "d", shapes, dict(i_n=n, i_k=k),
+                      label="paths window1d_d narrow")
+    p = _paths(case, low, "window1d_d")
+    assert p["split"] > 0

@@ -322,6 +322,26 @@ def test_gather_only_where_exact(what, expect):
     assert _gathered(_SCATTER.replace("WHAT", what), "s_b") == expect
 
 
+def test_no_gather_for_a_value_carried_from_the_previous_iteration():
+    """c is assigned after the scatter that reads it, so the scatter adds the previous
+    iteration's x (xb[t] gets x[t - 2]); a gather that recomputed c from the source iteration
+    would add x[t - 1] instead.  The loop must be left as it is (and then runs in order)."""
+    text = """function s_b(x, xb, n)
+    c = 0.0
+    for i = 1:n
+        ip = mod(i, n) + 1
+        xb[ip] = xb[ip] + c
+        c = x[i]
+    end
+    return nothing
+end
+"""
+    assert _gathered(text, "s_b") == 0
+    # and with the carried value read by a statement of the value's slice
+    text2 = text.replace("xb[ip] = xb[ip] + c", "d = 2.0 * c\n        xb[ip] = xb[ip] + d")
+    assert _gathered(text2, "s_b") == 0
+
+
 def test_no_gather_for_a_map_that_is_not_a_bijection():
     text = _SCATTER.replace("ip = mod(i, n) + 1", "ip = mod(i, 2) + 1").replace("WHAT", "old")
     assert _gathered(text, "s_b") == 0

@@ -53,3 +53,31 @@ def test_noalloc_matches_allocating_entry_point(sizes):
         for key in ("loss", "ub", "un", "unb"):
             assert torch.equal(a[key], b[key]), f"n={n}: {key} differs between the two entry points"
         assert not torch.any(b["unb"]), "unb is reset"
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    """Two calls on two streams, issued back to back with no synchronisation between them,
+    share the one static scratch array: the library orders the second after the first (the
+    device's call lock and an event wait, as for every entry point), so each result equals the
+    allocating entry point's on the same inputs, bit for bit."""
+    import torch
+    ref, new = _fn("stade_hip_diffusion2d_b"), _fn("stade_hip_diffusion2d_b_noalloc")
+    n = 4096
+    print(f"diffusion2d_b_noalloc n={n} on two streams", flush=True)
+    ins = [_inputs(n, 200 + k) for k in range(2)]
+    want = []
+    for a in ins:
+        w = {key: v.clone() for key, v in a.items()}
+        _run(ref, w, n)
+        want.append(w)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for s, a in zip(streams, ins):
+        with torch.cuda.stream(s):
+            _run(new, a, n)
+    torch.cuda.synchronize()
+    for k, (a, w) in enumerate(zip(ins, want)):
+        for key in ("loss", "ub", "un", "unb"):
+            assert torch.equal(a[key], w[key]), f"call {k}: {key} differs from the allocating entry point"
