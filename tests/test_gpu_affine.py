@@ -7,9 +7,11 @@ pytestmark = pytest.mark.gpu
 
 # column tiles of 64 are grouped into at most 16 row-sum chunks: one tile a chunk up to n = 1024,
 # then 2 (2048; 1088: 17 tiles in 9 chunks, the last a single tile), 3 (3000: 47 tiles, the
-# last chunk short) and 5 tiles a chunk (5000: 79 tiles, a ragged last tile)
+# last chunk short), 5 (5000: 79 tiles, a ragged last tile), 8 (4096^2: 64 tiles in 8 full
+# chunks) and 9 tiles a chunk (8200: 129 tiles, the last chunk one tile short of 9).
 SIZES = [(1, 1), (3, 5), (64, 64), (65, 130), (200, 77), (1, 300), (300, 1), (1024, 1024), (4, 0), (0, 3),
-         (5000, 3), (5000, 0), (2048, 2048), (1000, 3000), (100, 1088), (70, 5000)]
+         (5000, 3), (5000, 0), (2048, 2048), (1000, 3000), (100, 1088), (70, 5000), (70, 8200), (4096, 4096),
+         (3000, 5000)]
 
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
