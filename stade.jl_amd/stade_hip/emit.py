@@ -345,7 +345,7 @@ def _lowered_call(fname: str, sig: dict, cfun: str, eltype: str) -> str:
     return "\n".join(lines)
 
 
-def _lowered_file(text: str, in_path, out_path, precision) -> str:
+def _lowered_file(text: str, in_path, out_path, precision, inbounds: bool = True) -> str:
     from .lower import LowerError, hipgen, lower
     if precision in (None, "Float64", "f64"):
         prec = "f32" if re.search(r"\bFloat32\b", text) and precision is None else "f64"
@@ -355,7 +355,7 @@ def _lowered_file(text: str, in_path, out_path, precision) -> str:
         raise StadeHipRefusal(f"precision={precision}: the lowering writes Float64 or Float32 code")
     eltype = "Float32" if prec == "f32" else "Float64"
     try:
-        lib = lower(text, prec, tag=Path(in_path).stem)
+        lib = lower(text, prec, tag=Path(in_path).stem, inbounds=inbounds)
     except LowerError as e:
         raise StadeHipRefusal(f"{Path(in_path).name}: the general lowering cannot take this file: {e}") from e
     funcs = _split_functions(text)
@@ -392,8 +392,10 @@ def stade_hip_file(in_path, out_path, *, precision=None, inbounds: bool = True, 
     `inbounds` mirrors it too: with `inbounds=false` the host functions read the device
     error flag after the call (one synchronisation) and throw a `BoundsError` where an
     index value held in an Int64 array (the MLP labels) is out of range; with the default
-    `true`, as in the reference's GPU code, nothing is checked.  (Lowered files check every
-    access either way.)
+    `true`, as in the reference's GPU code, nothing is checked.  A file that goes through the
+    general lowering is built the same way: with `inbounds=false` every array access is checked
+    and an index out of range throws `BoundsError`; with `true` accesses are unchecked, as
+    under Julia's `@inbounds`.
     `general=False` refuses, instead of lowering, a file whose primal matches none of the
     library's hand-written kernels.
     Returns the written text.
@@ -404,7 +406,7 @@ def stade_hip_file(in_path, out_path, *, precision=None, inbounds: bool = True, 
     except StadeHipRefusal:
         if not general:
             raise
-        return _lowered_file(text, in_path, out_path, precision)
+        return _lowered_file(text, in_path, out_path, precision, inbounds)
     if precision not in (None, spec.eltype):
         raise StadeHipRefusal(f"{spec.name}: libstade_hip implements {spec.eltype} only, precision={precision} requested")
     libp = lib_path or "libstade_hip"

@@ -31,7 +31,7 @@ import re
 from dataclasses import dataclass, field
 
 from .analysis import ArrayUse, ParallelLoop, Types, classify, infer_types, split_loops, _reads_of, _thaw
-from . import fuse, gather
+from . import finish, fuse, gather
 from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, If, LowerError, Nothing_, Num, Range,
                      Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
@@ -98,7 +98,15 @@ class ReturnOp:
 
 
 class FuncLower:
-    def __init__(self, f: Func, precision: str, arg_types: dict | None = None):
+    def __init__(self, f: Func, precision: str, arg_types: dict | None = None, stacks_allocated: set | None = None,
+                 inbounds: bool = True, dead_scalars: bool = True, merge_accum: bool = True):
+        # kernel finishing (finish.py, as `stade_gpu` runs it before and after planning): dead
+        # restores and the stack stores nothing reads then, merged accumulations, dead scalars
+        f, self.finish_rec = finish.finish(f, stacks_allocated or set(), inbounds=inbounds, dead=dead_scalars,
+                                           merge=merge_accum)
+        # inbounds (`stade_amdgpu_file`'s default): no check on array accesses; otherwise an
+        # index out of range raises the frame's flag and is reported as a BoundsError
+        self.inbounds = inbounds
         # periodic scatters into owner-computes gathers where the index maps are bijections
         # (gather.py); STADE_LOWER_GATHER=0 keeps every loop as written
         if os.environ.get("STADE_LOWER_GATHER", "1") != "0":
@@ -489,8 +497,11 @@ class Ctx:
         return " + ".join(parts)
 
     def ref(self, ref: Ref) -> str:
-        # bounds-checked: an index outside the array raises the frame's flag (the call then
-        # reports Julia's BoundsError) and reads 0 instead of touching memory
+        # inbounds: a plain load; otherwise bounds-checked: an index outside the array raises
+        # the frame's flag (the call then reports Julia's BoundsError) and reads 0 instead of
+        # touching memory
+        if self.fl.inbounds:
+            return f"a.A_{cname(ref.name)}[{self.lin(ref)}]"
         return f"rd(a.A_{cname(ref.name)}, {self.lin(ref)}, a.N_{cname(ref.name)})"
 
 
@@ -554,19 +565,25 @@ class Emitter:
                 c, _ = fl.ex(other, ctx)
                 val = f"({et})({c})" if sign == "+" else f"(-({et})({c}))"
                 nm = cname(ref.name)
+                chk = "" if fl.inbounds else f"if ((uint64_t)_i < (uint64_t)a.N_{nm}) "
+                els = "" if fl.inbounds else " else oob();"
                 if ref.name in ctx.hoist:
                     self.emit(f"{{ const int64_t _i = {ctx.lin(ref)};")
-                    self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) {ctx.hoist[ref.name]} += {val}; else oob(); }}")
+                    self.emit(f"  {chk}{ctx.hoist[ref.name]} += {val};{els} }}")
                     return
                 self.emit(("if (_lane == 0) " if self.one_lane() else "") + f"{{ const int64_t _i = {ctx.lin(ref)};")
                 if ctx.lds == ref.name:
-                    self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::lds_add(&lds_priv[_i], {val}); else oob(); }}")
+                    self.emit(f"  {chk}stade_lowered::lds_add(&lds_priv[_i], {val});{els} }}")
                 else:
-                    self.emit(f"  if ((uint64_t)_i < (uint64_t)a.N_{nm}) stade_lowered::wave_add(&a.A_{nm}[_i], {val}, a.st); else oob(); }}")
+                    self.emit(f"  {chk}stade_lowered::wave_add(&a.A_{nm}[_i], {val}, a.st);{els} }}")
                 return
             c, _ = fl.ex(s.rhs, ctx)
-            self.emit(("if (_lane == 0) " if self.one_lane() else "") +
-                      f"wr(a.A_{cname(ref.name)}, {ctx.lin(ref)}, a.N_{cname(ref.name)}, ({et})({c}));")
+            if fl.inbounds:
+                self.emit(("if (_lane == 0) " if self.one_lane() else "") +
+                          f"a.A_{cname(ref.name)}[{ctx.lin(ref)}] = ({et})({c});")
+            else:
+                self.emit(("if (_lane == 0) " if self.one_lane() else "") +
+                          f"wr(a.A_{cname(ref.name)}, {ctx.lin(ref)}, a.N_{cname(ref.name)}, ({et})({c}));")
             return
         if isinstance(s, For) and id(s) in self.split_loops:
             self.split_for(s)
@@ -924,8 +941,9 @@ class FuncGen:
         for n, r in hoist.items():
             ref = pl.arrays[n].index
             out.append(f"    {{ const int64_t _i = {Ctx(fl, dict(locals_), hl).lin(ref)};")
-            out.append(f"      stade_lowered::block_add((uint64_t)_i < (uint64_t)a.N_{cname(n)} ? &a.A_{cname(n)}[_i] : nullptr, {r}, "
-                       f"reinterpret_cast<{et_of(n)}*>(_blk), a.st); }}")
+            tgt = (f"&a.A_{cname(n)}[_i]" if fl.inbounds else
+                   f"(uint64_t)_i < (uint64_t)a.N_{cname(n)} ? &a.A_{cname(n)}[_i] : nullptr")
+            out.append(f"      stade_lowered::block_add({tgt}, {r}, reinterpret_cast<{et_of(n)}*>(_blk), a.st); }}")
         pre = "    extern __shared__ __align__(16) unsigned char lds_raw[];\n    (void)lds_raw;\n" if cands else ""
         if reds or hoist:
             pre += "    __shared__ double _blk[16];  // the waves' sums of block_add\n"
@@ -1307,10 +1325,12 @@ extern "C" const char* stade_hip_gen_last_error(void) { return g_gen_err; }
 """
 
 
-def generate(text: str, precision: str = "f64", arg_types: dict | None = None) -> tuple[str, dict]:
+def generate(text: str, precision: str = "f64", arg_types: dict | None = None, inbounds: bool = True,
+             dead_scalars: bool = True, merge_accum: bool = True) -> tuple[str, dict]:
     """HIP source for every generated function of `text` (the initstacks_* functions stay on
     the host) and, per function, its signature: [(name, kind, ndim)] with kind 'Af', 'Ai',
-    'f', 'i'."""
+    'f', 'i'.  `inbounds`, `dead_scalars` and `merge_accum` are `stade_gpu`'s switches
+    (/root/reference/src/STADE.jl:18522), on by default as `stade_amdgpu_file` has them."""
     from .syntax import parse
     funcs = parse(text)
     src = [PRELUDE]
@@ -1336,7 +1356,8 @@ def generate(text: str, precision: str = "f64", arg_types: dict | None = None) -
             continue
         kinds = {a: k for a, k in stack_kinds.items() if a in f.args}
         kinds.update((arg_types or {}).get(f.name) or {})
-        fl = FuncLower(f, precision, kinds)
+        fl = FuncLower(f, precision, kinds, stacks_allocated={a for a, k in stack_kinds.items() if k in ("Ai", "Af")},
+                       inbounds=inbounds, dead_scalars=dead_scalars, merge_accum=merge_accum)
         src.append(FuncGen(fl).source())
         sig = []
         for n in f.args:
@@ -1344,7 +1365,8 @@ def generate(text: str, precision: str = "f64", arg_types: dict | None = None) -
                 sig.append((n, "Ai" if fl.arrays[n] == "i" else "Af", fl.T.ndim.get(n, 1)))
             else:
                 sig.append((n, fl.scalars.get(n, "f"), 0))
-        sigs[f.name] = dict(args=sig, plan=describe(fl.ops), reasons=list(fl.reasons))
+        sigs[f.name] = dict(args=sig, plan=describe(fl.ops), reasons=list(fl.reasons), finish=fl.finish_rec,
+                            inbounds=inbounds)
     return "\n".join(src), sigs
 
 

@@ -206,16 +206,22 @@ def _ret_kinds(text: str, precision: str, arg_types) -> dict:
 
 
 def lower(src, precision: str = "f64", arg_types: dict | None = None, tag: str | None = None,
-          out_dir: Path | None = None) -> LoweredLib:
+          out_dir: Path | None = None, inbounds: bool = True, dead_scalars: bool = True,
+          merge_accum: bool = True) -> LoweredLib:
     """Lower a generated file (path or text), build it once (into stade.jl_amd/lib/gen, or
-    `out_dir`), load it."""
+    `out_dir`), load it.  `inbounds`, `dead_scalars` and `merge_accum` are the reference's
+    switches of the same names (on by default, as `stade_amdgpu_file` has them): with
+    `inbounds=False` every array access is checked and an index out of range raises
+    StadeHipBoundsError; with `inbounds=True` such an index is undefined behaviour, as under
+    Julia's @inbounds."""
     p = Path(src) if not (isinstance(src, str) and "\n" in src) else None
     text = p.read_text() if p is not None else str(src)
-    key = (text, precision, repr(sorted((arg_types or {}).items())), str(out_dir))
+    key = (text, precision, repr(sorted((arg_types or {}).items())), str(out_dir), inbounds, dead_scalars, merge_accum)
     ck = hashlib.sha256(repr(key).encode()).hexdigest()
     if ck in _cache:
         return _cache[ck]
-    hip, sigs = hipgen.generate(text, precision, arg_types)
+    hip, sigs = hipgen.generate(text, precision, arg_types, inbounds=inbounds, dead_scalars=dead_scalars,
+                                merge_accum=merge_accum)
     for name, kinds in _ret_kinds(text, precision, arg_types).items():
         sigs[name]["ret"] = kinds
     so = build_source(hip, tag or (p.stem if p is not None else "inline"), out_dir)

@@ -145,13 +145,15 @@ def test_emitted_mlp_label_out_of_range_throws(tmp_path, bad):
 
 @pytest.mark.parametrize("bad", [0, 17])
 def test_emitted_lowered_bin_out_of_range_throws(tmp_path, bad):
-    """An index outside its array in a lowered file: every lowered access is checked, the
-    kernel skips the access and flags it, the emitted host code throws BoundsError."""
+    """An index outside its array in a lowered file written with `inbounds=false`: every
+    lowered access is checked, the kernel skips the access and flags it, the emitted host code
+    throws BoundsError.  (With the default `inbounds=true`, as under Julia's @inbounds, such an
+    index is undefined behaviour; no test gives one to an unchecked build.)"""
     import torch
     n, b = 5000, 16
     bins = _bins(n, b, 9)
     bins[1234] = bad
-    host = _host(tmp_path, GENERIC / "binsum_b.jl")
+    host = _host(tmp_path, GENERIC / "binsum_b.jl", inbounds=False)
     dev = lambda k: torch.zeros(k, dtype=torch.float64, device="cuda")
     v = torch.randn(n, dtype=torch.float64, device="cuda")
     args = [dev(1), torch.ones(1, dtype=torch.float64, device="cuda"), v, dev(n),

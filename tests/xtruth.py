@@ -397,7 +397,12 @@ def run(text: str, fname: str, args):
     the final contents of every array argument (None for scalars) and the returned values
     as a tuple (empty for `nothing`)."""
     funcs = {f.name: f for f in S.parse(text)}
-    f = funcs[fname]
+    return run_func(funcs[fname], args)
+
+
+def run_func(f, args):
+    """`run` on a parsed function (a syntax tree, transformed or not)."""
+    fname = f.name
     if len(args) != len(f.args):
         raise TypeError(f"{fname} takes {len(f.args)} arguments, got {len(args)}")
     env = {a: _to_j(v) for a, v in zip(f.args, args)}
