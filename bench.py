@@ -673,6 +673,49 @@ def measure(wl: Workload, steps: int, warmup: int, dev) -> dict:
     return out
 
 
+def twins_bench(dev) -> None:
+    """The flat twins of the general lowering against its ordinary form (the same text lowered
+    with STADE_LOWER_TWINS=0): ms per call of flatmv_d and flatmv_b, fp64, seeded N(0,1) inputs,
+    20 calls after 3 warm-ups."""
+    import torch
+    from stade_hip.lower import runtime
+    gen = ROOT / "stade.jl_amd" / "corpus" / "generic"
+    libs = {}
+    for tw in ("1", "0"):
+        os.environ["STADE_LOWER_TWINS"] = tw
+        runtime._cache.clear()
+        libs[tw] = {m: runtime.lower(gen / f"flatmv_{m}.jl", "f64") for m in ("b", "d")}
+    os.environ.pop("STADE_LOWER_TWINS", None)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+
+    def run(low, mode, m, n, reps=20):
+        f = lambda k: torch.randn(k, dtype=torch.float64, device=dev, generator=g)
+        z = lambda k: torch.zeros(k, dtype=torch.float64, device=dev)
+        if mode == "b":
+            args = [z(1), torch.ones(1, dtype=torch.float64, device=dev), f(m * n), z(m * n), f(n), z(n), z(m), z(m), m, n]
+        else:
+            args = [z(1), z(1), f(m * n), f(m * n), f(n), f(n), z(m), z(m), m, n]
+        for _ in range(3):
+            low.call(f"flatmv_{mode}", *args)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            low.call(f"flatmv_{mode}", *args)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps * 1e3
+
+    for m, n, what in [(40960, 1024, "MLP head z = W2 h1 flattened: 40960 outputs of 1024 terms"),
+                       (4096, 1024, "4096 rows of 1024"), (1024, 8192, "1024 rows of 8192"),
+                       (10, 1 << 22, "10 outputs of 4194304 terms (the row twin's chunks)")]:
+        for mode in ("d", "b"):
+            t_on, t_off = run(libs["1"][mode], mode, m, n), run(libs["0"][mode], mode, m, n)
+            nbytes = 8 * m * n * (2 if mode == "d" else 3)
+            print(json.dumps({"shape": what, "m": m, "n": n, "function": f"flatmv_{mode}", "twins_ms": round(t_on, 4),
+                              "ordinary_ms": round(t_off, 4), "speedup": round(t_off / t_on, 2),
+                              "twins_GBps": round(nbytes / t_on / 1e6, 1)}), flush=True)
+
+
 def cpu_baseline(wl: Workload, budget_s: float = 12.0, max_runs: int = 30) -> dict | None:
     sample = wl.cpu_sample()
     if sample is None:
@@ -737,6 +780,10 @@ def main():
                     help="time, with torch's own kernels, what any evaluation of the affine config must pay at "
                          "1024^2 fp64: one launch moving its 24 MiB matrix bytes (wb += w), the same bytes split "
                          "over three dependent launches, and chains of 1 and 3 launches of one element each")
+    ap.add_argument("--twins", action="store_true",
+                    help="time the general lowering's flat-loop twins (row-block, column-block) against the ordinary "
+                         "form on the row-major flat mat-vec text (corpus/generic/flatmv_{b,d}.jl) at the MLP head's "
+                         "shape and others, one JSON line per shape and function")
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="run only torch's own elementwise kernels over the headline's bytes (4096^2 fp64: "
                          "un = u, ub += unb; 40 B per cell) and print their rate, a practical ceiling for "
@@ -762,6 +809,9 @@ def main():
         return
     if args.launch_floor:
         print(json.dumps(launch_floor(dev)))
+        return
+    if args.twins:
+        twins_bench(dev)
         return
     if args.stream_ceiling:
         n = 4096 * 4096

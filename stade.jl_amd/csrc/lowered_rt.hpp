@@ -105,6 +105,8 @@ enum : int {
     ST_PRIV_BLOCK = 2,   // blocks that accumulated into an LDS-privatised copy
     ST_SPLIT_BLOCK = 3,  // blocks of the wave-per-iteration (narrow-output) form
     ST_BLOCK_ADD = 4,    // block_add calls that added a nonzero block total
+    ST_ROW_BLOCK = 5,    // blocks of a flat loop's row-block twin
+    ST_COL_BLOCK = 6,    // blocks of a flat loop's column-block twin
     ST_N = 8,
 };
 

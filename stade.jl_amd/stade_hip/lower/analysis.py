@@ -687,3 +687,109 @@ def split_loops(pl: ParallelLoop, types: Types) -> dict:
         if ok:
             out[id(L)] = targets
     return out
+
+
+@dataclass
+class FlatTwin:
+    """A flat loop over the elements of an R x N row-major range whose accumulations all
+    target the row (kind 'row') or all the column (kind 'col'): see `flat_twin`."""
+    kind: str                  # 'row' | 'col'
+    N: object                  # the row length (an expression of Int arguments)
+    sites: list                # the accumulated arrays
+    iv: str                    # the row variable, i = div(idx - 1, N) + 1
+    jv: str                    # the column variable, j = mod(idx - 1, N) + 1
+
+
+def _derived(s, v, idxm1_names):
+    """(var, 'div'|'mod', N) of `x = div(r, N) + 1` / `x = mod(r, N) + 1` with r = v - 1 (or
+    a scalar holding it), else None (`cgen_rowblock_derived` /root/reference/src/STADE.jl:18162)."""
+    if not (isinstance(s, Assign) and isinstance(s.lhs, Var)):
+        return None
+    r = s.rhs
+    if not (isinstance(r, Bin) and r.op == "+" and isinstance(r.b, Num) and r.b.is_int and int(r.b.text) == 1):
+        return None
+    d = r.a
+    if not (isinstance(d, Call) and d.fn in ("div", "mod") and len(d.args) == 2):
+        return None
+    x = d.args[0]
+    is_vm1 = (isinstance(x, Bin) and x.op == "-" and x.a == Var(v) and isinstance(x.b, Num) and x.b.is_int
+              and int(x.b.text) == 1)
+    if not (is_vm1 or (isinstance(x, Var) and x.name in idxm1_names)):
+        return None
+    return s.lhs.name, d.fn, d.args[1]
+
+
+def flat_twin(pl: ParallelLoop, int_args: set) -> FlatTwin | None:
+    """The row-block or column-block twin of a parallel loop, or None.
+
+    The reference's twins (`cgen_rowblock_kernel` /root/reference/src/STADE.jl:18187,
+    `cgen_colblock_kernel` 18371) match a flat loop `for idx = 1:R*N` (ascending from 1, or
+    descending to 1) with `i = div(idx - 1, N) + 1` and `j = mod(idx - 1, N) + 1` whose body is
+    straight-line (scalar assignments, stores, accumulations) and whose accumulations go to at
+    most four arrays, each touched by nothing else in the body:
+    - 'row' when every accumulation's index reads i and nothing that depends on the column
+      (idx, j, or a scalar computed from them): the N iterations of a row add into one element;
+    - 'col' when every accumulation's index is j itself: the R iterations of a column do.
+    N must be an expression of the function's Int arguments (the host checks at run time that
+    the range is whole rows).  Loops with sums into scalars' last values read after the loop
+    (live-out scalars) are left to the ordinary form."""
+    loop = pl.loop
+    body = loop.body
+    v = loop.var
+    if not body or not all(isinstance(s, Assign) for s in body) or pl.live_out:
+        return None
+    r = loop.rng
+    step = 1 if r.step is None else (int(r.step.text) if isinstance(r.step, Num) and r.step.is_int else 0)
+    one = lambda e: isinstance(e, Num) and e.is_int and int(e.text) == 1
+    if not ((step == 1 and one(r.lo)) or (step == -1 and one(r.hi))):
+        return None
+    count = {}
+    for s in body:
+        if isinstance(s.lhs, Var):
+            count[s.lhs.name] = count.get(s.lhs.name, 0) + 1
+    vm1 = {s.lhs.name for s in body if isinstance(s.lhs, Var) and isinstance(s.rhs, Bin) and s.rhs.op == "-"
+           and s.rhs.a == Var(v) and isinstance(s.rhs.b, Num) and s.rhs.b.is_int and int(s.rhs.b.text) == 1
+           and count[s.lhs.name] == 1}
+    der = [d for d in (_derived(s, v, vm1) for s in body) if d is not None]
+    divs = [d for d in der if d[1] == "div"]
+    mods = [d for d in der if d[1] == "mod"]
+    if len(divs) != 1 or len(mods) != 1 or divs[0][2] != mods[0][2]:
+        return None
+    iv, jv, N = divs[0][0], mods[0][0], divs[0][2]
+    nn = {x.name for x in walk_expr(N) if isinstance(x, Var)}
+    if not nn or not nn <= int_args:
+        return None
+    if count.get(iv) != 1 or count.get(jv) != 1 or v in count:
+        return None
+    atomic = {n for n, u in pl.arrays.items() if u.kind == "atomic"}
+    if not atomic or len(atomic) > 4 or pl.reductions or any(u.hoist for u in pl.arrays.values()):
+        return None
+    # names whose value depends on the column: idx, j, and scalars computed from them, in order
+    tainted = {v, jv} | vm1
+    site_idx = {}
+    for s in body:
+        if isinstance(s.lhs, Var):
+            if s.lhs.name in (iv, jv) or s.lhs.name in vm1:
+                continue          # the row, the column and idx - 1 themselves
+            if _reads_of(s.rhs) & tainted:
+                tainted.add(s.lhs.name)
+            continue
+        if s.lhs.name in atomic:
+            if not (isinstance(s.rhs, Bin) and s.rhs.op in ("+", "-") and s.lhs in (s.rhs.a, s.rhs.b)):
+                return None
+            site_idx.setdefault(s.lhs.name, []).append(s.lhs)
+    # each accumulated array is touched only by its accumulations
+    for s in body:
+        for e in stmt_exprs(s):
+            for x in walk_expr(e):
+                if isinstance(x, Ref) and x.name in atomic and not (isinstance(s.lhs, Ref) and s.lhs.name == x.name):
+                    return None
+    refs = [ref for refs in site_idx.values() for ref in refs]
+    if len(site_idx) != len(atomic):
+        return None
+    if all(len(ref.idx) == 1 and ref.idx[0] == Var(jv) for ref in refs):
+        return FlatTwin("col", N, sorted(atomic), iv, jv)
+    if all(not (set().union(*(_reads_of(i) for i in ref.idx)) & tainted)
+           and iv in set().union(*(_reads_of(i) for i in ref.idx)) for ref in refs):
+        return FlatTwin("row", N, sorted(atomic), iv, jv)
+    return None

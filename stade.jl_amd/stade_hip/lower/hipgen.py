@@ -30,7 +30,7 @@ import re
 
 from dataclasses import dataclass, field
 
-from .analysis import ArrayUse, ParallelLoop, Types, classify, infer_types, split_loops, _reads_of, _thaw
+from .analysis import ArrayUse, ParallelLoop, Types, classify, flat_twin, infer_types, split_loops, _reads_of, _thaw
 from . import finish, fuse, gather
 from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, If, LowerError, Nothing_, Num, Range,
                      Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
@@ -39,6 +39,11 @@ MAX_BLOCKS = 8192          # grid of a parallel loop whose trip count the host c
 RED_MAX_BLOCKS = 2048      # at most, for a loop with sums (each block adds its sums once)
 PRIV_MAX_BYTES = 48 * 1024  # LDS-privatised accumulation target, at most
 PRIV_RATIO = 32            # and at least this many iterations per target element
+TWIN_MIN_N = 256           # flat twins: rows of at least this many iterations (`row_block`, `col_block`
+TWIN_MIN_ROWS = 64         # defaults of stade_gpu); the column twin at least this many rows (`cgen_colblock_min_rows`)
+ROWBLOCK_GRID = 4096       # the row twin splits few rows over several blocks: about this many blocks,
+ROWBLOCK_CHUNK = 2048      # each at least this many iterations of its row (the block's one atomic amortised)
+COLBLOCK_ROWS = 128        # rows of a column-block tile (`cgen_colblock_rows`), 8 row lanes x 32 columns
 SPLIT_MAX_TRIP = 16384     # a parallel loop with at most this many iterations (64 blocks of 256 threads)
 SPLIT_MIN_INNER = 256      # whose shared inner loop runs at least this many iterations (when the host
 SPLIT_MAX_TRIP_UNKNOWN = 4096  # can evaluate it; otherwise at most this many outer iterations) gives
@@ -127,6 +132,7 @@ class FuncLower:
         self.nhl = 0
         self.kernels: list[str] = []
         self.reasons: list[str] = []
+        self.twins: list = []          # (loop variable, 'row' | 'col', sites) of the flat twins
         self.refuse_reasons()
         self.ops = self.plan()
 
@@ -462,6 +468,7 @@ class Ctx:
         self.serial_acc = serial_acc   # accumulations as plain read-modify-writes
         self.reductions = reductions or {}
         self.lds = lds                 # array privatised in LDS (its accumulations go to lds_priv)
+        self.site_ix = {}              # hoisted array -> local recording its index (the flat twins)
 
     def var(self, n):
         if n in self.locals:
@@ -569,7 +576,8 @@ class Emitter:
                 els = "" if fl.inbounds else " else oob();"
                 if ref.name in ctx.hoist:
                     self.emit(f"{{ const int64_t _i = {ctx.lin(ref)};")
-                    self.emit(f"  {chk}{ctx.hoist[ref.name]} += {val};{els} }}")
+                    track = f" {ctx.site_ix[ref.name]} = _i;" if ref.name in ctx.site_ix else ""
+                    self.emit(f"  {chk}{ctx.hoist[ref.name]} += {val};{els}{track} }}")
                     return
                 self.emit(("if (_lane == 0) " if self.one_lane() else "") + f"{{ const int64_t _i = {ctx.lin(ref)};")
                 if ctx.lds == ref.name:
@@ -826,6 +834,77 @@ class FuncGen:
                 i += 1
         self.host = out
 
+    # -- flat twins ----------------------------------------------------------------------------
+    def twin_kernel(self, k: int, tw, head: list, guards: str, body_lines, n_dev: str) -> str:
+        """k<k>t, the row-block or column-block twin of a flat loop (`cgen_rowblock_kernel`
+        /root/reference/src/STADE.jl:18187, `cgen_colblock_kernel` 18371): the same iterations,
+        mapped so that the accumulations of a row (a column) meet in one block (one thread).
+        - row: block b runs the N iterations _k = b N .. b N + N - 1, which for an ascending
+          loop from 1, or a descending one to 1, are exactly row b + 1 (or R - b) of the range;
+          each thread sums its iterations' values per site in a register, the block adds them
+          in a fixed order and makes one atomic addition per site.
+        - col: a block of 32 columns x 8 row lanes takes COLBLOCK_ROWS rows; a thread sums its
+          column's rows in a register, the 8 lanes of a column add up in a fixed order through
+          LDS and one thread adds the tile's total, one atomic per column and tile.
+        The host launches it only when the range is whole rows (checked at run time)."""
+        fl = self.fl
+        sites = tw.sites
+        acc = {n: f"t_{cname(n)}" for n in sites}
+        ix = {n: f"ti_{cname(n)}" for n in sites}
+        et = lambda n: "int64_t" if fl.arrays[n] == "i" else fl.fty
+        out = list(head)
+        out.append(f"    if (!({guards})) {{")
+        out.append("        if (blockIdx.x != 0 || blockIdx.y != 0 || threadIdx.x != 0) return;")
+        out.append("        for (int64_t _k = 0; _k < _trip; ++_k) {")
+        out += body_lines(False, None)
+        out.append("        }")
+        out.append("        return;")
+        out.append("    }")
+        out.append(f"    const int64_t _tn = {n_dev};")
+        for n in sites:
+            out.append(f"    {et(n)} {acc[n]} = 0;")
+            out.append(f"    int64_t {ix[n]} = 0;")
+        lines = body_lines(True, None, twin_sites=acc, twin_ix=ix)
+        if tw.kind == "row":
+            # S = gridDim.x / rows blocks a row, each a chunk of ceil(N / S) >= 256 iterations
+            out.append("    if (threadIdx.x == 0) stade_lowered::count(a.st, stade_lowered::ST_ROW_BLOCK);")
+            out.append("    const int64_t _tr = _trip / _tn, _ts = (int64_t)gridDim.x / _tr;")
+            out.append("    const int64_t _row = (int64_t)blockIdx.x / _ts, _cs = (_tn + _ts - 1) / _ts;")
+            out.append("    const int64_t _t0 = ((int64_t)blockIdx.x % _ts) * _cs, _t1 = _t0 + _cs < _tn ? _t0 + _cs : _tn;")
+            out.append("    for (int64_t _t = _t0 + threadIdx.x; _t < _t1; _t += blockDim.x) {")
+            out.append("        const int64_t _k = _row * _tn + _t;")
+            out += lines
+            out.append("    }")
+            out.append(f"    __shared__ double _blk[16];")
+            for n in sites:
+                # thread 0 ran the chunk's first iteration (every chunk has one): its index is the row's
+                out.append(f"    stade_lowered::block_add(&a.A_{cname(n)}[{ix[n]}], {acc[n]}, "
+                           f"reinterpret_cast<{et(n)}*>(_blk), a.st);")
+        else:
+            out.append("    if (threadIdx.x == 0) stade_lowered::count(a.st, stade_lowered::ST_COL_BLOCK);")
+            out.append("    const int _tx = threadIdx.x & 31, _ty = threadIdx.x >> 5;")
+            out.append("    const int64_t _tr = _trip / _tn, _col = (int64_t)blockIdx.x * 32 + _tx;")
+            out.append(f"    const int64_t _r0 = (int64_t)blockIdx.y * {COLBLOCK_ROWS}, "
+                       f"_r1 = _r0 + {COLBLOCK_ROWS} < _tr ? _r0 + {COLBLOCK_ROWS} : _tr;")
+            out.append("    if (_col < _tn) {")
+            out.append("        for (int64_t _row = _r0 + _ty; _row < _r1; _row += 8) {")
+            out.append("            const int64_t _q = _row * _tn + _col;   // idx - 1")
+            out.append("            const int64_t _k = _st > 0 ? _q : _trip - 1 - _q;")
+            out += lines
+            out.append("        }")
+            out.append("    }")
+            for q, n in enumerate(sites):
+                out.append(f"    __shared__ {et(n)} _cb{q}[8][32];")
+                out.append(f"    _cb{q}[_ty][_tx] = {acc[n]};")
+            out.append("    __syncthreads();")
+            out.append("    if (_ty == 0 && _col < _tn) {")
+            for q, n in enumerate(sites):
+                terms = " + ".join(f"_cb{q}[{l}][_tx]" for l in range(8))
+                out.append(f"        const {et(n)} _v{q} = {terms};")
+                out.append(f"        if (_v{q} != ({et(n)})0) stade_lowered::atomic_add(&a.A_{cname(n)}[{ix[n]}], _v{q});")
+            out.append("    }")
+        return f"__global__ __launch_bounds__(256) void k{k}t(const Args a) {{\n" + "\n".join(out) + "\n}\n"
+
     # -- parallel loops -----------------------------------------------------------------------
     def parallel(self, op: ParOp) -> None:
         fl, pl = self.fl, op.pl
@@ -850,10 +929,21 @@ class FuncGen:
         locals_[v] = f"l_{cname(v)}"
 
         split = split_loops(pl, fl.T)
+        # the flat loops' row-block and column-block twins (launched when the host proves the
+        # range whole rows of at least TWIN_MIN_N, at least TWIN_MIN_ROWS of them)
+        int_args = {a for a in fl.f.args if a not in fl.arrays and fl.scalars.get(a) == "i"}
+        twin = None if split or os.environ.get("STADE_LOWER_TWINS", "1") == "0" else flat_twin(pl, int_args)
+        if twin is not None and not fl.host_ok(loop.rng, set(hl)):
+            twin = None
+        if twin is not None:
+            fl.twins.append((v, twin.kind, list(twin.sites)))
 
-        def body_lines(parallel: bool, lds: str | None, wave: bool = False) -> list[str]:
+        def body_lines(parallel: bool, lds: str | None, wave: bool = False, twin_sites: dict | None = None,
+                       twin_ix: dict | None = None) -> list[str]:
             ctx = Ctx(fl, dict(locals_), hl, acc={n: "atomic" for n in atomic}, serial_acc=not parallel,
-                      reductions=reds, lds=lds, hoist=hoist if parallel and not wave else None)
+                      reductions=reds, lds=lds,
+                      hoist=twin_sites if twin_sites is not None else (hoist if parallel and not wave else None))
+            ctx.site_ix = twin_ix or {}
             em = Emitter(fl, ctx)
             if wave:
                 em.split_loops = split
@@ -973,6 +1063,8 @@ class FuncGen:
                 sp.append(f"    {r} = stade_lowered::wave_sum({r});")
                 sp.append(f"    if ((threadIdx.x & 63) == 0 && {r} != 0) stade_lowered::atomic_add(&fr.v_{cname(n)}, {r});")
             self.kern.append(f"__global__ __launch_bounds__(256) void k{k}s(const Args a) {{\n" + "\n".join(sp) + "\n}\n")
+        if twin is not None:
+            self.kern.append(self.twin_kernel(k, twin, head, guards, body_lines, fl.ex(twin.N, ctx0)[0]))
         # host: grid from the trip count when the host can evaluate it
         if fl.host_ok(loop.rng, set(hl)):
             hctx = HostCtx(fl, self.hlv)
@@ -994,6 +1086,28 @@ class FuncGen:
                 self.hemit(f"if ({cond}) {{")
                 self.hind += 1
                 self.launch(f"k{k}s", f"(unsigned)std::min<int64_t>((_trip + 3) / 4, {MAX_BLOCKS})", "256", "0")
+                self.hind -= 1
+                self.hemit("} else")
+            if twin is not None:
+                hN = hctx.ex(twin.N)
+                self.hemit(f"const int64_t _tn = {hN}, _tr = _tn > 0 ? _trip / _tn : 0;")
+                if twin.kind == "row":
+                    # blocks a row: about ROWBLOCK_GRID blocks in all, each at least ROWBLOCK_CHUNK iterations
+                    self.hemit(f"const int64_t _ts = std::max<int64_t>(1, std::min<int64_t>((_tn + {ROWBLOCK_CHUNK - 1}) / "
+                               f"{ROWBLOCK_CHUNK}, ({ROWBLOCK_GRID} + _tr - 1) / "
+                               f"std::max<int64_t>(_tr, 1)));")
+                    cond = (f"_tn >= {TWIN_MIN_N} && _trip > 0 && _trip % _tn == 0 && _tr >= 1 && "
+                            f"_tr * _ts <= (int64_t)2147483647")
+                else:
+                    cond = (f"_tn >= {TWIN_MIN_N} && _trip > 0 && _trip % _tn == 0 && _tr >= {TWIN_MIN_ROWS}"
+                            f" && _tr <= (int64_t)65535 * {COLBLOCK_ROWS}")
+                self.hemit(f"if ({cond}) {{")
+                self.hind += 1
+                if twin.kind == "row":
+                    self.launch(f"k{k}t", "(unsigned)(_tr * _ts)", "256", "0")
+                else:
+                    self.launch(f"k{k}t", f"dim3((unsigned)((_tn + 31) / 32), (unsigned)((_tr + {COLBLOCK_ROWS - 1}) / {COLBLOCK_ROWS}))",
+                                "256", "0")
                 self.hind -= 1
                 self.hemit("} else")
             self.hemit("if (_trip > 0) {")
@@ -1366,7 +1480,7 @@ def generate(text: str, precision: str = "f64", arg_types: dict | None = None, i
             else:
                 sig.append((n, fl.scalars.get(n, "f"), 0))
         sigs[f.name] = dict(args=sig, plan=describe(fl.ops), reasons=list(fl.reasons), finish=fl.finish_rec,
-                            inbounds=inbounds)
+                            inbounds=inbounds, twins=list(fl.twins))
     return "\n".join(src), sigs
 
 

@@ -191,8 +191,9 @@ def _paths(case, low, fname):
     finally:
         low.set_stats(fname, None)
     c = st.cpu().tolist()
-    print(f"{case.label}: paths agg={c[0]} lane={c[1]} priv={c[2]} split={c[3]} block={c[4]}", flush=True)
-    return dict(agg=c[0], lane=c[1], priv=c[2], split=c[3], block=c[4])
+    print(f"{case.label}: paths agg={c[0]} lane={c[1]} priv={c[2]} split={c[3]} block={c[4]} row={c[5]} col={c[6]}",
+          flush=True)
+    return dict(agg=c[0], lane=c[1], priv=c[2], split=c[3], block=c[4], row=c[5], col=c[6])
 
 
 def _matvec_b(m, n):
@@ -256,3 +257,38 @@ def test_paths_narrow_output_form():
                       label="paths window1d_d narrow")
     p = _paths(case, low, "window1d_d")
     assert p["split"] > 0
+
+
+
+# ---- flat loops: the row-block and column-block twins ------------------------------------
+
+# (rows, columns): rows of 300, 256 and 513 columns (the last column block partial) take the
+# row twin, and with at least 64 rows the column twin; a row of 255 columns, a single element and
+# no rows take neither.  Few long rows split over several blocks each (10 x 100000: 49 chunks of
+# 2041 iterations; 3 x 40000: 20 chunks).
+FLAT_SIZES = [(100, 300), (64, 256), (2000, 513), (300, 5000), (63, 256), (64, 255), (1, 1), (0, 3),
+              (10, 100000), (3, 40000)]
+
+
+def _row_blocks(m, n):
+    """Blocks of the row twin: `_tr * _ts` of the lowered host code."""
+    ts = max(1, min(-(-n // 2048), -(-4096 // max(m, 1))))
+    return m * ts
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("mn", FLAT_SIZES)
+def test_lowered_flat_twins(mode, mn):
+    """The row-major flat mat-vec through the lowering against the oracle, with the path counters:
+    the forward loop's row sums run as the row-block twin when the range is whole rows of at least
+    256 (blocks of at least 2048 iterations of one row, about 4096 blocks), and the adjoint loop's
+    column sums as the column-block twin when there are also at least 64 rows (32-column,
+    128-row tiles)."""
+    m, n = mn
+    shapes = {k + s: v for k, v in dict(loss=1, a=m * n, x=n, y=m).items() for s in ("", "b", "d", "bd")}
+    case, low = _case(GENERIC / f"flatmv_{mode}.jl", "flatmv", mode, shapes, dict(i_m=m, i_n=n),
+                      label=f"flat twins flatmv_{mode} m={m} n={n}")
+    p = _paths(case, low, f"flatmv_{mode}")
+    assert p["row"] == (_row_blocks(m, n) if n >= 256 and m >= 1 else 0)
+    col_blocks = (-(-n // 32)) * (-(-m // 128)) if n >= 256 and m >= 64 else 0
+    assert p["col"] == (col_blocks if mode != "d" else 0)

@@ -175,6 +175,7 @@ def test_reference_kernels_compile(name, tmp_path):
 
 GENERIC_CASES = {
     "matvec_scatter": (dict(i_m=5, i_n=4), dict(loss=1, a=20, x=4, y=5), {}),
+    "flatmv": (dict(i_m=5, i_n=4), dict(loss=1, a=20, x=4, y=5), {}),
     "window1d": (dict(i_n=11, i_k=4), dict(loss=1, inp=11, w=4, out=8), {}),
     "binsum": (dict(i_n=13, i_b=4), dict(loss=1, v=13, c=4),
                dict(bins=np.array([1, 2, 3, 4, 1, 2, 3, 4, 2, 2, 3, 1, 4], dtype=np.int64))),
@@ -383,3 +384,29 @@ def test_fusion_only_where_iterations_stay_independent(body, fused):
     par = [p for p in sigs["f_b"]["plan"] if p.startswith("parallel")]
     assert (len(par) == 1) == fused, par
 
+
+
+@pytest.mark.parametrize("mode, twins", [
+    ("b", [("idx", "row", ["y"]), ("idx", "col", ["xb"])]),
+    ("d", [("idx", "row", ["y", "yd"])]),
+    ("hv", [("idx", "row", ["y", "yd"]), ("idx", "col", ["xb", "xbd"])]),
+])
+def test_flat_loops_get_their_twins(mode, twins):
+    """The row-major flat mat-vec: the forward loop's y[i] (a row sum) takes the row-block twin,
+    the adjoint loop's xb[j] (a column sum) the column-block twin (`cgen_rowblock_kernel`
+    /root/reference/src/STADE.jl:18187, `cgen_colblock_kernel` 18371)."""
+    from stade_hip.lower import hipgen
+    _, sigs = hipgen.generate((GENERIC / f"flatmv_{mode}.jl").read_text())
+    assert [tuple(t) for t in sigs[f"flatmv_{mode}"]["twins"]] == twins
+
+
+@pytest.mark.parametrize("change", [
+    "y[i] = y[i] + a[idx] * x[j]\n        y[j] = y[j] + 1.0",   # a second site at the column: mixed
+    "y[i] = y[i] + a[idx] * x[j]\n        a[idx] = y[i]",       # the site is read in the loop
+    "y[j + 1 - 1 + i - i] = y[j + 1 - 1 + i - i] + a[idx]",      # the index reads the column
+])
+def test_no_twin_unless_the_sites_agree(change):
+    from stade_hip.lower import hipgen
+    text = (GENERIC / "flatmv.jl").read_text().replace("y[i] = y[i] + a[idx] * x[j]", change)
+    _, sigs = hipgen.generate(text)
+    assert sigs["flatmv"]["twins"] == []
