@@ -1449,8 +1449,45 @@ def generate(text: str, precision: str = "f64", arg_types: dict | None = None, i
     funcs = parse(text)
     src = [PRELUDE]
     sigs = {}
-    # the element types of the stacks that the file's initstacks_* allocate (Int64 branch and
-    # tripcount stacks, Float64 value stacks) type the stack arguments of its functions
+    stack_kinds = _stack_kinds(funcs, precision)
+    for f in funcs:
+        if f.name.startswith("initstacks_"):
+            continue
+        fl = _func_lower(f, stack_kinds, precision, arg_types, inbounds, dead_scalars, merge_accum)
+        src.append(FuncGen(fl).source())
+        sig = []
+        for n in f.args:
+            if n in fl.arrays:
+                sig.append((n, "Ai" if fl.arrays[n] == "i" else "Af", fl.T.ndim.get(n, 1)))
+            else:
+                sig.append((n, fl.scalars.get(n, "f"), 0))
+        sigs[f.name] = dict(args=sig, plan=describe(fl.ops), reasons=list(fl.reasons), finish=fl.finish_rec,
+                            inbounds=inbounds, twins=list(fl.twins))
+    return "\n".join(src), sigs
+
+
+def _func_lower(f, stack_kinds, precision, arg_types, inbounds, dead_scalars, merge_accum):
+    kinds = {a: k for a, k in stack_kinds.items() if a in f.args}
+    kinds.update((arg_types or {}).get(f.name) or {})
+    return FuncLower(f, precision, kinds, stacks_allocated={a for a, k in stack_kinds.items() if k in ("Ai", "Af")},
+                     inbounds=inbounds, dead_scalars=dead_scalars, merge_accum=merge_accum)
+
+
+def lower_function(text: str, fname: str, precision: str = "f64", arg_types: dict | None = None,
+                   inbounds: bool = True, dead_scalars: bool = True, merge_accum: bool = True) -> FuncLower:
+    """The plan of one generated function of `text`, built as `generate` builds it (the same
+    stack types from the file's initstacks_*, the same passes): its transformed syntax tree is
+    `.f` and its operations `.ops`."""
+    from .syntax import parse
+    funcs = parse(text)
+    f = next(g for g in funcs if g.name == fname)
+    return _func_lower(f, _stack_kinds(funcs, precision), precision, arg_types, inbounds, dead_scalars, merge_accum)
+
+
+def _stack_kinds(funcs, precision) -> dict:
+    """The element types of the stacks that the file's initstacks_* allocate (Int64 branch and
+    tripcount stacks, Float64 value stacks), which type the stack arguments of its functions,
+    and the kinds of the other values they return."""
     stack_kinds = {}
     for f in funcs:
         if f.name.startswith("initstacks_"):
@@ -1465,23 +1502,7 @@ def generate(text: str, precision: str = "f64", arg_types: dict | None = None, i
                     for it in (s.value.items if isinstance(s.value, Tup) else (s.value,)):
                         if isinstance(it, Var) and it.name not in stack_kinds and it.name not in ti.arrays:
                             stack_kinds[it.name] = ti.scalars.get(it.name, "i")
-    for f in funcs:
-        if f.name.startswith("initstacks_"):
-            continue
-        kinds = {a: k for a, k in stack_kinds.items() if a in f.args}
-        kinds.update((arg_types or {}).get(f.name) or {})
-        fl = FuncLower(f, precision, kinds, stacks_allocated={a for a, k in stack_kinds.items() if k in ("Ai", "Af")},
-                       inbounds=inbounds, dead_scalars=dead_scalars, merge_accum=merge_accum)
-        src.append(FuncGen(fl).source())
-        sig = []
-        for n in f.args:
-            if n in fl.arrays:
-                sig.append((n, "Ai" if fl.arrays[n] == "i" else "Af", fl.T.ndim.get(n, 1)))
-            else:
-                sig.append((n, fl.scalars.get(n, "f"), 0))
-        sigs[f.name] = dict(args=sig, plan=describe(fl.ops), reasons=list(fl.reasons), finish=fl.finish_rec,
-                            inbounds=inbounds, twins=list(fl.twins))
-    return "\n".join(src), sigs
+    return stack_kinds
 
 
 def describe(ops, depth=0) -> list[str]:

@@ -190,8 +190,15 @@ def _jmin(a, b):
     return min(a, b)
 
 
+def _jfld(a, b):
+    """Julia's fld: the quotient rounded toward minus infinity."""
+    if _isf(a) or _isf(b):
+        return CTX.divide(dec(a), dec(b)).to_integral_value(rounding=decimal.ROUND_FLOOR)
+    return a // b
+
+
 _CALLS = {
-    "div": _jdiv, "mod": _jmod, "max": _jmax, "min": _jmin, "sign": _sign,
+    "div": _jdiv, "mod": _jmod, "fld": _jfld, "max": _jmax, "min": _jmin, "sign": _sign,
     "abs": lambda x: abs(x) if not _isf(x) else CTX.copy_abs(x),
     "sqrt": lambda x: CTX.sqrt(dec(x)), "exp": lambda x: CTX.exp(dec(x)),
     "log": lambda x: CTX.ln(dec(x)), "tanh": _tanh,
@@ -215,8 +222,49 @@ def _lin(arr: JArr, idx):
     return k
 
 
+class Tracer:
+    """Array accesses of the iterations of the loops a plan runs in parallel, one logical
+    thread per iteration: which element each iteration plainly wrote, plainly read or added to
+    atomically (`record`), set up by `run_func(..., tracer=...)`.
+
+    parallel: {id(For): {array: kind}} for the loops run one iteration per thread, with the
+    plan's kind of each array ('atomic' accumulations become atomic additions; everything else
+    is a plain read or write)."""
+
+    def __init__(self, parallel: dict):
+        self.parallel = parallel
+        self.thread = None
+        self.log: dict = {}
+        self.violations: list = []
+        self.loops_checked = 0
+
+    def note(self, name, k, slot):
+        if self.thread is None:
+            return
+        e = self.log.setdefault((name, k), (set(), set(), set()))
+        e[slot].add(self.thread)
+
+    def close(self, label):
+        """The checks of `ownership_shim.jl` (/root/reference/test/ownership_shim.jl:1-20) on
+        one loop's log: an element two threads write; one written by a thread and read or
+        added to by another; one read by a thread and added to by another."""
+        for (name, k), (w, r, a) in self.log.items():
+            if len(w) >= 2:
+                self.violations.append((label, name, k + 1, "multi_writer"))
+            elif w and ((r | a) - w):
+                self.violations.append((label, name, k + 1, "write_vs_other"))
+            elif r and a and (len(r | a) > 1):
+                self.violations.append((label, name, k + 1, "read_vs_atomic"))
+        self.log = {}
+        self.loops_checked += 1
+
+
 class _Compiler:
     """Syntax tree -> Python closures over an environment dict."""
+
+    def __init__(self, tracer: Tracer | None = None):
+        self.tracer = tracer
+        self.kinds: dict = {}     # the innermost parallel loop's array kinds, while compiling it
 
     def expr(self, e):
         if isinstance(e, S.Num):
@@ -234,11 +282,16 @@ class _Compiler:
         if isinstance(e, S.Ref):
             nm, ix = e.name, [self.expr(i) for i in e.idx]
 
+            tr = self.tracer
+
             def ref(env):
                 a = env[nm]
-                v = a.data[_lin(a, [f(env) for f in ix])]
+                k = _lin(a, [f(env) for f in ix])
+                v = a.data[k]
                 if v is None:
                     raise ValueError(f"read of an unset element of {nm}")
+                if tr is not None:
+                    tr.note(nm, k, 1)
                 return v
             return ref
         if isinstance(e, S.Un):
@@ -300,6 +353,29 @@ class _Compiler:
                     env[nm] = rhs(env)
                 return assign
             nm, ix = s.lhs.name, [self.expr(i) for i in s.lhs.idx]
+            tr = self.tracer
+            r = s.rhs
+            if (tr is not None and self.kinds.get(nm) == "atomic" and isinstance(r, S.Bin) and r.op in ("+", "-")
+                    and s.lhs in (r.a, r.b)):
+                # an accumulation the plan makes atomic: the element's read is part of the addition
+                other = self.expr(r.b if r.a == s.lhs else r.a)
+                neg = r.op == "-" and r.a == s.lhs
+                first = r.a == s.lhs
+
+                def atomic(env):
+                    a = env[nm]
+                    v = other(env)
+                    k = _lin(a, [f(env) for f in ix])
+                    old = a.data[k]
+                    if old is None:
+                        raise ValueError(f"read of an unset element of {nm}")
+                    if neg:
+                        nv = _sub(old, v)
+                    else:
+                        nv = _add(old, v) if first else _add(v, old)
+                    a.data[k] = nv if not a.isint else int(nv)
+                    tr.note(nm, k, 2)
+                return atomic
 
             def store(env):
                 a = env[nm]
@@ -311,19 +387,31 @@ class _Compiler:
                         v = int(v)
                 elif not _isf(v):
                     v = dec(v)
-                a.data[_lin(a, [f(env) for f in ix])] = v
+                k = _lin(a, [f(env) for f in ix])
+                a.data[k] = v
+                if tr is not None:
+                    tr.note(nm, k, 0)
             return store
         if isinstance(s, S.For):
             var, lo, hi = s.var, self.expr(s.rng.lo), self.expr(s.rng.hi)
             st = self.expr(s.rng.step) if s.rng.step is not None else (lambda env: 1)
+            tr = self.tracer
+            par = tr is not None and id(s) in tr.parallel
+            if par:
+                saved, self.kinds = self.kinds, tr.parallel[id(s)]
             body = self.block(s.body)
+            if par:
+                self.kinds = saved
+            label = f"for {var}"
 
             def loop(env):
                 a, step, b = lo(env), st(env), hi(env)
                 had, old = var in env, env.get(var)
                 rng = range(a, b + 1, step) if step > 0 else range(a, b - 1, step)
                 try:
-                    for v in rng:
+                    for it, v in enumerate(rng):
+                        if par:
+                            tr.thread = it
                         env[var] = v
                         try:
                             body(env)
@@ -336,6 +424,9 @@ class _Compiler:
                         env[var] = old
                     else:
                         env.pop(var, None)
+                    if par:
+                        tr.thread = None
+                        tr.close(label)
             return loop
         if isinstance(s, S.While):
             cond, body = self.expr(s.cond), self.block(s.body)
@@ -400,13 +491,14 @@ def run(text: str, fname: str, args):
     return run_func(funcs[fname], args)
 
 
-def run_func(f, args):
-    """`run` on a parsed function (a syntax tree, transformed or not)."""
+def run_func(f, args, tracer: Tracer | None = None):
+    """`run` on a parsed function (a syntax tree, transformed or not); with a tracer, the
+    accesses of its parallel loops' iterations are recorded and checked (`Tracer`)."""
     fname = f.name
     if len(args) != len(f.args):
         raise TypeError(f"{fname} takes {len(f.args)} arguments, got {len(args)}")
     env = {a: _to_j(v) for a, v in zip(f.args, args)}
-    body = _Compiler().block(f.body)
+    body = _Compiler(tracer).block(f.body)
     ret = None
     try:
         body(env)
