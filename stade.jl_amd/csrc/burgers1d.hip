@@ -44,16 +44,31 @@ constexpr int kInitBlockCells = NT * 8;  // cells per block of the backward init
 #define STADE_BURG_FS 4096
 #endif
 #ifndef STADE_BURG_FS_NOTAPE
-#define STADE_BURG_FS_NOTAPE 1024
+#define STADE_BURG_FS_NOTAPE 960
 #endif
-// forward chunk kernel (register form): threads and owned cells per block.  With a tape to
-// write (adjoint, HVP, checkpoints) 512 / 4096: against the LDS form it replaced (1024 /
-// 4096), the HVP 3-6 % faster and the adjoint 0-2 %; 1024 / 4096, 256 / 4096 and 512 / 2048
-// measured between the two.  The tangent, which writes no tape and is bound by its fp64
-// arithmetic, 512 / 1024: 20 % faster than the LDS form (512 / 2048 17 %, 1024 / 4096 13 %).
-constexpr int BNT = STADE_BURG_FT;
-constexpr int FWD_S = STADE_BURG_FS;
-constexpr int FWD_S_NOTAPE = STADE_BURG_FS_NOTAPE;
+#ifndef STADE_BURG_FT_NOTAPE
+#define STADE_BURG_FT_NOTAPE 256
+#endif
+#ifndef STADE_BURG_FC
+#define STADE_BURG_FC 1
+#endif
+#ifndef STADE_BURG_FC_NOTAPE
+#define STADE_BURG_FC_NOTAPE 4
+#endif
+// forward chunk kernel (register form): threads, owned cells and cells per lane of a block.
+// With a tape to write (adjoint, HVP, checkpoints) 512 / 4096 / 1: against the LDS form it
+// replaced (1024 / 4096), the HVP 3-6 % faster and the adjoint 0-2 %; 1024 / 4096, 256 / 4096
+// and 512 / 2048 measured between the two; two cells a lane (512 / 4032 / 2) halved both
+// rates (its tape stores cover every other element).  The tangent, which writes no tape and is
+// bound by its instruction issue (fp64 arithmetic and the neighbour shifts), 256 / 960 / 4:
+// the region of 1024 cells is one slot of four cells a lane, every wave does the same work,
+// and a lane shifts two values an array a step for four cells; 18 % faster than 512 / 1024 /
+// 1 (one cell a lane, wave 0 computing a third slot the others skip).  Measured at 2^20 cells:
+// 512 / 960 / 2 +9 %, 256 / 448 / 2 +11 %, 128 / 448 / 4 +7 %, 64 / 448 / 8 +7 %, 512 / 1984 /
+// 4 +5 %, 64 / 960 / 16 (137 registers) -15 %.
+constexpr int BNT = STADE_BURG_FT, BNT_NOTAPE = STADE_BURG_FT_NOTAPE;
+constexpr int FWD_S = STADE_BURG_FS, FWD_C = STADE_BURG_FC;
+constexpr int FWD_S_NOTAPE = STADE_BURG_FS_NOTAPE, FWD_C_NOTAPE = STADE_BURG_FC_NOTAPE;
 #ifndef STADE_BURG_BT
 #define STADE_BURG_BT 512
 #endif
@@ -94,33 +109,42 @@ __device__ __forceinline__ double step_ud(double um, double uc, double up, doubl
 
 // ---------------------------------------------------------------------------------------
 // forward: `nk` steps starting at 0-based step t0, from src (+ srcd) to dst (+ dstd), with the
-// state in registers.  Thread t holds positions e = t + i * T (slot i) of the extended region [x0 - KMAX, x0 + S + KMAX);
-// the neighbours e -/+ 1 are the adjacent lanes (DPP wavefront shifts), and a wave's two end
-// lanes take theirs from the end lanes the waves publish in a small LDS array, double
-// buffered by step: one barrier a step and no LDS traffic for the interior.  Any nk <= KMAX
-// (the owned cells stay valid for KMAX steps; the region's ends go stale one cell a step).
+// state in registers.  Thread t holds the C consecutive positions e = C (t + i T) + j, j < C
+// (slot i) of the extended region [x0 - KMAX, x0 + S + KMAX).  A position's neighbours are the
+// lane's own registers except at the lane's two ends: e - 1 of its first position and e + 1 of
+// its last come from the adjacent lanes (DPP wavefront shifts), and a wave's two end lanes take
+// theirs from the end values the waves publish in a small LDS array, double buffered by step:
+// one barrier a step and no LDS traffic for the interior.  C cells a lane make C - 1 of every C
+// neighbour pairs register reads: two shifts per array a step for C cells instead of 2 C.
+// Any nk <= KMAX (the owned cells stay valid for KMAX steps; the region's ends go stale one
+// cell a step, and the lanes past its end, in a wave that starts inside it, hold copies of the
+// last position that nothing stores).
 // ---------------------------------------------------------------------------------------
-template <bool TAN, int S, int T>
+template <bool TAN, int S, int T, int C>
 __global__ __launch_bounds__(T) void fwd_reg_kernel(const double* __restrict__ src, const double* __restrict__ srcd,
                                                     double* __restrict__ dst, double* __restrict__ dstd,
                                                     double* __restrict__ tape, double* __restrict__ taped, int n, int64_t t0,
                                                     int nk, Coef c, int64_t row0, int every) {
     constexpr int L = S + 2 * KMAX;
-    constexpr int M = (L + T - 1) / T, NWV = T / 64;
+    constexpr int SP = C * T;  // positions per slot
+    constexpr int M = (L + SP - 1) / SP, NWV = T / 64;
     constexpr int NA = TAN ? 2 : 1;  // exchanged arrays: u (+ ud)
-    static_assert(L - (M - 1) * T <= 64, "the last slot belongs to wave 0 alone");
+    static_assert(S % 64 == 0 && T % 64 == 0, "whole waves");
     __shared__ double edge[2][NA][M][NWV][2];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int x0 = blockIdx.x * S;
     const int own = min(S, n - x0);
-    int xc[M], eo[M];
-    bool owned[M];
+    int xc[M][C], eo[M];
+    bool owned[M][C];
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        const int e = threadIdx.x + i * T;
-        xc[i] = wrapn(x0 - KMAX + min(e, L - 1), n);
-        owned[i] = e >= KMAX && e < KMAX + own;
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const int e = C * (threadIdx.x + i * T) + j;
+            xc[i][j] = wrapn(x0 - KMAX + min(e, L - 1), n);
+            owned[i][j] = e >= KMAX && e < KMAX + own;
+        }
         int si, sv, ss;
         if (lane == 0) {
             ss = 1;
@@ -133,20 +157,26 @@ __global__ __launch_bounds__(T) void fwd_reg_kernel(const double* __restrict__ s
         }
         eo[i] = (si * NWV + sv) * 2 + ss;
     }
+    // a wave whose first position of slot i lies past the region computes nothing there (uniform)
+    auto past = [&](int i) { return C * (i * T + wave * 64) >= L; };
     auto edge_at = [&](int buf, int a, int i) { return (&edge[buf][a][0][0][0])[eo[i]]; };
-    double u[M], ud[M];
+    double u[M][C], ud[M][C];
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        u[i] = src[xc[i]];
-        ud[i] = TAN ? srcd[xc[i]] : 0.0;
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            u[i][j] = src[xc[i][j]];
+            ud[i][j] = TAN ? srcd[xc[i][j]] : 0.0;
+        }
     }
+    // lane 0 publishes its first position (the west wave's east neighbour), lane 63 its last
     auto publish = [&](int buf) {
         if (lane == 0 || lane == 63) {
             const int side = lane == 63;
 #pragma unroll
             for (int i = 0; i < M; ++i) {
-                edge[buf][0][i][wave][side] = u[i];
-                if constexpr (TAN) edge[buf][1][i][wave][side] = ud[i];
+                edge[buf][0][i][wave][side] = side ? u[i][C - 1] : u[i][0];
+                if constexpr (TAN) edge[buf][1][i][wave][side] = side ? ud[i][C - 1] : ud[i][0];
             }
         }
     };
@@ -162,41 +192,63 @@ __global__ __launch_bounds__(T) void fwd_reg_kernel(const double* __restrict__ s
             const size_t row = (size_t)(tr / every) * (size_t)n + (size_t)(x0 - KMAX);
 #pragma unroll
             for (int i = 0; i < M; ++i) {
-                if (owned[i]) {
-                    const size_t g = row + (size_t)(threadIdx.x + i * T);
-                    __builtin_nontemporal_store(u[i], &tape[g]);
-                    if (TAN && taped) __builtin_nontemporal_store(ud[i], &taped[g]);
+#pragma unroll
+                for (int j = 0; j < C; ++j) {
+                    if (owned[i][j]) {
+                        const size_t g = row + (size_t)(C * (threadIdx.x + i * T) + j);
+                        __builtin_nontemporal_store(u[i][j], &tape[g]);
+                        if (TAN && taped) __builtin_nontemporal_store(ud[i][j], &taped[g]);
+                    }
                 }
             }
         }
-        double un[M], udn[M];
+        double un[M][C], udn[M][C];
 #pragma unroll
         for (int i = 0; i < M; ++i) {
-            un[i] = u[i];
-            udn[i] = ud[i];
-            if (i == M - 1 && wave != 0) continue;  // past the extended region (uniform)
-            const double uc = u[i], eu = edge_at(buf, 0, i);
-            const double um = from_west(uc, eu), up = from_east(uc, eu);
-            if constexpr (TAN) {
-                const double dc = ud[i], ed = edge_at(buf, 1, i);
-                udn[i] = step_ud(um, uc, up, from_west(dc, ed), dc, from_east(dc, ed), c);
+#pragma unroll
+            for (int j = 0; j < C; ++j) {
+                un[i][j] = u[i][j];
+                udn[i][j] = ud[i][j];
             }
-            un[i] = step_u(um, uc, up, c);
+            if (past(i)) continue;
+            const double eu = edge_at(buf, 0, i);
+            const double uw = from_west(u[i][C - 1], eu), ue = from_east(u[i][0], eu);
+            double dw = 0.0, de = 0.0;
+            if constexpr (TAN) {
+                const double ed = edge_at(buf, 1, i);
+                dw = from_west(ud[i][C - 1], ed);
+                de = from_east(ud[i][0], ed);
+            }
+#pragma unroll
+            for (int j = 0; j < C; ++j) {
+                const double um = j > 0 ? u[i][j - 1] : uw, up = j < C - 1 ? u[i][j + 1] : ue;
+                if constexpr (TAN) {
+                    const double dm = j > 0 ? ud[i][j - 1] : dw, dp = j < C - 1 ? ud[i][j + 1] : de;
+                    udn[i][j] = step_ud(um, u[i][j], up, dm, ud[i][j], dp, c);
+                }
+                un[i][j] = step_u(um, u[i][j], up, c);
+            }
         }
 #pragma unroll
         for (int i = 0; i < M; ++i) {
-            u[i] = un[i];
-            ud[i] = udn[i];
+#pragma unroll
+            for (int j = 0; j < C; ++j) {
+                u[i][j] = un[i][j];
+                ud[i][j] = udn[i][j];
+            }
         }
         publish(buf ^ 1);
         __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        if (owned[i]) {
-            const int x = x0 + threadIdx.x + i * T - KMAX;
-            dst[x] = u[i];
-            if (TAN) dstd[x] = ud[i];
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            if (owned[i][j]) {
+                const int x = x0 + C * (threadIdx.x + i * T) + j - KMAX;
+                dst[x] = u[i][j];
+                if (TAN) dstd[x] = ud[i][j];
+            }
         }
     }
 }
@@ -656,11 +708,11 @@ int32_t forward(const double* src, const double* srcd, double* fin, double* find
         double* dd = last ? find : (flip ? Qd : Pd);
         if (notape) {
             STADE_TIMED(TAN ? "burgers1d_fwd_tan" : "burgers1d_fwd", stream,
-                        fwd_reg_kernel<TAN, FWD_S_NOTAPE, BNT><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c,
+                        fwd_reg_kernel<TAN, FWD_S_NOTAPE, BNT_NOTAPE, FWD_C_NOTAPE><<<nb, BNT_NOTAPE, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c,
                                                                                         row0, every));
         } else {
             STADE_TIMED(TAN ? "burgers1d_fwd_tan" : "burgers1d_fwd", stream,
-                        fwd_reg_kernel<TAN, FWD_S, BNT><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c, row0,
+                        fwd_reg_kernel<TAN, FWD_S, BNT, FWD_C><<<nb, BNT, 0, stream>>>(cs, csd, d, dd, tape, taped, n, t0, nk, c, row0,
                                                                                  every));
         }
         STADE_LAUNCHED("burgers1d fwd_reg_kernel");
