@@ -1,0 +1,509 @@
+"""Contractions of the generated code onto the matrix cores.
+
+A dense layer's generated code sums products in a sequential loop nested in a parallel flat
+loop.  The forward form (one iteration per output element (i, j), a sum over k):
+
+    for idx = 1:R * N                       # i = div(idx - 1, N) + 1, j = mod(idx - 1, N) + 1
+        s = b[j]
+        for k = 1:K
+            s = s + w[(k - 1) * N + j] * x[(i - 1) * K + k]
+        end
+        h[...] = tanh(s)
+    end
+
+and the adjoint form, whose inner loop scatters products of a per-iteration scalar into two
+arrays, each summed over the other coordinate:
+
+    for idx = R * N:-1:1
+        ... sb = ... ;
+        for k = K:-1:1
+            wb[(k - 1) * N + j] = wb[(k - 1) * N + j] + x[(i - 1) * K + k] * sb
+            xb[(i - 1) * K + k] = xb[(i - 1) * K + k] + w[(k - 1) * N + j] * sb
+        end
+    end
+
+On the vector units these run one thread per (i, j) with K-long dot products or K atomics
+per thread.  Here the inner loop becomes matrix products on the fp32 matrix cores
+(csrc/gemm_f32.hpp) around a loop that keeps the rest of the body:
+- forward: a product T(j, i) = sum_k A(j, k) B(k, i) of the two factors, run before the
+  loop, and `s = s + T[j, i]` in place of the inner loop (one per accumulated scalar; a
+  term list `A1 B1 + A2 B2` is a two-segment product);
+- adjoint: the loop stores each scalar the products scale into a scratch array V[j, i] in
+  place of the inner loop, and a product per accumulated array after the loop adds
+  sum over the other coordinate of V times the factor into it (`C(j, k) += sum_i V(j, i)
+  x(k, i)`).
+
+The reference's AMDGPU path has no such rewrite: its `stade_gpu` runs these loops as
+written (`cgen_body` /root/reference/src/STADE.jl:11937); the hand-written configs
+(csrc/mlp2_ce.hip, conv3x3.hip) are this build's products of the same loops.  The sums are
+reassociated (a product sums K terms in its own order, and s adds the whole sum to its
+initial value), so results match the loops to fp32 rounding, not bit for bit: fp32 only (the
+configs' fp32 tolerance), and only with unchecked accesses (a product reads exactly the
+elements the loops read, without the per-access range checks).
+
+Conditions, all checked, else the loop stays as it is:
+- the loop is at the function's top level, a flat loop over 1:R*N (either direction) with
+  i = div(idx - 1, N) + 1 and j = mod(idx - 1, N) + 1 and R, N expressions of Int arguments;
+- the inner loop runs k over all of 1:K (either direction), K an expression of Int
+  arguments, and holds only Int index temporaries, float temporaries that name one element,
+  and accumulations (all scalar `s = s + E`, or all array `C[e] = C[e] + E`);
+- each term of E is a product of two elements (forward) or of an element and a scalar the
+  inner loop does not assign (adjoint), every index affine in k and in one of i, j with
+  coefficients of Int arguments and a unit stride in k or in that coordinate;
+- forward: no array a product reads is written anywhere in the loop; adjoint: an accumulated
+  array is touched by nothing else in the loop, and no factor array is written in it;
+- the inner loop's temporaries are read nowhere else.
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+
+from .analysis import NotAffine, Types, _derived, _linear_index, _reads_of, linear_in, to_poly
+from .syntax import Alloc, Assign, Bin, For, Func, Gemm, GemmSeg, Num, Ref, Var, stmt_exprs, walk_expr, walk_stmts
+
+ONE = {(): 1}
+
+
+class _No(Exception):
+    pass
+
+
+def _num(v: int) -> Num:
+    return Num(str(v), True)
+
+
+def poly_expr(p: dict):
+    """The Int expression of a polynomial over Int-argument atoms."""
+    terms = []
+    for m, c in sorted(p.items()):
+        if c == 0:
+            continue
+        e = None
+        for a in m:
+            if a[0] != "v":
+                raise _No("a coefficient that is not a product of Int arguments")
+            e = Var(a[1]) if e is None else Bin("*", e, Var(a[1]))
+        if e is None:
+            e = _num(c)
+        elif c != 1:
+            e = Bin("*", _num(c), e)
+        terms.append(e)
+    if not terms:
+        return _num(0)
+    out = terms[0]
+    for t in terms[1:]:
+        out = Bin("+", out, t)
+    return out
+
+
+def _host_poly(p: dict, host_ints: set) -> bool:
+    return all(a[0] == "v" and a[1] in host_ints for m in p for a in m)
+
+
+@dataclass
+class Affine:
+    """A reference's 0-based element offset as off + sk (k - 1) + sc (c - 1), c the one outer
+    coordinate it depends on (None: neither)."""
+    array: str
+    off: dict
+    sk: dict
+    coord: str | None
+    sc: dict
+
+
+@dataclass
+class Flat:
+    var: str
+    iv: str
+    jv: str
+    R: object
+    N: object
+
+
+def flat_of(loop: For, host_ints: set) -> Flat | None:
+    """The flat decomposition of `for idx = 1:R*N` (or `R*N:-1:1`) with i = div(idx - 1, N) + 1
+    and j = mod(idx - 1, N) + 1 assigned once each at the top of the body."""
+    r = loop.rng
+    step = 1 if r.step is None else (int(r.step.text) if isinstance(r.step, Num) and r.step.is_int else 0)
+    one = lambda e: isinstance(e, Num) and e.is_int and int(e.text) == 1
+    if step == 1 and one(r.lo):
+        trip = r.hi
+    elif step == -1 and one(r.hi):
+        trip = r.lo
+    else:
+        return None
+    v = loop.var
+    count = {}
+    for s in loop.body:
+        if isinstance(s, Assign) and isinstance(s.lhs, Var):
+            count[s.lhs.name] = count.get(s.lhs.name, 0) + 1
+    vm1 = {s.lhs.name for s in loop.body if isinstance(s, Assign) and isinstance(s.lhs, Var)
+           and isinstance(s.rhs, Bin) and s.rhs.op == "-" and s.rhs.a == Var(v) and one(s.rhs.b)
+           and count[s.lhs.name] == 1}
+    der = [d for d in (_derived(s, v, vm1) for s in loop.body) if d is not None]
+    divs = [d for d in der if d[1] == "div"]
+    mods = [d for d in der if d[1] == "mod"]
+    if len(divs) != 1 or len(mods) != 1 or divs[0][2] != mods[0][2]:
+        return None
+    iv, jv, N = divs[0][0], mods[0][0], divs[0][2]
+    if count.get(iv) != 1 or count.get(jv) != 1:
+        return None
+    if not (isinstance(trip, Bin) and trip.op == "*"):
+        return None
+    if trip.b == N:
+        R = trip.a
+    elif trip.a == N:
+        R = trip.b
+    else:
+        return None
+    names = lambda e: {x.name for x in walk_expr(e) if isinstance(x, Var)}
+    if not (names(N) | names(R)) <= host_ints:
+        return None
+    return Flat(v, iv, jv, R, N)
+
+
+class _Rewriter:
+    def __init__(self, f: Func, T: Types, host_ints: set, is_parallel):
+        self.f = f
+        self.T = T
+        self.host_ints = host_ints
+        self.is_parallel = is_parallel
+        self.n = 0
+        self.rec = {"forward": 0, "adjoint": 0, "gemms": 0, "loops": []}
+
+    def fresh(self, stem: str) -> str:
+        self.n += 1
+        return f"__gemm_{stem}{self.n}"
+
+    # -- index analysis ------------------------------------------------------------------------
+    def affine(self, ref: Ref, env: dict, k: str, fl: Flat) -> Affine:
+        try:
+            p = to_poly(_linear_index(ref, self.T), env, self.T)
+        except NotAffine:
+            raise _No(f"{ref.name}: index not affine")
+        lk = linear_in(p, k)
+        if lk is None:
+            raise _No(f"{ref.name}: not linear in {k}")
+        sk, rest = lk
+        li = linear_in(rest, fl.iv)
+        lj = linear_in(li[1] if li else {}, fl.jv) if li else None
+        if li is None or lj is None:
+            raise _No(f"{ref.name}: not linear in the coordinates")
+        si, (sj, off) = li[0], lj
+        for q in (sk, si, sj, off):
+            if not _host_poly(q, self.host_ints):
+                raise _No(f"{ref.name}: a coefficient the host cannot evaluate")
+        if si and sj:
+            raise _No(f"{ref.name}: depends on both coordinates")
+        coord, sc = (fl.iv, si) if si else ((fl.jv, sj) if sj else (None, {}))
+        # 0-based offset at k = 1, c = 1: (p - 1) = off + sk + sc - 1 + sk (k - 1) + sc (c - 1)
+        off0 = dict(off)
+        for q in (sk, sc):
+            for m, c in q.items():
+                off0[m] = off0.get(m, 0) + c
+        off0[()] = off0.get((), 0) - 1
+        off0 = {m: c for m, c in off0.items() if c}
+        return Affine(ref.name, off0, sk, coord, sc)
+
+    # -- the inner loop ---------------------------------------------------------------------------
+    def inner_parts(self, inner: For, outer_env: dict, fl: Flat):
+        k = inner.var
+        r = inner.rng
+        one = lambda e: isinstance(e, Num) and e.is_int and int(e.text) == 1
+        step = 1 if r.step is None else (int(r.step.text) if isinstance(r.step, Num) and r.step.is_int else 0)
+        if step == 1 and one(r.lo):
+            K = r.hi
+        elif step == -1 and one(r.hi):
+            K = r.lo
+        else:
+            raise _No("inner range not 1:K")
+        if not {x.name for x in walk_expr(K) if isinstance(x, Var)} <= self.host_ints:
+            raise _No("inner bound not host-evaluable")
+        env = dict(outer_env)
+        alias = {}
+        temps = set()
+        accs = []
+        assigned = set()
+        for s in inner.body:
+            if not isinstance(s, Assign):
+                raise _No("inner loop holds a non-assignment")
+            if isinstance(s.lhs, Var):
+                nm = s.lhs.name
+                if nm in assigned:
+                    raise _No(f"{nm} assigned twice in the inner loop")
+                r_ = s.rhs
+                if isinstance(r_, Bin) and r_.op == "+" and Var(nm) in (r_.a, r_.b):
+                    other = r_.b if r_.a == Var(nm) else r_.a
+                    if nm in _reads_of(other):
+                        raise _No("accumulation reads itself twice")
+                    accs.append(("s", Var(nm), other))
+                    assigned.add(nm)
+                    continue
+                if self.T.scalars.get(nm) == "i":
+                    env[nm] = r_
+                elif isinstance(r_, Ref) and self.T.arrays.get(r_.name) == "f":
+                    alias[nm] = r_
+                else:
+                    raise _No(f"inner temporary {nm} is not an index or an element")
+                temps.add(nm)
+                assigned.add(nm)
+                continue
+            ref = s.lhs
+            r_ = s.rhs
+            if not (isinstance(r_, Bin) and r_.op == "+" and ref in (r_.a, r_.b)):
+                raise _No(f"store to {ref.name} is not an accumulation")
+            other = r_.b if r_.a == ref else r_.a
+            if any(isinstance(x, Ref) and x.name == ref.name for x in walk_expr(other)):
+                raise _No("accumulation reads its own array")
+            accs.append(("c", ref, other))
+        if not accs or len({a[0] for a in accs}) != 1:
+            raise _No("no accumulation, or scalar and array accumulations mixed")
+        acc_names = {a[1].name for a in accs if a[0] == "s"}
+        for _, _, e in accs:
+            if _reads_of(e) & acc_names:
+                raise _No("a product reads an accumulated scalar")
+        return k, K, env, alias, temps, accs
+
+    def terms(self, e) -> list:
+        if isinstance(e, Bin) and e.op == "+":
+            return self.terms(e.a) + self.terms(e.b)
+        if isinstance(e, Bin) and e.op == "*":
+            return [(e.a, e.b)]
+        raise _No("a term that is not a product")
+
+    def resolve(self, x, alias):
+        if isinstance(x, Var) and x.name in alias:
+            return alias[x.name]
+        return x
+
+    # -- products ------------------------------------------------------------------------------------
+    @staticmethod
+    def layout(a: Affine):
+        """(km, ld) of an element factor as a gemm operand over (its coordinate, the summed
+        index): km when the summed index is contiguous (X[s + c ld], ld the coordinate's
+        stride), else the coordinate is (X[c + s ld], ld the summed index's stride).  The
+        same flag means A_KM for the gemm's A operand (rows the coordinate) and B_KM for its
+        B operand (columns the coordinate)."""
+        if a.sk == ONE:
+            return True, a.sc
+        if a.sc == ONE:
+            return False, a.sk
+        raise _No(f"{a.array}: no unit stride")
+
+    def seg(self, A: Affine, B: Affine, K) -> GemmSeg:
+        a_km, lda = self.layout(A)
+        b_km, ldb = self.layout(B)
+        return GemmSeg(A.array, poly_expr(A.off), a_km, poly_expr(lda), B.array, poly_expr(B.off), b_km,
+                       poly_expr(ldb), K)
+
+    def written_in(self, body) -> set:
+        out = set()
+        for s in walk_stmts(body):
+            if isinstance(s, Assign) and isinstance(s.lhs, Ref):
+                out.add(s.lhs.name)
+        return out
+
+    def refs_in(self, stmts) -> set:
+        out = set()
+        for s in walk_stmts(stmts):
+            for e in stmt_exprs(s):
+                out |= {x.name for x in walk_expr(e) if isinstance(x, Ref)}
+            if isinstance(s, Assign) and isinstance(s.lhs, Ref):
+                out.add(s.lhs.name)
+        return out
+
+    def reads_elsewhere(self, names: set, inner: For) -> bool:
+        """Any of `names` read or assigned anywhere in the function outside `inner`."""
+        inside = {id(s) for s in walk_stmts([inner])}
+        for s in walk_stmts(self.f.body):
+            if id(s) in inside:
+                continue
+            for e in stmt_exprs(s):
+                if _reads_of(e) & names:
+                    return True
+            if isinstance(s, Assign) and isinstance(s.lhs, Var) and s.lhs.name in names:
+                return True
+        return False
+
+    def rewrite_loop(self, loop: For):
+        """(statements before, the new loop, statements after) or raises _No."""
+        fl = flat_of(loop, self.host_ints)
+        if fl is None:
+            raise _No("not a flat loop")
+        # outer Int temporaries (assigned once, not the coordinates) substitute into indices
+        count = {}
+        for s in walk_stmts(loop.body):
+            if isinstance(s, Assign) and isinstance(s.lhs, Var):
+                count[s.lhs.name] = count.get(s.lhs.name, 0) + 1
+        outer_env = {s.lhs.name: s.rhs for s in loop.body if isinstance(s, Assign) and isinstance(s.lhs, Var)
+                     and self.T.scalars.get(s.lhs.name) == "i" and count[s.lhs.name] == 1
+                     and s.lhs.name not in (fl.iv, fl.jv)}
+        inners = [s for s in loop.body if isinstance(s, For)]
+        if not inners:
+            raise _No("no inner loop")
+        written = self.written_in(loop.body)
+        before, after, new_body = [], [], []
+        done = 0
+        lin = Bin("+", Var(fl.jv), Bin("*", Bin("-", Var(fl.iv), _num(1)), fl.N))   # 1-based (j, i), j fastest
+        size = Bin("*", fl.R, fl.N)
+        for s in loop.body:
+            if not isinstance(s, For):
+                new_body.append(s)
+                continue
+            try:
+                k, K, env, alias, temps, accs = self.inner_parts(s, outer_env, fl)
+                # (k itself is the loop's own: a Julia loop variable is a new local of the loop)
+                if self.reads_elsewhere(temps, s):
+                    raise _No("an inner temporary is read outside the inner loop")
+                if accs[0][0] == "s":
+                    pre, repl = self.forward(s, k, K, env, alias, accs, fl, written, lin, size)
+                    before += pre
+                    new_body += repl
+                    self.rec["forward"] += 1
+                else:
+                    repl, post = self.adjoint(loop, s, k, K, env, alias, accs, fl, written, lin, size)
+                    new_body += repl
+                    after += post
+                    self.rec["adjoint"] += 1
+                done += 1
+            except _No:
+                new_body.append(s)
+        if not done:
+            raise _No("no inner loop is a contraction")
+        return before, For(loop.var, loop.rng, new_body), after
+
+    def forward(self, inner, k, K, env, alias, accs, fl, written, lin, size):
+        pre, repl = [], []
+        for _, acc, e in accs:
+            segs = []
+            for a, b in self.terms(e):
+                a, b = self.resolve(a, alias), self.resolve(b, alias)
+                if not (isinstance(a, Ref) and isinstance(b, Ref)):
+                    raise _No("a forward term that is not a product of two elements")
+                fa, fb = self.affine(a, env, k, fl), self.affine(b, env, k, fl)
+                if {fa.coord, fb.coord} != {fl.iv, fl.jv}:
+                    raise _No("the factors do not split the coordinates")
+                if fa.array in written or fb.array in written:
+                    raise _No("a factor is written in the loop")
+                A, B = (fa, fb) if fa.coord == fl.jv else (fb, fa)   # T(j, i): rows j
+                segs.append(self.seg(A, B, K))
+            tname = self.fresh("T")
+            pre.append(Assign(Var(tname), Alloc("Float32", size)))
+            pre += self.gemms(tname, _num(0), _num(1), fl.N, False, fl.N, fl.R, segs)
+            repl.append(Assign(acc, Bin("+", acc, Ref(tname, (lin,)))))
+        return pre, repl
+
+    def adjoint(self, loop, inner, k, K, env, alias, accs, fl, written, lin, size):
+        inner_ids = {id(s) for s in walk_stmts([inner])}
+        rest = [s for s in loop.body if id(s) not in inner_ids]
+        touched_elsewhere = self.refs_in(rest)
+        vnames = {}
+        repl, post = [], []
+        for _, acc, e in accs:
+            c = self.affine(acc, env, k, fl)
+            if c.coord is None or not c.sk:
+                raise _No("an accumulated array that does not run over k and one coordinate")
+            if c.array in touched_elsewhere:
+                raise _No(f"{c.array} is touched elsewhere in the loop")
+            other = fl.iv if c.coord == fl.jv else fl.jv       # summed over
+            srange = fl.R if other == fl.iv else fl.N
+            # output rows: C's coordinate when its stride there is 1, else k when that is 1
+            rows_coord = c.sc == ONE or c.sk != ONE
+            segs = []
+            for a, b in self.terms(e):
+                a, b = self.resolve(a, alias), self.resolve(b, alias)
+                if isinstance(a, Var) and isinstance(b, Ref):
+                    a, b = b, a
+                if not (isinstance(a, Ref) and isinstance(b, Var)):
+                    raise _No("an adjoint term that is not an element times a scalar")
+                if b.name == k or b.name in alias or self.T.scalars.get(b.name) != "f":
+                    raise _No("the scalar factor varies in the inner loop or is not a float")
+                fa = self.affine(a, env, k, fl)
+                if fa.coord != other or not fa.sk:
+                    raise _No("the element factor does not run over k and the summed coordinate")
+                if fa.array in written:
+                    raise _No("a factor is written in the loop")
+                vn = vnames.setdefault(b.name, self.fresh("V"))
+                # the factor over (summed index s = `other`, k): km when s is contiguous
+                f_km, f_ld = (True, fa.sk) if fa.sc == ONE else ((False, fa.sc) if fa.sk == ONE else (None, None))
+                if f_km is None:
+                    raise _No(f"{fa.array}: no unit stride")
+                if rows_coord:
+                    # A(m = C's coordinate, s) = V: V(j, i) = V[(j - 1) + (i - 1) N], so s
+                    # contiguous when the coordinate is i;  B(s, n = k) = the factor
+                    segs.append(GemmSeg(vn, _num(0), c.coord == fl.iv, fl.N, fa.array, poly_expr(fa.off), f_km,
+                                        poly_expr(f_ld), srange))
+                else:
+                    # A(m = k, s) = the factor;  B(s, n = C's coordinate) = V, s contiguous
+                    # when s is j
+                    segs.append(GemmSeg(fa.array, poly_expr(fa.off), f_km, poly_expr(f_ld), vn, _num(0),
+                                        other == fl.jv, fl.N, srange))
+            crange = fl.R if c.coord == fl.iv else fl.N
+            if rows_coord:
+                M_, N_, sm, sn = crange, K, c.sc, c.sk
+            else:
+                M_, N_, sm, sn = K, crange, c.sk, c.sc
+            post += self.gemms(c.array, poly_expr(c.off), poly_expr(sm), poly_expr(sn), True, M_, N_, segs)
+        for sname, vn in vnames.items():
+            repl.append(Assign(Ref(vn, (lin,)), Var(sname)))
+        allocs = [Assign(Var(vn), Alloc("Float32", size)) for vn in vnames.values()]
+        self._allocs += allocs
+        return repl, post
+
+    def gemms(self, out, off, sm, sn, acc, M, N, segs):
+        """Gemm statements for the segments: two to a launch when they share a layout, the
+        first storing (unless acc) and the rest adding."""
+        out_stmts = []
+        groups = []
+        for g in segs:
+            if groups and len(groups[-1]) < 2 and (groups[-1][0].a_km, groups[-1][0].b_km) == (g.a_km, g.b_km):
+                groups[-1].append(g)
+            else:
+                groups.append([g])
+        for n_, grp in enumerate(groups):
+            out_stmts.append(Gemm(out, off, sm, sn, acc or n_ > 0, M, N, grp))
+            self.rec["gemms"] += 1
+        return out_stmts
+
+    def run(self, exclude: set) -> Func:
+        self._allocs = []
+        self.pairs = []
+        body = []
+        for s in self.f.body:
+            if isinstance(s, For) and id(s) not in exclude and self.is_parallel(s):
+                try:
+                    before, loop, after = self.rewrite_loop(s)
+                except _No:
+                    body.append(s)
+                    continue
+                body += before + [loop] + after
+                self.pairs.append((s, loop))
+                self.rec["loops"].append(s.var)
+                continue
+            body.append(s)
+        return Func(self.f.name, self.f.args, self._allocs + body, self.f.annot)
+
+
+def transform(f: Func, T: Types, is_parallel, retype, host_ints: set | None = None) -> tuple[Func, dict, Types]:
+    """(f with its contractions on the matrix cores, a record {forward, adjoint, gemms, loops},
+    the rewritten function's types); f, {} and T unchanged when there is none or
+    `STADE_LOWER_GEMM=0`.  is_parallel(loop, func, types): the planner's verdict on a loop of
+    func; retype(func): the types of a rewritten function.  A rewritten loop that the planner
+    would no longer run in parallel is left as written."""
+    if os.environ.get("STADE_LOWER_GEMM", "1") == "0":
+        return f, {}, T
+    if host_ints is None:
+        assigned = {s.lhs.name for s in walk_stmts(f.body) if isinstance(s, Assign) and isinstance(s.lhs, Var)}
+        host_ints = {a for a in f.args if T.scalars.get(a) == "i" and a not in assigned and a not in T.arrays}
+    exclude: set = set()
+    while True:
+        rw = _Rewriter(f, T, host_ints, lambda loop: is_parallel(loop, f, T))
+        g = rw.run(exclude)
+        if not rw.rec["gemms"]:
+            return f, {}, T
+        T2 = retype(g)
+        bad = {id(orig) for orig, new in rw.pairs if not is_parallel(new, g, T2)}
+        if not bad:
+            return g, rw.rec, T2
+        exclude |= bad

@@ -31,9 +31,9 @@ import re
 from dataclasses import dataclass, field
 
 from .analysis import ArrayUse, ParallelLoop, Types, classify, flat_twin, infer_types, split_loops, _reads_of, _thaw
-from . import finish, fuse, gather
-from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, If, LowerError, Nothing_, Num, Range,
-                     Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
+from . import contract, finish, fuse, gather
+from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, Gemm, If, LowerError, Nothing_, Num,
+                     Range, Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
 MAX_BLOCKS = 8192          # grid of a parallel loop whose trip count the host cannot evaluate
 RED_MAX_BLOCKS = 2048      # at most, for a loop with sums (each block adds its sums once)
@@ -102,6 +102,11 @@ class ReturnOp:
     kid: int = 0
 
 
+@dataclass
+class GemmOp:
+    g: Gemm
+
+
 class FuncLower:
     def __init__(self, f: Func, precision: str, arg_types: dict | None = None, stacks_allocated: set | None = None,
                  inbounds: bool = True, dead_scalars: bool = True, merge_accum: bool = True):
@@ -124,6 +129,12 @@ class FuncLower:
         if os.environ.get("STADE_LOWER_FUSE", "1") != "0":
             f = self._fused(f)
             self.f = f
+        # contractions onto the fp32 matrix cores (contract.py): fp32 texts with unchecked
+        # accesses; STADE_LOWER_GEMM=0 keeps the loops
+        self.contract_rec: dict = {}
+        if precision == "f32" and inbounds:
+            f = self._contracted(f, arg_types, precision)
+            self.f = f
         self.fty = "float" if precision == "f32" else "double"
         self.arrays = self.T.arrays
         self.scalars = {n: t for n, t in self.T.scalars.items() if n not in self.arrays}
@@ -135,6 +146,35 @@ class FuncLower:
         self.twins: list = []          # (loop variable, 'row' | 'col', sites) of the flat twins
         self.refuse_reasons()
         self.ops = self.plan()
+
+    @staticmethod
+    def _parallel(loop: For, f: Func, T: Types) -> bool:
+        """The planner's verdict on a loop of f (live-out scalars: every scalar the loop assigns
+        that is read anywhere else in the function, a superset of what the planner computes)."""
+        inside = {id(t) for t in walk_stmts([loop])}
+        outside = set()
+        for s in walk_stmts(f.body):
+            if id(s) in inside:
+                continue
+            for e in stmt_exprs(s):
+                outside |= _reads_of(e)
+        pl, _ = classify(loop, T, outside, set())
+        return pl is not None
+
+    def _contracted(self, f: Func, arg_types, precision) -> Func:
+        def retype(g: Func) -> Types:
+            # every array keeps its kind and rank (an operand only the products read is still
+            # an argument of the same signature)
+            T2 = infer_types(g, arg_types, precision)
+            for n, kind in self.T.arrays.items():
+                T2.arrays.setdefault(n, kind)
+                T2.ndim[n] = max(T2.ndim.get(n, 1), self.T.ndim.get(n, 1))
+            return T2
+        g, rec, T2 = contract.transform(f, self.T, self._parallel, retype)
+        if rec:
+            self.T = T2
+            self.contract_rec = rec
+        return g
 
     def _fused(self, f: Func) -> Func:
         from .analysis import _upward_exposed
@@ -259,6 +299,12 @@ class FuncLower:
                 ops.append(SerialOp(list(cur), pred))
                 cur.clear()
         for s in stmts:
+            if isinstance(s, Gemm):
+                if not top or pred:
+                    raise LowerError(f"{self.f.name}: a matrix product below the top level")
+                flush()
+                ops.append(GemmOp(s))
+                continue
             if isinstance(s, Assign) and isinstance(s.rhs, Alloc):
                 if not (top and isinstance(s.lhs, Var) and self.host_ok(s.rhs.n, hl)):
                     raise LowerError(f"{self.f.name}: allocation of {s.lhs} needs a size the host can evaluate, "
@@ -758,6 +804,8 @@ class FuncGen:
         self.nk = 0
         self.hind = 1
         self.nalloc = 0
+        self.ngemm = 0
+        self.uses_gemm = False
         self.hlv: dict[str, int] = {}   # host loop variables in scope -> their slot in Args.hl
         self.serial_kernels: set[str] = set()
 
@@ -1203,6 +1251,8 @@ class FuncGen:
                 self.parallel(op)
             elif isinstance(op, ReturnOp):
                 self.serial([], op.pred, op.value)
+            elif isinstance(op, GemmOp):
+                self.gemm(op.g)
             elif isinstance(op, AllocOp):
                 hctx = HostCtx(fl, self.hlv)
                 et = 8 if fl.arrays[op.name] == "i" or fl.fty == "double" else 4
@@ -1253,6 +1303,55 @@ class FuncGen:
                 self.launch(f"k{k}")
                 for b in op.branches:
                     self.ops(b)
+
+    def gemm(self, g: Gemm) -> None:
+        """Host code of a matrix product (contract.py) on the fp32 matrix-core GEMM: the plan's
+        tile width and K split (an accumulating product adds its split's slices by atomics, a
+        stored one reduces them from a partials buffer)."""
+        fl = self.fl
+        hctx = HostCtx(fl, self.hlv)
+        self.uses_gemm = True
+        n = self.ngemm
+        self.ngemm += 1
+        km = {(x.a_km, x.b_km) for x in g.segs}
+        assert len(g.segs) in (1, 2) and len(km) == 1
+        a_km, b_km = km.pop()
+        tf = lambda b: "true" if b else "false"
+        self.hemit("{")
+        self.hind += 1
+        self.hemit(f"const int64_t _gm = {hctx.ex(g.M)}, _gn = {hctx.ex(g.N)};")
+        ks = []
+        for j, x in enumerate(g.segs):
+            self.hemit(f"const int64_t _gk{j} = {hctx.ex(x.K)};")
+            ks.append(f"_gk{j}")
+        kt = " + ".join(ks)
+        self.hemit(f"if (_gm > 0x7fffffff || _gn > 0x7fffffff || {kt} > 0x7fffffff) "
+                   f"return _fail(hipErrorInvalidValue, \"matrix product {n} into {g.out}: a dimension past 2^31\");")
+        self.hemit("if (_gm > 0 && _gn > 0) {")
+        self.hind += 1
+        self.hemit("stade::gemm::Args _g{};")
+        self.hemit(f"_g.nseg = {len(g.segs)};")
+        self.hemit("_g.M = (int)_gm;")
+        self.hemit("_g.N = (int)_gn;")
+        for j, x in enumerate(g.segs):
+            self.hemit(f"_g.seg[{j}] = stade::gemm::Seg{{a.A_{cname(x.a)} + ({hctx.ex(x.a_off)}), "
+                       f"a.A_{cname(x.b)} + ({hctx.ex(x.b_off)}), (long)({hctx.ex(x.lda)}), (long)({hctx.ex(x.ldb)}), "
+                       f"(int)_gk{j}}};")
+        self.hemit(f"const stade::gemm::Plan _p = stade::gemm::plan(_g.M, _g.N, (int)({kt}), stade::gemm::device_cus(), 1, "
+                   f"{tf(g.acc)});")
+        if not g.acc:
+            slot = self.nalloc
+            self.nalloc += 1
+            self.hemit(f"if (_p.ksplit > 1 && !(_g.part = (float*)_buf({slot}, (size_t)_p.ksplit * (size_t)_gm * (size_t)_gn * 4)))")
+            self.hemit(f"    return _fail(hipErrorOutOfMemory, \"matrix product {n}: partial sums\");")
+        self.hemit(f"const stade_lowered::GemmOut<{tf(g.acc)}> _ep{{a.A_{cname(g.out)} + ({hctx.ex(g.out_off)}), "
+                   f"(long)({hctx.ex(g.out_sm)}), (long)({hctx.ex(g.out_sn)})}};")
+        self.hemit(f"if ((_e = stade::gemm::launch<{tf(a_km)}, {tf(b_km)}>(_g, _ep, stream, _p)) != hipSuccess) "
+                   f"return _fail(_e, \"matrix product {n} into {g.out}\");")
+        self.hind -= 1
+        self.hemit("}")
+        self.hind -= 1
+        self.hemit("}")
 
     def source(self) -> str:
         fl = self.fl
@@ -1439,6 +1538,9 @@ extern "C" const char* stade_hip_gen_last_error(void) { return g_gen_err; }
 """
 
 
+GEMM_INCLUDE = '#include "lowered_gemm.hpp"'
+
+
 def generate(text: str, precision: str = "f64", arg_types: dict | None = None, inbounds: bool = True,
              dead_scalars: bool = True, merge_accum: bool = True) -> tuple[str, dict]:
     """HIP source for every generated function of `text` (the initstacks_* functions stay on
@@ -1454,7 +1556,10 @@ def generate(text: str, precision: str = "f64", arg_types: dict | None = None, i
         if f.name.startswith("initstacks_"):
             continue
         fl = _func_lower(f, stack_kinds, precision, arg_types, inbounds, dead_scalars, merge_accum)
-        src.append(FuncGen(fl).source())
+        gen = FuncGen(fl)
+        src.append(gen.source())
+        if gen.uses_gemm and GEMM_INCLUDE not in src:
+            src.insert(1, GEMM_INCLUDE)
         sig = []
         for n in f.args:
             if n in fl.arrays:
@@ -1462,7 +1567,7 @@ def generate(text: str, precision: str = "f64", arg_types: dict | None = None, i
             else:
                 sig.append((n, fl.scalars.get(n, "f"), 0))
         sigs[f.name] = dict(args=sig, plan=describe(fl.ops), reasons=list(fl.reasons), finish=fl.finish_rec,
-                            inbounds=inbounds, twins=list(fl.twins))
+                            inbounds=inbounds, twins=list(fl.twins), contract=fl.contract_rec)
     return "\n".join(src), sigs
 
 
@@ -1530,4 +1635,8 @@ def describe(ops, depth=0) -> list[str]:
             out.append(pad + f"allocate {op.name}")
         elif isinstance(op, ReturnOp):
             out.append(pad + "return")
+        elif isinstance(op, GemmOp):
+            g = op.g
+            out.append(pad + f"matrix product into {g.out} ({'added' if g.acc else 'stored'}; "
+                       + " + ".join(f"{x.a} x {x.b}" for x in g.segs) + ")")
     return out

@@ -132,6 +132,37 @@ class ExprStmt:
 
 
 @dataclass
+class GemmSeg:
+    """One product of a Gemm: A(m, k) = a[a_off + (k + m * lda if a_km else m + k * lda)],
+    B(k, n) = b[b_off + (k + n * ldb if b_km else n + k * ldb)], k < K (0-based offsets;
+    every expression an Int expression of the function's Int arguments)."""
+    a: str
+    a_off: object
+    a_km: bool
+    lda: object
+    b: str
+    b_off: object
+    b_km: bool
+    ldb: object
+    K: object
+
+
+@dataclass
+class Gemm:
+    """A statement the general lowering makes of a contraction (contract.py), not Julia text:
+    out[out_off + m * out_sm + n * out_sn] (+)= sum over segments of sum_k A(m, k) B(k, n) for
+    m < M, n < N (`acc`: added to the element, else stored)."""
+    out: str
+    out_off: object
+    out_sm: object
+    out_sn: object
+    acc: bool
+    M: object
+    N: object
+    segs: list
+
+
+@dataclass
 class Func:
     name: str
     args: list
@@ -543,6 +574,11 @@ def stmt_exprs(s):
         return [s.value] if s.value is not None else []
     if isinstance(s, ExprStmt):
         return [s.e]
+    if isinstance(s, Gemm):
+        out = [s.out_off, s.out_sm, s.out_sn, s.M, s.N]
+        for g in s.segs:
+            out += [g.a_off, g.lda, g.b_off, g.ldb, g.K]
+        return out
     return []
 
 

@@ -82,7 +82,9 @@ PLANS = {
     # the forward, loss and seed loops over the same cells fused into one)
     ("diffusion2d_b", "diffusion2d_b"): [("idx", "un", "owned"), ("idx", "ub", "owned"), ("idx", "unb", "read"),
                                          ("idx", "unb", "owned"), ("idx", "loss", "atomic")],
-    ("mlp2_ce_b", "mlp2_ce_b"): [("idx", "h1", "owned"), ("idx", "w1b", "atomic"), ("idx", "xb", "atomic")],
+    # (the dense layers' sums and scatters as matrix products around the loops: contract.py)
+    ("mlp2_ce_b", "mlp2_ce_b"): [("idx", "h1", "owned"), ("idx", "b1b", "atomic"), ("gemm", "w1b", "added"),
+                                 ("gemm", "xb", "added"), ("gemm", "h1b", "added")],
     ("conv3x3_b", "conv3x3_b"): [("idx", "out", "owned"), ("idx", "wb", "atomic"), ("idx", "xpb", "atomic")],
     ("generic/binsum_b", "binsum_b"): [("i", "c", "atomic"), ("i", "vb", "owned")],
     ("generic/window1d_b", "window1d_b"): [("i", "wb", "atomic"), ("i", "inpb", "atomic"), ("i", "outb", "owned")],
@@ -98,6 +100,9 @@ def test_plans(key):
     _, sigs = hipgen.generate((CORPUS / f"{text}.jl").read_text(), prec)
     plan = " | ".join(sigs[fname]["plan"])
     for var, arr, kind in PLANS[key]:
+        if var == "gemm":
+            assert re.search(rf"matrix product into {arr} \({kind}", plan), (arr, kind, plan)
+            continue
         assert re.search(rf"parallel over {var} \[[^\]]*\b{arr}:{kind}\b", plan), (var, arr, kind, plan)
     assert "loops in order" not in plan, plan       # every loop runs one iteration per thread
 

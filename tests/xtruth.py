@@ -470,7 +470,43 @@ class _Compiler:
         if isinstance(s, S.ExprStmt):
             f = self.expr(s.e)
             return lambda env: (f(env), None)[1]
+        if isinstance(s, S.Gemm):
+            return self.gemm(s)
         raise NotImplementedError(type(s).__name__)
+
+    def gemm(self, s):
+        """A matrix product of the lowering (stade_hip.lower.contract) by its definition:
+        out[off + m sm + n sn] (+)= sum over segments of sum_k A(m, k) B(k, n), every element
+        addressed as the statement's offsets and leading dimensions say (an address outside
+        an array, or an unset element, raises)."""
+        ex = self.expr
+        head = [ex(e) for e in (s.out_off, s.out_sm, s.out_sn, s.M, s.N)]
+        segs = [(g.a, ex(g.a_off), g.a_km, ex(g.lda), g.b, ex(g.b_off), g.b_km, ex(g.ldb), ex(g.K)) for g in s.segs]
+
+        def elem(arr, k, nm):
+            if k < 0 or k >= len(arr.data):
+                raise IndexError(f"matrix product: {nm}[{k}] outside an array of {len(arr.data)}")
+            v = arr.data[k]
+            if v is None:
+                raise ValueError(f"matrix product: read of an unset element of {nm}")
+            return v
+
+        def gemm(env):
+            off, sm, sn, M, N = (f(env) for f in head)
+            C = env[s.out]
+            sv = [(a, env[a], ao(env), akm, la(env), b, env[b], bo(env), bkm, lb(env), K(env))
+                  for a, ao, akm, la, b, bo, bkm, lb, K in segs]
+            for m in range(M):
+                for n in range(N):
+                    t = Decimal(0)
+                    for a, A, ao, akm, la, b, B, bo, bkm, lb, K in sv:
+                        for k in range(K):
+                            x = elem(A, ao + (k + m * la if akm else m + k * la), a)
+                            y = elem(B, bo + (k + n * lb if bkm else n + k * lb), b)
+                            t = _add(t, _mul(x, y))
+                    ic = off + m * sm + n * sn
+                    C.data[ic] = _add(elem(C, ic, s.out), t) if s.acc else t
+        return gemm
 
 
 def _to_j(v):
