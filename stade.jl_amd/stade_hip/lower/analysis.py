@@ -21,8 +21,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
-from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, Gemm, If, LowerError, Num, Range,
-                     Ref, Return, Tup, Un, Var, While, children, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
+from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, Gemm, GemmT, If, LowerError, Num,
+                     Range, Ref, Return, Tup, Un, Var, While, children, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
 FLOAT_FNS = {"exp", "log", "tanh", "sin", "cos", "tan", "sqrt", "sinh", "cosh", "atan", "asin", "acos", "log10", "log2",
              "exp2", "expm1", "log1p", "cbrt", "float", "Float64", "Float32", "inv"}
@@ -126,8 +126,9 @@ def infer_types(f: Func, arg_types: dict | None = None, precision: str = "f64") 
                 if isinstance(x, Call) and x.fn in ("length", "size") and x.args and isinstance(x.args[0], Var):
                     T.arrays.setdefault(x.args[0].name, "f")
                     T.ndim.setdefault(x.args[0].name, 1)
-        if isinstance(s, Gemm):   # (a contraction's operands and output are float arrays)
-            for nm in [s.out] + [x for g in s.segs for x in (g.a, g.b)]:
+        if isinstance(s, (Gemm, GemmT)):   # (a contraction's operands and output are float arrays)
+            names = [s.out] + ([x for g in s.segs for x in (g.a, g.b)] if isinstance(s, Gemm) else [s.a, s.b])
+            for nm in names:
                 T.arrays.setdefault(nm, "f")
                 T.ndim.setdefault(nm, 1)
         if isinstance(s, Assign):

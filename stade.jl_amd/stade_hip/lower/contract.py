@@ -59,8 +59,10 @@ from __future__ import annotations
 import os
 from dataclasses import dataclass
 
-from .analysis import NotAffine, Types, _derived, _linear_index, _reads_of, linear_in, to_poly
-from .syntax import Alloc, Assign, Bin, For, Func, Gemm, GemmSeg, Num, Ref, Var, stmt_exprs, walk_expr, walk_stmts
+from .analysis import (NotAffine, Types, _derived, _freeze, _linear_index, _mul, _reads_of, _upward_exposed, linear_in,
+                       to_poly)
+from .syntax import (Alloc, Assign, Bin, Call, For, Func, Gemm, GemmSeg, GemmT, Num, Range, Ref, TabDim, Un, Var,
+                     stmt_exprs, walk_expr, walk_stmts)
 
 ONE = {(): 1}
 
@@ -163,6 +165,282 @@ def flat_of(loop: For, host_ints: set) -> Flat | None:
     return Flat(v, iv, jv, R, N)
 
 
+@dataclass
+class Digit:
+    """One digit of a flat loop variable: name = mod(div(idx - 1, P), R) + 1 (the top digit:
+    div(idx - 1, P) + 1, its range the trip count / P)."""
+    name: str
+    P: dict
+    R: dict
+    Re: object
+
+
+def _mono_div(p: dict, q: dict):
+    """p / q for single monomials with an exact quotient, else None."""
+    if len(p) != 1 or len(q) != 1:
+        return None
+    (mp, cp), = p.items()
+    (mq, cq), = q.items()
+    if cq == 0 or cp % cq:
+        return None
+    rest = list(mp)
+    for a in mq:
+        if a not in rest:
+            return None
+        rest.remove(a)
+    return {tuple(rest): cp // cq}
+
+
+def digits_of(loop: For, T: Types, host_ints: set) -> list | None:
+    """The digits of `for idx = 1:trip` (or `trip:-1:1`) in increasing place value, when the
+    body's top Int temporaries decompose idx - 1 into a complete mixed radix
+    (idx - 1 = sum (d - 1) P_d, P of the first 1, each next P the product of those before and
+    their ranges, the trip count the product of all), else None."""
+    r = loop.rng
+    step = 1 if r.step is None else (int(r.step.text) if isinstance(r.step, Num) and r.step.is_int else 0)
+    one = lambda e: isinstance(e, Num) and e.is_int and int(e.text) == 1
+    if step == 1 and one(r.lo):
+        trip = r.hi
+    elif step == -1 and one(r.hi):
+        trip = r.lo
+    else:
+        return None
+    v = loop.var
+    count = {}
+    for s in loop.body:
+        if isinstance(s, Assign) and isinstance(s.lhs, Var):
+            count[s.lhs.name] = count.get(s.lhs.name, 0) + 1
+    vm1 = {s.lhs.name for s in loop.body if isinstance(s, Assign) and isinstance(s.lhs, Var)
+           and isinstance(s.rhs, Bin) and s.rhs.op == "-" and s.rhs.a == Var(v) and one(s.rhs.b)
+           and count[s.lhs.name] == 1}
+    is_e0 = lambda x: (isinstance(x, Var) and x.name in vm1) or (isinstance(x, Bin) and x.op == "-" and x.a == Var(v)
+                                                                   and one(x.b))
+
+    def poly(e):
+        try:
+            p = to_poly(e, {}, T)
+        except NotAffine:
+            return None
+        return p if _host_poly(p, host_ints) and p else None
+    found = []
+    for s in loop.body:
+        if not (isinstance(s, Assign) and isinstance(s.lhs, Var) and count.get(s.lhs.name) == 1):
+            continue
+        e = s.rhs
+        if not (isinstance(e, Bin) and e.op == "+" and one(e.b) and isinstance(e.a, Call) and len(e.a.args) == 2):
+            continue
+        c = e.a
+        if c.fn == "mod" and is_e0(c.args[0]):
+            P, R, Re = {(): 1}, poly(c.args[1]), c.args[1]
+        elif (c.fn == "mod" and isinstance(c.args[0], Call) and c.args[0].fn == "div" and len(c.args[0].args) == 2
+              and is_e0(c.args[0].args[0])):
+            P, R, Re = poly(c.args[0].args[1]), poly(c.args[1]), c.args[1]
+        elif c.fn == "div" and is_e0(c.args[0]):
+            P, R, Re = poly(c.args[1]), None, None
+        else:
+            continue
+        if P is None or (Re is not None and R is None):
+            return None
+        found.append(Digit(s.lhs.name, P, R, Re))
+    if len(found) < 2:
+        return None
+    tp = poly(trip)
+    if tp is None:
+        return None
+    out, cur, left = [], {(): 1}, list(found)
+    while left:
+        nxt = [d for d in left if _freeze(d.P) == _freeze(cur)]
+        if len(nxt) != 1:
+            return None
+        d = nxt[0]
+        left.remove(d)
+        out.append(d)
+        if d.R is None:
+            if left:
+                return None
+            q = _mono_div(tp, d.P)
+            if q is None:
+                return None
+            d.R = q
+            d.Re = poly_expr(q)
+            return out
+        cur = _mul(cur, d.R)
+    return out if _freeze(cur) == _freeze(tp) else None
+
+
+BIG = 1 << 30      # the run of a digit whose range is an argument (taken as long)
+
+
+def _run_of(R) -> int:
+    """A digit's range as a run length: its value when a literal, else BIG."""
+    return int(R.text) if isinstance(R, Num) and R.is_int else BIG
+
+
+def _subst(e, f):
+    """e with every Var replaced by f(name) (an expression)."""
+    if isinstance(e, Var):
+        return f(e.name)
+    if isinstance(e, Bin):
+        return Bin(e.op, _subst(e.a, f), _subst(e.b, f))
+    if isinstance(e, Un):
+        return Un(e.op, _subst(e.a, f))
+    if isinstance(e, Call):
+        return Call(e.fn, tuple(_subst(x, f) for x in e.args))
+    if isinstance(e, Ref):
+        return Ref(e.name, tuple(_subst(x, f) for x in e.idx))
+    return e
+
+
+@dataclass
+class Split:
+    """A reference's 0-based offset as outer(digits) + inner(k) + const - 1, the two parts
+    polynomials in disjoint variables."""
+    array: str
+    outer: dict
+    inner: dict
+    uses: set
+
+
+class _Tables:
+    """The table form of one inner loop: splitting of references, and the loops that fill the
+    offset tables (over a set of digits, or over the inner index)."""
+
+    def __init__(self, rw, digits, inner: For, k: str, K, outer_env: dict, var: str):
+        self.rw, self.digits, self.k, self.K, self.var = rw, digits, k, K, var
+        self.loops, self.allocs, self.cache = [], [], {}
+        T = rw.T
+        # inner Int temporaries: those with div / mod stay variables of the inner offset (their
+        # definitions, in order, are copied into the inner tables' loops); the rest substitute
+        self.int_stmts, self.atoms, env = [], set(), dict(outer_env)
+        for s in inner.body:
+            if isinstance(s, Assign) and isinstance(s.lhs, Var) and T.scalars.get(s.lhs.name) == "i":
+                self.int_stmts.append(s)
+                if any(isinstance(x, Call) and x.fn in ("div", "mod") for x in walk_expr(s.rhs)):
+                    self.atoms.add(s.lhs.name)
+                else:
+                    env[s.lhs.name] = s.rhs
+        self.env = env
+        # the inner index's fastest digit: a temporary mod(k - 1, R) + 1 (or k itself)
+        km1 = {s.lhs.name for s in self.int_stmts if isinstance(s.rhs, Bin) and s.rhs.op == "-"
+               and s.rhs.a == Var(k) and isinstance(s.rhs.b, Num) and s.rhs.b.text == "1"}
+        self.fast, self.fast_run = k, BIG
+        for s in self.int_stmts:
+            e = s.rhs
+            if (isinstance(e, Bin) and e.op == "+" and isinstance(e.b, Num) and e.b.text == "1"
+                    and isinstance(e.a, Call) and e.a.fn == "mod"
+                    and (e.a.args[0] in [Var(x) for x in km1] or e.a.args[0] == Bin("-", Var(k), Num("1", True)))):
+                self.fast = s.lhs.name
+                self.fast_run = _run_of(e.a.args[1])
+        # the inner tables' loops recompute the div / mod temporaries and what they read; those
+        # may depend on nothing of the outer loop
+        inner_names = {s.lhs.name for s in self.int_stmts}
+        need = set(self.atoms)
+        for s in reversed(self.int_stmts):
+            if s.lhs.name in need:
+                need |= _reads_of(s.rhs) & inner_names
+        self.int_stmts = [s for s in self.int_stmts if s.lhs.name in need]
+        for s in self.int_stmts:
+            if not _reads_of(s.rhs) <= inner_names | {k} | rw.host_ints:
+                raise _No("an inner index temporary reads the outer loop")
+
+    def split(self, ref: Ref) -> Split:
+        T = self.rw.T
+        try:
+            p = to_poly(_linear_index(ref, T), self.env, T)
+        except NotAffine:
+            raise _No(f"{ref.name}: index not a polynomial")
+        dn = {d.name for d in self.digits}
+        inner_v = self.atoms | {self.k}
+        outer, inner, const = {}, {}, {}
+        for m, c in p.items():
+            if any(a[0] != "v" for a in m):
+                raise _No(f"{ref.name}: a div / mod outside the digits")
+            names = {a[1] for a in m}
+            o, i = names & dn, names & inner_v
+            if not names - dn - inner_v <= self.rw.host_ints:
+                raise _No(f"{ref.name}: reads a variable of neither loop")
+            if o and i:
+                raise _No(f"{ref.name}: the offset does not split into outer and inner parts")
+            (outer if o else inner if i else const)[m] = c
+        inner = dict(inner)
+        for m, c in const.items():
+            inner[m] = inner.get(m, 0) + c
+        inner[()] = inner.get((), 0) - 1
+        inner = {m: c for m, c in inner.items() if c}
+        return Split(ref.name, outer, inner, {a[1] for m in outer for a in m} & dn)
+
+    def size(self, D):
+        out = None
+        for d in D:
+            out = d.Re if out is None else Bin("*", out, d.Re)
+        return out if out is not None else _num(1)
+
+    def unit_t(self, poly: dict) -> int:
+        """How many adjacent k are adjacent elements: the run of the inner index's fastest
+        digit when its coefficient is 1, else 0."""
+        if poly.get(((("v", self.k),)), 0) == 1:
+            return BIG
+        return self.fast_run if poly.get(((("v", self.fast),)), 0) == 1 else 0
+
+    @staticmethod
+    def unit_rows(D, poly: dict) -> int:
+        """How many adjacent rows over digits D are adjacent elements (0: none)."""
+        return _run_of(D[0].Re) if D and poly.get(((("v", D[0].name),)), 0) == 1 else 0
+
+    def place(self, D) -> dict:
+        """The digits' share of idx - 1: sum over D of (d - 1) P_d."""
+        out = {}
+        for d in D:
+            for m, c in _mul({(("v", d.name),): 1}, d.P).items():
+                out[m] = out.get(m, 0) + c
+            for m, c in d.P.items():
+                out[m] = out.get(m, 0) - c
+        return {m: c for m, c in out.items() if c}
+
+    def row_table(self, D, sp) -> TabDim:
+        """A table over the mixed radix of digits D of a polynomial in them (a Split's outer
+        part, or a polynomial)."""
+        poly = sp.outer if isinstance(sp, Split) else sp
+        key = ("row", tuple(d.name for d in D), _freeze(poly))
+        if key in self.cache:
+            return self.cache[key]
+        rw = self.rw
+        name, q, r0 = rw.fresh("R"), rw.fresh("q"), rw.fresh("r")
+        stmts = [Assign(Var(r0), Bin("-", Var(q), _num(1)))]
+        ren, Q = {}, None
+        for j, d in enumerate(D):
+            dv = rw.fresh("d")
+            x = Var(r0) if Q is None else Call("div", (Var(r0), Q))
+            val = x if j == len(D) - 1 else Call("mod", (x, d.Re))
+            stmts.append(Assign(Var(dv), Bin("+", val, _num(1))))
+            ren[d.name] = dv
+            Q = d.Re if Q is None else Bin("*", Q, d.Re)
+        stmts.append(Assign(Ref(name, (Var(q),)), _subst(poly_expr(poly), lambda n: Var(ren.get(n, n)))))
+        n_ = self.size(D)
+        self.allocs.append(Assign(Var(name), Alloc("Int64", n_)))
+        self.loops.append(For(q, Range(_num(1), None, n_), stmts))
+        self.cache[key] = TabDim(name, _num(0))
+        return self.cache[key]
+
+    def t_table(self, sp: Split) -> TabDim:
+        key = ("t", _freeze(sp.inner))
+        if key in self.cache:
+            return self.cache[key]
+        rw = self.rw
+        name, kv = rw.fresh("K"), rw.fresh("k")
+        ren = {self.k: kv}
+        stmts = []
+        for s in self.int_stmts:
+            nv = rw.fresh("t")
+            stmts.append(Assign(Var(nv), _subst(s.rhs, lambda n: Var(ren.get(n, n)))))
+            ren[s.lhs.name] = nv
+        stmts.append(Assign(Ref(name, (Var(kv),)), _subst(poly_expr(sp.inner), lambda n: Var(ren.get(n, n)))))
+        self.allocs.append(Assign(Var(name), Alloc("Int64", self.K)))
+        self.loops.append(For(kv, Range(_num(1), None, self.K), stmts))
+        self.cache[key] = TabDim(name, _num(0))
+        return self.cache[key]
+
+
 class _Rewriter:
     def __init__(self, f: Func, T: Types, host_ints: set, is_parallel):
         self.f = f
@@ -171,6 +449,16 @@ class _Rewriter:
         self.is_parallel = is_parallel
         self.n = 0
         self.rec = {"forward": 0, "adjoint": 0, "gemms": 0, "loops": []}
+        # Int names the function sets once, at its top level, from its Int arguments (`i_wp =
+        # i_w + 2`): substituted into indices like the arguments themselves
+        count = {}
+        for s in walk_stmts(f.body):
+            if isinstance(s, Assign) and isinstance(s.lhs, Var):
+                count[s.lhs.name] = count.get(s.lhs.name, 0) + 1
+        self.fenv = {s.lhs.name: s.rhs for s in f.body if isinstance(s, Assign) and isinstance(s.lhs, Var)
+                     and count[s.lhs.name] == 1 and T.scalars.get(s.lhs.name) == "i"
+                     and {x.name for x in walk_expr(s.rhs) if isinstance(x, Var)} <= host_ints
+                     and not any(isinstance(x, Ref) for x in walk_expr(s.rhs))}
 
     def fresh(self, stem: str) -> str:
         self.n += 1
@@ -313,40 +601,41 @@ class _Rewriter:
                 out.add(s.lhs.name)
         return out
 
-    def reads_elsewhere(self, names: set, inner: For) -> bool:
-        """Any of `names` read or assigned anywhere in the function outside `inner`."""
-        inside = {id(s) for s in walk_stmts([inner])}
-        for s in walk_stmts(self.f.body):
-            if id(s) in inside:
-                continue
-            for e in stmt_exprs(s):
-                if _reads_of(e) & names:
-                    return True
-            if isinstance(s, Assign) and isinstance(s.lhs, Var) and s.lhs.name in names:
-                return True
-        return False
+    def live_after(self, names: set, loop: For, inner: For) -> bool:
+        """Any of `names` (assigned in `inner`, a top-level statement of `loop`'s body) read
+        after `inner` before being assigned again: in the rest of the iteration, the next
+        iteration, or the statements after `loop` in the function."""
+        pos = next(j for j, x in enumerate(loop.body) if x is inner)
+        top = next(j for j, x in enumerate(self.f.body) if x is loop)
+        cont = loop.body[pos + 1:] + loop.body + self.f.body[top + 1:]
+        return any(_upward_exposed(cont, n) for n in names)
 
     def rewrite_loop(self, loop: For):
-        """(statements before, the new loop, statements after) or raises _No."""
+        """(statements before, the new loop, statements after) or raises _No.  Each inner loop
+        is tried in the strided form (a two-coordinate flat loop, operands with a unit
+        stride: the tuned GEMM), then in the table form (any mixed-radix flat loop, factors
+        that are sums of an outer and an inner offset)."""
         fl = flat_of(loop, self.host_ints)
-        if fl is None:
+        dg = digits_of(loop, self.T, self.host_ints)
+        if fl is None and dg is None:
             raise _No("not a flat loop")
         # outer Int temporaries (assigned once, not the coordinates) substitute into indices
         count = {}
         for s in walk_stmts(loop.body):
             if isinstance(s, Assign) and isinstance(s.lhs, Var):
                 count[s.lhs.name] = count.get(s.lhs.name, 0) + 1
-        outer_env = {s.lhs.name: s.rhs for s in loop.body if isinstance(s, Assign) and isinstance(s.lhs, Var)
-                     and self.T.scalars.get(s.lhs.name) == "i" and count[s.lhs.name] == 1
-                     and s.lhs.name not in (fl.iv, fl.jv)}
+        coords = {fl.iv, fl.jv} if fl is not None else set()
+        digit_names = {d.name for d in dg} if dg is not None else set()
+        outer_ints = {s.lhs.name: s.rhs for s in loop.body if isinstance(s, Assign) and isinstance(s.lhs, Var)
+                      and self.T.scalars.get(s.lhs.name) == "i" and count[s.lhs.name] == 1}
+        outer_env = dict(self.fenv, **{n: e for n, e in outer_ints.items() if n not in coords})
+        outer_env_t = dict(self.fenv, **{n: e for n, e in outer_ints.items() if n not in digit_names})
         inners = [s for s in loop.body if isinstance(s, For)]
         if not inners:
             raise _No("no inner loop")
         written = self.written_in(loop.body)
         before, after, new_body = [], [], []
         done = 0
-        lin = Bin("+", Var(fl.jv), Bin("*", Bin("-", Var(fl.iv), _num(1)), fl.N))   # 1-based (j, i), j fastest
-        size = Bin("*", fl.R, fl.N)
         for s in loop.body:
             if not isinstance(s, For):
                 new_body.append(s)
@@ -354,24 +643,130 @@ class _Rewriter:
             try:
                 k, K, env, alias, temps, accs = self.inner_parts(s, outer_env, fl)
                 # (k itself is the loop's own: a Julia loop variable is a new local of the loop)
-                if self.reads_elsewhere(temps, s):
+                if self.live_after(temps, loop, s):
                     raise _No("an inner temporary is read outside the inner loop")
-                if accs[0][0] == "s":
-                    pre, repl = self.forward(s, k, K, env, alias, accs, fl, written, lin, size)
-                    before += pre
-                    new_body += repl
-                    self.rec["forward"] += 1
-                else:
-                    repl, post = self.adjoint(loop, s, k, K, env, alias, accs, fl, written, lin, size)
-                    new_body += repl
-                    after += post
-                    self.rec["adjoint"] += 1
+                pre = repl = post = None
+                if fl is not None:
+                    lin = Bin("+", Var(fl.jv), Bin("*", Bin("-", Var(fl.iv), _num(1)), fl.N))   # (j, i), j fastest
+                    size = Bin("*", fl.R, fl.N)
+                    try:
+                        if accs[0][0] == "s":
+                            pre, repl = self.forward(s, k, K, env, alias, accs, fl, written, lin, size)
+                            post = []
+                        else:
+                            repl, post = self.adjoint(loop, s, k, K, env, alias, accs, fl, written, lin, size)
+                            pre = []
+                    except _No:
+                        pre = None
+                if pre is None:
+                    if dg is None:
+                        raise _No("no strided form and no digits")
+                    tb = _Tables(self, dg, s, k, K, outer_env_t, loop.var)
+                    if accs[0][0] == "s":
+                        pre, repl = self.forward_tab(tb, accs, alias, written)
+                        post = []
+                    else:
+                        repl, post = self.adjoint_tab(tb, loop, s, accs, alias, written)
+                        pre = []
+                    pre = tb.loops + pre
+                    self._allocs += tb.allocs
+                before += pre
+                new_body += repl
+                after += post
+                self.rec["forward" if accs[0][0] == "s" else "adjoint"] += 1
+                self.rec["gemms"] += sum(1 for x in pre + post if isinstance(x, (Gemm, GemmT)))
                 done += 1
             except _No:
                 new_body.append(s)
         if not done:
             raise _No("no inner loop is a contraction")
         return before, For(loop.var, loop.rng, new_body), after
+
+    # -- the table form -------------------------------------------------------------------------------
+    def forward_tab(self, tb, accs, alias, written):
+        pre, repl = [], []
+        for _, acc, e in accs:
+            parts = None
+            launches = []
+            for a, b in self.terms(e):
+                a, b = self.resolve(a, alias), self.resolve(b, alias)
+                if not (isinstance(a, Ref) and isinstance(b, Ref)):
+                    raise _No("a forward term that is not a product of two elements")
+                sa, sb = tb.split(a), tb.split(b)
+                if sa.array in written or sb.array in written:
+                    raise _No("a factor is written in the loop")
+                fast = tb.digits[0].name
+                X, Y = (sa, sb) if fast in sa.uses else (sb, sa)
+                if fast not in X.uses:
+                    raise _No("no factor runs over the fastest digit")
+                Dm = [d for d in tb.digits if d.name in X.uses]
+                Dn = [d for d in tb.digits if d.name not in X.uses]
+                if not Y.uses <= {d.name for d in Dn}:
+                    raise _No("the factors share a digit")
+                if parts is not None and parts != (tuple(d.name for d in Dm), tuple(d.name for d in Dn)):
+                    raise _No("the terms split the digits differently")
+                parts = (tuple(d.name for d in Dm), tuple(d.name for d in Dn))
+                launches.append((X, Y, Dm, Dn))
+            _, _, Dm, Dn = launches[0]
+            Mm, Mn = tb.size(Dm), tb.size(Dn)
+            # T in the loop's own order: T(m, n) at the idx whose digits they are, read as T[idx]
+            tname = self.fresh("T")
+            pre.append(Assign(Var(tname), Alloc("Float32", Bin("*", Mm, Mn))))
+            ro, co = tb.row_table(Dm, tb.place(Dm)), tb.row_table(Dn, tb.place(Dn))
+            for j, (X, Y, _, _) in enumerate(launches):
+                pre.append(GemmT(tname, _num(0), ro, co, 0 if j == 0 else 1, Mm, Mn, tb.K, X.array, _num(0),
+                                 tb.row_table(Dm, X), tb.t_table(X), Y.array, _num(0), tb.t_table(Y), tb.row_table(Dn, Y),
+                                 a_km=tb.unit_t(X.inner) > tb.unit_rows(Dm, X.outer),
+                                 b_km=tb.unit_t(Y.inner) > tb.unit_rows(Dn, Y.outer)))
+            repl.append(Assign(acc, Bin("+", acc, Ref(tname, (Var(tb.var),)))))
+        return pre, repl
+
+    def adjoint_tab(self, tb, loop, inner, accs, alias, written):
+        inner_ids = {id(x) for x in walk_stmts([inner])}
+        rest = [x for x in loop.body if id(x) not in inner_ids]
+        touched_elsewhere = self.refs_in(rest)
+        allnames = {d.name for d in tb.digits}
+        fast = tb.digits[0].name
+        vnames, post = {}, []
+        D1 = D2 = None
+        for _, acc, e in accs:
+            sc = tb.split(acc)
+            if sc.array in touched_elsewhere:
+                raise _No(f"{sc.array} is touched elsewhere in the loop")
+            if not sc.inner:
+                raise _No("an accumulated array that does not run over the inner index")
+            DC = [d for d in tb.digits if d.name in sc.uses]
+            DR = [d for d in tb.digits if d.name not in sc.uses]
+            for a, b in self.terms(e):
+                a, b = self.resolve(a, alias), self.resolve(b, alias)
+                if isinstance(a, Var) and isinstance(b, Ref):
+                    a, b = b, a
+                if not (isinstance(a, Ref) and isinstance(b, Var)):
+                    raise _No("an adjoint term that is not an element times a scalar")
+                if b.name == tb.k or b.name in alias or self.T.scalars.get(b.name) != "f":
+                    raise _No("the scalar factor varies in the inner loop or is not a float")
+                sr = tb.split(a)
+                if sr.array in written:
+                    raise _No("a factor is written in the loop")
+                if not sr.inner or sr.uses & sc.uses or (sr.uses | sc.uses) != allnames:
+                    raise _No("the accumulation and its factor do not split the digits")
+                d1 = [d for d in tb.digits if d.name in (sc.uses if fast in sc.uses else sr.uses)]
+                d2 = [d for d in tb.digits if d.name not in {x.name for x in d1}]
+                if D1 is not None and [d.name for d in d1] != [d.name for d in D1]:
+                    raise _No("the accumulations split the digits differently")
+                D1, D2 = d1, d2
+                vn = vnames.setdefault(b.name, self.fresh("V"))
+                # V in the loop's own order (V[idx]): V(m, s) at the place of C's digits m plus
+                # the place of the factor's digits s
+                post.append(GemmT(sc.array, _num(0), tb.row_table(DC, sc), tb.t_table(sc), 2, tb.size(DC), tb.K,
+                                  tb.size(DR), vn, _num(0), tb.row_table(DC, tb.place(DC)), tb.row_table(DR, tb.place(DR)),
+                                  sr.array, _num(0), tb.row_table(DR, sr), tb.t_table(sr),
+                                  a_km=tb.unit_rows(DR, tb.place(DR)) > tb.unit_rows(DC, tb.place(DC)),
+                                  b_km=tb.unit_rows(DR, sr.outer) > tb.unit_t(sr.inner)))
+        repl = [Assign(Ref(vn, (Var(tb.var),)), Var(sname)) for sname, vn in vnames.items()]
+        size = Bin("*", tb.size(D1), tb.size(D2))
+        tb.allocs += [Assign(Var(vn), Alloc("Float32", size)) for vn in vnames.values()]
+        return repl, post
 
     def forward(self, inner, k, K, env, alias, accs, fl, written, lin, size):
         pre, repl = [], []
@@ -463,7 +858,6 @@ class _Rewriter:
                 groups.append([g])
         for n_, grp in enumerate(groups):
             out_stmts.append(Gemm(out, off, sm, sn, acc or n_ > 0, M, N, grp))
-            self.rec["gemms"] += 1
         return out_stmts
 
     def run(self, exclude: set) -> Func:

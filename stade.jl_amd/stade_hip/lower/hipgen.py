@@ -32,8 +32,8 @@ from dataclasses import dataclass, field
 
 from .analysis import ArrayUse, ParallelLoop, Types, classify, flat_twin, infer_types, split_loops, _reads_of, _thaw
 from . import contract, finish, fuse, gather
-from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, Gemm, If, LowerError, Nothing_, Num,
-                     Range, Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
+from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, Func, Gemm, GemmT, If, LowerError,
+                     Nothing_, Num, Range, Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
 MAX_BLOCKS = 8192          # grid of a parallel loop whose trip count the host cannot evaluate
 RED_MAX_BLOCKS = 2048      # at most, for a loop with sums (each block adds its sums once)
@@ -104,7 +104,7 @@ class ReturnOp:
 
 @dataclass
 class GemmOp:
-    g: Gemm
+    g: object                  # Gemm | GemmT
 
 
 class FuncLower:
@@ -149,16 +149,15 @@ class FuncLower:
 
     @staticmethod
     def _parallel(loop: For, f: Func, T: Types) -> bool:
-        """The planner's verdict on a loop of f (live-out scalars: every scalar the loop assigns
-        that is read anywhere else in the function, a superset of what the planner computes)."""
-        inside = {id(t) for t in walk_stmts([loop])}
-        outside = set()
-        for s in walk_stmts(f.body):
-            if id(s) in inside:
-                continue
-            for e in stmt_exprs(s):
-                outside |= _reads_of(e)
-        pl, _ = classify(loop, T, outside, set())
+        """The planner's verdict on a top-level loop of f: its live-out scalars are those it
+        assigns that the statements after it may read before assigning them."""
+        from .analysis import _assigned, _upward_exposed
+        pos = next((j for j, x in enumerate(f.body) if x is loop), None)
+        if pos is None:
+            return False
+        cont = f.body[pos + 1:]
+        live = {n for n in _assigned(loop.body) if _upward_exposed(cont, n)}
+        pl, _ = classify(loop, T, live, set())
         return pl is not None
 
     def _contracted(self, f: Func, arg_types, precision) -> Func:
@@ -299,7 +298,7 @@ class FuncLower:
                 ops.append(SerialOp(list(cur), pred))
                 cur.clear()
         for s in stmts:
-            if isinstance(s, Gemm):
+            if isinstance(s, (Gemm, GemmT)):
                 if not top or pred:
                     raise LowerError(f"{self.f.name}: a matrix product below the top level")
                 flush()
@@ -1252,7 +1251,10 @@ class FuncGen:
             elif isinstance(op, ReturnOp):
                 self.serial([], op.pred, op.value)
             elif isinstance(op, GemmOp):
-                self.gemm(op.g)
+                if isinstance(op.g, GemmT):
+                    self.gemm_tab(op.g)
+                else:
+                    self.gemm(op.g)
             elif isinstance(op, AllocOp):
                 hctx = HostCtx(fl, self.hlv)
                 et = 8 if fl.arrays[op.name] == "i" or fl.fty == "double" else 4
@@ -1350,6 +1352,40 @@ class FuncGen:
                    f"return _fail(_e, \"matrix product {n} into {g.out}\");")
         self.hind -= 1
         self.hemit("}")
+        self.hind -= 1
+        self.hemit("}")
+
+    def gemm_tab(self, g: GemmT) -> None:
+        """Host code of a table-addressed product (contract.py's table form) on the matrix
+        cores (stade_lowered::gemm_tab)."""
+        fl = self.fl
+        hctx = HostCtx(fl, self.hlv)
+        self.uses_gemm = True
+        n = self.ngemm
+        self.ngemm += 1
+        dim = lambda d: (f"stade_lowered::TabDim{{a.A_{cname(d.table)}, 0}}" if d.table is not None
+                         else f"stade_lowered::TabDim{{nullptr, (long)({hctx.ex(d.stride)})}}")
+        self.hemit("{")
+        self.hind += 1
+        self.hemit(f"const int64_t _gm = {hctx.ex(g.M)}, _gn = {hctx.ex(g.N)}, _gk = {hctx.ex(g.K)};")
+        self.hemit(f"if (_gm > 0x7fffffff || _gn > 0x7fffffff || _gk > 0x7fffffff) "
+                   f"return _fail(hipErrorInvalidValue, \"matrix product {n} into {g.out}: a dimension past 2^31\");")
+        self.hemit("stade_lowered::GemmTabArgs _g{};")
+        self.hemit(f"_g.A = a.A_{cname(g.a)} + ({hctx.ex(g.a_off)});")
+        self.hemit(f"_g.ar = {dim(g.ar)};")
+        self.hemit(f"_g.ak = {dim(g.ak)};")
+        self.hemit(f"_g.B = a.A_{cname(g.b)} + ({hctx.ex(g.b_off)});")
+        self.hemit(f"_g.bk = {dim(g.bk)};")
+        self.hemit(f"_g.bc = {dim(g.bc)};")
+        self.hemit(f"_g.C = a.A_{cname(g.out)} + ({hctx.ex(g.out_off)});")
+        self.hemit(f"_g.ro = {dim(g.ro)};")
+        self.hemit(f"_g.co = {dim(g.co)};")
+        self.hemit("_g.M = (int)_gm;")
+        self.hemit("_g.N = (int)_gn;")
+        self.hemit("_g.K = (int)_gk;")
+        tf = lambda b: "true" if b else "false"
+        self.hemit(f"if ((_e = stade_lowered::gemm_tab<{g.mode}, {tf(g.a_km)}, {tf(g.b_km)}>(_g, stream)) != hipSuccess) "
+                   f"return _fail(_e, \"matrix product {n} into {g.out}\");")
         self.hind -= 1
         self.hemit("}")
 
@@ -1635,6 +1671,10 @@ def describe(ops, depth=0) -> list[str]:
             out.append(pad + f"allocate {op.name}")
         elif isinstance(op, ReturnOp):
             out.append(pad + "return")
+        elif isinstance(op, GemmOp) and isinstance(op.g, GemmT):
+            g = op.g
+            out.append(pad + f"matrix product into {g.out} ({('stored', 'added', 'added atomically')[g.mode]}; "
+                       f"{g.a} x {g.b}, offset tables)")
         elif isinstance(op, GemmOp):
             g = op.g
             out.append(pad + f"matrix product into {g.out} ({'added' if g.acc else 'stored'}; "

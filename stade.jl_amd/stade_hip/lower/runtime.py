@@ -41,9 +41,12 @@ _cache: dict[str, "LoweredLib"] = {}
 def _src_key(src: str) -> str:
     # the flags without the include directory's absolute path: the key (and so the library's
     # file name) must not depend on where the tree sits, or a copied tree would rebuild
-    # (the device runtime header is part of the source)
+    # (the device runtime header is part of the source, and so are the matrix-product headers
+    # where the source includes them)
     flags = " ".join(f for f in FLAGS[1:] if f != str(CSRC))
     rt = (CSRC / "lowered_rt.hpp").read_text()
+    if '#include "lowered_gemm.hpp"' in src:
+        rt += (CSRC / "lowered_gemm.hpp").read_text() + (CSRC / "gemm_f32.hpp").read_text()
     return hashlib.sha256((src + flags + rt).encode()).hexdigest()[:16]
 
 

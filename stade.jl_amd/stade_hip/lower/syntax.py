@@ -163,6 +163,41 @@ class Gemm:
 
 
 @dataclass
+class TabDim:
+    """An offset along one dimension of a GemmT operand: table[i] (a local Int64 array of
+    0-based element offsets) or, with no table, i * stride."""
+    table: str | None
+    stride: object
+
+
+@dataclass
+class GemmT:
+    """A table-addressed product the general lowering makes of a contraction whose factors are
+    gathers (contract.py), not Julia text:
+    out[out_off + ro(m) + co(n)] (+)= sum_{k < K} a[a_off + ar(m) + ak(k)] * b[b_off + bk(k) + bc(n)]
+    for m < M, n < N (0-based); mode 0 stores, 1 adds, 2 adds atomically (elements that
+    several (m, n) share)."""
+    out: str
+    out_off: object
+    ro: TabDim
+    co: TabDim
+    mode: int
+    M: object
+    N: object
+    K: object
+    a: str
+    a_off: object
+    ar: TabDim
+    ak: TabDim
+    b: str
+    b_off: object
+    bk: TabDim
+    bc: TabDim
+    a_km: bool = False         # a's k are adjacent in memory (else its rows): how to gather it
+    b_km: bool = False         # b's k are adjacent (else its columns)
+
+
+@dataclass
 class Func:
     name: str
     args: list
@@ -574,6 +609,9 @@ def stmt_exprs(s):
         return [s.value] if s.value is not None else []
     if isinstance(s, ExprStmt):
         return [s.e]
+    if isinstance(s, GemmT):
+        return [s.out_off, s.M, s.N, s.K, s.a_off, s.b_off] + [d.stride for d in (s.ro, s.co, s.ar, s.ak, s.bk, s.bc)
+                                                                if d.table is None]
     if isinstance(s, Gemm):
         out = [s.out_off, s.out_sm, s.out_sn, s.M, s.N]
         for g in s.segs:

@@ -2,8 +2,10 @@
 
 The fp32 texts whose dense-layer loops become matrix products on the matrix cores: the MLP
 config's three texts at sizes that are not multiples of the product's 128 x 64 x 16 tiles,
-with inner sums long enough for a K split, and two test texts with the other storage orders
-(row-major weights with an offset into the input; flat loops that run the batch fastest).
+with inner sums long enough for a K split, the conv config's three texts (the table form:
+gathered factors, atomic scatters into the input shadow), and two test texts with the other
+storage orders (row-major weights with an offset into the input; flat loops that run the
+batch fastest).
 Every output against the oracle (the text as written, transpiled to C) to the fp32 bar with
 the truth rule, as for every lowered text; each plan must hold the products."""
 import numpy as np
@@ -49,6 +51,19 @@ def test_contracted_mlp2_ce(mode, size):
     scales = {"w1": g1, "w1d": g1, "w2": g2, "w2d": g2, "b1": 0.1, "b2": 0.1}
     _run(CORPUS / f"mlp2_ce_{mode}.jl", "mlp2_ce", mode, shapes, dict(i_b=B, i_in=I, i_h=H, i_out=O),
          int_arrays=dict(lab=lab), scales=scales)
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("size", [(1, 1, 1, 1, 1), (2, 3, 5, 7, 9), (2, 16, 20, 33, 17), (1, 64, 64, 40, 70)])
+def test_contracted_conv3x3(mode, size):
+    """The table form: both factors gathered through offset tables, the input shadow added
+    atomically (its elements take several taps' products)."""
+    N, C, K, H, W = size
+    sz = dict(loss=1, xp=(W + 2) * (H + 2) * C * N, w=9 * C * K, out=W * H * K * N)
+    shapes = {k + s: v for k, v in sz.items() for s in ("", "b", "d", "bd")}
+    s = 1.0 / np.sqrt(9.0 * C)
+    _run(CORPUS / f"conv3x3_{mode}.jl", "conv3x3", mode, shapes, dict(i_nb=N, i_c=C, i_k=K, i_h=H, i_w=W),
+         scales={"w": s, "wd": s})
 
 
 @pytest.mark.parametrize("text", ["dense_rm", "dense_bf"])

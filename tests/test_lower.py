@@ -85,7 +85,8 @@ PLANS = {
     # (the dense layers' sums and scatters as matrix products around the loops: contract.py)
     ("mlp2_ce_b", "mlp2_ce_b"): [("idx", "h1", "owned"), ("idx", "b1b", "atomic"), ("gemm", "w1b", "added"),
                                  ("gemm", "xb", "added"), ("gemm", "h1b", "added")],
-    ("conv3x3_b", "conv3x3_b"): [("idx", "out", "owned"), ("idx", "wb", "atomic"), ("idx", "xpb", "atomic")],
+    ("conv3x3_b", "conv3x3_b"): [("idx", "out", "owned"), ("gemm", "wb", "added atomically"),
+                                 ("gemm", "xpb", "added atomically")],
     ("generic/binsum_b", "binsum_b"): [("i", "c", "atomic"), ("i", "vb", "owned")],
     ("generic/window1d_b", "window1d_b"): [("i", "wb", "atomic"), ("i", "inpb", "atomic"), ("i", "outb", "owned")],
     ("generic/matvec_scatter_b", "matvec_scatter_b"): [("idx", "y", "atomic"), ("idx", "ab", "owned"), ("idx", "xb", "atomic")],

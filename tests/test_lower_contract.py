@@ -76,6 +76,34 @@ def test_mlp_texts_contract_and_agree(mode):
     assert rec["adjoint"] == {"b": 2, "d": 0, "hv": 2}[mode]
 
 
+CONV = dict(i_nb=2, i_c=2, i_k=3, i_h=3, i_w=4)
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+def test_conv_texts_contract_by_tables_and_agree(mode):
+    """The convolution's loops run over a four-digit flat index (x, y, output channel,
+    sample) with a three-digit tap index: the table form, whose products gather both factors
+    through offset tables and add into the input shadow atomically."""
+    from oracle import runner
+    path = CORPUS / f"conv3x3_{mode}.jl"
+    lib = runner.load(path)
+    fname = f"conv3x3_{mode}"
+    N, C, K, H, W = (CONV[k] for k in ("i_nb", "i_c", "i_k", "i_h", "i_w"))
+    base = dict(loss=1, xp=(W + 2) * (H + 2) * C * N, w=9 * C * K, out=W * H * K * N)
+    shapes = {k + s: v for k, v in base.items() for s in ("", "b", "d", "bd")}
+    args = make_args(lib, fname, shapes, CONV, {}, f"contract-{fname}", np.float64)
+    fl = _equivalent(path.read_text(), fname, [v for _, _, v in args])
+    rec = fl.contract_rec
+    assert rec["forward"] == 1 and rec["adjoint"] == {"b": 1, "d": 0, "hv": 1}[mode]
+    plan = fl_plan(fl)
+    assert "offset tables" in plan and ("added atomically" in plan) == (mode != "d")
+
+
+def fl_plan(fl) -> str:
+    from stade_hip.lower import hipgen
+    return " | ".join(hipgen.describe(fl.ops))
+
+
 def test_f64_and_checked_texts_are_not_contracted():
     text = (CORPUS / "mlp2_ce_b.jl").read_text()
     assert not _lower(text, "mlp2_ce_b", "f64").contract_rec
@@ -111,8 +139,8 @@ def test_other_layouts_contract_and_agree(text):
     ("        sb = y[(i_s - 1) * i_h + i_j] * 2.0\n", "        sb = y[(i_s - 1) * i_h + i_j] * 2.0 + xb[1]\n"),
     # a factor is written in the loop
     ("        y[idx] = s\n", "        y[idx] = s\n        w[idx] = 0.0\n"),
-    # a stride that is not 1 in either direction
-    ("w[(i_j - 1) * i_in + i_k] * x", "w[(i_j - 1) * i_in * 2 + i_k * 2 - 1] * x"),
+    # an offset that does not split into a part of the outer loop and a part of the inner one
+    ("w[(i_j - 1) * i_in + i_k] * x", "w[(i_j - 1) * i_k + i_k] * x"),
 ])
 def test_loops_that_are_not_contractions_stay(change):
     old, new = change
@@ -121,6 +149,17 @@ def test_loops_that_are_not_contractions_stay(change):
     fl = _lower(text, "dense_b")
     rec = fl.contract_rec or {"forward": 0, "adjoint": 0}
     assert rec["forward"] + rec["adjoint"] == 1, rec    # the other loop of the pair still is
+
+
+def test_strides_other_than_one_take_the_table_form():
+    """No unit stride in either direction: not the strided form, but the table form's gathers
+    (the forward loop's products through offset tables), agreeing with the text."""
+    text = ROWMAJOR.replace("w[(i_j - 1) * i_in + i_k] * x", "w[(i_j - 1) * i_in * 2 + i_k * 2 - 1] * x")
+    b, i, h = 3, 5, 4
+    args = _dense_args(b, i, h)
+    args[3] = np.random.default_rng(3).standard_normal(2 * h * i)
+    fl = _equivalent(text, "dense_b", args)
+    assert fl.contract_rec["forward"] == 1 and "offset tables" in fl_plan(fl)
 
 
 def test_planted_layout_mistake_is_caught(monkeypatch):
@@ -135,3 +174,27 @@ def test_planted_layout_mistake_is_caught(monkeypatch):
     monkeypatch.setattr(contract._Rewriter, "layout", staticmethod(flipped))
     with pytest.raises((AssertionError, IndexError, ValueError)):
         _equivalent(ROWMAJOR, "dense_b", _dense_args(b=3, i=5, h=5, pad=0))
+
+
+def test_planted_table_mistake_is_caught(monkeypatch):
+    """A table form that places a digit one step off (d P_d instead of (d - 1) P_d, a plausible
+    slip in the mixed radix) reads or writes the wrong elements: the decimal comparison fails."""
+    from stade_hip.lower import contract
+    from oracle import runner
+    real = contract._Tables.place
+
+    def shifted(self, D):
+        p = real(self, D)
+        for d in D[:1]:
+            for m, c in d.P.items():
+                p[m] = p.get(m, 0) + c
+        return {m: c for m, c in p.items() if c}
+    monkeypatch.setattr(contract._Tables, "place", shifted)
+    path = CORPUS / "conv3x3_b.jl"
+    lib = runner.load(path)
+    N, C, K, H, W = (CONV[k] for k in ("i_nb", "i_c", "i_k", "i_h", "i_w"))
+    base = dict(loss=1, xp=(W + 2) * (H + 2) * C * N, w=9 * C * K, out=W * H * K * N)
+    shapes = {k + s: v for k, v in base.items() for s in ("", "b", "d", "bd")}
+    args = make_args(lib, "conv3x3_b", shapes, CONV, {}, "contract-planted", np.float64)
+    with pytest.raises((AssertionError, IndexError, ValueError)):
+        _equivalent(path.read_text(), "conv3x3_b", [v for _, _, v in args])

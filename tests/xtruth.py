@@ -472,7 +472,49 @@ class _Compiler:
             return lambda env: (f(env), None)[1]
         if isinstance(s, S.Gemm):
             return self.gemm(s)
+        if isinstance(s, S.GemmT):
+            return self.gemm_tab(s)
         raise NotImplementedError(type(s).__name__)
+
+    def gemm_tab(self, s):
+        """A table-addressed product of the lowering by its definition (every offset through
+        its table or stride; an address outside an array, or an unset element, raises)."""
+        ex = self.expr
+        head = [ex(e) for e in (s.out_off, s.M, s.N, s.K, s.a_off, s.b_off)]
+        dims = [(d.table, ex(d.stride) if d.table is None else None) for d in (s.ro, s.co, s.ar, s.ak, s.bk, s.bc)]
+
+        def elem(arr, k, nm):
+            if k < 0 or k >= len(arr.data):
+                raise IndexError(f"matrix product: {nm}[{k}] outside an array of {len(arr.data)}")
+            v = arr.data[k]
+            if v is None:
+                raise ValueError(f"matrix product: read of an unset element of {nm}")
+            return v
+
+        def gemm(env):
+            c0, M, N, K, a0, b0 = (f(env) for f in head)
+
+            def at(d):
+                tab, st = d
+                if tab is None:
+                    sv = st(env)
+                    return lambda i: i * sv
+                arr = env[tab]
+                return lambda i: int(elem(arr, i, tab))
+            ro, co, ar, ak, bk, bc = (at(d) for d in dims)
+            A, B, C = env[s.a], env[s.b], env[s.out]
+            akv = [ak(k) for k in range(K)]
+            bkv = [bk(k) for k in range(K)]
+            for m in range(M):
+                am = a0 + ar(m)
+                for n in range(N):
+                    bn = b0 + bc(n)
+                    t = Decimal(0)
+                    for k in range(K):
+                        t = _add(t, _mul(elem(A, am + akv[k], s.a), elem(B, bkv[k] + bn, s.b)))
+                    ic = c0 + ro(m) + co(n)
+                    C.data[ic] = t if s.mode == 0 else _add(elem(C, ic, s.out), t)
+        return gemm
 
     def gemm(self, s):
         """A matrix product of the lowering (stade_hip.lower.contract) by its definition:
