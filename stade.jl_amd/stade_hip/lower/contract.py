@@ -268,6 +268,28 @@ def digits_of(loop: For, T: Types, host_ints: set) -> list | None:
     return out if _freeze(cur) == _freeze(tp) else None
 
 
+def _rename_expr(e, ren: dict):
+    if isinstance(e, Ref):
+        return Ref(ren.get(e.name, e.name), tuple(_rename_expr(x, ren) for x in e.idx))
+    if isinstance(e, Bin):
+        return Bin(e.op, _rename_expr(e.a, ren), _rename_expr(e.b, ren))
+    if isinstance(e, Un):
+        return Un(e.op, _rename_expr(e.a, ren))
+    if isinstance(e, Call):
+        return Call(e.fn, tuple(_rename_expr(x, ren) for x in e.args))
+    return e
+
+
+def _rename_refs(st, ren: dict) -> None:
+    """Rename the arrays `ren` maps in the references of a statement and its nested ones, in
+    place (the statements keep their identity)."""
+    for x in walk_stmts([st]):
+        if isinstance(x, Assign):
+            x.rhs = _rename_expr(x.rhs, ren)
+            if isinstance(x.lhs, Ref):
+                x.lhs = _rename_expr(x.lhs, ren)
+
+
 BIG = 1 << 30      # the run of a digit whose range is an argument (taken as long)
 
 
@@ -876,7 +898,56 @@ class _Rewriter:
                 self.rec["loops"].append(s.var)
                 continue
             body.append(s)
+        body = self.reuse(body)
         return Func(self.f.name, self.f.args, self._allocs + body, self.f.annot)
+
+    def reuse(self, body: list) -> list:
+        """A forward product computed again with operands unchanged since (the adjoint's
+        backward loop recomputes the forward sums): the later loop reads the first product's
+        sums, and the second product and its scratch go."""
+        groups, j = [], 0
+        while j < len(body):     # runs of products into one scratch sums array, first one storing
+            g = body[j]
+            if isinstance(g, Gemm) and g.out.startswith("__gemm_T") and not g.acc:
+                k = j + 1
+                while k < len(body) and isinstance(body[k], Gemm) and body[k].out == g.out:
+                    k += 1
+                groups.append((j, k))
+                j = k
+            else:
+                j += 1
+        if len(groups) < 2:
+            return body
+        sig = lambda g: repr((g.acc, g.M, g.N, g.out_off, g.out_sm, g.out_sn, g.segs))
+        drop, rename, avail = set(), {}, {}
+        starts = {a: b for a, b in groups}
+        j = 0
+        while j < len(body):
+            if j in starts:
+                run = body[j:starts[j]]
+                key = tuple(sig(g) for g in run)
+                reads = {x for g in run for sg in g.segs for x in (sg.a, sg.b)}
+                if key in avail:
+                    rename[run[0].out] = avail[key][0]
+                    drop |= set(range(j, starts[j]))
+                else:
+                    avail[key] = (run[0].out, reads)
+                j = starts[j]
+                continue
+            written = self.written_in([body[j]]) | ({body[j].out} if isinstance(body[j], (Gemm, GemmT)) else set())
+            avail = {k: v for k, v in avail.items() if not (v[1] & written)}
+            j += 1
+        if not rename:
+            return body
+        out = []
+        for j, st in enumerate(body):
+            if j in drop or (isinstance(st, Assign) and isinstance(st.lhs, Var) and st.lhs.name in rename):
+                continue
+            _rename_refs(st, rename)
+            out.append(st)
+        self.rec["gemms"] -= len(drop)
+        self.rec["reused"] = len(rename)
+        return out
 
 
 def transform(f: Func, T: Types, is_parallel, retype, host_ints: set | None = None) -> tuple[Func, dict, Types]:

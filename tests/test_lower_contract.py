@@ -74,6 +74,8 @@ def test_mlp_texts_contract_and_agree(mode):
     # s1), and the two adjoint scatters
     assert rec["forward"] == {"b": 3, "d": 2, "hv": 3}[mode]
     assert rec["adjoint"] == {"b": 2, "d": 0, "hv": 2}[mode]
+    # the backward loop's recomputed forward sums read the forward loop's products
+    assert rec.get("reused", 0) == {"b": 1, "d": 0, "hv": 2}[mode]
 
 
 CONV = dict(i_nb=2, i_c=2, i_k=3, i_h=3, i_w=4)
@@ -198,3 +200,38 @@ def test_planted_table_mistake_is_caught(monkeypatch):
     args = make_args(lib, "conv3x3_b", shapes, CONV, {}, "contract-planted", np.float64)
     with pytest.raises((AssertionError, IndexError, ValueError)):
         _equivalent(path.read_text(), "conv3x3_b", [v for _, _, v in args])
+
+
+TWICE = """function twice_b(y, y2, x, w, i_b, i_in, i_h)
+    for idx = 1:i_b * i_h
+        i_s = div(idx - 1, i_h) + 1
+        i_j = mod(idx - 1, i_h) + 1
+        s = 0.0
+        for i_k = 1:i_in
+            s = s + w[(i_k - 1) * i_h + i_j] * x[(i_s - 1) * i_in + i_k]
+        end
+        y[idx] = s
+    end
+    BETWEEN
+    for idx = 1:i_b * i_h
+        i_s = div(idx - 1, i_h) + 1
+        i_j = mod(idx - 1, i_h) + 1
+        s = 1.0
+        for i_k = 1:i_in
+            s = s + w[(i_k - 1) * i_h + i_j] * x[(i_s - 1) * i_in + i_k]
+        end
+        y2[idx] = tanh(s)
+    end
+    return nothing
+end
+"""
+
+
+@pytest.mark.parametrize("between,reused", [("", 1), ("w[1] = w[1] * 2.0", 0), ("y[1] = 0.0", 1)])
+def test_a_repeated_product_is_reused_only_while_its_operands_stand(between, reused):
+    text = TWICE.replace("BETWEEN", between)
+    r = np.random.default_rng(5)
+    b, i, h = 3, 5, 4
+    args = [np.zeros(b * h), np.zeros(b * h), r.standard_normal(b * i), r.standard_normal(h * i), b, i, h]
+    fl = _equivalent(text, "twice_b", args)
+    assert fl.contract_rec.get("reused", 0) == reused

@@ -46,9 +46,9 @@ def plan_tracer(fl) -> xtruth.Tracer:
     return xtruth.Tracer(par)
 
 
-def check_ownership(text: str, fname: str, args) -> xtruth.Tracer:
+def check_ownership(text: str, fname: str, args, precision: str = "f64") -> xtruth.Tracer:
     from stade_hip.lower import hipgen
-    fl = hipgen.lower_function(text, fname)
+    fl = hipgen.lower_function(text, fname, precision=precision)
     tr = plan_tracer(fl)
     xtruth.run_func(fl.f, [v.copy() if isinstance(v, np.ndarray) else v for v in args], tracer=tr)
     return tr
@@ -123,6 +123,23 @@ def test_config_and_generic_plans_own_what_they_write(name, mode):
     shapes["__stacks__"] = names
     args = make_args(lib, fname, shapes, ints, scalars, f"own-{fname}", np.float64, int_arrays=ia)
     tr = check_ownership(path.read_text(), fname, [v for _, _, v in args] + stacks)
+    assert tr.loops_checked > 0
+    assert not tr.violations, tr.violations[:5]
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("name", ["mlp2_ce", "conv3x3"])
+def test_contracted_plans_own_what_they_write(name, mode):
+    """The fp32 plans, whose dense-layer loops became matrix products (contract.py): the loops
+    that remain (and the loops that fill the products' offset tables) write only what they own."""
+    from oracle import runner
+    ints, base, scalars, ia = CONFIG_CASES[name]
+    path = CORPUS / f"{name}_{mode}.jl"
+    lib = runner.load(path)
+    fname = f"{name}_{mode}"
+    shapes = {k + s: v for k, v in base.items() for s in ("", "b", "d", "bd")}
+    args = make_args(lib, fname, shapes, ints, scalars, f"own32-{fname}", np.float64, int_arrays=ia)
+    tr = check_ownership(path.read_text(), fname, [v for _, _, v in args], precision="f32")
     assert tr.loops_checked > 0
     assert not tr.violations, tr.violations[:5]
 
