@@ -90,6 +90,22 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
+// The lanes-over-iterations form: lane l of every wave holds a partial of the same outer
+// iteration, each wave over a share of the inner loop; the block's NW partials of a lane,
+// added in wave order through `lds` (NW x 64 slots), in every wave.  Every thread of the
+// block must call it.
+template <int NW, class T>
+__device__ __forceinline__ T xwave_sum(T v, T* lds) {
+    const int ln = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    lds[wv * 64 + ln] = v;
+    __syncthreads();
+    T s = lds[ln];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) s += lds[w * 64 + ln];
+    __syncthreads();  // (the slots are reused by the next call)
+    return s;
+}
+
 __device__ __forceinline__ void atomic_add(double* p, double v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add(int64_t* p, int64_t v) {
@@ -107,6 +123,7 @@ enum : int {
     ST_BLOCK_ADD = 4,    // block_add calls that added a nonzero block total
     ST_ROW_BLOCK = 5,    // blocks of a flat loop's row-block twin
     ST_COL_BLOCK = 6,    // blocks of a flat loop's column-block twin
+    ST_XSPLIT_BLOCK = 7, // blocks of the lanes-over-iterations form (waves share the inner loops)
     ST_N = 8,
 };
 

@@ -101,8 +101,8 @@ class LoweredLib:
         CUDA tensor of at least 8 elements, added to, never cleared) until called with None.
         Slots: 0 wave-aggregated atomics (one per wave), 1 per-lane atomics (one per wave), 2
         blocks of an LDS-privatised variant, 3 blocks of the wave-per-iteration form, 4 block
-        sums added, 5 blocks of a flat loop's row-block twin, 6 of its column-block twin
-        (`csrc/lowered_rt.hpp`, ST_*).  A test hook: the calls of the generated
+        sums added, 5 blocks of a flat loop's row-block twin, 6 of its column-block twin, 7
+        blocks of the lanes-over-iterations form (`csrc/lowered_rt.hpp`, ST_*).  A test hook: the calls of the generated
         function are unchanged."""
         f = getattr(self.lib, f"stade_hip_gen_{hipgen.cname(name)}_set_stats")
         f.restype = None

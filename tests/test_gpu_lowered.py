@@ -191,9 +191,9 @@ def _paths(case, low, fname):
     finally:
         low.set_stats(fname, None)
     c = st.cpu().tolist()
-    print(f"{case.label}: paths agg={c[0]} lane={c[1]} priv={c[2]} split={c[3]} block={c[4]} row={c[5]} col={c[6]}",
-          flush=True)
-    return dict(agg=c[0], lane=c[1], priv=c[2], split=c[3], block=c[4], row=c[5], col=c[6])
+    print(f"{case.label}: paths agg={c[0]} lane={c[1]} priv={c[2]} split={c[3]} block={c[4]} row={c[5]} col={c[6]}"
+          f" xsplit={c[7]}", flush=True)
+    return dict(agg=c[0], lane=c[1], priv=c[2], split=c[3], block=c[4], row=c[5], col=c[6], xsplit=c[7])
 
 
 def _matvec_b(m, n):
@@ -258,6 +258,27 @@ def test_paths_narrow_output_form():
     p = _paths(case, low, "window1d_d")
     assert p["split"] > 0
 
+
+
+@pytest.mark.parametrize("mode", ["b", "d", "hv"])
+@pytest.mark.parametrize("mn", [(1000, 1024), (64, 257), (130, 700), (256, 300)])
+def test_lowered_affine_lanes_over_rows(mode, mn):
+    """A column-major matrix updated by rows (the affine adjoint's and HVP's row loops, whose
+    inner loops accumulate into wb): the lanes take 64 consecutive rows and the block's 16 waves
+    share each row's inner loop, the rows' sums combined in wave order; rows past the range
+    (1000 and 130 are not multiples of 64) compute a row again and store nothing.  The row sums
+    alone (the tangent's loop reads the matrix, updates nothing along it) keep the
+    wave-per-row form.  Every output against the oracle; the forms' blocks ran."""
+    m, n = mn
+    shapes = {k: (m, n) for k in ("w", "wb", "wd", "wbd")}
+    shapes.update({k: n for k in ("x", "xb", "xd", "xbd")})
+    shapes.update({k: m for k in ("b", "bb", "bd", "bbd", "t", "tb", "td", "tbd", "r", "rb", "rd", "rbd")})
+    shapes.update({k: 1 for k in ("loss", "lossb", "lossd", "lossbd")})
+    case, low = _case(CORPUS / f"affine_lsq_{mode}.jl", "affine_lsq", mode, shapes, dict(i_m=m, i_n=n),
+                      label=f"xsplit affine_lsq_{mode} {m}x{n}")
+    p = _paths(case, low, f"affine_lsq_{mode}")
+    assert p["split"] > 0
+    assert (p["xsplit"] > 0) == (mode != "d")
 
 
 # ---- flat loops: the row-block and column-block twins ------------------------------------

@@ -416,3 +416,15 @@ def test_no_twin_unless_the_sites_agree(change):
     text = (GENERIC / "flatmv.jl").read_text().replace("y[i] = y[i] + a[idx] * x[j]", change)
     _, sigs = hipgen.generate(text)
     assert sigs["flatmv"]["twins"] == []
+
+
+@pytest.mark.parametrize("name,expect", [("affine_lsq_b", ["i_i"]), ("affine_lsq_hv", ["i_i"]), ("affine_lsq_d", []),
+                                         ("generic/window1d_b", []), ("generic/matvec_scatter_b", [])])
+def test_lanes_over_rows_for_column_major_updates(name, expect):
+    """The lanes-over-iterations form is chosen for a shared inner loop whose accumulations
+    step along the outer loop with stride 1 and along their own index with a larger stride (the
+    affine adjoint's wb[i, j]), not for loops that only read along the outer loop (the affine
+    tangent's row sums) nor for updates along their own index (a window's taps)."""
+    from stade_hip.lower import hipgen
+    _, sigs = hipgen.generate((CORPUS / f"{name}.jl").read_text(), "f64")
+    assert sigs[name.split("/")[-1]]["xsplit"] == expect
