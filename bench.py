@@ -168,6 +168,9 @@ class Diffusion(Workload):
     tangent / HVP direction ud ~ N(0,1) from the next seed."""
     family = "diffusion2d"
     dtype = "f64"
+    # the steps as replays of a captured HIP graph, as a caller looping over evaluations would
+    # issue them: 2-5 % faster than eager launches (the evaluation is two or three launches)
+    graph_steps = 10
 
     def __init__(self, mode="b", n=4096):
         super().__init__(mode)
@@ -370,6 +373,7 @@ class Mlp(Workload):
     family = "mlp2_ce"
     dtype = "f32"
     bound = "mfma"
+    graph_steps = 10   # (replayed graphs, as for diffusion: 1-4 % faster than eager launches)
 
     def __init__(self, mode="b", B=4096, I=784, H=1024, O=10):
         super().__init__(mode)
@@ -428,6 +432,7 @@ class Conv(Workload):
     family = "conv3x3"
     dtype = "f32"
     bound = "mfma"
+    graph_steps = 10   # (replayed graphs, as for diffusion: about 1 % faster than eager launches)
 
     def __init__(self, mode="b", N=8, C=64, K=64, H=256, W=256):
         super().__init__(mode)
