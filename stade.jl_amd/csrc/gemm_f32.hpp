@@ -199,6 +199,13 @@ template <class E, class = void>
 struct has_atomic : std::false_type {};
 template <class E>
 struct has_atomic<E, std::void_t<decltype(E::kAtomic)>> : std::integral_constant<bool, E::kAtomic> {};
+// an epilogue whose load(m, n) depends on m only (a bias per row) declares
+// `static constexpr bool kRowLoad = true`: the block reads its rows' values before the main
+// loop, so that their latency is hidden under the products
+template <class E, class = void>
+struct has_row_load : std::false_type {};
+template <class E>
+struct has_row_load<E, std::void_t<decltype(E::kRowLoad)>> : std::integral_constant<bool, E::kRowLoad> {};
 
 template <int... U, class F>
 __device__ __forceinline__ void unroll_seq(std::integer_sequence<int, U...>, F&& f) {
@@ -319,6 +326,16 @@ __device__ __forceinline__ void gemm_block(const Args& g, bool vec, const Epi& e
             store_tile<B_KM, BNT>(sb[rs][o], Bs[buf][o]);
         }
     };
+    // the epilogue's per-row values, read now when they depend on the row only (kRowLoad)
+    using Pre = decltype(epi.load(0, 0));
+    Pre prow[2] = {};
+    if constexpr (has_row_load<Epi>::value) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int m = m0 + wm + i * 32 + (lane & 31);
+            if (m < g.M) prow[i] = epi.load(m, 0);
+        }
+    }
     auto mainloop = [&](auto fast_tag) {
         constexpr bool FAST = decltype(fast_tag)::value;
         if (t_begin >= t_end) return;
@@ -454,7 +471,6 @@ __device__ __forceinline__ void gemm_block(const Args& g, bool vec, const Epi& e
     // the epilogue's inputs (e.g. C of C += v) for the whole tile first, then the stores: the
     // output may alias them as far as the compiler knows, and interleaving would serialise one
     // memory round trip per element
-    using Pre = decltype(epi.load(0, 0));
     Pre pre[2][NJ][16];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -464,7 +480,10 @@ __device__ __forceinline__ void gemm_block(const Args& g, bool vec, const Epi& e
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm + i * 32 + (lane & 31);
                 const int n = n0 + wn + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                pre[i][j][r] = (m < g.M && n < g.N) ? epi.load(m, n) : Pre{};
+                if constexpr (has_row_load<Epi>::value)
+                    pre[i][j][r] = prow[i];
+                else
+                    pre[i][j][r] = (m < g.M && n < g.N) ? epi.load(m, n) : Pre{};
             }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
