@@ -12,12 +12,17 @@
 //   the hardware, as the generated adjoint's `@atomic` leaves it.
 //   block_add: a value a thread has summed in a register over its iterations (a loop's sum
 //   into a scalar, or into an array element whose index does not change over the loop: the
-//   reference's hoisted atomic), added once per block.
+//   reference's hoisted atomic), added once per block (the row-block twin's rows).
+//   block_part + fold_parts: the same block sums in a loop's one-thread-per-iteration grid,
+//   stored per block and added in block order by a one-block kernel after the loop.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
+
+#include <cstring>
+#include <mutex>
 
 namespace stade_lowered {
 
@@ -120,7 +125,7 @@ enum : int {
     ST_WAVE_LANE = 1,    // wave_add calls that made one atomic per lane
     ST_PRIV_BLOCK = 2,   // blocks that accumulated into an LDS-privatised copy
     ST_SPLIT_BLOCK = 3,  // blocks of the wave-per-iteration (narrow-output) form
-    ST_BLOCK_ADD = 4,    // block_add calls that added a nonzero block total
+    ST_BLOCK_ADD = 4,    // block sums (block_add, block_part) that were nonzero
     ST_ROW_BLOCK = 5,    // blocks of a flat loop's row-block twin
     ST_COL_BLOCK = 6,    // blocks of a flat loop's column-block twin
     ST_XSPLIT_BLOCK = 7, // blocks of the lanes-over-iterations form (waves share the inner loops)
@@ -173,6 +178,47 @@ __device__ __forceinline__ void block_add(T* p, T v, T* lds, unsigned long long*
     __syncthreads();
 }
 
+// The block's sum of its threads' values (a loop's sum into a scalar, or its accumulations
+// into one array element whose index does not change over the loop), stored by thread 0 into
+// slots[blockIdx.x]: no atomic.  A one-block fold launched after the loop (fold_parts) adds
+// the launch's slots in block order into the target, so that the sum's order is fixed and no
+// address takes one atomic per block (thousands of same-address device atomics serialise).
+// Every thread of the block must call it.
+template <class T>
+__device__ __forceinline__ void block_part(T* slots, T v, T* lds, unsigned long long* st) {
+    v = wave_sum(v);
+    const int nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        T s = lds[0];
+        for (int w = 1; w < nw; ++w) s += lds[w];
+        slots[blockIdx.x] = s;
+        if (s != (T)0) count(st, ST_BLOCK_ADD);
+    }
+    __syncthreads();
+}
+
+// The fold: the first nb slots, each thread its stride of them, then the waves' sums in wave
+// order; the total is returned to thread 0 (the other threads get 0).  Every thread of the
+// block must call it.
+template <class T>
+__device__ __forceinline__ T fold_parts(const T* slots, unsigned nb, T* lds) {
+    T s = 0;
+    for (unsigned b = threadIdx.x; b < nb; b += blockDim.x) s += slots[b];
+    s = wave_sum(s);
+    const int nw = blockDim.x >> 6;
+    __syncthreads();  // (the slots of lds are reused by the next call)
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = s;
+    __syncthreads();
+    T t = 0;
+    if (threadIdx.x == 0) {
+        t = lds[0];
+        for (int w = 1; w < nw; ++w) t += lds[w];
+    }
+    return t;
+}
+
 // LDS-privatised accumulation: the block's copy, then one global atomic per nonzero element
 template <class T>
 __device__ __forceinline__ void lds_add(T* p, T v) {
@@ -181,5 +227,141 @@ __device__ __forceinline__ void lds_add(T* p, T v) {
 __device__ __forceinline__ void lds_add(int64_t* p, int64_t v) {
     atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
 }
+
+// ------------------------------------------------------------------------------------------
+// Host side: replays of a lowered function's launch sequence as a HIP graph.
+//
+// The host part of a generated function reads and writes nothing but its frame `a` (array
+// pointers and sizes, scalar arguments, host loop variables, its local arrays' addresses), and
+// its kernels take `a` by value, so two calls whose frames are byte-identical issue the same
+// launches with the same arguments.  A function with host loops (a time loop: thousands of
+// small dependent launches, each paying the host's launch cost) runs a frame by direct
+// launches the first time it sees it; when the same frame comes back (same device, arrays,
+// sizes and scalars), its sequence is captured once, on a private stream, into a HIP graph,
+// which that call and every later call with that frame launch onto the caller's stream.  A
+// few frames are kept (the least recently used is dropped); every graph is dropped when one of
+// the function's local arrays is reallocated, since the graphs hold its old address.  A frame
+// whose capture fails runs by direct launches from then on.  The lock is recursive: a direct
+// run (under it) that reallocates a local array drops the graphs through clear().
+// ------------------------------------------------------------------------------------------
+template <class A>
+class LaunchGraphs {
+  public:
+    using Fn = int32_t (*)(A, hipStream_t);
+
+    int32_t run(const A& a, hipStream_t stream, Fn fn) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) {
+            (void)hipGetLastError();
+            return fn(a, stream);
+        }
+        std::lock_guard<std::recursive_mutex> lk(mu_);
+        ++tick_;
+        Slot* s = find(a, dev);
+        if (!s) {
+            s = oldest();
+            drop(*s);
+            std::memcpy(&s->key, &a, sizeof(A));
+            s->dev = dev;
+            s->used = true;
+            s->tick = tick_;
+            return fn(a, stream);
+        }
+        s->tick = tick_;
+        if (!s->exec && !s->failed) capture(*s, a, fn, dev);
+        if (s->exec) {
+            if (hipGraphLaunch(s->exec, stream) == hipSuccess) {
+                ++replays_;
+                return 0;
+            }
+            (void)hipGetLastError();
+            drop(*s);
+            s->failed = true;
+        }
+        return fn(a, stream);
+    }
+
+    // every graph dropped (the caller has synchronised the device)
+    void clear() {
+        std::lock_guard<std::recursive_mutex> lk(mu_);
+        for (Slot& s : slots_) {
+            drop(s);
+            s.used = false;
+        }
+    }
+
+    void counts(int64_t* out) const {
+        out[0] = captures_;
+        out[1] = replays_;
+    }
+
+  private:
+    static constexpr int kSlots = 4, kDevices = 64;
+    struct Slot {
+        A key;
+        int dev;
+        bool used, failed;
+        hipGraphExec_t exec;
+        unsigned long long tick;
+    };
+    Slot slots_[kSlots] = {};
+    hipStream_t cap_[kDevices] = {};
+    std::recursive_mutex mu_;
+    unsigned long long tick_ = 0;
+    int64_t captures_ = 0, replays_ = 0;
+
+    Slot* find(const A& a, int dev) {
+        for (Slot& s : slots_)
+            if (s.used && s.dev == dev && std::memcmp(&s.key, &a, sizeof(A)) == 0) return &s;
+        return nullptr;
+    }
+    Slot* oldest() {
+        Slot* o = &slots_[0];
+        for (Slot& s : slots_) {
+            if (!s.used) return &s;
+            if (s.tick < o->tick) o = &s;
+        }
+        return o;
+    }
+    void drop(Slot& s) {
+        if (s.exec) {
+            // a launch of the graph may still run: the exec is destroyed after the device is idle
+            (void)hipDeviceSynchronize();
+            (void)hipGraphExecDestroy(s.exec);
+            s.exec = nullptr;
+        }
+        s.failed = false;
+    }
+    void capture(Slot& s, const A& a, Fn fn, int dev) {
+        s.failed = true;
+        if (!cap_[dev] && hipStreamCreateWithFlags(&cap_[dev], hipStreamNonBlocking) != hipSuccess) {
+            cap_[dev] = nullptr;
+            (void)hipGetLastError();
+            return;
+        }
+        if (hipStreamBeginCapture(cap_[dev], hipStreamCaptureModeThreadLocal) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        const int32_t rc = fn(a, cap_[dev]);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(cap_[dev], &g);
+        if (rc != 0 || e != hipSuccess || !g) {
+            if (g) (void)hipGraphDestroy(g);
+            (void)hipGetLastError();
+            return;
+        }
+        hipGraphExec_t x = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ei != hipSuccess || !x) {
+            (void)hipGetLastError();
+            return;
+        }
+        s.exec = x;
+        s.failed = false;
+        ++captures_;
+    }
+};
 
 }  // namespace stade_lowered

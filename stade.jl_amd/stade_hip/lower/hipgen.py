@@ -36,7 +36,7 @@ from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, F
                      Nothing_, Num, Range, Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
 MAX_BLOCKS = 8192          # grid of a parallel loop whose trip count the host cannot evaluate
-RED_MAX_BLOCKS = 2048      # at most, for a loop with sums (each block adds its sums once)
+FOLD_MIN_BLOCKS = 256      # a loop's block sums: atomics up to this many blocks, a fold kernel above
 PRIV_MAX_BYTES = 48 * 1024  # LDS-privatised accumulation target, at most
 PRIV_RATIO = 32            # and at least this many iterations per target element
 TWIN_MIN_N = 256           # flat twins: rows of at least this many iterations (`row_block`, `col_block`
@@ -1099,20 +1099,56 @@ class FuncGen:
             out.append(f"            if (lds_priv[_j] != ({et_of(n)})0) stade_lowered::atomic_add(&a.A_{cname(n)}[_j], lds_priv[_j]);")
             out.append("        if (threadIdx.x == 0) stade_lowered::count(a.st, stade_lowered::ST_PRIV_BLOCK);")
             out.append("    }")
-        # the block's sums: one atomic addition per block
+        # the block's sums: with few blocks one atomic addition per block; with more, stored per
+        # block (no atomics) and added in block order into their targets by the one-block fold
+        # kernel k<k>f that the host then launches after this one (same-address atomics
+        # serialise: thousands of them cost more than a launch)
+        parts = []   # (C type, slot array, register, the fold's addition of its total `_s`, target)
         for n, r in reds.items():
-            out.append(f"    stade_lowered::block_add(&fr.v_{cname(n)}, {r}, reinterpret_cast<{fl.cty(fl.scalars[n])}*>(_blk), a.st);")
+            parts.append((fl.cty(fl.scalars[n]), f"g_p{k}_{len(parts)}", r, f"fr.v_{cname(n)} += _s;",
+                          f"&fr.v_{cname(n)}"))
         for n, r in hoist.items():
-            ref = pl.arrays[n].index
-            out.append(f"    {{ const int64_t _i = {Ctx(fl, dict(locals_), hl).lin(ref)};")
+            ix = Ctx(fl, dict(locals_), hl).lin(pl.arrays[n].index)
+            add = (f"a.A_{cname(n)}[_i] += _s;" if fl.inbounds else
+                   f"if ((uint64_t)_i < (uint64_t)a.N_{cname(n)}) a.A_{cname(n)}[_i] += _s;")
             tgt = (f"&a.A_{cname(n)}[_i]" if fl.inbounds else
                    f"(uint64_t)_i < (uint64_t)a.N_{cname(n)} ? &a.A_{cname(n)}[_i] : nullptr")
-            out.append(f"      stade_lowered::block_add({tgt}, {r}, reinterpret_cast<{et_of(n)}*>(_blk), a.st); }}")
+            parts.append((et_of(n), f"g_p{k}_{len(parts)}", r, f"{{ const int64_t _i = {ix}; {add} }}",
+                          (ix, tgt)))
+        if parts:
+            out.append(f"    if (gridDim.x <= {FOLD_MIN_BLOCKS}) {{")
+            for ct, arr, r, _, tgt in parts:
+                if isinstance(tgt, tuple):
+                    out.append(f"        {{ const int64_t _i = {tgt[0]};")
+                    out.append(f"          stade_lowered::block_add({tgt[1]}, {r}, reinterpret_cast<{ct}*>(_blk), a.st); }}")
+                else:
+                    out.append(f"        stade_lowered::block_add({tgt}, {r}, reinterpret_cast<{ct}*>(_blk), a.st);")
+            out.append("    } else {")
+            for ct, arr, r, _, _ in parts:
+                self.kern.append(f"__device__ {ct} {arr}[{MAX_BLOCKS}];   // k{k}'s block sums (at most {MAX_BLOCKS} blocks)\n")
+                out.append(f"        stade_lowered::block_part({arr}, {r}, reinterpret_cast<{ct}*>(_blk), a.st);")
+            out.append("    }")
         pre = "    extern __shared__ __align__(16) unsigned char lds_raw[];\n    (void)lds_raw;\n" if cands else ""
-        if reds or hoist:
-            pre += "    __shared__ double _blk[16];  // the waves' sums of block_add\n"
+        if parts:
+            pre += "    __shared__ double _blk[16];  // the waves' sums of block_part\n"
         self.kern.append(f"template <int PRIV>\n__global__ __launch_bounds__(256) void k{k}(const Args a) {{\n" + pre +
                          "\n".join(out) + "\n}\n")
+        if parts:
+            fo = list(head)
+            # (a failed index condition ran the loop in order on one thread, which added its sums)
+            fo.append(f"    if (!({guards})) return;")
+            for ct, arr, r, add, _ in parts:
+                fo.append(f"    {{ const {ct} _s = stade_lowered::fold_parts({arr}, _nb, reinterpret_cast<{ct}*>(_blk));")
+                fo.append(f"      if (threadIdx.x == 0 && _s != ({ct})0) {add} }}")
+            self.kern.append(f"__global__ __launch_bounds__(256) void k{k}f(const Args a, const unsigned _nb) {{\n"
+                             "    __shared__ double _blk[16];\n" + "\n".join(fo) + "\n}\n")
+
+        def fold(nb):
+            if parts:
+                self.hemit(f"if ({nb} > {FOLD_MIN_BLOCKS}) {{")
+                self.hemit(f"    k{k}f<<<1, 256, 0, stream>>>(a, {nb});")
+                self.hemit(f"    if ((_e = hipGetLastError()) != hipSuccess) return _fail(_e, \"k{k}f\");")
+                self.hemit("}")
         # the lanes-over-iterations variant of the narrow-output form, for inner loops whose
         # accesses run along the outer loop (a column-major matrix read by rows)
         xsplit = bool(split) and os.environ.get("STADE_LOWER_XSPLIT", "1") != "0" and self.xsplit_ok(pl, split)
@@ -1229,8 +1265,7 @@ class FuncGen:
                 self.hemit("} else")
             self.hemit("if (_trip > 0) {")
             self.hind += 1
-            cap = RED_MAX_BLOCKS if (reds or hoist) else MAX_BLOCKS
-            self.hemit(f"const unsigned _g = (unsigned)std::min<int64_t>((_trip + 255) / 256, {cap});")
+            self.hemit(f"const unsigned _g = (unsigned)std::min<int64_t>((_trip + 255) / 256, {MAX_BLOCKS});")
             if cands:
                 self.hemit("int _priv = 0;")
                 self.hemit("size_t _lds = 0;")
@@ -1249,12 +1284,14 @@ class FuncGen:
                 self.hemit("}")
             else:
                 self.launch(f"k{k}", "_g", "256", "0", "<0>")
+            fold("_g")
             self.hind -= 1
             self.hemit("}")
             self.hind -= 1
             self.hemit("}")
         else:
             self.launch(f"k{k}", str(MAX_BLOCKS), "256", "0", "<0>")
+            fold(f"{MAX_BLOCKS}u")
         if pl.live_out:
             kc = self.nk
             self.nk += 1
@@ -1582,11 +1619,14 @@ class FuncGen:
             *self.kern,
             f"static void* g_buf[{nb}];",
             f"static size_t g_bytes[{nb}];",
+            "// the launch sequences replayed as HIP graphs (functions with host loops; lowered_rt.hpp)",
+            "static LaunchGraphs<Args> g_graphs;",
             "// local arrays (allocated inside the generated function): kept per process, grown on demand",
+            "// (a reallocation drops the captured graphs, which hold the old address)",
             "static void* _buf(int slot, size_t bytes) {",
             "    if (bytes == 0) bytes = 8;   // an empty array still gets an address (nothing reads it)",
             "    if (g_bytes[slot] < bytes) {",
-            "        if (g_buf[slot]) { (void)hipDeviceSynchronize(); (void)hipFree(g_buf[slot]); g_buf[slot] = nullptr; g_bytes[slot] = 0; }",
+            "        if (g_buf[slot]) { (void)hipDeviceSynchronize(); g_graphs.clear(); (void)hipFree(g_buf[slot]); g_buf[slot] = nullptr; g_bytes[slot] = 0; }",
             "        if (hipMalloc(&g_buf[slot], bytes) != hipSuccess) return nullptr;",
             "        g_bytes[slot] = bytes;",
             "    }",
@@ -1594,6 +1634,15 @@ class FuncGen:
             "}",
             "// where the kernels count their accumulation paths (stade_lowered::ST_*; null: nowhere)",
             "static unsigned long long* g_stats = nullptr;",
+            "// the function's launches in order on `stream` (the caller's, or a private stream under",
+            "// capture): the host statements read and write nothing but the frame `a`",
+            "static int32_t _launches(Args a, hipStream_t stream) {",
+            "    hipError_t _e;",
+            "    kinit<<<1, 1, 0, stream>>>(a);",
+            "    if ((_e = hipGetLastError()) != hipSuccess) return _fail(_e, \"kinit\");",
+            *self.host,
+            "    return 0;",
+            "}",
             "}  // namespace",
             "",
             "// Test hook, not part of the generated function's ABI: until it is called again with null,",
@@ -1601,16 +1650,22 @@ class FuncGen:
             f"extern \"C\" void stade_hip_gen_{cname(f.name)}_set_stats(unsigned long long* stats) {{",
             f"    {self.ns}::g_stats = stats;",
             "}",
+            "// Test hook: the launch sequences captured into graphs so far, and the graph launches.",
+            f"extern \"C\" void stade_hip_gen_{cname(f.name)}_graphs(int64_t* out) {{",
+            f"    {self.ns}::g_graphs.counts(out);",
+            "}",
             "",
             f"extern \"C\" int32_t stade_hip_gen_{cname(f.name)}({', '.join(params)}) {{",
             f"    using namespace {self.ns};",
-            "    Args a{};",
+            "    Args a;",
+            "    std::memset(&a, 0, sizeof a);   // (padding too: frames are compared bytewise)",
             "    a.st = g_stats;",
             *fill,
+            # a host loop issues its launches once per iteration: replayed as a graph when the
+            # same frame comes back
+            f"    const int32_t _rc = {'g_graphs.run(a, stream, _launches)' if fl.nhl else '_launches(a, stream)'};",
+            "    if (_rc != 0) return _rc;",
             "    hipError_t _e;",
-            "    kinit<<<1, 1, 0, stream>>>(a);",
-            "    if ((_e = hipGetLastError()) != hipSuccess) return _fail(_e, \"kinit\");",
-            *self.host,
             "    Frame h;",
             "    if ((_e = hipMemcpyFromSymbolAsync(&h, HIP_SYMBOL(fr), sizeof(Frame), 0, hipMemcpyDeviceToHost, stream)) != hipSuccess)",
             "        return _fail(_e, \"returned values\");",

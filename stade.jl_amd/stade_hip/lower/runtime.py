@@ -116,6 +116,18 @@ class LoweredLib:
             raise ValueError("counters must be a contiguous int64 CUDA tensor of at least 8 elements")
         f(ctypes.c_void_p(counters.data_ptr()))
 
+    def graphs(self, name: str) -> tuple[int, int]:
+        """(launch sequences of function `name` captured into HIP graphs, graph launches) so far
+        in this process.  A function with host loops replays its launches as a graph when a
+        call repeats an earlier call's frame (device, array addresses, sizes and scalars alike;
+        `csrc/lowered_rt.hpp`, LaunchGraphs).  A test hook."""
+        f = getattr(self.lib, f"stade_hip_gen_{hipgen.cname(name)}_graphs")
+        f.restype = None
+        f.argtypes = [ctypes.c_void_p]
+        out = (ctypes.c_int64 * 2)()
+        f(ctypes.cast(out, ctypes.c_void_p))
+        return int(out[0]), int(out[1])
+
     def _fn(self, name):
         if name not in self._fns:
             f = getattr(self.lib, f"stade_hip_gen_{hipgen.cname(name)}")

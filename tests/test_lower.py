@@ -116,6 +116,22 @@ def test_burgers_time_loop_stays_on_the_host_with_a_device_guard():
     assert sigs["burgers1d_b"]["args"][-2] == ("branch_stack", "Ai", 1)
 
 
+@pytest.mark.parametrize("name, replayed", [("burgers1d_b", True), ("burgers1d_d", True), ("diffusion2d_b", False)])
+def test_host_loops_replay_as_graphs(name, replayed):
+    """A function with host loops runs its launch sequence through the graph cache (replayed
+    when a frame repeats); one without issues its launches directly.  Either way the sequence
+    sits in one function of the frame alone, and a reallocated local array drops the graphs."""
+    from stade_hip.lower import hipgen
+    src, _ = hipgen.generate((CORPUS / f"{name}.jl").read_text())
+    body = src[src.index(f"extern \"C\" int32_t stade_hip_gen_{name}("):]
+    body = body[:body.index("\n}\n")]
+    assert ("g_graphs.run(a, stream, _launches)" in body) == replayed
+    assert ("_launches(a, stream);" in body) == (not replayed)
+    assert "<<<" not in body                     # every launch is in _launches
+    assert "std::memset(&a, 0, sizeof a)" in body
+    assert "g_graphs.clear();" in src
+
+
 def test_initstacks_on_the_host_matches_the_oracle():
     from stade_hip.lower import initstacks
     from oracle import runner
