@@ -13,8 +13,9 @@
 //   block_add: a value a thread has summed in a register over its iterations (a loop's sum
 //   into a scalar, or into an array element whose index does not change over the loop: the
 //   reference's hoisted atomic), added once per block (the row-block twin's rows).
-//   block_part + fold_parts: the same block sums in a loop's one-thread-per-iteration grid,
-//   stored per block and added in block order by a one-block kernel after the loop.
+//   block_part + fold_load / fold_sum: the same block sums in a loop's one-thread-per-
+//   iteration grid, stored per block and added in a fixed order by a one-block kernel after
+//   the loop.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -26,7 +27,15 @@
 
 namespace stade_lowered {
 
+// (an argument within one period of [0, b) -- a periodic neighbour's index, `mod(i - 2, n)` with
+// i in 1:n -- by compares and an add, the reference's mod-reduced form (`cgen_mod_reduce_body`
+// /root/reference/src/STADE.jl:8126-8169) taken at run time; the division otherwise)
 __device__ __forceinline__ int64_t jl_mod(int64_t a, int64_t b) {
+    if (b > 0) {
+        if (a >= 0 && a < b) return a;
+        if (a < 0 && a >= -b) return a + b;
+        if (a >= b && a - b < b) return a - b;
+    }
     int64_t r = a % b;
     return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r;
 }
@@ -180,7 +189,7 @@ __device__ __forceinline__ void block_add(T* p, T v, T* lds, unsigned long long*
 
 // The block's sum of its threads' values (a loop's sum into a scalar, or its accumulations
 // into one array element whose index does not change over the loop), stored by thread 0 into
-// slots[blockIdx.x]: no atomic.  A one-block fold launched after the loop (fold_parts) adds
+// slots[blockIdx.x]: no atomic.  A one-block fold launched after the loop (fold_load, fold_sum) adds
 // the launch's slots in block order into the target, so that the sum's order is fixed and no
 // address takes one atomic per block (thousands of same-address device atomics serialise).
 // Every thread of the block must call it.
@@ -199,13 +208,23 @@ __device__ __forceinline__ void block_part(T* slots, T v, T* lds, unsigned long 
     __syncthreads();
 }
 
-// The fold: the first nb slots, each thread its stride of them, then the waves' sums in wave
-// order; the total is returned to thread 0 (the other threads get 0).  Every thread of the
-// block must call it.
+// The fold, run by one block of FOLD_NT threads: fold_load issues the loads of a thread's
+// slots (b = threadIdx.x + u FOLD_NT, zero past nb) all at once, so that a fold costs one
+// memory round trip whatever nb; fold_sum adds them in a fixed tree, then the waves' sums in
+// wave order, and returns the total to thread 0 (the other threads get 0).  Every thread of the
+// block must call fold_sum.
+constexpr int FOLD_NT = 1024, FOLD_PER = 8;  // at most FOLD_NT x FOLD_PER = 8192 slots
 template <class T>
-__device__ __forceinline__ T fold_parts(const T* slots, unsigned nb, T* lds) {
-    T s = 0;
-    for (unsigned b = threadIdx.x; b < nb; b += blockDim.x) s += slots[b];
+__device__ __forceinline__ void fold_load(const T* slots, unsigned nb, T (&v)[FOLD_PER]) {
+#pragma unroll
+    for (int u = 0; u < FOLD_PER; ++u) {
+        const unsigned b = threadIdx.x + (unsigned)u * FOLD_NT;
+        v[u] = b < nb ? slots[b] : (T)0;
+    }
+}
+template <class T>
+__device__ __forceinline__ T fold_sum(const T (&v)[FOLD_PER], T* lds) {
+    T s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
     s = wave_sum(s);
     const int nw = blockDim.x >> 6;
     __syncthreads();  // (the slots of lds are reused by the next call)

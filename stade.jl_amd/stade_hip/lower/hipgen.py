@@ -36,6 +36,7 @@ from .syntax import (Alloc, Assign, Bin, Break, Call, Continue, ExprStmt, For, F
                      Nothing_, Num, Range, Ref, Return, Tup, Un, Var, While, stmt_exprs, sub_blocks, walk_expr, walk_stmts)
 
 MAX_BLOCKS = 8192          # grid of a parallel loop whose trip count the host cannot evaluate
+                           # (and at most the fold's slots: FOLD_NT x FOLD_PER in lowered_rt.hpp)
 FOLD_MIN_BLOCKS = 256      # a loop's block sums: atomics up to this many blocks, a fold kernel above
 PRIV_MAX_BYTES = 48 * 1024  # LDS-privatised accumulation target, at most
 PRIV_RATIO = 32            # and at least this many iterations per target element
@@ -1137,16 +1138,20 @@ class FuncGen:
             fo = list(head)
             # (a failed index condition ran the loop in order on one thread, which added its sums)
             fo.append(f"    if (!({guards})) return;")
-            for ct, arr, r, add, _ in parts:
-                fo.append(f"    {{ const {ct} _s = stade_lowered::fold_parts({arr}, _nb, reinterpret_cast<{ct}*>(_blk));")
+            # every slot's load in flight at once, then the sums
+            for c, (ct, arr, r, add, _) in enumerate(parts):
+                fo.append(f"    {ct} _v{c}[stade_lowered::FOLD_PER];")
+                fo.append(f"    stade_lowered::fold_load({arr}, _nb, _v{c});")
+            for c, (ct, arr, r, add, _) in enumerate(parts):
+                fo.append(f"    {{ const {ct} _s = stade_lowered::fold_sum(_v{c}, reinterpret_cast<{ct}*>(_blk));")
                 fo.append(f"      if (threadIdx.x == 0 && _s != ({ct})0) {add} }}")
-            self.kern.append(f"__global__ __launch_bounds__(256) void k{k}f(const Args a, const unsigned _nb) {{\n"
+            self.kern.append(f"__global__ __launch_bounds__(stade_lowered::FOLD_NT) void k{k}f(const Args a, const unsigned _nb) {{\n"
                              "    __shared__ double _blk[16];\n" + "\n".join(fo) + "\n}\n")
 
         def fold(nb):
             if parts:
                 self.hemit(f"if ({nb} > {FOLD_MIN_BLOCKS}) {{")
-                self.hemit(f"    k{k}f<<<1, 256, 0, stream>>>(a, {nb});")
+                self.hemit(f"    k{k}f<<<1, stade_lowered::FOLD_NT, 0, stream>>>(a, {nb});")
                 self.hemit(f"    if ((_e = hipGetLastError()) != hipSuccess) return _fail(_e, \"k{k}f\");")
                 self.hemit("}")
         # the lanes-over-iterations variant of the narrow-output form, for inner loops whose
