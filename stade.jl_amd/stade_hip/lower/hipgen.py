@@ -123,6 +123,13 @@ class FuncLower:
         # (gather.py); STADE_LOWER_GATHER=0 keeps every loop as written
         if os.environ.get("STADE_LOWER_GATHER", "1") != "0":
             f = Func(f.name, f.args, gather.transform(f.body), f.annot)
+            # the owner's replayed terms add into its one element: merged as the finishing pass
+            # merges the text's own (`stade_gpu` finishes after planning too), so that an
+            # iteration loads and stores the element once
+            if merge_accum:
+                cnt = [0]
+                f = Func(f.name, f.args, finish.merge_accum(f.body, cnt), f.annot)
+                self.finish_rec["merged_gathered"] = cnt[0]
         self.f = f
         self.precision = precision
         self.T: Types = infer_types(f, arg_types, precision)

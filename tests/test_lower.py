@@ -324,6 +324,21 @@ def test_periodic_scatter_becomes_a_gather():
     assert "ub:atomic" not in plan.split("host loop over i_t")[2], plan
 
 
+def test_gathered_terms_merge_into_one_update():
+    """The owner's four replayed neighbour terms and its own term add into ub[i_x]: merged
+    into one update per iteration (four merges), one load and one store of the element."""
+    from stade_hip.lower import hipgen
+    src, sigs = hipgen.generate((CORPUS / "burgers1d_b.jl").read_text())
+    assert sigs["burgers1d_b"]["finish"]["merged_gathered"] == 4
+    fl = hipgen.lower_function((CORPUS / "burgers1d_b.jl").read_text(), "burgers1d_b")
+    from stade_hip.lower.syntax import Assign, For, Ref, walk_stmts
+    loops = [s for s in walk_stmts(fl.f.body) if isinstance(s, For) and s.var == "i_x"]
+    rev = [L for L in loops if any(isinstance(t, Assign) and isinstance(t.lhs, Ref) and t.lhs.name == "ub"
+                                   for t in L.body)]
+    assert rev and all(sum(1 for t in L.body if isinstance(t, Assign) and isinstance(t.lhs, Ref) and t.lhs.name == "ub")
+                       == 1 for L in rev), rev
+
+
 _SCATTER = """function s_b(x, xb, y, yb, n)
     for i = 1:n
         ip = mod(i, n) + 1
