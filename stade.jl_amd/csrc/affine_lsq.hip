@@ -26,9 +26,13 @@ namespace stade {
 namespace {
 
 constexpr int RT = 64, CT = 64, CW = 16, NT = 256;  // rows per tile, columns per tile, columns per wave
-constexpr int kMaxChunks = 16;                      // row-sum partials per row
-
 enum Mode { ADJ = 0, TAN = 1, HVP = 2 };
+// the column kernel's columns per wave and per block (4 waves)
+template <int M>
+constexpr int cols_cw() { return M == HVP ? 8 : CW; }
+template <int M>
+constexpr int cols_ct() { return 4 * cols_cw<M>(); }
+constexpr int kMaxChunks = 16;                      // row-sum partials per row
 
 template <int M>
 __global__ __launch_bounds__(NT) void rows_kernel(const double* __restrict__ w, const double* __restrict__ wd,
@@ -179,7 +183,10 @@ __global__ __launch_bounds__(BT) void finish_kernel(FinishArgs a, double* partia
 // The adjoint forms with n > 0.  Every block recomputes the row values of its 64 rows from
 // the chunk partials (r, then sb = rb + (2 r / 2) lossb with rb as staged by rows_kernel),
 // and the blocks of column chunk 0 also write r, bb, tb (and the tangents) and the row
-// tile's loss partials.
+// tile's loss partials.  A wave takes cols_cw<M>() columns: 16 for the adjoint, 8 for the
+// HVP, whose six streams of a column (w, wd, wb, wbd, x, xd) would otherwise hold 192
+// registers a lane (two blocks a CU instead of one: 12-17 % faster from 2048^2 up, the
+// same at 1024^2; the adjoint with 8 was within 3 % either way).
 template <int M>
 __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, const double* __restrict__ wd,
                                                   double* __restrict__ wb, double* __restrict__ wbd,
@@ -187,18 +194,19 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
                                                   const double* __restrict__ RBc, const double* __restrict__ RBdc,
                                                   double* __restrict__ XP, double* __restrict__ XPd, int m, int n,
                                                   double* __restrict__ partials) {
+    constexpr int CWC = cols_cw<M>();
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     // row tiles along x: blocks dispatched together stream consecutive segments of the same
     // columns (measured 6-20 % faster at 4096^2-8192^2 than column tiles along x)
     const int rtile = blockIdx.x, i = rtile * RT + lane;
-    const int j0 = blockIdx.y * CT + wv * CW;
+    const int j0 = blockIdx.y * cols_ct<M>() + wv * CWC;
     const bool live = i < m;
     const int ic = min(i, m - 1);
     // every read of the wave's 16 columns (w, wb, x and the tangents) issued before any use or
     // store: clamped and unconditional, with dead rows and columns masked afterwards
-    double wv_[CW], wbv_[CW], xv_[CW], wdv_[CW], wbdv_[CW], xdv_[CW];
+    double wv_[CWC], wbv_[CWC], xv_[CWC], wdv_[CWC], wbdv_[CWC], xdv_[CWC];
 #pragma unroll
-    for (int jj = 0; jj < CW; ++jj) {
+    for (int jj = 0; jj < CWC; ++jj) {
         const int jc = min(j0 + jj, n - 1);
         const size_t g = (size_t)jc * m + ic;
         wv_[jj] = w[g];
@@ -246,9 +254,9 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    double cx[CW], cxd[CW];
+    double cx[CWC], cxd[CWC];
 #pragma unroll
-    for (int jj = 0; jj < CW; ++jj) {
+    for (int jj = 0; jj < CWC; ++jj) {
         const bool ok = live && j0 + jj < n;
         const size_t g = (size_t)(j0 + jj) * m + i;
         const double xj = xv_[jj], wij = wv_[jj];
@@ -261,13 +269,13 @@ __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, 
     }
     // column sums over the tile's rows (DPP wave sums), all 16 columns at once
 #pragma unroll
-    for (int jj = 0; jj < CW; ++jj) {
+    for (int jj = 0; jj < CWC; ++jj) {
         cx[jj] = wave_sum(cx[jj]);
         if (M == HVP) cxd[jj] = wave_sum(cxd[jj]);
     }
     if (lane == 0) {
 #pragma unroll
-        for (int jj = 0; jj < CW; ++jj) {
+        for (int jj = 0; jj < CWC; ++jj) {
             if (j0 + jj >= n) continue;
             XP[(size_t)rtile * n + j0 + jj] = cx[jj];
             if (M == HVP) XPd[(size_t)rtile * n + j0 + jj] = cxd[jj];
@@ -406,6 +414,12 @@ template <int M>
 int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double* wbd, const double* x, const double* xd,
             double* xb, double* xbd, int64_t m, int64_t n, hipStream_t stream) {
     if (m == 0) return STADE_HIP_OK;
+    // the column kernel's tiles along its grid's y dimension (checked before any device work;
+    // the adjoint's 64-column tiles are checked with the other sizes)
+    const int ctiles = (int)((n + cols_ct<M>() - 1) / cols_ct<M>());
+    if (M != TAN && ctiles > 65535)
+        return set_error(STADE_HIP_ERANGE, "stade_hip_affine_lsq_%s: i_n = %lld exceeds 65535 column tiles of %d",
+                         M == HVP ? "hv" : "b", (long long)n, cols_ct<M>());
     WsCall call_(stream);
     Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
@@ -461,7 +475,7 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
         return STADE_HIP_OK;
     }
     STADE_TIMED("affine_cols", stream,
-                cols_kernel<M><<<dim3(mtiles, ntiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, fa, S, Sd, XP, XPd, (int)m, (int)n,
+                cols_kernel<M><<<dim3(mtiles, ctiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, fa, S, Sd, XP, XPd, (int)m, (int)n,
                                                                           ws->partials));
     STADE_LAUNCHED("affine cols_kernel");
     STADE_TIMED("affine_xfinish", stream,

@@ -51,6 +51,11 @@ def test_argument_errors_before_device_work():
     assert rc == -3 and b"65535 row tiles" in L.stade_hip_last_error()
     rc = L.stade_hip_affine_lsq_b(*([null] * 12), ctypes.c_int64(1), ctypes.c_int64(65536 * 64), null)
     assert rc == -3 and b"65535 column tiles" in L.stade_hip_last_error()
+    # the HVP's column kernel takes 32-column tiles: refused past 65535 of them, before any
+    # device work (the pointers are never read)
+    fake = ctypes.c_void_p(256)
+    rc = L.stade_hip_affine_lsq_hv(*([fake] * 12), ctypes.c_int64(1), ctypes.c_int64(65535 * 32 + 1), *([fake] * 12), null)
+    assert rc == -3 and b"65535 column tiles of 32" in L.stade_hip_last_error()
     # zero-trip: n = 0 runs no loop and needs no device
     assert L.stade_hip_diffusion2d_b(null, null, null, null, null, null, 0, null) == 0
     assert L.stade_hip_affine_lsq_d(*([null] * 12), 0, 5, null) == 0
