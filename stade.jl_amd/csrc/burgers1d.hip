@@ -56,7 +56,8 @@ constexpr int kInitBlockCells = NT * 8;  // cells per block of the backward init
 #define STADE_BURG_FC_NOTAPE 4
 #endif
 // forward chunk kernel (register form): threads, owned cells and cells per lane of a block.
-// With a tape to write (adjoint, HVP, checkpoints) 512 / 4096 / 1: against the LDS form it
+// With a tape row to write every step (adjoint, HVP, the checkpoint policy's recomputed
+// segments) 512 / 4096 / 1: against the LDS form it
 // replaced (1024 / 4096), the HVP 3-6 % faster and the adjoint 0-2 %; 1024 / 4096, 256 / 4096
 // and 512 / 2048 measured between the two; two cells a lane (512 / 4032 / 2) halved both
 // rates (its tape stores cover every other element).  The tangent, which writes no tape and is
@@ -65,7 +66,8 @@ constexpr int kInitBlockCells = NT * 8;  // cells per block of the backward init
 // and a lane shifts two values an array a step for four cells; 18 % faster than 512 / 1024 /
 // 1 (one cell a lane, wave 0 computing a third slot the others skip).  Measured at 2^20 cells:
 // 512 / 960 / 2 +9 %, 256 / 448 / 2 +11 %, 128 / 448 / 4 +7 %, 64 / 448 / 8 +7 %, 512 / 1984 /
-// 4 +5 %, 64 / 960 / 16 (137 registers) -15 %.
+// 4 +5 %, 64 / 960 / 16 (137 registers) -15 %.  The checkpoint policy's first sweep, which
+// writes a row every `every` >= KMAX steps (at most one a launch), takes the tangent's form.
 constexpr int BNT = STADE_BURG_FT, BNT_NOTAPE = STADE_BURG_FT_NOTAPE;
 constexpr int FWD_S = STADE_BURG_FS, FWD_C = STADE_BURG_FC;
 constexpr int FWD_S_NOTAPE = STADE_BURG_FS_NOTAPE, FWD_C_NOTAPE = STADE_BURG_FC_NOTAPE;
@@ -696,7 +698,9 @@ template <bool TAN>
 int32_t forward(const double* src, const double* srcd, double* fin, double* find, double* tape, double* taped, int n,
                 int64_t t_begin, int64_t t_end, const Coef& c, double* P, double* Q, double* Pd, double* Qd, hipStream_t stream,
                 int64_t row0 = 0, int every = 1) {
-    const bool notape = tape == nullptr;
+    // the four-cell form also where the tape is sparse: at most one row a launch (the checkpoint
+    // policy's first sweep, a row every `every` >= KMAX steps)
+    const bool notape = tape == nullptr || every >= KMAX;
     const unsigned nb = grid_for(n, notape ? FWD_S_NOTAPE : FWD_S);
     const double *cs = src, *csd = srcd;
     int64_t t0 = t_begin;
