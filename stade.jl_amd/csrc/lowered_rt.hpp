@@ -120,6 +120,25 @@ __device__ __forceinline__ T xwave_sum(T v, T* lds) {
     return s;
 }
 
+// The same with G outer iterations a block (G = 16, 32 or 64): lane l of wave w takes
+// iteration l % G and share l / G + (64 / G) w of the shared inner loops, so that a block has
+// 64 / G x NW shares.  An iteration's partials: the wave's 64 / G groups added by xor shuffles,
+// then the waves' sums in wave order through `lds` (NW x G slots), in every lane.  With G = 64
+// it is xwave_sum.
+template <int NW, int G, class T>
+__device__ __forceinline__ T xgroup_sum(T v, T* lds) {
+#pragma unroll
+    for (int o = G; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+    const int ln = threadIdx.x & 63, wv = threadIdx.x >> 6, r = ln & (G - 1);
+    if (ln < G) lds[wv * G + r] = v;
+    __syncthreads();
+    T s = lds[r];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) s += lds[w * G + r];
+    __syncthreads();  // (the slots are reused by the next call)
+    return s;
+}
+
 __device__ __forceinline__ void atomic_add(double* p, double v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add(int64_t* p, int64_t v) {
@@ -130,7 +149,7 @@ __device__ __forceinline__ void atomic_add(int64_t* p, int64_t v) {
 // `_set_stats` entry point of a lowered function): a 64-bit counter per accumulation path,
 // counted once per wave or block, so that a test can tell which path a launch took.
 enum : int {
-    ST_WAVE_AGG = 0,     // wave_add calls that made one atomic for the whole wave
+    ST_WAVE_AGG = 0,     // wave_add (group_add) calls that made one atomic for the whole wave (group)
     ST_WAVE_LANE = 1,    // wave_add calls that made one atomic per lane
     ST_PRIV_BLOCK = 2,   // blocks that accumulated into an LDS-privatised copy
     ST_SPLIT_BLOCK = 3,  // blocks of the wave-per-iteration (narrow-output) form
@@ -163,6 +182,39 @@ __device__ __forceinline__ void wave_add(T* p, T v, unsigned long long* st) {
     }
     atomic_add(p, v);
     if (st && (threadIdx.x & 63) == (unsigned)__builtin_ctzll(active)) count(st, ST_WAVE_LANE);
+}
+
+// wave_add for the lanes-over-iterations form with G iterations a block: the lanes of a
+// G-lane group share an inner-loop iteration, and so, typically, an accumulation target (a
+// column's shadow updated by every row).  If the whole wave is active and each group's lanes
+// add into their group's first lane's element, each group's values are summed (xor shuffles)
+// and its first lane makes one atomic addition (counted as aggregated); otherwise each lane
+// adds atomically.  G = 64 is wave_add.
+template <int G, class T>
+__device__ __forceinline__ void group_add(T* p, T v, unsigned long long* st) {
+    if constexpr (G == 64) {
+        wave_add(p, v, st);
+    } else {
+        const uint64_t active = __ballot(1);
+        const int ln = threadIdx.x & 63;
+        if (active == ~0ull) {
+            const uint64_t u = reinterpret_cast<uint64_t>(p);
+            const int g0 = ln & ~(G - 1);
+            const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)u, g0, 64);
+            const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(u >> 32), g0, 64);
+            if (__ballot(u == (((uint64_t)hi << 32) | lo)) == ~0ull) {
+#pragma unroll
+                for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, 64);
+                if ((ln & (G - 1)) == 0) {
+                    atomic_add(p, v);
+                    count(st, ST_WAVE_AGG);
+                }
+                return;
+            }
+        }
+        atomic_add(p, v);
+        if (st && ln == __builtin_ctzll(active)) count(st, ST_WAVE_LANE);
+    }
 }
 
 // One atomic addition per block of the block's values (a loop's sum into a scalar, or its

@@ -45,7 +45,7 @@ TWIN_MIN_ROWS = 64         # defaults of stade_gpu); the column twin at least th
 ROWBLOCK_GRID = 4096       # the row twin splits few rows over several blocks: about this many blocks,
 ROWBLOCK_CHUNK = 2048      # each at least this many iterations of its row (the block's one atomic amortised)
 COLBLOCK_ROWS = 128        # rows of a column-block tile (`cgen_colblock_rows`), 8 row lanes x 32 columns
-XSPLIT_NW = 16             # waves of a block of the lanes-over-iterations form (64 iterations a block)
+XSPLIT_NW = 16             # waves of a block of the lanes-over-iterations form (16 to 64 iterations a block)
 SPLIT_MAX_TRIP = 16384     # a parallel loop with at most this many iterations (64 blocks of 256 threads)
 SPLIT_MIN_INNER = 256      # whose shared inner loop runs at least this many iterations (when the host
 SPLIT_MAX_TRIP_UNKNOWN = 4096  # can evaluate it; otherwise at most this many outer iterations) gives
@@ -589,6 +589,9 @@ class Emitter:
         # them, combined through LDS), whose inactive lanes (`act`) store nothing
         self.share_var, self.share_n, self.xsum = "_lane", "64", None
         self.act = None
+        # the lanes-over-iterations form's iterations a block (a template parameter of its
+        # kernel): accumulations inside shared loops aggregate per lane group (group_add)
+        self.group = None
 
     def one_lane(self) -> bool:
         return self.lane0 and not self.in_split
@@ -655,7 +658,8 @@ class Emitter:
                 if ctx.lds == ref.name:
                     self.emit(f"  {chk}stade_lowered::lds_add(&lds_priv[_i], {val});{els} }}")
                 else:
-                    self.emit(f"  {chk}stade_lowered::wave_add(&a.A_{nm}[_i], {val}, a.st);{els} }}")
+                    add = f"group_add<{self.group}>" if self.group and self.in_split else "wave_add"
+                    self.emit(f"  {chk}stade_lowered::{add}(&a.A_{nm}[_i], {val}, a.st);{els} }}")
                 return
             c, _ = fl.ex(s.rhs, ctx)
             if self.act and self.one_lane():
@@ -1027,9 +1031,10 @@ class FuncGen:
                 em.split_loops = split
                 em.lane0 = True
             if xs:
-                em.share_var, em.share_n = "_wv", str(XSPLIT_NW)
-                em.xsum = lambda part, t: f"stade_lowered::xwave_sum<{XSPLIT_NW}>({part}, {xs_lds[t]})"
+                em.share_var, em.share_n = "_sh", "_nsh"
+                em.xsum = lambda part, t: f"stade_lowered::xgroup_sum<{XSPLIT_NW}, XG>({part}, {xs_lds[t]})"
                 em.act = "_act"
+                em.group = "XG"
             em.ind = 3
             em.emit(f"const int64_t l_{cname(v)} = _lo + _k * _st;")
             for n in priv:
@@ -1186,19 +1191,24 @@ class FuncGen:
             sp.append("        return;")
             sp.append("    }")
             sp += red_decl
+            # XG consecutive outer iterations a block (16, 32 or 64, chosen by the host from the
+            # trip count so that few rows still fill the CUs): lane l of wave w takes iteration
+            # l % XG and share l / XG + (64 / XG) w of the shared inner loops
+            sp.append(f"    constexpr int _nsh = {XSPLIT_NW} * 64 / XG;")
             sp.append("    const int _ln = threadIdx.x & 63, _wv = threadIdx.x >> 6;")
+            sp.append("    const int _r = _ln & (XG - 1), _sh = _ln / XG + (64 / XG) * _wv;")
             sp.append("    if (threadIdx.x == 0) stade_lowered::count(a.st, stade_lowered::ST_XSPLIT_BLOCK);")
-            # block-uniform steps of 64 iterations: every thread reaches the waves' barriers
+            # block-uniform steps of XG iterations: every thread reaches the waves' barriers
             # (a lane past the range computes the last iteration again and stores nothing)
-            sp.append("    for (int64_t _base = (int64_t)blockIdx.x * 64; _base < _trip; _base += (int64_t)gridDim.x * 64) {")
-            sp.append("        const bool _act = _base + _ln < _trip;")
-            sp.append("        const int64_t _k = _act ? _base + _ln : _trip - 1;")
+            sp.append("    for (int64_t _base = (int64_t)blockIdx.x * XG; _base < _trip; _base += (int64_t)gridDim.x * XG) {")
+            sp.append("        const bool _act = _base + _r < _trip;")
+            sp.append("        const int64_t _k = _act ? _base + _r : _trip - 1;")
             sp += body_lines(True, None, wave=True, xs=True)
             sp.append("    }")
             for n, r in reds.items():
                 sp.append(f"    {r} = stade_lowered::wave_sum({r});")
                 sp.append(f"    if (_ln == 0 && {r} != 0) stade_lowered::atomic_add(&fr.v_{cname(n)}, {r});")
-            self.kern.append(f"__global__ __launch_bounds__({64 * XSPLIT_NW}) void k{k}s(const Args a) {{\n"
+            self.kern.append(f"template <int XG>\n__global__ __launch_bounds__({64 * XSPLIT_NW}) void k{k}s(const Args a) {{\n"
                              + "\n".join(pre_x) + "\n" + "\n".join(sp) + "\n}\n")
         if split and not xsplit:
             # the narrow-output form: a wave per iteration, its lanes sharing the inner loops
@@ -1247,8 +1257,18 @@ class FuncGen:
                 self.hemit(f"if ({cond}) {{")
                 self.hind += 1
                 if xsplit:
-                    self.launch(f"k{k}s", f"(unsigned)std::min<int64_t>((_trip + 63) / 64, {MAX_BLOCKS})",
-                                str(64 * XSPLIT_NW), "0")
+                    # rows a block: 64 when that still gives 256 blocks, else 32, else 16 (a
+                    # wave's loads then cover 16 rows of 4 columns: 128-byte segments)
+                    for g, cond in ((64, f"_trip >= {64 * 256}"), (32, f"_trip >= {32 * 256}"), (16, None)):
+                        if cond:
+                            self.hemit(f"if ({cond}) {{")
+                        else:
+                            self.hemit("{")
+                        self.hind += 1
+                        self.launch(f"k{k}s", f"(unsigned)std::min<int64_t>((_trip + {g - 1}) / {g}, {MAX_BLOCKS})",
+                                    str(64 * XSPLIT_NW), "0", f"<{g}>")
+                        self.hind -= 1
+                        self.hemit("} else" if cond else "}")
                 else:
                     self.launch(f"k{k}s", f"(unsigned)std::min<int64_t>((_trip + 3) / 4, {MAX_BLOCKS})", "256", "0")
                 self.hind -= 1

@@ -301,12 +301,14 @@ def test_paths_narrow_output_form():
 
 
 @pytest.mark.parametrize("mode", ["b", "d", "hv"])
-@pytest.mark.parametrize("mn", [(1000, 1024), (64, 257), (130, 700), (256, 300)])
+@pytest.mark.parametrize("mn", [(1000, 1024), (64, 257), (130, 700), (256, 300), (9000, 300), (16384, 260)])
 def test_lowered_affine_lanes_over_rows(mode, mn):
     """A column-major matrix updated by rows (the affine adjoint's and HVP's row loops, whose
-    inner loops accumulate into wb): the lanes take 64 consecutive rows and the block's 16 waves
-    share each row's inner loop, the rows' sums combined in wave order; rows past the range
-    (1000 and 130 are not multiples of 64) compute a row again and store nothing.  The row sums
+    inner loops accumulate into wb): the lanes take 16, 32 or 64 consecutive rows (fewer rows a
+    block when the rows are few: 16 up to 8191 rows, 32 up to 16383, 64 at 16384) and the block's
+    shares of each row's inner loop (64 / rows-a-block per wave, 16 waves) run it in parts,
+    the rows' sums combined in a fixed order; rows past the range (1000, 130 and 9000 are not
+    multiples of the block's rows) compute a row again and store nothing.  The row sums
     alone (the tangent's loop reads the matrix, updates nothing along it) keep the
     wave-per-row form.  Every output against the oracle; the forms' blocks ran."""
     m, n = mn
