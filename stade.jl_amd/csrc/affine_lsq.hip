@@ -27,11 +27,6 @@ namespace {
 
 constexpr int RT = 64, CT = 64, CW = 16, NT = 256;  // rows per tile, columns per tile, columns per wave
 enum Mode { ADJ = 0, TAN = 1, HVP = 2 };
-// the column kernel's columns per wave and per block (4 waves)
-template <int M>
-constexpr int cols_cw() { return M == HVP ? 8 : CW; }
-template <int M>
-constexpr int cols_ct() { return 4 * cols_cw<M>(); }
 constexpr int kMaxChunks = 16;                      // row-sum partials per row
 
 template <int M>
@@ -183,23 +178,24 @@ __global__ __launch_bounds__(BT) void finish_kernel(FinishArgs a, double* partia
 // The adjoint forms with n > 0.  Every block recomputes the row values of its 64 rows from
 // the chunk partials (r, then sb = rb + (2 r / 2) lossb with rb as staged by rows_kernel),
 // and the blocks of column chunk 0 also write r, bb, tb (and the tangents) and the row
-// tile's loss partials.  A wave takes cols_cw<M>() columns: 16 for the adjoint, 8 for the
-// HVP, whose six streams of a column (w, wd, wb, wbd, x, xd) would otherwise hold 192
-// registers a lane (two blocks a CU instead of one: 12-17 % faster from 2048^2 up, the
-// same at 1024^2; the adjoint with 8 was within 3 % either way).
-template <int M>
+// tile's loss partials.  A wave takes CWC columns (8 or 16; a block 4 CWC).  The HVP takes 8:
+// its six streams of a column (w, wd, wb, wbd, x, xd) would otherwise hold 192 registers a
+// lane (two blocks a CU instead of one: 12-17 % faster from 2048^2 up, the same at 1024^2).
+// The adjoint takes 8 up to 2^21 matrix elements, where an evaluation is launch-bound and
+// two blocks a CU overlap one's loads with the other's stores (+4.6 % at 1024^2 by graph
+// replays), and 16 above (2-3 % faster there).
+template <int M, int CWC>
 __global__ __launch_bounds__(NT) void cols_kernel(const double* __restrict__ w, const double* __restrict__ wd,
                                                   double* __restrict__ wb, double* __restrict__ wbd,
                                                   const double* __restrict__ x, const double* __restrict__ xd, FinishArgs fa,
                                                   const double* __restrict__ RBc, const double* __restrict__ RBdc,
                                                   double* __restrict__ XP, double* __restrict__ XPd, int m, int n,
                                                   double* __restrict__ partials) {
-    constexpr int CWC = cols_cw<M>();
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     // row tiles along x: blocks dispatched together stream consecutive segments of the same
     // columns (measured 6-20 % faster at 4096^2-8192^2 than column tiles along x)
     const int rtile = blockIdx.x, i = rtile * RT + lane;
-    const int j0 = blockIdx.y * cols_ct<M>() + wv * CWC;
+    const int j0 = blockIdx.y * (4 * CWC) + wv * CWC;
     const bool live = i < m;
     const int ic = min(i, m - 1);
     // every read of the wave's 16 columns (w, wb, x and the tangents) issued before any use or
@@ -414,12 +410,14 @@ template <int M>
 int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double* wbd, const double* x, const double* xd,
             double* xb, double* xbd, int64_t m, int64_t n, hipStream_t stream) {
     if (m == 0) return STADE_HIP_OK;
-    // the column kernel's tiles along its grid's y dimension (checked before any device work;
-    // the adjoint's 64-column tiles are checked with the other sizes)
-    const int ctiles = (int)((n + cols_ct<M>() - 1) / cols_ct<M>());
+    // the column kernel's columns a wave (8 or 16, above) and its tiles along the grid's y
+    // dimension (checked before any device work; the 64-column tiles with the other sizes)
+    const bool narrow = M == HVP || (m * n <= ((int64_t)1 << 21) && (n + 31) / 32 <= 65535);
+    const int ct = narrow ? 32 : 64;
+    const int ctiles = (int)((n + ct - 1) / ct);
     if (M != TAN && ctiles > 65535)
         return set_error(STADE_HIP_ERANGE, "stade_hip_affine_lsq_%s: i_n = %lld exceeds 65535 column tiles of %d",
-                         M == HVP ? "hv" : "b", (long long)n, cols_ct<M>());
+                         M == HVP ? "hv" : "b", (long long)n, ct);
     WsCall call_(stream);
     Workspace* ws = call_.ws;
     if (!ws) return STADE_HIP_ENOMEM;
@@ -474,9 +472,15 @@ int32_t run(FinishArgs fa, const double* w, const double* wd, double* wb, double
         STADE_LAUNCHED("affine finalize_kernel");
         return STADE_HIP_OK;
     }
-    STADE_TIMED("affine_cols", stream,
-                cols_kernel<M><<<dim3(mtiles, ctiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, fa, S, Sd, XP, XPd, (int)m, (int)n,
-                                                                          ws->partials));
+    if (narrow) {
+        STADE_TIMED("affine_cols", stream,
+                    (cols_kernel<M, 8><<<dim3(mtiles, ctiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, fa, S, Sd, XP, XPd, (int)m,
+                                                                              (int)n, ws->partials)));
+    } else {
+        STADE_TIMED("affine_cols", stream,
+                    (cols_kernel<M, 16><<<dim3(mtiles, ctiles), NT, 0, stream>>>(w, wd, wb, wbd, x, xd, fa, S, Sd, XP, XPd, (int)m,
+                                                                               (int)n, ws->partials)));
+    }
     STADE_LAUNCHED("affine cols_kernel");
     STADE_TIMED("affine_xfinish", stream,
                 xfinish_kernel<M><<<(unsigned)((n + 63) / 64 + 1), 64, 0, stream>>>(xb, xbd, XP, XPd, (int)n, mtiles, ws->partials,
