@@ -1148,6 +1148,13 @@ class FuncGen:
                          "\n".join(out) + "\n}\n")
         if parts:
             fo = list(head)
+            # the loop's last values committed here (when it ran), instead of by a one-thread
+            # kernel of their own; in either form the last iteration left them in `wb`
+            if pl.live_out:
+                fo.append("    if (threadIdx.x == 0 && _trip > 0) {")
+                for n in pl.live_out:
+                    fo.append(f"        fr.v_{cname(n)} = wb.v_{cname(n)};")
+                fo.append("    }")
             # (a failed index condition ran the loop in order on one thread, which added its sums)
             fo.append(f"    if (!({guards})) return;")
             # every slot's load in flight at once, then the sums
@@ -1160,11 +1167,18 @@ class FuncGen:
             self.kern.append(f"__global__ __launch_bounds__(stade_lowered::FOLD_NT) void k{k}f(const Args a, const unsigned _nb) {{\n"
                              "    __shared__ double _blk[16];\n" + "\n".join(fo) + "\n}\n")
 
+        # `_cm<k>`: the fold ran and committed the loop's last values (live_out)
+        commit_in_fold = bool(parts) and bool(pl.live_out)
+        if commit_in_fold:
+            self.hemit(f"bool _cm{k} = false;")
+
         def fold(nb):
             if parts:
                 self.hemit(f"if ({nb} > {FOLD_MIN_BLOCKS}) {{")
                 self.hemit(f"    k{k}f<<<1, stade_lowered::FOLD_NT, 0, stream>>>(a, {nb});")
                 self.hemit(f"    if ((_e = hipGetLastError()) != hipSuccess) return _fail(_e, \"k{k}f\");")
+                if commit_in_fold:
+                    self.hemit(f"    _cm{k} = true;")
                 self.hemit("}")
         # the lanes-over-iterations variant of the narrow-output form, for inner loops whose
         # accesses run along the outer loop (a column-major matrix read by rows)
@@ -1335,7 +1349,14 @@ class FuncGen:
             for n in pl.live_out:
                 lines.append(f"    fr.v_{cname(n)} = wb.v_{cname(n)};")
             self.one_thread_kernel(kc, lines)
-            self.launch(f"k{kc}")
+            if commit_in_fold:
+                self.hemit(f"if (!_cm{k}) {{")
+                self.hind += 1
+                self.launch(f"k{kc}")
+                self.hind -= 1
+                self.hemit("}")
+            else:
+                self.launch(f"k{kc}")
 
     def xsplit_ok(self, pl: ParallelLoop, split: dict) -> bool:
         """The lanes-over-iterations form: every shared inner loop at the top of the body (the

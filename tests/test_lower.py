@@ -132,6 +132,24 @@ def test_host_loops_replay_as_graphs(name, replayed):
     assert "g_graphs.clear();" in src
 
 
+def test_block_sums_fold_and_commit():
+    """The Burgers reverse loop sums into two scalars and leaves `ucb`'s last value: its blocks
+    store their sums in slots (no atomic when the grid is large), and the one-block fold kernel
+    adds them and also commits the last value, so that the one-thread commit kernel runs only
+    when the fold does not."""
+    from stade_hip.lower import hipgen
+    src, _ = hipgen.generate((CORPUS / "burgers1d_b.jl").read_text())
+    fold = src[src.index("void k12f("):]
+    fold = fold[:fold.index("\n}\n")]
+    assert "fold_load(g_p12_0" in fold and "fold_load(g_p12_1" in fold
+    assert "fr.v_ucb = wb.v_ucb;" in fold
+    assert fold.index("fr.v_ucb = wb.v_ucb;") < fold.index("return;\n    double _v0")  # before the guard's return
+    assert "if (_g > 256) {" in src and "_cm12 = true;" in src and "if (!_cm12) {" in src
+    k12 = src[src.index("void k12(const Args a)"):]
+    k12 = k12[:k12.index("\n}\n")]
+    assert "if (gridDim.x <= 256) {" in k12 and "block_part(g_p12_0" in k12
+
+
 def test_initstacks_on_the_host_matches_the_oracle():
     from stade_hip.lower import initstacks
     from oracle import runner
