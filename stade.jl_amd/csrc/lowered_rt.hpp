@@ -326,6 +326,15 @@ class LaunchGraphs {
             (void)hipGetLastError();
             return fn(a, stream);
         }
+        // on a stream the caller is capturing: launched directly, with no second capture, graph
+        // launch or device synchronisation inside the caller's capture (the generated function's
+        // own stream synchronisation then fails the call)
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+            (void)hipGetLastError();
+            return fn(a, stream);
+        }
+        if (cs != hipStreamCaptureStatusNone) return fn(a, stream);
         std::lock_guard<std::recursive_mutex> lk(mu_);
         ++tick_;
         Slot* s = find(a, dev);
